@@ -1,0 +1,101 @@
+"""Pin the CPU oracle against golden vectors written by the reference module.
+
+The fixtures (tests/golden/*.npz) hold the reference's own outputs and
+gradients (tests/golden/make_golden.py).  Here the oracle restatement
+(oracle/dsa3d_ref.py) and the loop restatement (oracle/bruteforce.py) must
+reproduce them: float64 cases to 1e-10 relative, the fp32 C1 case to 1e-5.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from goldens import CASES, load, regenerate, rel_err
+from oracle import bruteforce
+from oracle.dsa3d_ref import PARAM_NAMES, dsa3d_core_ref, dsa3d_module_ref, param_shapes
+
+NAMES = [c["name"] for c in CASES]
+
+
+def _core_inputs(case, arrs, off_np):
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a))  # noqa: E731
+    off = t(off_np) if off_np is not None else t(arrs["offsets"])
+    return t(arrs["q"]), t(arrs["k"]), t(arrs["v"]), off
+
+
+@pytest.mark.parametrize("name", NAMES)
+def test_module_restatement_matches_reference(name):
+    meta, arrs = load(name)
+    case, p, x_np, gy_np, off_np = regenerate(meta)
+    assert tuple(meta["param_names"]) == PARAM_NAMES
+    shapes = param_shapes(case["D"], case["nh"], case["kernel"])
+    params = {}
+    for n in PARAM_NAMES:
+        assert p[n].shape == shapes[n]
+        params[n] = torch.from_numpy(p[n]).requires_grad_(True)
+    x = torch.from_numpy(x_np).requires_grad_(True)
+    off = None if off_np is None else torch.from_numpy(off_np)
+    y = dsa3d_module_ref(x, params, (case["T"], case["H"], case["W"]), case["nh"],
+                         case["kernel"], case["scale"], offsets=off)
+    (y * torch.from_numpy(gy_np)).sum().backward()
+    assert rel_err(y.detach(), arrs["y"]) < 1e-10
+    assert rel_err(x.grad, arrs["dx"]) < 1e-10
+    for n in PARAM_NAMES:
+        if "grad." + n not in arrs:  # offset_net replaced by injected offsets
+            assert off is not None and n.startswith("offset_net")
+            continue
+        g = params[n].grad if params[n].grad is not None else torch.zeros_like(params[n])
+        assert rel_err(g, arrs["grad." + n]) < 1e-10, n
+
+
+@pytest.mark.parametrize("name", NAMES)
+def test_core_restatement_matches_reference(name):
+    meta, arrs = load(name)
+    case, _, _, _, off_np = regenerate(meta)
+    q, k, v, off = (a.clone().requires_grad_(True) for a in _core_inputs(case, arrs, off_np))
+    out, lse = dsa3d_core_ref(q, k, v, off, (case["T"], case["H"], case["W"]), case["nh"],
+                              case["kernel"], case["scale"], return_lse=True)
+    assert rel_err(out.detach(), arrs["attn"]) < 1e-10
+    out.backward(torch.from_numpy(arrs["dattn"]))
+    for name_, t in (("q", q), ("k", k), ("v", v)):
+        assert rel_err(t.grad, arrs["d" + name_]) < 1e-10, name_
+    # no gradient reaches the offsets when every slot's divisor dim is 1
+    doff = off.grad if off.grad is not None else torch.zeros_like(off)
+    assert rel_err(doff, arrs["doffsets"]) < 1e-10
+    assert torch.isfinite(lse).all()
+
+
+@pytest.mark.parametrize("name", ["k377_tiny", "k377_inject", "k333_T1", "k333_H1",
+                                  "k333_W1", "k333_111", "k133", "k311", "k111"])
+def test_bruteforce_closed_form_matches_reference(name):
+    """Loop restatement of the forward and of the closed-form backward.
+
+    This pins the formulas the HIP kernels implement (softmax backward, dK/dV
+    scatter, coordinate gradient through clamp and unnormalisation, slot/axis
+    mapping) against the reference's autograd.
+    """
+    meta, arrs = load(name)
+    case, _, _, _, off_np = regenerate(meta)
+    q, k, v, off = (a.numpy() for a in _core_inputs(case, arrs, off_np))
+    out, dq, dk, dv, doff = bruteforce.dsa3d_core_bruteforce(
+        q, k, v, off, (case["T"], case["H"], case["W"]), case["nh"], case["kernel"],
+        case["scale"], dout=arrs["dattn"])
+    assert rel_err(out, arrs["attn"]) < 1e-10
+    # floor 1e-6: dq and dk vanish identically on a 1x1x1 grid (all taps equal)
+    assert rel_err(dq, arrs["dq"], floor=1e-6) < 1e-10
+    assert rel_err(dk, arrs["dk"], floor=1e-6) < 1e-10
+    assert rel_err(dv, arrs["dv"]) < 1e-10
+    assert rel_err(doff, arrs["doffsets"]) < 1e-10
+
+
+def test_c1_forward_fp32_matches_reference():
+    meta, arrs = load("c1_fwd_fp32")
+    case, p, x_np, _, _ = regenerate(meta)
+    params = {n: torch.from_numpy(p[n]).float() for n in PARAM_NAMES}
+    x = torch.from_numpy(x_np).float()
+    with torch.no_grad():
+        y = dsa3d_module_ref(x, params, (case["T"], case["H"], case["W"]), case["nh"],
+                             case["kernel"], case["scale"], head_chunk=2)
+    rows = arrs["rows"]
+    assert rel_err(y[:, rows], arrs["y_rows"]) < 1e-5
+    assert abs(float(y.double().norm()) / float(arrs["y_norm"]) - 1.0) < 1e-5
