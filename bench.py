@@ -1,0 +1,249 @@
+"""Benchmark: 3D-DSA forward + backward through the HIP kernel set on one MI355X.
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu-baseline]
+
+Workload (one step = one pass of the hot path over one batch): the 65,536-token
+long-clip case -- B=1, T=64, H=W=32, dim 1024, 16 heads x 64, window 3x7x7,
+bf16 storage with fp32 accumulation, raw offsets ~ N(0, 0.5), x ~ N(0, 1),
+upstream grads ~ N(0, 1).  A step runs, on preallocated device buffers:
+  dw_conv 3x7x7 fwd, offset_net depthwise 3x3x3+GELU fwd, attention core fwd,
+  attention core bwd, 3x3x3+GELU bwd, 3x7x7 bwd
+i.e. every HIP kernel of the module's forward and backward (the dense GEMMs of
+the projections stay in hipBLASLt and are not part of the step).
+
+Prints one JSON line.  `value` is tokens/s of the whole step; `roofline` is the
+dominant kernel's algorithmic HBM bytes per launch over its average duration,
+timed with events on the launch stream; `cpu_baseline` is the float32 CPU
+oracle (the reference op sequence) on a bounded T-slab of the same workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "3D-DSA fwd+bwd tokens/sec at 65k tokens bf16; achieved HBM GB/s (% of peak)"
+HBM_PEAK_GBPS = 8000.0
+
+CFG = dict(B=1, T=64, H=32, W=32, D=1024, nh=16, hd=64, kernel=(3, 7, 7), off_std=0.5)
+
+
+def algorithmic_bytes(cfg, e):
+    """Compulsory interface bytes per launch of each kernel (each tensor once)."""
+    N = cfg["B"] * cfg["T"] * cfg["H"] * cfg["W"]
+    D, nh = cfg["D"], cfg["nh"]
+    kt, kh, kw = cfg["kernel"]
+    C = nh * kt * kh * kw * 3
+    return {
+        "dwconv7_fwd": N * 2 * e * D,            # read x, write y
+        "dwconv3_gelu_fwd": N * 2 * e * D,       # read x, write gelu(z)
+        "dsa3d_fwd": N * (e * (4 * D + C) + 4 * nh),   # read q,k,v,off; write out, lse
+        "dsa3d_bwd": N * (e * (8 * D + 2 * C) + 4 * nh),  # read q,k,v,off,out,dout,lse; write dq,dk,dv,doff
+        "dwconv3_gelu_bwd": N * 3 * e * D,       # read x, dF; write dx
+        "dwconv7_bwd": N * 3 * e * D,            # read x, dy; write dx
+    }
+
+
+def run_gpu(steps, warmup):
+    from megaslide_amd import _lib
+
+    lib = _lib.load()
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    c = CFG
+    B, T, H, W, D, nh, hd = c["B"], c["T"], c["H"], c["W"], c["D"], c["nh"], c["hd"]
+    kt, kh, kw = c["kernel"]
+    N = T * H * W
+    C = nh * kt * kh * kw * 3
+    dt = torch.bfloat16
+    g = torch.Generator(device=dev).manual_seed(3)
+
+    def rnd(*shape, std=1.0):
+        return (torch.randn(*shape, generator=g, device=dev) * std).to(dt)
+
+    x = rnd(B, N, D)
+    q, k, v = rnd(B, N, D), rnd(B, N, D), rnd(B, N, D)
+    off = rnd(B, N, C, std=c["off_std"])
+    dout, dF, dY = rnd(B, N, D), rnd(B, N, D), rnd(B, N, D)
+    w7, b7 = rnd(D, 1, kt, kh, kw, std=0.05), rnd(D, std=0.02)
+    w3, b3 = rnd(D, 1, 3, 3, 3, std=0.1), rnd(D, std=0.02)
+    y7, F = torch.empty_like(x), torch.empty_like(x)
+    out = torch.empty_like(q)
+    lse = torch.empty(B, N, nh, device=dev, dtype=torch.float32)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    doff = torch.empty_like(off)
+    dx3, dx7 = torch.empty_like(x), torch.empty_like(x)
+    dw3, db3, dw7, db7 = (torch.empty_like(t) for t in (w3, b3, w7, b7))
+
+    dsa = _lib.DsaDesc(B, T, H, W, nh, hd, kt, kh, kw, _lib.MSD_BF16, D, D, D, 1.0,
+                       1.0 / math.sqrt(hd))
+    cv7 = _lib.ConvDesc(B, T, H, W, D, kt, kh, kw, _lib.MSD_BF16, 0)
+    cv3 = _lib.ConvDesc(B, T, H, W, D, 3, 3, 3, _lib.MSD_BF16, 1)
+    ws_dsa = torch.empty(lib.msd_dsa3d_bwd_workspace_size(ctypes.byref(dsa)), dtype=torch.uint8,
+                         device=dev)
+    ws7 = torch.empty(lib.msd_dwconv3d_bwd_workspace_size(ctypes.byref(cv7)), dtype=torch.uint8,
+                      device=dev)
+    ws3 = torch.empty(lib.msd_dwconv3d_bwd_workspace_size(ctypes.byref(cv3)), dtype=torch.uint8,
+                      device=dev)
+    stream = torch.cuda.current_stream(dev)
+    sh = stream.cuda_stream
+    P = lambda t: t.data_ptr()  # noqa: E731
+
+    phases = [
+        ("dwconv7_fwd", lambda: lib.msd_dwconv3d_fwd(ctypes.byref(cv7), P(x), P(w7), P(b7), P(y7), sh)),
+        ("dwconv3_gelu_fwd", lambda: lib.msd_dwconv3d_fwd(ctypes.byref(cv3), P(x), P(w3), P(b3), P(F), sh)),
+        ("dsa3d_fwd", lambda: lib.msd_dsa3d_fwd(ctypes.byref(dsa), P(q), P(k), P(v), P(off), P(out),
+                                                P(lse), sh)),
+        ("dsa3d_bwd", lambda: lib.msd_dsa3d_bwd(ctypes.byref(dsa), P(q), P(k), P(v), P(off), P(out),
+                                                P(dout), P(lse), None, P(dq), P(dk), P(dv), P(doff),
+                                                P(ws_dsa), ws_dsa.numel(), sh)),
+        ("dwconv3_gelu_bwd", lambda: lib.msd_dwconv3d_bwd(ctypes.byref(cv3), P(x), P(w3), P(b3), P(dF),
+                                                          P(dx3), P(dw3), P(db3), P(ws3), ws3.numel(), sh)),
+        ("dwconv7_bwd", lambda: lib.msd_dwconv3d_bwd(ctypes.byref(cv7), P(x), P(w7), P(b7), P(dY),
+                                                     P(dx7), P(dw7), P(db7), P(ws7), ws7.numel(), sh)),
+    ]
+
+    def step(events=None):
+        for i, (name, fn) in enumerate(phases):
+            if events is not None:
+                events[i][0].record(stream)
+            rc = fn()
+            if events is not None:
+                events[i][1].record(stream)
+            if rc != 0:
+                raise RuntimeError(f"{name} failed: {lib.msd_last_error().decode()}")
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+
+    # timed region: K steps, bracketed by device synchronisation
+    ev = [[[torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)]
+           for _ in phases] for _ in range(steps)]
+    t_start = torch.cuda.Event(enable_timing=True)
+    t_end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    wall0 = time.perf_counter()
+    t_start.record(stream)
+    for s in range(steps):
+        step(ev[s])
+    t_end.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    total_ms = t_start.elapsed_time(t_end)
+    per_phase = {name: sum(ev[s][i][0].elapsed_time(ev[s][i][1]) for s in range(steps)) / steps
+                 for i, (name, _) in enumerate(phases)}
+    return dict(total_ms=total_ms, wall_s=wall, per_phase_ms=per_phase, tokens=B * N)
+
+
+def cpu_baseline(slab_T=2):
+    """float32 CPU oracle (reference op sequence) on a T-slab of the workload."""
+    from oracle.dsa3d_ref import dsa3d_core_ref, dwconv3d_ref
+
+    c = CFG
+    B, H, W, D, nh = c["B"], c["H"], c["W"], c["D"], c["nh"]
+    T = slab_T
+    N = T * H * W
+    C = nh * 147 * 3
+    torch.manual_seed(0)
+    x = torch.randn(B, N, D, requires_grad=True)
+    q, k, v = (torch.randn(B, N, D, requires_grad=True) for _ in range(3))
+    off = (torch.randn(B, N, C) * c["off_std"]).requires_grad_(True)
+    w7 = (torch.randn(D, 1, 3, 7, 7) * 0.05).requires_grad_(True)
+    w3 = (torch.randn(D, 1, 3, 3, 3) * 0.1).requires_grad_(True)
+    b = torch.zeros(D, requires_grad=True)
+    g = torch.randn(B, N, D)
+
+    def one():
+        y7 = dwconv3d_ref(x, w7, b, (T, H, W))
+        f = dwconv3d_ref(x, w3, b, (T, H, W), act="gelu")
+        o = dsa3d_core_ref(q, k, v, off, (T, H, W), nh, (3, 7, 7), 1.0, head_chunk=4)
+        torch.autograd.backward([y7, f, o], [g, g, g])
+
+    t0 = time.perf_counter()
+    one()
+    dt = time.perf_counter() - t0
+    return dict(value=N / dt, unit="tokens/s", cores=torch.get_num_threads(), kind="port",
+                sample=f"float32 CPU oracle (grid_sample/matmul/softmax restatement + conv3d), "
+                       f"fwd+bwd of the same kernel set on a T={T} slab "
+                       f"({N} tokens, H=W=32, dim 1024, 16x64, window 3x7x7), one run of {dt:.1f} s",
+                seconds=dt)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: the 3D-DSA kernels run on a single MI355X "
+              "and no multi-GPU path is built (see DESIGN.md for how it would shard).",
+              file=sys.stderr)
+        sys.exit(2)
+
+    r = run_gpu(args.steps, args.warmup)
+    e = 2
+    ab = algorithmic_bytes(CFG, e)
+    ms_step = r["total_ms"] / args.steps
+    tokens_s = r["tokens"] / (ms_step / 1e3)
+    step_bytes = sum(ab.values())
+    dom = max(r["per_phase_ms"], key=r["per_phase_ms"].get)
+    dom_ms = r["per_phase_ms"][dom]
+    achieved = ab[dom] / (dom_ms / 1e3) / 1e9
+    line = {
+        "metric": METRIC,
+        "value": round(tokens_s, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "3D-DSA fwd+bwd HIP kernel set, long-clip 65,536 tokens",
+            "B": CFG["B"], "T": CFG["T"], "H": CFG["H"], "W": CFG["W"], "dim": CFG["D"],
+            "heads": CFG["nh"], "head_dim": CFG["hd"], "window": list(CFG["kernel"]),
+            "offsets": "raw ~ N(0, 0.5)", "accumulation": "fp32",
+        },
+        "hbm_gbps": round(step_bytes / (ms_step / 1e3) / 1e9, 1),
+        "hbm_frac_of_peak": round(step_bytes / (ms_step / 1e3) / 1e9 / HBM_PEAK_GBPS, 4),
+        "roofline": {
+            "bound": "hbm",
+            "kernel": dom,
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBPS, 4),
+            "traffic": None,
+            "algorithmic_bytes_per_launch": ab[dom],
+            "avg_launch_ms": round(dom_ms, 4),
+        },
+        "per_kernel_ms": {k: round(v, 4) for k, v in r["per_phase_ms"].items()},
+        "wall_s_timed_region": round(r["wall_s"], 3),
+    }
+    if not args.no_cpu_baseline:
+        cb = cpu_baseline()
+        line["cpu_baseline"] = {k: (round(v, 2) if isinstance(v, float) else v)
+                                for k, v in cb.items() if k != "seconds"}
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,136 @@
+/*
+ * megaslide_dsa3d.h -- C ABI of the MI355X (gfx950) 3D Deformable Slide
+ * Attention kernels.
+ *
+ * The library replaces, inside DeformableSlideAttention3D
+ * (infinity/video/attention.py:19-273 of the reference):
+ *   - the trilinear K/V sampling, local softmax attention and weighted sum
+ *     (F.grid_sample x2, matmul, softmax, matmul: attention.py:106-186)
+ *     and their autograd backward                    -> msd_dsa3d_fwd / _bwd
+ *   - the depthwise Conv3d terms dw_conv (attention.py:58-65, :102) and
+ *     offset_net[0:2] = depthwise 3x3x3 conv + GELU (attention.py:71-72, :105)
+ *     and their backward                             -> msd_dwconv3d_fwd / _bwd
+ * The Linear projections and the 1x1 offset conv stay dense GEMMs in the host
+ * framework.
+ *
+ * Conventions
+ *   - Tensors are channel-last: token n = (t*H + h)*W + w, as the reference
+ *     flattens video tokens (infinity/video/model.py:206).  q, k, v, out and
+ *     their gradients are [B, N, D] with D = num_heads*head_dim and channel
+ *     c = head*head_dim + d (attention.py:135-137, :186).
+ *   - Offsets are [B, N, C], C = num_heads*kt*kh*kw*3, channel
+ *     ((((head*kt + i)*kh + j)*kw + k)*3 + slot): the reference's
+ *     offsets.view(B, nh, kt, kh, kw, 3, T, H, W) order (attention.py:109),
+ *     unscaled (the kernels multiply by offset_scale, attention.py:106).
+ *   - Every pointer is device memory owned by the caller.  The library never
+ *     allocates or frees device memory and keeps no pointer after return.
+ *   - `stream` is a hipStream_t (NULL = the null stream).  Work is enqueued;
+ *     nothing synchronises the device.
+ *   - Return value 0 = success, negative = msd_status; msd_last_error() gives a
+ *     thread-local message for the last failure on the calling thread.
+ */
+#ifndef MEGASLIDE_DSA3D_H
+#define MEGASLIDE_DSA3D_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MSD_ABI_VERSION 1
+
+typedef enum msd_dtype { MSD_F32 = 0, MSD_BF16 = 1 } msd_dtype;
+
+typedef enum msd_status {
+  MSD_OK = 0,
+  MSD_ERR_ARG = -1,         /* null pointer, bad size or stride            */
+  MSD_ERR_UNSUPPORTED = -2, /* head_dim / kernel / dtype outside the build */
+  MSD_ERR_ALIGN = -3,       /* pointer not aligned to its element type     */
+  MSD_ERR_WORKSPACE = -4,   /* workspace missing or too small              */
+  MSD_ERR_LAUNCH = -5       /* the HIP runtime rejected a launch           */
+} msd_status;
+
+/* Shape and options of one attention-core call. */
+typedef struct msd_dsa3d_desc {
+  int32_t B, T, H, W;          /* batch, latent grid (N = T*H*W)                  */
+  int32_t num_heads, head_dim; /* D = num_heads*head_dim                          */
+  int32_t kt, kh, kw;          /* window, reference default (3, 7, 7)             */
+  int32_t dtype;               /* msd_dtype of q/k/v/offsets/out and their grads  */
+  int64_t q_stride;            /* elements between consecutive tokens of q, dq    */
+  int64_t k_stride;            /* ... of k, dk                                    */
+  int64_t v_stride;            /* ... of v, dv                                    */
+  float offset_scale;          /* reference offset_scale (attention.py:106)       */
+  float softmax_scale;         /* 1/sqrt(head_dim) in the reference (:176)        */
+} msd_dsa3d_desc;
+
+/* Shape and options of one depthwise-conv call. */
+typedef struct msd_dwconv3d_desc {
+  int32_t B, T, H, W, C;       /* x and y are [B, T*H*W, C]                       */
+  int32_t kt, kh, kw;          /* odd kernel; zero padding kt/2, kh/2, kw/2       */
+  int32_t dtype;               /* msd_dtype of x, y, weight, bias and grads       */
+  int32_t act;                 /* 0 = none, 1 = exact-erf GELU after the bias     */
+} msd_dwconv3d_desc;
+
+/* Version of this header's ABI (MSD_ABI_VERSION). */
+int msd_abi_version(void);
+
+/* Message for the last failed call on this thread ("" if none). */
+const char* msd_last_error(void);
+
+/*
+ * Forward of the attention core: replaces attention.py:106-186 (offset scale,
+ * base grid + normalised offsets, grid_sample of K and V with border padding
+ * and align_corners=False, scores / sqrt(hd), softmax, weighted sum of V).
+ * out [B, N, D] (contiguous, token stride D).  lse [B, N, num_heads] fp32
+ * receives the log-sum-exp of each query's scores for the backward; it may be
+ * NULL when no backward follows.
+ */
+int msd_dsa3d_fwd(const msd_dsa3d_desc* desc, const void* q, const void* k, const void* v,
+                  const void* offsets, void* out, float* lse, void* stream);
+
+/* Bytes of device workspace msd_dsa3d_bwd needs for `desc`. */
+size_t msd_dsa3d_bwd_workspace_size(const msd_dsa3d_desc* desc);
+
+/*
+ * Backward of the attention core: the gradients autograd takes through
+ * attention.py:106-186 (softmax/matmul backward, grid_sampler_3d_backward for
+ * the volumes and the grid, offset normalisation and scale).
+ *   out, dout : [B, N, D] contiguous; lse from msd_dsa3d_fwd.
+ *   dlse      : optional [B, N, num_heads] fp32 gradient w.r.t. lse (NULL = 0),
+ *               for callers that merge extra keys through the log-sum-exp.
+ *   dq, dk, dv: written (not accumulated) with the strides of q, k, v.
+ *   doffsets  : [B, N, C], gradient w.r.t. the unscaled offsets.
+ */
+int msd_dsa3d_bwd(const msd_dsa3d_desc* desc, const void* q, const void* k, const void* v,
+                  const void* offsets, const void* out, const void* dout, const float* lse,
+                  const float* dlse, void* dq, void* dk, void* dv, void* doffsets,
+                  void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Depthwise 3-D convolution, channel-last: replaces nn.Conv3d(C, C, k,
+ * padding=k//2, groups=C) (attention.py:58-65) and, with act = 1, the
+ * offset_net[0:2] pair Conv3d(3, groups=C) + GELU (attention.py:71-72).
+ * weight [C, kt*kh*kw] (nn.Conv3d's [C, 1, kt, kh, kw]); bias [C] or NULL.
+ */
+int msd_dwconv3d_fwd(const msd_dwconv3d_desc* desc, const void* x, const void* weight,
+                     const void* bias, void* y, void* stream);
+
+/* Bytes of device workspace msd_dwconv3d_bwd needs for `desc`. */
+size_t msd_dwconv3d_bwd_workspace_size(const msd_dwconv3d_desc* desc);
+
+/*
+ * Backward of msd_dwconv3d_fwd (conv3d input/weight backward, GELU backward
+ * from the recomputed pre-activation).  dx, dweight, dbias may each be NULL
+ * when not wanted; dx is written, not accumulated.
+ */
+int msd_dwconv3d_bwd(const msd_dwconv3d_desc* desc, const void* x, const void* weight,
+                     const void* bias, const void* dy, void* dx, void* dweight, void* dbias,
+                     void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MEGASLIDE_DSA3D_H */

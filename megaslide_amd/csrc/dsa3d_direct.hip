@@ -1,0 +1,417 @@
+// Direct-form 3D-DSA kernels for gfx950: one 16-lane group per
+// (batch, token, head), every tap's eight trilinear corners gathered from
+// global memory, online softmax in registers.
+//
+// These are the general kernels: any head_dim <= 256, any window, fp32 or
+// bf16.  They restate, for one query and head, what the reference computes
+// with grid_sample + matmul + softmax + matmul (infinity/video/attention.py:
+// 106-186) and autograd's backward of it:
+//
+//   per tap (i, j, k), kappa = (i*kh + j)*kw + k, raw offsets o = off[...]*scale
+//     g_x = 2(w + k - kw/2)/max(W-1,1) - 1 + (T>1 ? o0/(T-1) : 0)   (:118-127,
+//     g_y = 2(h + j - kh/2)/max(H-1,1) - 1 + (H>1 ? o1/(H-1) : 0)    :209-236;
+//     g_z = 2(t + i - kt/2)/max(T-1,1) - 1 + (W>1 ? o2/(W-1) : 0)    slot 0 goes
+//                                                                      to x, slot 2 to z)
+//     u = ((g + 1)*S - 1)/2, clamped to [0, S-1]  (grid_sample, align_corners
+//     = False, padding_mode = 'border', :262-268); corners beyond S-1 carry
+//     weight 0 and are skipped.
+//   s = q . sum_c w_c K_c / sqrt(hd); p = softmax(s); o = sum p sum_c w_c V_c.
+//
+// Backward per tap: dp = dO . v_s, ds = p (dp - Delta), Delta = dO . o - dlse;
+// dq += ds*scale*k_s; dK_c += w_c ds scale q; dV_c += w_c p dO (fp32 atomics
+// into an fp32 accumulator); d u = sum_c dw_c/du (ds scale q.K_c + p dO.V_c),
+// zeroed where u <= 0 or u >= S-1 (border clamp), times S/2 (unnormalise),
+// divided by the slot's divisor and times offset_scale.
+#include "common.h"
+
+namespace msd {
+
+namespace {
+
+constexpr int kGroup = 16;            // lanes per (token, head)
+constexpr int kBlock = 256;           // threads per block
+constexpr int kGroupsPerBlock = kBlock / kGroup;
+
+struct CoreArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* off;
+  int64_t qs, ks, vs;  // token strides of q, k, v (elements)
+  int64_t N;           // tokens per sample
+  int B, T, H, W, nh, hd, kt, kh, kw, C;
+  float offset_scale, softmax_scale;
+  float rdiv_x, rdiv_y, rdiv_z;  // 1/(T-1), 1/(H-1), 1/(W-1) for slots 0,1,2 (0 if dim==1)
+};
+
+// Base grid value of one axis, in fp32 and in the reference's op order.
+__device__ __forceinline__ float base_coord(int p, int c, int S) {
+  const float pos = static_cast<float>(p) + static_cast<float>(c);
+  return 2.0f * pos / static_cast<float>(S > 1 ? S - 1 : 1) - 1.0f;
+}
+
+struct Axis {
+  int i0;      // lower corner index (0 <= i0 <= S-1)
+  bool hi_ok;  // upper corner i0+1 inside the volume
+  float f;     // weight of the upper corner
+  float u;     // unnormalised, unclamped coordinate (for the clamp gradient)
+};
+
+__device__ __forceinline__ Axis axis_sample(float g, int S) {
+  Axis a;
+  a.u = ((g + 1.0f) * static_cast<float>(S) - 1.0f) * 0.5f;
+  // fmaxf returns the non-NaN operand, so a NaN coordinate lands on 0.
+  const float c = fminf(fmaxf(a.u, 0.0f), static_cast<float>(S - 1));
+  const float fl = floorf(c);
+  a.i0 = min(max(static_cast<int>(fl), 0), S - 1);
+  a.f = c - fl;
+  a.hi_ok = (a.i0 + 1) < S;
+  return a;
+}
+
+template <typename T>
+__device__ __forceinline__ void load_offsets(const T* p, float scale, float& o0, float& o1,
+                                             float& o2) {
+  o0 = ld(p, 0) * scale;
+  o1 = ld(p, 1) * scale;
+  o2 = ld(p, 2) * scale;
+}
+
+template <typename T, int CPL>
+__global__ __launch_bounds__(kBlock) void dsa3d_fwd_direct_kernel(CoreArgs a, T* __restrict__ out,
+                                                                   float* __restrict__ lse) {
+  const int lane = threadIdx.x % kGroup;
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * kGroupsPerBlock + threadIdx.x / kGroup;
+  const int64_t total = static_cast<int64_t>(a.B) * a.N * a.nh;
+  if (gid >= total) return;  // uniform across the 16-lane group
+  const int head = static_cast<int>(gid % a.nh);
+  const int64_t bn = gid / a.nh;
+  const int b = static_cast<int>(bn / a.N);
+  const int64_t n = bn - static_cast<int64_t>(b) * a.N;
+  const int w = static_cast<int>(n % a.W);
+  const int h = static_cast<int>((n / a.W) % a.H);
+  const int t = static_cast<int>(n / (static_cast<int64_t>(a.W) * a.H));
+  const T* __restrict__ qp = static_cast<const T*>(a.q);
+  const T* __restrict__ kp = static_cast<const T*>(a.k);
+  const T* __restrict__ vp = static_cast<const T*>(a.v);
+  const int K = a.kt * a.kh * a.kw;
+  const T* __restrict__ op = static_cast<const T*>(a.off) + bn * a.C + static_cast<int64_t>(head) * K * 3;
+  const int cbase = head * a.hd + lane * CPL;
+  const int64_t sample0 = static_cast<int64_t>(b) * a.N;
+
+  float qv[CPL], acc[CPL];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    const int d = lane * CPL + j;
+    qv[j] = d < a.hd ? ld(qp, bn * a.qs + cbase + j) : 0.0f;
+    acc[j] = 0.0f;
+  }
+  float m = -INFINITY, l = 0.0f;
+  int kap = 0;
+  for (int i = 0; i < a.kt; ++i) {
+    const float bz = base_coord(t, i - a.kt / 2, a.T);
+    for (int jj = 0; jj < a.kh; ++jj) {
+      const float by = base_coord(h, jj - a.kh / 2, a.H);
+      for (int kk = 0; kk < a.kw; ++kk, ++kap) {
+        const float bx = base_coord(w, kk - a.kw / 2, a.W);
+        float o0, o1, o2;
+        load_offsets(op + kap * 3, a.offset_scale, o0, o1, o2);
+        const Axis ax = axis_sample(bx + o0 * a.rdiv_x, a.W);
+        const Axis ay = axis_sample(by + o1 * a.rdiv_y, a.H);
+        const Axis az = axis_sample(bz + o2 * a.rdiv_z, a.T);
+        float ksum[CPL], vsum[CPL];
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) ksum[j] = vsum[j] = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          const int dz = c >> 2, dy = (c >> 1) & 1, dx = c & 1;
+          if ((dz && !az.hi_ok) || (dy && !ay.hi_ok) || (dx && !ax.hi_ok)) continue;
+          const float wgt = (dz ? az.f : 1.0f - az.f) * (dy ? ay.f : 1.0f - ay.f) *
+                            (dx ? ax.f : 1.0f - ax.f);
+          const int64_t row =
+              sample0 + (static_cast<int64_t>(az.i0 + dz) * a.H + (ay.i0 + dy)) * a.W + (ax.i0 + dx);
+#pragma unroll
+          for (int j = 0; j < CPL; ++j) {
+            if (lane * CPL + j < a.hd) {
+              ksum[j] += wgt * ld(kp, row * a.ks + cbase + j);
+              vsum[j] += wgt * ld(vp, row * a.vs + cbase + j);
+            }
+          }
+        }
+        float part = 0.0f;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) part += qv[j] * ksum[j];
+        const float s = group_sum<kGroup>(part) * a.softmax_scale;
+        const float mn = fmaxf(m, s);
+        const float corr = __expf(m - mn);
+        const float e = __expf(s - mn);
+        l = l * corr + e;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) acc[j] = acc[j] * corr + e * vsum[j];
+        m = mn;
+      }
+    }
+  }
+  T* __restrict__ orow = out + bn * (static_cast<int64_t>(a.nh) * a.hd);
+  const float inv = 1.0f / l;
+#pragma unroll
+  for (int j = 0; j < CPL; ++j)
+    if (lane * CPL + j < a.hd) st(orow, cbase + j, acc[j] * inv);
+  if (lse != nullptr && lane == 0) lse[bn * a.nh + head] = m + logf(l);
+}
+
+template <typename T, int CPL>
+__global__ __launch_bounds__(kBlock) void dsa3d_bwd_direct_kernel(
+    CoreArgs a, const T* __restrict__ out, const T* __restrict__ dout, const float* __restrict__ lse,
+    const float* __restrict__ dlse, T* __restrict__ dq, float* __restrict__ dk_acc,
+    float* __restrict__ dv_acc, T* __restrict__ doff) {
+  const int lane = threadIdx.x % kGroup;
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * kGroupsPerBlock + threadIdx.x / kGroup;
+  const int64_t total = static_cast<int64_t>(a.B) * a.N * a.nh;
+  if (gid >= total) return;
+  const int head = static_cast<int>(gid % a.nh);
+  const int64_t bn = gid / a.nh;
+  const int b = static_cast<int>(bn / a.N);
+  const int64_t n = bn - static_cast<int64_t>(b) * a.N;
+  const int w = static_cast<int>(n % a.W);
+  const int h = static_cast<int>((n / a.W) % a.H);
+  const int t = static_cast<int>(n / (static_cast<int64_t>(a.W) * a.H));
+  const T* __restrict__ qp = static_cast<const T*>(a.q);
+  const T* __restrict__ kp = static_cast<const T*>(a.k);
+  const T* __restrict__ vp = static_cast<const T*>(a.v);
+  const int K = a.kt * a.kh * a.kw;
+  const int64_t obase = bn * a.C + static_cast<int64_t>(head) * K * 3;
+  const T* __restrict__ op = static_cast<const T*>(a.off) + obase;
+  const int D = a.nh * a.hd;
+  const int cbase = head * a.hd + lane * CPL;
+  const int64_t sample0 = static_cast<int64_t>(b) * a.N;
+
+  float qv[CPL], gov[CPL], dqv[CPL];
+  float delta_part = 0.0f;
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    const bool on = lane * CPL + j < a.hd;
+    qv[j] = on ? ld(qp, bn * a.qs + cbase + j) : 0.0f;
+    gov[j] = on ? ld(dout, bn * D + cbase + j) : 0.0f;
+    const float ov = on ? ld(out, bn * D + cbase + j) : 0.0f;
+    delta_part += gov[j] * ov;
+    dqv[j] = 0.0f;
+  }
+  float delta = group_sum<kGroup>(delta_part);
+  if (dlse != nullptr) delta -= dlse[bn * a.nh + head];
+  const float lse_q = lse[bn * a.nh + head];
+  const float sc = a.softmax_scale;
+
+  int kap = 0;
+  for (int i = 0; i < a.kt; ++i) {
+    const float bz = base_coord(t, i - a.kt / 2, a.T);
+    for (int jj = 0; jj < a.kh; ++jj) {
+      const float by = base_coord(h, jj - a.kh / 2, a.H);
+      for (int kk = 0; kk < a.kw; ++kk, ++kap) {
+        const float bx = base_coord(w, kk - a.kw / 2, a.W);
+        float o0, o1, o2;
+        load_offsets(op + kap * 3, a.offset_scale, o0, o1, o2);
+        const Axis ax = axis_sample(bx + o0 * a.rdiv_x, a.W);
+        const Axis ay = axis_sample(by + o1 * a.rdiv_y, a.H);
+        const Axis az = axis_sample(bz + o2 * a.rdiv_z, a.T);
+        float ksum[CPL];
+        float pk[8], pv[8];
+        int64_t rows[8];
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) ksum[j] = 0.0f;
+        float s_part = 0.0f, dp_part = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          const int dz = c >> 2, dy = (c >> 1) & 1, dx = c & 1;
+          pk[c] = pv[c] = 0.0f;
+          rows[c] = -1;
+          if ((dz && !az.hi_ok) || (dy && !ay.hi_ok) || (dx && !ax.hi_ok)) continue;
+          const float wgt = (dz ? az.f : 1.0f - az.f) * (dy ? ay.f : 1.0f - ay.f) *
+                            (dx ? ax.f : 1.0f - ax.f);
+          const int64_t row =
+              sample0 + (static_cast<int64_t>(az.i0 + dz) * a.H + (ay.i0 + dy)) * a.W + (ax.i0 + dx);
+          rows[c] = row;
+#pragma unroll
+          for (int j = 0; j < CPL; ++j) {
+            if (lane * CPL + j < a.hd) {
+              const float kv = ld(kp, row * a.ks + cbase + j);
+              const float vv = ld(vp, row * a.vs + cbase + j);
+              ksum[j] += wgt * kv;
+              pk[c] += qv[j] * kv;
+              pv[c] += gov[j] * vv;
+            }
+          }
+          s_part += wgt * pk[c];
+          dp_part += wgt * pv[c];
+        }
+        const float s = group_sum<kGroup>(s_part) * sc;
+        const float dp = group_sum<kGroup>(dp_part);
+        const float p = __expf(s - lse_q);
+        const float ds = p * (dp - delta);
+        const float dss = ds * sc;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) dqv[j] += dss * ksum[j];
+        float gx = 0.0f, gy = 0.0f, gz = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          if (rows[c] < 0) continue;
+          const int dz = c >> 2, dy = (c >> 1) & 1, dx = c & 1;
+          const float wz = dz ? az.f : 1.0f - az.f;
+          const float wy = dy ? ay.f : 1.0f - ay.f;
+          const float wx = dx ? ax.f : 1.0f - ax.f;
+          const float wgt = wz * wy * wx;
+          const float tc = dss * pk[c] + p * pv[c];
+          gx += (dx ? 1.0f : -1.0f) * wy * wz * tc;
+          gy += (dy ? 1.0f : -1.0f) * wx * wz * tc;
+          gz += (dz ? 1.0f : -1.0f) * wx * wy * tc;
+          const int64_t row = rows[c];
+#pragma unroll
+          for (int j = 0; j < CPL; ++j) {
+            if (lane * CPL + j < a.hd) {
+              atomicAdd(dk_acc + row * D + cbase + j, wgt * dss * qv[j]);
+              atomicAdd(dv_acc + row * D + cbase + j, wgt * p * gov[j]);
+            }
+          }
+        }
+        gx = group_sum<kGroup>(gx);
+        gy = group_sum<kGroup>(gy);
+        gz = group_sum<kGroup>(gz);
+        if (lane == 0) {
+          const float mx = (ax.u > 0.0f && ax.u < static_cast<float>(a.W - 1)) ? 0.5f * a.W : 0.0f;
+          const float my = (ay.u > 0.0f && ay.u < static_cast<float>(a.H - 1)) ? 0.5f * a.H : 0.0f;
+          const float mz = (az.u > 0.0f && az.u < static_cast<float>(a.T - 1)) ? 0.5f * a.T : 0.0f;
+          T* __restrict__ dop = doff + obase + kap * 3;
+          st(dop, 0, gx * mx * a.rdiv_x * a.offset_scale);
+          st(dop, 1, gy * my * a.rdiv_y * a.offset_scale);
+          st(dop, 2, gz * mz * a.rdiv_z * a.offset_scale);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < CPL; ++j)
+    if (lane * CPL + j < a.hd) st(dq, bn * a.qs + cbase + j, dqv[j]);
+}
+
+// Accumulator [rows, D] fp32 -> dst with token stride `stride`, element type T.
+template <typename T>
+__global__ __launch_bounds__(256) void strided_convert_kernel(const float* __restrict__ src,
+                                                              T* __restrict__ dst, int64_t rows,
+                                                              int D, int64_t stride) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= rows * D) return;
+  const int64_t r = i / D;
+  const int c = static_cast<int>(i - r * D);
+  st(dst, r * stride + c, src[i]);
+}
+
+CoreArgs make_args(const msd_dsa3d_desc& d, const void* q, const void* k, const void* v,
+                   const void* off) {
+  CoreArgs a;
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.off = off;
+  a.qs = d.q_stride;
+  a.ks = d.k_stride;
+  a.vs = d.v_stride;
+  a.N = static_cast<int64_t>(d.T) * d.H * d.W;
+  a.B = d.B;
+  a.T = d.T;
+  a.H = d.H;
+  a.W = d.W;
+  a.nh = d.num_heads;
+  a.hd = d.head_dim;
+  a.kt = d.kt;
+  a.kh = d.kh;
+  a.kw = d.kw;
+  a.C = d.num_heads * d.kt * d.kh * d.kw * 3;
+  a.offset_scale = d.offset_scale;
+  a.softmax_scale = d.softmax_scale;
+  a.rdiv_x = d.T > 1 ? 1.0f / static_cast<float>(d.T - 1) : 0.0f;
+  a.rdiv_y = d.H > 1 ? 1.0f / static_cast<float>(d.H - 1) : 0.0f;
+  a.rdiv_z = d.W > 1 ? 1.0f / static_cast<float>(d.W - 1) : 0.0f;
+  return a;
+}
+
+template <typename F>
+hipError_t dispatch_cpl(int hd, F&& f) {
+  const int need = (hd + kGroup - 1) / kGroup;
+  if (need <= 1) return f.template operator()<1>();
+  if (need <= 2) return f.template operator()<2>();
+  if (need <= 3) return f.template operator()<3>();
+  if (need <= 4) return f.template operator()<4>();
+  if (need <= 6) return f.template operator()<6>();
+  if (need <= 8) return f.template operator()<8>();
+  if (need <= 12) return f.template operator()<12>();
+  return f.template operator()<16>();
+}
+
+template <typename T>
+hipError_t fwd_typed(const msd_dsa3d_desc& d, const CoreArgs& a, void* out, float* lse,
+                     hipStream_t s) {
+  const int64_t groups = static_cast<int64_t>(a.B) * a.N * a.nh;
+  const dim3 grid(static_cast<unsigned>((groups + kGroupsPerBlock - 1) / kGroupsPerBlock));
+  return dispatch_cpl(d.head_dim, [&]<int CPL>() {
+    hipLaunchKernelGGL((dsa3d_fwd_direct_kernel<T, CPL>), grid, dim3(kBlock), 0, s, a,
+                       static_cast<T*>(out), lse);
+    return hipGetLastError();
+  });
+}
+
+template <typename T>
+hipError_t bwd_typed(const msd_dsa3d_desc& d, const CoreArgs& a, const void* out, const void* dout,
+                     const float* lse, const float* dlse, void* dq, void* dk, void* dv, void* doff,
+                     void* ws, hipStream_t s) {
+  const int64_t rows = static_cast<int64_t>(a.B) * a.N;
+  const int D = a.nh * a.hd;
+  float* dk_acc = static_cast<float*>(ws);
+  float* dv_acc = dk_acc + rows * D;
+  const int64_t nacc = 2 * rows * D;
+  hipLaunchKernelGGL(fill_zero_f32, dim3(fill_blocks(nacc)), dim3(256), 0, s, dk_acc, nacc);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int64_t groups = rows * a.nh;
+  const dim3 grid(static_cast<unsigned>((groups + kGroupsPerBlock - 1) / kGroupsPerBlock));
+  e = dispatch_cpl(d.head_dim, [&]<int CPL>() {
+    hipLaunchKernelGGL((dsa3d_bwd_direct_kernel<T, CPL>), grid, dim3(kBlock), 0, s, a,
+                       static_cast<const T*>(out), static_cast<const T*>(dout), lse, dlse,
+                       static_cast<T*>(dq), dk_acc, dv_acc, static_cast<T*>(doff));
+    return hipGetLastError();
+  });
+  if (e != hipSuccess) return e;
+  const dim3 cgrid(static_cast<unsigned>((rows * D + 255) / 256));
+  hipLaunchKernelGGL((strided_convert_kernel<T>), cgrid, dim3(256), 0, s, dk_acc,
+                     static_cast<T*>(dk), rows, D, a.ks);
+  hipLaunchKernelGGL((strided_convert_kernel<T>), cgrid, dim3(256), 0, s, dv_acc,
+                     static_cast<T*>(dv), rows, D, a.vs);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+int dsa3d_max_head_dim() { return kGroup * 16; }
+
+size_t dsa3d_bwd_ws_bytes(const msd_dsa3d_desc& d) {
+  const int64_t rows = static_cast<int64_t>(d.B) * d.T * d.H * d.W;
+  return static_cast<size_t>(2 * rows * d.num_heads * d.head_dim) * sizeof(float);
+}
+
+hipError_t launch_dsa3d_fwd(const msd_dsa3d_desc& d, const void* q, const void* k, const void* v,
+                            const void* off, void* out, float* lse, hipStream_t s) {
+  const CoreArgs a = make_args(d, q, k, v, off);
+  if (d.dtype == MSD_BF16) return fwd_typed<bf16>(d, a, out, lse, s);
+  return fwd_typed<float>(d, a, out, lse, s);
+}
+
+hipError_t launch_dsa3d_bwd(const msd_dsa3d_desc& d, const void* q, const void* k, const void* v,
+                            const void* off, const void* out, const void* dout, const float* lse,
+                            const float* dlse, void* dq, void* dk, void* dv, void* doff,
+                            void* ws, hipStream_t s) {
+  const CoreArgs a = make_args(d, q, k, v, off);
+  if (d.dtype == MSD_BF16)
+    return bwd_typed<bf16>(d, a, out, dout, lse, dlse, dq, dk, dv, doff, ws, s);
+  return bwd_typed<float>(d, a, out, dout, lse, dlse, dq, dk, dv, doff, ws, s);
+}
+
+}  // namespace msd

@@ -1,0 +1,247 @@
+"""Autograd functions over the HIP kernels.
+
+``dsa3d_core``   attention core (trilinear K/V sampling + local softmax attention)
+                 replacing infinity/video/attention.py:106-186 of the reference.
+``dwconv3d``     depthwise 3-D conv (+ optional exact-erf GELU) replacing the
+                 reference's nn.Conv3d(groups=D) terms (attention.py:58-74).
+
+Both follow the reference's own idiom for custom autograd
+(infinity/ops/layers.py:16-62: save_for_backward + explicit backward).  They
+run only on ROCm device tensors; there is no CPU path.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+from typing import Optional, Sequence, Tuple
+
+import torch
+
+from . import _lib
+
+Tensor = torch.Tensor
+
+
+def _require_device(*ts: Optional[Tensor]) -> torch.device:
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise RuntimeError(
+                "megaslide_amd kernels run on ROCm devices only; got a tensor on "
+                f"{t.device} (there is no CPU implementation)")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise RuntimeError(f"megaslide_amd: tensors on different devices ({dev}, {t.device})")
+    return dev
+
+
+def _tokens_major(t: Tensor, B: int, N: int, D: int) -> Tensor:
+    """[B, N, D] view with unit channel stride and a uniform token stride."""
+    if t.shape != (B, N, D):
+        raise ValueError(f"expected shape {(B, N, D)}, got {tuple(t.shape)}")
+    if t.stride(2) == 1 and t.stride(0) == N * t.stride(1) and t.stride(1) >= D:
+        return t
+    return t.contiguous()
+
+
+def _dsa_desc(B, T, H, W, nh, hd, kernel_size, dtype, qs, ks, vs, offset_scale) -> _lib.DsaDesc:
+    kt, kh, kw = kernel_size
+    return _lib.DsaDesc(B, T, H, W, nh, hd, kt, kh, kw, _lib.dtype_code(dtype), qs, ks, vs,
+                        float(offset_scale), 1.0 / math.sqrt(hd))
+
+
+class DSA3DCoreFunction(torch.autograd.Function):
+    """out, lse = core(q, k, v, offsets); both outputs differentiable."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, offsets, video_shape, num_heads, kernel_size, offset_scale):
+        dev = _require_device(q, k, v, offsets)
+        B, N, D = q.shape
+        T, H, W = (int(s) for s in video_shape)
+        if N != T * H * W:
+            raise ValueError(f"N={N} but T*H*W={T * H * W}")
+        if D % num_heads != 0:
+            raise ValueError(f"D={D} not divisible by num_heads={num_heads}")
+        hd = D // num_heads
+        kt, kh, kw = (int(s) for s in kernel_size)
+        C = num_heads * kt * kh * kw * 3
+        dt = q.dtype
+        for name, t in (("k", k), ("v", v), ("offsets", offsets)):
+            if t.dtype != dt:
+                raise TypeError(f"dsa3d_core: {name} is {t.dtype}, q is {dt}")
+        q = _tokens_major(q, B, N, D)
+        k = _tokens_major(k, B, N, D)
+        v = _tokens_major(v, B, N, D)
+        if offsets.shape != (B, N, C):
+            raise ValueError(f"offsets must be {(B, N, C)}, got {tuple(offsets.shape)}")
+        offsets = offsets.contiguous()
+        desc = _dsa_desc(B, T, H, W, num_heads, hd, (kt, kh, kw), dt, q.stride(1), k.stride(1),
+                         v.stride(1), offset_scale)
+        out = torch.empty((B, N, D), dtype=dt, device=dev)
+        lse = torch.empty((B, N, num_heads), dtype=torch.float32, device=dev)
+        lib = _lib.load()
+        with torch.cuda.device(dev):
+            _lib.check(lib.msd_dsa3d_fwd(ctypes.byref(desc), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                         offsets.data_ptr(), out.data_ptr(), lse.data_ptr(),
+                                         _lib.stream_handle(dev)), "dsa3d_fwd")
+        ctx.desc_args = (B, T, H, W, num_heads, hd, (kt, kh, kw), dt, offset_scale)
+        ctx.save_for_backward(q, k, v, offsets, out, lse)
+        return out, lse
+
+    @staticmethod
+    def backward(ctx, dout, dlse):
+        q, k, v, offsets, out, lse = ctx.saved_tensors
+        B, T, H, W, nh, hd, ksz, dt, offset_scale = ctx.desc_args
+        dev = q.device
+        N = T * H * W
+        D = nh * hd
+        if dout is None:
+            dout = torch.zeros_like(out)
+        dout = dout.to(dt).contiguous()
+        if dlse is not None:
+            dlse = dlse.to(torch.float32).contiguous()
+        dq = torch.empty((B, N, D), dtype=dt, device=dev)
+        dk = torch.empty((B, N, D), dtype=dt, device=dev)
+        dv = torch.empty((B, N, D), dtype=dt, device=dev)
+        doff = torch.empty_like(offsets)
+        # grads are written with the token strides given in the desc: contiguous here
+        desc = _dsa_desc(B, T, H, W, nh, hd, ksz, dt, D, D, D, offset_scale)
+        qc, kc, vc = (t if t.stride(1) == D else t.contiguous() for t in (q, k, v))
+        lib = _lib.load()
+        ws_bytes = lib.msd_dsa3d_bwd_workspace_size(ctypes.byref(desc))
+        ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
+        with torch.cuda.device(dev):
+            _lib.check(lib.msd_dsa3d_bwd(
+                ctypes.byref(desc), qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), offsets.data_ptr(),
+                out.data_ptr(), dout.data_ptr(), lse.data_ptr(),
+                None if dlse is None else dlse.data_ptr(),
+                dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), doff.data_ptr(),
+                ws.data_ptr(), ws_bytes, _lib.stream_handle(dev)), "dsa3d_bwd")
+        return dq, dk, dv, doff, None, None, None, None
+
+
+def dsa3d_core(q: Tensor, k: Tensor, v: Tensor, offsets: Tensor, video_shape: Sequence[int],
+               num_heads: int, kernel_size: Sequence[int] = (3, 7, 7), offset_scale: float = 1.0,
+               return_lse: bool = False):
+    """Attention core on device tensors.
+
+    q, k, v: [B, N, D]; offsets: [B, N, num_heads*kt*kh*kw*3] unscaled, channel
+    order [head][i][j][k][slot] (the reference's offsets.view order,
+    attention.py:109).  Returns out [B, N, D] (and lse [B, N, num_heads]).
+    """
+    if not (torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v, offsets))):
+        return _dsa3d_core_nograd(q, k, v, offsets, video_shape, num_heads, kernel_size,
+                                  offset_scale, return_lse)
+    out, lse = DSA3DCoreFunction.apply(q, k, v, offsets, tuple(video_shape), int(num_heads),
+                                       tuple(kernel_size), float(offset_scale))
+    return (out, lse) if return_lse else out
+
+
+def _dsa3d_core_nograd(q, k, v, offsets, video_shape, num_heads, kernel_size, offset_scale,
+                       return_lse):
+    """Forward only: no saved tensors, no lse unless asked for."""
+    dev = _require_device(q, k, v, offsets)
+    B, N, D = q.shape
+    T, H, W = (int(s) for s in video_shape)
+    if N != T * H * W:
+        raise ValueError(f"N={N} but T*H*W={T * H * W}")
+    hd = D // num_heads
+    kt, kh, kw = (int(s) for s in kernel_size)
+    C = num_heads * kt * kh * kw * 3
+    dt = q.dtype
+    for name, t in (("k", k), ("v", v), ("offsets", offsets)):
+        if t.dtype != dt:
+            raise TypeError(f"dsa3d_core: {name} is {t.dtype}, q is {dt}")
+    q = _tokens_major(q, B, N, D)
+    k = _tokens_major(k, B, N, D)
+    v = _tokens_major(v, B, N, D)
+    if offsets.shape != (B, N, C):
+        raise ValueError(f"offsets must be {(B, N, C)}, got {tuple(offsets.shape)}")
+    offsets = offsets.contiguous()
+    desc = _dsa_desc(B, T, H, W, num_heads, hd, (kt, kh, kw), dt, q.stride(1), k.stride(1),
+                     v.stride(1), offset_scale)
+    out = torch.empty((B, N, D), dtype=dt, device=dev)
+    lse = torch.empty((B, N, num_heads), dtype=torch.float32, device=dev) if return_lse else None
+    lib = _lib.load()
+    with torch.cuda.device(dev):
+        _lib.check(lib.msd_dsa3d_fwd(ctypes.byref(desc), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                     offsets.data_ptr(), out.data_ptr(), _lib.ptr(lse),
+                                     _lib.stream_handle(dev)), "dsa3d_fwd")
+    return (out, lse) if return_lse else out
+
+
+# ---------------------------------------------------------------------------
+# depthwise conv
+# ---------------------------------------------------------------------------
+
+_ACT = {None: 0, "none": 0, "gelu": 1}
+
+
+def _conv_desc(x: Tensor, video_shape, kernel: Tuple[int, int, int], act: int) -> _lib.ConvDesc:
+    B, N, C = x.shape
+    T, H, W = (int(s) for s in video_shape)
+    if N != T * H * W:
+        raise ValueError(f"N={N} but T*H*W={T * H * W}")
+    kt, kh, kw = kernel
+    return _lib.ConvDesc(B, T, H, W, C, kt, kh, kw, _lib.dtype_code(x.dtype), act)
+
+
+class DwConv3dFunction(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, weight, bias, video_shape, act):
+        dev = _require_device(x, weight, bias)
+        x = x.contiguous()
+        C = x.shape[2]
+        kernel = tuple(int(s) for s in weight.shape[-3:])
+        if weight.numel() != C * kernel[0] * kernel[1] * kernel[2]:
+            raise ValueError(f"weight {tuple(weight.shape)} does not match {C} channels")
+        w = weight.to(x.dtype).contiguous()
+        b = None if bias is None else bias.to(x.dtype).contiguous()
+        desc = _conv_desc(x, video_shape, kernel, _ACT[act])
+        y = torch.empty_like(x)
+        lib = _lib.load()
+        with torch.cuda.device(dev):
+            _lib.check(lib.msd_dwconv3d_fwd(ctypes.byref(desc), x.data_ptr(), w.data_ptr(),
+                                            _lib.ptr(b), y.data_ptr(), _lib.stream_handle(dev)),
+                       "dwconv3d_fwd")
+        ctx.video_shape = tuple(video_shape)
+        ctx.act = act
+        ctx.kernel = kernel
+        ctx.wdtype = weight.dtype
+        ctx.bdtype = None if bias is None else bias.dtype
+        ctx.save_for_backward(x, w, b)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, w, b = ctx.saved_tensors
+        dev = x.device
+        dy = dy.to(x.dtype).contiguous()
+        need_x, need_w, need_b = ctx.needs_input_grad[:3]
+        desc = _conv_desc(x, ctx.video_shape, ctx.kernel, _ACT[ctx.act])
+        dx = torch.empty_like(x) if need_x else None
+        dw = torch.empty_like(w) if need_w else None
+        db = torch.empty_like(b) if (need_b and b is not None) else None
+        lib = _lib.load()
+        ws_bytes = lib.msd_dwconv3d_bwd_workspace_size(ctypes.byref(desc))
+        ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
+        with torch.cuda.device(dev):
+            _lib.check(lib.msd_dwconv3d_bwd(
+                ctypes.byref(desc), x.data_ptr(), w.data_ptr(), _lib.ptr(b), dy.data_ptr(),
+                _lib.ptr(dx), _lib.ptr(dw), _lib.ptr(db), ws.data_ptr(), ws_bytes,
+                _lib.stream_handle(dev)), "dwconv3d_bwd")
+        if dw is not None:
+            dw = dw.to(ctx.wdtype)
+        if db is not None:
+            db = db.to(ctx.bdtype)
+        return dx, dw, db, None, None
+
+
+def dwconv3d(x: Tensor, weight: Tensor, bias: Optional[Tensor], video_shape: Sequence[int],
+             act: Optional[str] = None) -> Tensor:
+    """Depthwise conv on channel-last tokens x [B, N, C]; weight [C, 1, kt, kh, kw]."""
+    return DwConv3dFunction.apply(x, weight, bias, tuple(video_shape), act)

@@ -77,18 +77,6 @@ def normalise_offsets(off: Tensor, T: int, H: int, W: int) -> Tensor:
     return out
 
 
-def offsets_to_grid_layout(off: Tensor, B: int, T: int, H: int, W: int, nh: int,
-                           kernel_size: Sequence[int]) -> Tensor:
-    """[B, N, C] channel-last offsets -> [B, nh, T, H, W, kt, kh, kw, 3].
-
-    Same element mapping as attention.py:109-111 applied to the channel-first
-    conv output.
-    """
-    kt, kh, kw = kernel_size
-    o = off.reshape(B, T, H, W, nh, kt, kh, kw, 3)
-    return o.permute(0, 4, 1, 2, 3, 5, 6, 7, 8)
-
-
 # ---------------------------------------------------------------------------
 # attention core
 # ---------------------------------------------------------------------------
@@ -101,7 +89,9 @@ def _heads_volume(t: Tensor, B: int, T: int, H: int, W: int, nh: int, hd: int) -
 def dsa3d_core_ref(q: Tensor, k: Tensor, v: Tensor, off: Tensor,
                    video_shape: Sequence[int], num_heads: int,
                    kernel_size: Sequence[int] = (3, 7, 7), offset_scale: float = 1.0,
-                   head_chunk: Optional[int] = None, return_lse: bool = False):
+                   head_chunk: Optional[int] = None, return_lse: bool = False,
+                   extra_k: Optional[Tensor] = None, extra_v: Optional[Tensor] = None,
+                   query_index: Optional[Tensor] = None):
     """Deformable local attention core, reference op sequence.
 
     Restates attention.py:106-186 without the projections: scale the offsets
@@ -110,9 +100,16 @@ def dsa3d_core_ref(q: Tensor, k: Tensor, v: Tensor, off: Tensor,
     (i*kh + j)*kw + k order (:152-157), ``matmul / sqrt(hd)`` (:176),
     ``softmax`` (:179), weighted sum (:183), heads back to [B, N, D] (:186).
 
+    ``extra_k``/``extra_v`` ([B, G, D], already projected) are appended to every
+    query's tap list before the softmax, as attention.py:160-173 does with the
+    projected ``extra_kv``.
+
     Heads are independent, so ``head_chunk`` splits them to bound memory; the
-    result is identical.  Returns out [B, N, D] (and the per-(b, head, token)
-    log-sum-exp [B, nh, N] of the scores when ``return_lse``).
+    result is identical.  ``query_index`` (1-D token indices) restricts the
+    queries to a subset while K/V keep the full volume -- exact for those
+    queries, since each query's output, dq and d offsets depend on its own taps
+    only.  Returns out [B, Nq, D] (and the per-(b, head, token) log-sum-exp
+    [B, nh, Nq] of the scores when ``return_lse``).
     """
     B, N, D = q.shape
     T, H, W = video_shape
@@ -123,32 +120,43 @@ def dsa3d_core_ref(q: Tensor, k: Tensor, v: Tensor, off: Tensor,
     K = kt * kh * kw
     hc = nh if head_chunk is None else max(1, min(nh, head_chunk))
 
-    grid0 = base_grid(T, H, W, kernel_size, device=q.device)
-    offs = offsets_to_grid_layout(off * offset_scale, B, T, H, W, nh, kernel_size)
+    grid0 = base_grid(T, H, W, kernel_size, device=q.device).reshape(N, kt, kh, kw, 3)
+    offs = (off * offset_scale).reshape(B, N, nh, kt, kh, kw, 3).permute(0, 2, 1, 3, 4, 5, 6)
     kvol = _heads_volume(k, B, T, H, W, nh, hd)
     vvol = _heads_volume(v, B, T, H, W, nh, hd)
     qh = q.reshape(B, N, nh, hd).permute(0, 2, 1, 3)  # [B, nh, N, hd]
+    if query_index is not None:
+        grid0 = grid0[query_index]
+        offs = offs[:, :, query_index]
+        qh = qh[:, :, query_index]
+    Nq = grid0.shape[0]
 
     outs, lses = [], []
     for h0 in range(0, nh, hc):
         h1 = min(nh, h0 + hc)
         m = h1 - h0
-        grid = grid0 + normalise_offsets(offs[:, h0:h1], T, H, W)  # [B,m,T,H,W,kt,kh,kw,3]
-        g = grid.reshape(B * m, N, K, 1, 3)
+        grid = grid0 + normalise_offsets(offs[:, h0:h1], T, H, W)  # [B,m,Nq,kt,kh,kw,3]
+        g = grid.reshape(B * m, Nq, K, 1, 3)
         ks = F.grid_sample(kvol[:, h0:h1].reshape(B * m, hd, T, H, W), g,
                            mode="bilinear", padding_mode="border", align_corners=False)
         vs = F.grid_sample(vvol[:, h0:h1].reshape(B * m, hd, T, H, W), g,
                            mode="bilinear", padding_mode="border", align_corners=False)
-        ks = ks.reshape(B, m, hd, N, K).permute(0, 1, 3, 2, 4)  # [B,m,N,hd,K]
-        vs = vs.reshape(B, m, hd, N, K).permute(0, 1, 3, 2, 4)
-        qq = qh[:, h0:h1]  # [B,m,N,hd]
+        ks = ks.reshape(B, m, hd, Nq, K).permute(0, 1, 3, 2, 4)  # [B,m,Nq,hd,K]
+        vs = vs.reshape(B, m, hd, Nq, K).permute(0, 1, 3, 2, 4)
+        if extra_k is not None:
+            G = extra_k.shape[1]
+            ek = extra_k.reshape(B, G, nh, hd)[:, :, h0:h1].permute(0, 2, 3, 1)  # [B,m,hd,G]
+            ev = extra_v.reshape(B, G, nh, hd)[:, :, h0:h1].permute(0, 2, 3, 1)
+            ks = torch.cat([ks, ek.unsqueeze(2).expand(B, m, Nq, hd, G)], dim=-1)
+            vs = torch.cat([vs, ev.unsqueeze(2).expand(B, m, Nq, hd, G)], dim=-1)
+        qq = qh[:, h0:h1]  # [B,m,Nq,hd]
         scores = torch.matmul(qq.unsqueeze(-2), ks).squeeze(-2) / math.sqrt(hd)  # [B,m,N,K]
         p = F.softmax(scores, dim=-1)
         o = torch.matmul(p.unsqueeze(-2), vs.transpose(-2, -1)).squeeze(-2)  # [B,m,N,hd]
         outs.append(o)
         if return_lse:
             lses.append(torch.logsumexp(scores, dim=-1))
-    out = torch.cat(outs, dim=1).permute(0, 2, 1, 3).reshape(B, N, D)
+    out = torch.cat(outs, dim=1).permute(0, 2, 1, 3).reshape(B, Nq, D)
     if return_lse:
         return out, torch.cat(lses, dim=1)
     return out
@@ -213,7 +221,8 @@ def param_shapes(D: int, nh: int, kernel_size: Sequence[int]) -> Dict[str, Tuple
 def dsa3d_module_ref(x: Tensor, params: Dict[str, Tensor], video_shape: Sequence[int],
                      num_heads: int, kernel_size: Sequence[int] = (3, 7, 7),
                      offset_scale: float = 1.0, head_chunk: Optional[int] = None,
-                     offsets: Optional[Tensor] = None) -> Tensor:
+                     offsets: Optional[Tensor] = None,
+                     extra_kv: Optional[Tensor] = None) -> Tensor:
     """Whole-module forward, attention.py:82-192 (dropout p = 0).
 
     ``offsets`` ([B, N, C], unscaled) replaces ``offset_net(x)`` when given, the
@@ -224,6 +233,10 @@ def dsa3d_module_ref(x: Tensor, params: Dict[str, Tensor], video_shape: Sequence
     q = F.linear(x, params["q_proj.weight"], params["q_proj.bias"])
     k = F.linear(x, params["k_proj.weight"], params["k_proj.bias"])
     v = F.linear(x, params["v_proj.weight"], params["v_proj.bias"])
+    ek = ev = None
+    if extra_kv is not None:
+        ek = F.linear(extra_kv, params["k_proj.weight"], params["k_proj.bias"])
+        ev = F.linear(extra_kv, params["v_proj.weight"], params["v_proj.bias"])
     a = dsa3d_core_ref(q, k, v, off, video_shape, num_heads, kernel_size, offset_scale,
-                       head_chunk=head_chunk)
+                       head_chunk=head_chunk, extra_k=ek, extra_v=ev)
     return F.linear(a, params["out_proj.weight"], params["out_proj.bias"]) + dw

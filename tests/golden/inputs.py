@@ -100,6 +100,8 @@ CASES = [
          mode="net", seed=19, on_std=0.5),
     dict(name="k355_b2", B=2, T=3, H=4, W=5, D=12, nh=3, kernel=(3, 5, 5), scale=0.5,
          mode="inject", seed=20, off_std=2.0, huge_frac=0.02),
+    dict(name="k355_extra", B=2, T=3, H=4, W=5, D=12, nh=3, kernel=(3, 5, 5), scale=1.0,
+         mode="net", seed=21, on_std=0.4, extra_g=4),
 ]
 
 # The tiny forward configuration run on the reference CPU path: B=1, T=8,
@@ -128,6 +130,9 @@ def case_params(case):
         if case.get("huge_frac", 0.0) > 0:
             mask = g.uniform(size=off.shape) < case["huge_frac"]
             off = np.where(mask, np.sign(off) * 50.0, off)
-    return p, x, gy, off
+    extra = None
+    if case.get("extra_g", 0) > 0:
+        extra = g.normal(0.0, 1.0, size=(case["B"], case["extra_g"], case["D"]))
+    return p, x, gy, off, extra
 
 

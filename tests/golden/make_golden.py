@@ -66,7 +66,7 @@ class _Inject(torch.nn.Module):
 
 
 def run_case(Ref, case, dtype):
-    p, x_np, gy_np, off_np = case_params(case)
+    p, x_np, gy_np, off_np, extra_np = case_params(case)
     B, T, H, W, D, nh = (case[k] for k in ("B", "T", "H", "W", "D", "nh"))
     N = T * H * W
     mod = Ref(D, nh, kernel_size=tuple(case["kernel"]), offset_scale=case["scale"], dropout=0.0)
@@ -106,12 +106,17 @@ def run_case(Ref, case, dtype):
 
     x = torch.from_numpy(x_np).to(dtype).requires_grad_(True)
     gy = torch.from_numpy(gy_np).to(dtype)
-    y = mod(x, (T, H, W))
+    extra = None
+    if extra_np is not None:
+        extra = torch.from_numpy(extra_np).to(dtype).requires_grad_(True)
+    y = mod(x, (T, H, W), extra_kv=extra)
     (y * gy).sum().backward()
 
     out = {}
     out["y"] = y.detach()
     out["dx"] = x.grad
+    if extra is not None:
+        out["dextra_kv"] = extra.grad
     for n, prm in mod.named_parameters():
         out["grad." + n] = prm.grad if prm.grad is not None else torch.zeros_like(prm)
     if off_np is not None:
@@ -129,7 +134,8 @@ def run_case(Ref, case, dtype):
     meta = dict(case, dtype=str(dtype).replace("torch.", ""), param_names=names,
                 x_sum=float(x_np.sum()), gy_sum=float(gy_np.sum()),
                 param_sums={k: float(v.sum()) for k, v in p.items()},
-                off_sum=None if off_np is None else float(off_np.sum()))
+                off_sum=None if off_np is None else float(off_np.sum()),
+                extra_sum=None if extra_np is None else float(extra_np.sum()))
     return meta, {k: v.detach().contiguous().numpy() for k, v in out.items()}
 
 

@@ -22,14 +22,16 @@ def load(name: str):
 def regenerate(meta):
     """Inputs of a case from its seed, checked against the sums in the fixture."""
     case = next(c for c in list(CASES) + [C1] if c["name"] == meta["name"])
-    p, x, gy, off = case_params(case)
+    p, x, gy, off, extra = case_params(case)
     assert abs(float(x.sum()) - meta["x_sum"]) < 1e-9
     assert abs(float(gy.sum()) - meta["gy_sum"]) < 1e-9
     for k, v in p.items():
         assert abs(float(v.sum()) - meta["param_sums"][k]) < 1e-9, k
     if off is not None:
         assert abs(float(off.sum()) - meta["off_sum"]) < 1e-6
-    return case, p, x, gy, off
+    if extra is not None:
+        assert abs(float(extra.sum()) - meta["extra_sum"]) < 1e-9
+    return case, p, x, gy, off, extra
 
 
 def rel_err(a, b, floor: float = 1e-12) -> float:

@@ -1,0 +1,113 @@
+"""C ABI checks that need no GPU: the library loads, exports every symbol the
+header declares, and rejects bad arguments with a status and a message before
+any device work."""
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch  # noqa: F401  (binds the library's HIP runtime dependency to torch's)
+
+from megaslide_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "megaslide_dsa3d.h")
+
+pytestmark = pytest.mark.skipif(not os.path.exists(_lib.LIB_PATH),
+                                reason="HIP library not built (python -m megaslide_amd.csrc.build)")
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(msd_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_exports_match_header():
+    lib = _lib.load()
+    declared = header_functions()
+    assert declared == sorted(_lib.EXPORTS)
+    for name in declared:
+        assert hasattr(lib, name), name
+
+
+def test_abi_version():
+    assert _lib.load().msd_abi_version() == _lib.ABI_VERSION == 1
+
+
+def _desc(**kw):
+    d = dict(B=1, T=4, H=5, W=6, num_heads=2, head_dim=64, kt=3, kh=7, kw=7, dtype=0,
+             q_stride=128, k_stride=128, v_stride=128, offset_scale=1.0, softmax_scale=0.125)
+    d.update(kw)
+    return _lib.DsaDesc(**d)
+
+
+def _fwd(desc, ptrs=(16, 16, 16, 16, 16), lse=None):
+    lib = _lib.load()
+    return lib.msd_dsa3d_fwd(ctypes.byref(desc) if desc is not None else None, *ptrs, lse, None)
+
+
+def test_null_desc_rejected():
+    lib = _lib.load()
+    assert lib.msd_dsa3d_fwd(None, 16, 16, 16, 16, 16, None, None) == -1
+    assert b"desc is NULL" in lib.msd_last_error()
+
+
+@pytest.mark.parametrize("field,value,code,needle", [
+    ("T", 0, -1, b"bad shape"),
+    ("num_heads", 0, -1, b"bad heads"),
+    ("head_dim", 4096, -2, b"head_dim"),
+    ("kt", 0, -1, b"bad window"),
+    ("dtype", 7, -2, b"dtype"),
+    ("q_stride", 64, -1, b"strides"),
+])
+def test_bad_desc_fields(field, value, code, needle):
+    rc = _fwd(_desc(**{field: value}))
+    assert rc == code
+    assert needle in _lib.load().msd_last_error()
+
+
+def test_null_and_misaligned_pointers():
+    lib = _lib.load()
+    assert _fwd(_desc(), ptrs=(16, None, 16, 16, 16)) == -1
+    assert b"NULL" in lib.msd_last_error()
+    assert _fwd(_desc(), ptrs=(16, 18, 16, 16, 16)) == -3  # fp32 needs 4-byte alignment
+    assert _fwd(_desc(dtype=1), ptrs=(16, 17, 16, 16, 16)) == -3
+
+
+def test_empty_batch_is_a_no_op():
+    assert _fwd(_desc(B=0)) == 0
+
+
+def test_workspace_size_and_check():
+    lib = _lib.load()
+    d = _desc(B=2)
+    need = lib.msd_dsa3d_bwd_workspace_size(ctypes.byref(d))
+    assert need == 2 * 2 * 4 * 5 * 6 * 128 * 4
+    rc = lib.msd_dsa3d_bwd(ctypes.byref(d), *([16] * 12), None, need - 1, None)
+    assert rc == -4 and b"workspace" in lib.msd_last_error()
+    assert lib.msd_dsa3d_bwd_workspace_size(None) == 0
+
+
+def test_dwconv_validation():
+    lib = _lib.load()
+    d = _lib.ConvDesc(1, 4, 5, 6, 32, 3, 7, 7, 0, 0)
+    bad = _lib.ConvDesc(1, 4, 5, 6, 32, 3, 6, 7, 0, 0)  # even kernel
+    assert lib.msd_dwconv3d_fwd(ctypes.byref(bad), 16, 16, None, 16, None) == -2
+    assert b"odd" in lib.msd_last_error()
+    assert lib.msd_dwconv3d_fwd(ctypes.byref(d), 16, None, None, 16, None) == -1
+    gelu = _lib.ConvDesc(2, 4, 5, 6, 32, 3, 3, 3, 1, 1)
+    ws = lib.msd_dwconv3d_bwd_workspace_size(ctypes.byref(gelu))
+    assert ws >= 4 * (2 * 4 * 5 * 6 * 32 + 32 * 28)
+    assert lib.msd_dwconv3d_bwd(ctypes.byref(gelu), 16, 16, 16, 16, 16, 16, 16, None, ws,
+                                None) == -4
+
+
+def test_module_rejects_cpu_tensors():
+    from megaslide_amd import DeformableSlideAttention3D
+    m = DeformableSlideAttention3D(16, 2, kernel_size=(3, 3, 3))
+    with pytest.raises(RuntimeError, match="ROCm"):
+        m(torch.randn(1, 8, 16), (2, 2, 2))
+    with pytest.raises(AssertionError):
+        m(torch.randn(1, 9, 16), (2, 2, 2))

@@ -1,0 +1,238 @@
+"""Parity of the HIP attention core and module against the reference (GPU).
+
+Tolerances, relative error = max|a-b| / max|b|
+(tests/goldens.py:rel_err):
+  * fp32 kernels vs the float64 reference / oracle: 1e-4;
+  * bf16 kernels vs the float64 oracle evaluated on the bf16-rounded inputs: 2e-2.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from goldens import C1, CASES, load, regenerate, rel_err
+from oracle.dsa3d_ref import PARAM_NAMES, dsa3d_core_ref, dsa3d_module_ref
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+FP32_TOL = 1e-4
+BF16_TOL = 2e-2
+
+
+def dev(a, dtype=torch.float32):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV, dtype)
+
+
+def core():
+    from megaslide_amd import dsa3d_core
+    return dsa3d_core
+
+
+def _grad_or_zero(t):
+    return t.grad if t.grad is not None else torch.zeros_like(t)
+
+
+@pytest.mark.parametrize("name", [c["name"] for c in CASES if "extra_g" not in c])
+def test_core_fp32_matches_reference_goldens(name):
+    meta, arrs = load(name)
+    case, _, _, _, off_np, _ = regenerate(meta)
+    print(f"[core golden] {name}", flush=True)
+    off_src = off_np if off_np is not None else arrs["offsets"]
+    q, k, v, off = (dev(a).requires_grad_(True) for a in (arrs["q"], arrs["k"], arrs["v"], off_src))
+    out = core()(q, k, v, off, (case["T"], case["H"], case["W"]), case["nh"], case["kernel"],
+                 case["scale"])
+    out.backward(dev(arrs["dattn"]))
+    torch.cuda.synchronize()
+    assert rel_err(out.detach().cpu(), arrs["attn"]) < FP32_TOL
+    # floor: dq/dk vanish identically on a 1x1x1 grid
+    assert rel_err(q.grad.cpu(), arrs["dq"], floor=1e-6) < FP32_TOL
+    assert rel_err(k.grad.cpu(), arrs["dk"], floor=1e-6) < FP32_TOL
+    assert rel_err(v.grad.cpu(), arrs["dv"]) < FP32_TOL
+    assert rel_err(off.grad.cpu(), arrs["doffsets"], floor=1e-6) < FP32_TOL
+
+
+def _module_from_case(case, p, dtype=torch.float32):
+    from megaslide_amd import DeformableSlideAttention3D
+    m = DeformableSlideAttention3D(case["D"], case["nh"], kernel_size=tuple(case["kernel"]),
+                                   offset_scale=case["scale"])
+    with torch.no_grad():
+        for n, prm in m.named_parameters():
+            prm.copy_(torch.from_numpy(p[n]))
+    return m.to(DEV, dtype)
+
+
+@pytest.mark.parametrize("name", [c["name"] for c in CASES if c["mode"] == "net"])
+def test_module_fp32_matches_reference_goldens(name):
+    meta, arrs = load(name)
+    case, p, x_np, gy_np, _, extra_np = regenerate(meta)
+    print(f"[module golden] {name}", flush=True)
+    m = _module_from_case(case, p)
+    x = dev(x_np).requires_grad_(True)
+    extra = None if extra_np is None else dev(extra_np).requires_grad_(True)
+    y = m(x, (case["T"], case["H"], case["W"]), extra_kv=extra)
+    (y * dev(gy_np)).sum().backward()
+    torch.cuda.synchronize()
+    assert rel_err(y.detach().cpu(), arrs["y"]) < FP32_TOL
+    assert rel_err(x.grad.cpu(), arrs["dx"]) < FP32_TOL
+    if extra is not None:
+        assert rel_err(extra.grad.cpu(), arrs["dextra_kv"]) < FP32_TOL
+    for n, prm in m.named_parameters():
+        assert rel_err(_grad_or_zero(prm).cpu(), arrs["grad." + n], floor=1e-6) < FP32_TOL, n
+
+
+def test_c1_forward_fp32_matches_reference_rows():
+    meta, arrs = load("c1_fwd_fp32")
+    case, p, x_np, _, _, _ = regenerate(meta)
+    print("[c1 forward]", flush=True)
+    m = _module_from_case(case, p)
+    with torch.no_grad():
+        y = m(dev(x_np), (case["T"], case["H"], case["W"]))
+    torch.cuda.synchronize()
+    rows = torch.from_numpy(arrs["rows"])
+    assert rel_err(y[:, rows.to(DEV)].cpu(), arrs["y_rows"]) < FP32_TOL
+
+
+def _oracle_core(q, k, v, off, vs, nh, ks, scale, dout, query_index=None, head_chunk=4):
+    """float64 oracle fwd + autograd bwd on CPU copies of the given tensors."""
+    qq, kk, vv, oo = (t.detach().double().cpu().requires_grad_(True) for t in (q, k, v, off))
+    out = dsa3d_core_ref(qq, kk, vv, oo, vs, nh, ks, scale, head_chunk=head_chunk,
+                         query_index=query_index)
+    out.backward(dout.detach().double().cpu())
+    return out.detach(), _grad_or_zero(qq), _grad_or_zero(kk), _grad_or_zero(vv), _grad_or_zero(oo)
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, FP32_TOL), (torch.bfloat16, BF16_TOL)])
+@pytest.mark.parametrize("shape", [
+    # B, T, H, W, nh, hd, kernel, off_std, scale
+    (2, 4, 12, 12, 2, 64, (3, 7, 7), 1.5, 1.0),
+    (1, 5, 9, 11, 3, 32, (3, 5, 5), 2.0, 0.7),
+    (1, 3, 6, 10, 2, 96, (3, 7, 7), 0.5, 1.0),
+    (1, 2, 5, 7, 1, 128, (3, 7, 7), 4.0, 1.0),
+])
+def test_core_vs_oracle_random(shape, dtype, tol):
+    B, T, H, W, nh, hd, ks, off_std, scale = shape
+    print(f"[core oracle] {shape} {dtype}", flush=True)
+    N, D = T * H * W, nh * hd
+    C = nh * ks[0] * ks[1] * ks[2] * 3
+    g = torch.Generator().manual_seed(1234 + N + hd)
+    q, k, v = (torch.randn(B, N, D, generator=g) for _ in range(3))
+    off = torch.randn(B, N, C, generator=g) * off_std
+    dout = torch.randn(B, N, D, generator=g)
+    # the bf16 kernels see bf16-rounded inputs; the oracle sees the same values in float64
+    q, k, v, off, dout = (t.to(dtype) for t in (q, k, v, off, dout))
+    ref = _oracle_core(q, k, v, off, (T, H, W), nh, ks, scale, dout)
+    qd, kd, vd, od = (t.to(DEV).requires_grad_(True) for t in (q, k, v, off))
+    out = core()(qd, kd, vd, od, (T, H, W), nh, ks, scale)
+    out.backward(dout.to(DEV))
+    torch.cuda.synchronize()
+    assert out.dtype == dtype
+    assert rel_err(out.detach().float().cpu(), ref[0]) < tol
+    assert rel_err(qd.grad.float().cpu(), ref[1]) < tol
+    assert rel_err(kd.grad.float().cpu(), ref[2]) < tol
+    assert rel_err(vd.grad.float().cpu(), ref[3]) < tol
+    assert rel_err(od.grad.float().cpu(), ref[4]) < tol
+
+
+@pytest.mark.parametrize("cfg", [
+    # name, dtype, B, T, H, W, nh, hd, off_std
+    ("fp32 B2 16x32x32 8x64", torch.float32, 2, 16, 32, 32, 8, 64, 1.5),
+    ("bf16 65536 tokens 16x64", torch.bfloat16, 1, 64, 32, 32, 16, 64, 0.5),
+])
+def test_core_full_size_sampled_queries_and_checksums(cfg):
+    """Full-size shapes: exact per-query parity on sampled queries (fwd, dq,
+    d offsets) plus size-independent checksums of dK and dV.
+
+    Sum over voxels of dV equals the sum over queries of dO (per channel),
+    because every query's tap weights p_k * w_c sum to one; the sum of dK is
+    zero because sum_k ds_k = 0.
+    """
+    name, dtype, B, T, H, W, nh, hd, off_std = cfg
+    print(f"[full size] {name}", flush=True)
+    ks = (3, 7, 7)
+    N, D = T * H * W, nh * hd
+    C = nh * 147 * 3
+    g = torch.Generator(device=DEV).manual_seed(7)
+    q, k, v = (torch.randn(B, N, D, generator=g, device=DEV).to(dtype) for _ in range(3))
+    off = (torch.randn(B, N, C, generator=g, device=DEV) * off_std).to(dtype)
+    dout = torch.randn(B, N, D, generator=g, device=DEV).to(dtype)
+    qd, kd, vd, od = (t.clone().requires_grad_(True) for t in (q, k, v, off))
+    out = core()(qd, kd, vd, od, (T, H, W), nh, ks, 1.0)
+    out.backward(dout)
+    torch.cuda.synchronize()
+    tol = FP32_TOL if dtype == torch.float32 else BF16_TOL
+    # checksums over every voxel
+    sum_dv = vd.grad.double().sum(dim=1)
+    sum_do = dout.double().sum(dim=1)
+    assert rel_err(sum_dv.cpu(), sum_do.cpu()) < (1e-5 if dtype == torch.float32 else 1e-2)
+    sum_dk = kd.grad.double().sum(dim=1).abs().max().item()
+    scale_dk = kd.grad.double().abs().sum(dim=1).max().item()
+    assert sum_dk < (1e-5 if dtype == torch.float32 else 1e-2) * scale_dk
+    # exact parity for sampled queries (first, last, random) against the float64 oracle
+    idx = torch.cat([torch.tensor([0, N - 1]), torch.randperm(N, generator=torch.Generator().manual_seed(3))[:30]])
+    ref_out, ref_dq, _, _, ref_doff = _oracle_core(
+        q.float(), k.float(), v.float(), off.float(), (T, H, W), nh, ks, 1.0,
+        dout.float()[:, idx], query_index=idx, head_chunk=2)
+    assert rel_err(out.detach()[:, idx.to(DEV)].float().cpu(), ref_out) < tol
+    qgrad = qd.grad[:, idx.to(DEV)].float().cpu()
+    ref_dq_rows = ref_dq[:, idx]
+    assert rel_err(qgrad, ref_dq_rows) < tol
+    assert rel_err(od.grad[:, idx.to(DEV)].float().cpu(), ref_doff[:, idx]) < tol
+
+
+def test_nograd_forward_matches_grad_forward_and_streams():
+    B, T, H, W, nh, hd = 1, 3, 8, 8, 2, 64
+    N, D, C = T * H * W, nh * hd, nh * 147 * 3
+    g = torch.Generator(device=DEV).manual_seed(5)
+    q, k, v = (torch.randn(B, N, D, generator=g, device=DEV) for _ in range(3))
+    off = torch.randn(B, N, C, generator=g, device=DEV)
+    with torch.no_grad():
+        a = core()(q, k, v, off, (T, H, W), nh)
+    b = core()(q.requires_grad_(True), k, v, off, (T, H, W), nh)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        c = core()(q.detach(), k, v, off, (T, H, W), nh)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b.detach())
+    assert torch.equal(a, c)
+
+
+def test_strided_qkv_views():
+    """q, k, v as column slices of one fused [B, N, 3D] projection output."""
+    B, T, H, W, nh, hd = 1, 3, 6, 7, 2, 32
+    N, D, C = T * H * W, nh * hd, nh * 147 * 3
+    g = torch.Generator(device=DEV).manual_seed(9)
+    qkv = torch.randn(B, N, 3 * D, generator=g, device=DEV, requires_grad=True)
+    off = torch.randn(B, N, C, generator=g, device=DEV)
+    q, k, v = qkv.split(D, dim=-1)
+    out = core()(q, k, v, off, (T, H, W), nh)
+    out.sum().backward()
+    qkv2 = qkv.detach().clone().requires_grad_(True)
+    q2, k2, v2 = (t.contiguous() for t in qkv2.split(D, dim=-1))
+    out2 = core()(q2, k2, v2, off, (T, H, W), nh)
+    out2.sum().backward()
+    torch.cuda.synchronize()
+    assert rel_err(out.detach().cpu(), out2.detach().cpu()) < 1e-6
+    assert rel_err(qkv.grad.cpu(), qkv2.grad.cpu()) < 1e-5
+
+
+def test_invariant_constant_values():
+    """A constant V volume gives that constant for any q and offsets."""
+    B, T, H, W, nh, hd = 1, 4, 9, 9, 2, 64
+    N, D, C = T * H * W, nh * hd, nh * 147 * 3
+    g = torch.Generator(device=DEV).manual_seed(11)
+    q, k = (torch.randn(B, N, D, generator=g, device=DEV) for _ in range(2))
+    const = torch.randn(D, generator=g, device=DEV)
+    v = const.expand(B, N, D).contiguous()
+    off = torch.randn(B, N, C, generator=g, device=DEV) * 3
+    out = core()(q, k, v, off, (T, H, W), nh)
+    torch.cuda.synchronize()
+    assert rel_err(out.cpu(), const.expand(B, N, D).cpu()) < 1e-5
+
+
+def test_cpu_tensor_raises():
+    with pytest.raises(RuntimeError, match="ROCm"):
+        core()(torch.zeros(1, 8, 16), torch.zeros(1, 8, 16), torch.zeros(1, 8, 16),
+               torch.zeros(1, 8, 2 * 27 * 3), (2, 2, 2), 2, (3, 3, 3))

@@ -26,7 +26,7 @@ def _core_inputs(case, arrs, off_np):
 @pytest.mark.parametrize("name", NAMES)
 def test_module_restatement_matches_reference(name):
     meta, arrs = load(name)
-    case, p, x_np, gy_np, off_np = regenerate(meta)
+    case, p, x_np, gy_np, off_np, extra_np = regenerate(meta)
     assert tuple(meta["param_names"]) == PARAM_NAMES
     shapes = param_shapes(case["D"], case["nh"], case["kernel"])
     params = {}
@@ -35,11 +35,14 @@ def test_module_restatement_matches_reference(name):
         params[n] = torch.from_numpy(p[n]).requires_grad_(True)
     x = torch.from_numpy(x_np).requires_grad_(True)
     off = None if off_np is None else torch.from_numpy(off_np)
+    extra = None if extra_np is None else torch.from_numpy(extra_np).requires_grad_(True)
     y = dsa3d_module_ref(x, params, (case["T"], case["H"], case["W"]), case["nh"],
-                         case["kernel"], case["scale"], offsets=off)
+                         case["kernel"], case["scale"], offsets=off, extra_kv=extra)
     (y * torch.from_numpy(gy_np)).sum().backward()
     assert rel_err(y.detach(), arrs["y"]) < 1e-10
     assert rel_err(x.grad, arrs["dx"]) < 1e-10
+    if extra is not None:
+        assert rel_err(extra.grad, arrs["dextra_kv"]) < 1e-10
     for n in PARAM_NAMES:
         if "grad." + n not in arrs:  # offset_net replaced by injected offsets
             assert off is not None and n.startswith("offset_net")
@@ -51,7 +54,9 @@ def test_module_restatement_matches_reference(name):
 @pytest.mark.parametrize("name", NAMES)
 def test_core_restatement_matches_reference(name):
     meta, arrs = load(name)
-    case, _, _, _, off_np = regenerate(meta)
+    case, p, _, _, off_np, extra_np = regenerate(meta)
+    if extra_np is not None:
+        pytest.skip("core-level fixture intermediates exclude the extra keys")
     q, k, v, off = (a.clone().requires_grad_(True) for a in _core_inputs(case, arrs, off_np))
     out, lse = dsa3d_core_ref(q, k, v, off, (case["T"], case["H"], case["W"]), case["nh"],
                               case["kernel"], case["scale"], return_lse=True)
@@ -75,7 +80,7 @@ def test_bruteforce_closed_form_matches_reference(name):
     mapping) against the reference's autograd.
     """
     meta, arrs = load(name)
-    case, _, _, _, off_np = regenerate(meta)
+    case, _, _, _, off_np, _ = regenerate(meta)
     q, k, v, off = (a.numpy() for a in _core_inputs(case, arrs, off_np))
     out, dq, dk, dv, doff = bruteforce.dsa3d_core_bruteforce(
         q, k, v, off, (case["T"], case["H"], case["W"]), case["nh"], case["kernel"],
@@ -90,7 +95,7 @@ def test_bruteforce_closed_form_matches_reference(name):
 
 def test_c1_forward_fp32_matches_reference():
     meta, arrs = load("c1_fwd_fp32")
-    case, p, x_np, _, _ = regenerate(meta)
+    case, p, x_np, _, _, _ = regenerate(meta)
     params = {n: torch.from_numpy(p[n]).float() for n in PARAM_NAMES}
     x = torch.from_numpy(x_np).float()
     with torch.no_grad():
