@@ -41,13 +41,29 @@ struct CoreArgs {
   int64_t N;           // tokens per sample
   int B, T, H, W, nh, hd, kt, kh, kw, C;
   float offset_scale, softmax_scale;
-  float rdiv_x, rdiv_y, rdiv_z;  // 1/(T-1), 1/(H-1), 1/(W-1) for slots 0,1,2 (0 if dim==1)
+  float div_x, div_y, div_z;     // T-1, H-1, W-1: divisors of slots 0, 1, 2 (0 if that dim is 1)
+  float rdiv_x, rdiv_y, rdiv_z;  // their reciprocals (0 if the dim is 1), for the gradient
 };
+
+// The sampling coordinate is computed op for op in fp32 as the reference does
+// it, with every operation rounded on its own (no FMA contraction, true
+// division): at coordinates that land exactly on a voxel the trilinear
+// gradient is discontinuous, so the corner choice must round identically.
+//   base: 2*(p + c) / max(S-1, 1) - 1          (attention.py:228-230)
+//   grid: base + (o * offset_scale) / (dim-1)  (:106, :118-127)
+//   u   : ((grid + 1) * S - 1) / 2             (grid_sample, align_corners=False)
 
 // Base grid value of one axis, in fp32 and in the reference's op order.
 __device__ __forceinline__ float base_coord(int p, int c, int S) {
+#pragma clang fp contract(off)
   const float pos = static_cast<float>(p) + static_cast<float>(c);
   return 2.0f * pos / static_cast<float>(S > 1 ? S - 1 : 1) - 1.0f;
+}
+
+// grid value: base + offset / divisor (divisor 0 means the slot is dropped).
+__device__ __forceinline__ float grid_coord(float base, float o, float divisor) {
+#pragma clang fp contract(off)
+  return divisor > 0.0f ? base + o / divisor : base;
 }
 
 struct Axis {
@@ -58,6 +74,7 @@ struct Axis {
 };
 
 __device__ __forceinline__ Axis axis_sample(float g, int S) {
+#pragma clang fp contract(off)
   Axis a;
   a.u = ((g + 1.0f) * static_cast<float>(S) - 1.0f) * 0.5f;
   // fmaxf returns the non-NaN operand, so a NaN coordinate lands on 0.
@@ -116,9 +133,9 @@ __global__ __launch_bounds__(kBlock) void dsa3d_fwd_direct_kernel(CoreArgs a, T*
         const float bx = base_coord(w, kk - a.kw / 2, a.W);
         float o0, o1, o2;
         load_offsets(op + kap * 3, a.offset_scale, o0, o1, o2);
-        const Axis ax = axis_sample(bx + o0 * a.rdiv_x, a.W);
-        const Axis ay = axis_sample(by + o1 * a.rdiv_y, a.H);
-        const Axis az = axis_sample(bz + o2 * a.rdiv_z, a.T);
+        const Axis ax = axis_sample(grid_coord(bx, o0, a.div_x), a.W);
+        const Axis ay = axis_sample(grid_coord(by, o1, a.div_y), a.H);
+        const Axis az = axis_sample(grid_coord(bz, o2, a.div_z), a.T);
         float ksum[CPL], vsum[CPL];
 #pragma unroll
         for (int j = 0; j < CPL; ++j) ksum[j] = vsum[j] = 0.0f;
@@ -211,9 +228,9 @@ __global__ __launch_bounds__(kBlock) void dsa3d_bwd_direct_kernel(
         const float bx = base_coord(w, kk - a.kw / 2, a.W);
         float o0, o1, o2;
         load_offsets(op + kap * 3, a.offset_scale, o0, o1, o2);
-        const Axis ax = axis_sample(bx + o0 * a.rdiv_x, a.W);
-        const Axis ay = axis_sample(by + o1 * a.rdiv_y, a.H);
-        const Axis az = axis_sample(bz + o2 * a.rdiv_z, a.T);
+        const Axis ax = axis_sample(grid_coord(bx, o0, a.div_x), a.W);
+        const Axis ay = axis_sample(grid_coord(by, o1, a.div_y), a.H);
+        const Axis az = axis_sample(grid_coord(bz, o2, a.div_z), a.T);
         float ksum[CPL];
         float pk[8], pv[8];
         int64_t rows[8];
@@ -328,6 +345,9 @@ CoreArgs make_args(const msd_dsa3d_desc& d, const void* q, const void* k, const 
   a.C = d.num_heads * d.kt * d.kh * d.kw * 3;
   a.offset_scale = d.offset_scale;
   a.softmax_scale = d.softmax_scale;
+  a.div_x = d.T > 1 ? static_cast<float>(d.T - 1) : 0.0f;
+  a.div_y = d.H > 1 ? static_cast<float>(d.H - 1) : 0.0f;
+  a.div_z = d.W > 1 ? static_cast<float>(d.W - 1) : 0.0f;
   a.rdiv_x = d.T > 1 ? 1.0f / static_cast<float>(d.T - 1) : 0.0f;
   a.rdiv_y = d.H > 1 ? 1.0f / static_cast<float>(d.H - 1) : 0.0f;
   a.rdiv_z = d.W > 1 ? 1.0f / static_cast<float>(d.W - 1) : 0.0f;
