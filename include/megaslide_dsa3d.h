@@ -63,7 +63,15 @@ typedef struct msd_dsa3d_desc {
   int64_t v_stride;            /* ... of v, dv                                    */
   float offset_scale;          /* reference offset_scale (attention.py:106)       */
   float softmax_scale;         /* 1/sqrt(head_dim) in the reference (:176)        */
+  int32_t algo;                /* msd_algo: kernel family (MSD_ALGO_AUTO default) */
+  int32_t reserved;            /* must be 0                                       */
 } msd_dsa3d_desc;
+
+/* Kernel family for the attention core.  AUTO picks the matrix-core tiled
+ * kernels when the call qualifies (bf16, head_dim 64, window <= 160 taps,
+ * 16-byte aligned rows) and the direct kernels otherwise.  DIRECT and TILED
+ * force one family (TILED fails with MSD_ERR_UNSUPPORTED if not eligible). */
+typedef enum msd_algo { MSD_ALGO_AUTO = 0, MSD_ALGO_DIRECT = 1, MSD_ALGO_TILED = 2 } msd_algo;
 
 /* Shape and options of one depthwise-conv call. */
 typedef struct msd_dwconv3d_desc {

@@ -44,7 +44,11 @@ class DsaDesc(ctypes.Structure):
         ("dtype", ctypes.c_int32),
         ("q_stride", ctypes.c_int64), ("k_stride", ctypes.c_int64), ("v_stride", ctypes.c_int64),
         ("offset_scale", ctypes.c_float), ("softmax_scale", ctypes.c_float),
+        ("algo", ctypes.c_int32), ("reserved", ctypes.c_int32),
     ]
+
+
+ALGOS = {"auto": 0, "direct": 1, "tiled": 2}
 
 
 class ConvDesc(ctypes.Structure):

@@ -43,6 +43,8 @@ int check_dsa(const msd_dsa3d_desc* d) {
     return fail(MSD_ERR_ARG, "dsa3d: bad window (%d, %d, %d)", d->kt, d->kh, d->kw);
   if (d->dtype != MSD_F32 && d->dtype != MSD_BF16)
     return fail(MSD_ERR_UNSUPPORTED, "dsa3d: dtype %d not supported", d->dtype);
+  if (d->algo < MSD_ALGO_AUTO || d->algo > MSD_ALGO_TILED || d->reserved != 0)
+    return fail(MSD_ERR_ARG, "dsa3d: bad algo %d / reserved %d", d->algo, d->reserved);
   const int64_t D = static_cast<int64_t>(d->num_heads) * d->head_dim;
   if (d->q_stride < D || d->k_stride < D || d->v_stride < D)
     return fail(MSD_ERR_ARG, "dsa3d: token strides (%lld, %lld, %lld) below D=%lld",
@@ -95,9 +97,17 @@ int msd_dsa3d_fwd(const msd_dsa3d_desc* desc, const void* q, const void* k, cons
   rc = check_ptrs("dsa3d_fwd", elem_bytes(desc->dtype), {q, k, v, offsets, out});
   if (rc != MSD_OK) return rc;
   if (lse != nullptr && !aligned(lse, 4)) return fail(MSD_ERR_ALIGN, "dsa3d_fwd: lse misaligned");
+  const bool tiled_ok = msd::dsa3d_tiled_supported(*desc, q, k, v);
+  if (desc->algo == MSD_ALGO_TILED && !tiled_ok)
+    return fail(MSD_ERR_UNSUPPORTED,
+                "dsa3d_fwd: tiled kernels need bf16, head_dim 64, <= 160 taps and 16-byte aligned "
+                "rows");
   if (desc->B == 0) return MSD_OK;
-  return launch_status(msd::launch_dsa3d_fwd(*desc, q, k, v, offsets, out, lse,
-                                             static_cast<hipStream_t>(stream)),
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (tiled_ok && desc->algo != MSD_ALGO_DIRECT)
+    return launch_status(msd::launch_dsa3d_fwd_tiled(*desc, q, k, v, offsets, out, lse, s),
+                         "dsa3d_fwd");
+  return launch_status(msd::launch_dsa3d_fwd_direct(*desc, q, k, v, offsets, out, lse, s),
                        "dsa3d_fwd");
 }
 
@@ -123,7 +133,7 @@ int msd_dsa3d_bwd(const msd_dsa3d_desc* desc, const void* q, const void* k, cons
   if (need > 0 && (workspace == nullptr || workspace_bytes < need || !aligned(workspace, 16)))
     return fail(MSD_ERR_WORKSPACE, "dsa3d_bwd: workspace of %zu bytes (16-aligned) needed, got %zu",
                 need, workspace == nullptr ? size_t(0) : workspace_bytes);
-  return launch_status(msd::launch_dsa3d_bwd(*desc, q, k, v, offsets, out, dout, lse, dlse, dq,
+  return launch_status(msd::launch_dsa3d_bwd_direct(*desc, q, k, v, offsets, out, dout, lse, dlse, dq,
                                              dk, dv, doffsets, workspace,
                                              static_cast<hipStream_t>(stream)),
                        "dsa3d_bwd");

@@ -23,7 +23,7 @@ LIB_DIR = os.path.join(PKG, "lib")
 LIB_NAME = "libmegaslide_dsa3d.so"
 OBJ_DIR = os.path.join(ROOT, "_build", "obj")
 
-SOURCES = ["abi.hip", "dsa3d_direct.hip", "dwconv3d.hip"]
+SOURCES = ["abi.hip", "dsa3d_direct.hip", "dsa3d_tiled.hip", "dwconv3d.hip"]
 
 ARCH = os.environ.get("MSD_OFFLOAD_ARCH", "gfx950")
 

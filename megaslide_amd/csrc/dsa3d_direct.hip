@@ -23,6 +23,7 @@
 // zeroed where u <= 0 or u >= S-1 (border clamp), times S/2 (unnormalise),
 // divided by the slot's divisor and times offset_scale.
 #include "common.h"
+#include "dsa3d_coords.h"
 
 namespace msd {
 
@@ -44,47 +45,6 @@ struct CoreArgs {
   float div_x, div_y, div_z;     // T-1, H-1, W-1: divisors of slots 0, 1, 2 (0 if that dim is 1)
   float rdiv_x, rdiv_y, rdiv_z;  // their reciprocals (0 if the dim is 1), for the gradient
 };
-
-// The sampling coordinate is computed op for op in fp32 as the reference does
-// it, with every operation rounded on its own (no FMA contraction, true
-// division): at coordinates that land exactly on a voxel the trilinear
-// gradient is discontinuous, so the corner choice must round identically.
-//   base: 2*(p + c) / max(S-1, 1) - 1          (attention.py:228-230)
-//   grid: base + (o * offset_scale) / (dim-1)  (:106, :118-127)
-//   u   : ((grid + 1) * S - 1) / 2             (grid_sample, align_corners=False)
-
-// Base grid value of one axis, in fp32 and in the reference's op order.
-__device__ __forceinline__ float base_coord(int p, int c, int S) {
-#pragma clang fp contract(off)
-  const float pos = static_cast<float>(p) + static_cast<float>(c);
-  return 2.0f * pos / static_cast<float>(S > 1 ? S - 1 : 1) - 1.0f;
-}
-
-// grid value: base + offset / divisor (divisor 0 means the slot is dropped).
-__device__ __forceinline__ float grid_coord(float base, float o, float divisor) {
-#pragma clang fp contract(off)
-  return divisor > 0.0f ? base + o / divisor : base;
-}
-
-struct Axis {
-  int i0;      // lower corner index (0 <= i0 <= S-1)
-  bool hi_ok;  // upper corner i0+1 inside the volume
-  float f;     // weight of the upper corner
-  float u;     // unnormalised, unclamped coordinate (for the clamp gradient)
-};
-
-__device__ __forceinline__ Axis axis_sample(float g, int S) {
-#pragma clang fp contract(off)
-  Axis a;
-  a.u = ((g + 1.0f) * static_cast<float>(S) - 1.0f) * 0.5f;
-  // fmaxf returns the non-NaN operand, so a NaN coordinate lands on 0.
-  const float c = fminf(fmaxf(a.u, 0.0f), static_cast<float>(S - 1));
-  const float fl = floorf(c);
-  a.i0 = min(max(static_cast<int>(fl), 0), S - 1);
-  a.f = c - fl;
-  a.hi_ok = (a.i0 + 1) < S;
-  return a;
-}
 
 template <typename T>
 __device__ __forceinline__ void load_offsets(const T* p, float scale, float& o0, float& o1,
@@ -417,14 +377,14 @@ size_t dsa3d_bwd_ws_bytes(const msd_dsa3d_desc& d) {
   return static_cast<size_t>(2 * rows * d.num_heads * d.head_dim) * sizeof(float);
 }
 
-hipError_t launch_dsa3d_fwd(const msd_dsa3d_desc& d, const void* q, const void* k, const void* v,
+hipError_t launch_dsa3d_fwd_direct(const msd_dsa3d_desc& d, const void* q, const void* k, const void* v,
                             const void* off, void* out, float* lse, hipStream_t s) {
   const CoreArgs a = make_args(d, q, k, v, off);
   if (d.dtype == MSD_BF16) return fwd_typed<bf16>(d, a, out, lse, s);
   return fwd_typed<float>(d, a, out, lse, s);
 }
 
-hipError_t launch_dsa3d_bwd(const msd_dsa3d_desc& d, const void* q, const void* k, const void* v,
+hipError_t launch_dsa3d_bwd_direct(const msd_dsa3d_desc& d, const void* q, const void* k, const void* v,
                             const void* off, const void* out, const void* dout, const float* lse,
                             const float* dlse, void* dq, void* dk, void* dv, void* doff,
                             void* ws, hipStream_t s) {

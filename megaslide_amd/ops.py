@@ -48,129 +48,121 @@ def _tokens_major(t: Tensor, B: int, N: int, D: int) -> Tensor:
     return t.contiguous()
 
 
-def _dsa_desc(B, T, H, W, nh, hd, kernel_size, dtype, qs, ks, vs, offset_scale) -> _lib.DsaDesc:
-    kt, kh, kw = kernel_size
-    return _lib.DsaDesc(B, T, H, W, nh, hd, kt, kh, kw, _lib.dtype_code(dtype), qs, ks, vs,
-                        float(offset_scale), 1.0 / math.sqrt(hd))
+class _CoreCall:
+    """Validated shapes of one attention-core call and its C descriptor."""
 
-
-class DSA3DCoreFunction(torch.autograd.Function):
-    """out, lse = core(q, k, v, offsets); both outputs differentiable."""
-
-    @staticmethod
-    def forward(ctx, q, k, v, offsets, video_shape, num_heads, kernel_size, offset_scale):
-        dev = _require_device(q, k, v, offsets)
+    def __init__(self, q, k, v, offsets, video_shape, num_heads, kernel_size, offset_scale, algo):
+        self.dev = _require_device(q, k, v, offsets)
         B, N, D = q.shape
         T, H, W = (int(s) for s in video_shape)
         if N != T * H * W:
             raise ValueError(f"N={N} but T*H*W={T * H * W}")
         if D % num_heads != 0:
             raise ValueError(f"D={D} not divisible by num_heads={num_heads}")
-        hd = D // num_heads
         kt, kh, kw = (int(s) for s in kernel_size)
         C = num_heads * kt * kh * kw * 3
         dt = q.dtype
         for name, t in (("k", k), ("v", v), ("offsets", offsets)):
             if t.dtype != dt:
                 raise TypeError(f"dsa3d_core: {name} is {t.dtype}, q is {dt}")
-        q = _tokens_major(q, B, N, D)
-        k = _tokens_major(k, B, N, D)
-        v = _tokens_major(v, B, N, D)
         if offsets.shape != (B, N, C):
             raise ValueError(f"offsets must be {(B, N, C)}, got {tuple(offsets.shape)}")
-        offsets = offsets.contiguous()
-        desc = _dsa_desc(B, T, H, W, num_heads, hd, (kt, kh, kw), dt, q.stride(1), k.stride(1),
-                         v.stride(1), offset_scale)
-        out = torch.empty((B, N, D), dtype=dt, device=dev)
-        lse = torch.empty((B, N, num_heads), dtype=torch.float32, device=dev)
+        if algo not in _lib.ALGOS:
+            raise ValueError(f"algo must be one of {sorted(_lib.ALGOS)}")
+        self.q = _tokens_major(q, B, N, D)
+        self.k = _tokens_major(k, B, N, D)
+        self.v = _tokens_major(v, B, N, D)
+        self.off = offsets.contiguous()
+        self.B, self.N, self.D, self.T, self.H, self.W = B, N, D, T, H, W
+        self.nh, self.hd = num_heads, D // num_heads
+        self.ksz = (kt, kh, kw)
+        self.dtype = dt
+        self.offset_scale = float(offset_scale)
+        self.algo = algo
+
+    def desc(self, qs=None, ks=None, vs=None) -> _lib.DsaDesc:
+        kt, kh, kw = self.ksz
+        return _lib.DsaDesc(
+            self.B, self.T, self.H, self.W, self.nh, self.hd, kt, kh, kw,
+            _lib.dtype_code(self.dtype),
+            self.q.stride(1) if qs is None else qs,
+            self.k.stride(1) if ks is None else ks,
+            self.v.stride(1) if vs is None else vs,
+            self.offset_scale, 1.0 / math.sqrt(self.hd), _lib.ALGOS[self.algo], 0)
+
+    def forward(self, want_lse: bool):
+        out = torch.empty((self.B, self.N, self.D), dtype=self.dtype, device=self.dev)
+        lse = (torch.empty((self.B, self.N, self.nh), dtype=torch.float32, device=self.dev)
+               if want_lse else None)
+        desc = self.desc()
         lib = _lib.load()
-        with torch.cuda.device(dev):
-            _lib.check(lib.msd_dsa3d_fwd(ctypes.byref(desc), q.data_ptr(), k.data_ptr(), v.data_ptr(),
-                                         offsets.data_ptr(), out.data_ptr(), lse.data_ptr(),
-                                         _lib.stream_handle(dev)), "dsa3d_fwd")
-        ctx.desc_args = (B, T, H, W, num_heads, hd, (kt, kh, kw), dt, offset_scale)
-        ctx.save_for_backward(q, k, v, offsets, out, lse)
+        with torch.cuda.device(self.dev):
+            _lib.check(lib.msd_dsa3d_fwd(ctypes.byref(desc), self.q.data_ptr(), self.k.data_ptr(),
+                                         self.v.data_ptr(), self.off.data_ptr(), out.data_ptr(),
+                                         _lib.ptr(lse), _lib.stream_handle(self.dev)), "dsa3d_fwd")
+        return out, lse
+
+
+class DSA3DCoreFunction(torch.autograd.Function):
+    """out, lse = core(q, k, v, offsets); both outputs differentiable."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, offsets, video_shape, num_heads, kernel_size, offset_scale, algo):
+        call = _CoreCall(q, k, v, offsets, video_shape, num_heads, kernel_size, offset_scale, algo)
+        out, lse = call.forward(want_lse=True)
+        ctx.call = (call.B, call.T, call.H, call.W, call.nh, call.hd, call.ksz, call.dtype,
+                    call.offset_scale, algo)
+        ctx.save_for_backward(call.q, call.k, call.v, call.off, out, lse)
         return out, lse
 
     @staticmethod
     def backward(ctx, dout, dlse):
         q, k, v, offsets, out, lse = ctx.saved_tensors
-        B, T, H, W, nh, hd, ksz, dt, offset_scale = ctx.desc_args
+        B, T, H, W, nh, hd, ksz, dt, offset_scale, algo = ctx.call
         dev = q.device
-        N = T * H * W
-        D = nh * hd
+        N, D = T * H * W, nh * hd
         if dout is None:
             dout = torch.zeros_like(out)
         dout = dout.to(dt).contiguous()
         if dlse is not None:
             dlse = dlse.to(torch.float32).contiguous()
+        # gradients are written with the token strides of the desc: contiguous here
+        qc, kc, vc = (t if t.stride(1) == D else t.contiguous() for t in (q, k, v))
+        call = _CoreCall(qc, kc, vc, offsets, (T, H, W), nh, ksz, offset_scale, algo)
+        desc = call.desc(D, D, D)
         dq = torch.empty((B, N, D), dtype=dt, device=dev)
         dk = torch.empty((B, N, D), dtype=dt, device=dev)
         dv = torch.empty((B, N, D), dtype=dt, device=dev)
         doff = torch.empty_like(offsets)
-        # grads are written with the token strides given in the desc: contiguous here
-        desc = _dsa_desc(B, T, H, W, nh, hd, ksz, dt, D, D, D, offset_scale)
-        qc, kc, vc = (t if t.stride(1) == D else t.contiguous() for t in (q, k, v))
         lib = _lib.load()
         ws_bytes = lib.msd_dsa3d_bwd_workspace_size(ctypes.byref(desc))
         ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
         with torch.cuda.device(dev):
             _lib.check(lib.msd_dsa3d_bwd(
                 ctypes.byref(desc), qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), offsets.data_ptr(),
-                out.data_ptr(), dout.data_ptr(), lse.data_ptr(),
-                None if dlse is None else dlse.data_ptr(),
+                out.data_ptr(), dout.data_ptr(), lse.data_ptr(), _lib.ptr(dlse),
                 dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), doff.data_ptr(),
                 ws.data_ptr(), ws_bytes, _lib.stream_handle(dev)), "dsa3d_bwd")
-        return dq, dk, dv, doff, None, None, None, None
+        return dq, dk, dv, doff, None, None, None, None, None
 
 
 def dsa3d_core(q: Tensor, k: Tensor, v: Tensor, offsets: Tensor, video_shape: Sequence[int],
                num_heads: int, kernel_size: Sequence[int] = (3, 7, 7), offset_scale: float = 1.0,
-               return_lse: bool = False):
+               return_lse: bool = False, algo: str = "auto"):
     """Attention core on device tensors.
 
     q, k, v: [B, N, D]; offsets: [B, N, num_heads*kt*kh*kw*3] unscaled, channel
     order [head][i][j][k][slot] (the reference's offsets.view order,
     attention.py:109).  Returns out [B, N, D] (and lse [B, N, num_heads]).
+    ``algo``: "auto" (default), "direct" or "tiled" kernel family.
     """
-    if not (torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v, offsets))):
-        return _dsa3d_core_nograd(q, k, v, offsets, video_shape, num_heads, kernel_size,
-                                  offset_scale, return_lse)
-    out, lse = DSA3DCoreFunction.apply(q, k, v, offsets, tuple(video_shape), int(num_heads),
-                                       tuple(kernel_size), float(offset_scale))
-    return (out, lse) if return_lse else out
-
-
-def _dsa3d_core_nograd(q, k, v, offsets, video_shape, num_heads, kernel_size, offset_scale,
-                       return_lse):
-    """Forward only: no saved tensors, no lse unless asked for."""
-    dev = _require_device(q, k, v, offsets)
-    B, N, D = q.shape
-    T, H, W = (int(s) for s in video_shape)
-    if N != T * H * W:
-        raise ValueError(f"N={N} but T*H*W={T * H * W}")
-    hd = D // num_heads
-    kt, kh, kw = (int(s) for s in kernel_size)
-    C = num_heads * kt * kh * kw * 3
-    dt = q.dtype
-    for name, t in (("k", k), ("v", v), ("offsets", offsets)):
-        if t.dtype != dt:
-            raise TypeError(f"dsa3d_core: {name} is {t.dtype}, q is {dt}")
-    q = _tokens_major(q, B, N, D)
-    k = _tokens_major(k, B, N, D)
-    v = _tokens_major(v, B, N, D)
-    if offsets.shape != (B, N, C):
-        raise ValueError(f"offsets must be {(B, N, C)}, got {tuple(offsets.shape)}")
-    offsets = offsets.contiguous()
-    desc = _dsa_desc(B, T, H, W, num_heads, hd, (kt, kh, kw), dt, q.stride(1), k.stride(1),
-                     v.stride(1), offset_scale)
-    out = torch.empty((B, N, D), dtype=dt, device=dev)
-    lse = torch.empty((B, N, num_heads), dtype=torch.float32, device=dev) if return_lse else None
-    lib = _lib.load()
-    with torch.cuda.device(dev):
-        _lib.check(lib.msd_dsa3d_fwd(ctypes.byref(desc), q.data_ptr(), k.data_ptr(), v.data_ptr(),
-                                     offsets.data_ptr(), out.data_ptr(), _lib.ptr(lse),
-                                     _lib.stream_handle(dev)), "dsa3d_fwd")
+    if torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v, offsets)):
+        out, lse = DSA3DCoreFunction.apply(q, k, v, offsets, tuple(video_shape), int(num_heads),
+                                           tuple(kernel_size), float(offset_scale), algo)
+        return (out, lse) if return_lse else out
+    # forward only: nothing saved, no lse unless asked for
+    call = _CoreCall(q, k, v, offsets, video_shape, num_heads, kernel_size, offset_scale, algo)
+    out, lse = call.forward(want_lse=return_lse)
     return (out, lse) if return_lse else out
 
 

@@ -253,3 +253,42 @@ def test_cpu_tensor_raises():
     with pytest.raises(RuntimeError, match="ROCm"):
         core()(torch.zeros(1, 8, 16), torch.zeros(1, 8, 16), torch.zeros(1, 8, 16),
                torch.zeros(1, 8, 2 * 27 * 3), (2, 2, 2), 2, (3, 3, 3))
+
+
+@pytest.mark.parametrize("shape", [
+    # B, T, H, W, nh, kernel, off_std, scale  (head_dim 64, bf16: the matrix-core kernels)
+    (1, 3, 7, 9, 2, (3, 7, 7), 0.5, 1.0),     # grid not a multiple of the 4x4 tile
+    (2, 4, 8, 8, 1, (3, 5, 5), 1.5, 0.8),
+    (1, 2, 5, 6, 2, (1, 3, 3), 0.7, 1.0),
+    (1, 5, 12, 40, 1, (3, 7, 7), 8.0, 1.0),   # large offsets: corner boxes span several chunks
+    (1, 1, 4, 4, 2, (3, 3, 3), 1.0, 1.0),     # T = 1
+])
+def test_tiled_forward_vs_oracle_and_direct(shape):
+    B, T, H, W, nh, ks, off_std, scale = shape
+    print(f"[tiled fwd] {shape}", flush=True)
+    hd = 64
+    N, D = T * H * W, nh * hd
+    C = nh * ks[0] * ks[1] * ks[2] * 3
+    g = torch.Generator().manual_seed(99 + N)
+    q, k, v = (torch.randn(B, N, D, generator=g).to(torch.bfloat16) for _ in range(3))
+    off = (torch.randn(B, N, C, generator=g) * off_std).to(torch.bfloat16)
+    ref, ref_lse = dsa3d_core_ref(q.float(), k.float(), v.float(), off.float(), (T, H, W), nh, ks,
+                                  scale, return_lse=True)
+    qd, kd, vd, od = (t.to(DEV) for t in (q, k, v, off))
+    with torch.no_grad():
+        out_t, lse_t = core()(qd, kd, vd, od, (T, H, W), nh, ks, scale, return_lse=True,
+                              algo="tiled")
+        out_d, lse_d = core()(qd, kd, vd, od, (T, H, W), nh, ks, scale, return_lse=True,
+                              algo="direct")
+    torch.cuda.synchronize()
+    assert rel_err(out_t.float().cpu(), ref) < BF16_TOL
+    assert rel_err(lse_t.cpu(), ref_lse.permute(0, 2, 1)) < 1e-5
+    assert rel_err(out_t.float().cpu(), out_d.float().cpu()) < BF16_TOL
+    assert rel_err(lse_t.cpu(), lse_d.cpu()) < 1e-5
+
+
+def test_tiled_rejects_ineligible_calls():
+    q = torch.zeros(1, 8, 32, device=DEV, dtype=torch.bfloat16)  # head_dim 32
+    off = torch.zeros(1, 8, 27 * 3, device=DEV, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="tiled"):
+        core()(q, q, q, off, (2, 2, 2), 1, (3, 3, 3), algo="tiled")
