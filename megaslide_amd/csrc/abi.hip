@@ -133,9 +133,20 @@ int msd_dsa3d_bwd(const msd_dsa3d_desc* desc, const void* q, const void* k, cons
   if (need > 0 && (workspace == nullptr || workspace_bytes < need || !aligned(workspace, 16)))
     return fail(MSD_ERR_WORKSPACE, "dsa3d_bwd: workspace of %zu bytes (16-aligned) needed, got %zu",
                 need, workspace == nullptr ? size_t(0) : workspace_bytes);
-  return launch_status(msd::launch_dsa3d_bwd_direct(*desc, q, k, v, offsets, out, dout, lse, dlse, dq,
-                                             dk, dv, doffsets, workspace,
-                                             static_cast<hipStream_t>(stream)),
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  // the tiled backward also writes dq with 16-byte rows and reads out/dout rows of D
+  const bool tiled_ok = msd::dsa3d_tiled_supported(*desc, q, k, v) &&
+                        msd::dsa3d_tiled_supported(*desc, dq, dk, dv);
+  if (desc->algo == MSD_ALGO_TILED && !tiled_ok)
+    return fail(MSD_ERR_UNSUPPORTED,
+                "dsa3d_bwd: tiled kernels need bf16, head_dim 64, <= 160 taps and 16-byte aligned "
+                "rows");
+  if (tiled_ok && desc->algo != MSD_ALGO_DIRECT)
+    return launch_status(msd::launch_dsa3d_bwd_tiled(*desc, q, k, v, offsets, out, dout, lse, dlse,
+                                                     dq, dk, dv, doffsets, workspace, s),
+                         "dsa3d_bwd");
+  return launch_status(msd::launch_dsa3d_bwd_direct(*desc, q, k, v, offsets, out, dout, lse, dlse,
+                                                    dq, dk, dv, doffsets, workspace, s),
                        "dsa3d_bwd");
 }
 

@@ -94,6 +94,10 @@ bool dsa3d_tiled_supported(const msd_dsa3d_desc& d, const void* q, const void* k
 hipError_t launch_dsa3d_fwd_tiled(const msd_dsa3d_desc& d, const void* q, const void* k,
                                   const void* v, const void* off, void* out, float* lse,
                                   hipStream_t s);
+hipError_t launch_dsa3d_bwd_tiled(const msd_dsa3d_desc& d, const void* q, const void* k,
+                                  const void* v, const void* off, const void* out,
+                                  const void* dout, const float* lse, const float* dlse, void* dq,
+                                  void* dk, void* dv, void* doff, void* ws, hipStream_t s);
 size_t dsa3d_bwd_ws_bytes(const msd_dsa3d_desc& d);
 hipError_t launch_dwconv3d_fwd(const msd_dwconv3d_desc& d, const void* x, const void* w,
                                const void* b, void* y, hipStream_t s);

@@ -63,6 +63,37 @@ def test_tiled_constant_values():
     assert err < 1e-2
 
 
+@pytest.mark.parametrize("shape", [
+    # B, T, H, W, nh, kernel, off_std, scale
+    (1, 3, 7, 9, 2, (3, 7, 7), 0.5, 1.0),
+    (2, 4, 8, 8, 1, (3, 5, 5), 1.5, 0.8),
+    (1, 5, 12, 40, 1, (3, 7, 7), 8.0, 1.0),   # corner boxes span several chunks
+    (1, 1, 4, 4, 2, (3, 3, 3), 1.0, 1.0),     # T = 1
+])
+def test_tiled_backward_vs_oracle_and_direct(shape):
+    B, T, H, W, nh, ks, off_std, scale = shape
+    print(f"[tiled bwd] {shape}", flush=True)
+    q, k, v, off = _inputs(B, T, H, W, nh, ks, off_std, 300 + T * H * W)
+    g = torch.Generator().manual_seed(17)
+    dout = torch.randn(q.shape, generator=g).to(torch.bfloat16)
+    qq, kk, vv, oo = (t.float().requires_grad_(True) for t in (q, k, v, off))
+    ref = dsa3d_core_ref(qq, kk, vv, oo, (T, H, W), nh, ks, scale)
+    ref.backward(dout.float())
+    grads = {}
+    for algo in ("tiled", "direct"):
+        ts = [t.to(DEV).requires_grad_(True) for t in (q, k, v, off)]
+        out = core()(*ts, (T, H, W), nh, ks, scale, algo=algo)
+        out.backward(dout.to(DEV))
+        grads[algo] = [t.grad.float().cpu() for t in ts]
+    torch.cuda.synchronize()
+    for name, r, gt, gd in zip(("dq", "dk", "dv", "doff"), (qq.grad, kk.grad, vv.grad, oo.grad),
+                               grads["tiled"], grads["direct"]):
+        e_ref, e_dir = rel_err(gt, r), rel_err(gt, gd)
+        print(f"  {name}: vs oracle {e_ref:.2e}  vs direct {e_dir:.2e}", flush=True)
+        assert e_ref < BF16_TOL, name
+        assert e_dir < BF16_TOL, name
+
+
 def test_tiled_lse_matches_oracle():
     B, T, H, W, nh, ks = 1, 3, 8, 8, 2, (3, 7, 7)
     q, k, v, off = _inputs(B, T, H, W, nh, ks, 0.5, 7)
