@@ -5,8 +5,17 @@
 // (infinity/video/attention.py:58-65) and offset_net[0] (:71), optionally
 // followed by exact-erf GELU (offset_net[1], :72):
 //   z[p, c] = b[c] + sum_tap w[c, tap] x[p + tap - pad, c],  y = act(z).
-// Backward: dz = dy * act'(z) (z recomputed), dx[r] = sum_tap w[tap] dz[r - tap + pad],
+// Backward: dz = dy * act'(z) (z recomputed), dx = conv(dz, flipped w),
 // dw[c, tap] = sum_p dz[p, c] x[p + tap - pad, c], db[c] = sum_p dz[p, c].
+//
+// Row kernels (kw in {3, 5, 7}, kt, kh <= 7): a thread owns one channel and a
+// run of kRun consecutive outputs along W; for every (dt, dh) it loads the
+// input row segment once into registers (kRun + kw - 1 values) and applies the
+// kw taps to all kRun outputs.  A wave covers 64 consecutive channels, so every
+// load is one 128-byte (bf16) or 256-byte (fp32) segment.  The weight-gradient
+// kernel keeps all kt*kh*kw tap sums of its channel in registers over a strip
+// of rows and flushes them with one fp32 atomic per (thread, tap).
+// Other odd kernel sizes use the simple one-output-per-thread kernels.
 #include "common.h"
 
 namespace msd {
@@ -18,13 +27,165 @@ struct ConvArgs {
   int64_t N;
 };
 
-// One thread per output element (token, channel); consecutive threads take
-// consecutive channels so x loads coalesce along C.
-template <typename T, bool GELU>
-__global__ __launch_bounds__(256) void dwconv3d_fwd_kernel(ConvArgs a, const T* __restrict__ x,
-                                                           const T* __restrict__ wt,
-                                                           const T* __restrict__ bias,
-                                                           T* __restrict__ y) {
+constexpr int kRun = 16;        // outputs per thread along W
+constexpr int kRowWaves = 4;    // waves per block in the row kernels
+constexpr int kStripRows = 8;   // (b, t, h) rows per weight-gradient work item
+
+enum Epilogue { kPlain = 0, kGelu = 1, kGeluGrad = 2 };
+
+// ---------------------------------------------------------------------------
+// row kernels: forward, GELU-gradient recompute, input gradient
+// ---------------------------------------------------------------------------
+
+// out[p] = epilogue(sum_tap w[tap'] in[p + tap - pad]) with tap' = tap, or the
+// mirrored tap K-1-tap when flip (input gradient of the convolution).
+// mode kGeluGrad writes dz = dy * gelu'(z) as fp32 into out_f32.
+template <typename T, typename G, int KW, int MODE>
+__global__ __launch_bounds__(64 * kRowWaves) void dwconv_rows_kernel(
+    ConvArgs a, const G* __restrict__ in, const T* __restrict__ wt, const T* __restrict__ bias,
+    const T* __restrict__ dy, T* __restrict__ out, float* __restrict__ out_f32, int flip) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int c = blockIdx.y * 64 + lane;
+  const int runs = (a.W + kRun - 1) / kRun;
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * kRowWaves + wave;  // (b, t, h, run)
+  const int64_t items = static_cast<int64_t>(a.B) * a.T * a.H * runs;
+  if (item >= items || c >= a.C) return;
+  const int run = static_cast<int>(item % runs);
+  const int64_t bth = item / runs;
+  const int h = static_cast<int>(bth % a.H);
+  const int t = static_cast<int>((bth / a.H) % a.T);
+  const int b = static_cast<int>(bth / (static_cast<int64_t>(a.H) * a.T));
+  const int w0 = run * kRun;
+  const int K = a.kt * a.kh * KW;
+  const int pt = a.kt / 2, ph = a.kh / 2, pw = KW / 2;
+  const T* __restrict__ wc = wt + static_cast<int64_t>(c) * K;
+
+  float acc[kRun];
+  const float b0 = bias != nullptr ? ld(bias, c) : 0.0f;
+#pragma unroll
+  for (int r = 0; r < kRun; ++r) acc[r] = b0;
+
+  for (int dt = 0; dt < a.kt; ++dt) {
+    const int tt = t + dt - pt;
+    if (tt < 0 || tt >= a.T) continue;
+    for (int dh = 0; dh < a.kh; ++dh) {
+      const int hh = h + dh - ph;
+      if (hh < 0 || hh >= a.H) continue;
+      float wk[KW];
+#pragma unroll
+      for (int k = 0; k < KW; ++k) {
+        const int tap = (dt * a.kh + dh) * KW + k;
+        wk[k] = ld(wc, flip ? K - 1 - tap : tap);
+      }
+      const int64_t row = (static_cast<int64_t>(b) * a.T + tt) * a.H + hh;
+      const G* __restrict__ ir = in + row * a.W * static_cast<int64_t>(a.C) + c;
+      float xr[kRun + KW - 1];
+#pragma unroll
+      for (int j = 0; j < kRun + KW - 1; ++j) {
+        const int ww = w0 + j - pw;
+        xr[j] = (ww >= 0 && ww < a.W) ? ld(ir, static_cast<int64_t>(ww) * a.C) : 0.0f;
+      }
+#pragma unroll
+      for (int r = 0; r < kRun; ++r) {
+#pragma unroll
+        for (int k = 0; k < KW; ++k) acc[r] += wk[k] * xr[r + k];
+      }
+    }
+  }
+  const int64_t orow = ((static_cast<int64_t>(b) * a.T + t) * a.H + h) * a.W;
+#pragma unroll
+  for (int r = 0; r < kRun; ++r) {
+    const int w = w0 + r;
+    if (w >= a.W) continue;
+    const int64_t i = (orow + w) * a.C + c;
+    if (MODE == kPlain) st(out, i, acc[r]);
+    if (MODE == kGelu) st(out, i, gelu_erf(acc[r]));
+    if (MODE == kGeluGrad) out_f32[i] = ld(dy, i) * gelu_erf_grad(acc[r]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// weight / bias gradient
+// ---------------------------------------------------------------------------
+
+// acc[c*(K+1) + tap] += sum over a strip of kStripRows rows (all of W) of
+// dz[p, c] * x[p + tap - pad, c]; acc[c*(K+1) + K] += sum dz[p, c].
+template <typename T, typename G, int KT, int KH, int KW>
+__global__ __launch_bounds__(64 * kRowWaves) void dwconv_dw_rows_kernel(ConvArgs a,
+                                                                        const T* __restrict__ x,
+                                                                        const G* __restrict__ dz,
+                                                                        float* __restrict__ acc) {
+  constexpr int K = KT * KH * KW;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int c = blockIdx.y * 64 + lane;
+  const int64_t rows = static_cast<int64_t>(a.B) * a.T * a.H;
+  const int64_t r0 = (static_cast<int64_t>(blockIdx.x) * kRowWaves + wave) * kStripRows;
+  if (c >= a.C || r0 >= rows) return;
+  const int64_t r1 = r0 + kStripRows < rows ? r0 + kStripRows : rows;
+  float s[K];
+  float sb = 0.0f;
+#pragma unroll
+  for (int i = 0; i < K; ++i) s[i] = 0.0f;
+  for (int64_t bth = r0; bth < r1; ++bth) {
+    const int h = static_cast<int>(bth % a.H);
+    const int t = static_cast<int>((bth / a.H) % a.T);
+    const int b = static_cast<int>(bth / (static_cast<int64_t>(a.H) * a.T));
+    for (int w0 = 0; w0 < a.W; w0 += kRun) {
+      float g[kRun];
+      const G* __restrict__ gr = dz + (bth * a.W) * static_cast<int64_t>(a.C) + c;
+#pragma unroll
+      for (int r = 0; r < kRun; ++r) {
+        const int w = w0 + r;
+        g[r] = w < a.W ? ld(gr, static_cast<int64_t>(w) * a.C) : 0.0f;
+        sb += g[r];
+      }
+#pragma unroll
+      for (int dt = 0; dt < KT; ++dt) {
+        const int tt = t + dt - KT / 2;
+        if (tt < 0 || tt >= a.T) continue;
+#pragma unroll
+        for (int dh = 0; dh < KH; ++dh) {
+          const int hh = h + dh - KH / 2;
+          if (hh < 0 || hh >= a.H) continue;
+          const int64_t row = (static_cast<int64_t>(b) * a.T + tt) * a.H + hh;
+          const T* __restrict__ xr = x + row * a.W * static_cast<int64_t>(a.C) + c;
+          float xv[kRun + KW - 1];
+#pragma unroll
+          for (int j = 0; j < kRun + KW - 1; ++j) {
+            const int ww = w0 + j - KW / 2;
+            xv[j] = (ww >= 0 && ww < a.W) ? ld(xr, static_cast<int64_t>(ww) * a.C) : 0.0f;
+          }
+#pragma unroll
+          for (int k = 0; k < KW; ++k) {
+            float part = 0.0f;
+#pragma unroll
+            for (int r = 0; r < kRun; ++r) part += g[r] * xv[r + k];
+            s[(dt * KH + dh) * KW + k] += part;
+          }
+        }
+      }
+    }
+  }
+  float* __restrict__ ac = acc + static_cast<int64_t>(c) * (K + 1);
+#pragma unroll
+  for (int i = 0; i < K; ++i)
+    if (s[i] != 0.0f) atomicAdd(ac + i, s[i]);
+  if (sb != 0.0f) atomicAdd(ac + K, sb);
+}
+
+// ---------------------------------------------------------------------------
+// simple kernels for other kernel sizes (one output per thread)
+// ---------------------------------------------------------------------------
+
+template <typename T, typename G, int MODE>
+__global__ __launch_bounds__(256) void dwconv_simple_kernel(ConvArgs a, const G* __restrict__ in,
+                                                            const T* __restrict__ wt,
+                                                            const T* __restrict__ bias,
+                                                            const T* __restrict__ dy,
+                                                            T* __restrict__ out,
+                                                            float* __restrict__ out_f32, int flip) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   const int64_t total = static_cast<int64_t>(a.B) * a.N * a.C;
   if (i >= total) return;
@@ -47,91 +208,21 @@ __global__ __launch_bounds__(256) void dwconv3d_fwd_kernel(ConvArgs a, const T* 
         const int ww = w + dw - a.kw / 2;
         if (tt < 0 || tt >= a.T || hh < 0 || hh >= a.H || ww < 0 || ww >= a.W) continue;
         const int64_t r = static_cast<int64_t>(b) * a.N + (static_cast<int64_t>(tt) * a.H + hh) * a.W + ww;
-        acc += ld(wc, tap) * ld(x, r * a.C + c);
+        acc += ld(wc, flip ? K - 1 - tap : tap) * ld(in, r * a.C + c);
       }
     }
   }
-  st(y, i, GELU ? gelu_erf(acc) : acc);
+  if (MODE == kPlain) st(out, i, acc);
+  if (MODE == kGelu) st(out, i, gelu_erf(acc));
+  if (MODE == kGeluGrad) out_f32[i] = ld(dy, i) * gelu_erf_grad(acc);
 }
 
-// dz = dy * gelu'(z) with z recomputed; written as fp32.
-template <typename T>
-__global__ __launch_bounds__(256) void dwconv3d_gelu_dz_kernel(ConvArgs a, const T* __restrict__ x,
-                                                               const T* __restrict__ wt,
-                                                               const T* __restrict__ bias,
-                                                               const T* __restrict__ dy,
-                                                               float* __restrict__ dz) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  const int64_t total = static_cast<int64_t>(a.B) * a.N * a.C;
-  if (i >= total) return;
-  const int c = static_cast<int>(i % a.C);
-  const int64_t bn = i / a.C;
-  const int b = static_cast<int>(bn / a.N);
-  const int64_t n = bn - static_cast<int64_t>(b) * a.N;
-  const int w = static_cast<int>(n % a.W);
-  const int h = static_cast<int>((n / a.W) % a.H);
-  const int t = static_cast<int>(n / (static_cast<int64_t>(a.W) * a.H));
-  const int K = a.kt * a.kh * a.kw;
-  const T* __restrict__ wc = wt + static_cast<int64_t>(c) * K;
-  float z = bias != nullptr ? ld(bias, c) : 0.0f;
-  int tap = 0;
-  for (int dt = 0; dt < a.kt; ++dt) {
-    const int tt = t + dt - a.kt / 2;
-    for (int dh = 0; dh < a.kh; ++dh) {
-      const int hh = h + dh - a.kh / 2;
-      for (int dw = 0; dw < a.kw; ++dw, ++tap) {
-        const int ww = w + dw - a.kw / 2;
-        if (tt < 0 || tt >= a.T || hh < 0 || hh >= a.H || ww < 0 || ww >= a.W) continue;
-        const int64_t r = static_cast<int64_t>(b) * a.N + (static_cast<int64_t>(tt) * a.H + hh) * a.W + ww;
-        z += ld(wc, tap) * ld(x, r * a.C + c);
-      }
-    }
-  }
-  dz[i] = ld(dy, i) * gelu_erf_grad(z);
-}
-
-// dx[r, c] = sum_tap w[c, tap] dz[r - tap + pad, c]
-template <typename T, typename G>
-__global__ __launch_bounds__(256) void dwconv3d_dx_kernel(ConvArgs a, const G* __restrict__ dz,
-                                                          const T* __restrict__ wt,
-                                                          T* __restrict__ dx) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  const int64_t total = static_cast<int64_t>(a.B) * a.N * a.C;
-  if (i >= total) return;
-  const int c = static_cast<int>(i % a.C);
-  const int64_t bn = i / a.C;
-  const int b = static_cast<int>(bn / a.N);
-  const int64_t n = bn - static_cast<int64_t>(b) * a.N;
-  const int w = static_cast<int>(n % a.W);
-  const int h = static_cast<int>((n / a.W) % a.H);
-  const int t = static_cast<int>(n / (static_cast<int64_t>(a.W) * a.H));
-  const int K = a.kt * a.kh * a.kw;
-  const T* __restrict__ wc = wt + static_cast<int64_t>(c) * K;
-  float acc = 0.0f;
-  int tap = 0;
-  for (int dt = 0; dt < a.kt; ++dt) {
-    const int tt = t - dt + a.kt / 2;
-    for (int dh = 0; dh < a.kh; ++dh) {
-      const int hh = h - dh + a.kh / 2;
-      for (int dw = 0; dw < a.kw; ++dw, ++tap) {
-        const int ww = w - dw + a.kw / 2;
-        if (tt < 0 || tt >= a.T || hh < 0 || hh >= a.H || ww < 0 || ww >= a.W) continue;
-        const int64_t r = static_cast<int64_t>(b) * a.N + (static_cast<int64_t>(tt) * a.H + hh) * a.W + ww;
-        acc += ld(wc, tap) * ld(dz, r * a.C + c);
-      }
-    }
-  }
-  st(dx, i, acc);
-}
-
-// Partial weight/bias gradients: block (channel tile, tap, token chunk); each
-// thread one channel; fp32 atomics into acc[c * (K + 1) + tap], tap == K is the bias.
 constexpr int kChunk = 512;
 
 template <typename T, typename G>
-__global__ __launch_bounds__(64) void dwconv3d_dw_kernel(ConvArgs a, const T* __restrict__ x,
-                                                         const G* __restrict__ dz,
-                                                         float* __restrict__ acc) {
+__global__ __launch_bounds__(64) void dwconv_dw_simple_kernel(ConvArgs a, const T* __restrict__ x,
+                                                              const G* __restrict__ dz,
+                                                              float* __restrict__ acc) {
   const int c = blockIdx.x * 64 + threadIdx.x;
   const int tap = blockIdx.y;
   const int K = a.kt * a.kh * a.kw;
@@ -161,9 +252,9 @@ __global__ __launch_bounds__(64) void dwconv3d_dw_kernel(ConvArgs a, const T* __
 }
 
 template <typename T>
-__global__ __launch_bounds__(256) void dwconv3d_dw_finish_kernel(const float* __restrict__ acc,
-                                                                 int C, int K, T* __restrict__ dw,
-                                                                 T* __restrict__ db) {
+__global__ __launch_bounds__(256) void dwconv_dw_finish_kernel(const float* __restrict__ acc, int C,
+                                                               int K, T* __restrict__ dw,
+                                                               T* __restrict__ db) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= static_cast<int64_t>(C) * (K + 1)) return;
   const int c = static_cast<int>(i / (K + 1));
@@ -174,6 +265,10 @@ __global__ __launch_bounds__(256) void dwconv3d_dw_finish_kernel(const float* __
     st(db, c, acc[i]);
   }
 }
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
 
 ConvArgs make_args(const msd_dwconv3d_desc& d) {
   ConvArgs a;
@@ -189,41 +284,83 @@ ConvArgs make_args(const msd_dwconv3d_desc& d) {
   return a;
 }
 
+bool rows_ok(const ConvArgs& a) { return (a.kw == 3 || a.kw == 5 || a.kw == 7) && a.kt <= 7 && a.kh <= 7; }
+
+// conv of `in` (type G) with w (flip: mirrored taps), epilogue MODE
+template <typename T, typename G, int MODE>
+hipError_t run_conv(const ConvArgs& a, const G* in, const T* w, const T* b, const T* dy, T* out,
+                    float* out_f32, int flip, hipStream_t s) {
+  if (rows_ok(a)) {
+    const int runs = (a.W + kRun - 1) / kRun;
+    const int64_t items = static_cast<int64_t>(a.B) * a.T * a.H * runs;
+    const dim3 grid(static_cast<unsigned>((items + kRowWaves - 1) / kRowWaves),
+                    static_cast<unsigned>((a.C + 63) / 64));
+    const dim3 block(64 * kRowWaves);
+    switch (a.kw) {
+      case 3:
+        hipLaunchKernelGGL((dwconv_rows_kernel<T, G, 3, MODE>), grid, block, 0, s, a, in, w, b, dy, out,
+                           out_f32, flip);
+        break;
+      case 5:
+        hipLaunchKernelGGL((dwconv_rows_kernel<T, G, 5, MODE>), grid, block, 0, s, a, in, w, b, dy, out,
+                           out_f32, flip);
+        break;
+      default:
+        hipLaunchKernelGGL((dwconv_rows_kernel<T, G, 7, MODE>), grid, block, 0, s, a, in, w, b, dy, out,
+                           out_f32, flip);
+        break;
+    }
+  } else {
+    const int64_t total = static_cast<int64_t>(a.B) * a.N * a.C;
+    hipLaunchKernelGGL((dwconv_simple_kernel<T, G, MODE>), dim3(static_cast<unsigned>((total + 255) / 256)),
+                       dim3(256), 0, s, a, in, w, b, dy, out, out_f32, flip);
+  }
+  return hipGetLastError();
+}
+
+template <typename T, typename G>
+void run_dw(const ConvArgs& a, const T* x, const G* dz, float* acc, hipStream_t s) {
+  const int64_t rows = static_cast<int64_t>(a.B) * a.T * a.H;
+  const dim3 grid(static_cast<unsigned>((rows + kStripRows * kRowWaves - 1) / (kStripRows * kRowWaves)),
+                  static_cast<unsigned>((a.C + 63) / 64));
+  const dim3 block(64 * kRowWaves);
+  if (a.kt == 3 && a.kh == 7 && a.kw == 7) {
+    hipLaunchKernelGGL((dwconv_dw_rows_kernel<T, G, 3, 7, 7>), grid, block, 0, s, a, x, dz, acc);
+  } else if (a.kt == 3 && a.kh == 3 && a.kw == 3) {
+    hipLaunchKernelGGL((dwconv_dw_rows_kernel<T, G, 3, 3, 3>), grid, block, 0, s, a, x, dz, acc);
+  } else {
+    const int K = a.kt * a.kh * a.kw;
+    const dim3 g(static_cast<unsigned>((a.C + 63) / 64), static_cast<unsigned>(K + 1),
+                 static_cast<unsigned>((a.B * a.N + kChunk - 1) / kChunk));
+    hipLaunchKernelGGL((dwconv_dw_simple_kernel<T, G>), g, dim3(64), 0, s, a, x, dz, acc);
+  }
+}
+
 template <typename T>
 hipError_t fwd_typed(const msd_dwconv3d_desc& d, const void* x, const void* w, const void* b,
                      void* y, hipStream_t s) {
   const ConvArgs a = make_args(d);
-  const int64_t total = static_cast<int64_t>(a.B) * a.N * a.C;
-  const dim3 grid(static_cast<unsigned>((total + 255) / 256));
   if (d.act == 1)
-    hipLaunchKernelGGL((dwconv3d_fwd_kernel<T, true>), grid, dim3(256), 0, s, a,
-                       static_cast<const T*>(x), static_cast<const T*>(w),
-                       static_cast<const T*>(b), static_cast<T*>(y));
-  else
-    hipLaunchKernelGGL((dwconv3d_fwd_kernel<T, false>), grid, dim3(256), 0, s, a,
-                       static_cast<const T*>(x), static_cast<const T*>(w),
-                       static_cast<const T*>(b), static_cast<T*>(y));
-  return hipGetLastError();
+    return run_conv<T, T, kGelu>(a, static_cast<const T*>(x), static_cast<const T*>(w),
+                                 static_cast<const T*>(b), nullptr, static_cast<T*>(y), nullptr, 0, s);
+  return run_conv<T, T, kPlain>(a, static_cast<const T*>(x), static_cast<const T*>(w),
+                                static_cast<const T*>(b), nullptr, static_cast<T*>(y), nullptr, 0, s);
 }
 
 template <typename T, typename G>
 hipError_t bwd_grads(const ConvArgs& a, const void* x, const void* w, const G* dz, void* dx,
                      void* dw, void* db, float* acc, hipStream_t s) {
-  const int64_t rows = static_cast<int64_t>(a.B) * a.N;
-  const int64_t total = rows * a.C;
   const int K = a.kt * a.kh * a.kw;
   if (dx != nullptr) {
-    hipLaunchKernelGGL((dwconv3d_dx_kernel<T, G>), dim3(static_cast<unsigned>((total + 255) / 256)),
-                       dim3(256), 0, s, a, dz, static_cast<const T*>(w), static_cast<T*>(dx));
+    hipError_t e = run_conv<T, G, kPlain>(a, dz, static_cast<const T*>(w), nullptr, nullptr,
+                                          static_cast<T*>(dx), nullptr, 1, s);
+    if (e != hipSuccess) return e;
   }
   if (dw != nullptr || db != nullptr) {
     const int64_t nacc = static_cast<int64_t>(a.C) * (K + 1);
     hipLaunchKernelGGL(fill_zero_f32, dim3(fill_blocks(nacc)), dim3(256), 0, s, acc, nacc);
-    const dim3 grid(static_cast<unsigned>((a.C + 63) / 64), static_cast<unsigned>(K + 1),
-                    static_cast<unsigned>((rows + kChunk - 1) / kChunk));
-    hipLaunchKernelGGL((dwconv3d_dw_kernel<T, G>), grid, dim3(64), 0, s, a,
-                       static_cast<const T*>(x), dz, acc);
-    hipLaunchKernelGGL((dwconv3d_dw_finish_kernel<T>), dim3(static_cast<unsigned>((nacc + 255) / 256)),
+    run_dw<T, G>(a, static_cast<const T*>(x), dz, acc, s);
+    hipLaunchKernelGGL((dwconv_dw_finish_kernel<T>), dim3(static_cast<unsigned>((nacc + 255) / 256)),
                        dim3(256), 0, s, acc, a.C, K, static_cast<T*>(dw), static_cast<T*>(db));
   }
   return hipGetLastError();
@@ -238,11 +375,9 @@ hipError_t bwd_typed(const msd_dwconv3d_desc& d, const void* x, const void* w, c
   const int64_t nacc = static_cast<int64_t>(a.C) * (K + 1);
   if (d.act == 1) {
     float* dz = acc + ((nacc + 63) / 64) * 64;
-    const int64_t total = static_cast<int64_t>(a.B) * a.N * a.C;
-    hipLaunchKernelGGL((dwconv3d_gelu_dz_kernel<T>), dim3(static_cast<unsigned>((total + 255) / 256)),
-                       dim3(256), 0, s, a, static_cast<const T*>(x), static_cast<const T*>(w),
-                       static_cast<const T*>(b), static_cast<const T*>(dy), dz);
-    hipError_t e = hipGetLastError();
+    hipError_t e = run_conv<T, T, kGeluGrad>(a, static_cast<const T*>(x), static_cast<const T*>(w),
+                                             static_cast<const T*>(b), static_cast<const T*>(dy),
+                                             nullptr, dz, 0, s);
     if (e != hipSuccess) return e;
     return bwd_grads<T, float>(a, x, w, dz, dx, dw, db, acc, s);
   }
