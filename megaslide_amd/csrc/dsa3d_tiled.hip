@@ -144,26 +144,32 @@ __device__ __forceinline__ bf16x8_t load_rows_transposed(const Args& a, const Ti
   return __builtin_bit_cast(bf16x8_t, r);
 }
 
-// Column block vb of a [16 queries][voxels] table as the MFMA A operand of
-// table^T (rows = voxels 16*vb + l%16, contraction over queries 8*(l/16) + j),
-// split into bf16 hi + lo; zeros for l >= 32.
-__device__ __forceinline__ void table_cols_hilo(const float* table, int vb, int lane, bf16x8_t& hi,
-                                                bf16x8_t& lo) {
-  float v[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j)
-    v[j] = (lane >> 4) < 2 ? table[(8 * (lane >> 4) + j) * kSRow + 16 * vb + (lane & 15)] : 0.0f;
-  to_bf16x8_hilo(v, hi, lo);
+// Transposed tables [voxel][query] (row of 16 queries + 4 pad floats) used for
+// dK = B^T q and dV = A^T dO.
+constexpr int kTRow = kTQ + 4;
+
+// Rows 16*vb + l%16 of a transposed table as the MFMA A operand (contraction over
+// the 16 queries 8*(l/16) + j; zeros for l >= 32), rounded to bf16.
+__device__ __forceinline__ bf16x8_t table_t_rows(const float* table_t, int vb, int lane) {
+  if ((lane >> 4) >= 2) return zero_bf16x8();
+  return to_bf16x8(&table_t[(16 * vb + (lane & 15)) * kTRow + 8 * (lane >> 4)]);
 }
 
 __global__ __launch_bounds__(kThreads) void dsa3d_bwd_tiled_kernel(
     Args a, const bf16* __restrict__ out, const bf16* __restrict__ dout,
     const float* __restrict__ lse, const float* __restrict__ dlse, bf16* __restrict__ dq,
     float* __restrict__ dk_acc, float* __restrict__ dv_acc, bf16* __restrict__ doff) {
-  __shared__ __attribute__((aligned(16))) float s_t0[kTQ * kSRow];      // S, then A = p w
-  __shared__ __attribute__((aligned(16))) float s_t1[kTQ * kSRow];      // dP, then B = ds scale w
+  // S and dP tables [query][voxel], later overwritten by the transposed A and B
+  // tables [voxel][query]
+  __shared__ __attribute__((aligned(16))) float s_buf[2 * kChunkNV * kTRow];
   __shared__ __attribute__((aligned(16))) uint16_t s_kt[kHD * kVRow];  // K^T chunk
+  __shared__ __attribute__((aligned(16))) int s_rows[kChunkNV];        // token row (within the sample) per voxel
   __shared__ int s_red[4][6];
+  static_assert(2 * kTQ * kSRow <= 2 * kChunkNV * kTRow, "tables must fit the shared buffer");
+  float* const s_t0 = s_buf;                 // S
+  float* const s_t1 = s_buf + kTQ * kSRow;   // dP
+  float* const s_at = s_buf;                 // A^T = p w
+  float* const s_bt = s_buf + kChunkNV * kTRow;  // B^T = ds scale w
 
   const Tile tl = make_tile(a);
   const int D = a.nh * kHD;
@@ -262,61 +268,68 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_tiled_kernel(
           }
         }
         __syncthreads();
-        zero_table(s_t0, c.nvp);
-        zero_table(s_t1, c.nvp);
+        // zero the transposed A and B tables; token rows of the chunk's voxels
+        for (int e = threadIdx.x; e < c.nvp * kTRow / 4; e += kThreads) {
+          const f32x4_t zz = {0.0f, 0.0f, 0.0f, 0.0f};
+          __builtin_memcpy(&s_at[4 * e], &zz, sizeof(zz));
+          __builtin_memcpy(&s_bt[4 * e], &zz, sizeof(zz));
+        }
+        for (int vi = threadIdx.x; vi < c.nv; vi += kThreads)
+          s_rows[vi] = static_cast<int>(chunk_row(a, tl, c, z, vi) - tl.sample0);
         __syncthreads();
         {
-          float* ra = &s_t0[tl.q * kSRow];
-          float* rb = &s_t1[tl.q * kSRow];
 #pragma unroll
           for (int i = 0; i < kSlots; ++i) {
             float wz, dwz;
             if (!slot_hits(sl[i], z, c.id, wz, dwz)) continue;
             const float pz = p[i] * wz, bz = ds[i] * a.softmax_scale * wz;
             const int base = sl[i].idx & 0x1ff, dy = (sl[i].idx >> 9) & 0x1f, dx = (sl[i].idx >> 14) & 1;
-            atomicAdd(&ra[base], pz * sl[i].w00);
-            atomicAdd(&rb[base], bz * sl[i].w00);
+            float* ra = &s_at[base * kTRow + tl.q];
+            float* rb = &s_bt[base * kTRow + tl.q];
+            atomicAdd(ra, pz * sl[i].w00);
+            atomicAdd(rb, bz * sl[i].w00);
             if (dx) {
-              atomicAdd(&ra[base + 1], pz * sl[i].w01);
-              atomicAdd(&rb[base + 1], bz * sl[i].w01);
+              atomicAdd(ra + kTRow, pz * sl[i].w01);
+              atomicAdd(rb + kTRow, bz * sl[i].w01);
             }
             if (dy) {
-              atomicAdd(&ra[base + dy], pz * sl[i].w10);
-              atomicAdd(&rb[base + dy], bz * sl[i].w10);
+              atomicAdd(ra + dy * kTRow, pz * sl[i].w10);
+              atomicAdd(rb + dy * kTRow, bz * sl[i].w10);
             }
             if (dx && dy) {
-              atomicAdd(&ra[base + dy + 1], pz * sl[i].w11);
-              atomicAdd(&rb[base + dy + 1], bz * sl[i].w11);
+              atomicAdd(ra + (dy + 1) * kTRow, pz * sl[i].w11);
+              atomicAdd(rb + (dy + 1) * kTRow, bz * sl[i].w11);
             }
           }
         }
         __syncthreads();
-        // dq[q] += sum_v B[q][v] K[v]   (this wave's 16 channels)
+        // dq[q] += sum_v B[q][v] K[v] (this wave's 16 channels); B as a bf16 hi/lo
+        // pair because sum_v B[q][v] = 0 and K may carry a large common part
         for (int kc = 0; kc < c.nvp; kc += 32) {
+          float bq[8];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) bq[j] = s_bt[(kc + kq + j) * kTRow + mq];
           bf16x8_t bhi, blo, kv;
-          to_bf16x8_hilo(&s_t1[mq * kSRow + kc + kq], bhi, blo);
+          to_bf16x8_hilo(bq, bhi, blo);
           __builtin_memcpy(&kv, &s_kt[(16 * tl.wave + mq) * kVRow + kc + kq], sizeof(kv));
           dq_acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bhi, kv, dq_acc, 0, 0, 0);
           dq_acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(blo, kv, dq_acc, 0, 0, 0);
         }
         // dK[v] += sum_q B[q][v] q[q];  dV[v] += sum_q A[q][v] dO[q]  (fp32 atomics)
+        const int ch = tl.head * kHD + 16 * tl.wave + mq;
         for (int vb = 0; vb * 16 < c.nv; ++vb) {
-          bf16x8_t hi, lo;
           f32x4_t dk4 = {0.0f, 0.0f, 0.0f, 0.0f}, dv4 = {0.0f, 0.0f, 0.0f, 0.0f};
-          table_cols_hilo(s_t1, vb, tl.lane, hi, lo);
-          dk4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hi, qT, dk4, 0, 0, 0);
-          dk4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lo, qT, dk4, 0, 0, 0);
-          table_cols_hilo(s_t0, vb, tl.lane, hi, lo);
-          dv4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hi, gT, dv4, 0, 0, 0);
-          dv4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lo, gT, dv4, 0, 0, 0);
-          const int ch = tl.head * kHD + 16 * tl.wave + mq;
+          dk4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(table_t_rows(s_bt, vb, tl.lane), qT, dk4, 0, 0, 0);
+          dv4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(table_t_rows(s_at, vb, tl.lane), gT, dv4, 0, 0, 0);
+          const int v0 = 16 * vb + 4 * (tl.lane >> 4);
+          int rr[4];
+          __builtin_memcpy(rr, &s_rows[v0], sizeof(rr));
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const int vi = 16 * vb + 4 * (tl.lane >> 4) + r;
-            if (vi >= c.nv) continue;
-            const int64_t row = chunk_row(a, tl, c, z, vi);
-            if (dk4[r] != 0.0f) atomicAdd(dk_acc + row * D + ch, dk4[r]);
-            if (dv4[r] != 0.0f) atomicAdd(dv_acc + row * D + ch, dv4[r]);
+            if (v0 + r >= c.nv) continue;
+            const int64_t off = (tl.sample0 + rr[r]) * D + ch;
+            if (dk4[r] != 0.0f) atomicAdd(dk_acc + off, dk4[r]);
+            if (dv4[r] != 0.0f) atomicAdd(dv_acc + off, dv4[r]);
           }
         }
         __syncthreads();
