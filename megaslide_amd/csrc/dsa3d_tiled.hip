@@ -1,8 +1,8 @@
-// Matrix-core (tiled) 3D-DSA forward for gfx950: bf16 storage, fp32
-// accumulation, head_dim 64.
+// Matrix-core (tiled) 3D-DSA forward and backward for gfx950: bf16 storage,
+// fp32 accumulation, head_dim 64.
 //
 // One workgroup = one (batch, head, tile of 16 queries).  Instead of gathering
-// the 8 corner rows of K and V for each of a query's 147 taps, it builds dense
+// the 8 corner rows of K and V for each of a query's taps, it builds dense
 // tables on the matrix cores over the bounding box of the tile's corners, one
 // z-plane (and 16x16 chunk) at a time:
 //   pass 1:  S[q][v] = q . K[v]  (MFMA)  ->  per tap s = scale * sum_c w_c S[q][c]
@@ -11,8 +11,8 @@
 //            O[q] += A[q] . V  (MFMA, V chunk staged transposed in LDS)
 // This equals the reference's grid_sample + matmul + softmax + matmul
 // (infinity/video/attention.py:106-186) because trilinear sampling is linear in
-// the sampled rows.  Coordinates, corner choice and weights round exactly as the
-// fp32 reference does (dsa3d_coords.h).
+// the sampled rows.  Coordinates and corner choice round exactly as the fp32
+// reference does (div_rn, dsa3d_coords.h).
 #include "dsa3d_tiled_common.h"
 
 namespace msd {
@@ -25,12 +25,14 @@ __global__ __launch_bounds__(kThreads) void dsa3d_fwd_tiled_kernel(Args a, bf16*
                                                                    float* __restrict__ lse) {
   __shared__ __attribute__((aligned(16))) float s_tab[kTQ * kSRow];     // S, then A
   __shared__ __attribute__((aligned(16))) uint16_t s_vt[kHD * kVRow];  // V^T chunk
-  __shared__ int s_red[4][6];
+  __shared__ int s_red[kWaves][6];
 
   const Tile tl = make_tile(a);
   Slot sl[kSlots];
   Box box;
   setup_slots(a, tl, sl, box, s_red);
+  const int nchunks = box.ncy * box.ncx;
+  const int nit = (box.zhi - box.zlo + 1) * nchunks;
 
   bf16x8_t q0, q1;
   load_rows_operand(a, tl, a.q, a.qs, q0, q1);
@@ -40,26 +42,26 @@ __global__ __launch_bounds__(kThreads) void dsa3d_fwd_tiled_kernel(Args a, bf16*
   float sc[kSlots];
 #pragma unroll
   for (int i = 0; i < kSlots; ++i) sc[i] = 0.0f;
-  for (int z = box.zlo; z <= box.zhi; ++z) {
-    for (int cy = 0; cy < box.ncy; ++cy) {
-      for (int cx = 0; cx < box.ncx; ++cx) {
-        const Chunk c = make_chunk(box, cy, cx);
-        mfma_table(a, tl, c, z, a.k, a.ks, q0, q1, s_tab);
-        __syncthreads();
+  for (int it = 0; it < nit; ++it) {
+    const int zi = it / nchunks;
+    const int z = box.zlo + zi;
+    const Chunk c = make_chunk(box, it - zi * nchunks);
+    TableRows rows;
+    load_table_rows(a, tl, c, z, a.k, a.ks, rows);
+    store_table(tl, c, q0, q1, rows, s_tab);
+    __syncthreads();
 #pragma unroll
-        for (int i = 0; i < kSlots; ++i) {
-          float wz, dwz;
-          if (!slot_hits(sl[i], z, c.id, wz, dwz)) continue;
-          float t00, t01, t10, t11;
-          corners4(sl[i], my_row, t00, t01, t10, t11);
-          sc[i] += wz * (sl[i].w00 * t00 + sl[i].w01 * t01 + sl[i].w10 * t10 + sl[i].w11 * t11);
-        }
-        __syncthreads();
-      }
+    for (int i = 0; i < kSlots; ++i) {
+      float wz, dwz;
+      if (!slot_hits(sl[i], z, c.id, wz, dwz)) continue;
+      float t00, t01, t10, t11;
+      corners4(sl[i], my_row, t00, t01, t10, t11);
+      sc[i] = __builtin_fmaf(wz, bilerp(sl[i], t00, t01, t10, t11).val, sc[i]);
     }
+    __syncthreads();
   }
 
-  // ---- softmax over each query's taps (16 lanes x kSlots) -------------------
+  // ---- softmax over each query's taps (32 lanes x kSlots) -------------------
   float mx = -INFINITY;
 #pragma unroll
   for (int i = 0; i < kSlots; ++i) {
@@ -67,7 +69,7 @@ __global__ __launch_bounds__(kThreads) void dsa3d_fwd_tiled_kernel(Args a, bf16*
     mx = fmaxf(mx, sc[i]);
   }
 #pragma unroll
-  for (int m = 4; m <= 32; m <<= 1) mx = fmaxf(mx, __shfl_xor(mx, m));
+  for (int m = 1; m < kSubs; m <<= 1) mx = fmaxf(mx, __shfl_xor(mx, m));
   float den = 0.0f;
 #pragma unroll
   for (int i = 0; i < kSlots; ++i) {
@@ -75,63 +77,76 @@ __global__ __launch_bounds__(kThreads) void dsa3d_fwd_tiled_kernel(Args a, bf16*
     den += sc[i];
   }
 #pragma unroll
-  for (int m = 4; m <= 32; m <<= 1) den += __shfl_xor(den, m);
+  for (int m = 1; m < kSubs; m <<= 1) den += __shfl_xor(den, m);
   const float inv_den = 1.0f / den;
 #pragma unroll
   for (int i = 0; i < kSlots; ++i) sc[i] *= inv_den;  // p
   if (lse != nullptr && tl.q_ok && tl.sub == 0) lse[tl.qn * a.nh + tl.head] = mx + logf(den);
 
   // ---- pass 2: O = A . V ------------------------------------------------------
+  // wave w: output channels 16*(w & 3) + [0, 16), voxel k-steps of parity w >> 2
   const int mq = tl.lane & 15, kq = 8 * (tl.lane >> 4);
+  const int ct = tl.wave & 3, half = tl.wave >> 2;
   f32x4_t oacc = {0.0f, 0.0f, 0.0f, 0.0f};
-  for (int z = box.zlo; z <= box.zhi; ++z) {
-    for (int cy = 0; cy < box.ncy; ++cy) {
-      for (int cx = 0; cx < box.ncx; ++cx) {
-        const Chunk c = make_chunk(box, cy, cx);
-        zero_table(s_tab, c.nvp);
-        stage_transposed(a, tl, c, z, a.v, a.vs, s_vt);
-        __syncthreads();
-        float* row = &s_tab[tl.q * kSRow];
+  float* row = &s_tab[tl.q * kSRow];
+  for (int it = 0; it < nit; ++it) {
+    const int zi = it / nchunks;
+    const int z = box.zlo + zi;
+    const Chunk c = make_chunk(box, it - zi * nchunks);
+    StageRows vr;
+    load_stage_rows(a, tl, c, z, a.v, a.vs, vr);
+    zero_table(s_tab, c.nvp);
+    store_stage(c, vr, s_vt);
+    __syncthreads();
 #pragma unroll
-        for (int i = 0; i < kSlots; ++i) {
-          float wz, dwz;
-          if (!slot_hits(sl[i], z, c.id, wz, dwz)) continue;
-          const float pz = sc[i] * wz;
-          const int base = sl[i].idx & 0x1ff, dy = (sl[i].idx >> 9) & 0x1f, dx = (sl[i].idx >> 14) & 1;
-          atomicAdd(&row[base], pz * sl[i].w00);
-          if (dx) atomicAdd(&row[base + 1], pz * sl[i].w01);
-          if (dy) atomicAdd(&row[base + dy], pz * sl[i].w10);
-          if (dx && dy) atomicAdd(&row[base + dy + 1], pz * sl[i].w11);
-        }
-        __syncthreads();
-        for (int kc = 0; kc < c.nvp; kc += 32) {
-          const bf16x8_t av = to_bf16x8(&s_tab[mq * kSRow + kc + kq]);
-          bf16x8_t bv;
-          __builtin_memcpy(&bv, &s_vt[(16 * tl.wave + mq) * kVRow + kc + kq], sizeof(bv));
-          oacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv, oacc, 0, 0, 0);
-        }
-        __syncthreads();
-      }
+    for (int i = 0; i < kSlots; ++i) {
+      float wz, dwz;
+      if (!slot_hits(sl[i], z, c.id, wz, dwz)) continue;
+      const float pz = sc[i] * wz;
+      const float gx = 1.0f - sl[i].fx, gy = 1.0f - sl[i].fy;
+      const int base = sl[i].idx & 0x1ff, dy = (sl[i].idx >> 9) & 0x1f, dx = (sl[i].idx >> 14) & 1;
+      atomicAdd(&row[base], pz * (gy * gx));
+      if (dx) atomicAdd(&row[base + 1], pz * (gy * sl[i].fx));
+      if (dy) atomicAdd(&row[base + dy], pz * (sl[i].fy * gx));
+      if (dx && dy) atomicAdd(&row[base + dy + 1], pz * (sl[i].fy * sl[i].fx));
     }
+    __syncthreads();
+    for (int kc = 32 * half; kc < c.nvp; kc += 64) {
+      const bf16x8_t av = to_bf16x8(&s_tab[mq * kSRow + kc + kq]);
+      bf16x8_t bv;
+      __builtin_memcpy(&bv, &s_vt[(16 * ct + mq) * kVRow + kc + kq], sizeof(bv));
+      oacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv, oacc, 0, 0, 0);
+    }
+    __syncthreads();
   }
-  // oacc[r] = O[query 4*(lane/16) + r][channel 16*wave + lane%16]
+  // oacc[r] = partial O[query 4*(lane/16) + r][channel 16*ct + lane%16]; the two
+  // halves of the k-steps are summed through LDS
+  float* red = s_tab;  // 16 x 64
+  if (half == 1) {
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int64_t n = tile_row(a, tl, 4 * (tl.lane >> 4) + r);
-    if (n >= 0)
-      out[n * (static_cast<int64_t>(a.nh) * kHD) + tl.head * kHD + 16 * tl.wave + mq] =
-          from_f32<bf16>(oacc[r]);
+    for (int r = 0; r < 4; ++r) red[(4 * (tl.lane >> 4) + r) * kHD + 16 * ct + mq] = oacc[r];
+  }
+  __syncthreads();
+  if (half == 0) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = 4 * (tl.lane >> 4) + r;
+      const int64_t n = tile_row(a, tl, m);
+      if (n >= 0)
+        out[n * (static_cast<int64_t>(a.nh) * kHD) + tl.head * kHD + 16 * ct + mq] =
+            from_f32<bf16>(oacc[r] + red[m * kHD + 16 * ct + mq]);
+    }
   }
 }
 
 // Q^T (or dO^T) as the MFMA B operand with the 16 tile queries as the
 // contraction index: lane l holds rows k = 8*(l/16) + j of channel
-// 16*wave + l%16; lanes 32..63 (k >= 16) hold zeros.
+// 16*ct + l%16; lanes 32..63 (k >= 16) hold zeros.
 __device__ __forceinline__ bf16x8_t load_rows_transposed(const Args& a, const Tile& tl,
-                                                         const bf16* base, int64_t stride) {
+                                                         const bf16* base, int64_t stride, int ct) {
   u32x4_t r = {0u, 0u, 0u, 0u};
   if ((tl.lane >> 4) < 2) {
-    const int ch = tl.head * kHD + 16 * tl.wave + (tl.lane & 15);
+    const int ch = tl.head * kHD + 16 * ct + (tl.lane & 15);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int64_t r0 = tile_row(a, tl, 8 * (tl.lane >> 4) + 2 * i);
@@ -159,16 +174,16 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_tiled_kernel(
     Args a, const bf16* __restrict__ out, const bf16* __restrict__ dout,
     const float* __restrict__ lse, const float* __restrict__ dlse, bf16* __restrict__ dq,
     float* __restrict__ dk_acc, float* __restrict__ dv_acc, bf16* __restrict__ doff) {
-  // S and dP tables [query][voxel], later overwritten by the transposed A and B
-  // tables [voxel][query]
+  // pass 1: S and dP tables [query][voxel]; pass 2: transposed A and B tables
+  // [voxel][query]; at the end: partial dq
   __shared__ __attribute__((aligned(16))) float s_buf[2 * kChunkNV * kTRow];
   __shared__ __attribute__((aligned(16))) uint16_t s_kt[kHD * kVRow];  // K^T chunk
   __shared__ __attribute__((aligned(16))) int s_rows[kChunkNV];        // token row (within the sample) per voxel
-  __shared__ int s_red[4][6];
+  __shared__ int s_red[kWaves][6];
   static_assert(2 * kTQ * kSRow <= 2 * kChunkNV * kTRow, "tables must fit the shared buffer");
-  float* const s_t0 = s_buf;                 // S
-  float* const s_t1 = s_buf + kTQ * kSRow;   // dP
-  float* const s_at = s_buf;                 // A^T = p w
+  float* const s_t0 = s_buf;                     // S
+  float* const s_t1 = s_buf + kTQ * kSRow;       // dP
+  float* const s_at = s_buf;                     // A^T = p w
   float* const s_bt = s_buf + kChunkNV * kTRow;  // B^T = ds scale w
 
   const Tile tl = make_tile(a);
@@ -176,188 +191,183 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_tiled_kernel(
   Slot sl[kSlots];
   Box box;
   setup_slots(a, tl, sl, box, s_red);
+  const int nchunks = box.ncy * box.ncx;
+  const int nit = (box.zhi - box.zlo + 1) * nchunks;
 
   bf16x8_t q0, q1, g0, g1;
   load_rows_operand(a, tl, a.q, a.qs, q0, q1);
   load_rows_operand(a, tl, dout, D, g0, g1);
 
-  // Delta = dO . O (- dlse) and lse for this lane's query: 16 lanes x 4 channels
+  // Delta = dO . O (- dlse) and lse for this lane's query: 32 lanes x 2 channels
   float delta = 0.0f, lse_q = 0.0f;
   if (tl.q_ok) {
-    const int64_t base = tl.qn * D + tl.head * kHD + 4 * tl.sub;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) delta += to_f32(dout[base + j]) * to_f32(out[base + j]);
+    const int64_t base = tl.qn * D + tl.head * kHD + 2 * tl.sub;
+    delta = to_f32(dout[base]) * to_f32(out[base]) + to_f32(dout[base + 1]) * to_f32(out[base + 1]);
     lse_q = lse[tl.qn * a.nh + tl.head];
   }
 #pragma unroll
-  for (int m = 4; m <= 32; m <<= 1) delta += __shfl_xor(delta, m);
+  for (int m = 1; m < kSubs; m <<= 1) delta += __shfl_xor(delta, m);
   if (dlse != nullptr && tl.q_ok) delta -= dlse[tl.qn * a.nh + tl.head];
 
-  // ---- pass 1: scores and dp per tap -----------------------------------------
-  float p[kSlots], ds[kSlots];
+  // ---- pass 1: per tap, the interpolated S and dP and their coordinate
+  // derivatives (x, y within a plane; z across planes) -------------------------
+  float s_[kSlots], dp_[kSlots], gxs[kSlots], gxd[kSlots], gys[kSlots], gyd[kSlots], gzs[kSlots],
+      gzd[kSlots];
 #pragma unroll
-  for (int i = 0; i < kSlots; ++i) p[i] = ds[i] = 0.0f;
-  for (int z = box.zlo; z <= box.zhi; ++z) {
-    for (int cy = 0; cy < box.ncy; ++cy) {
-      for (int cx = 0; cx < box.ncx; ++cx) {
-        const Chunk c = make_chunk(box, cy, cx);
-        mfma_table(a, tl, c, z, a.k, a.ks, q0, q1, s_t0);
-        mfma_table(a, tl, c, z, a.v, a.vs, g0, g1, s_t1);
-        __syncthreads();
-        const float* r0 = &s_t0[tl.q * kSRow];
-        const float* r1 = &s_t1[tl.q * kSRow];
+  for (int i = 0; i < kSlots; ++i)
+    s_[i] = dp_[i] = gxs[i] = gxd[i] = gys[i] = gyd[i] = gzs[i] = gzd[i] = 0.0f;
+  for (int it = 0; it < nit; ++it) {
+    const int zi = it / nchunks;
+    const int z = box.zlo + zi;
+    const Chunk c = make_chunk(box, it - zi * nchunks);
+    TableRows rk, rv;
+    load_table_rows(a, tl, c, z, a.k, a.ks, rk);
+    load_table_rows(a, tl, c, z, a.v, a.vs, rv);
+    store_table(tl, c, q0, q1, rk, s_t0);
+    store_table(tl, c, g0, g1, rv, s_t1);
+    __syncthreads();
+    const float* r0 = &s_t0[tl.q * kSRow];
+    const float* r1 = &s_t1[tl.q * kSRow];
 #pragma unroll
-        for (int i = 0; i < kSlots; ++i) {
-          float wz, dwz;
-          if (!slot_hits(sl[i], z, c.id, wz, dwz)) continue;
-          float t00, t01, t10, t11;
-          corners4(sl[i], r0, t00, t01, t10, t11);
-          p[i] += wz * (sl[i].w00 * t00 + sl[i].w01 * t01 + sl[i].w10 * t10 + sl[i].w11 * t11);
-          corners4(sl[i], r1, t00, t01, t10, t11);
-          ds[i] += wz * (sl[i].w00 * t00 + sl[i].w01 * t01 + sl[i].w10 * t10 + sl[i].w11 * t11);
-        }
-        __syncthreads();
-      }
+    for (int i = 0; i < kSlots; ++i) {
+      float wz, dwz;
+      if (!slot_hits(sl[i], z, c.id, wz, dwz)) continue;
+      float t00, t01, t10, t11;
+      corners4(sl[i], r0, t00, t01, t10, t11);
+      const Bilerp bs = bilerp(sl[i], t00, t01, t10, t11);
+      corners4(sl[i], r1, t00, t01, t10, t11);
+      const Bilerp bd = bilerp(sl[i], t00, t01, t10, t11);
+      s_[i] = __builtin_fmaf(wz, bs.val, s_[i]);
+      gxs[i] = __builtin_fmaf(wz, bs.dx, gxs[i]);
+      gys[i] = __builtin_fmaf(wz, bs.dy, gys[i]);
+      gzs[i] = __builtin_fmaf(dwz, bs.val, gzs[i]);
+      dp_[i] = __builtin_fmaf(wz, bd.val, dp_[i]);
+      gxd[i] = __builtin_fmaf(wz, bd.dx, gxd[i]);
+      gyd[i] = __builtin_fmaf(wz, bd.dy, gyd[i]);
+      gzd[i] = __builtin_fmaf(dwz, bd.val, gzd[i]);
     }
-  }
-  // p = exp(scale * s - lse), ds = p (dp - Delta)
-#pragma unroll
-  for (int i = 0; i < kSlots; ++i) {
-    if (slot_z0(sl[i]) < 0) {
-      p[i] = ds[i] = 0.0f;
-      continue;
-    }
-    p[i] = __expf(p[i] * a.softmax_scale - lse_q);
-    ds[i] = p[i] * (ds[i] - delta);
+    __syncthreads();
   }
 
-  // ---- pass 2: gradients ------------------------------------------------------
-  const int mq = tl.lane & 15, kq = 8 * (tl.lane >> 4);
-  const bf16x8_t qT = load_rows_transposed(a, tl, a.q, a.qs);
-  const bf16x8_t gT = load_rows_transposed(a, tl, dout, D);
-  f32x4_t dq_acc = {0.0f, 0.0f, 0.0f, 0.0f};
-  float gx[kSlots], gy[kSlots], gz[kSlots];
-#pragma unroll
-  for (int i = 0; i < kSlots; ++i) gx[i] = gy[i] = gz[i] = 0.0f;
-  for (int z = box.zlo; z <= box.zhi; ++z) {
-    for (int cy = 0; cy < box.ncy; ++cy) {
-      for (int cx = 0; cx < box.ncx; ++cx) {
-        const Chunk c = make_chunk(box, cy, cx);
-        mfma_table(a, tl, c, z, a.k, a.ks, q0, q1, s_t0);
-        mfma_table(a, tl, c, z, a.v, a.vs, g0, g1, s_t1);
-        stage_transposed(a, tl, c, z, a.k, a.ks, s_kt);
-        __syncthreads();
-        // coordinate gradients: T_c = ds*scale*S_c + p*dP_c at the 4 corners of this plane
-        {
-          const float* r0 = &s_t0[tl.q * kSRow];
-          const float* r1 = &s_t1[tl.q * kSRow];
-#pragma unroll
-          for (int i = 0; i < kSlots; ++i) {
-            float wz, dwz;
-            if (!slot_hits(sl[i], z, c.id, wz, dwz)) continue;
-            float s00, s01, s10, s11, d00, d01, d10, d11;
-            corners4(sl[i], r0, s00, s01, s10, s11);
-            corners4(sl[i], r1, d00, d01, d10, d11);
-            const float dss = ds[i] * a.softmax_scale, pp = p[i];
-            const float t00 = dss * s00 + pp * d00, t01 = dss * s01 + pp * d01;
-            const float t10 = dss * s10 + pp * d10, t11 = dss * s11 + pp * d11;
-            const float fx = sl[i].fx, fy = sl[i].fy;
-            gx[i] += wz * ((1.0f - fy) * (t01 - t00) + fy * (t11 - t10));
-            gy[i] += wz * ((1.0f - fx) * (t10 - t00) + fx * (t11 - t01));
-            gz[i] += dwz * (sl[i].w00 * t00 + sl[i].w01 * t01 + sl[i].w10 * t10 + sl[i].w11 * t11);
-          }
-        }
-        __syncthreads();
-        // zero the transposed A and B tables; token rows of the chunk's voxels
-        for (int e = threadIdx.x; e < c.nvp * kTRow / 4; e += kThreads) {
-          const f32x4_t zz = {0.0f, 0.0f, 0.0f, 0.0f};
-          __builtin_memcpy(&s_at[4 * e], &zz, sizeof(zz));
-          __builtin_memcpy(&s_bt[4 * e], &zz, sizeof(zz));
-        }
-        for (int vi = threadIdx.x; vi < c.nv; vi += kThreads)
-          s_rows[vi] = static_cast<int>(chunk_row(a, tl, c, z, vi) - tl.sample0);
-        __syncthreads();
-        {
-#pragma unroll
-          for (int i = 0; i < kSlots; ++i) {
-            float wz, dwz;
-            if (!slot_hits(sl[i], z, c.id, wz, dwz)) continue;
-            const float pz = p[i] * wz, bz = ds[i] * a.softmax_scale * wz;
-            const int base = sl[i].idx & 0x1ff, dy = (sl[i].idx >> 9) & 0x1f, dx = (sl[i].idx >> 14) & 1;
-            float* ra = &s_at[base * kTRow + tl.q];
-            float* rb = &s_bt[base * kTRow + tl.q];
-            atomicAdd(ra, pz * sl[i].w00);
-            atomicAdd(rb, bz * sl[i].w00);
-            if (dx) {
-              atomicAdd(ra + kTRow, pz * sl[i].w01);
-              atomicAdd(rb + kTRow, bz * sl[i].w01);
-            }
-            if (dy) {
-              atomicAdd(ra + dy * kTRow, pz * sl[i].w10);
-              atomicAdd(rb + dy * kTRow, bz * sl[i].w10);
-            }
-            if (dx && dy) {
-              atomicAdd(ra + (dy + 1) * kTRow, pz * sl[i].w11);
-              atomicAdd(rb + (dy + 1) * kTRow, bz * sl[i].w11);
-            }
-          }
-        }
-        __syncthreads();
-        // dq[q] += sum_v B[q][v] K[v] (this wave's 16 channels); B as a bf16 hi/lo
-        // pair because sum_v B[q][v] = 0 and K may carry a large common part
-        for (int kc = 0; kc < c.nvp; kc += 32) {
-          float bq[8];
-#pragma unroll
-          for (int j = 0; j < 8; ++j) bq[j] = s_bt[(kc + kq + j) * kTRow + mq];
-          bf16x8_t bhi, blo, kv;
-          to_bf16x8_hilo(bq, bhi, blo);
-          __builtin_memcpy(&kv, &s_kt[(16 * tl.wave + mq) * kVRow + kc + kq], sizeof(kv));
-          dq_acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bhi, kv, dq_acc, 0, 0, 0);
-          dq_acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(blo, kv, dq_acc, 0, 0, 0);
-        }
-        // dK[v] += sum_q B[q][v] q[q];  dV[v] += sum_q A[q][v] dO[q]  (fp32 atomics)
-        const int ch = tl.head * kHD + 16 * tl.wave + mq;
-        for (int vb = 0; vb * 16 < c.nv; ++vb) {
-          f32x4_t dk4 = {0.0f, 0.0f, 0.0f, 0.0f}, dv4 = {0.0f, 0.0f, 0.0f, 0.0f};
-          dk4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(table_t_rows(s_bt, vb, tl.lane), qT, dk4, 0, 0, 0);
-          dv4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(table_t_rows(s_at, vb, tl.lane), gT, dv4, 0, 0, 0);
-          const int v0 = 16 * vb + 4 * (tl.lane >> 4);
-          int rr[4];
-          __builtin_memcpy(rr, &s_rows[v0], sizeof(rr));
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            if (v0 + r >= c.nv) continue;
-            const int64_t off = (tl.sample0 + rr[r]) * D + ch;
-            if (dk4[r] != 0.0f) atomicAdd(dk_acc + off, dk4[r]);
-            if (dv4[r] != 0.0f) atomicAdd(dv_acc + off, dv4[r]);
-          }
-        }
-        __syncthreads();
-      }
-    }
-  }
-
-  // ---- outputs ------------------------------------------------------------------
-  // dq_acc[r] = dq[query 4*(lane/16) + r][channel 16*wave + lane%16]
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int64_t n = tile_row(a, tl, 4 * (tl.lane >> 4) + r);
-    if (n >= 0) dq[n * a.qs + tl.head * kHD + 16 * tl.wave + mq] = from_f32<bf16>(dq_acc[r]);
-  }
-  // d offsets: chain the coordinate gradients through the clamp mask, the
-  // unnormalisation (S/2), the slot divisor and offset_scale
+  // p = exp(scale * s - lse), ds = p (dp - Delta).  The coordinate gradient of
+  // a tap is ds*scale*dS/du + p*dP/du; chain it through the clamp mask, the
+  // unnormalisation (S/2), the slot divisor and offset_scale into d offsets.
   const float cxs = 0.5f * a.W * a.rdiv_x * a.offset_scale;
   const float cys = 0.5f * a.H * a.rdiv_y * a.offset_scale;
   const float czs = 0.5f * a.T * a.rdiv_z * a.offset_scale;
+  float p[kSlots], bsc[kSlots];
 #pragma unroll
   for (int i = 0; i < kSlots; ++i) {
+    p[i] = bsc[i] = 0.0f;
     if (slot_z0(sl[i]) < 0) continue;
-    const int kap = tl.sub + 16 * i;
+    const float pi = __expf(s_[i] * a.softmax_scale - lse_q);
+    const float dss = pi * (dp_[i] - delta) * a.softmax_scale;
+    p[i] = pi;
+    bsc[i] = dss;
+    const int kap = tl.sub + kSubs * i;
     bf16* dp = doff + tl.qn * a.C + (static_cast<int64_t>(tl.head) * a.K + kap) * 3;
     const int m = sl[i].zc >> 17;
-    dp[0] = from_f32<bf16>((m & 1) ? gx[i] * cxs : 0.0f);
-    dp[1] = from_f32<bf16>((m & 2) ? gy[i] * cys : 0.0f);
-    dp[2] = from_f32<bf16>((m & 4) ? gz[i] * czs : 0.0f);
+    dp[0] = from_f32<bf16>((m & 1) ? (dss * gxs[i] + pi * gxd[i]) * cxs : 0.0f);
+    dp[1] = from_f32<bf16>((m & 2) ? (dss * gys[i] + pi * gyd[i]) * cys : 0.0f);
+    dp[2] = from_f32<bf16>((m & 4) ? (dss * gzs[i] + pi * gzd[i]) * czs : 0.0f);
+  }
+
+  // ---- pass 2: dq = B K, dK = B^T q, dV = A^T dO ---------------------------------
+  // wave w: channels 16*(w & 3) + [0, 16); k-steps / voxel blocks of parity w >> 2
+  const int mq = tl.lane & 15, kq = 8 * (tl.lane >> 4);
+  const int ct = tl.wave & 3, half = tl.wave >> 2;
+  const bf16x8_t qT = load_rows_transposed(a, tl, a.q, a.qs, ct);
+  const bf16x8_t gT = load_rows_transposed(a, tl, dout, D, ct);
+  const int ch = tl.head * kHD + 16 * ct + mq;
+  f32x4_t dq_acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int it = 0; it < nit; ++it) {
+    const int zi = it / nchunks;
+    const int z = box.zlo + zi;
+    const Chunk c = make_chunk(box, it - zi * nchunks);
+    StageRows kr;
+    load_stage_rows(a, tl, c, z, a.k, a.ks, kr);
+    // zero the transposed A and B tables; token rows of the chunk's voxels
+    for (int e = threadIdx.x; e < c.nvp * kTRow / 4; e += kThreads) {
+      const f32x4_t zz = {0.0f, 0.0f, 0.0f, 0.0f};
+      __builtin_memcpy(&s_at[4 * e], &zz, sizeof(zz));
+      __builtin_memcpy(&s_bt[4 * e], &zz, sizeof(zz));
+    }
+    for (int vi = threadIdx.x; vi < c.nv; vi += kThreads)
+      s_rows[vi] = static_cast<int>(chunk_row(a, tl, c, z, vi) - tl.sample0);
+    store_stage(c, kr, s_kt);
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kSlots; ++i) {
+      float wz, dwz;
+      if (!slot_hits(sl[i], z, c.id, wz, dwz)) continue;
+      const float pz = p[i] * wz, bz = bsc[i] * wz;
+      const float fx = sl[i].fx, fy = sl[i].fy, gx = 1.0f - fx, gy = 1.0f - fy;
+      const float w00 = gy * gx, w01 = gy * fx, w10 = fy * gx, w11 = fy * fx;
+      const int base = sl[i].idx & 0x1ff, dy = (sl[i].idx >> 9) & 0x1f, dx = (sl[i].idx >> 14) & 1;
+      float* ra = &s_at[base * kTRow + tl.q];
+      float* rb = &s_bt[base * kTRow + tl.q];
+      atomicAdd(ra, pz * w00);
+      atomicAdd(rb, bz * w00);
+      if (dx) {
+        atomicAdd(ra + kTRow, pz * w01);
+        atomicAdd(rb + kTRow, bz * w01);
+      }
+      if (dy) {
+        atomicAdd(ra + dy * kTRow, pz * w10);
+        atomicAdd(rb + dy * kTRow, bz * w10);
+      }
+      if (dx && dy) {
+        atomicAdd(ra + (dy + 1) * kTRow, pz * w11);
+        atomicAdd(rb + (dy + 1) * kTRow, bz * w11);
+      }
+    }
+    __syncthreads();
+    // dq[q] += sum_v B[q][v] K[v]; B as a bf16 hi/lo pair because
+    // sum_v B[q][v] = 0 and K may carry a large common part
+    for (int kc = 32 * half; kc < c.nvp; kc += 64) {
+      float bq[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) bq[j] = s_bt[(kc + kq + j) * kTRow + mq];
+      bf16x8_t bhi, blo, kv;
+      to_bf16x8_hilo(bq, bhi, blo);
+      __builtin_memcpy(&kv, &s_kt[(16 * ct + mq) * kVRow + kc + kq], sizeof(kv));
+      dq_acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bhi, kv, dq_acc, 0, 0, 0);
+      dq_acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(blo, kv, dq_acc, 0, 0, 0);
+    }
+    // dK[v] += sum_q B[q][v] q[q];  dV[v] += sum_q A[q][v] dO[q]  (fp32 atomics)
+    for (int vb = half; vb * 16 < c.nv; vb += 2) {
+      f32x4_t dk4 = {0.0f, 0.0f, 0.0f, 0.0f}, dv4 = {0.0f, 0.0f, 0.0f, 0.0f};
+      dk4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(table_t_rows(s_bt, vb, tl.lane), qT, dk4, 0, 0, 0);
+      dv4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(table_t_rows(s_at, vb, tl.lane), gT, dv4, 0, 0, 0);
+      const int v0 = 16 * vb + 4 * (tl.lane >> 4);
+      int rr[4];
+      __builtin_memcpy(rr, &s_rows[v0], sizeof(rr));
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        if (v0 + r >= c.nv) continue;
+        const int64_t off = (tl.sample0 + rr[r]) * D + ch;
+        if (dk4[r] != 0.0f) atomicAdd(dk_acc + off, dk4[r]);
+        if (dv4[r] != 0.0f) atomicAdd(dv_acc + off, dv4[r]);
+      }
+    }
+    __syncthreads();
+  }
+
+  // ---- dq: dq_acc[r] = partial dq[query 4*(lane/16) + r][channel 16*ct + lane%16];
+  // the two halves of the k-steps are summed through LDS
+  float* red = s_buf;  // 16 x 64
+  if (half == 1) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[(4 * (tl.lane >> 4) + r) * kHD + 16 * ct + mq] = dq_acc[r];
+  }
+  __syncthreads();
+  if (half == 0) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = 4 * (tl.lane >> 4) + r;
+      const int64_t n = tile_row(a, tl, m);
+      if (n >= 0) dq[n * a.qs + ch] = from_f32<bf16>(dq_acc[r] + red[m * kHD + 16 * ct + mq]);
+    }
   }
 }
 
@@ -386,6 +396,8 @@ tiled::Args make_tiled_args(const msd_dsa3d_desc& d, const void* q, const void* 
   a.C = d.num_heads * a.K * 3;
   a.tiles_h = (d.H + tiled::kTileH - 1) / tiled::kTileH;
   a.tiles_w = (d.W + tiled::kTileW - 1) / tiled::kTileW;
+  const int64_t tiles = static_cast<int64_t>(d.B) * d.T * a.tiles_h * a.tiles_w;
+  a.xcd_remap = (tiles % 8 == 0) ? static_cast<int>(tiles / 8) : 0;
   a.offset_scale = d.offset_scale;
   a.softmax_scale = d.softmax_scale;
   a.div_x = d.T > 1 ? static_cast<float>(d.T - 1) : 0.0f;
@@ -394,6 +406,14 @@ tiled::Args make_tiled_args(const msd_dsa3d_desc& d, const void* q, const void* 
   a.rdiv_x = d.T > 1 ? 1.0f / static_cast<float>(d.T - 1) : 0.0f;
   a.rdiv_y = d.H > 1 ? 1.0f / static_cast<float>(d.H - 1) : 0.0f;
   a.rdiv_z = d.W > 1 ? 1.0f / static_cast<float>(d.W - 1) : 0.0f;
+  a.bdiv_x = static_cast<float>(d.W > 1 ? d.W - 1 : 1);
+  a.bdiv_y = static_cast<float>(d.H > 1 ? d.H - 1 : 1);
+  a.bdiv_z = static_cast<float>(d.T > 1 ? d.T - 1 : 1);
+  a.rbdiv_x = 1.0f / a.bdiv_x;
+  a.rbdiv_y = 1.0f / a.bdiv_y;
+  a.rbdiv_z = 1.0f / a.bdiv_z;
+  a.r_kw = 1.0f / static_cast<float>(d.kw);
+  a.r_khkw = 1.0f / static_cast<float>(d.kh * d.kw);
   return a;
 }
 
@@ -405,8 +425,12 @@ dim3 tiled_grid(const msd_dsa3d_desc& d) {
 
 bool dsa3d_tiled_supported(const msd_dsa3d_desc& d, const void* q, const void* k, const void* v) {
   if (d.dtype != MSD_BF16 || d.head_dim != tiled::kHD) return false;
-  if (d.kt * d.kh * d.kw > 16 * tiled::kSlots) return false;
-  if (d.H > 32767 || d.W > 32767 || d.T > 32767) return false;
+  if (d.kt * d.kh * d.kw > tiled::kMaxTaps) return false;
+  if (d.T > 32767 || d.H > 32767 || d.W > 32767) return false;
+  // the chunk grid of any corner box must number fewer than kMaxChunks
+  const int64_t cy = (d.H + tiled::kChunkStep - 1) / tiled::kChunkStep + 1;
+  const int64_t cx = (d.W + tiled::kChunkStep - 1) / tiled::kChunkStep + 1;
+  if (cy * cx >= tiled::kMaxChunks) return false;
   const int64_t tiles = static_cast<int64_t>(d.B) * d.T * ((d.H + 3) / 4) * ((d.W + 3) / 4);
   if (tiles > 0x7fffffff || d.num_heads > 65535) return false;
   // 16-byte vector loads of q/k/v rows

@@ -1,8 +1,8 @@
 // Shared building blocks of the matrix-core (tiled) 3D-DSA kernels.
 //
-// A workgroup of 4 waves owns one (batch, head, tile of 16 queries = 1 frame x
-// 4 rows x 4 columns).  Lane l of wave w serves query q = 4w + (l & 3) and the
-// taps kappa = (l >> 2) + 16 i, i < kSlots.  Every tap's 2x2 (y, x) corner
+// A workgroup of 8 waves owns one (batch, head, tile of 16 queries = 1 frame x
+// 4 rows x 4 columns).  Lane l of wave w serves query q = 2w + (l >> 5) and the
+// taps kappa = (l & 31) + 32 i, i < kSlots.  Every tap's 2x2 (y, x) corner
 // footprint is resolved against per-plane score tables
 //   S[q][v] = X[q] . Y[v]   (X = q or dO rows, Y = K or V rows; MFMA, fp32 in LDS)
 // built over the (y, x) bounding box of all corners of the tile, cut into
@@ -11,6 +11,7 @@
 #pragma once
 
 #include "common.h"
+#include "div_rn.h"
 #include "dsa3d_coords.h"
 
 namespace msd {
@@ -25,11 +26,15 @@ typedef __attribute__((ext_vector_type(4))) unsigned int u32x4_t;
 constexpr int kHD = 64;                 // head_dim served by the tiled kernels
 constexpr int kTileH = 4, kTileW = 4;
 constexpr int kTQ = kTileH * kTileW;    // queries per tile
-constexpr int kThreads = 256;           // 4 waves
-constexpr int kSlots = 10;              // taps per lane: windows of <= 160 taps
+constexpr int kWaves = 8;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kSubs = 32;               // lanes per query
+constexpr int kSlots = 5;               // taps per lane: windows of <= kSubs * kSlots taps
+constexpr int kMaxTaps = kSubs * kSlots;
 constexpr int kChunk = 16;              // chunk edge in y and x
 constexpr int kChunkStep = 15;          // chunk start spacing (one voxel of overlap)
 constexpr int kChunkNV = kChunk * kChunk;
+constexpr int kMaxChunks = 1 << 16;     // chunk ids are kept in 16 bits
 // fp32 row stride of the tables: 260 = 4 (mod 64 banks), so the four row groups
 // an MFMA result writes (rows r, r+4, r+8, r+12) and the 16 rows an operand
 // read touches fall on distinct banks.
@@ -45,23 +50,28 @@ struct Args {
   int64_t N;
   int B, T, H, W, nh, kt, kh, kw, K, C;
   int tiles_h, tiles_w;
+  int xcd_remap;       // tiles per XCD when tiles are spread XCD-contiguously, else 0
   float offset_scale, softmax_scale;
   float div_x, div_y, div_z;     // divisors of offset slots 0, 1, 2 (0 = slot dropped)
-  float rdiv_x, rdiv_y, rdiv_z;  // their reciprocals (0 = slot dropped)
+  float rdiv_x, rdiv_y, rdiv_z;  // their reciprocals, rounded to nearest (0 = slot dropped)
+  float bdiv_x, bdiv_y, bdiv_z;  // base-grid divisors max(S-1, 1) of x (W), y (H), z (T)
+  float rbdiv_x, rbdiv_y, rbdiv_z;
+  float r_kw, r_khkw;            // 1/kw, 1/(kh*kw): exact small-integer division
 };
 
 // Geometry of one tap, kept in registers between the passes.
 struct Slot {
-  int zc;    // z0 (bits 0-15, -1 = empty) | hz << 16 | clamp-gradient mask x,y,z << 17..19 | chunk << 20
-  int idx;   // table index of corner (y0, x0) | dy_off << 9 | dx_off << 14
-  float w00, w01, w10, w11;  // (y, x) bilinear weights of the corners (0 outside the volume)
-  float fz;                  // weight of the upper z corner
-  float fx, fy;              // fractional parts (for coordinate gradients)
+  int zc;    // z0 (bits 0-15, -1 = empty) | hz << 16 | clamp-gradient mask x,y,z << 17..19
+  int idx;   // table index of corner (y0, x0) | dy_off << 9 | dx_off << 14 | chunk << 16
+  float fz;  // weight of the upper z corner
+  float fx, fy;  // weights of the upper x / y corners (0 when that corner is outside)
 };
 
 __device__ __forceinline__ int slot_z0(const Slot& s) { return static_cast<int16_t>(s.zc & 0xffff); }
 __device__ __forceinline__ bool slot_hz(const Slot& s) { return (s.zc >> 16) & 1; }
-__device__ __forceinline__ int slot_chunk(const Slot& s) { return s.zc >> 20; }
+__device__ __forceinline__ int slot_chunk(const Slot& s) {
+  return static_cast<int>(static_cast<uint32_t>(s.idx) >> 16);
+}
 
 struct Tile {
   int b, head, t, h0, w0;
@@ -74,7 +84,10 @@ struct Tile {
 __device__ __forceinline__ Tile make_tile(const Args& a) {
   Tile t;
   t.head = blockIdx.y;
+  // Workgroups are dispatched round-robin over the 8 XCDs; give each XCD a
+  // contiguous run of tiles so neighbouring tiles share its L2.
   int tile = blockIdx.x;
+  if (a.xcd_remap > 0) tile = (tile & 7) * a.xcd_remap + (tile >> 3);
   const int tw_i = tile % a.tiles_w;
   tile /= a.tiles_w;
   const int th_i = tile % a.tiles_h;
@@ -86,8 +99,8 @@ __device__ __forceinline__ Tile make_tile(const Args& a) {
   t.sample0 = static_cast<int64_t>(t.b) * a.N;
   t.wave = threadIdx.x >> 6;
   t.lane = threadIdx.x & 63;
-  t.q = t.wave * 4 + (t.lane & 3);
-  t.sub = t.lane >> 2;
+  t.q = 2 * t.wave + (t.lane >> 5);
+  t.sub = t.lane & 31;
   const int qh = t.h0 + t.q / kTileW, qw = t.w0 + t.q % kTileW;
   t.q_ok = qh < a.H && qw < a.W;
   t.qn = t.sample0 + (static_cast<int64_t>(t.t) * a.H + qh) * a.W + qw;
@@ -106,43 +119,63 @@ struct Box {
   int ncy, ncx;  // chunk grid
 };
 
+// Offset-free base-grid coordinate 2*(p + c)/max(S-1, 1) - 1 (attention.py:228-230).
+__device__ __forceinline__ float base_coord_rn(int p, int c, float bdiv, float rbdiv) {
+#pragma clang fp contract(off)
+  const float pos = static_cast<float>(p) + static_cast<float>(c);
+  return div_rn(2.0f * pos, bdiv, rbdiv) - 1.0f;
+}
+
+__device__ __forceinline__ float grid_coord_rn(float base, float o, float div, float rdiv) {
+#pragma clang fp contract(off)
+  return div > 0.0f ? base + div_rn(o, div, rdiv) : base;
+}
+
 // Tap geometry for all slots of this lane (coordinates exactly as the
 // reference rounds them) and the block-wide bounding box of every corner.
 __device__ __forceinline__ void setup_slots(const Args& a, const Tile& tl, Slot* sl, Box& box,
                                             int (*s_red)[6]) {
   int zlo = 1 << 30, zhi = -1, ylo = 1 << 30, yhi = -1, xlo = 1 << 30, xhi = -1;
-  int y0s[kSlots], x0s[kSlots], hys[kSlots], hxs[kSlots];
+  int y0s[kSlots], x0s[kSlots];
   const int qh = tl.h0 + tl.q / kTileW, qw = tl.w0 + tl.q % kTileW;
+  const int khkw = a.kh * a.kw;
 #pragma unroll
   for (int i = 0; i < kSlots; ++i) {
-    const int kap = tl.sub + 16 * i;
+    const int kap = tl.sub + kSubs * i;
     sl[i].zc = 0xffff;  // z0 = -1: empty
     sl[i].idx = 0;
-    sl[i].w00 = sl[i].w01 = sl[i].w10 = sl[i].w11 = sl[i].fz = sl[i].fx = sl[i].fy = 0.0f;
-    y0s[i] = x0s[i] = hys[i] = hxs[i] = 0;
+    sl[i].fz = sl[i].fx = sl[i].fy = 0.0f;
+    y0s[i] = x0s[i] = 0;
     if (!tl.q_ok || kap >= a.K) continue;
-    const int ci = kap / (a.kh * a.kw) - a.kt / 2;
-    const int cj = (kap / a.kw) % a.kh - a.kh / 2;
-    const int ck = kap % a.kw - a.kw / 2;
+    // kap = (ci*kh + cj)*kw + ck; (kap + 0.5) * (1/d) truncates exactly for kap < 2^16
+    const int ci_ = static_cast<int>((static_cast<float>(kap) + 0.5f) * a.r_khkw);
+    const int rem = kap - ci_ * khkw;
+    const int cj_ = static_cast<int>((static_cast<float>(rem) + 0.5f) * a.r_kw);
+    const int ck_ = rem - cj_ * a.kw;
+    const int ci = ci_ - a.kt / 2, cj = cj_ - a.kh / 2, ck = ck_ - a.kw / 2;
     const bf16* op = a.off + tl.qn * a.C + (static_cast<int64_t>(tl.head) * a.K + kap) * 3;
     const float o0 = to_f32(op[0]) * a.offset_scale;
     const float o1 = to_f32(op[1]) * a.offset_scale;
     const float o2 = to_f32(op[2]) * a.offset_scale;
-    const Axis ax = axis_sample(grid_coord(base_coord(qw, ck, a.W), o0, a.div_x), a.W);
-    const Axis ay = axis_sample(grid_coord(base_coord(qh, cj, a.H), o1, a.div_y), a.H);
-    const Axis az = axis_sample(grid_coord(base_coord(tl.t, ci, a.T), o2, a.div_z), a.T);
+    const Axis ax = axis_sample(grid_coord_rn(base_coord_rn(qw, ck, a.bdiv_x, a.rbdiv_x), o0,
+                                              a.div_x, a.rdiv_x), a.W);
+    const Axis ay = axis_sample(grid_coord_rn(base_coord_rn(qh, cj, a.bdiv_y, a.rbdiv_y), o1,
+                                              a.div_y, a.rdiv_y), a.H);
+    const Axis az = axis_sample(grid_coord_rn(base_coord_rn(tl.t, ci, a.bdiv_z, a.rbdiv_z), o2,
+                                              a.div_z, a.rdiv_z), a.T);
     // clamp-gradient masks: zero where u <= 0 or u >= S-1 (grid_sample border padding)
     const int mx = (ax.u > 0.0f && ax.u < static_cast<float>(a.W - 1)) ? 1 : 0;
     const int my = (ay.u > 0.0f && ay.u < static_cast<float>(a.H - 1)) ? 1 : 0;
     const int mz = (az.u > 0.0f && az.u < static_cast<float>(a.T - 1)) ? 1 : 0;
     sl[i].zc = az.i0 | (az.hi_ok << 16) | (mx << 17) | (my << 18) | (mz << 19);
+    // an upper corner outside the volume only occurs with weight 0 (the
+    // coordinate is clamped to S-1), so fx/fy/fz are 0 there
     sl[i].fx = ax.f;
     sl[i].fy = ay.f;
     sl[i].fz = az.f;
     y0s[i] = ay.i0;
     x0s[i] = ax.i0;
-    hys[i] = ay.hi_ok;
-    hxs[i] = ax.hi_ok;
+    sl[i].idx = (ay.hi_ok ? 1 : 0) | (ax.hi_ok ? 2 : 0);  // flags until the chunk is known
     zlo = min(zlo, az.i0);
     zhi = max(zhi, az.i0 + (az.hi_ok ? 1 : 0));
     ylo = min(ylo, ay.i0);
@@ -168,12 +201,28 @@ __device__ __forceinline__ void setup_slots(const Args& a, const Tile& tl, Slot*
     s_red[tl.wave][5] = xhi;
   }
   __syncthreads();
-  box.zlo = min(min(s_red[0][0], s_red[1][0]), min(s_red[2][0], s_red[3][0]));
-  box.zhi = max(max(s_red[0][1], s_red[1][1]), max(s_red[2][1], s_red[3][1]));
-  box.ylo = min(min(s_red[0][2], s_red[1][2]), min(s_red[2][2], s_red[3][2]));
-  box.yhi = max(max(s_red[0][3], s_red[1][3]), max(s_red[2][3], s_red[3][3]));
-  box.xlo = min(min(s_red[0][4], s_red[1][4]), min(s_red[2][4], s_red[3][4]));
-  box.xhi = max(max(s_red[0][5], s_red[1][5]), max(s_red[2][5], s_red[3][5]));
+  box.zlo = s_red[0][0];
+  box.zhi = s_red[0][1];
+  box.ylo = s_red[0][2];
+  box.yhi = s_red[0][3];
+  box.xlo = s_red[0][4];
+  box.xhi = s_red[0][5];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) {
+    box.zlo = min(box.zlo, s_red[w][0]);
+    box.zhi = max(box.zhi, s_red[w][1]);
+    box.ylo = min(box.ylo, s_red[w][2]);
+    box.yhi = max(box.yhi, s_red[w][3]);
+    box.xlo = min(box.xlo, s_red[w][4]);
+    box.xhi = max(box.xhi, s_red[w][5]);
+  }
+  // the same for every lane: keep it in scalar registers
+  box.zlo = __builtin_amdgcn_readfirstlane(box.zlo);
+  box.zhi = __builtin_amdgcn_readfirstlane(box.zhi);
+  box.ylo = __builtin_amdgcn_readfirstlane(box.ylo);
+  box.yhi = __builtin_amdgcn_readfirstlane(box.yhi);
+  box.xlo = __builtin_amdgcn_readfirstlane(box.xlo);
+  box.xhi = __builtin_amdgcn_readfirstlane(box.xhi);
   // chunk grid: starts lo, lo+15, ...; ceil((extent-1)/15) chunks (at least one)
   box.ncy = max(1, (box.yhi - box.ylo + kChunkStep - 1) / kChunkStep);
   box.ncx = max(1, (box.xhi - box.xlo + kChunkStep - 1) / kChunkStep);
@@ -181,18 +230,13 @@ __device__ __forceinline__ void setup_slots(const Args& a, const Tile& tl, Slot*
 #pragma unroll
   for (int i = 0; i < kSlots; ++i) {
     if (slot_z0(sl[i]) < 0) continue;
+    const bool hy = sl[i].idx & 1, hx = sl[i].idx & 2;
     const int cy = min((y0s[i] - box.ylo) / kChunkStep, box.ncy - 1);
     const int cx = min((x0s[i] - box.xlo) / kChunkStep, box.ncx - 1);
     const int cy0 = box.ylo + kChunkStep * cy, cx0 = box.xlo + kChunkStep * cx;
     const int nx = min(kChunk, box.xhi - cx0 + 1);
     const int base = (y0s[i] - cy0) * nx + (x0s[i] - cx0);
-    sl[i].idx = base | ((hys[i] ? nx : 0) << 9) | ((hxs[i] ? 1 : 0) << 14);
-    sl[i].zc |= (cy * box.ncx + cx) << 20;
-    const float fx = sl[i].fx, fy = sl[i].fy;
-    sl[i].w00 = (1.0f - fy) * (1.0f - fx);
-    sl[i].w01 = hxs[i] ? (1.0f - fy) * fx : 0.0f;
-    sl[i].w10 = hys[i] ? fy * (1.0f - fx) : 0.0f;
-    sl[i].w11 = (hys[i] && hxs[i]) ? fy * fx : 0.0f;
+    sl[i].idx = base | ((hy ? nx : 0) << 9) | ((hx ? 1 : 0) << 14) | ((cy * box.ncx + cx) << 16);
   }
 }
 
@@ -201,9 +245,10 @@ struct Chunk {
   float rnx;  // 1/nx, for division-free voxel coordinates
 };
 
-__device__ __forceinline__ Chunk make_chunk(const Box& box, int cy, int cx) {
+__device__ __forceinline__ Chunk make_chunk(const Box& box, int id) {
   Chunk c;
-  c.id = cy * box.ncx + cx;
+  c.id = id;
+  const int cy = id / box.ncx, cx = id - cy * box.ncx;
   c.cy0 = box.ylo + kChunkStep * cy;
   c.cx0 = box.xlo + kChunkStep * cx;
   c.ny = min(kChunk, box.yhi - c.cy0 + 1);
@@ -227,10 +272,10 @@ __device__ __forceinline__ bf16x8_t zero_bf16x8() {
   return __builtin_bit_cast(bf16x8_t, z);
 }
 
-__device__ __forceinline__ bf16x8_t load8(const bf16* p) {
+__device__ __forceinline__ u32x4_t load16(const bf16* p) {
   u32x4_t r;
   __builtin_memcpy(&r, p, sizeof(r));
-  return __builtin_bit_cast(bf16x8_t, r);
+  return r;
 }
 
 // Rows of the tile (queries m = lane % 16) as MFMA A operands, channels
@@ -241,55 +286,88 @@ __device__ __forceinline__ void load_rows_operand(const Args& a, const Tile& tl,
   const int64_t row = tile_row(a, tl, tl.lane & 15);
   if (row < 0) return;
   const bf16* p = base + row * stride + tl.head * kHD + 8 * (tl.lane >> 4);
-  lo = load8(p);
-  hi = load8(p + 32);
+  lo = __builtin_bit_cast(bf16x8_t, load16(p));
+  hi = __builtin_bit_cast(bf16x8_t, load16(p + 32));
 }
 
-// table[m][vi] = X[m] . Y[vi] for the chunk's voxels of plane z (X as MFMA A
-// operands, Y rows read from global).  Blocks of 16 voxels are split over waves.
-__device__ __forceinline__ void mfma_table(const Args& a, const Tile& tl, const Chunk& c, int z,
-                                           const bf16* ybase, int64_t ystride, bf16x8_t x0,
-                                           bf16x8_t x1, float* table) {
+// Y rows of a chunk as MFMA B operands, for the two 16-voxel blocks of this
+// wave (blocks w and w + 8; a chunk has at most 16 blocks).  All loads are
+// issued before any is used.
+struct TableRows {
+  u32x4_t y[2][2];  // [block][channels kq / kq + 32]
+};
+
+__device__ __forceinline__ void load_table_rows(const Args& a, const Tile& tl, const Chunk& c,
+                                                int z, const bf16* ybase, int64_t ystride,
+                                                TableRows& r) {
   const int kq = 8 * (tl.lane >> 4);
-  for (int blk = tl.wave; blk * 16 < c.nv; blk += 4) {
-    const int vi = blk * 16 + (tl.lane & 15);
-    bf16x8_t y0 = zero_bf16x8(), y1 = zero_bf16x8();
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int vi = (tl.wave + kWaves * j) * 16 + (tl.lane & 15);
+    const u32x4_t z4 = {0u, 0u, 0u, 0u};
+    r.y[j][0] = r.y[j][1] = z4;
     if (vi < c.nv) {
       const bf16* p = ybase + chunk_row(a, tl, c, z, vi) * ystride + tl.head * kHD + kq;
-      y0 = load8(p);
-      y1 = load8(p + 32);
+      r.y[j][0] = load16(p);
+      r.y[j][1] = load16(p + 32);
     }
-    f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x0, y0, acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x1, y1, acc, 0, 0, 0);
+  }
+}
+
+// table[m][vi] = X[m] . Y[vi] for the wave's blocks of the chunk.
+__device__ __forceinline__ void store_table(const Tile& tl, const Chunk& c, bf16x8_t x0,
+                                            bf16x8_t x1, const TableRows& r, float* table) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) table[(4 * (tl.lane >> 4) + r) * kSRow + vi] = acc[r];
+  for (int j = 0; j < 2; ++j) {
+    const int blk = tl.wave + kWaves * j;
+    if (blk * 16 >= c.nv) continue;
+    f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x0, __builtin_bit_cast(bf16x8_t, r.y[j][0]), acc,
+                                                  0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x1, __builtin_bit_cast(bf16x8_t, r.y[j][1]), acc,
+                                                  0, 0, 0);
+    const int vi = blk * 16 + (tl.lane & 15);
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) table[(4 * (tl.lane >> 4) + rr) * kSRow + vi] = acc[rr];
   }
 }
 
 // Chunk rows of Y (plane z) transposed into LDS: yt[channel][voxel] (bf16),
-// zero padded up to nvp voxels.
-__device__ __forceinline__ void stage_transposed(const Args& a, const Tile& tl, const Chunk& c,
-                                                 int z, const bf16* ybase, int64_t ystride,
-                                                 uint16_t* yt) {
-  // lanes walk voxel pairs fastest, so a wave's dword stores hit consecutive banks
-  for (int task = threadIdx.x; task < 8 * (kChunkNV / 2); task += kThreads) {
-    const int cg = task >> 7, vp = task & 127;
-    const int v0 = 2 * vp, v1 = v0 + 1;
-    if (v0 >= c.nvp) continue;
-    u32x4_t x0 = {0u, 0u, 0u, 0u}, x1 = {0u, 0u, 0u, 0u};
-    if (v0 < c.nv)
-      __builtin_memcpy(&x0, ybase + chunk_row(a, tl, c, z, v0) * ystride + tl.head * kHD + 8 * cg,
-                       sizeof(x0));
-    if (v1 < c.nv)
-      __builtin_memcpy(&x1, ybase + chunk_row(a, tl, c, z, v1) * ystride + tl.head * kHD + 8 * cg,
-                       sizeof(x1));
+// zero padded up to nvp voxels.  Thread t moves voxels 2*(t & 127) + {0, 1},
+// channel groups (t >> 7) and (t >> 7) + 4 (8 channels each); the four loads
+// are issued first.
+struct StageRows {
+  u32x4_t x[2][2];  // [channel group][voxel]
+};
+
+__device__ __forceinline__ void load_stage_rows(const Args& a, const Tile& tl, const Chunk& c,
+                                                int z, const bf16* ybase, int64_t ystride,
+                                                StageRows& r) {
+  const int cg = threadIdx.x >> 7, v0 = 2 * (threadIdx.x & 127);
+  const u32x4_t z4 = {0u, 0u, 0u, 0u};
+  r.x[0][0] = r.x[0][1] = r.x[1][0] = r.x[1][1] = z4;
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    if (v0 + e < c.nv) {
+      const bf16* p = ybase + chunk_row(a, tl, c, z, v0 + e) * ystride + tl.head * kHD + 8 * cg;
+      r.x[0][e] = load16(p);
+      r.x[1][e] = load16(p + 32);
+    }
+  }
+}
+
+__device__ __forceinline__ void store_stage(const Chunk& c, const StageRows& r, uint16_t* yt) {
+  const int cg = threadIdx.x >> 7, v0 = 2 * (threadIdx.x & 127);
+  if (v0 >= c.nvp) return;
+#pragma unroll
+  for (int g = 0; g < 2; ++g) {
+    const int ch0 = 8 * (cg + 4 * g);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const uint32_t even = (x0[i] & 0xffffu) | (x1[i] << 16);
-      const uint32_t odd = (x0[i] >> 16) | (x1[i] & 0xffff0000u);
-      __builtin_memcpy(&yt[(8 * cg + 2 * i) * kVRow + v0], &even, sizeof(even));
-      __builtin_memcpy(&yt[(8 * cg + 2 * i + 1) * kVRow + v0], &odd, sizeof(odd));
+      const uint32_t even = (r.x[g][0][i] & 0xffffu) | (r.x[g][1][i] << 16);
+      const uint32_t odd = (r.x[g][0][i] >> 16) | (r.x[g][1][i] & 0xffff0000u);
+      __builtin_memcpy(&yt[(ch0 + 2 * i) * kVRow + v0], &even, sizeof(even));
+      __builtin_memcpy(&yt[(ch0 + 2 * i + 1) * kVRow + v0], &odd, sizeof(odd));
     }
   }
 }
@@ -322,7 +400,8 @@ __device__ __forceinline__ bool slot_hits(const Slot& s, int z, int chunk, float
   return false;
 }
 
-// Table values at the slot's 4 (y, x) corners of the current plane.
+// Table values at the slot's 4 (y, x) corners of the current plane.  A corner
+// outside the volume reads its in-volume neighbour (it has weight 0).
 __device__ __forceinline__ void corners4(const Slot& s, const float* row, float& t00, float& t01,
                                          float& t10, float& t11) {
   const int base = s.idx & 0x1ff, dy = (s.idx >> 9) & 0x1f, dx = (s.idx >> 14) & 1;
@@ -330,6 +409,23 @@ __device__ __forceinline__ void corners4(const Slot& s, const float* row, float&
   t01 = row[base + dx];
   t10 = row[base + dy];
   t11 = row[base + dy + dx];
+}
+
+// Bilinear (y, x) interpolation of 4 corner values and its two partial
+// derivatives: val = lerp_y(top, bot), d/dfx and d/dfy.
+struct Bilerp {
+  float val, dx, dy;
+};
+
+__device__ __forceinline__ Bilerp bilerp(const Slot& s, float t00, float t01, float t10, float t11) {
+  const float dtop = t01 - t00, dbot = t11 - t10;
+  const float top = __builtin_fmaf(s.fx, dtop, t00);
+  const float bot = __builtin_fmaf(s.fx, dbot, t10);
+  Bilerp r;
+  r.dy = bot - top;
+  r.val = __builtin_fmaf(s.fy, r.dy, top);
+  r.dx = __builtin_fmaf(s.fy, dbot - dtop, dtop);
+  return r;
 }
 
 // 8 fp32 table entries -> bf16x8 MFMA operand (round to nearest even).
