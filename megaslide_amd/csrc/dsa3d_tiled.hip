@@ -21,7 +21,7 @@ namespace {
 
 using namespace tiled;
 
-__global__ __launch_bounds__(kThreads) void dsa3d_fwd_tiled_kernel(Args a, bf16* __restrict__ out,
+__global__ __launch_bounds__(kThreads, 4) void dsa3d_fwd_tiled_kernel(Args a, bf16* __restrict__ out,
                                                                    float* __restrict__ lse) {
   __shared__ __attribute__((aligned(16))) float s_tab[kTQ * kSRow];     // S, then A
   __shared__ __attribute__((aligned(16))) uint16_t s_vt[kHD * kVRow];  // V^T chunk
@@ -39,24 +39,32 @@ __global__ __launch_bounds__(kThreads) void dsa3d_fwd_tiled_kernel(Args a, bf16*
   const float* my_row = &s_tab[tl.q * kSRow];
 
   // ---- pass 1: scores -------------------------------------------------------
+  // K rows of the next (plane, chunk) are loaded while the current one is used
   float sc[kSlots];
 #pragma unroll
   for (int i = 0; i < kSlots; ++i) sc[i] = 0.0f;
+  TableRows rows;
+  if (nit > 0) load_table_rows(a, tl, make_chunk(box, 0), box.zlo, a.k, a.ks, rows);
   for (int it = 0; it < nit; ++it) {
     const int zi = it / nchunks;
     const int z = box.zlo + zi;
     const Chunk c = make_chunk(box, it - zi * nchunks);
-    TableRows rows;
-    load_table_rows(a, tl, c, z, a.k, a.ks, rows);
     store_table(tl, c, q0, q1, rows, s_tab);
+    if (it + 1 < nit) {
+      const int zn = (it + 1) / nchunks;
+      load_table_rows(a, tl, make_chunk(box, it + 1 - zn * nchunks), box.zlo + zn, a.k, a.ks, rows);
+    }
     __syncthreads();
+    // every slot reads its corners (in-bounds for any slot); misses are discarded
+    float t[kSlots][4];
+#pragma unroll
+    for (int i = 0; i < kSlots; ++i) corners4(sl[i], my_row, t[i][0], t[i][1], t[i][2], t[i][3]);
 #pragma unroll
     for (int i = 0; i < kSlots; ++i) {
       float wz, dwz;
-      if (!slot_hits(sl[i], z, c.id, wz, dwz)) continue;
-      float t00, t01, t10, t11;
-      corners4(sl[i], my_row, t00, t01, t10, t11);
-      sc[i] = __builtin_fmaf(wz, bilerp(sl[i], t00, t01, t10, t11).val, sc[i]);
+      const bool hit = slot_weight(sl[i], z, c.id, wz, dwz);
+      const float v = bilerp(sl[i], t[i][0], t[i][1], t[i][2], t[i][3]).val;
+      sc[i] = hit ? __builtin_fmaf(wz, v, sc[i]) : sc[i];
     }
     __syncthreads();
   }
@@ -88,31 +96,36 @@ __global__ __launch_bounds__(kThreads) void dsa3d_fwd_tiled_kernel(Args a, bf16*
   const int mq = tl.lane & 15, kq = 8 * (tl.lane >> 4);
   const int ct = tl.wave & 3, half = tl.wave >> 2;
   f32x4_t oacc = {0.0f, 0.0f, 0.0f, 0.0f};
-  float* row = &s_tab[tl.q * kSRow];
+  int* const s_atab = reinterpret_cast<int*>(s_tab);  // A in fixed point (scale 2^30)
+  int* row = &s_atab[tl.q * kSRow];
+  StageRows vr;
+  if (nit > 0) load_stage_rows(a, tl, make_chunk(box, 0), box.zlo, a.v, a.vs, vr);
   for (int it = 0; it < nit; ++it) {
     const int zi = it / nchunks;
     const int z = box.zlo + zi;
     const Chunk c = make_chunk(box, it - zi * nchunks);
-    StageRows vr;
-    load_stage_rows(a, tl, c, z, a.v, a.vs, vr);
     zero_table(s_tab, c.nvp);
     store_stage(c, vr, s_vt);
+    if (it + 1 < nit) {
+      const int zn = (it + 1) / nchunks;
+      load_stage_rows(a, tl, make_chunk(box, it + 1 - zn * nchunks), box.zlo + zn, a.v, a.vs, vr);
+    }
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < kSlots; ++i) {
       float wz, dwz;
       if (!slot_hits(sl[i], z, c.id, wz, dwz)) continue;
-      const float pz = sc[i] * wz;
+      const float pz = sc[i] * wz * kFixA;
       const float gx = 1.0f - sl[i].fx, gy = 1.0f - sl[i].fy;
       const int base = sl[i].idx & 0x1ff, dy = (sl[i].idx >> 9) & 0x1f, dx = (sl[i].idx >> 14) & 1;
-      atomicAdd(&row[base], pz * (gy * gx));
-      if (dx) atomicAdd(&row[base + 1], pz * (gy * sl[i].fx));
-      if (dy) atomicAdd(&row[base + dy], pz * (sl[i].fy * gx));
-      if (dx && dy) atomicAdd(&row[base + dy + 1], pz * (sl[i].fy * sl[i].fx));
+      atomicAdd(&row[base], to_fix(pz * (gy * gx)));
+      if (dx) atomicAdd(&row[base + 1], to_fix(pz * (gy * sl[i].fx)));
+      if (dy) atomicAdd(&row[base + dy], to_fix(pz * (sl[i].fy * gx)));
+      if (dx && dy) atomicAdd(&row[base + dy + 1], to_fix(pz * (sl[i].fy * sl[i].fx)));
     }
     __syncthreads();
     for (int kc = 32 * half; kc < c.nvp; kc += 64) {
-      const bf16x8_t av = to_bf16x8(&s_tab[mq * kSRow + kc + kq]);
+      const bf16x8_t av = fix_to_bf16x8(&s_atab[mq * kSRow + kc + kq], kFixAInv);
       bf16x8_t bv;
       __builtin_memcpy(&bv, &s_vt[(16 * ct + mq) * kVRow + kc + kq], sizeof(bv));
       oacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv, oacc, 0, 0, 0);
@@ -163,11 +176,21 @@ __device__ __forceinline__ bf16x8_t load_rows_transposed(const Args& a, const Ti
 // dK = B^T q and dV = A^T dO.
 constexpr int kTRow = kTQ + 4;
 
-// Rows 16*vb + l%16 of a transposed table as the MFMA A operand (contraction over
-// the 16 queries 8*(l/16) + j; zeros for l >= 32), rounded to bf16.
-__device__ __forceinline__ bf16x8_t table_t_rows(const float* table_t, int vb, int lane) {
+// Rows 16*vb + l%16 of a transposed fixed-point table as the MFMA A operand
+// (contraction over the 16 queries 8*(l/16) + j, entry j scaled by inv[j]; zeros
+// for l >= 32), rounded to bf16.
+__device__ __forceinline__ bf16x8_t table_t_rows(const int* table_t, int vb, int lane,
+                                                 const float* inv) {
   if ((lane >> 4) >= 2) return zero_bf16x8();
-  return to_bf16x8(&table_t[(16 * vb + (lane & 15)) * kTRow + 8 * (lane >> 4)]);
+  const int* p = &table_t[(16 * vb + (lane & 15)) * kTRow + 8 * (lane >> 4)];
+  u32x4_t r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const f32x2_t f = {static_cast<float>(p[2 * i]) * inv[2 * i],
+                       static_cast<float>(p[2 * i + 1]) * inv[2 * i + 1]};
+    r[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_t));
+  }
+  return __builtin_bit_cast(bf16x8_t, r);
 }
 
 __global__ __launch_bounds__(kThreads) void dsa3d_bwd_tiled_kernel(
@@ -183,8 +206,9 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_tiled_kernel(
   static_assert(2 * kTQ * kSRow <= 2 * kChunkNV * kTRow, "tables must fit the shared buffer");
   float* const s_t0 = s_buf;                     // S
   float* const s_t1 = s_buf + kTQ * kSRow;       // dP
-  float* const s_at = s_buf;                     // A^T = p w
-  float* const s_bt = s_buf + kChunkNV * kTRow;  // B^T = ds scale w
+  int* const s_at = reinterpret_cast<int*>(s_buf);                     // A^T = p w (fixed point)
+  int* const s_bt = reinterpret_cast<int*>(s_buf + kChunkNV * kTRow);  // B^T = ds scale w (fixed point)
+  __shared__ float s_binv[kTQ];  // per query: 1 / fixed-point scale of B
 
   const Tile tl = make_tile(a);
   const int D = a.nh * kHD;
@@ -216,35 +240,49 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_tiled_kernel(
 #pragma unroll
   for (int i = 0; i < kSlots; ++i)
     s_[i] = dp_[i] = gxs[i] = gxd[i] = gys[i] = gyd[i] = gzs[i] = gzd[i] = 0.0f;
+  // K and V rows of the next (plane, chunk) are loaded while the current one is used
+  TableRows rk, rv;
+  if (nit > 0) {
+    const Chunk c0 = make_chunk(box, 0);
+    load_table_rows(a, tl, c0, box.zlo, a.k, a.ks, rk);
+    load_table_rows(a, tl, c0, box.zlo, a.v, a.vs, rv);
+  }
+  const float* r0 = &s_t0[tl.q * kSRow];
+  const float* r1 = &s_t1[tl.q * kSRow];
   for (int it = 0; it < nit; ++it) {
     const int zi = it / nchunks;
     const int z = box.zlo + zi;
     const Chunk c = make_chunk(box, it - zi * nchunks);
-    TableRows rk, rv;
-    load_table_rows(a, tl, c, z, a.k, a.ks, rk);
-    load_table_rows(a, tl, c, z, a.v, a.vs, rv);
     store_table(tl, c, q0, q1, rk, s_t0);
     store_table(tl, c, g0, g1, rv, s_t1);
+    if (it + 1 < nit) {
+      const int zn = (it + 1) / nchunks;
+      const Chunk cn = make_chunk(box, it + 1 - zn * nchunks);
+      load_table_rows(a, tl, cn, box.zlo + zn, a.k, a.ks, rk);
+      load_table_rows(a, tl, cn, box.zlo + zn, a.v, a.vs, rv);
+    }
     __syncthreads();
-    const float* r0 = &s_t0[tl.q * kSRow];
-    const float* r1 = &s_t1[tl.q * kSRow];
+    // every slot reads its corners (in-bounds for any slot); misses are discarded
 #pragma unroll
     for (int i = 0; i < kSlots; ++i) {
       float wz, dwz;
-      if (!slot_hits(sl[i], z, c.id, wz, dwz)) continue;
+      const bool hit = slot_weight(sl[i], z, c.id, wz, dwz);
       float t00, t01, t10, t11;
       corners4(sl[i], r0, t00, t01, t10, t11);
       const Bilerp bs = bilerp(sl[i], t00, t01, t10, t11);
       corners4(sl[i], r1, t00, t01, t10, t11);
       const Bilerp bd = bilerp(sl[i], t00, t01, t10, t11);
-      s_[i] = __builtin_fmaf(wz, bs.val, s_[i]);
-      gxs[i] = __builtin_fmaf(wz, bs.dx, gxs[i]);
-      gys[i] = __builtin_fmaf(wz, bs.dy, gys[i]);
-      gzs[i] = __builtin_fmaf(dwz, bs.val, gzs[i]);
-      dp_[i] = __builtin_fmaf(wz, bd.val, dp_[i]);
-      gxd[i] = __builtin_fmaf(wz, bd.dx, gxd[i]);
-      gyd[i] = __builtin_fmaf(wz, bd.dy, gyd[i]);
-      gzd[i] = __builtin_fmaf(dwz, bd.val, gzd[i]);
+      // misses may read stale (even non-finite) entries: select, never scale by 0
+      const float sv = hit ? bs.val : 0.0f, sx = hit ? bs.dx : 0.0f, sy = hit ? bs.dy : 0.0f;
+      const float dv = hit ? bd.val : 0.0f, dx = hit ? bd.dx : 0.0f, dy = hit ? bd.dy : 0.0f;
+      s_[i] = __builtin_fmaf(wz, sv, s_[i]);
+      gxs[i] = __builtin_fmaf(wz, sx, gxs[i]);
+      gys[i] = __builtin_fmaf(wz, sy, gys[i]);
+      gzs[i] = __builtin_fmaf(dwz, sv, gzs[i]);
+      dp_[i] = __builtin_fmaf(wz, dv, dp_[i]);
+      gxd[i] = __builtin_fmaf(wz, dx, gxd[i]);
+      gyd[i] = __builtin_fmaf(wz, dy, gyd[i]);
+      gzd[i] = __builtin_fmaf(dwz, dv, gzd[i]);
     }
     __syncthreads();
   }
@@ -272,6 +310,17 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_tiled_kernel(
     dp[2] = from_f32<bf16>((m & 4) ? (dss * gzs[i] + pi * gzd[i]) * czs : 0.0f);
   }
 
+  // fixed-point scale of this query's B entries: 2^30 / sum_k |ds_k scale|
+  float l1 = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kSlots; ++i) l1 += fabsf(bsc[i]);
+#pragma unroll
+  for (int m = 1; m < kSubs; m <<= 1) l1 += __shfl_xor(l1, m);
+  const bool l1_ok = l1 > 1e-30f;
+  const float bscale = l1_ok ? kFixA / l1 : 0.0f;
+  if (tl.sub == 0) s_binv[tl.q] = l1_ok ? l1 * kFixAInv : 0.0f;
+  __syncthreads();
+
   // ---- pass 2: dq = B K, dK = B^T q, dV = A^T dO ---------------------------------
   // wave w: channels 16*(w & 3) + [0, 16); k-steps / voxel blocks of parity w >> 2
   const int mq = tl.lane & 15, kq = 8 * (tl.lane >> 4);
@@ -279,13 +328,21 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_tiled_kernel(
   const bf16x8_t qT = load_rows_transposed(a, tl, a.q, a.qs, ct);
   const bf16x8_t gT = load_rows_transposed(a, tl, dout, D, ct);
   const int ch = tl.head * kHD + 16 * ct + mq;
+  // B scales of this lane's dq row (query mq) and of its dK contraction queries
+  const float binv_m = s_binv[mq];
+  float binv_k[8], ainv_k[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    binv_k[j] = s_binv[(8 * (tl.lane >> 4) + j) & 15];
+    ainv_k[j] = kFixAInv;
+  }
   f32x4_t dq_acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  StageRows kr;
+  if (nit > 0) load_stage_rows(a, tl, make_chunk(box, 0), box.zlo, a.k, a.ks, kr);
   for (int it = 0; it < nit; ++it) {
     const int zi = it / nchunks;
     const int z = box.zlo + zi;
     const Chunk c = make_chunk(box, it - zi * nchunks);
-    StageRows kr;
-    load_stage_rows(a, tl, c, z, a.k, a.ks, kr);
     // zero the transposed A and B tables; token rows of the chunk's voxels
     for (int e = threadIdx.x; e < c.nvp * kTRow / 4; e += kThreads) {
       const f32x4_t zz = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -295,30 +352,34 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_tiled_kernel(
     for (int vi = threadIdx.x; vi < c.nv; vi += kThreads)
       s_rows[vi] = static_cast<int>(chunk_row(a, tl, c, z, vi) - tl.sample0);
     store_stage(c, kr, s_kt);
+    if (it + 1 < nit) {
+      const int zn = (it + 1) / nchunks;
+      load_stage_rows(a, tl, make_chunk(box, it + 1 - zn * nchunks), box.zlo + zn, a.k, a.ks, kr);
+    }
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < kSlots; ++i) {
       float wz, dwz;
       if (!slot_hits(sl[i], z, c.id, wz, dwz)) continue;
-      const float pz = p[i] * wz, bz = bsc[i] * wz;
+      const float pz = p[i] * wz * kFixA, bz = bsc[i] * wz * bscale;
       const float fx = sl[i].fx, fy = sl[i].fy, gx = 1.0f - fx, gy = 1.0f - fy;
       const float w00 = gy * gx, w01 = gy * fx, w10 = fy * gx, w11 = fy * fx;
       const int base = sl[i].idx & 0x1ff, dy = (sl[i].idx >> 9) & 0x1f, dx = (sl[i].idx >> 14) & 1;
-      float* ra = &s_at[base * kTRow + tl.q];
-      float* rb = &s_bt[base * kTRow + tl.q];
-      atomicAdd(ra, pz * w00);
-      atomicAdd(rb, bz * w00);
+      int* ra = &s_at[base * kTRow + tl.q];
+      int* rb = &s_bt[base * kTRow + tl.q];
+      atomicAdd(ra, to_fix(pz * w00));
+      atomicAdd(rb, to_fix(bz * w00));
       if (dx) {
-        atomicAdd(ra + kTRow, pz * w01);
-        atomicAdd(rb + kTRow, bz * w01);
+        atomicAdd(ra + kTRow, to_fix(pz * w01));
+        atomicAdd(rb + kTRow, to_fix(bz * w01));
       }
       if (dy) {
-        atomicAdd(ra + dy * kTRow, pz * w10);
-        atomicAdd(rb + dy * kTRow, bz * w10);
+        atomicAdd(ra + dy * kTRow, to_fix(pz * w10));
+        atomicAdd(rb + dy * kTRow, to_fix(bz * w10));
       }
       if (dx && dy) {
-        atomicAdd(ra + (dy + 1) * kTRow, pz * w11);
-        atomicAdd(rb + (dy + 1) * kTRow, bz * w11);
+        atomicAdd(ra + (dy + 1) * kTRow, to_fix(pz * w11));
+        atomicAdd(rb + (dy + 1) * kTRow, to_fix(bz * w11));
       }
     }
     __syncthreads();
@@ -327,7 +388,7 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_tiled_kernel(
     for (int kc = 32 * half; kc < c.nvp; kc += 64) {
       float bq[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) bq[j] = s_bt[(kc + kq + j) * kTRow + mq];
+      for (int j = 0; j < 8; ++j) bq[j] = static_cast<float>(s_bt[(kc + kq + j) * kTRow + mq]) * binv_m;
       bf16x8_t bhi, blo, kv;
       to_bf16x8_hilo(bq, bhi, blo);
       __builtin_memcpy(&kv, &s_kt[(16 * ct + mq) * kVRow + kc + kq], sizeof(kv));
@@ -337,8 +398,10 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_tiled_kernel(
     // dK[v] += sum_q B[q][v] q[q];  dV[v] += sum_q A[q][v] dO[q]  (fp32 atomics)
     for (int vb = half; vb * 16 < c.nv; vb += 2) {
       f32x4_t dk4 = {0.0f, 0.0f, 0.0f, 0.0f}, dv4 = {0.0f, 0.0f, 0.0f, 0.0f};
-      dk4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(table_t_rows(s_bt, vb, tl.lane), qT, dk4, 0, 0, 0);
-      dv4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(table_t_rows(s_at, vb, tl.lane), gT, dv4, 0, 0, 0);
+      dk4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(table_t_rows(s_bt, vb, tl.lane, binv_k), qT, dk4,
+                                                    0, 0, 0);
+      dv4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(table_t_rows(s_at, vb, tl.lane, ainv_k), gT, dv4,
+                                                    0, 0, 0);
       const int v0 = 16 * vb + 4 * (tl.lane >> 4);
       int rr[4];
       __builtin_memcpy(rr, &s_rows[v0], sizeof(rr));

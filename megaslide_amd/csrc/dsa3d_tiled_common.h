@@ -400,8 +400,22 @@ __device__ __forceinline__ bool slot_hits(const Slot& s, int z, int chunk, float
   return false;
 }
 
+// Branch-free form of slot_hits: the z weight (0 when the slot has no corners
+// on plane z of chunk c), its z derivative sign (0 likewise) and the hit flag.
+__device__ __forceinline__ bool slot_weight(const Slot& s, int z, int chunk, float& wz, float& dwz) {
+  const int z0 = slot_z0(s);
+  const bool same = slot_chunk(s) == chunk;
+  const bool h0 = same && z0 == z;
+  const bool h1 = same && slot_hz(s) && z0 + 1 == z;
+  wz = h0 ? 1.0f - s.fz : (h1 ? s.fz : 0.0f);
+  dwz = h0 ? -1.0f : (h1 ? 1.0f : 0.0f);
+  return h0 || h1;
+}
+
 // Table values at the slot's 4 (y, x) corners of the current plane.  A corner
-// outside the volume reads its in-volume neighbour (it has weight 0).
+// outside the volume reads its in-volume neighbour (it has weight 0).  Every
+// index is below kChunkNV, so the reads stay inside a table row even for a slot
+// of another chunk (whose values are then discarded).
 __device__ __forceinline__ void corners4(const Slot& s, const float* row, float& t00, float& t01,
                                          float& t10, float& t11) {
   const int base = s.idx & 0x1ff, dy = (s.idx >> 9) & 0x1f, dx = (s.idx >> 14) & 1;
@@ -426,6 +440,27 @@ __device__ __forceinline__ Bilerp bilerp(const Slot& s, float t00, float t01, fl
   r.val = __builtin_fmaf(s.fy, r.dy, top);
   r.dx = __builtin_fmaf(s.fy, dbot - dtop, dtop);
   return r;
+}
+
+// Scatter tables (A = p w, B = ds scale w) accumulate in int32 fixed point:
+// LDS integer atomics run ~30x faster than fp32 ones on gfx950, and integer
+// sums are exact and order-independent.  A query's entries of A sum to at most
+// sum_k p_k = 1, so A uses the fixed scale 2^30; B uses 2^30 / sum_k |ds_k scale|
+// per query, which bounds every entry and every partial sum below 2^30.
+constexpr float kFixA = 1073741824.0f;          // 2^30
+constexpr float kFixAInv = 1.0f / 1073741824.0f;
+
+__device__ __forceinline__ int to_fix(float x) { return static_cast<int>(__builtin_rintf(x)); }
+
+// 8 fixed-point table entries (scaled by 1/inv) -> bf16x8 MFMA operand.
+__device__ __forceinline__ bf16x8_t fix_to_bf16x8(const int* p, float inv) {
+  u32x4_t r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const f32x2_t f = {static_cast<float>(p[2 * i]) * inv, static_cast<float>(p[2 * i + 1]) * inv};
+    r[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_t));
+  }
+  return __builtin_bit_cast(bf16x8_t, r);
 }
 
 // 8 fp32 table entries -> bf16x8 MFMA operand (round to nearest even).
