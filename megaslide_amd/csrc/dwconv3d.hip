@@ -106,6 +106,215 @@ __global__ __launch_bounds__(64 * kRowWaves) void dwconv_rows_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// block kernels for square (kh, kw) in {3, 5, 7}: a thread owns one channel and
+// an R x kRun block of outputs (R rows along H, kRun along W) of one frame.  Per
+// input row it loads kRun + KW - 1 values once and applies them to every output
+// row the row reaches (up to min(R, KH) of them); the KH x KW weights of the
+// current dt stay in registers.
+// ---------------------------------------------------------------------------
+
+constexpr int kBlockRows = 4;  // R: output rows per thread
+
+// Element `lane_off` (a 32-bit per-lane offset) past the wave-uniform pointer
+// `base`: written so the compiler addresses it as scalar base + vector offset
+// instead of building (and hoisting) a 64-bit vector address per load.
+template <typename T>
+__device__ __forceinline__ float ldu(const T* base, uint32_t lane_off) {
+  const uint32_t bytes = lane_off * static_cast<uint32_t>(sizeof(T));  // 32-bit: zero-extended offset
+  return to_f32(*reinterpret_cast<const T*>(reinterpret_cast<const char*>(base) + bytes));
+}
+
+template <typename T>
+__device__ __forceinline__ void stu(T* base, uint32_t lane_off, float v) {
+  const uint32_t bytes = lane_off * static_cast<uint32_t>(sizeof(T));
+  *reinterpret_cast<T*>(reinterpret_cast<char*>(base) + bytes) = from_f32<T>(v);
+}
+
+// Input value at column ww of a row, 0 outside [0, W): the column is clamped and
+// the value selected, so the loads of a row form one branch-free block.
+template <typename G>
+__device__ __forceinline__ float ld_col(const G* row, int ww, int W, int C, uint32_t lc) {
+  const int wc = min(max(ww, 0), W - 1);
+  const float v = ldu(row + static_cast<int64_t>(wc) * C, lc);
+  return ww == wc ? v : 0.0f;
+}
+
+template <typename T, typename G, int KH, int KW, int MODE>
+__global__ __launch_bounds__(64 * kRowWaves) void dwconv_block_kernel(
+    ConvArgs a, const G* __restrict__ in, const T* __restrict__ wt, const T* __restrict__ bias,
+    const T* __restrict__ dy, T* __restrict__ out, float* __restrict__ out_f32, int flip) {
+  constexpr int R = kBlockRows, PH = KH / 2, PW = KW / 2, NX = kRun + KW - 1;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c = blockIdx.y * 64 + lane;
+  const int runs = (a.W + kRun - 1) / kRun;
+  const int hblocks = (a.H + R - 1) / R;
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * kRowWaves + wave;  // (b, t, hblock, run)
+  const int64_t items = static_cast<int64_t>(a.B) * a.T * hblocks * runs;
+  if (item >= items) return;
+  const bool c_ok = c < a.C;
+  const uint32_t lc = c_ok ? c : a.C - 1;  // lanes past C read a valid channel and store nothing
+  const int run = static_cast<int>(item % runs);
+  const int64_t rest = item / runs;
+  const int hb = static_cast<int>(rest % hblocks);
+  const int64_t bt = rest / hblocks;
+  const int t = static_cast<int>(bt % a.T);
+  const int b = static_cast<int>(bt / a.T);
+  const int h0 = hb * R, w0 = run * kRun;
+  const int K = a.kt * KH * KW;
+  const int64_t rowstride = static_cast<int64_t>(a.W) * a.C;
+
+  float acc[R][kRun];
+  const float b0 = bias != nullptr ? ldu(bias, lc) : 0.0f;
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int j = 0; j < kRun; ++j) acc[r][j] = b0;
+
+  for (int dt = 0; dt < a.kt; ++dt) {
+    const int tt = t + dt - a.kt / 2;
+    if (tt < 0 || tt >= a.T) continue;
+    float wk[KH][KW];
+#pragma unroll
+    for (int dh = 0; dh < KH; ++dh)
+#pragma unroll
+      for (int k = 0; k < KW; ++k) {
+        const int tap = (dt * KH + dh) * KW + k;
+        wk[dh][k] = ldu(wt + (flip ? K - 1 - tap : tap), lc * K);
+      }
+    const G* plane = in + (static_cast<int64_t>(b) * a.T + tt) * a.H * rowstride;
+#pragma unroll
+    for (int ii = 0; ii < R + KH - 1; ++ii) {
+      const int hh = h0 + ii - PH;
+      if (hh < 0 || hh >= a.H) continue;
+      const G* row = plane + hh * rowstride;
+      float x[NX];
+#pragma unroll
+      for (int j = 0; j < NX; ++j) {
+        const int ww = w0 + j - PW;
+        x[j] = ld_col(row, ww, a.W, a.C, lc);
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int dh = ii - r;
+        if (dh < 0 || dh >= KH) continue;
+#pragma unroll
+        for (int j = 0; j < kRun; ++j)
+#pragma unroll
+          for (int k = 0; k < KW; ++k) acc[r][j] = __builtin_fmaf(wk[dh][k], x[j + k], acc[r][j]);
+      }
+    }
+  }
+  if (!c_ok) return;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int h = h0 + r;
+    if (h >= a.H) continue;
+    const int64_t orow = ((static_cast<int64_t>(b) * a.T + t) * a.H + h) * a.W;
+#pragma unroll
+    for (int j = 0; j < kRun; ++j) {
+      const int w = w0 + j;
+      if (w >= a.W) continue;
+      const int64_t i0 = (orow + w) * a.C;  // uniform; + lc per lane
+      if (MODE == kPlain) stu(out + i0, lc, acc[r][j]);
+      if (MODE == kGelu) stu(out + i0, lc, gelu_erf(acc[r][j]));
+      if (MODE == kGeluGrad) out_f32[i0 + lc] = ldu(dy + i0, lc) * gelu_erf_grad(acc[r][j]);
+    }
+  }
+}
+
+// Weight / bias gradient for square (kh, kw) in {3, 5, 7}: a thread owns one
+// channel and one dt (KH x KW tap sums in registers) and walks a strip of
+// kDwStripBlocks blocks of R output rows of one frame.  For every R-row block and
+// run it keeps the R x kRun dz values in registers and loads each input row once.
+// acc[c*(K+1) + tap] += partial sums; acc[c*(K+1) + K] += sum dz (dt == 0 threads).
+constexpr int kDwStripBlocks = 4;
+
+template <typename T, typename G, int KH, int KW>
+__global__ __launch_bounds__(64 * kRowWaves) void dwconv_dw_block_kernel(ConvArgs a,
+                                                                         const T* __restrict__ x,
+                                                                         const G* __restrict__ dz,
+                                                                         float* __restrict__ acc) {
+  constexpr int R = kBlockRows, PH = KH / 2, PW = KW / 2, NX = kRun + KW - 1;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c = blockIdx.y * 64 + lane;
+  const int dt = blockIdx.z;
+  const int hblocks = (a.H + R - 1) / R;
+  const int strips_per_frame = (hblocks + kDwStripBlocks - 1) / kDwStripBlocks;
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * kRowWaves + wave;  // (b, t, strip)
+  const int64_t items = static_cast<int64_t>(a.B) * a.T * strips_per_frame;
+  if (item >= items) return;
+  const int strip = static_cast<int>(item % strips_per_frame);
+  const int64_t bt = item / strips_per_frame;
+  const int t = static_cast<int>(bt % a.T);
+  const int b = static_cast<int>(bt / a.T);
+  const int tt = t + dt - a.kt / 2;
+  const bool plane_ok = tt >= 0 && tt < a.T;
+  if (!plane_ok && dt != 0) return;  // no taps; the dt == 0 threads still sum dz for the bias
+  const bool c_ok = c < a.C;
+  const uint32_t lc = c_ok ? c : a.C - 1;
+  const int K = a.kt * KH * KW;
+  const int64_t rowstride = static_cast<int64_t>(a.W) * a.C;
+  float s[KH][KW];
+#pragma unroll
+  for (int dh = 0; dh < KH; ++dh)
+#pragma unroll
+    for (int k = 0; k < KW; ++k) s[dh][k] = 0.0f;
+  float sb = 0.0f;
+  const T* plane = x + (static_cast<int64_t>(b) * a.T + (plane_ok ? tt : 0)) * a.H * rowstride;
+  const G* gplane = dz + (static_cast<int64_t>(b) * a.T + t) * a.H * rowstride;
+  const int hb_end = min(hblocks, (strip + 1) * kDwStripBlocks);
+  for (int hb = strip * kDwStripBlocks; hb < hb_end; ++hb) {
+    const int h0 = hb * R;
+    for (int w0 = 0; w0 < a.W; w0 += kRun) {
+      float g[R][kRun];
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int j = 0; j < kRun; ++j) {
+          const int h = h0 + r, w = w0 + j;
+          g[r][j] = h < a.H ? ld_col(gplane + h * rowstride, w, a.W, a.C, lc) : 0.0f;
+          if (dt == 0) sb += g[r][j];
+        }
+      if (!plane_ok) continue;
+#pragma unroll
+      for (int ii = 0; ii < R + KH - 1; ++ii) {
+        const int hh = h0 + ii - PH;
+        if (hh < 0 || hh >= a.H) continue;
+        const T* row = plane + hh * rowstride;
+        float xv[NX];
+#pragma unroll
+        for (int j = 0; j < NX; ++j) {
+          const int ww = w0 + j - PW;
+          xv[j] = ld_col(row, ww, a.W, a.C, lc);
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const int dh = ii - r;
+          if (dh < 0 || dh >= KH) continue;
+#pragma unroll
+          for (int k = 0; k < KW; ++k) {
+            float part = 0.0f;
+#pragma unroll
+            for (int j = 0; j < kRun; ++j) part = __builtin_fmaf(g[r][j], xv[j + k], part);
+            s[dh][k] += part;
+          }
+        }
+      }
+    }
+  }
+  if (!c_ok) return;
+  float* __restrict__ ac = acc + static_cast<int64_t>(c) * (K + 1) + dt * KH * KW;
+#pragma unroll
+  for (int dh = 0; dh < KH; ++dh)
+#pragma unroll
+    for (int k = 0; k < KW; ++k)
+      if (s[dh][k] != 0.0f) atomicAdd(ac + dh * KW + k, s[dh][k]);
+  if (dt == 0 && sb != 0.0f) atomicAdd(acc + static_cast<int64_t>(c) * (K + 1) + K, sb);
+}
+
+// ---------------------------------------------------------------------------
 // weight / bias gradient
 // ---------------------------------------------------------------------------
 
@@ -285,12 +494,29 @@ ConvArgs make_args(const msd_dwconv3d_desc& d) {
 }
 
 bool rows_ok(const ConvArgs& a) { return (a.kw == 3 || a.kw == 5 || a.kw == 7) && a.kt <= 7 && a.kh <= 7; }
+bool block_ok(const ConvArgs& a) { return a.kh == a.kw && (a.kw == 3 || a.kw == 5 || a.kw == 7); }
+
+template <typename T, typename G, int KS, int MODE>
+void launch_block(const ConvArgs& a, const G* in, const T* w, const T* b, const T* dy, T* out,
+                  float* out_f32, int flip, hipStream_t s) {
+  const int runs = (a.W + kRun - 1) / kRun;
+  const int hblocks = (a.H + kBlockRows - 1) / kBlockRows;
+  const int64_t items = static_cast<int64_t>(a.B) * a.T * hblocks * runs;
+  const dim3 grid(static_cast<unsigned>((items + kRowWaves - 1) / kRowWaves),
+                  static_cast<unsigned>((a.C + 63) / 64));
+  hipLaunchKernelGGL((dwconv_block_kernel<T, G, KS, KS, MODE>), grid, dim3(64 * kRowWaves), 0, s, a,
+                     in, w, b, dy, out, out_f32, flip);
+}
 
 // conv of `in` (type G) with w (flip: mirrored taps), epilogue MODE
 template <typename T, typename G, int MODE>
 hipError_t run_conv(const ConvArgs& a, const G* in, const T* w, const T* b, const T* dy, T* out,
                     float* out_f32, int flip, hipStream_t s) {
-  if (rows_ok(a)) {
+  if (block_ok(a)) {
+    if (a.kw == 3) launch_block<T, G, 3, MODE>(a, in, w, b, dy, out, out_f32, flip, s);
+    else if (a.kw == 5) launch_block<T, G, 5, MODE>(a, in, w, b, dy, out, out_f32, flip, s);
+    else launch_block<T, G, 7, MODE>(a, in, w, b, dy, out, out_f32, flip, s);
+  } else if (rows_ok(a)) {
     const int runs = (a.W + kRun - 1) / kRun;
     const int64_t items = static_cast<int64_t>(a.B) * a.T * a.H * runs;
     const dim3 grid(static_cast<unsigned>((items + kRowWaves - 1) / kRowWaves),
@@ -318,13 +544,28 @@ hipError_t run_conv(const ConvArgs& a, const G* in, const T* w, const T* b, cons
   return hipGetLastError();
 }
 
+template <typename T, typename G, int KS>
+void launch_dw_block(const ConvArgs& a, const T* x, const G* dz, float* acc, hipStream_t s) {
+  const int hblocks = (a.H + kBlockRows - 1) / kBlockRows;
+  const int strips = (hblocks + kDwStripBlocks - 1) / kDwStripBlocks;
+  const int64_t items = static_cast<int64_t>(a.B) * a.T * strips;
+  const dim3 grid(static_cast<unsigned>((items + kRowWaves - 1) / kRowWaves),
+                  static_cast<unsigned>((a.C + 63) / 64), static_cast<unsigned>(a.kt));
+  hipLaunchKernelGGL((dwconv_dw_block_kernel<T, G, KS, KS>), grid, dim3(64 * kRowWaves), 0, s, a, x,
+                     dz, acc);
+}
+
 template <typename T, typename G>
 void run_dw(const ConvArgs& a, const T* x, const G* dz, float* acc, hipStream_t s) {
   const int64_t rows = static_cast<int64_t>(a.B) * a.T * a.H;
   const dim3 grid(static_cast<unsigned>((rows + kStripRows * kRowWaves - 1) / (kStripRows * kRowWaves)),
                   static_cast<unsigned>((a.C + 63) / 64));
   const dim3 block(64 * kRowWaves);
-  if (a.kt == 3 && a.kh == 7 && a.kw == 7) {
+  if (block_ok(a)) {
+    if (a.kw == 3) launch_dw_block<T, G, 3>(a, x, dz, acc, s);
+    else if (a.kw == 5) launch_dw_block<T, G, 5>(a, x, dz, acc, s);
+    else launch_dw_block<T, G, 7>(a, x, dz, acc, s);
+  } else if (a.kt == 3 && a.kh == 7 && a.kw == 7) {
     hipLaunchKernelGGL((dwconv_dw_rows_kernel<T, G, 3, 7, 7>), grid, block, 0, s, a, x, dz, acc);
   } else if (a.kt == 3 && a.kh == 3 && a.kw == 3) {
     hipLaunchKernelGGL((dwconv_dw_rows_kernel<T, G, 3, 3, 3>), grid, block, 0, s, a, x, dz, acc);
