@@ -225,17 +225,19 @@ __global__ __launch_bounds__(64 * kRowWaves) void dwconv_block_kernel(
 
 // Weight / bias gradient for square (kh, kw) in {3, 5, 7}: a thread owns one
 // channel and one dt (KH x KW tap sums in registers) and walks a strip of
-// kDwStripBlocks blocks of R output rows of one frame.  For every R-row block and
+// kDwStripBlocks blocks of R = kDwRows output rows of one frame.  For every R-row block and
 // run it keeps the R x kRun dz values in registers and loads each input row once.
-// acc[c*(K+1) + tap] += partial sums; acc[c*(K+1) + K] += sum dz (dt == 0 threads).
-constexpr int kDwStripBlocks = 4;
+// acc[tap*C + c] += partial sums; acc[K*C + c] += sum dz (dt == 0 threads).  The
+// tap-major layout puts a wave's 64 channels of one tap on two cache lines.
+constexpr int kDwRows = 4;         // output rows per weight-gradient step
+constexpr int kDwStripBlocks = 2;  // steps per work item
 
 template <typename T, typename G, int KH, int KW>
 __global__ __launch_bounds__(64 * kRowWaves) void dwconv_dw_block_kernel(ConvArgs a,
                                                                          const T* __restrict__ x,
                                                                          const G* __restrict__ dz,
                                                                          float* __restrict__ acc) {
-  constexpr int R = kBlockRows, PH = KH / 2, PW = KW / 2, NX = kRun + KW - 1;
+  constexpr int R = kDwRows, PH = KH / 2, PW = KW / 2, NX = kRun + KW - 1;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int c = blockIdx.y * 64 + lane;
@@ -305,21 +307,21 @@ __global__ __launch_bounds__(64 * kRowWaves) void dwconv_dw_block_kernel(ConvArg
     }
   }
   if (!c_ok) return;
-  float* __restrict__ ac = acc + static_cast<int64_t>(c) * (K + 1) + dt * KH * KW;
+  float* __restrict__ ac = acc + static_cast<int64_t>(dt * KH * KW) * a.C + c;
 #pragma unroll
   for (int dh = 0; dh < KH; ++dh)
 #pragma unroll
     for (int k = 0; k < KW; ++k)
-      if (s[dh][k] != 0.0f) atomicAdd(ac + dh * KW + k, s[dh][k]);
-  if (dt == 0 && sb != 0.0f) atomicAdd(acc + static_cast<int64_t>(c) * (K + 1) + K, sb);
+      if (s[dh][k] != 0.0f) atomicAdd(ac + static_cast<int64_t>(dh * KW + k) * a.C, s[dh][k]);
+  if (dt == 0 && sb != 0.0f) atomicAdd(acc + static_cast<int64_t>(K) * a.C + c, sb);
 }
 
 // ---------------------------------------------------------------------------
 // weight / bias gradient
 // ---------------------------------------------------------------------------
 
-// acc[c*(K+1) + tap] += sum over a strip of kStripRows rows (all of W) of
-// dz[p, c] * x[p + tap - pad, c]; acc[c*(K+1) + K] += sum dz[p, c].
+// acc[tap*C + c] += sum over a strip of kStripRows rows (all of W) of
+// dz[p, c] * x[p + tap - pad, c]; acc[K*C + c] += sum dz[p, c].
 template <typename T, typename G, int KT, int KH, int KW>
 __global__ __launch_bounds__(64 * kRowWaves) void dwconv_dw_rows_kernel(ConvArgs a,
                                                                         const T* __restrict__ x,
@@ -377,11 +379,10 @@ __global__ __launch_bounds__(64 * kRowWaves) void dwconv_dw_rows_kernel(ConvArgs
       }
     }
   }
-  float* __restrict__ ac = acc + static_cast<int64_t>(c) * (K + 1);
 #pragma unroll
   for (int i = 0; i < K; ++i)
-    if (s[i] != 0.0f) atomicAdd(ac + i, s[i]);
-  if (sb != 0.0f) atomicAdd(ac + K, sb);
+    if (s[i] != 0.0f) atomicAdd(acc + static_cast<int64_t>(i) * a.C + c, s[i]);
+  if (sb != 0.0f) atomicAdd(acc + static_cast<int64_t>(K) * a.C + c, sb);
 }
 
 // ---------------------------------------------------------------------------
@@ -457,7 +458,7 @@ __global__ __launch_bounds__(64) void dwconv_dw_simple_kernel(ConvArgs a, const 
       s += ld(dz, r * a.C + c) * ld(x, rs * a.C + c);
     }
   }
-  atomicAdd(acc + static_cast<int64_t>(c) * (K + 1) + tap, s);
+  atomicAdd(acc + static_cast<int64_t>(tap) * a.C + c, s);
 }
 
 template <typename T>
@@ -465,9 +466,9 @@ __global__ __launch_bounds__(256) void dwconv_dw_finish_kernel(const float* __re
                                                                int K, T* __restrict__ dw,
                                                                T* __restrict__ db) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i >= static_cast<int64_t>(C) * (K + 1)) return;
-  const int c = static_cast<int>(i / (K + 1));
-  const int tap = static_cast<int>(i - static_cast<int64_t>(c) * (K + 1));
+  if (i >= static_cast<int64_t>(C) * (K + 1)) return;  // acc is [K + 1][C]
+  const int tap = static_cast<int>(i / C);
+  const int c = static_cast<int>(i - static_cast<int64_t>(tap) * C);
   if (tap < K) {
     if (dw != nullptr) st(dw, static_cast<int64_t>(c) * K + tap, acc[i]);
   } else if (db != nullptr) {
@@ -546,7 +547,7 @@ hipError_t run_conv(const ConvArgs& a, const G* in, const T* w, const T* b, cons
 
 template <typename T, typename G, int KS>
 void launch_dw_block(const ConvArgs& a, const T* x, const G* dz, float* acc, hipStream_t s) {
-  const int hblocks = (a.H + kBlockRows - 1) / kBlockRows;
+  const int hblocks = (a.H + kDwRows - 1) / kDwRows;
   const int strips = (hblocks + kDwStripBlocks - 1) / kDwStripBlocks;
   const int64_t items = static_cast<int64_t>(a.B) * a.T * strips;
   const dim3 grid(static_cast<unsigned>((items + kRowWaves - 1) / kRowWaves),
