@@ -152,37 +152,35 @@ __global__ __launch_bounds__(kThreads, 4) void dsa3d_fwd_tiled_kernel(Args a, bf
   }
 }
 
-// Q^T (or dO^T) as the MFMA B operand with the 16 tile queries as the
-// contraction index: lane l holds rows k = 8*(l/16) + j of channel
-// 16*ct + l%16; lanes 32..63 (k >= 16) hold zeros.
+// Q^T (or dO^T) as the B operand of the 32x32x16 MFMA, the 16 tile queries
+// being the contraction index: lane l holds queries k = 8*(l/32) + j of channel
+// 32*c2 + l%32 of the head.
 __device__ __forceinline__ bf16x8_t load_rows_transposed(const Args& a, const Tile& tl,
-                                                         const bf16* base, int64_t stride, int ct) {
+                                                         const bf16* base, int64_t stride, int c2) {
   u32x4_t r = {0u, 0u, 0u, 0u};
-  if ((tl.lane >> 4) < 2) {
-    const int ch = tl.head * kHD + 16 * ct + (tl.lane & 15);
+  const int ch = tl.head * kHD + 32 * c2 + (tl.lane & 31);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int64_t r0 = tile_row(a, tl, 8 * (tl.lane >> 4) + 2 * i);
-      const int64_t r1 = tile_row(a, tl, 8 * (tl.lane >> 4) + 2 * i + 1);
-      const uint32_t lo = r0 >= 0 ? base[r0 * stride + ch].bits : 0u;
-      const uint32_t hi = r1 >= 0 ? base[r1 * stride + ch].bits : 0u;
-      r[i] = lo | (hi << 16);
-    }
+  for (int i = 0; i < 4; ++i) {
+    const int64_t r0 = tile_row(a, tl, 8 * (tl.lane >> 5) + 2 * i);
+    const int64_t r1 = tile_row(a, tl, 8 * (tl.lane >> 5) + 2 * i + 1);
+    const uint32_t lo = r0 >= 0 ? base[r0 * stride + ch].bits : 0u;
+    const uint32_t hi = r1 >= 0 ? base[r1 * stride + ch].bits : 0u;
+    r[i] = lo | (hi << 16);
   }
   return __builtin_bit_cast(bf16x8_t, r);
 }
 
-// Transposed tables [voxel][query] (row of 16 queries + 4 pad floats) used for
-// dK = B^T q and dV = A^T dO.
-constexpr int kTRow = kTQ + 4;
+// Transposed tables [voxel][query] (row of 16 queries + 2 pad ints) used for
+// dK = B^T q and dV = A^T dO.  Stride 18 spreads the scatter atomics of a
+// wave's two queries over all LDS banks and keeps 8-byte aligned rows.
+constexpr int kTRow = kTQ + 2;
 
-// Rows 16*vb + l%16 of a transposed fixed-point table as the MFMA A operand
-// (contraction over the 16 queries 8*(l/16) + j, entry j scaled by inv[j]; zeros
-// for l >= 32), rounded to bf16.
+// 32 x 16 block vb of a transposed fixed-point table as the A operand of the
+// 32x32x16 MFMA: lane l holds voxel 32*vb + l%32, queries 8*(l/32) + j (entry j
+// scaled by inv[j]), rounded to bf16.
 __device__ __forceinline__ bf16x8_t table_t_rows(const int* table_t, int vb, int lane,
                                                  const float* inv) {
-  if ((lane >> 4) >= 2) return zero_bf16x8();
-  const int* p = &table_t[(16 * vb + (lane & 15)) * kTRow + 8 * (lane >> 4)];
+  const int* p = &table_t[(32 * vb + (lane & 31)) * kTRow + 8 * (lane >> 5)];
   u32x4_t r;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -322,18 +320,22 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_tiled_kernel(
   __syncthreads();
 
   // ---- pass 2: dq = B K, dK = B^T q, dV = A^T dO ---------------------------------
-  // wave w: channels 16*(w & 3) + [0, 16); k-steps / voxel blocks of parity w >> 2
+  // dq (16x16x32 MFMA): wave w owns channels 16*(w & 3) + [0, 16) and the voxel
+  // k-steps of parity w >> 2.  dK/dV (32x32x16 MFMA): wave w owns channels
+  // 32*(w & 1) + [0, 32) and the 32-voxel blocks (w >> 1) + 4 i.
   const int mq = tl.lane & 15, kq = 8 * (tl.lane >> 4);
   const int ct = tl.wave & 3, half = tl.wave >> 2;
-  const bf16x8_t qT = load_rows_transposed(a, tl, a.q, a.qs, ct);
-  const bf16x8_t gT = load_rows_transposed(a, tl, dout, D, ct);
+  const int c2 = tl.wave & 1, vq = tl.wave >> 1;
+  const bf16x8_t qT = load_rows_transposed(a, tl, a.q, a.qs, c2);
+  const bf16x8_t gT = load_rows_transposed(a, tl, dout, D, c2);
   const int ch = tl.head * kHD + 16 * ct + mq;
+  const int ch2 = tl.head * kHD + 32 * c2 + (tl.lane & 31);
   // B scales of this lane's dq row (query mq) and of its dK contraction queries
   const float binv_m = s_binv[mq];
   float binv_k[8], ainv_k[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    binv_k[j] = s_binv[(8 * (tl.lane >> 4) + j) & 15];
+    binv_k[j] = s_binv[8 * (tl.lane >> 5) + j];
     ainv_k[j] = kFixAInv;
   }
   f32x4_t dq_acc = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -395,22 +397,27 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_tiled_kernel(
       dq_acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bhi, kv, dq_acc, 0, 0, 0);
       dq_acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(blo, kv, dq_acc, 0, 0, 0);
     }
-    // dK[v] += sum_q B[q][v] q[q];  dV[v] += sum_q A[q][v] dO[q]  (fp32 atomics)
-    for (int vb = half; vb * 16 < c.nv; vb += 2) {
-      f32x4_t dk4 = {0.0f, 0.0f, 0.0f, 0.0f}, dv4 = {0.0f, 0.0f, 0.0f, 0.0f};
-      dk4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(table_t_rows(s_bt, vb, tl.lane, binv_k), qT, dk4,
-                                                    0, 0, 0);
-      dv4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(table_t_rows(s_at, vb, tl.lane, ainv_k), gT, dv4,
-                                                    0, 0, 0);
-      const int v0 = 16 * vb + 4 * (tl.lane >> 4);
-      int rr[4];
-      __builtin_memcpy(rr, &s_rows[v0], sizeof(rr));
+    // dK[v] += sum_q B[q][v] q[q];  dV[v] += sum_q A[q][v] dO[q]  (fp32 atomics;
+    // one register across the wave covers 2 voxels x 32 contiguous channels)
+    for (int vb = vq; vb * 32 < c.nv; vb += 4) {
+      f32x16_t dk = {}, dv = {};
+      dk = __builtin_amdgcn_mfma_f32_32x32x16_bf16(table_t_rows(s_bt, vb, tl.lane, binv_k), qT, dk,
+                                                   0, 0, 0);
+      dv = __builtin_amdgcn_mfma_f32_32x32x16_bf16(table_t_rows(s_at, vb, tl.lane, ainv_k), gT, dv,
+                                                   0, 0, 0);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        if (v0 + r >= c.nv) continue;
-        const int64_t off = (tl.sample0 + rr[r]) * D + ch;
-        if (dk4[r] != 0.0f) atomicAdd(dk_acc + off, dk4[r]);
-        if (dv4[r] != 0.0f) atomicAdd(dv_acc + off, dv4[r]);
+      for (int g = 0; g < 4; ++g) {
+        // registers 4g + i: voxel 32*vb + 8*g + 4*(lane/32) + i
+        const int v0 = 32 * vb + 8 * g + 4 * (tl.lane >> 5);
+        int rr[4];
+        __builtin_memcpy(rr, &s_rows[v0], sizeof(rr));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if (v0 + i >= c.nv) continue;
+          const int64_t off = (tl.sample0 + rr[i]) * D + ch2;
+          if (dk[4 * g + i] != 0.0f) atomicAdd(dk_acc + off, dk[4 * g + i]);
+          if (dv[4 * g + i] != 0.0f) atomicAdd(dv_acc + off, dv[4 * g + i]);
+        }
       }
     }
     __syncthreads();

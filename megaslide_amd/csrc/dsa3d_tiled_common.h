@@ -20,6 +20,7 @@ namespace tiled {
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
 typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
 typedef __attribute__((ext_vector_type(4))) float f32x4_t;
+typedef __attribute__((ext_vector_type(16))) float f32x16_t;
 typedef __attribute__((ext_vector_type(2))) float f32x2_t;
 typedef __attribute__((ext_vector_type(4))) unsigned int u32x4_t;
 
@@ -85,15 +86,17 @@ __device__ __forceinline__ Tile make_tile(const Args& a) {
   Tile t;
   t.head = blockIdx.y;
   // Workgroups are dispatched round-robin over the 8 XCDs; give each XCD a
-  // contiguous run of tiles so neighbouring tiles share its L2.
+  // contiguous run of tiles so neighbouring tiles share its L2.  Frames vary
+  // fastest: consecutive tiles of one (h, w) column read and accumulate into
+  // nearly the same K/V planes.
   int tile = blockIdx.x;
   if (a.xcd_remap > 0) tile = (tile & 7) * a.xcd_remap + (tile >> 3);
+  t.t = tile % a.T;
+  tile /= a.T;
   const int tw_i = tile % a.tiles_w;
   tile /= a.tiles_w;
   const int th_i = tile % a.tiles_h;
-  tile /= a.tiles_h;
-  t.t = tile % a.T;
-  t.b = tile / a.T;
+  t.b = tile / a.tiles_h;
   t.h0 = th_i * kTileH;
   t.w0 = tw_i * kTileW;
   t.sample0 = static_cast<int64_t>(t.b) * a.N;
