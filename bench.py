@@ -1,6 +1,7 @@
 """Benchmark: 3D-DSA forward + backward through the HIP kernel set on one MI355X.
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu-baseline] [--copy-calibration]
+    python bench.py --summarize TRACE_DIR FETCH_DIR WRITE_DIR   (rocprofv3 csv output -> profiles/)
 
 Workload (one step = one pass of the hot path over one batch): the 65,536-token
 long-clip case -- B=1, T=64, H=W=32, dim 1024, 16 heads x 64, window 3x7x7,
@@ -13,8 +14,16 @@ the projections stay in hipBLASLt and are not part of the step).
 
 Prints one JSON line.  `value` is tokens/s of the whole step; `roofline` is the
 dominant kernel's algorithmic HBM bytes per launch over its average duration,
-timed with events on the launch stream; `cpu_baseline` is the float32 CPU
+timed with events on the launch stream; `roofline.traffic` is the measured
+L2<->fabric bytes per launch of that kernel from profiles/traffic.json (two
+rocprofv3 --pmc runs, FETCH_SIZE and WRITE_SIZE, each scaled by the same
+counter on a plain copy of known size -- see --copy-calibration), or null when
+no measurement for that kernel is recorded; `cpu_baseline` is the float32 CPU
 oracle (the reference op sequence) on a bounded T-slab of the same workload.
+
+--copy-calibration first runs a plain 512 MiB -> 512 MiB bf16 copy (torch.neg)
+twice, so a counter run of this script also measures the copy the counters
+are scaled by.
 """
 
 from __future__ import annotations
@@ -55,12 +64,37 @@ def algorithmic_bytes(cfg, e):
     }
 
 
-def run_gpu(steps, warmup):
+COPY_BYTES = 512 * 2 ** 20  # read and written once each by the calibration copy
+
+
+def copy_calibration(dev):
+    src = torch.ones(COPY_BYTES // 2, dtype=torch.bfloat16, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(2):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    del src, dst
+
+
+def measured_traffic(kernel):
+    """Traffic bytes per launch recorded for `kernel` in profiles/traffic.json, or None."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            rec = json.load(f).get(kernel)
+    except (OSError, ValueError):
+        return None
+    return None if rec is None else rec.get("bytes_per_launch")
+
+
+def run_gpu(steps, warmup, calibrate=False):
     from megaslide_amd import _lib
 
     lib = _lib.load()
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if calibrate:
+        copy_calibration(dev)
     c = CFG
     B, T, H, W, D, nh, hd = c["B"], c["T"], c["H"], c["W"], c["D"], c["nh"], c["hd"]
     kt, kh, kw = c["kernel"]
@@ -181,12 +215,84 @@ def cpu_baseline(slab_T=2):
                 seconds=dt)
 
 
+KERNEL_KEYS = {  # rocprof kernel-name fragment -> bench phase
+    "dsa3d_bwd_tiled_kernel": "dsa3d_bwd",
+    "dsa3d_fwd_tiled_kernel": "dsa3d_fwd",
+}
+
+
+def summarize(trace_dir, fetch_dir, write_dir):
+    """Per-kernel averages from a rocprofv3 --kernel-trace --stats run and the
+    FETCH_SIZE / WRITE_SIZE runs of this script (--copy-calibration); prints a
+    markdown summary and writes profiles/traffic.json."""
+    import csv
+    import glob
+
+    def one(pattern):
+        hits = glob.glob(os.path.join(pattern))
+        if not hits:
+            raise FileNotFoundError(pattern)
+        with open(hits[0]) as f:
+            return list(csv.DictReader(f))
+
+    stats = one(os.path.join(trace_dir, "*kernel_stats.csv"))
+    print("| kernel | calls | avg ms | share |\n|---|---|---|---|")
+    for r in sorted(stats, key=lambda r: -float(r["TotalDurationNs"])):
+        print(f"| `{r['Name'][:90]}` | {r['Calls']} | {float(r['AverageNs']) / 1e6:.3f} | "
+              f"{float(r['Percentage']):.1f}% |")
+
+    def per_kernel(rows, counter):
+        acc = {}
+        for r in rows:
+            if r["Counter_Name"] != counter:
+                continue
+            key = (r["Kernel_Name"], r["Dispatch_Id"])
+            acc[key] = acc.get(key, 0.0) + float(r["Counter_Value"])
+        out = {}
+        for (name, _), v in acc.items():
+            out.setdefault(name, []).append(v)
+        return {k: sum(v) / len(v) for k, v in out.items()}
+
+    fetch = per_kernel(one(os.path.join(fetch_dir, "*counter_collection.csv")), "FETCH_SIZE")
+    write = per_kernel(one(os.path.join(write_dir, "*counter_collection.csv")), "WRITE_SIZE")
+    copy_f = [v for k, v in fetch.items() if "neg_kernel" in k]
+    copy_w = [v for k, v in write.items() if "neg_kernel" in k]
+    if not copy_f or not copy_w:
+        raise RuntimeError("no calibration copy (neg_kernel) in the counter runs")
+    kib = COPY_BYTES / 1024.0
+    sf, sw = copy_f[0] / kib, copy_w[0] / kib  # counter KiB per true KiB
+    print(f"\ncalibration copy {COPY_BYTES >> 20} MiB -> {COPY_BYTES >> 20} MiB: "
+          f"FETCH_SIZE {copy_f[0]:.0f} KiB (x{sf:.3f}), WRITE_SIZE {copy_w[0]:.0f} KiB (x{sw:.3f})\n")
+    ab = algorithmic_bytes(CFG, 2)
+    rec = {}
+    print("| kernel | FETCH KiB | WRITE KiB | traffic (scaled) | algorithmic | traffic / algorithmic |")
+    print("|---|---|---|---|---|---|")
+    for frag, phase in KERNEL_KEYS.items():
+        names = [k for k in fetch if frag in k]
+        if not names or names[0] not in write:
+            continue
+        n = names[0]
+        traffic = 1024.0 * (fetch[n] / sf + write[n] / sw)
+        rec[phase] = {"kernel": frag, "bytes_per_launch": int(traffic),
+                      "fetch_kib": round(fetch[n], 1), "write_kib": round(write[n], 1),
+                      "fetch_scale": round(sf, 4), "write_scale": round(sw, 4)}
+        print(f"| `{frag}` | {fetch[n]:.0f} | {write[n]:.0f} | {traffic / 1e9:.3f} GB | "
+              f"{ab[phase] / 1e9:.3f} GB | {traffic / ab[phase]:.2f} |")
+    with open(os.path.join(ROOT, "profiles", "traffic.json"), "w") as f:
+        json.dump(rec, f, indent=1)
+
+
 def main():
+    if len(sys.argv) == 5 and sys.argv[1] == "--summarize":
+        summarize(*sys.argv[2:])
+        return
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run a 512 MiB copy first (scale for the FETCH_SIZE/WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: the 3D-DSA kernels run on a single MI355X "
@@ -194,7 +300,7 @@ def main():
               file=sys.stderr)
         sys.exit(2)
 
-    r = run_gpu(args.steps, args.warmup)
+    r = run_gpu(args.steps, args.warmup, args.copy_calibration)
     e = 2
     ab = algorithmic_bytes(CFG, e)
     ms_step = r["total_ms"] / args.steps
@@ -231,7 +337,7 @@ def main():
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(dom),
             "algorithmic_bytes_per_launch": ab[dom],
             "avg_launch_ms": round(dom_ms, 4),
         },
