@@ -372,9 +372,12 @@ hipError_t bwd_typed(const msd_dsa3d_desc& d, const CoreArgs& a, const void* out
 
 int dsa3d_max_head_dim() { return kGroup * 16; }
 
+// dK/dV fp32 accumulators, plus what the tiled backward needs when the
+// descriptor can take that path.
 size_t dsa3d_bwd_ws_bytes(const msd_dsa3d_desc& d) {
   const int64_t rows = static_cast<int64_t>(d.B) * d.T * d.H * d.W;
-  return static_cast<size_t>(2 * rows * d.num_heads * d.head_dim) * sizeof(float);
+  return static_cast<size_t>(2 * rows * d.num_heads * d.head_dim) * sizeof(float) +
+         dsa3d_tiled_bwd_extra_bytes(d);
 }
 
 hipError_t launch_dsa3d_fwd_direct(const msd_dsa3d_desc& d, const void* q, const void* k, const void* v,

@@ -27,10 +27,10 @@ __global__ __launch_bounds__(kThreads, 4) void dsa3d_fwd_tiled_kernel(Args a, bf
   __shared__ __attribute__((aligned(16))) uint16_t s_vt[kHD * kVRow];  // V^T chunk
   __shared__ int s_red[kWaves][6];
 
-  const Tile tl = make_tile(a);
+  const Tile tl = make_tile<1, kSubs>(a);
   Slot sl[kSlots];
   Box box;
-  setup_slots(a, tl, sl, box, s_red);
+  setup_slots<kSubs, kSlots>(a, tl, sl, box, s_red);
   const int nchunks = box.ncy * box.ncx;
   const int nit = (box.zhi - box.zlo + 1) * nchunks;
 
@@ -152,35 +152,13 @@ __global__ __launch_bounds__(kThreads, 4) void dsa3d_fwd_tiled_kernel(Args a, bf
   }
 }
 
-// Q^T (or dO^T) as the B operand of the 32x32x16 MFMA, the 16 tile queries
-// being the contraction index: lane l holds queries k = 8*(l/32) + j of channel
-// 32*c2 + l%32 of the head.
-__device__ __forceinline__ bf16x8_t load_rows_transposed(const Args& a, const Tile& tl,
-                                                         const bf16* base, int64_t stride, int c2) {
-  u32x4_t r = {0u, 0u, 0u, 0u};
-  const int ch = tl.head * kHD + 32 * c2 + (tl.lane & 31);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int64_t r0 = tile_row(a, tl, 8 * (tl.lane >> 5) + 2 * i);
-    const int64_t r1 = tile_row(a, tl, 8 * (tl.lane >> 5) + 2 * i + 1);
-    const uint32_t lo = r0 >= 0 ? base[r0 * stride + ch].bits : 0u;
-    const uint32_t hi = r1 >= 0 ? base[r1 * stride + ch].bits : 0u;
-    r[i] = lo | (hi << 16);
-  }
-  return __builtin_bit_cast(bf16x8_t, r);
-}
-
-// Transposed tables [voxel][query] (row of 16 queries + 2 pad ints) used for
-// dK = B^T q and dV = A^T dO.  Stride 18 spreads the scatter atomics of a
-// wave's two queries over all LDS banks and keeps 8-byte aligned rows.
-constexpr int kTRow = kTQ + 2;
-
-// 32 x 16 block vb of a transposed fixed-point table as the A operand of the
-// 32x32x16 MFMA: lane l holds voxel 32*vb + l%32, queries 8*(l/32) + j (entry j
-// scaled by inv[j]), rounded to bf16.
-__device__ __forceinline__ bf16x8_t table_t_rows(const int* table_t, int vb, int lane,
-                                                 const float* inv) {
-  const int* p = &table_t[(32 * vb + (lane & 31)) * kTRow + 8 * (lane >> 5)];
+// 32 x 16 block vb of a transposed [voxel][query] fixed-point table (row stride
+// `row`, queries from column col0) as the A operand of the 32x32x16 MFMA: lane l
+// holds voxel 32*vb + l%32, queries col0 + 8*(l/32) + j (entry j scaled by
+// inv[j]), rounded to bf16.
+__device__ __forceinline__ bf16x8_t table_t_rows(const int* table_t, int row, int col0, int vb,
+                                                 int lane, const float* inv) {
+  const int* p = &table_t[(32 * vb + (lane & 31)) * row + col0 + 8 * (lane >> 5)];
   u32x4_t r;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -191,28 +169,23 @@ __device__ __forceinline__ bf16x8_t table_t_rows(const int* table_t, int vb, int
   return __builtin_bit_cast(bf16x8_t, r);
 }
 
-__global__ __launch_bounds__(kThreads) void dsa3d_bwd_tiled_kernel(
+// First backward kernel (one frame, 16 queries): pass 1 of the backward.  It
+// rebuilds S and dP = dO V^T per plane, accumulates per tap s, dp and their
+// coordinate derivatives, then writes the offset gradients and, for the second
+// kernel, p and ds * softmax_scale of every tap (fp32, [token][head][tap]).
+__global__ __launch_bounds__(kThreads) void dsa3d_bwd_p1_kernel(
     Args a, const bf16* __restrict__ out, const bf16* __restrict__ dout,
-    const float* __restrict__ lse, const float* __restrict__ dlse, bf16* __restrict__ dq,
-    float* __restrict__ dk_acc, float* __restrict__ dv_acc, bf16* __restrict__ doff) {
-  // pass 1: S and dP tables [query][voxel]; pass 2: transposed A and B tables
-  // [voxel][query]; at the end: partial dq
-  __shared__ __attribute__((aligned(16))) float s_buf[2 * kChunkNV * kTRow];
-  __shared__ __attribute__((aligned(16))) uint16_t s_kt[kHD * kVRow];  // K^T chunk
-  __shared__ __attribute__((aligned(16))) int s_rows[kChunkNV];        // token row (within the sample) per voxel
+    const float* __restrict__ lse, const float* __restrict__ dlse, bf16* __restrict__ doff,
+    float* __restrict__ p_ws, float* __restrict__ b_ws) {
+  __shared__ __attribute__((aligned(16))) float s_t0[kTQ * kSRow];  // S
+  __shared__ __attribute__((aligned(16))) float s_t1[kTQ * kSRow];  // dP
   __shared__ int s_red[kWaves][6];
-  static_assert(2 * kTQ * kSRow <= 2 * kChunkNV * kTRow, "tables must fit the shared buffer");
-  float* const s_t0 = s_buf;                     // S
-  float* const s_t1 = s_buf + kTQ * kSRow;       // dP
-  int* const s_at = reinterpret_cast<int*>(s_buf);                     // A^T = p w (fixed point)
-  int* const s_bt = reinterpret_cast<int*>(s_buf + kChunkNV * kTRow);  // B^T = ds scale w (fixed point)
-  __shared__ float s_binv[kTQ];  // per query: 1 / fixed-point scale of B
 
-  const Tile tl = make_tile(a);
+  const Tile tl = make_tile<1, kSubs>(a);
   const int D = a.nh * kHD;
   Slot sl[kSlots];
   Box box;
-  setup_slots(a, tl, sl, box, s_red);
+  setup_slots<kSubs, kSlots>(a, tl, sl, box, s_red);
   const int nchunks = box.ncy * box.ncx;
   const int nit = (box.zhi - box.zlo + 1) * nchunks;
 
@@ -291,16 +264,15 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_tiled_kernel(
   const float cxs = 0.5f * a.W * a.rdiv_x * a.offset_scale;
   const float cys = 0.5f * a.H * a.rdiv_y * a.offset_scale;
   const float czs = 0.5f * a.T * a.rdiv_z * a.offset_scale;
-  float p[kSlots], bsc[kSlots];
+  const int64_t tap0 = (tl.qn * a.nh + tl.head) * a.K;
 #pragma unroll
   for (int i = 0; i < kSlots; ++i) {
-    p[i] = bsc[i] = 0.0f;
     if (slot_z0(sl[i]) < 0) continue;
     const float pi = __expf(s_[i] * a.softmax_scale - lse_q);
     const float dss = pi * (dp_[i] - delta) * a.softmax_scale;
-    p[i] = pi;
-    bsc[i] = dss;
     const int kap = tl.sub + kSubs * i;
+    p_ws[tap0 + kap] = pi;
+    b_ws[tap0 + kap] = dss;
     bf16* dp = doff + tl.qn * a.C + (static_cast<int64_t>(tl.head) * a.K + kap) * 3;
     const int m = sl[i].zc >> 17;
     dp[0] = from_f32<bf16>((m & 1) ? (dss * gxs[i] + pi * gxd[i]) * cxs : 0.0f);
@@ -308,36 +280,100 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_tiled_kernel(
     dp[2] = from_f32<bf16>((m & 4) ? (dss * gzs[i] + pi * gzd[i]) * czs : 0.0f);
   }
 
+}
+
+// Second backward kernel: dq, dK and dV for tiles of kP2Frames consecutive
+// frames (kP2Q queries) of one 4x4 (h, w) column.  Consecutive frames reach
+// nearly the same planes, so one flush of the [voxel][query] tables per plane
+// serves all of them: the fp32 dK/dV atomics (executed past the L2, the
+// backward's dominant cost) drop accordingly.  Tap geometry is recomputed from
+// the offsets; p and ds * scale come from the first kernel.
+constexpr int kP2Frames = 2;
+constexpr int kP2Q = kTQ * kP2Frames;          // queries per tile
+constexpr int kP2Subs = kThreads / kP2Q;       // lanes per query
+constexpr int kP2Slots = kMaxTaps / kP2Subs;   // taps per lane
+constexpr int kP2Row = kP2Q + 2;               // [voxel][query] table row (ints)
+constexpr int kP2QRow = kP2Q + 8;              // [channel][query] row of staged q / dO (bf16)
+static_assert(kP2Subs * kP2Slots == kMaxTaps, "the tap capacity must match the first kernel");
+
+__global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
+    Args a, const bf16* __restrict__ dout, const float* __restrict__ p_ws,
+    const float* __restrict__ b_ws, bf16* __restrict__ dq, float* __restrict__ dk_acc,
+    float* __restrict__ dv_acc) {
+  __shared__ __attribute__((aligned(16))) int s_at[kChunkNV * kP2Row];  // A^T = p w (fixed point)
+  __shared__ __attribute__((aligned(16))) int s_bt[kChunkNV * kP2Row];  // B^T = ds scale w (fixed point)
+  __shared__ __attribute__((aligned(16))) uint16_t s_kt[kHD * kVRow];   // K^T chunk
+  __shared__ __attribute__((aligned(16))) int s_rows[kChunkNV];         // token row (within the sample) per voxel
+  __shared__ int s_red[kWaves][6];
+  __shared__ float s_binv[kP2Q];  // per query: 1 / fixed-point scale of B
+  // the tile's q and dO rows of this head, transposed: [tensor][channel][query]
+  __shared__ __attribute__((aligned(16))) uint16_t s_qt[2][kHD][kP2QRow];
+
+  const Tile tl = make_tile<kP2Frames, kP2Subs>(a);
+  const int D = a.nh * kHD;
+  Slot sl[kP2Slots];
+  Box box;
+  setup_slots<kP2Subs, kP2Slots>(a, tl, sl, box, s_red);
+  const int nchunks = box.ncy * box.ncx;
+  const int nit = (box.zhi - box.zlo + 1) * nchunks;
+
+  float p[kP2Slots], bsc[kP2Slots];
+  const int64_t tap0 = (tl.qn * a.nh + tl.head) * a.K;
+#pragma unroll
+  for (int i = 0; i < kP2Slots; ++i) {
+    p[i] = bsc[i] = 0.0f;
+    if (slot_z0(sl[i]) < 0) continue;
+    const int kap = tl.sub + kP2Subs * i;
+    p[i] = p_ws[tap0 + kap];
+    bsc[i] = b_ws[tap0 + kap];
+  }
   // fixed-point scale of this query's B entries: 2^30 / sum_k |ds_k scale|
   float l1 = 0.0f;
 #pragma unroll
-  for (int i = 0; i < kSlots; ++i) l1 += fabsf(bsc[i]);
+  for (int i = 0; i < kP2Slots; ++i) l1 += fabsf(bsc[i]);
 #pragma unroll
-  for (int m = 1; m < kSubs; m <<= 1) l1 += __shfl_xor(l1, m);
+  for (int m = 1; m < kP2Subs; m <<= 1) l1 += __shfl_xor(l1, m);
   const bool l1_ok = l1 > 1e-30f;
   const float bscale = l1_ok ? kFixA / l1 : 0.0f;
   if (tl.sub == 0) s_binv[tl.q] = l1_ok ? l1 * kFixAInv : 0.0f;
+  // stage q and dO of the tile transposed: thread i moves 8 channels of one row
+  {
+    const int tensor = threadIdx.x >> 8, m = (threadIdx.x >> 3) & (kP2Q - 1), cg = threadIdx.x & 7;
+    const int64_t n = tile_row(a, tl, m);
+    u32x4_t x = {0u, 0u, 0u, 0u};
+    if (n >= 0) {
+      const bf16* src = tensor == 0 ? a.q + n * a.qs : dout + n * D;
+      x = load16(src + tl.head * kHD + 8 * cg);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      s_qt[tensor][8 * cg + 2 * i][m] = static_cast<uint16_t>(x[i] & 0xffffu);
+      s_qt[tensor][8 * cg + 2 * i + 1][m] = static_cast<uint16_t>(x[i] >> 16);
+    }
+  }
   __syncthreads();
 
-  // ---- pass 2: dq = B K, dK = B^T q, dV = A^T dO ---------------------------------
-  // dq (16x16x32 MFMA): wave w owns channels 16*(w & 3) + [0, 16) and the voxel
-  // k-steps of parity w >> 2.  dK/dV (32x32x16 MFMA): wave w owns channels
-  // 32*(w & 1) + [0, 32) and the 32-voxel blocks (w >> 1) + 4 i.
+  // dq (16x16x32 MFMA): wave w owns frame w >> 2 of the tile, channels
+  // 16*(w & 3) + [0, 16).  dK/dV (32x32x16 MFMA, one per frame): wave w owns
+  // channels 32*(w & 1) + [0, 32) and the 32-voxel blocks (w >> 1) + 4 i.
   const int mq = tl.lane & 15, kq = 8 * (tl.lane >> 4);
-  const int ct = tl.wave & 3, half = tl.wave >> 2;
+  const int fq = tl.wave >> 2, ct = tl.wave & 3;
   const int c2 = tl.wave & 1, vq = tl.wave >> 1;
-  const bf16x8_t qT = load_rows_transposed(a, tl, a.q, a.qs, c2);
-  const bf16x8_t gT = load_rows_transposed(a, tl, dout, D, c2);
+  bf16x8_t qT[kP2Frames], gT[kP2Frames];
+  float binv_k[kP2Frames][8], ainv_k[8];
+#pragma unroll
+  for (int f = 0; f < kP2Frames; ++f) {
+    const int ch = 32 * c2 + (tl.lane & 31), q0 = kTQ * f + 8 * (tl.lane >> 5);
+    __builtin_memcpy(&qT[f], &s_qt[0][ch][q0], sizeof(bf16x8_t));
+    __builtin_memcpy(&gT[f], &s_qt[1][ch][q0], sizeof(bf16x8_t));
+#pragma unroll
+    for (int j = 0; j < 8; ++j) binv_k[f][j] = s_binv[kTQ * f + 8 * (tl.lane >> 5) + j];
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) ainv_k[j] = kFixAInv;
+  const float binv_m = s_binv[kTQ * fq + mq];
   const int ch = tl.head * kHD + 16 * ct + mq;
   const int ch2 = tl.head * kHD + 32 * c2 + (tl.lane & 31);
-  // B scales of this lane's dq row (query mq) and of its dK contraction queries
-  const float binv_m = s_binv[mq];
-  float binv_k[8], ainv_k[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    binv_k[j] = s_binv[8 * (tl.lane >> 5) + j];
-    ainv_k[j] = kFixAInv;
-  }
   f32x4_t dq_acc = {0.0f, 0.0f, 0.0f, 0.0f};
   StageRows kr;
   if (nit > 0) load_stage_rows(a, tl, make_chunk(box, 0), box.zlo, a.k, a.ks, kr);
@@ -346,8 +382,8 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_tiled_kernel(
     const int z = box.zlo + zi;
     const Chunk c = make_chunk(box, it - zi * nchunks);
     // zero the transposed A and B tables; token rows of the chunk's voxels
-    for (int e = threadIdx.x; e < c.nvp * kTRow / 4; e += kThreads) {
-      const f32x4_t zz = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int e = threadIdx.x; e < c.nvp * kP2Row / 4; e += kThreads) {
+      const u32x4_t zz = {0u, 0u, 0u, 0u};
       __builtin_memcpy(&s_at[4 * e], &zz, sizeof(zz));
       __builtin_memcpy(&s_bt[4 * e], &zz, sizeof(zz));
     }
@@ -360,37 +396,38 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_tiled_kernel(
     }
     __syncthreads();
 #pragma unroll
-    for (int i = 0; i < kSlots; ++i) {
+    for (int i = 0; i < kP2Slots; ++i) {
       float wz, dwz;
       if (!slot_hits(sl[i], z, c.id, wz, dwz)) continue;
       const float pz = p[i] * wz * kFixA, bz = bsc[i] * wz * bscale;
       const float fx = sl[i].fx, fy = sl[i].fy, gx = 1.0f - fx, gy = 1.0f - fy;
       const float w00 = gy * gx, w01 = gy * fx, w10 = fy * gx, w11 = fy * fx;
       const int base = sl[i].idx & 0x1ff, dy = (sl[i].idx >> 9) & 0x1f, dx = (sl[i].idx >> 14) & 1;
-      int* ra = &s_at[base * kTRow + tl.q];
-      int* rb = &s_bt[base * kTRow + tl.q];
+      int* ra = &s_at[base * kP2Row + tl.q];
+      int* rb = &s_bt[base * kP2Row + tl.q];
       atomicAdd(ra, to_fix(pz * w00));
       atomicAdd(rb, to_fix(bz * w00));
       if (dx) {
-        atomicAdd(ra + kTRow, to_fix(pz * w01));
-        atomicAdd(rb + kTRow, to_fix(bz * w01));
+        atomicAdd(ra + kP2Row, to_fix(pz * w01));
+        atomicAdd(rb + kP2Row, to_fix(bz * w01));
       }
       if (dy) {
-        atomicAdd(ra + dy * kTRow, to_fix(pz * w10));
-        atomicAdd(rb + dy * kTRow, to_fix(bz * w10));
+        atomicAdd(ra + dy * kP2Row, to_fix(pz * w10));
+        atomicAdd(rb + dy * kP2Row, to_fix(bz * w10));
       }
       if (dx && dy) {
-        atomicAdd(ra + (dy + 1) * kTRow, to_fix(pz * w11));
-        atomicAdd(rb + (dy + 1) * kTRow, to_fix(bz * w11));
+        atomicAdd(ra + (dy + 1) * kP2Row, to_fix(pz * w11));
+        atomicAdd(rb + (dy + 1) * kP2Row, to_fix(bz * w11));
       }
     }
     __syncthreads();
     // dq[q] += sum_v B[q][v] K[v]; B as a bf16 hi/lo pair because
     // sum_v B[q][v] = 0 and K may carry a large common part
-    for (int kc = 32 * half; kc < c.nvp; kc += 64) {
+    for (int kc = 0; kc < c.nvp; kc += 32) {
       float bq[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) bq[j] = static_cast<float>(s_bt[(kc + kq + j) * kTRow + mq]) * binv_m;
+      for (int j = 0; j < 8; ++j)
+        bq[j] = static_cast<float>(s_bt[(kc + kq + j) * kP2Row + kTQ * fq + mq]) * binv_m;
       bf16x8_t bhi, blo, kv;
       to_bf16x8_hilo(bq, bhi, blo);
       __builtin_memcpy(&kv, &s_kt[(16 * ct + mq) * kVRow + kc + kq], sizeof(kv));
@@ -401,10 +438,13 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_tiled_kernel(
     // one register across the wave covers 2 voxels x 32 contiguous channels)
     for (int vb = vq; vb * 32 < c.nv; vb += 4) {
       f32x16_t dk = {}, dv = {};
-      dk = __builtin_amdgcn_mfma_f32_32x32x16_bf16(table_t_rows(s_bt, vb, tl.lane, binv_k), qT, dk,
-                                                   0, 0, 0);
-      dv = __builtin_amdgcn_mfma_f32_32x32x16_bf16(table_t_rows(s_at, vb, tl.lane, ainv_k), gT, dv,
-                                                   0, 0, 0);
+#pragma unroll
+      for (int f = 0; f < kP2Frames; ++f) {
+        dk = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+            table_t_rows(s_bt, kP2Row, kTQ * f, vb, tl.lane, binv_k[f]), qT[f], dk, 0, 0, 0);
+        dv = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+            table_t_rows(s_at, kP2Row, kTQ * f, vb, tl.lane, ainv_k), gT[f], dv, 0, 0, 0);
+      }
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         // registers 4g + i: voxel 32*vb + 8*g + 4*(lane/32) + i
@@ -422,29 +462,19 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_tiled_kernel(
     }
     __syncthreads();
   }
-
-  // ---- dq: dq_acc[r] = partial dq[query 4*(lane/16) + r][channel 16*ct + lane%16];
-  // the two halves of the k-steps are summed through LDS
-  float* red = s_buf;  // 16 x 64
-  if (half == 1) {
+  // dq_acc[r] = dq[query 16*fq + 4*(lane/16) + r][channel 16*ct + lane%16]
 #pragma unroll
-    for (int r = 0; r < 4; ++r) red[(4 * (tl.lane >> 4) + r) * kHD + 16 * ct + mq] = dq_acc[r];
-  }
-  __syncthreads();
-  if (half == 0) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int m = 4 * (tl.lane >> 4) + r;
-      const int64_t n = tile_row(a, tl, m);
-      if (n >= 0) dq[n * a.qs + ch] = from_f32<bf16>(dq_acc[r] + red[m * kHD + 16 * ct + mq]);
-    }
+  for (int r = 0; r < 4; ++r) {
+    const int64_t n = tile_row(a, tl, kTQ * fq + 4 * (tl.lane >> 4) + r);
+    if (n >= 0) dq[n * a.qs + ch] = from_f32<bf16>(dq_acc[r]);
   }
 }
 
 }  // namespace
 
+// Kernel arguments for a launch over `tiles` workgroups per head.
 tiled::Args make_tiled_args(const msd_dsa3d_desc& d, const void* q, const void* k, const void* v,
-                            const void* off) {
+                            const void* off, int64_t tiles) {
   tiled::Args a;
   a.q = static_cast<const bf16*>(q);
   a.k = static_cast<const bf16*>(k);
@@ -466,7 +496,6 @@ tiled::Args make_tiled_args(const msd_dsa3d_desc& d, const void* q, const void* 
   a.C = d.num_heads * a.K * 3;
   a.tiles_h = (d.H + tiled::kTileH - 1) / tiled::kTileH;
   a.tiles_w = (d.W + tiled::kTileW - 1) / tiled::kTileW;
-  const int64_t tiles = static_cast<int64_t>(d.B) * d.T * a.tiles_h * a.tiles_w;
   a.xcd_remap = (tiles % 8 == 0) ? static_cast<int>(tiles / 8) : 0;
   a.offset_scale = d.offset_scale;
   a.softmax_scale = d.softmax_scale;
@@ -487,10 +516,14 @@ tiled::Args make_tiled_args(const msd_dsa3d_desc& d, const void* q, const void* 
   return a;
 }
 
+template <int FRAMES>
+int64_t tiled_tiles(const msd_dsa3d_desc& d) {
+  return tiled::tile_count<FRAMES>(d.B, d.T, d.H, d.W);
+}
+
+template <int FRAMES>
 dim3 tiled_grid(const msd_dsa3d_desc& d) {
-  const int64_t tiles = static_cast<int64_t>(d.B) * d.T * ((d.H + tiled::kTileH - 1) / tiled::kTileH) *
-                        ((d.W + tiled::kTileW - 1) / tiled::kTileW);
-  return dim3(static_cast<unsigned>(tiles), d.num_heads);
+  return dim3(static_cast<unsigned>(tiled_tiles<FRAMES>(d)), d.num_heads);
 }
 
 bool dsa3d_tiled_supported(const msd_dsa3d_desc& d, const void* q, const void* k, const void* v) {
@@ -513,8 +546,8 @@ bool dsa3d_tiled_supported(const msd_dsa3d_desc& d, const void* q, const void* k
 hipError_t launch_dsa3d_fwd_tiled(const msd_dsa3d_desc& d, const void* q, const void* k,
                                   const void* v, const void* off, void* out, float* lse,
                                   hipStream_t s) {
-  const tiled::Args a = make_tiled_args(d, q, k, v, off);
-  hipLaunchKernelGGL(dsa3d_fwd_tiled_kernel, tiled_grid(d), dim3(tiled::kThreads), 0, s, a,
+  const tiled::Args a = make_tiled_args(d, q, k, v, off, tiled_tiles<1>(d));
+  hipLaunchKernelGGL(dsa3d_fwd_tiled_kernel, tiled_grid<1>(d), dim3(tiled::kThreads), 0, s, a,
                      static_cast<bf16*>(out), lse);
   return hipGetLastError();
 }
@@ -532,20 +565,36 @@ __global__ __launch_bounds__(256) void acc_to_bf16_kernel(const float* __restric
 }
 }  // namespace
 
+// Workspace of the tiled backward beyond the dK/dV accumulators: p and
+// ds * softmax_scale of every tap (fp32 [token][head][tap] each).
+size_t dsa3d_tiled_bwd_extra_bytes(const msd_dsa3d_desc& d) {
+  if (d.dtype != MSD_BF16 || d.head_dim != tiled::kHD || d.kt * d.kh * d.kw > tiled::kMaxTaps)
+    return 0;
+  const int64_t rows = static_cast<int64_t>(d.B) * d.T * d.H * d.W;
+  return static_cast<size_t>(2 * rows * d.num_heads * d.kt * d.kh * d.kw) * sizeof(float);
+}
+
 hipError_t launch_dsa3d_bwd_tiled(const msd_dsa3d_desc& d, const void* q, const void* k,
                                   const void* v, const void* off, const void* out,
                                   const void* dout, const float* lse, const float* dlse, void* dq,
                                   void* dk, void* dv, void* doff, void* ws, hipStream_t s) {
-  const tiled::Args a = make_tiled_args(d, q, k, v, off);
   const int64_t rows = static_cast<int64_t>(d.B) * d.T * d.H * d.W;
   const int D = d.num_heads * d.head_dim;
+  const int64_t taps = rows * d.num_heads * d.kt * d.kh * d.kw;
   float* dk_acc = static_cast<float*>(ws);
   float* dv_acc = dk_acc + rows * D;
+  float* p_ws = dv_acc + rows * D;
+  float* b_ws = p_ws + taps;
   hipLaunchKernelGGL(fill_zero_f32, dim3(fill_blocks(2 * rows * D)), dim3(256), 0, s, dk_acc,
                      2 * rows * D);
-  hipLaunchKernelGGL(dsa3d_bwd_tiled_kernel, tiled_grid(d), dim3(tiled::kThreads), 0, s, a,
+  const tiled::Args a1 = make_tiled_args(d, q, k, v, off, tiled_tiles<1>(d));
+  hipLaunchKernelGGL(dsa3d_bwd_p1_kernel, tiled_grid<1>(d), dim3(tiled::kThreads), 0, s, a1,
                      static_cast<const bf16*>(out), static_cast<const bf16*>(dout), lse, dlse,
-                     static_cast<bf16*>(dq), dk_acc, dv_acc, static_cast<bf16*>(doff));
+                     static_cast<bf16*>(doff), p_ws, b_ws);
+  const tiled::Args a2 = make_tiled_args(d, q, k, v, off, tiled_tiles<kP2Frames>(d));
+  hipLaunchKernelGGL(dsa3d_bwd_p2_kernel, tiled_grid<kP2Frames>(d), dim3(tiled::kThreads), 0, s,
+                     a2, static_cast<const bf16*>(dout), p_ws, b_ws, static_cast<bf16*>(dq), dk_acc,
+                     dv_acc);
   const dim3 cgrid(static_cast<unsigned>((rows * D + 255) / 256));
   hipLaunchKernelGGL(acc_to_bf16_kernel, cgrid, dim3(256), 0, s, dk_acc, static_cast<bf16*>(dk),
                      rows, D, d.k_stride);

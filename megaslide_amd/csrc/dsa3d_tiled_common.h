@@ -1,8 +1,11 @@
 // Shared building blocks of the matrix-core (tiled) 3D-DSA kernels.
 //
-// A workgroup of 8 waves owns one (batch, head, tile of 16 queries = 1 frame x
-// 4 rows x 4 columns).  Lane l of wave w serves query q = 2w + (l >> 5) and the
-// taps kappa = (l & 31) + 32 i, i < kSlots.  Every tap's 2x2 (y, x) corner
+// A workgroup of 8 waves owns one (batch, head, tile of FRAMES consecutive
+// frames x 4 rows x 4 columns of queries).  Thread i serves group query
+// q = i / SUBS (frame q / 16 of the tile, position q % 16) and the taps
+// kappa = (i % SUBS) + SUBS * j, j < SLOTS.  The forward and the first backward
+// kernel use FRAMES = 1, SUBS = 32, SLOTS = 5; the dK/dV/dq kernel FRAMES = 2,
+// SUBS = 16, SLOTS = 10.  Every tap's 2x2 (y, x) corner
 // footprint is resolved against per-plane score tables
 //   S[q][v] = X[q] . Y[v]   (X = q or dO rows, Y = K or V rows; MFMA, fp32 in LDS)
 // built over the (y, x) bounding box of all corners of the tile, cut into
@@ -29,7 +32,7 @@ constexpr int kTileH = 4, kTileW = 4;
 constexpr int kTQ = kTileH * kTileW;    // queries per tile
 constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
-constexpr int kSubs = 32;               // lanes per query
+constexpr int kSubs = 32;               // lanes per query (single-frame kernels)
 constexpr int kSlots = 5;               // taps per lane: windows of <= kSubs * kSlots taps
 constexpr int kMaxTaps = kSubs * kSlots;
 constexpr int kChunk = 16;              // chunk edge in y and x
@@ -75,13 +78,22 @@ __device__ __forceinline__ int slot_chunk(const Slot& s) {
 }
 
 struct Tile {
-  int b, head, t, h0, w0;
+  int b, head, t0, t, h0, w0;  // t0: first frame of the tile; t: this lane's frame
   int64_t sample0;
-  int wave, lane, q, sub;
+  int wave, lane, q, sub;      // q: group query of this lane (table column)
+  int qh, qw;                  // this lane's query position
   bool q_ok;
   int64_t qn;  // token row of this lane's query
 };
 
+// Tiles of one launch: B x ceil(T / FRAMES) x tiles_h x tiles_w.
+template <int FRAMES>
+inline int64_t tile_count(int B, int T, int H, int W) {
+  return static_cast<int64_t>(B) * ((T + FRAMES - 1) / FRAMES) * ((H + kTileH - 1) / kTileH) *
+         ((W + kTileW - 1) / kTileW);
+}
+
+template <int FRAMES, int SUBS>
 __device__ __forceinline__ Tile make_tile(const Args& a) {
   Tile t;
   t.head = blockIdx.y;
@@ -91,8 +103,9 @@ __device__ __forceinline__ Tile make_tile(const Args& a) {
   // nearly the same K/V planes.
   int tile = blockIdx.x;
   if (a.xcd_remap > 0) tile = (tile & 7) * a.xcd_remap + (tile >> 3);
-  t.t = tile % a.T;
-  tile /= a.T;
+  const int groups = (a.T + FRAMES - 1) / FRAMES;
+  t.t0 = (tile % groups) * FRAMES;
+  tile /= groups;
   const int tw_i = tile % a.tiles_w;
   tile /= a.tiles_w;
   const int th_i = tile % a.tiles_h;
@@ -102,19 +115,23 @@ __device__ __forceinline__ Tile make_tile(const Args& a) {
   t.sample0 = static_cast<int64_t>(t.b) * a.N;
   t.wave = threadIdx.x >> 6;
   t.lane = threadIdx.x & 63;
-  t.q = 2 * t.wave + (t.lane >> 5);
-  t.sub = t.lane & 31;
-  const int qh = t.h0 + t.q / kTileW, qw = t.w0 + t.q % kTileW;
-  t.q_ok = qh < a.H && qw < a.W;
-  t.qn = t.sample0 + (static_cast<int64_t>(t.t) * a.H + qh) * a.W + qw;
+  t.q = threadIdx.x / SUBS;
+  t.sub = threadIdx.x % SUBS;
+  t.t = t.t0 + t.q / kTQ;
+  const int s = t.q % kTQ;
+  t.qh = t.h0 + s / kTileW;
+  t.qw = t.w0 + s % kTileW;
+  t.q_ok = t.t < a.T && t.qh < a.H && t.qw < a.W;
+  t.qn = t.sample0 + (static_cast<int64_t>(t.t) * a.H + t.qh) * a.W + t.qw;
   return t;
 }
 
-// Token row of tile query m (0..15), or -1 outside the grid.
+// Token row of group query m (frame m / 16, position m % 16), or -1 outside the grid.
 __device__ __forceinline__ int64_t tile_row(const Args& a, const Tile& t, int m) {
-  const int h = t.h0 + m / kTileW, w = t.w0 + m % kTileW;
-  if (h >= a.H || w >= a.W) return -1;
-  return t.sample0 + (static_cast<int64_t>(t.t) * a.H + h) * a.W + w;
+  const int tt = t.t0 + m / kTQ, s = m % kTQ;
+  const int h = t.h0 + s / kTileW, w = t.w0 + s % kTileW;
+  if (tt >= a.T || h >= a.H || w >= a.W) return -1;
+  return t.sample0 + (static_cast<int64_t>(tt) * a.H + h) * a.W + w;
 }
 
 struct Box {
@@ -134,17 +151,18 @@ __device__ __forceinline__ float grid_coord_rn(float base, float o, float div, f
   return div > 0.0f ? base + div_rn(o, div, rdiv) : base;
 }
 
-// Tap geometry for all slots of this lane (coordinates exactly as the
+// Tap geometry for all SLOTS slots of this lane (coordinates exactly as the
 // reference rounds them) and the block-wide bounding box of every corner.
+template <int SUBS, int SLOTS>
 __device__ __forceinline__ void setup_slots(const Args& a, const Tile& tl, Slot* sl, Box& box,
                                             int (*s_red)[6]) {
   int zlo = 1 << 30, zhi = -1, ylo = 1 << 30, yhi = -1, xlo = 1 << 30, xhi = -1;
-  int y0s[kSlots], x0s[kSlots];
-  const int qh = tl.h0 + tl.q / kTileW, qw = tl.w0 + tl.q % kTileW;
+  int y0s[SLOTS], x0s[SLOTS];
+  const int qh = tl.qh, qw = tl.qw;
   const int khkw = a.kh * a.kw;
 #pragma unroll
-  for (int i = 0; i < kSlots; ++i) {
-    const int kap = tl.sub + kSubs * i;
+  for (int i = 0; i < SLOTS; ++i) {
+    const int kap = tl.sub + SUBS * i;
     sl[i].zc = 0xffff;  // z0 = -1: empty
     sl[i].idx = 0;
     sl[i].fz = sl[i].fx = sl[i].fy = 0.0f;
@@ -231,7 +249,7 @@ __device__ __forceinline__ void setup_slots(const Args& a, const Tile& tl, Slot*
   box.ncx = max(1, (box.xhi - box.xlo + kChunkStep - 1) / kChunkStep);
   // assign every tap to the chunk holding its whole 2x2 footprint
 #pragma unroll
-  for (int i = 0; i < kSlots; ++i) {
+  for (int i = 0; i < SLOTS; ++i) {
     if (slot_z0(sl[i]) < 0) continue;
     const bool hy = sl[i].idx & 1, hx = sl[i].idx & 2;
     const int cy = min((y0s[i] - box.ylo) / kChunkStep, box.ncy - 1);
