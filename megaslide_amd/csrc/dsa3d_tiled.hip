@@ -305,7 +305,7 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
   __shared__ __attribute__((aligned(16))) uint16_t s_kt[kHD * kVRow];   // K^T chunk
   __shared__ __attribute__((aligned(16))) int s_rows[kChunkNV];         // token row (within the sample) per voxel
   __shared__ int s_red[kWaves][6];
-  __shared__ float s_binv[kP2Q];  // per query: 1 / fixed-point scale of B
+  __shared__ __attribute__((aligned(16))) float s_binv[kP2Q];  // per query: 1 / fixed-point scale of B
   // the tile's q and dO rows of this head, transposed: [tensor][channel][query]
   __shared__ __attribute__((aligned(16))) uint16_t s_qt[2][kHD][kP2QRow];
 
@@ -359,16 +359,10 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
   const int mq = tl.lane & 15, kq = 8 * (tl.lane >> 4);
   const int fq = tl.wave >> 2, ct = tl.wave & 3;
   const int c2 = tl.wave & 1, vq = tl.wave >> 1;
-  bf16x8_t qT[kP2Frames], gT[kP2Frames];
-  float binv_k[kP2Frames][8], ainv_k[8];
-#pragma unroll
-  for (int f = 0; f < kP2Frames; ++f) {
-    const int ch = 32 * c2 + (tl.lane & 31), q0 = kTQ * f + 8 * (tl.lane >> 5);
-    __builtin_memcpy(&qT[f], &s_qt[0][ch][q0], sizeof(bf16x8_t));
-    __builtin_memcpy(&gT[f], &s_qt[1][ch][q0], sizeof(bf16x8_t));
-#pragma unroll
-    for (int j = 0; j < 8; ++j) binv_k[f][j] = s_binv[kTQ * f + 8 * (tl.lane >> 5) + j];
-  }
+  // operands of the dK/dV MFMAs are re-read from LDS where used (registers are
+  // the limit here: a spill reload would wait for every outstanding atomic)
+  const int och = 32 * c2 + (tl.lane & 31), oq = 8 * (tl.lane >> 5);
+  float ainv_k[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) ainv_k[j] = kFixAInv;
   const float binv_m = s_binv[kTQ * fq + mq];
@@ -402,7 +396,11 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
       const float pz = p[i] * wz * kFixA, bz = bsc[i] * wz * bscale;
       const float fx = sl[i].fx, fy = sl[i].fy, gx = 1.0f - fx, gy = 1.0f - fy;
       const float w00 = gy * gx, w01 = gy * fx, w10 = fy * gx, w11 = fy * fx;
-      const int base = sl[i].idx & 0x1ff, dy = (sl[i].idx >> 9) & 0x1f, dx = (sl[i].idx >> 14) & 1;
+      // decode the corner index here rather than keeping 4 addresses per tap live
+      // across the plane loop
+      int idx = sl[i].idx;
+      asm volatile("" : "+v"(idx));
+      const int base = idx & 0x1ff, dy = (idx >> 9) & 0x1f, dx = (idx >> 14) & 1;
       int* ra = &s_at[base * kP2Row + tl.q];
       int* rb = &s_bt[base * kP2Row + tl.q];
       atomicAdd(ra, to_fix(pz * w00));
@@ -440,10 +438,15 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
       f32x16_t dk = {}, dv = {};
 #pragma unroll
       for (int f = 0; f < kP2Frames; ++f) {
+        float binv_k[8];
+        __builtin_memcpy(binv_k, &s_binv[kTQ * f + oq], sizeof(binv_k));
+        bf16x8_t qTf, gTf;
+        __builtin_memcpy(&qTf, &s_qt[0][och][kTQ * f + oq], sizeof(qTf));
+        __builtin_memcpy(&gTf, &s_qt[1][och][kTQ * f + oq], sizeof(gTf));
         dk = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-            table_t_rows(s_bt, kP2Row, kTQ * f, vb, tl.lane, binv_k[f]), qT[f], dk, 0, 0, 0);
+            table_t_rows(s_bt, kP2Row, kTQ * f, vb, tl.lane, binv_k), qTf, dk, 0, 0, 0);
         dv = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-            table_t_rows(s_at, kP2Row, kTQ * f, vb, tl.lane, ainv_k), gT[f], dv, 0, 0, 0);
+            table_t_rows(s_at, kP2Row, kTQ * f, vb, tl.lane, ainv_k), gTf, dv, 0, 0, 0);
       }
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
