@@ -98,7 +98,7 @@ __global__ __launch_bounds__(kThreads, 4) void dsa3d_fwd_tiled_kernel(Args a, bf
   f32x4_t oacc = {0.0f, 0.0f, 0.0f, 0.0f};
   int* const s_atab = reinterpret_cast<int*>(s_tab);  // A in fixed point (scale 2^30)
   int* row = &s_atab[tl.q * kSRow];
-  StageRows vr;
+  StageRows<kThreads> vr;
   if (nit > 0) load_stage_rows(a, tl, make_chunk(box, 0), box.zlo, a.v, a.vs, vr);
   for (int it = 0; it < nit; ++it) {
     const int zi = it / nchunks;
@@ -369,7 +369,7 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
   const int ch = tl.head * kHD + 16 * ct + mq;
   const int ch2 = tl.head * kHD + 32 * c2 + (tl.lane & 31);
   f32x4_t dq_acc = {0.0f, 0.0f, 0.0f, 0.0f};
-  StageRows kr;
+  StageRows<kThreads> kr;
   if (nit > 0) load_stage_rows(a, tl, make_chunk(box, 0), box.zlo, a.k, a.ks, kr);
   for (int it = 0; it < nit; ++it) {
     const int zi = it / nchunks;

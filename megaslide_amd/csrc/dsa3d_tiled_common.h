@@ -354,35 +354,42 @@ __device__ __forceinline__ void store_table(const Tile& tl, const Chunk& c, bf16
 }
 
 // Chunk rows of Y (plane z) transposed into LDS: yt[channel][voxel] (bf16),
-// zero padded up to nvp voxels.  Thread t moves voxels 2*(t & 127) + {0, 1},
-// channel groups (t >> 7) and (t >> 7) + 4 (8 channels each); the four loads
-// are issued first.
+// zero padded up to nvp voxels, by the first NT threads of the workgroup.
+// Thread t moves voxels 2*(t % 128) + {0, 1}, channel groups t / 128 + P*g
+// (P = NT / 128, g < 8 / P; 8 channels each); its loads are issued first.
+template <int NT>
 struct StageRows {
-  u32x4_t x[2][2];  // [channel group][voxel]
+  static constexpr int P = NT / 128, G = 8 / P;
+  u32x4_t x[G][2];  // [channel group][voxel]
 };
 
+template <int NT>
 __device__ __forceinline__ void load_stage_rows(const Args& a, const Tile& tl, const Chunk& c,
                                                 int z, const bf16* ybase, int64_t ystride,
-                                                StageRows& r) {
-  const int cg = threadIdx.x >> 7, v0 = 2 * (threadIdx.x & 127);
+                                                StageRows<NT>& r) {
+  constexpr int P = StageRows<NT>::P, G = StageRows<NT>::G;
+  const int cg0 = threadIdx.x >> 7, v0 = 2 * (threadIdx.x & 127);
   const u32x4_t z4 = {0u, 0u, 0u, 0u};
-  r.x[0][0] = r.x[0][1] = r.x[1][0] = r.x[1][1] = z4;
+#pragma unroll
+  for (int g = 0; g < G; ++g) r.x[g][0] = r.x[g][1] = z4;
 #pragma unroll
   for (int e = 0; e < 2; ++e) {
     if (v0 + e < c.nv) {
-      const bf16* p = ybase + chunk_row(a, tl, c, z, v0 + e) * ystride + tl.head * kHD + 8 * cg;
-      r.x[0][e] = load16(p);
-      r.x[1][e] = load16(p + 32);
+      const bf16* p = ybase + chunk_row(a, tl, c, z, v0 + e) * ystride + tl.head * kHD + 8 * cg0;
+#pragma unroll
+      for (int g = 0; g < G; ++g) r.x[g][e] = load16(p + 8 * P * g);
     }
   }
 }
 
-__device__ __forceinline__ void store_stage(const Chunk& c, const StageRows& r, uint16_t* yt) {
-  const int cg = threadIdx.x >> 7, v0 = 2 * (threadIdx.x & 127);
+template <int NT>
+__device__ __forceinline__ void store_stage(const Chunk& c, const StageRows<NT>& r, uint16_t* yt) {
+  constexpr int P = StageRows<NT>::P, G = StageRows<NT>::G;
+  const int cg0 = threadIdx.x >> 7, v0 = 2 * (threadIdx.x & 127);
   if (v0 >= c.nvp) return;
 #pragma unroll
-  for (int g = 0; g < 2; ++g) {
-    const int ch0 = 8 * (cg + 4 * g);
+  for (int g = 0; g < G; ++g) {
+    const int ch0 = 8 * (cg0 + P * g);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const uint32_t even = (r.x[g][0][i] & 0xffffu) | (r.x[g][1][i] << 16);
