@@ -215,16 +215,18 @@ def cpu_baseline(slab_T=2):
                 seconds=dt)
 
 
-KERNEL_KEYS = {  # rocprof kernel-name fragment -> bench phase
-    "dsa3d_bwd_tiled_kernel": "dsa3d_bwd",
-    "dsa3d_fwd_tiled_kernel": "dsa3d_fwd",
+PHASE_KERNELS = {  # bench phase -> the kernels its ABI call launches, in order
+    "dsa3d_fwd": ["dsa3d_fwd_tiled_kernel"],
+    "dsa3d_bwd": ["fill_zero_f32", "dsa3d_bwd_p1_kernel", "dsa3d_bwd_p2_kernel",
+                  "acc_to_bf16_kernel", "acc_to_bf16_kernel"],
 }
 
 
 def summarize(trace_dir, fetch_dir, write_dir):
     """Per-kernel averages from a rocprofv3 --kernel-trace --stats run and the
-    FETCH_SIZE / WRITE_SIZE runs of this script (--copy-calibration); prints a
-    markdown summary and writes profiles/traffic.json."""
+    FETCH_SIZE / WRITE_SIZE runs of this script (--copy-calibration, one step);
+    prints a markdown summary and writes profiles/traffic.json (per bench phase:
+    the summed counters of the kernels of one ABI call, scaled by the copy)."""
     import csv
     import glob
 
@@ -241,22 +243,26 @@ def summarize(trace_dir, fetch_dir, write_dir):
         print(f"| `{r['Name'][:90]}` | {r['Calls']} | {float(r['AverageNs']) / 1e6:.3f} | "
               f"{float(r['Percentage']):.1f}% |")
 
-    def per_kernel(rows, counter):
+    def dispatches(rows, counter):
         acc = {}
         for r in rows:
             if r["Counter_Name"] != counter:
                 continue
-            key = (r["Kernel_Name"], r["Dispatch_Id"])
+            key = (int(r["Dispatch_Id"]), r["Kernel_Name"])
             acc[key] = acc.get(key, 0.0) + float(r["Counter_Value"])
-        out = {}
-        for (name, _), v in acc.items():
-            out.setdefault(name, []).append(v)
-        return {k: sum(v) / len(v) for k, v in out.items()}
+        return sorted((d, name, v) for (d, name), v in acc.items())
 
-    fetch = per_kernel(one(os.path.join(fetch_dir, "*counter_collection.csv")), "FETCH_SIZE")
-    write = per_kernel(one(os.path.join(write_dir, "*counter_collection.csv")), "WRITE_SIZE")
-    copy_f = [v for k, v in fetch.items() if "neg_kernel" in k]
-    copy_w = [v for k, v in write.items() if "neg_kernel" in k]
+    def phase_sum(seq, names):
+        """Counter sum over the first run of consecutive dispatches matching `names`."""
+        for i in range(len(seq) - len(names) + 1):
+            if all(names[j] in seq[i + j][1] for j in range(len(names))):
+                return sum(seq[i + j][2] for j in range(len(names)))
+        return None
+
+    fetch = dispatches(one(os.path.join(fetch_dir, "*counter_collection.csv")), "FETCH_SIZE")
+    write = dispatches(one(os.path.join(write_dir, "*counter_collection.csv")), "WRITE_SIZE")
+    copy_f = [v for _, n, v in fetch if "neg_kernel" in n]
+    copy_w = [v for _, n, v in write if "neg_kernel" in n]
     if not copy_f or not copy_w:
         raise RuntimeError("no calibration copy (neg_kernel) in the counter runs")
     kib = COPY_BYTES / 1024.0
@@ -265,19 +271,23 @@ def summarize(trace_dir, fetch_dir, write_dir):
           f"FETCH_SIZE {copy_f[0]:.0f} KiB (x{sf:.3f}), WRITE_SIZE {copy_w[0]:.0f} KiB (x{sw:.3f})\n")
     ab = algorithmic_bytes(CFG, 2)
     rec = {}
-    print("| kernel | FETCH KiB | WRITE KiB | traffic (scaled) | algorithmic | traffic / algorithmic |")
+    print("| phase (kernels) | FETCH KiB | WRITE KiB | traffic (scaled) | algorithmic | traffic / algorithmic |")
     print("|---|---|---|---|---|---|")
-    for frag, phase in KERNEL_KEYS.items():
-        names = [k for k in fetch if frag in k]
-        if not names or names[0] not in write:
+    for phase, names in PHASE_KERNELS.items():
+        f_kib, w_kib = phase_sum(fetch, names), phase_sum(write, names)
+        if f_kib is None or w_kib is None:
             continue
-        n = names[0]
-        traffic = 1024.0 * (fetch[n] / sf + write[n] / sw)
-        rec[phase] = {"kernel": frag, "bytes_per_launch": int(traffic),
-                      "fetch_kib": round(fetch[n], 1), "write_kib": round(write[n], 1),
+        traffic = 1024.0 * (f_kib / sf + w_kib / sw)
+        rec[phase] = {"kernels": names, "bytes_per_launch": int(traffic),
+                      "fetch_kib": round(f_kib, 1), "write_kib": round(w_kib, 1),
                       "fetch_scale": round(sf, 4), "write_scale": round(sw, 4)}
-        print(f"| `{frag}` | {fetch[n]:.0f} | {write[n]:.0f} | {traffic / 1e9:.3f} GB | "
+        print(f"| {phase} ({', '.join(names)}) | {f_kib:.0f} | {w_kib:.0f} | {traffic / 1e9:.3f} GB | "
               f"{ab[phase] / 1e9:.3f} GB | {traffic / ab[phase]:.2f} |")
+    print("\nPer kernel (counter KiB, unscaled):\n\n| dispatch | kernel | FETCH | WRITE |\n|---|---|---|---|")
+    wmap = {(d, n): v for d, n, v in write}
+    for d, n, v in fetch:
+        if "msd::" in n:
+            print(f"| {d} | `{n[:70]}` | {v:.0f} | {wmap.get((d, n), float('nan')):.0f} |")
     with open(os.path.join(ROOT, "profiles", "traffic.json"), "w") as f:
         json.dump(rec, f, indent=1)
 
