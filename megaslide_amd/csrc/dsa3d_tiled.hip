@@ -1,5 +1,5 @@
 // Matrix-core (tiled) 3D-DSA forward and backward for gfx950: bf16 storage,
-// fp32 accumulation, head_dim 64.
+// fp32 accumulation, head_dim 64, 96 or 128.
 //
 // One workgroup = one (batch, head, tile of 16 queries).  Instead of gathering
 // the 8 corner rows of K and V for each of a query's taps, it builds dense
@@ -21,10 +21,19 @@ namespace {
 
 using namespace tiled;
 
-__global__ __launch_bounds__(kThreads, 4) void dsa3d_fwd_tiled_kernel(Args a, bf16* __restrict__ out,
-                                                                   float* __restrict__ lse) {
-  __shared__ __attribute__((aligned(16))) float s_tab[kTQ * kSRow];     // S, then A
-  __shared__ __attribute__((aligned(16))) uint16_t s_vt[kHD * kVRow];  // V^T chunk
+// Minimum waves per SIMD of the forward kernel: two 512-thread workgroups per
+// CU fit in the LDS up to head_dim 96; head_dim 128 stages 66 KB of V^T, so
+// one workgroup per CU, and the register cap is raised to match.
+template <int HD>
+constexpr int fwd_min_waves() {
+  return HD <= 96 ? 4 : 2;
+}
+
+template <int HD>
+__global__ __launch_bounds__(kThreads, fwd_min_waves<HD>()) void dsa3d_fwd_tiled_kernel(
+    Args a, bf16* __restrict__ out, float* __restrict__ lse) {
+  __shared__ __attribute__((aligned(16))) float s_tab[kTQ * kSRow];    // S, then A
+  __shared__ __attribute__((aligned(16))) uint16_t s_vt[HD * kVRow];  // V^T chunk
   __shared__ int s_red[kWaves][6];
 
   const Tile tl = make_tile<1, kSubs>(a);
@@ -34,8 +43,8 @@ __global__ __launch_bounds__(kThreads, 4) void dsa3d_fwd_tiled_kernel(Args a, bf
   const int nchunks = box.ncy * box.ncx;
   const int nit = (box.zhi - box.zlo + 1) * nchunks;
 
-  bf16x8_t q0, q1;
-  load_rows_operand(a, tl, a.q, a.qs, q0, q1);
+  bf16x8_t qx[HD / 32];
+  load_rows_operand<HD>(a, tl, a.q, a.qs, qx);
   const float* my_row = &s_tab[tl.q * kSRow];
 
   // ---- pass 1: scores -------------------------------------------------------
@@ -43,16 +52,17 @@ __global__ __launch_bounds__(kThreads, 4) void dsa3d_fwd_tiled_kernel(Args a, bf
   float sc[kSlots];
 #pragma unroll
   for (int i = 0; i < kSlots; ++i) sc[i] = 0.0f;
-  TableRows rows;
-  if (nit > 0) load_table_rows(a, tl, make_chunk(box, 0), box.zlo, a.k, a.ks, rows);
+  TableRows<HD> rows;
+  if (nit > 0) load_table_rows<HD>(a, tl, make_chunk(box, 0), box.zlo, a.k, a.ks, rows);
   for (int it = 0; it < nit; ++it) {
     const int zi = it / nchunks;
     const int z = box.zlo + zi;
     const Chunk c = make_chunk(box, it - zi * nchunks);
-    store_table(tl, c, q0, q1, rows, s_tab);
+    store_table<HD>(tl, c, qx, rows, s_tab);
     if (it + 1 < nit) {
       const int zn = (it + 1) / nchunks;
-      load_table_rows(a, tl, make_chunk(box, it + 1 - zn * nchunks), box.zlo + zn, a.k, a.ks, rows);
+      load_table_rows<HD>(a, tl, make_chunk(box, it + 1 - zn * nchunks), box.zlo + zn, a.k, a.ks,
+                          rows);
     }
     __syncthreads();
     // every slot reads its corners (in-bounds for any slot); misses are discarded
@@ -92,23 +102,28 @@ __global__ __launch_bounds__(kThreads, 4) void dsa3d_fwd_tiled_kernel(Args a, bf
   if (lse != nullptr && tl.q_ok && tl.sub == 0) lse[tl.qn * a.nh + tl.head] = mx + logf(den);
 
   // ---- pass 2: O = A . V ------------------------------------------------------
-  // wave w: output channels 16*(w & 3) + [0, 16), voxel k-steps of parity w >> 2
+  // wave w: output channels 16*(w % CT) + [0, 16), voxel k-steps of phase
+  // w / CT out of NH (waves with w >= CT * NH have no A . V work)
+  constexpr int CT = HD / 16;
+  constexpr int NH = (kWaves % CT == 0) ? kWaves / CT : 1;
   const int mq = tl.lane & 15, kq = 8 * (tl.lane >> 4);
-  const int ct = tl.wave & 3, half = tl.wave >> 2;
+  const int ct = tl.wave % CT, half = tl.wave / CT;
   f32x4_t oacc = {0.0f, 0.0f, 0.0f, 0.0f};
   int* const s_atab = reinterpret_cast<int*>(s_tab);  // A in fixed point (scale 2^30)
   int* row = &s_atab[tl.q * kSRow];
-  StageRows<kThreads> vr;
-  if (nit > 0) load_stage_rows(a, tl, make_chunk(box, 0), box.zlo, a.v, a.vs, vr);
+  StageRows<kThreads, HD> vr;
+  if (nit > 0)
+    load_stage_rows<kThreads, HD>(a, tl, make_chunk(box, 0), box.zlo, a.v, a.vs, tl.head * HD, vr);
   for (int it = 0; it < nit; ++it) {
     const int zi = it / nchunks;
     const int z = box.zlo + zi;
     const Chunk c = make_chunk(box, it - zi * nchunks);
     zero_table(s_tab, c.nvp);
-    store_stage(c, vr, s_vt);
+    store_stage<kThreads, HD>(c, vr, s_vt);
     if (it + 1 < nit) {
       const int zn = (it + 1) / nchunks;
-      load_stage_rows(a, tl, make_chunk(box, it + 1 - zn * nchunks), box.zlo + zn, a.v, a.vs, vr);
+      load_stage_rows<kThreads, HD>(a, tl, make_chunk(box, it + 1 - zn * nchunks), box.zlo + zn,
+                                    a.v, a.vs, tl.head * HD, vr);
     }
     __syncthreads();
 #pragma unroll
@@ -124,30 +139,35 @@ __global__ __launch_bounds__(kThreads, 4) void dsa3d_fwd_tiled_kernel(Args a, bf
       if (dx && dy) atomicAdd(&row[base + dy + 1], to_fix(pz * (sl[i].fy * sl[i].fx)));
     }
     __syncthreads();
-    for (int kc = 32 * half; kc < c.nvp; kc += 64) {
-      const bf16x8_t av = fix_to_bf16x8(&s_atab[mq * kSRow + kc + kq], kFixAInv);
-      bf16x8_t bv;
-      __builtin_memcpy(&bv, &s_vt[(16 * ct + mq) * kVRow + kc + kq], sizeof(bv));
-      oacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv, oacc, 0, 0, 0);
+    if (half < NH) {
+      for (int kc = 32 * half; kc < c.nvp; kc += 32 * NH) {
+        const bf16x8_t av = fix_to_bf16x8(&s_atab[mq * kSRow + kc + kq], kFixAInv);
+        bf16x8_t bv;
+        __builtin_memcpy(&bv, &s_vt[(16 * ct + mq) * kVRow + kc + kq], sizeof(bv));
+        oacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv, oacc, 0, 0, 0);
+      }
     }
     __syncthreads();
   }
-  // oacc[r] = partial O[query 4*(lane/16) + r][channel 16*ct + lane%16]; the two
-  // halves of the k-steps are summed through LDS
-  float* red = s_tab;  // 16 x 64
-  if (half == 1) {
+  // oacc[r] = partial O[query 4*(lane/16) + r][channel 16*ct + lane%16]; with
+  // two phases the second's partial sums are added through LDS
+  float* red = s_tab;  // 16 x HD
+  if constexpr (NH == 2) {
+    if (half == 1) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) red[(4 * (tl.lane >> 4) + r) * kHD + 16 * ct + mq] = oacc[r];
+      for (int r = 0; r < 4; ++r) red[(4 * (tl.lane >> 4) + r) * HD + 16 * ct + mq] = oacc[r];
+    }
+    __syncthreads();
   }
-  __syncthreads();
   if (half == 0) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int m = 4 * (tl.lane >> 4) + r;
       const int64_t n = tile_row(a, tl, m);
+      float o = oacc[r];
+      if constexpr (NH == 2) o += red[m * HD + 16 * ct + mq];
       if (n >= 0)
-        out[n * (static_cast<int64_t>(a.nh) * kHD) + tl.head * kHD + 16 * ct + mq] =
-            from_f32<bf16>(oacc[r] + red[m * kHD + 16 * ct + mq]);
+        out[n * (static_cast<int64_t>(a.nh) * HD) + tl.head * HD + 16 * ct + mq] = from_f32<bf16>(o);
     }
   }
 }
@@ -173,6 +193,7 @@ __device__ __forceinline__ bf16x8_t table_t_rows(const int* table_t, int row, in
 // rebuilds S and dP = dO V^T per plane, accumulates per tap s, dp and their
 // coordinate derivatives, then writes the offset gradients and, for the second
 // kernel, p and ds * softmax_scale of every tap (fp32, [token][head][tap]).
+template <int HD>
 __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p1_kernel(
     Args a, const bf16* __restrict__ out, const bf16* __restrict__ dout,
     const float* __restrict__ lse, const float* __restrict__ dlse, bf16* __restrict__ doff,
@@ -182,22 +203,24 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p1_kernel(
   __shared__ int s_red[kWaves][6];
 
   const Tile tl = make_tile<1, kSubs>(a);
-  const int D = a.nh * kHD;
+  const int D = a.nh * HD;
   Slot sl[kSlots];
   Box box;
   setup_slots<kSubs, kSlots>(a, tl, sl, box, s_red);
   const int nchunks = box.ncy * box.ncx;
   const int nit = (box.zhi - box.zlo + 1) * nchunks;
 
-  bf16x8_t q0, q1, g0, g1;
-  load_rows_operand(a, tl, a.q, a.qs, q0, q1);
-  load_rows_operand(a, tl, dout, D, g0, g1);
+  bf16x8_t qx[HD / 32], gx[HD / 32];
+  load_rows_operand<HD>(a, tl, a.q, a.qs, qx);
+  load_rows_operand<HD>(a, tl, dout, D, gx);
 
-  // Delta = dO . O (- dlse) and lse for this lane's query: 32 lanes x 2 channels
+  // Delta = dO . O (- dlse) and lse for this lane's query: 32 lanes x HD/32 channels
+  constexpr int CPL = HD / kSubs;
   float delta = 0.0f, lse_q = 0.0f;
   if (tl.q_ok) {
-    const int64_t base = tl.qn * D + tl.head * kHD + 2 * tl.sub;
-    delta = to_f32(dout[base]) * to_f32(out[base]) + to_f32(dout[base + 1]) * to_f32(out[base + 1]);
+    const int64_t base = tl.qn * D + tl.head * HD + CPL * tl.sub;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) delta += to_f32(dout[base + j]) * to_f32(out[base + j]);
     lse_q = lse[tl.qn * a.nh + tl.head];
   }
 #pragma unroll
@@ -212,11 +235,11 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p1_kernel(
   for (int i = 0; i < kSlots; ++i)
     s_[i] = dp_[i] = gxs[i] = gxd[i] = gys[i] = gyd[i] = gzs[i] = gzd[i] = 0.0f;
   // K and V rows of the next (plane, chunk) are loaded while the current one is used
-  TableRows rk, rv;
+  TableRows<HD> rk, rv;
   if (nit > 0) {
     const Chunk c0 = make_chunk(box, 0);
-    load_table_rows(a, tl, c0, box.zlo, a.k, a.ks, rk);
-    load_table_rows(a, tl, c0, box.zlo, a.v, a.vs, rv);
+    load_table_rows<HD>(a, tl, c0, box.zlo, a.k, a.ks, rk);
+    load_table_rows<HD>(a, tl, c0, box.zlo, a.v, a.vs, rv);
   }
   const float* r0 = &s_t0[tl.q * kSRow];
   const float* r1 = &s_t1[tl.q * kSRow];
@@ -224,13 +247,13 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p1_kernel(
     const int zi = it / nchunks;
     const int z = box.zlo + zi;
     const Chunk c = make_chunk(box, it - zi * nchunks);
-    store_table(tl, c, q0, q1, rk, s_t0);
-    store_table(tl, c, g0, g1, rv, s_t1);
+    store_table<HD>(tl, c, qx, rk, s_t0);
+    store_table<HD>(tl, c, gx, rv, s_t1);
     if (it + 1 < nit) {
       const int zn = (it + 1) / nchunks;
       const Chunk cn = make_chunk(box, it + 1 - zn * nchunks);
-      load_table_rows(a, tl, cn, box.zlo + zn, a.k, a.ks, rk);
-      load_table_rows(a, tl, cn, box.zlo + zn, a.v, a.vs, rv);
+      load_table_rows<HD>(a, tl, cn, box.zlo + zn, a.k, a.ks, rk);
+      load_table_rows<HD>(a, tl, cn, box.zlo + zn, a.v, a.vs, rv);
     }
     __syncthreads();
     // every slot reads its corners (in-bounds for any slot); misses are discarded
@@ -283,11 +306,14 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p1_kernel(
 }
 
 // Second backward kernel: dq, dK and dV for tiles of kP2Frames consecutive
-// frames (kP2Q queries) of one 4x4 (h, w) column.  Consecutive frames reach
-// nearly the same planes, so one flush of the [voxel][query] tables per plane
-// serves all of them: the fp32 dK/dV atomics (executed past the L2, the
-// backward's dominant cost) drop accordingly.  Tap geometry is recomputed from
-// the offsets; p and ds * scale come from the first kernel.
+// frames (kP2Q queries) of one 4x4 (h, w) column, over a window of CW of the
+// head's HD channels (window blockIdx.z).  Consecutive frames reach nearly the
+// same planes, so one flush of the [voxel][query] tables per plane serves all
+// of them: the fp32 dK/dV atomics (executed past the L2, the backward's
+// dominant cost) drop accordingly.  Tap geometry is recomputed from the
+// offsets; p and ds * scale come from the first kernel.  The A and B tables
+// do not depend on the channel, so a window narrower than the head rebuilds
+// them per window in exchange for fewer registers and less LDS.
 constexpr int kP2Frames = 2;
 constexpr int kP2Q = kTQ * kP2Frames;          // queries per tile
 constexpr int kP2Subs = kThreads / kP2Q;       // lanes per query
@@ -296,21 +322,24 @@ constexpr int kP2Row = kP2Q + 2;               // [voxel][query] table row (ints
 constexpr int kP2QRow = kP2Q + 8;              // [channel][query] row of staged q / dO (bf16)
 static_assert(kP2Subs * kP2Slots == kMaxTaps, "the tap capacity must match the first kernel");
 
+template <int HD, int CW>
 __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
     Args a, const bf16* __restrict__ dout, const float* __restrict__ p_ws,
     const float* __restrict__ b_ws, bf16* __restrict__ dq, float* __restrict__ dk_acc,
     float* __restrict__ dv_acc) {
+  static_assert(HD % CW == 0 && CW % 32 == 0, "channel windows are whole 32-channel blocks");
   __shared__ __attribute__((aligned(16))) int s_at[kChunkNV * kP2Row];  // A^T = p w (fixed point)
   __shared__ __attribute__((aligned(16))) int s_bt[kChunkNV * kP2Row];  // B^T = ds scale w (fixed point)
-  __shared__ __attribute__((aligned(16))) uint16_t s_kt[kHD * kVRow];   // K^T chunk
+  __shared__ __attribute__((aligned(16))) uint16_t s_kt[CW * kVRow];    // K^T chunk
   __shared__ __attribute__((aligned(16))) int s_rows[kChunkNV];         // token row (within the sample) per voxel
   __shared__ int s_red[kWaves][6];
   __shared__ __attribute__((aligned(16))) float s_binv[kP2Q];  // per query: 1 / fixed-point scale of B
-  // the tile's q and dO rows of this head, transposed: [tensor][channel][query]
-  __shared__ __attribute__((aligned(16))) uint16_t s_qt[2][kHD][kP2QRow];
+  // the tile's q and dO rows of this window, transposed: [tensor][channel][query]
+  __shared__ __attribute__((aligned(16))) uint16_t s_qt[2][CW][kP2QRow];
 
   const Tile tl = make_tile<kP2Frames, kP2Subs>(a);
-  const int D = a.nh * kHD;
+  const int D = a.nh * HD;
+  const int cw0 = tl.head * HD + CW * static_cast<int>(blockIdx.z);  // first channel of the window
   Slot sl[kP2Slots];
   Box box;
   setup_slots<kP2Subs, kP2Slots>(a, tl, sl, box, s_red);
@@ -336,14 +365,14 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
   const bool l1_ok = l1 > 1e-30f;
   const float bscale = l1_ok ? kFixA / l1 : 0.0f;
   if (tl.sub == 0) s_binv[tl.q] = l1_ok ? l1 * kFixAInv : 0.0f;
-  // stage q and dO of the tile transposed: thread i moves 8 channels of one row
-  {
-    const int tensor = threadIdx.x >> 8, m = (threadIdx.x >> 3) & (kP2Q - 1), cg = threadIdx.x & 7;
+  // stage q and dO of the tile transposed: item e moves 8 channels of one row
+  for (int e = threadIdx.x; e < 2 * kP2Q * (CW / 8); e += kThreads) {
+    const int cg = e % (CW / 8), m = (e / (CW / 8)) % kP2Q, tensor = e / (kP2Q * (CW / 8));
     const int64_t n = tile_row(a, tl, m);
     u32x4_t x = {0u, 0u, 0u, 0u};
     if (n >= 0) {
       const bf16* src = tensor == 0 ? a.q + n * a.qs : dout + n * D;
-      x = load16(src + tl.head * kHD + 8 * cg);
+      x = load16(src + cw0 + 8 * cg);
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -353,24 +382,24 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
   }
   __syncthreads();
 
-  // dq (16x16x32 MFMA): wave w owns frame w >> 2 of the tile, channels
-  // 16*(w & 3) + [0, 16).  dK/dV (32x32x16 MFMA, one per frame): wave w owns
-  // channels 32*(w & 1) + [0, 32) and the 32-voxel blocks (w >> 1) + 4 i.
+  // dq (16x16x32 MFMA): task t = (frame t / CT, channels 16*(t % CT) + [0, 16))
+  // for t = w + 8 j.  dK/dV (32x32x16 MFMA, one per frame): task t = (channels
+  // 32*(t % NC2) + [0, 32), 32-voxel block t / NC2) for t = w + 8 i.
+  constexpr int CT = CW / 16, NC2 = CW / 32;
+  constexpr int NDQ = (kP2Frames * CT + kWaves - 1) / kWaves;  // dq tasks per wave
   const int mq = tl.lane & 15, kq = 8 * (tl.lane >> 4);
-  const int fq = tl.wave >> 2, ct = tl.wave & 3;
-  const int c2 = tl.wave & 1, vq = tl.wave >> 1;
   // operands of the dK/dV MFMAs are re-read from LDS where used (registers are
   // the limit here: a spill reload would wait for every outstanding atomic)
-  const int och = 32 * c2 + (tl.lane & 31), oq = 8 * (tl.lane >> 5);
+  const int oq = 8 * (tl.lane >> 5);
   float ainv_k[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) ainv_k[j] = kFixAInv;
-  const float binv_m = s_binv[kTQ * fq + mq];
-  const int ch = tl.head * kHD + 16 * ct + mq;
-  const int ch2 = tl.head * kHD + 32 * c2 + (tl.lane & 31);
-  f32x4_t dq_acc = {0.0f, 0.0f, 0.0f, 0.0f};
-  StageRows<kThreads> kr;
-  if (nit > 0) load_stage_rows(a, tl, make_chunk(box, 0), box.zlo, a.k, a.ks, kr);
+  f32x4_t dq_acc[NDQ];
+#pragma unroll
+  for (int j = 0; j < NDQ; ++j) dq_acc[j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  StageRows<kThreads, CW> kr;
+  if (nit > 0)
+    load_stage_rows<kThreads, CW>(a, tl, make_chunk(box, 0), box.zlo, a.k, a.ks, cw0, kr);
   for (int it = 0; it < nit; ++it) {
     const int zi = it / nchunks;
     const int z = box.zlo + zi;
@@ -383,10 +412,11 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
     }
     for (int vi = threadIdx.x; vi < c.nv; vi += kThreads)
       s_rows[vi] = static_cast<int>(chunk_row(a, tl, c, z, vi) - tl.sample0);
-    store_stage(c, kr, s_kt);
+    store_stage<kThreads, CW>(c, kr, s_kt);
     if (it + 1 < nit) {
       const int zn = (it + 1) / nchunks;
-      load_stage_rows(a, tl, make_chunk(box, it + 1 - zn * nchunks), box.zlo + zn, a.k, a.ks, kr);
+      load_stage_rows<kThreads, CW>(a, tl, make_chunk(box, it + 1 - zn * nchunks), box.zlo + zn,
+                                    a.k, a.ks, cw0, kr);
     }
     __syncthreads();
 #pragma unroll
@@ -421,20 +451,30 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
     __syncthreads();
     // dq[q] += sum_v B[q][v] K[v]; B as a bf16 hi/lo pair because
     // sum_v B[q][v] = 0 and K may carry a large common part
-    for (int kc = 0; kc < c.nvp; kc += 32) {
-      float bq[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
-        bq[j] = static_cast<float>(s_bt[(kc + kq + j) * kP2Row + kTQ * fq + mq]) * binv_m;
-      bf16x8_t bhi, blo, kv;
-      to_bf16x8_hilo(bq, bhi, blo);
-      __builtin_memcpy(&kv, &s_kt[(16 * ct + mq) * kVRow + kc + kq], sizeof(kv));
-      dq_acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bhi, kv, dq_acc, 0, 0, 0);
-      dq_acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(blo, kv, dq_acc, 0, 0, 0);
+    for (int j = 0; j < NDQ; ++j) {
+      const int t = tl.wave + kWaves * j;
+      if (t >= kP2Frames * CT) continue;
+      const int fq = t / CT, ct = t % CT;
+      const float binv_m = s_binv[kTQ * fq + mq];
+      for (int kc = 0; kc < c.nvp; kc += 32) {
+        float bq[8];
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj)
+          bq[jj] = static_cast<float>(s_bt[(kc + kq + jj) * kP2Row + kTQ * fq + mq]) * binv_m;
+        bf16x8_t bhi, blo, kv;
+        to_bf16x8_hilo(bq, bhi, blo);
+        __builtin_memcpy(&kv, &s_kt[(16 * ct + mq) * kVRow + kc + kq], sizeof(kv));
+        dq_acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bhi, kv, dq_acc[j], 0, 0, 0);
+        dq_acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(blo, kv, dq_acc[j], 0, 0, 0);
+      }
     }
     // dK[v] += sum_q B[q][v] q[q];  dV[v] += sum_q A[q][v] dO[q]  (fp32 atomics;
     // one register across the wave covers 2 voxels x 32 contiguous channels)
-    for (int vb = vq; vb * 32 < c.nv; vb += 4) {
+    for (int t = tl.wave;; t += kWaves) {
+      const int c2 = t % NC2, vb = t / NC2;
+      if (vb * 32 >= c.nv) break;
+      const int och = 32 * c2 + (tl.lane & 31);
       f32x16_t dk = {}, dv = {};
 #pragma unroll
       for (int f = 0; f < kP2Frames; ++f) {
@@ -448,6 +488,7 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
         dv = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
             table_t_rows(s_at, kP2Row, kTQ * f, vb, tl.lane, ainv_k), gTf, dv, 0, 0, 0);
       }
+      const int ch2 = cw0 + och;
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         // registers 4g + i: voxel 32*vb + 8*g + 4*(lane/32) + i
@@ -465,11 +506,17 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
     }
     __syncthreads();
   }
-  // dq_acc[r] = dq[query 16*fq + 4*(lane/16) + r][channel 16*ct + lane%16]
+  // dq_acc[j][r] = dq[query 16*fq + 4*(lane/16) + r][channel 16*ct + lane%16]
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int64_t n = tile_row(a, tl, kTQ * fq + 4 * (tl.lane >> 4) + r);
-    if (n >= 0) dq[n * a.qs + ch] = from_f32<bf16>(dq_acc[r]);
+  for (int j = 0; j < NDQ; ++j) {
+    const int t = tl.wave + kWaves * j;
+    if (t >= kP2Frames * CT) continue;
+    const int fq = t / CT, ct = t % CT;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t n = tile_row(a, tl, kTQ * fq + 4 * (tl.lane >> 4) + r);
+      if (n >= 0) dq[n * a.qs + cw0 + 16 * ct + mq] = from_f32<bf16>(dq_acc[j][r]);
+    }
   }
 }
 
@@ -529,8 +576,13 @@ dim3 tiled_grid(const msd_dsa3d_desc& d) {
   return dim3(static_cast<unsigned>(tiled_tiles<FRAMES>(d)), d.num_heads);
 }
 
+namespace {
+// head sizes with compiled tiled kernels
+bool tiled_head_dim(int hd) { return hd == 64 || hd == 96 || hd == 128; }
+}  // namespace
+
 bool dsa3d_tiled_supported(const msd_dsa3d_desc& d, const void* q, const void* k, const void* v) {
-  if (d.dtype != MSD_BF16 || d.head_dim != tiled::kHD) return false;
+  if (d.dtype != MSD_BF16 || !tiled_head_dim(d.head_dim)) return false;
   if (d.kt * d.kh * d.kw > tiled::kMaxTaps) return false;
   if (d.T > 32767 || d.H > 32767 || d.W > 32767) return false;
   // the chunk grid of any corner box must number fewer than kMaxChunks
@@ -550,8 +602,14 @@ hipError_t launch_dsa3d_fwd_tiled(const msd_dsa3d_desc& d, const void* q, const 
                                   const void* v, const void* off, void* out, float* lse,
                                   hipStream_t s) {
   const tiled::Args a = make_tiled_args(d, q, k, v, off, tiled_tiles<1>(d));
-  hipLaunchKernelGGL(dsa3d_fwd_tiled_kernel, tiled_grid<1>(d), dim3(tiled::kThreads), 0, s, a,
-                     static_cast<bf16*>(out), lse);
+  const dim3 grid = tiled_grid<1>(d), block(tiled::kThreads);
+  bf16* o = static_cast<bf16*>(out);
+  switch (d.head_dim) {
+    case 64: hipLaunchKernelGGL(dsa3d_fwd_tiled_kernel<64>, grid, block, 0, s, a, o, lse); break;
+    case 96: hipLaunchKernelGGL(dsa3d_fwd_tiled_kernel<96>, grid, block, 0, s, a, o, lse); break;
+    case 128: hipLaunchKernelGGL(dsa3d_fwd_tiled_kernel<128>, grid, block, 0, s, a, o, lse); break;
+    default: return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 
@@ -571,7 +629,7 @@ __global__ __launch_bounds__(256) void acc_to_bf16_kernel(const float* __restric
 // Workspace of the tiled backward beyond the dK/dV accumulators: p and
 // ds * softmax_scale of every tap (fp32 [token][head][tap] each).
 size_t dsa3d_tiled_bwd_extra_bytes(const msd_dsa3d_desc& d) {
-  if (d.dtype != MSD_BF16 || d.head_dim != tiled::kHD || d.kt * d.kh * d.kw > tiled::kMaxTaps)
+  if (d.dtype != MSD_BF16 || !tiled_head_dim(d.head_dim) || d.kt * d.kh * d.kw > tiled::kMaxTaps)
     return 0;
   const int64_t rows = static_cast<int64_t>(d.B) * d.T * d.H * d.W;
   return static_cast<size_t>(2 * rows * d.num_heads * d.kt * d.kh * d.kw) * sizeof(float);
@@ -591,13 +649,38 @@ hipError_t launch_dsa3d_bwd_tiled(const msd_dsa3d_desc& d, const void* q, const 
   hipLaunchKernelGGL(fill_zero_f32, dim3(fill_blocks(2 * rows * D)), dim3(256), 0, s, dk_acc,
                      2 * rows * D);
   const tiled::Args a1 = make_tiled_args(d, q, k, v, off, tiled_tiles<1>(d));
-  hipLaunchKernelGGL(dsa3d_bwd_p1_kernel, tiled_grid<1>(d), dim3(tiled::kThreads), 0, s, a1,
-                     static_cast<const bf16*>(out), static_cast<const bf16*>(dout), lse, dlse,
-                     static_cast<bf16*>(doff), p_ws, b_ws);
   const tiled::Args a2 = make_tiled_args(d, q, k, v, off, tiled_tiles<kP2Frames>(d));
-  hipLaunchKernelGGL(dsa3d_bwd_p2_kernel, tiled_grid<kP2Frames>(d), dim3(tiled::kThreads), 0, s,
-                     a2, static_cast<const bf16*>(dout), p_ws, b_ws, static_cast<bf16*>(dq), dk_acc,
-                     dv_acc);
+  const dim3 block(tiled::kThreads), g1 = tiled_grid<1>(d);
+  const auto* o = static_cast<const bf16*>(out);
+  const auto* go = static_cast<const bf16*>(dout);
+  auto* gq = static_cast<bf16*>(dq);
+  auto* goff = static_cast<bf16*>(doff);
+  // the second kernel's channel window: the whole head up to 96 channels, two
+  // windows of 64 for head_dim 128 (registers and LDS of the 64-channel kernel)
+  dim3 g2 = tiled_grid<kP2Frames>(d);
+  switch (d.head_dim) {
+    case 64:
+      hipLaunchKernelGGL(dsa3d_bwd_p1_kernel<64>, g1, block, 0, s, a1, o, go, lse, dlse, goff,
+                         p_ws, b_ws);
+      hipLaunchKernelGGL((dsa3d_bwd_p2_kernel<64, 64>), g2, block, 0, s, a2, go, p_ws, b_ws, gq,
+                         dk_acc, dv_acc);
+      break;
+    case 96:
+      hipLaunchKernelGGL(dsa3d_bwd_p1_kernel<96>, g1, block, 0, s, a1, o, go, lse, dlse, goff,
+                         p_ws, b_ws);
+      hipLaunchKernelGGL((dsa3d_bwd_p2_kernel<96, 96>), g2, block, 0, s, a2, go, p_ws, b_ws, gq,
+                         dk_acc, dv_acc);
+      break;
+    case 128:
+      hipLaunchKernelGGL(dsa3d_bwd_p1_kernel<128>, g1, block, 0, s, a1, o, go, lse, dlse, goff,
+                         p_ws, b_ws);
+      g2.z = 2;
+      hipLaunchKernelGGL((dsa3d_bwd_p2_kernel<128, 64>), g2, block, 0, s, a2, go, p_ws, b_ws, gq,
+                         dk_acc, dv_acc);
+      break;
+    default:
+      return hipErrorInvalidValue;
+  }
   const dim3 cgrid(static_cast<unsigned>((rows * D + 255) / 256));
   hipLaunchKernelGGL(acc_to_bf16_kernel, cgrid, dim3(256), 0, s, dk_acc, static_cast<bf16*>(dk),
                      rows, D, d.k_stride);

@@ -27,7 +27,6 @@ typedef __attribute__((ext_vector_type(16))) float f32x16_t;
 typedef __attribute__((ext_vector_type(2))) float f32x2_t;
 typedef __attribute__((ext_vector_type(4))) unsigned int u32x4_t;
 
-constexpr int kHD = 64;                 // head_dim served by the tiled kernels
 constexpr int kTileH = 4, kTileW = 4;
 constexpr int kTQ = kTileH * kTileW;    // queries per tile
 constexpr int kWaves = 8;
@@ -299,75 +298,84 @@ __device__ __forceinline__ u32x4_t load16(const bf16* p) {
   return r;
 }
 
-// Rows of the tile (queries m = lane % 16) as MFMA A operands, channels
-// 8*(lane/16) + [0, 8) and 32 + 8*(lane/16) + [0, 8).
+// Rows of the tile (queries m = lane % 16) as MFMA A operands: x[c] holds
+// channels 32*c + 8*(lane/16) + [0, 8), c < HD/32.
+template <int HD>
 __device__ __forceinline__ void load_rows_operand(const Args& a, const Tile& tl, const bf16* base,
-                                                  int64_t stride, bf16x8_t& lo, bf16x8_t& hi) {
-  lo = hi = zero_bf16x8();
+                                                  int64_t stride, bf16x8_t (&x)[HD / 32]) {
+#pragma unroll
+  for (int c = 0; c < HD / 32; ++c) x[c] = zero_bf16x8();
   const int64_t row = tile_row(a, tl, tl.lane & 15);
   if (row < 0) return;
-  const bf16* p = base + row * stride + tl.head * kHD + 8 * (tl.lane >> 4);
-  lo = __builtin_bit_cast(bf16x8_t, load16(p));
-  hi = __builtin_bit_cast(bf16x8_t, load16(p + 32));
+  const bf16* p = base + row * stride + tl.head * HD + 8 * (tl.lane >> 4);
+#pragma unroll
+  for (int c = 0; c < HD / 32; ++c) x[c] = __builtin_bit_cast(bf16x8_t, load16(p + 32 * c));
 }
 
 // Y rows of a chunk as MFMA B operands, for the two 16-voxel blocks of this
 // wave (blocks w and w + 8; a chunk has at most 16 blocks).  All loads are
 // issued before any is used.
+template <int HD>
 struct TableRows {
-  u32x4_t y[2][2];  // [block][channels kq / kq + 32]
+  u32x4_t y[2][HD / 32];  // [block][channels 32*c + kq]
 };
 
+template <int HD>
 __device__ __forceinline__ void load_table_rows(const Args& a, const Tile& tl, const Chunk& c,
                                                 int z, const bf16* ybase, int64_t ystride,
-                                                TableRows& r) {
+                                                TableRows<HD>& r) {
   const int kq = 8 * (tl.lane >> 4);
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int vi = (tl.wave + kWaves * j) * 16 + (tl.lane & 15);
     const u32x4_t z4 = {0u, 0u, 0u, 0u};
-    r.y[j][0] = r.y[j][1] = z4;
+#pragma unroll
+    for (int cc = 0; cc < HD / 32; ++cc) r.y[j][cc] = z4;
     if (vi < c.nv) {
-      const bf16* p = ybase + chunk_row(a, tl, c, z, vi) * ystride + tl.head * kHD + kq;
-      r.y[j][0] = load16(p);
-      r.y[j][1] = load16(p + 32);
+      const bf16* p = ybase + chunk_row(a, tl, c, z, vi) * ystride + tl.head * HD + kq;
+#pragma unroll
+      for (int cc = 0; cc < HD / 32; ++cc) r.y[j][cc] = load16(p + 32 * cc);
     }
   }
 }
 
 // table[m][vi] = X[m] . Y[vi] for the wave's blocks of the chunk.
-__device__ __forceinline__ void store_table(const Tile& tl, const Chunk& c, bf16x8_t x0,
-                                            bf16x8_t x1, const TableRows& r, float* table) {
+template <int HD>
+__device__ __forceinline__ void store_table(const Tile& tl, const Chunk& c,
+                                            const bf16x8_t (&x)[HD / 32], const TableRows<HD>& r,
+                                            float* table) {
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int blk = tl.wave + kWaves * j;
     if (blk * 16 >= c.nv) continue;
     f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x0, __builtin_bit_cast(bf16x8_t, r.y[j][0]), acc,
-                                                  0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x1, __builtin_bit_cast(bf16x8_t, r.y[j][1]), acc,
-                                                  0, 0, 0);
+#pragma unroll
+    for (int cc = 0; cc < HD / 32; ++cc)
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x[cc], __builtin_bit_cast(bf16x8_t, r.y[j][cc]),
+                                                    acc, 0, 0, 0);
     const int vi = blk * 16 + (tl.lane & 15);
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) table[(4 * (tl.lane >> 4) + rr) * kSRow + vi] = acc[rr];
   }
 }
 
-// Chunk rows of Y (plane z) transposed into LDS: yt[channel][voxel] (bf16),
-// zero padded up to nvp voxels, by the first NT threads of the workgroup.
-// Thread t moves voxels 2*(t % 128) + {0, 1}, channel groups t / 128 + P*g
-// (P = NT / 128, g < 8 / P; 8 channels each); its loads are issued first.
-template <int NT>
+// Chunk rows of Y (plane z), channels col0 + [0, CW), transposed into LDS:
+// yt[channel][voxel] (bf16), zero padded up to nvp voxels, by the first NT
+// threads of the workgroup.  Thread t moves voxels 2*(t % 128) + {0, 1},
+// channel groups t / 128 + P*g (P = NT / 128, g < CW / 8 / P; 8 channels
+// each); its loads are issued first.
+template <int NT, int CW>
 struct StageRows {
-  static constexpr int P = NT / 128, G = 8 / P;
+  static constexpr int P = NT / 128, G = CW / 8 / P;
+  static_assert(G * P * 8 == CW, "channel groups must split evenly over the staging threads");
   u32x4_t x[G][2];  // [channel group][voxel]
 };
 
-template <int NT>
+template <int NT, int CW>
 __device__ __forceinline__ void load_stage_rows(const Args& a, const Tile& tl, const Chunk& c,
                                                 int z, const bf16* ybase, int64_t ystride,
-                                                StageRows<NT>& r) {
-  constexpr int P = StageRows<NT>::P, G = StageRows<NT>::G;
+                                                int col0, StageRows<NT, CW>& r) {
+  constexpr int P = StageRows<NT, CW>::P, G = StageRows<NT, CW>::G;
   const int cg0 = threadIdx.x >> 7, v0 = 2 * (threadIdx.x & 127);
   const u32x4_t z4 = {0u, 0u, 0u, 0u};
 #pragma unroll
@@ -375,16 +383,17 @@ __device__ __forceinline__ void load_stage_rows(const Args& a, const Tile& tl, c
 #pragma unroll
   for (int e = 0; e < 2; ++e) {
     if (v0 + e < c.nv) {
-      const bf16* p = ybase + chunk_row(a, tl, c, z, v0 + e) * ystride + tl.head * kHD + 8 * cg0;
+      const bf16* p = ybase + chunk_row(a, tl, c, z, v0 + e) * ystride + col0 + 8 * cg0;
 #pragma unroll
       for (int g = 0; g < G; ++g) r.x[g][e] = load16(p + 8 * P * g);
     }
   }
 }
 
-template <int NT>
-__device__ __forceinline__ void store_stage(const Chunk& c, const StageRows<NT>& r, uint16_t* yt) {
-  constexpr int P = StageRows<NT>::P, G = StageRows<NT>::G;
+template <int NT, int CW>
+__device__ __forceinline__ void store_stage(const Chunk& c, const StageRows<NT, CW>& r,
+                                            uint16_t* yt) {
+  constexpr int P = StageRows<NT, CW>::P, G = StageRows<NT, CW>::G;
   const int cg0 = threadIdx.x >> 7, v0 = 2 * (threadIdx.x & 127);
   if (v0 >= c.nvp) return;
 #pragma unroll

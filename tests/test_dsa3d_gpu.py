@@ -155,6 +155,8 @@ def test_core_vs_oracle_random(shape, dtype, tol):
     # name, dtype, B, T, H, W, nh, hd, off_std
     ("fp32 B2 16x32x32 8x64", torch.float32, 2, 16, 32, 32, 8, 64, 1.5),
     ("bf16 65536 tokens 16x64", torch.bfloat16, 1, 64, 32, 32, 16, 64, 0.5),
+    ("bf16 131072 tokens 24x128", torch.bfloat16, 1, 32, 64, 64, 24, 128, 0.5),
+    ("bf16 46800 tokens 16x96 (13x45x80)", torch.bfloat16, 1, 13, 45, 80, 16, 96, 2.5),
 ])
 def test_core_full_size_sampled_queries_and_checksums(cfg):
     """Full-size shapes: exact per-query parity on sampled queries (fwd, dq,

@@ -1,6 +1,6 @@
 """Matrix-core (tiled) attention-core kernels: parity and invariants (GPU).
 
-The tiled kernels serve bf16, head_dim 64.  They must agree with the fp32
+The tiled kernels serve bf16, head_dim 64, 96 and 128.  They must agree with the fp32
 oracle (tolerance 2e-2, relative to max|ref|) and with the direct kernels; the
 log-sum-exp they return must match the oracle's to 1e-5.
 """
@@ -64,28 +64,36 @@ def test_tiled_constant_values():
 
 
 @pytest.mark.parametrize("shape", [
-    # B, T, H, W, nh, kernel, off_std, scale
-    (1, 3, 7, 9, 2, (3, 7, 7), 0.5, 1.0),
-    (2, 4, 8, 8, 1, (3, 5, 5), 1.5, 0.8),
-    (1, 5, 12, 40, 1, (3, 7, 7), 8.0, 1.0),   # corner boxes span several chunks
-    (1, 1, 4, 4, 2, (3, 3, 3), 1.0, 1.0),     # T = 1
+    # B, T, H, W, nh, kernel, off_std, scale, head_dim
+    (1, 3, 7, 9, 2, (3, 7, 7), 0.5, 1.0, 64),
+    (2, 4, 8, 8, 1, (3, 5, 5), 1.5, 0.8, 64),
+    (1, 5, 12, 40, 1, (3, 7, 7), 8.0, 1.0, 64),   # corner boxes span several chunks
+    (1, 1, 4, 4, 2, (3, 3, 3), 1.0, 1.0, 64),     # T = 1
+    (1, 3, 7, 9, 2, (3, 7, 7), 0.5, 1.0, 96),
+    (1, 4, 13, 18, 1, (3, 7, 7), 4.0, 0.9, 96),   # non-tile-aligned grid, large offsets
+    (1, 3, 8, 8, 2, (3, 7, 7), 0.5, 1.0, 128),
+    (1, 5, 12, 40, 1, (3, 7, 7), 8.0, 1.0, 128),  # corner boxes span several chunks
 ])
 def test_tiled_backward_vs_oracle_and_direct(shape):
-    B, T, H, W, nh, ks, off_std, scale = shape
+    B, T, H, W, nh, ks, off_std, scale, hd = shape
     print(f"[tiled bwd] {shape}", flush=True)
-    q, k, v, off = _inputs(B, T, H, W, nh, ks, off_std, 300 + T * H * W)
+    q, k, v, off = _inputs(B, T, H, W, nh, ks, off_std, 300 + T * H * W + hd, hd=hd)
     g = torch.Generator().manual_seed(17)
     dout = torch.randn(q.shape, generator=g).to(torch.bfloat16)
     qq, kk, vv, oo = (t.float().requires_grad_(True) for t in (q, k, v, off))
     ref = dsa3d_core_ref(qq, kk, vv, oo, (T, H, W), nh, ks, scale)
     ref.backward(dout.float())
-    grads = {}
+    grads, outs = {}, {}
     for algo in ("tiled", "direct"):
         ts = [t.to(DEV).requires_grad_(True) for t in (q, k, v, off)]
         out = core()(*ts, (T, H, W), nh, ks, scale, algo=algo)
         out.backward(dout.to(DEV))
+        outs[algo] = out.detach().float().cpu()
         grads[algo] = [t.grad.float().cpu() for t in ts]
     torch.cuda.synchronize()
+    e_out = rel_err(outs["tiled"], ref.detach())
+    print(f"  out: vs oracle {e_out:.2e}", flush=True)
+    assert e_out < BF16_TOL
     for name, r, gt, gd in zip(("dq", "dk", "dv", "doff"), (qq.grad, kk.grad, vv.grad, oo.grad),
                                grads["tiled"], grads["direct"]):
         e_ref, e_dir = rel_err(gt, r), rel_err(gt, gd)
