@@ -141,7 +141,7 @@ __global__ __launch_bounds__(kThreads, fwd_min_waves<HD>()) void dsa3d_fwd_tiled
     __syncthreads();
     if (half < NH) {
       for (int kc = 32 * half; kc < c.nvp; kc += 32 * NH) {
-        const bf16x8_t av = fix_to_bf16x8(&s_atab[mq * kSRow + kc + kq], kFixAInv);
+        const bf16x8_t av = fix_to_bf16x8(&s_atab[mq * kSRow + kc + kq]);
         bf16x8_t bv;
         __builtin_memcpy(&bv, &s_vt[(16 * ct + mq) * kVRow + kc + kq], sizeof(bv));
         oacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv, oacc, 0, 0, 0);
@@ -149,8 +149,9 @@ __global__ __launch_bounds__(kThreads, fwd_min_waves<HD>()) void dsa3d_fwd_tiled
     }
     __syncthreads();
   }
-  // oacc[r] = partial O[query 4*(lane/16) + r][channel 16*ct + lane%16]; with
-  // two phases the second's partial sums are added through LDS
+  // oacc[r] = partial O[query 4*(lane/16) + r][channel 16*ct + lane%16] in
+  // fixed-point units of A; with two phases the second's partial sums are added
+  // through LDS
   float* red = s_tab;  // 16 x HD
   if constexpr (NH == 2) {
     if (half == 1) {
@@ -167,26 +168,19 @@ __global__ __launch_bounds__(kThreads, fwd_min_waves<HD>()) void dsa3d_fwd_tiled
       float o = oacc[r];
       if constexpr (NH == 2) o += red[m * HD + 16 * ct + mq];
       if (n >= 0)
-        out[n * (static_cast<int64_t>(a.nh) * HD) + tl.head * HD + 16 * ct + mq] = from_f32<bf16>(o);
+        out[n * (static_cast<int64_t>(a.nh) * HD) + tl.head * HD + 16 * ct + mq] =
+            from_f32<bf16>(o * kFixAInv);
     }
   }
 }
 
 // 32 x 16 block vb of a transposed [voxel][query] fixed-point table (row stride
 // `row`, queries from column col0) as the A operand of the 32x32x16 MFMA: lane l
-// holds voxel 32*vb + l%32, queries col0 + 8*(l/32) + j (entry j scaled by
-// inv[j]), rounded to bf16.
+// holds voxel 32*vb + l%32, queries col0 + 8*(l/32) + j, rounded to bf16 in
+// fixed-point units (the per-query scales ride on the other operand).
 __device__ __forceinline__ bf16x8_t table_t_rows(const int* table_t, int row, int col0, int vb,
-                                                 int lane, const float* inv) {
-  const int* p = &table_t[(32 * vb + (lane & 31)) * row + col0 + 8 * (lane >> 5)];
-  u32x4_t r;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const f32x2_t f = {static_cast<float>(p[2 * i]) * inv[2 * i],
-                       static_cast<float>(p[2 * i + 1]) * inv[2 * i + 1]};
-    r[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_t));
-  }
-  return __builtin_bit_cast(bf16x8_t, r);
+                                                 int lane) {
+  return fix_to_bf16x8(&table_t[(32 * vb + (lane & 31)) * row + col0 + 8 * (lane >> 5)]);
 }
 
 // First backward kernel (one frame, 16 queries): pass 1 of the backward.  It
@@ -365,7 +359,10 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
   const bool l1_ok = l1 > 1e-30f;
   const float bscale = l1_ok ? kFixA / l1 : 0.0f;
   if (tl.sub == 0) s_binv[tl.q] = l1_ok ? l1 * kFixAInv : 0.0f;
-  // stage q and dO of the tile transposed: item e moves 8 channels of one row
+  __syncthreads();
+  // stage q and dO of the tile transposed, carrying the fixed-point scales of
+  // B (per query) and A (2^-30) for the dK/dV products: item e moves 8
+  // channels of one row
   for (int e = threadIdx.x; e < 2 * kP2Q * (CW / 8); e += kThreads) {
     const int cg = e % (CW / 8), m = (e / (CW / 8)) % kP2Q, tensor = e / (kP2Q * (CW / 8));
     const int64_t n = tile_row(a, tl, m);
@@ -374,10 +371,13 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
       const bf16* src = tensor == 0 ? a.q + n * a.qs : dout + n * D;
       x = load16(src + cw0 + 8 * cg);
     }
+    const float sc = tensor == 0 ? s_binv[m] : kFixAInv;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      s_qt[tensor][8 * cg + 2 * i][m] = static_cast<uint16_t>(x[i] & 0xffffu);
-      s_qt[tensor][8 * cg + 2 * i + 1][m] = static_cast<uint16_t>(x[i] >> 16);
+      const f32x2_t f = {__uint_as_float(x[i] << 16) * sc, __uint_as_float(x[i] & 0xffff0000u) * sc};
+      const uint32_t h = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_t));
+      s_qt[tensor][8 * cg + 2 * i][m] = static_cast<uint16_t>(h & 0xffffu);
+      s_qt[tensor][8 * cg + 2 * i + 1][m] = static_cast<uint16_t>(h >> 16);
     }
   }
   __syncthreads();
@@ -391,9 +391,6 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
   // operands of the dK/dV MFMAs are re-read from LDS where used (registers are
   // the limit here: a spill reload would wait for every outstanding atomic)
   const int oq = 8 * (tl.lane >> 5);
-  float ainv_k[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) ainv_k[j] = kFixAInv;
   f32x4_t dq_acc[NDQ];
 #pragma unroll
   for (int j = 0; j < NDQ; ++j) dq_acc[j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
@@ -456,12 +453,11 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
       const int t = tl.wave + kWaves * j;
       if (t >= kP2Frames * CT) continue;
       const int fq = t / CT, ct = t % CT;
-      const float binv_m = s_binv[kTQ * fq + mq];
       for (int kc = 0; kc < c.nvp; kc += 32) {
-        float bq[8];
+        float bq[8];  // fixed-point units; the query's scale is applied to dq at the end
 #pragma unroll
         for (int jj = 0; jj < 8; ++jj)
-          bq[jj] = static_cast<float>(s_bt[(kc + kq + jj) * kP2Row + kTQ * fq + mq]) * binv_m;
+          bq[jj] = static_cast<float>(s_bt[(kc + kq + jj) * kP2Row + kTQ * fq + mq]);
         bf16x8_t bhi, blo, kv;
         to_bf16x8_hilo(bq, bhi, blo);
         __builtin_memcpy(&kv, &s_kt[(16 * ct + mq) * kVRow + kc + kq], sizeof(kv));
@@ -478,15 +474,13 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
       f32x16_t dk = {}, dv = {};
 #pragma unroll
       for (int f = 0; f < kP2Frames; ++f) {
-        float binv_k[8];
-        __builtin_memcpy(binv_k, &s_binv[kTQ * f + oq], sizeof(binv_k));
         bf16x8_t qTf, gTf;
         __builtin_memcpy(&qTf, &s_qt[0][och][kTQ * f + oq], sizeof(qTf));
         __builtin_memcpy(&gTf, &s_qt[1][och][kTQ * f + oq], sizeof(gTf));
-        dk = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-            table_t_rows(s_bt, kP2Row, kTQ * f, vb, tl.lane, binv_k), qTf, dk, 0, 0, 0);
-        dv = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-            table_t_rows(s_at, kP2Row, kTQ * f, vb, tl.lane, ainv_k), gTf, dv, 0, 0, 0);
+        dk = __builtin_amdgcn_mfma_f32_32x32x16_bf16(table_t_rows(s_bt, kP2Row, kTQ * f, vb, tl.lane),
+                                                     qTf, dk, 0, 0, 0);
+        dv = __builtin_amdgcn_mfma_f32_32x32x16_bf16(table_t_rows(s_at, kP2Row, kTQ * f, vb, tl.lane),
+                                                     gTf, dv, 0, 0, 0);
       }
       const int ch2 = cw0 + och;
 #pragma unroll
@@ -514,8 +508,9 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
     const int fq = t / CT, ct = t % CT;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int64_t n = tile_row(a, tl, kTQ * fq + 4 * (tl.lane >> 4) + r);
-      if (n >= 0) dq[n * a.qs + cw0 + 16 * ct + mq] = from_f32<bf16>(dq_acc[j][r]);
+      const int m = kTQ * fq + 4 * (tl.lane >> 4) + r;
+      const int64_t n = tile_row(a, tl, m);
+      if (n >= 0) dq[n * a.qs + cw0 + 16 * ct + mq] = from_f32<bf16>(dq_acc[j][r] * s_binv[m]);
     }
   }
 }
@@ -593,6 +588,12 @@ bool dsa3d_tiled_supported(const msd_dsa3d_desc& d, const void* q, const void* k
   if (tiles > 0x7fffffff || d.num_heads > 65535) return false;
   // 16-byte vector loads of q/k/v rows
   if ((d.q_stride % 8) || (d.k_stride % 8) || (d.v_stride % 8)) return false;
+  // K/V chunk rows are addressed as a 64-bit chunk base plus a 32-bit lane byte
+  // offset (24-bit multiplies): kChunk * (W + 1) rows must span < 2^31 bytes
+  for (const int64_t st : {d.k_stride, d.v_stride})
+    if (st >= (int64_t{1} << 23) ||
+        static_cast<int64_t>(tiled::kChunk) * (d.W + 1) * st * 2 >= (int64_t{1} << 31))
+      return false;
   for (const void* p : {q, k, v})
     if (reinterpret_cast<uintptr_t>(p) % 16) return false;
   return true;

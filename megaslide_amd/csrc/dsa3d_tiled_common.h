@@ -275,7 +275,9 @@ __device__ __forceinline__ Chunk make_chunk(const Box& box, int id) {
   c.nx = min(kChunk, box.xhi - c.cx0 + 1);
   c.nv = c.ny * c.nx;
   c.nvp = (c.nv + 31) & ~31;
-  c.rnx = 1.0f / static_cast<float>(c.nx);
+  // hardware reciprocal (1 ulp): (vi + 0.5) / nx is at least 1/32 away from an
+  // integer for vi < 256, nx <= 16, so the truncation below stays exact
+  c.rnx = __builtin_amdgcn_rcpf(static_cast<float>(c.nx));
   return c;
 }
 
@@ -285,6 +287,23 @@ __device__ __forceinline__ int64_t chunk_row(const Args& a, const Tile& tl, cons
   const int vy = static_cast<int>((static_cast<float>(vi) + 0.5f) * c.rnx);
   const int vx = vi - vy * c.nx;
   return tl.sample0 + (static_cast<int64_t>(z) * a.H + c.cy0 + vy) * a.W + c.cx0 + vx;
+}
+
+// Address of channel `col` of voxel vi of chunk c in plane z, in rows of
+// `stride` elements: a wave-uniform 64-bit base (the chunk's first voxel) plus
+// a 32-bit per-lane byte offset, so loads use scalar-base addressing.  The host
+// only admits shapes where (kChunk + 1) * W rows of every operand span less
+// than 2^31 bytes and strides are below 2^23 elements.
+__device__ __forceinline__ const bf16* chunk_voxel_ptr(const Args& a, const Tile& tl,
+                                                       const Chunk& c, int z, const bf16* base,
+                                                       int64_t stride, int col, int vi) {
+  const int64_t origin = tl.sample0 + (static_cast<int64_t>(z) * a.H + c.cy0) * a.W + c.cx0;
+  const char* rb = reinterpret_cast<const char*>(base + origin * stride + col);
+  const int vy = static_cast<int>((static_cast<float>(vi) + 0.5f) * c.rnx);
+  const uint32_t vrow = static_cast<uint32_t>(__umul24(vy, a.W)) +
+                        static_cast<uint32_t>(vi - vy * c.nx);
+  const uint32_t bytes = static_cast<uint32_t>(__umul24(vrow, static_cast<uint32_t>(stride) * 2u));
+  return reinterpret_cast<const bf16*>(rb + bytes);
 }
 
 __device__ __forceinline__ bf16x8_t zero_bf16x8() {
@@ -332,7 +351,7 @@ __device__ __forceinline__ void load_table_rows(const Args& a, const Tile& tl, c
 #pragma unroll
     for (int cc = 0; cc < HD / 32; ++cc) r.y[j][cc] = z4;
     if (vi < c.nv) {
-      const bf16* p = ybase + chunk_row(a, tl, c, z, vi) * ystride + tl.head * HD + kq;
+      const bf16* p = chunk_voxel_ptr(a, tl, c, z, ybase, ystride, tl.head * HD + kq, vi);
 #pragma unroll
       for (int cc = 0; cc < HD / 32; ++cc) r.y[j][cc] = load16(p + 32 * cc);
     }
@@ -383,7 +402,7 @@ __device__ __forceinline__ void load_stage_rows(const Args& a, const Tile& tl, c
 #pragma unroll
   for (int e = 0; e < 2; ++e) {
     if (v0 + e < c.nv) {
-      const bf16* p = ybase + chunk_row(a, tl, c, z, v0 + e) * ystride + col0 + 8 * cg0;
+      const bf16* p = chunk_voxel_ptr(a, tl, c, z, ybase, ystride, col0 + 8 * cg0, v0 + e);
 #pragma unroll
       for (int g = 0; g < G; ++g) r.x[g][e] = load16(p + 8 * P * g);
     }
@@ -487,20 +506,22 @@ __device__ __forceinline__ Bilerp bilerp(const Slot& s, float t00, float t01, fl
 constexpr float kFixA = 1073741824.0f;          // 2^30
 constexpr float kFixAInv = 1.0f / 1073741824.0f;
 
-__device__ __forceinline__ int to_fix(float x) { return static_cast<int>(__builtin_rintf(x)); }
+// Truncating conversion: one instruction; its error (< 2^-30 of the scale)
+// is far below the bf16 rounding the tables get before the MFMA.
+__device__ __forceinline__ int to_fix(float x) { return static_cast<int>(x); }
 
-// 8 fixed-point table entries (scaled by 1/inv) -> bf16x8 MFMA operand.
-__device__ __forceinline__ bf16x8_t fix_to_bf16x8(const int* p, float inv) {
+// 8 fixed-point table entries -> bf16x8 MFMA operand, still in fixed-point
+// units: the power-of-two scale is taken off the MFMA result instead (exact).
+__device__ __forceinline__ bf16x8_t fix_to_bf16x8(const int* p) {
   u32x4_t r;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const f32x2_t f = {static_cast<float>(p[2 * i]) * inv, static_cast<float>(p[2 * i + 1]) * inv};
+    const f32x2_t f = {static_cast<float>(p[2 * i]), static_cast<float>(p[2 * i + 1])};
     r[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_t));
   }
   return __builtin_bit_cast(bf16x8_t, r);
 }
 
-// 8 fp32 table entries -> bf16x8 MFMA operand (round to nearest even).
 __device__ __forceinline__ bf16x8_t to_bf16x8(const float* p) {
   u32x4_t r;
 #pragma unroll
