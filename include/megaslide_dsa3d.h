@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define MSD_ABI_VERSION 1
+#define MSD_ABI_VERSION 2
 
 typedef enum msd_dtype { MSD_F32 = 0, MSD_BF16 = 1 } msd_dtype;
 
@@ -64,6 +64,13 @@ typedef struct msd_dsa3d_desc {
   float offset_scale;          /* reference offset_scale (attention.py:106)       */
   float softmax_scale;         /* 1/sqrt(head_dim) in the reference (:176)        */
   int32_t algo;                /* msd_algo: kernel family (MSD_ALGO_AUTO default) */
+  /* Attention dropout on the softmax weights (nn.Dropout, attention.py:80,
+   * :180).  dropout_p in [0, 1); 0 = off.  The keep mask is drawn from
+   * Philox4x32-10 keyed by dropout_seed (see msd_dsa3d_fwd); backward must be
+   * called with the same three values as its forward.                        */
+  uint32_t dropout_offset;     /* counter word: distinct per call for one seed    */
+  uint64_t dropout_seed;       /* generator key                                   */
+  float dropout_p;             /* drop probability                                */
   int32_t reserved;            /* must be 0                                       */
 } msd_dsa3d_desc;
 
@@ -90,7 +97,13 @@ const char* msd_last_error(void);
 /*
  * Forward of the attention core: replaces attention.py:106-186 (offset scale,
  * base grid + normalised offsets, grid_sample of K and V with border padding
- * and align_corners=False, scores / sqrt(hd), softmax, weighted sum of V).
+ * and align_corners=False, scores / sqrt(hd), softmax, dropout, weighted sum
+ * of V).  With dropout_p > 0, tap k (0 <= k < kt*kh*kw, in the reference's
+ * (i*kh + j)*kw + k order) of global token row r = b*N + n and head m is
+ * dropped when the first word of Philox4x32-10 (Salmon et al., SC'11) for
+ * counter (k, r mod 2^32, (r >> 32) << 16 | m, dropout_offset) and key
+ * (dropout_seed mod 2^32, dropout_seed >> 32) is below floor(p * 2^32); kept
+ * weights are scaled by 1 / (1 - p) (fp32).
  * out [B, N, D] (contiguous, token stride D).  lse [B, N, num_heads] fp32
  * receives the log-sum-exp of each query's scores for the backward; it may be
  * NULL when no backward follows.

@@ -16,7 +16,7 @@ import threading
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libmegaslide_dsa3d.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 MSD_F32 = 0
 MSD_BF16 = 1
@@ -44,7 +44,9 @@ class DsaDesc(ctypes.Structure):
         ("dtype", ctypes.c_int32),
         ("q_stride", ctypes.c_int64), ("k_stride", ctypes.c_int64), ("v_stride", ctypes.c_int64),
         ("offset_scale", ctypes.c_float), ("softmax_scale", ctypes.c_float),
-        ("algo", ctypes.c_int32), ("reserved", ctypes.c_int32),
+        ("algo", ctypes.c_int32), ("dropout_offset", ctypes.c_uint32),
+        ("dropout_seed", ctypes.c_uint64), ("dropout_p", ctypes.c_float),
+        ("reserved", ctypes.c_int32),
     ]
 
 

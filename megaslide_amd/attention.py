@@ -44,8 +44,10 @@ class DeformableSlideAttention3D(nn.Module):
         num_heads: Number of attention heads.
         kernel_size: Tuple (k_t, k_h, k_w) for the local neighbourhood.
         offset_scale: Scale factor for the learned offsets.
-        dropout: Attention dropout rate (p > 0 in training mode is not supported
-            by the kernels yet and raises).
+        dropout: Attention dropout rate on the softmax weights (training mode
+            only, like nn.Dropout).  The kernels draw the keep mask from a
+            Philox4x32-10 stream seeded from torch's default generator, so a
+            fixed torch.manual_seed repeats it; it is not PyTorch's own stream.
     """
 
     def __init__(self, hidden_size: int, num_heads: int,
@@ -90,9 +92,8 @@ class DeformableSlideAttention3D(nn.Module):
         if x.device.type != "cuda":
             raise RuntimeError("megaslide_amd.DeformableSlideAttention3D runs on ROCm devices "
                                "only (HIP kernels; no CPU implementation)")
-        if self.training and self.dropout.p > 0:
-            raise NotImplementedError(
-                "attention dropout p>0 in training mode is not implemented in the HIP kernels")
+        # attention dropout (attention.py:180): in training mode only, as nn.Dropout
+        drop_p = self.dropout.p if self.training else 0.0
 
         # depthwise conv term and offset predictor, channel-last
         dw = dwconv3d(x, self.dw_conv.weight, self.dw_conv.bias, video_shape)
@@ -108,22 +109,27 @@ class DeformableSlideAttention3D(nn.Module):
         off = off.to(dt)
         if extra_kv is None:
             attn = dsa3d_core(q, k.to(dt), v.to(dt), off, video_shape, self.num_heads,
-                              self.kernel_size, self.offset_scale)
+                              self.kernel_size, self.offset_scale, dropout_p=drop_p)
         else:
-            attn = self._with_extra_kv(q, k.to(dt), v.to(dt), off, video_shape, extra_kv)
+            attn = self._with_extra_kv(q, k.to(dt), v.to(dt), off, video_shape, extra_kv, drop_p)
         return self.out_proj(attn) + dw
 
-    def _with_extra_kv(self, q, k, v, off, video_shape, extra_kv):
+    def _with_extra_kv(self, q, k, v, off, video_shape, extra_kv, drop_p=0.0):
         """Local taps + G shared extra keys, merged through the log-sum-exp.
 
         Exactly the reference's concatenation of the extra keys/values to every
-        query's tap list followed by one softmax (attention.py:160-183).
+        query's tap list followed by one softmax (attention.py:160-183).  With
+        dropout, the merged weights of the local taps are a_l * p_local and of
+        the extra keys a_e * p_extra; dropping them is dropping p_local (in the
+        kernel) and p_extra (here), since the mask and scale commute with a_l
+        and a_e.
         """
         B, N, D = q.shape
         nh, hd = self.num_heads, self.head_dim
         G = extra_kv.shape[1]
         loc, lse_loc = dsa3d_core(q, k, v, off, video_shape, nh, self.kernel_size,
-                                  self.offset_scale, return_lse=True)  # [B,N,D], [B,N,nh]
+                                  self.offset_scale, return_lse=True,
+                                  dropout_p=drop_p)  # [B,N,D], [B,N,nh]
         ek = self.k_proj(extra_kv).float()
         ev = self.v_proj(extra_kv).float()
         qh = q.float().view(B, N, nh, hd).permute(0, 2, 1, 3).contiguous()      # [B,nh,N,hd]
@@ -131,7 +137,10 @@ class DeformableSlideAttention3D(nn.Module):
         evh = ev.view(B, G, nh, hd).permute(0, 2, 1, 3).contiguous()             # [B,nh,G,hd]
         s = torch.matmul(qh, ekh) * (1.0 / math.sqrt(hd))                       # [B,nh,N,G]
         lse_e = torch.logsumexp(s, dim=-1)                                       # [B,nh,N]
-        o_e = torch.matmul(torch.softmax(s, dim=-1), evh)                        # [B,nh,N,hd]
+        pe = torch.softmax(s, dim=-1)
+        if drop_p > 0:
+            pe = F.dropout(pe, drop_p, training=True)
+        o_e = torch.matmul(pe, evh)                                              # [B,nh,N,hd]
         lse_l = lse_loc.permute(0, 2, 1)                                         # [B,nh,N]
         lse = torch.logaddexp(lse_l, lse_e)
         a_l = torch.exp(lse_l - lse).unsqueeze(-1)

@@ -45,6 +45,8 @@ int check_dsa(const msd_dsa3d_desc* d) {
     return fail(MSD_ERR_UNSUPPORTED, "dsa3d: dtype %d not supported", d->dtype);
   if (d->algo < MSD_ALGO_AUTO || d->algo > MSD_ALGO_TILED || d->reserved != 0)
     return fail(MSD_ERR_ARG, "dsa3d: bad algo %d / reserved %d", d->algo, d->reserved);
+  if (!(d->dropout_p >= 0.0f && d->dropout_p < 1.0f))
+    return fail(MSD_ERR_ARG, "dsa3d: dropout_p %g outside [0, 1)", static_cast<double>(d->dropout_p));
   const int64_t D = static_cast<int64_t>(d->num_heads) * d->head_dim;
   if (d->q_stride < D || d->k_stride < D || d->v_stride < D)
     return fail(MSD_ERR_ARG, "dsa3d: token strides (%lld, %lld, %lld) below D=%lld",

@@ -4,9 +4,26 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <cmath>
+
+#include "dropout.h"
 #include "megaslide_dsa3d.h"
 
 namespace msd {
+
+// Kernel-side dropout parameters of a call (threshold 0 = off).
+inline DropoutArgs dropout_args(const msd_dsa3d_desc& d) {
+  DropoutArgs r{};
+  if (d.dropout_p > 0.0f) {
+    const double t = std::floor(static_cast<double>(d.dropout_p) * 4294967296.0);
+    r.threshold = t >= 4294967295.0 ? 0xFFFFFFFFu : static_cast<uint32_t>(t);
+    r.scale = 1.0f / (1.0f - d.dropout_p);
+  }
+  r.key0 = static_cast<uint32_t>(d.dropout_seed);
+  r.key1 = static_cast<uint32_t>(d.dropout_seed >> 32);
+  r.offset = d.dropout_offset;
+  return r;
+}
 
 // ---------------------------------------------------------------------------
 // element types: fp32 and bf16 stored as raw 16-bit words

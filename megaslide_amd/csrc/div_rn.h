@@ -2,10 +2,12 @@
 // Host- and device-compilable so the CPU tests check this exact source.
 #pragma once
 
+#ifndef MSD_HD
 #if defined(__HIPCC__)
 #define MSD_HD __host__ __device__
 #else
 #define MSD_HD
+#endif
 #endif
 
 namespace msd {

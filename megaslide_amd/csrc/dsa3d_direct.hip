@@ -44,6 +44,7 @@ struct CoreArgs {
   float offset_scale, softmax_scale;
   float div_x, div_y, div_z;     // T-1, H-1, W-1: divisors of slots 0, 1, 2 (0 if that dim is 1)
   float rdiv_x, rdiv_y, rdiv_z;  // their reciprocals (0 if the dim is 1), for the gradient
+  DropoutArgs drop;              // attention dropout on the softmax weights
 };
 
 template <typename T>
@@ -122,9 +123,10 @@ __global__ __launch_bounds__(kBlock) void dsa3d_fwd_direct_kernel(CoreArgs a, T*
         const float mn = fmaxf(m, s);
         const float corr = __expf(m - mn);
         const float e = __expf(s - mn);
-        l = l * corr + e;
+        l = l * corr + e;  // the softmax normaliser counts dropped taps too
+        const float ed = e * dropout_factor(a.drop, bn, head, kap);
 #pragma unroll
-        for (int j = 0; j < CPL; ++j) acc[j] = acc[j] * corr + e * vsum[j];
+        for (int j = 0; j < CPL; ++j) acc[j] = acc[j] * corr + ed * vsum[j];
         m = mn;
       }
     }
@@ -224,7 +226,10 @@ __global__ __launch_bounds__(kBlock) void dsa3d_bwd_direct_kernel(
         const float s = group_sum<kGroup>(s_part) * sc;
         const float dp = group_sum<kGroup>(dp_part);
         const float p = __expf(s - lse_q);
-        const float ds = p * (dp - delta);
+        // dropout: o sums pd * v_s with pd = p * factor, so dp/ds see the factor
+        const float dfac = dropout_factor(a.drop, bn, head, kap);
+        const float pd = p * dfac;
+        const float ds = p * (dfac * dp - delta);
         const float dss = ds * sc;
 #pragma unroll
         for (int j = 0; j < CPL; ++j) dqv[j] += dss * ksum[j];
@@ -237,7 +242,7 @@ __global__ __launch_bounds__(kBlock) void dsa3d_bwd_direct_kernel(
           const float wy = dy ? ay.f : 1.0f - ay.f;
           const float wx = dx ? ax.f : 1.0f - ax.f;
           const float wgt = wz * wy * wx;
-          const float tc = dss * pk[c] + p * pv[c];
+          const float tc = dss * pk[c] + pd * pv[c];
           gx += (dx ? 1.0f : -1.0f) * wy * wz * tc;
           gy += (dy ? 1.0f : -1.0f) * wx * wz * tc;
           gz += (dz ? 1.0f : -1.0f) * wx * wy * tc;
@@ -246,7 +251,7 @@ __global__ __launch_bounds__(kBlock) void dsa3d_bwd_direct_kernel(
           for (int j = 0; j < CPL; ++j) {
             if (lane * CPL + j < a.hd) {
               atomicAdd(dk_acc + row * D + cbase + j, wgt * dss * qv[j]);
-              atomicAdd(dv_acc + row * D + cbase + j, wgt * p * gov[j]);
+              atomicAdd(dv_acc + row * D + cbase + j, wgt * pd * gov[j]);
             }
           }
         }
@@ -311,6 +316,7 @@ CoreArgs make_args(const msd_dsa3d_desc& d, const void* q, const void* k, const 
   a.rdiv_x = d.T > 1 ? 1.0f / static_cast<float>(d.T - 1) : 0.0f;
   a.rdiv_y = d.H > 1 ? 1.0f / static_cast<float>(d.H - 1) : 0.0f;
   a.rdiv_z = d.W > 1 ? 1.0f / static_cast<float>(d.W - 1) : 0.0f;
+  a.drop = dropout_args(d);
   return a;
 }
 

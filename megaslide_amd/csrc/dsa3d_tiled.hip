@@ -39,7 +39,7 @@ __global__ __launch_bounds__(kThreads, fwd_min_waves<HD>()) void dsa3d_fwd_tiled
   const Tile tl = make_tile<1, kSubs>(a);
   Slot sl[kSlots];
   Box box;
-  setup_slots<kSubs, kSlots>(a, tl, sl, box, s_red);
+  setup_slots<kSubs, kSlots>(a, tl, sl, box, s_red, true);
   const int nchunks = box.ncy * box.ncx;
   const int nit = (box.zhi - box.zlo + 1) * nchunks;
 
@@ -98,7 +98,7 @@ __global__ __launch_bounds__(kThreads, fwd_min_waves<HD>()) void dsa3d_fwd_tiled
   for (int m = 1; m < kSubs; m <<= 1) den += __shfl_xor(den, m);
   const float inv_den = 1.0f / den;
 #pragma unroll
-  for (int i = 0; i < kSlots; ++i) sc[i] *= inv_den;  // p
+  for (int i = 0; i < kSlots; ++i) sc[i] *= inv_den * slot_dropout(sl[i], a.drop);  // p (dropped)
   if (lse != nullptr && tl.q_ok && tl.sub == 0) lse[tl.qn * a.nh + tl.head] = mx + logf(den);
 
   // ---- pass 2: O = A . V ------------------------------------------------------
@@ -186,7 +186,8 @@ __device__ __forceinline__ bf16x8_t table_t_rows(const int* table_t, int row, in
 // First backward kernel (one frame, 16 queries): pass 1 of the backward.  It
 // rebuilds S and dP = dO V^T per plane, accumulates per tap s, dp and their
 // coordinate derivatives, then writes the offset gradients and, for the second
-// kernel, p and ds * softmax_scale of every tap (fp32, [token][head][tap]).
+// kernel, p times its dropout factor and ds * softmax_scale of every tap (fp32,
+// [token][head][tap]).
 template <int HD>
 __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p1_kernel(
     Args a, const bf16* __restrict__ out, const bf16* __restrict__ dout,
@@ -200,7 +201,7 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p1_kernel(
   const int D = a.nh * HD;
   Slot sl[kSlots];
   Box box;
-  setup_slots<kSubs, kSlots>(a, tl, sl, box, s_red);
+  setup_slots<kSubs, kSlots>(a, tl, sl, box, s_red, true);
   const int nchunks = box.ncy * box.ncx;
   const int nit = (box.zhi - box.zlo + 1) * nchunks;
 
@@ -286,15 +287,19 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p1_kernel(
   for (int i = 0; i < kSlots; ++i) {
     if (slot_z0(sl[i]) < 0) continue;
     const float pi = __expf(s_[i] * a.softmax_scale - lse_q);
-    const float dss = pi * (dp_[i] - delta) * a.softmax_scale;
+    // dropout: o sums pd * v_s with pd = p * factor, so dp and the V-side
+    // coordinate gradient see the factor
+    const float dfac = slot_dropout(sl[i], a.drop);
+    const float pd = pi * dfac;
+    const float dss = pi * (dfac * dp_[i] - delta) * a.softmax_scale;
     const int kap = tl.sub + kSubs * i;
-    p_ws[tap0 + kap] = pi;
+    p_ws[tap0 + kap] = pd;
     b_ws[tap0 + kap] = dss;
     bf16* dp = doff + tl.qn * a.C + (static_cast<int64_t>(tl.head) * a.K + kap) * 3;
     const int m = sl[i].zc >> 17;
-    dp[0] = from_f32<bf16>((m & 1) ? (dss * gxs[i] + pi * gxd[i]) * cxs : 0.0f);
-    dp[1] = from_f32<bf16>((m & 2) ? (dss * gys[i] + pi * gyd[i]) * cys : 0.0f);
-    dp[2] = from_f32<bf16>((m & 4) ? (dss * gzs[i] + pi * gzd[i]) * czs : 0.0f);
+    dp[0] = from_f32<bf16>((m & 1) ? (dss * gxs[i] + pd * gxd[i]) * cxs : 0.0f);
+    dp[1] = from_f32<bf16>((m & 2) ? (dss * gys[i] + pd * gyd[i]) * cys : 0.0f);
+    dp[2] = from_f32<bf16>((m & 4) ? (dss * gzs[i] + pd * gzd[i]) * czs : 0.0f);
   }
 
 }
@@ -305,9 +310,10 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p1_kernel(
 // same planes, so one flush of the [voxel][query] tables per plane serves all
 // of them: the fp32 dK/dV atomics (executed past the L2, the backward's
 // dominant cost) drop accordingly.  Tap geometry is recomputed from the
-// offsets; p and ds * scale come from the first kernel.  The A and B tables
-// do not depend on the channel, so a window narrower than the head rebuilds
-// them per window in exchange for fewer registers and less LDS.
+// offsets; p (with its dropout factor) and ds * scale come from the first
+// kernel.  The A and B tables do not depend on the channel, so a window
+// narrower than the head rebuilds them per window in exchange for fewer
+// registers and less LDS.
 constexpr int kP2Frames = 2;
 constexpr int kP2Q = kTQ * kP2Frames;          // queries per tile
 constexpr int kP2Subs = kThreads / kP2Q;       // lanes per query
@@ -558,6 +564,7 @@ tiled::Args make_tiled_args(const msd_dsa3d_desc& d, const void* q, const void* 
   a.rbdiv_z = 1.0f / a.bdiv_z;
   a.r_kw = 1.0f / static_cast<float>(d.kw);
   a.r_khkw = 1.0f / static_cast<float>(d.kh * d.kw);
+  a.drop = dropout_args(d);
   return a;
 }
 

@@ -60,11 +60,13 @@ struct Args {
   float bdiv_x, bdiv_y, bdiv_z;  // base-grid divisors max(S-1, 1) of x (W), y (H), z (T)
   float rbdiv_x, rbdiv_y, rbdiv_z;
   float r_kw, r_khkw;            // 1/kw, 1/(kh*kw): exact small-integer division
+  DropoutArgs drop;              // attention dropout on the softmax weights
 };
 
 // Geometry of one tap, kept in registers between the passes.
 struct Slot {
   int zc;    // z0 (bits 0-15, -1 = empty) | hz << 16 | clamp-gradient mask x,y,z << 17..19
+             // | dropped by attention dropout << 20
   int idx;   // table index of corner (y0, x0) | dy_off << 9 | dx_off << 14 | chunk << 16
   float fz;  // weight of the upper z corner
   float fx, fy;  // weights of the upper x / y corners (0 when that corner is outside)
@@ -74,6 +76,10 @@ __device__ __forceinline__ int slot_z0(const Slot& s) { return static_cast<int16
 __device__ __forceinline__ bool slot_hz(const Slot& s) { return (s.zc >> 16) & 1; }
 __device__ __forceinline__ int slot_chunk(const Slot& s) {
   return static_cast<int>(static_cast<uint32_t>(s.idx) >> 16);
+}
+// Dropout factor of the slot's softmax weight: 1 (off), 0 (dropped) or 1/(1-p).
+__device__ __forceinline__ float slot_dropout(const Slot& s, const DropoutArgs& d) {
+  return d.threshold == 0 ? 1.0f : (((s.zc >> 20) & 1) ? 0.0f : d.scale);
 }
 
 struct Tile {
@@ -152,9 +158,10 @@ __device__ __forceinline__ float grid_coord_rn(float base, float o, float div, f
 
 // Tap geometry for all SLOTS slots of this lane (coordinates exactly as the
 // reference rounds them) and the block-wide bounding box of every corner.
+// With `dropout`, each tap's keep decision is drawn here once (bit 20 of zc).
 template <int SUBS, int SLOTS>
 __device__ __forceinline__ void setup_slots(const Args& a, const Tile& tl, Slot* sl, Box& box,
-                                            int (*s_red)[6]) {
+                                            int (*s_red)[6], bool dropout = false) {
   int zlo = 1 << 30, zhi = -1, ylo = 1 << 30, yhi = -1, xlo = 1 << 30, xhi = -1;
   int y0s[SLOTS], x0s[SLOTS];
   const int qh = tl.qh, qw = tl.qw;
@@ -188,6 +195,8 @@ __device__ __forceinline__ void setup_slots(const Args& a, const Tile& tl, Slot*
     const int my = (ay.u > 0.0f && ay.u < static_cast<float>(a.H - 1)) ? 1 : 0;
     const int mz = (az.u > 0.0f && az.u < static_cast<float>(a.T - 1)) ? 1 : 0;
     sl[i].zc = az.i0 | (az.hi_ok << 16) | (mx << 17) | (my << 18) | (mz << 19);
+    if (dropout && a.drop.threshold != 0 && dropout_factor(a.drop, tl.qn, tl.head, kap) == 0.0f)
+      sl[i].zc |= 1 << 20;
     // an upper corner outside the volume only occurs with weight 0 (the
     // coordinate is clamped to S-1), so fx/fy/fz are 0 there
     sl[i].fx = ax.f;

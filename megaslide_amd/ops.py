@@ -51,7 +51,8 @@ def _tokens_major(t: Tensor, B: int, N: int, D: int) -> Tensor:
 class _CoreCall:
     """Validated shapes of one attention-core call and its C descriptor."""
 
-    def __init__(self, q, k, v, offsets, video_shape, num_heads, kernel_size, offset_scale, algo):
+    def __init__(self, q, k, v, offsets, video_shape, num_heads, kernel_size, offset_scale, algo,
+                 dropout=(0.0, 0, 0)):
         self.dev = _require_device(q, k, v, offsets)
         B, N, D = q.shape
         T, H, W = (int(s) for s in video_shape)
@@ -79,6 +80,10 @@ class _CoreCall:
         self.dtype = dt
         self.offset_scale = float(offset_scale)
         self.algo = algo
+        p, seed, offset = dropout
+        if not 0.0 <= float(p) < 1.0:
+            raise ValueError(f"dropout probability must be in [0, 1), got {p}")
+        self.dropout = (float(p), int(seed) & 0xFFFFFFFFFFFFFFFF, int(offset) & 0xFFFFFFFF)
 
     def desc(self, qs=None, ks=None, vs=None) -> _lib.DsaDesc:
         kt, kh, kw = self.ksz
@@ -88,7 +93,8 @@ class _CoreCall:
             self.q.stride(1) if qs is None else qs,
             self.k.stride(1) if ks is None else ks,
             self.v.stride(1) if vs is None else vs,
-            self.offset_scale, 1.0 / math.sqrt(self.hd), _lib.ALGOS[self.algo], 0)
+            self.offset_scale, 1.0 / math.sqrt(self.hd), _lib.ALGOS[self.algo],
+            self.dropout[2], self.dropout[1], self.dropout[0], 0)
 
     def forward(self, want_lse: bool):
         out = torch.empty((self.B, self.N, self.D), dtype=self.dtype, device=self.dev)
@@ -107,18 +113,20 @@ class DSA3DCoreFunction(torch.autograd.Function):
     """out, lse = core(q, k, v, offsets); both outputs differentiable."""
 
     @staticmethod
-    def forward(ctx, q, k, v, offsets, video_shape, num_heads, kernel_size, offset_scale, algo):
-        call = _CoreCall(q, k, v, offsets, video_shape, num_heads, kernel_size, offset_scale, algo)
+    def forward(ctx, q, k, v, offsets, video_shape, num_heads, kernel_size, offset_scale, algo,
+                dropout):
+        call = _CoreCall(q, k, v, offsets, video_shape, num_heads, kernel_size, offset_scale, algo,
+                         dropout)
         out, lse = call.forward(want_lse=True)
         ctx.call = (call.B, call.T, call.H, call.W, call.nh, call.hd, call.ksz, call.dtype,
-                    call.offset_scale, algo)
+                    call.offset_scale, algo, call.dropout)
         ctx.save_for_backward(call.q, call.k, call.v, call.off, out, lse)
         return out, lse
 
     @staticmethod
     def backward(ctx, dout, dlse):
         q, k, v, offsets, out, lse = ctx.saved_tensors
-        B, T, H, W, nh, hd, ksz, dt, offset_scale, algo = ctx.call
+        B, T, H, W, nh, hd, ksz, dt, offset_scale, algo, dropout = ctx.call
         dev = q.device
         N, D = T * H * W, nh * hd
         if dout is None:
@@ -128,7 +136,7 @@ class DSA3DCoreFunction(torch.autograd.Function):
             dlse = dlse.to(torch.float32).contiguous()
         # gradients are written with the token strides of the desc: contiguous here
         qc, kc, vc = (t if t.stride(1) == D else t.contiguous() for t in (q, k, v))
-        call = _CoreCall(qc, kc, vc, offsets, (T, H, W), nh, ksz, offset_scale, algo)
+        call = _CoreCall(qc, kc, vc, offsets, (T, H, W), nh, ksz, offset_scale, algo, dropout)
         desc = call.desc(D, D, D)
         dq = torch.empty((B, N, D), dtype=dt, device=dev)
         dk = torch.empty((B, N, D), dtype=dt, device=dev)
@@ -143,25 +151,37 @@ class DSA3DCoreFunction(torch.autograd.Function):
                 out.data_ptr(), dout.data_ptr(), lse.data_ptr(), _lib.ptr(dlse),
                 dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), doff.data_ptr(),
                 ws.data_ptr(), ws_bytes, _lib.stream_handle(dev)), "dsa3d_bwd")
-        return dq, dk, dv, doff, None, None, None, None, None
+        return dq, dk, dv, doff, None, None, None, None, None, None
 
 
 def dsa3d_core(q: Tensor, k: Tensor, v: Tensor, offsets: Tensor, video_shape: Sequence[int],
                num_heads: int, kernel_size: Sequence[int] = (3, 7, 7), offset_scale: float = 1.0,
-               return_lse: bool = False, algo: str = "auto"):
+               return_lse: bool = False, algo: str = "auto", dropout_p: float = 0.0,
+               dropout_seed: Optional[int] = None, dropout_offset: int = 0):
     """Attention core on device tensors.
 
     q, k, v: [B, N, D]; offsets: [B, N, num_heads*kt*kh*kw*3] unscaled, channel
     order [head][i][j][k][slot] (the reference's offsets.view order,
     attention.py:109).  Returns out [B, N, D] (and lse [B, N, num_heads]).
     ``algo``: "auto" (default), "direct" or "tiled" kernel family.
+
+    ``dropout_p`` > 0 drops softmax weights as the reference's nn.Dropout does
+    (attention.py:180): kept weights are scaled by 1 / (1 - p).  The keep mask
+    comes from Philox4x32-10 keyed by ``dropout_seed`` (drawn from torch's
+    default CPU generator when None, so torch.manual_seed makes it repeatable);
+    the backward reuses the forward's mask.
     """
+    p = float(dropout_p)
+    if p > 0.0 and dropout_seed is None:
+        dropout_seed = int(torch.randint(0, 2**63 - 1, (1,), dtype=torch.int64).item())
+    dropout = (p, 0 if dropout_seed is None else int(dropout_seed), int(dropout_offset))
     if torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v, offsets)):
         out, lse = DSA3DCoreFunction.apply(q, k, v, offsets, tuple(video_shape), int(num_heads),
-                                           tuple(kernel_size), float(offset_scale), algo)
+                                           tuple(kernel_size), float(offset_scale), algo, dropout)
         return (out, lse) if return_lse else out
     # forward only: nothing saved, no lse unless asked for
-    call = _CoreCall(q, k, v, offsets, video_shape, num_heads, kernel_size, offset_scale, algo)
+    call = _CoreCall(q, k, v, offsets, video_shape, num_heads, kernel_size, offset_scale, algo,
+                     dropout)
     out, lse = call.forward(want_lse=return_lse)
     return (out, lse) if return_lse else out
 

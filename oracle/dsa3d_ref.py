@@ -86,12 +86,31 @@ def _heads_volume(t: Tensor, B: int, T: int, H: int, W: int, nh: int, hd: int) -
     return t.reshape(B, T, H, W, nh, hd).permute(0, 4, 5, 1, 2, 3)
 
 
+def _dropout_factors(dropout, B, N, Nq, nh, h0, h1, K, query_index, p) -> Tensor:
+    """[B, h1-h0, Nq, K(+G)] factors 0 or 1/(1-p) for the local taps (1 for extra keys)."""
+    import numpy as np
+
+    from .philox import dropout_scale, keep_mask
+
+    prob, seed, offset = dropout
+    n = (np.arange(Nq) if query_index is None
+         else np.asarray(torch.as_tensor(query_index).cpu(), dtype=np.int64))
+    rows = (np.arange(B, dtype=np.int64).reshape(B, 1) * N + n.reshape(1, -1)).reshape(-1)
+    keep = keep_mask(prob, seed, offset, rows, nh, K).reshape(B, Nq, nh, K)[:, :, h0:h1]
+    f = torch.from_numpy(np.where(keep, dropout_scale(prob), np.float32(0.0)).astype(np.float32))
+    f = f.permute(0, 2, 1, 3).to(p.dtype)
+    if p.shape[-1] > K:  # extra keys appended after the taps are not dropped here
+        f = torch.cat([f, torch.ones(*f.shape[:-1], p.shape[-1] - K, dtype=p.dtype)], dim=-1)
+    return f
+
+
 def dsa3d_core_ref(q: Tensor, k: Tensor, v: Tensor, off: Tensor,
                    video_shape: Sequence[int], num_heads: int,
                    kernel_size: Sequence[int] = (3, 7, 7), offset_scale: float = 1.0,
                    head_chunk: Optional[int] = None, return_lse: bool = False,
                    extra_k: Optional[Tensor] = None, extra_v: Optional[Tensor] = None,
-                   query_index: Optional[Tensor] = None):
+                   query_index: Optional[Tensor] = None,
+                   dropout: Optional[Tuple[float, int, int]] = None):
     """Deformable local attention core, reference op sequence.
 
     Restates attention.py:106-186 without the projections: scale the offsets
@@ -110,6 +129,11 @@ def dsa3d_core_ref(q: Tensor, k: Tensor, v: Tensor, off: Tensor,
     queries, since each query's output, dq and d offsets depend on its own taps
     only.  Returns out [B, Nq, D] (and the per-(b, head, token) log-sum-exp
     [B, nh, Nq] of the scores when ``return_lse``).
+
+    ``dropout = (p, seed, offset)`` applies the reference's attention dropout
+    (attention.py:180) to the local taps' softmax weights with the keep mask of
+    ``oracle.philox.keep_mask`` (the generator the HIP kernels use) and the
+    fp32 scale 1 / (1 - p).  Extra keys are not dropped here.
     """
     B, N, D = q.shape
     T, H, W = video_shape
@@ -152,6 +176,8 @@ def dsa3d_core_ref(q: Tensor, k: Tensor, v: Tensor, off: Tensor,
         qq = qh[:, h0:h1]  # [B,m,Nq,hd]
         scores = torch.matmul(qq.unsqueeze(-2), ks).squeeze(-2) / math.sqrt(hd)  # [B,m,N,K]
         p = F.softmax(scores, dim=-1)
+        if dropout is not None and dropout[0] > 0:
+            p = p * _dropout_factors(dropout, B, N, Nq, nh, h0, h1, K, query_index, p)
         o = torch.matmul(p.unsqueeze(-2), vs.transpose(-2, -1)).squeeze(-2)  # [B,m,N,hd]
         outs.append(o)
         if return_lse:

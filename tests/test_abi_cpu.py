@@ -33,7 +33,7 @@ def test_exports_match_header():
 
 
 def test_abi_version():
-    assert _lib.load().msd_abi_version() == _lib.ABI_VERSION == 1
+    assert _lib.load().msd_abi_version() == _lib.ABI_VERSION == 2
 
 
 def _desc(**kw):
@@ -61,6 +61,9 @@ def test_null_desc_rejected():
     ("kt", 0, -1, b"bad window"),
     ("dtype", 7, -2, b"dtype"),
     ("q_stride", 64, -1, b"strides"),
+    ("dropout_p", 1.0, -1, b"dropout_p"),
+    ("dropout_p", -0.1, -1, b"dropout_p"),
+    ("dropout_p", float("nan"), -1, b"dropout_p"),
 ])
 def test_bad_desc_fields(field, value, code, needle):
     rc = _fwd(_desc(**{field: value}))
