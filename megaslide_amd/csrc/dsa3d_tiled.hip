@@ -663,9 +663,9 @@ hipError_t launch_dsa3d_bwd_tiled(const msd_dsa3d_desc& d, const void* q, const 
   const auto* go = static_cast<const bf16*>(dout);
   auto* gq = static_cast<bf16*>(dq);
   auto* goff = static_cast<bf16*>(doff);
-  // the second kernel's channel window: the whole head up to 96 channels, two
-  // windows of 64 for head_dim 128 (registers and LDS of the 64-channel kernel)
-  dim3 g2 = tiled_grid<kP2Frames>(d);
+  // the second kernel takes the whole head as its channel window (for
+  // head_dim 128, two windows of 64 measured 4% slower than one of 128)
+  const dim3 g2 = tiled_grid<kP2Frames>(d);
   switch (d.head_dim) {
     case 64:
       hipLaunchKernelGGL(dsa3d_bwd_p1_kernel<64>, g1, block, 0, s, a1, o, go, lse, dlse, goff,
@@ -682,8 +682,7 @@ hipError_t launch_dsa3d_bwd_tiled(const msd_dsa3d_desc& d, const void* q, const 
     case 128:
       hipLaunchKernelGGL(dsa3d_bwd_p1_kernel<128>, g1, block, 0, s, a1, o, go, lse, dlse, goff,
                          p_ws, b_ws);
-      g2.z = 2;
-      hipLaunchKernelGGL((dsa3d_bwd_p2_kernel<128, 64>), g2, block, 0, s, a2, go, p_ws, b_ws, gq,
+      hipLaunchKernelGGL((dsa3d_bwd_p2_kernel<128, 128>), g2, block, 0, s, a2, go, p_ws, b_ws, gq,
                          dk_acc, dv_acc);
       break;
     default:

@@ -16,6 +16,8 @@
 // kernel keeps all kt*kh*kw tap sums of its channel in registers over a strip
 // of rows and flushes them with one fp32 atomic per (thread, tap).
 // Other odd kernel sizes use the simple one-output-per-thread kernels.
+#include <type_traits>
+
 #include "common.h"
 
 namespace msd {
@@ -202,6 +204,121 @@ __global__ __launch_bounds__(64 * kRowWaves) void dwconv_block_kernel(
         for (int j = 0; j < kRun; ++j)
 #pragma unroll
           for (int k = 0; k < KW; ++k) acc[r][j] = __builtin_fmaf(wk[dh][k], x[j + k], acc[r][j]);
+      }
+    }
+  }
+  if (!c_ok) return;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int h = h0 + r;
+    if (h >= a.H) continue;
+    const int64_t orow = ((static_cast<int64_t>(b) * a.T + t) * a.H + h) * a.W;
+#pragma unroll
+    for (int j = 0; j < kRun; ++j) {
+      const int w = w0 + j;
+      if (w >= a.W) continue;
+      const int64_t i0 = (orow + w) * a.C;  // uniform; + lc per lane
+      if (MODE == kPlain) stu(out + i0, lc, acc[r][j]);
+      if (MODE == kGelu) stu(out + i0, lc, gelu_erf(acc[r][j]));
+      if (MODE == kGeluGrad) out_f32[i0 + lc] = ldu(dy + i0, lc) * gelu_erf_grad(acc[r][j]);
+    }
+  }
+}
+
+// bf16 input and weights: the same blocking, with each pair of taps along W
+// as one v_dot2 (two exact bf16 products added into the fp32 accumulator); the
+// odd last tap stays an fp32 FMA.  Pairs (x[m], x[m+1]) of the loaded row
+// segment are packed once and shared by every output of the run.
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_dot_t;
+
+__device__ __forceinline__ uint32_t ldu_bits(const bf16* base, uint32_t lane_off) {
+  return reinterpret_cast<const bf16*>(reinterpret_cast<const char*>(base) + lane_off * 2u)->bits;
+}
+
+__device__ __forceinline__ float dot2_bf16(uint32_t w, uint32_t x, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_dot_t, w),
+                                         __builtin_bit_cast(bf16x2_dot_t, x), acc, false);
+}
+
+template <int KH, int KW, int MODE>
+__global__ __launch_bounds__(64 * kRowWaves) void dwconv_block_dot2_kernel(
+    ConvArgs a, const bf16* __restrict__ in, const bf16* __restrict__ wt,
+    const bf16* __restrict__ bias, const bf16* __restrict__ dy, bf16* __restrict__ out,
+    float* __restrict__ out_f32, int flip) {
+  constexpr int R = kBlockRows, PH = KH / 2, PW = KW / 2, NX = kRun + KW - 1, KP = KW / 2;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c = blockIdx.y * 64 + lane;
+  const int runs = (a.W + kRun - 1) / kRun;
+  const int hblocks = (a.H + R - 1) / R;
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * kRowWaves + wave;  // (b, t, hblock, run)
+  const int64_t items = static_cast<int64_t>(a.B) * a.T * hblocks * runs;
+  if (item >= items) return;
+  const bool c_ok = c < a.C;
+  const uint32_t lc = c_ok ? c : a.C - 1;  // lanes past C read a valid channel and store nothing
+  const int run = static_cast<int>(item % runs);
+  const int64_t rest = item / runs;
+  const int hb = static_cast<int>(rest % hblocks);
+  const int64_t bt = rest / hblocks;
+  const int t = static_cast<int>(bt % a.T);
+  const int b = static_cast<int>(bt / a.T);
+  const int h0 = hb * R, w0 = run * kRun;
+  const int K = a.kt * KH * KW;
+  const int64_t rowstride = static_cast<int64_t>(a.W) * a.C;
+
+  float acc[R][kRun];
+  const float b0 = bias != nullptr ? ldu(bias, lc) : 0.0f;
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int j = 0; j < kRun; ++j) acc[r][j] = b0;
+
+  for (int dt = 0; dt < a.kt; ++dt) {
+    const int tt = t + dt - a.kt / 2;
+    if (tt < 0 || tt >= a.T) continue;
+    uint32_t wp[KH][KP];  // taps (2kp, 2kp+1) of row dh, packed bf16
+    float wl[KH];         // tap KW-1
+#pragma unroll
+    for (int dh = 0; dh < KH; ++dh) {
+      const int tap0 = (dt * KH + dh) * KW;
+#pragma unroll
+      for (int kp = 0; kp < KP; ++kp) {
+        const int ta = tap0 + 2 * kp, tb = ta + 1;
+        const uint32_t lo = ldu_bits(wt + (flip ? K - 1 - ta : ta), lc * K);
+        const uint32_t hi = ldu_bits(wt + (flip ? K - 1 - tb : tb), lc * K);
+        wp[dh][kp] = lo | (hi << 16);
+      }
+      const int tl = tap0 + KW - 1;
+      wl[dh] = ldu(wt + (flip ? K - 1 - tl : tl), lc * K);
+    }
+    const bf16* plane = in + (static_cast<int64_t>(b) * a.T + tt) * a.H * rowstride;
+#pragma unroll
+    for (int ii = 0; ii < R + KH - 1; ++ii) {
+      const int hh = h0 + ii - PH;
+      if (hh < 0 || hh >= a.H) continue;
+      const bf16* row = plane + hh * rowstride;
+      uint32_t xb[NX];
+#pragma unroll
+      for (int j = 0; j < NX; ++j) {
+        const int ww = w0 + j - PW;
+        const int wc = min(max(ww, 0), a.W - 1);
+        const uint32_t v = ldu_bits(row + static_cast<int64_t>(wc) * a.C, lc);
+        xb[j] = ww == wc ? v : 0u;
+      }
+      uint32_t xp[NX - 1];
+#pragma unroll
+      for (int m = 0; m < NX - 1; ++m) xp[m] = xb[m] | (xb[m + 1] << 16);
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int dh = ii - r;
+        if (dh < 0 || dh >= KH) continue;
+#pragma unroll
+        for (int j = 0; j < kRun; ++j) {
+          float v = acc[r][j];
+#pragma unroll
+          for (int kp = 0; kp < KP; ++kp) v = dot2_bf16(wp[dh][kp], xp[j + 2 * kp], v);
+          acc[r][j] = __builtin_fmaf(wl[dh], __uint_as_float(xb[j + KW - 1] << 16), v);
+        }
       }
     }
   }
@@ -505,8 +622,12 @@ void launch_block(const ConvArgs& a, const G* in, const T* w, const T* b, const 
   const int64_t items = static_cast<int64_t>(a.B) * a.T * hblocks * runs;
   const dim3 grid(static_cast<unsigned>((items + kRowWaves - 1) / kRowWaves),
                   static_cast<unsigned>((a.C + 63) / 64));
-  hipLaunchKernelGGL((dwconv_block_kernel<T, G, KS, KS, MODE>), grid, dim3(64 * kRowWaves), 0, s, a,
-                     in, w, b, dy, out, out_f32, flip);
+  if constexpr (std::is_same<T, bf16>::value && std::is_same<G, bf16>::value)
+    hipLaunchKernelGGL((dwconv_block_dot2_kernel<KS, KS, MODE>), grid, dim3(64 * kRowWaves), 0, s,
+                       a, in, w, b, dy, out, out_f32, flip);
+  else
+    hipLaunchKernelGGL((dwconv_block_kernel<T, G, KS, KS, MODE>), grid, dim3(64 * kRowWaves), 0, s,
+                       a, in, w, b, dy, out, out_f32, flip);
 }
 
 // conv of `in` (type G) with w (flip: mirrored taps), epilogue MODE

@@ -73,6 +73,9 @@ def test_tiled_constant_values():
     (1, 4, 13, 18, 1, (3, 7, 7), 4.0, 0.9, 96),   # non-tile-aligned grid, large offsets
     (1, 3, 8, 8, 2, (3, 7, 7), 0.5, 1.0, 128),
     (1, 5, 12, 40, 1, (3, 7, 7), 8.0, 1.0, 128),  # corner boxes span several chunks
+    (1, 4, 1, 9, 2, (3, 7, 7), 1.0, 1.0, 64),     # H = 1: y slot dropped, base y divisor 1
+    (1, 3, 6, 1, 1, (3, 7, 7), 1.0, 1.0, 64),     # W = 1: z slot dropped (slot/axis quirk)
+    (2, 2, 3, 5, 2, (1, 3, 5), 3.0, 1.2, 96),     # B = 2, asymmetric window
 ])
 def test_tiled_backward_vs_oracle_and_direct(shape):
     B, T, H, W, nh, ks, off_std, scale, hd = shape
