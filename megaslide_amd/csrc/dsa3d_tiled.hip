@@ -24,6 +24,10 @@ using namespace tiled;
 // Minimum waves per SIMD of the forward kernel: two 512-thread workgroups per
 // CU fit in the LDS up to head_dim 96; head_dim 128 stages 66 KB of V^T, so
 // one workgroup per CU, and the register cap is raised to match.
+//
+// The S (pass 1) and A (pass 2) tables are double-buffered: a plane's table is
+// written while the other buffer may still be read for the previous plane, so
+// pass 1 needs one barrier per plane and pass 2 two (instead of two and three).
 template <int HD>
 constexpr int fwd_min_waves() {
   return HD <= 96 ? 4 : 2;
@@ -32,8 +36,8 @@ constexpr int fwd_min_waves() {
 template <int HD>
 __global__ __launch_bounds__(kThreads, fwd_min_waves<HD>()) void dsa3d_fwd_tiled_kernel(
     Args a, bf16* __restrict__ out, float* __restrict__ lse) {
-  __shared__ __attribute__((aligned(16))) float s_tab[kTQ * kSRow];    // S, then A
-  __shared__ __attribute__((aligned(16))) uint16_t s_vt[HD * kVRow];  // V^T chunk
+  __shared__ __attribute__((aligned(16))) float s_tab[2][kTQ * kSRow];  // S, then A (2 buffers)
+  __shared__ __attribute__((aligned(16))) uint16_t s_vt[HD * kVRow];    // V^T chunk
   __shared__ int s_red[kWaves][6];
 
   const Tile tl = make_tile<1, kSubs>(a);
@@ -45,7 +49,6 @@ __global__ __launch_bounds__(kThreads, fwd_min_waves<HD>()) void dsa3d_fwd_tiled
 
   bf16x8_t qx[HD / 32];
   load_rows_operand<HD>(a, tl, a.q, a.qs, qx);
-  const float* my_row = &s_tab[tl.q * kSRow];
 
   // ---- pass 1: scores -------------------------------------------------------
   // K rows of the next (plane, chunk) are loaded while the current one is used
@@ -55,17 +58,20 @@ __global__ __launch_bounds__(kThreads, fwd_min_waves<HD>()) void dsa3d_fwd_tiled
   TableRows<HD> rows;
   if (nit > 0) load_table_rows<HD>(a, tl, make_chunk(box, 0), box.zlo, a.k, a.ks, rows);
   for (int it = 0; it < nit; ++it) {
-    const int zi = it / nchunks;
+    const int zi = uniform_div(it, nchunks);
     const int z = box.zlo + zi;
     const Chunk c = make_chunk(box, it - zi * nchunks);
-    store_table<HD>(tl, c, qx, rows, s_tab);
+    // buffer it & 1 was last read for plane it - 2, before the previous barrier
+    float* tab = s_tab[it & 1];
+    store_table<HD>(tl, c, qx, rows, tab);
     if (it + 1 < nit) {
-      const int zn = (it + 1) / nchunks;
+      const int zn = uniform_div(it + 1, nchunks);
       load_table_rows<HD>(a, tl, make_chunk(box, it + 1 - zn * nchunks), box.zlo + zn, a.k, a.ks,
                           rows);
     }
     __syncthreads();
     // every slot reads its corners (in-bounds for any slot); misses are discarded
+    const float* my_row = &tab[tl.q * kSRow];
     float t[kSlots][4];
 #pragma unroll
     for (int i = 0; i < kSlots; ++i) corners4(sl[i], my_row, t[i][0], t[i][1], t[i][2], t[i][3]);
@@ -76,7 +82,6 @@ __global__ __launch_bounds__(kThreads, fwd_min_waves<HD>()) void dsa3d_fwd_tiled
       const float v = bilerp(sl[i], t[i][0], t[i][1], t[i][2], t[i][3]).val;
       sc[i] = hit ? __builtin_fmaf(wz, v, sc[i]) : sc[i];
     }
-    __syncthreads();
   }
 
   // ---- softmax over each query's taps (32 lanes x kSlots) -------------------
@@ -109,23 +114,25 @@ __global__ __launch_bounds__(kThreads, fwd_min_waves<HD>()) void dsa3d_fwd_tiled
   const int mq = tl.lane & 15, kq = 8 * (tl.lane >> 4);
   const int ct = tl.wave % CT, half = tl.wave / CT;
   f32x4_t oacc = {0.0f, 0.0f, 0.0f, 0.0f};
-  int* const s_atab = reinterpret_cast<int*>(s_tab);  // A in fixed point (scale 2^30)
-  int* row = &s_atab[tl.q * kSRow];
   StageRows<kThreads, HD> vr;
   if (nit > 0)
     load_stage_rows<kThreads, HD>(a, tl, make_chunk(box, 0), box.zlo, a.v, a.vs, tl.head * HD, vr);
+  __syncthreads();  // pass-1 reads of both buffers are done
+  zero_table(s_tab[0], kChunkNV);
   for (int it = 0; it < nit; ++it) {
-    const int zi = it / nchunks;
+    const int zi = uniform_div(it, nchunks);
     const int z = box.zlo + zi;
     const Chunk c = make_chunk(box, it - zi * nchunks);
-    zero_table(s_tab, c.nvp);
+    // A in fixed point (scale 2^30), buffer it & 1: zeroed during the previous plane
+    int* const s_atab = reinterpret_cast<int*>(s_tab[it & 1]);
+    int* row = &s_atab[tl.q * kSRow];
+    __syncthreads();  // the previous plane's MFMAs are done with V^T; this buffer is zeroed
     store_stage<kThreads, HD>(c, vr, s_vt);
     if (it + 1 < nit) {
-      const int zn = (it + 1) / nchunks;
+      const int zn = uniform_div(it + 1, nchunks);
       load_stage_rows<kThreads, HD>(a, tl, make_chunk(box, it + 1 - zn * nchunks), box.zlo + zn,
                                     a.v, a.vs, tl.head * HD, vr);
     }
-    __syncthreads();
 #pragma unroll
     for (int i = 0; i < kSlots; ++i) {
       float wz, dwz;
@@ -133,10 +140,12 @@ __global__ __launch_bounds__(kThreads, fwd_min_waves<HD>()) void dsa3d_fwd_tiled
       const float pz = sc[i] * wz * kFixA;
       const float gx = 1.0f - sl[i].fx, gy = 1.0f - sl[i].fy;
       const int base = sl[i].idx & 0x1ff, dy = (sl[i].idx >> 9) & 0x1f, dx = (sl[i].idx >> 14) & 1;
+      // an upper corner outside the volume has offset 0 and weight 0: it adds 0
+      // to the lower corner, so all four adds run without branches
       atomicAdd(&row[base], to_fix(pz * (gy * gx)));
-      if (dx) atomicAdd(&row[base + 1], to_fix(pz * (gy * sl[i].fx)));
-      if (dy) atomicAdd(&row[base + dy], to_fix(pz * (sl[i].fy * gx)));
-      if (dx && dy) atomicAdd(&row[base + dy + 1], to_fix(pz * (sl[i].fy * sl[i].fx)));
+      atomicAdd(&row[base + dx], to_fix(pz * (gy * sl[i].fx)));
+      atomicAdd(&row[base + dy], to_fix(pz * (sl[i].fy * gx)));
+      atomicAdd(&row[base + dy + dx], to_fix(pz * (sl[i].fy * sl[i].fx)));
     }
     __syncthreads();
     if (half < NH) {
@@ -147,12 +156,14 @@ __global__ __launch_bounds__(kThreads, fwd_min_waves<HD>()) void dsa3d_fwd_tiled
         oacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv, oacc, 0, 0, 0);
       }
     }
-    __syncthreads();
+    // the other buffer was last read for the previous plane, before the barrier above
+    if (it + 1 < nit) zero_table(s_tab[(it + 1) & 1], kChunkNV);
   }
+  __syncthreads();
   // oacc[r] = partial O[query 4*(lane/16) + r][channel 16*ct + lane%16] in
   // fixed-point units of A; with two phases the second's partial sums are added
   // through LDS
-  float* red = s_tab;  // 16 x HD
+  float* red = s_tab[0];  // 16 x HD
   if constexpr (NH == 2) {
     if (half == 1) {
 #pragma unroll
@@ -193,8 +204,9 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p1_kernel(
     Args a, const bf16* __restrict__ out, const bf16* __restrict__ dout,
     const float* __restrict__ lse, const float* __restrict__ dlse, bf16* __restrict__ doff,
     float* __restrict__ p_ws, float* __restrict__ b_ws) {
-  __shared__ __attribute__((aligned(16))) float s_t0[kTQ * kSRow];  // S
-  __shared__ __attribute__((aligned(16))) float s_t1[kTQ * kSRow];  // dP
+  // S and dP tables, double-buffered: one barrier per plane
+  __shared__ __attribute__((aligned(16))) float s_t0[2][kTQ * kSRow];  // S
+  __shared__ __attribute__((aligned(16))) float s_t1[2][kTQ * kSRow];  // dP
   __shared__ int s_red[kWaves][6];
 
   const Tile tl = make_tile<1, kSubs>(a);
@@ -236,22 +248,23 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p1_kernel(
     load_table_rows<HD>(a, tl, c0, box.zlo, a.k, a.ks, rk);
     load_table_rows<HD>(a, tl, c0, box.zlo, a.v, a.vs, rv);
   }
-  const float* r0 = &s_t0[tl.q * kSRow];
-  const float* r1 = &s_t1[tl.q * kSRow];
   for (int it = 0; it < nit; ++it) {
-    const int zi = it / nchunks;
+    const int zi = uniform_div(it, nchunks);
     const int z = box.zlo + zi;
     const Chunk c = make_chunk(box, it - zi * nchunks);
-    store_table<HD>(tl, c, qx, rk, s_t0);
-    store_table<HD>(tl, c, gx, rv, s_t1);
+    // buffer it & 1 was last read for plane it - 2, before the previous barrier
+    store_table<HD>(tl, c, qx, rk, s_t0[it & 1]);
+    store_table<HD>(tl, c, gx, rv, s_t1[it & 1]);
     if (it + 1 < nit) {
-      const int zn = (it + 1) / nchunks;
+      const int zn = uniform_div(it + 1, nchunks);
       const Chunk cn = make_chunk(box, it + 1 - zn * nchunks);
       load_table_rows<HD>(a, tl, cn, box.zlo + zn, a.k, a.ks, rk);
       load_table_rows<HD>(a, tl, cn, box.zlo + zn, a.v, a.vs, rv);
     }
     __syncthreads();
     // every slot reads its corners (in-bounds for any slot); misses are discarded
+    const float* r0 = &s_t0[it & 1][tl.q * kSRow];
+    const float* r1 = &s_t1[it & 1][tl.q * kSRow];
 #pragma unroll
     for (int i = 0; i < kSlots; ++i) {
       float wz, dwz;
@@ -273,7 +286,6 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p1_kernel(
       gyd[i] = __builtin_fmaf(wz, dy, gyd[i]);
       gzd[i] = __builtin_fmaf(dwz, dv, gzd[i]);
     }
-    __syncthreads();
   }
 
   // p = exp(scale * s - lse), ds = p (dp - Delta).  The coordinate gradient of
@@ -404,7 +416,7 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
   if (nit > 0)
     load_stage_rows<kThreads, CW>(a, tl, make_chunk(box, 0), box.zlo, a.k, a.ks, cw0, kr);
   for (int it = 0; it < nit; ++it) {
-    const int zi = it / nchunks;
+    const int zi = uniform_div(it, nchunks);
     const int z = box.zlo + zi;
     const Chunk c = make_chunk(box, it - zi * nchunks);
     // zero the transposed A and B tables; token rows of the chunk's voxels
@@ -417,7 +429,7 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
       s_rows[vi] = static_cast<int>(chunk_row(a, tl, c, z, vi) - tl.sample0);
     store_stage<kThreads, CW>(c, kr, s_kt);
     if (it + 1 < nit) {
-      const int zn = (it + 1) / nchunks;
+      const int zn = uniform_div(it + 1, nchunks);
       load_stage_rows<kThreads, CW>(a, tl, make_chunk(box, it + 1 - zn * nchunks), box.zlo + zn,
                                     a.k, a.ks, cw0, kr);
     }
@@ -436,20 +448,16 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
       const int base = idx & 0x1ff, dy = (idx >> 9) & 0x1f, dx = (idx >> 14) & 1;
       int* ra = &s_at[base * kP2Row + tl.q];
       int* rb = &s_bt[base * kP2Row + tl.q];
+      // an upper corner outside the volume has offset 0 and weight 0: it adds 0
+      // to the lower corner, so all eight adds run without branches
       atomicAdd(ra, to_fix(pz * w00));
       atomicAdd(rb, to_fix(bz * w00));
-      if (dx) {
-        atomicAdd(ra + kP2Row, to_fix(pz * w01));
-        atomicAdd(rb + kP2Row, to_fix(bz * w01));
-      }
-      if (dy) {
-        atomicAdd(ra + dy * kP2Row, to_fix(pz * w10));
-        atomicAdd(rb + dy * kP2Row, to_fix(bz * w10));
-      }
-      if (dx && dy) {
-        atomicAdd(ra + (dy + 1) * kP2Row, to_fix(pz * w11));
-        atomicAdd(rb + (dy + 1) * kP2Row, to_fix(bz * w11));
-      }
+      atomicAdd(ra + dx * kP2Row, to_fix(pz * w01));
+      atomicAdd(rb + dx * kP2Row, to_fix(bz * w01));
+      atomicAdd(ra + dy * kP2Row, to_fix(pz * w10));
+      atomicAdd(rb + dy * kP2Row, to_fix(bz * w10));
+      atomicAdd(ra + (dy + dx) * kP2Row, to_fix(pz * w11));
+      atomicAdd(rb + (dy + dx) * kP2Row, to_fix(bz * w11));
     }
     __syncthreads();
     // dq[q] += sum_v B[q][v] K[v]; B as a bf16 hi/lo pair because

@@ -274,10 +274,17 @@ struct Chunk {
   float rnx;  // 1/nx, for division-free voxel coordinates
 };
 
+// a / n for a wave-uniform n, skipping the (scalar, multi-instruction)
+// division in the common case n == 1: the whole corner box fits one chunk.
+__device__ __forceinline__ int uniform_div(int a, int n) {
+  if (n == 1) return a;
+  return a / n;
+}
+
 __device__ __forceinline__ Chunk make_chunk(const Box& box, int id) {
   Chunk c;
   c.id = id;
-  const int cy = id / box.ncx, cx = id - cy * box.ncx;
+  const int cy = uniform_div(id, box.ncx), cx = id - cy * box.ncx;
   c.cy0 = box.ylo + kChunkStep * cy;
   c.cx0 = box.xlo + kChunkStep * cx;
   c.ny = min(kChunk, box.yhi - c.cy0 + 1);
