@@ -25,18 +25,27 @@ using namespace tiled;
 // CU fit in the LDS up to head_dim 96; head_dim 128 stages 66 KB of V^T, so
 // one workgroup per CU, and the register cap is raised to match.
 //
-// The S (pass 1) and A (pass 2) tables are double-buffered: a plane's table is
-// written while the other buffer may still be read for the previous plane, so
-// pass 1 needs one barrier per plane and pass 2 two (instead of two and three).
+// The S (pass 1) and A (pass 2) tables are double-buffered where that keeps
+// the workgroups per CU: a step's table is written while the other buffer may
+// still be read for the previous step, so pass 1 needs one barrier per step and
+// pass 2 two (instead of two and three).  head_dim 96 keeps one buffer: two
+// would drop it to one workgroup per CU (measured 30% slower).
 template <int HD>
 constexpr int fwd_min_waves() {
   return HD <= 96 ? 4 : 2;
 }
 
 template <int HD>
+constexpr int fwd_table_bufs() {
+  constexpr int kLds = 160 * 1024, kTab = kTQ * kSRow * 4, kVt = HD * kVRow * 2;
+  return 2 * (2 * kTab + kVt) <= kLds ? 2 : (2 * (kTab + kVt) <= kLds ? 1 : 2);
+}
+
+template <int HD>
 __global__ __launch_bounds__(kThreads, fwd_min_waves<HD>()) void dsa3d_fwd_tiled_kernel(
     Args a, bf16* __restrict__ out, float* __restrict__ lse) {
-  __shared__ __attribute__((aligned(16))) float s_tab[2][kTQ * kSRow];  // S, then A (2 buffers)
+  constexpr int NB = fwd_table_bufs<HD>();
+  __shared__ __attribute__((aligned(16))) float s_tab[NB][kTQ * kSRow];  // S, then A
   __shared__ __attribute__((aligned(16))) uint16_t s_vt[HD * kVRow];    // V^T chunk
   __shared__ int s_red[kWaves][6];
 
@@ -56,19 +65,16 @@ __global__ __launch_bounds__(kThreads, fwd_min_waves<HD>()) void dsa3d_fwd_tiled
 #pragma unroll
   for (int i = 0; i < kSlots; ++i) sc[i] = 0.0f;
   TableRows<HD> rows;
-  if (nit > 0) load_table_rows<HD>(a, tl, make_chunk(box, 0), box.zlo, a.k, a.ks, rows);
+  Walk w = walk_begin(box);
+  if (nit > 0) load_table_rows<HD>(a, tl, w.c, w.z, a.k, a.ks, rows);
   for (int it = 0; it < nit; ++it) {
-    const int zi = uniform_div(it, nchunks);
-    const int z = box.zlo + zi;
-    const Chunk c = make_chunk(box, it - zi * nchunks);
-    // buffer it & 1 was last read for plane it - 2, before the previous barrier
-    float* tab = s_tab[it & 1];
+    const Walk wn = walk_next(box, w);
+    const Chunk& c = w.c;
+    const int z = w.z;
+    // buffer it % NB was last read for step it - NB, before the previous barrier
+    float* tab = s_tab[it % NB];
     store_table<HD>(tl, c, qx, rows, tab);
-    if (it + 1 < nit) {
-      const int zn = uniform_div(it + 1, nchunks);
-      load_table_rows<HD>(a, tl, make_chunk(box, it + 1 - zn * nchunks), box.zlo + zn, a.k, a.ks,
-                          rows);
-    }
+    if (it + 1 < nit) load_table_rows<HD>(a, tl, wn.c, wn.z, a.k, a.ks, rows);
     __syncthreads();
     // every slot reads its corners (in-bounds for any slot); misses are discarded
     const float* my_row = &tab[tl.q * kSRow];
@@ -82,6 +88,8 @@ __global__ __launch_bounds__(kThreads, fwd_min_waves<HD>()) void dsa3d_fwd_tiled
       const float v = bilerp(sl[i], t[i][0], t[i][1], t[i][2], t[i][3]).val;
       sc[i] = hit ? __builtin_fmaf(wz, v, sc[i]) : sc[i];
     }
+    if constexpr (NB == 1) __syncthreads();  // the next step overwrites the table
+    w = wn;
   }
 
   // ---- softmax over each query's taps (32 lanes x kSlots) -------------------
@@ -115,24 +123,21 @@ __global__ __launch_bounds__(kThreads, fwd_min_waves<HD>()) void dsa3d_fwd_tiled
   const int ct = tl.wave % CT, half = tl.wave / CT;
   f32x4_t oacc = {0.0f, 0.0f, 0.0f, 0.0f};
   StageRows<kThreads, HD> vr;
-  if (nit > 0)
-    load_stage_rows<kThreads, HD>(a, tl, make_chunk(box, 0), box.zlo, a.v, a.vs, tl.head * HD, vr);
+  w = walk_begin(box);
+  if (nit > 0) load_stage_rows<kThreads, HD>(a, tl, w.c, w.z, a.v, a.vs, tl.head * HD, vr);
   __syncthreads();  // pass-1 reads of both buffers are done
   zero_table(s_tab[0], kChunkNV);
   for (int it = 0; it < nit; ++it) {
-    const int zi = uniform_div(it, nchunks);
-    const int z = box.zlo + zi;
-    const Chunk c = make_chunk(box, it - zi * nchunks);
-    // A in fixed point (scale 2^30), buffer it & 1: zeroed during the previous plane
-    int* const s_atab = reinterpret_cast<int*>(s_tab[it & 1]);
+    const Walk wn = walk_next(box, w);
+    const Chunk& c = w.c;
+    const int z = w.z;
+    // A in fixed point (scale 2^30), buffer it % NB: zeroed during the previous step
+    int* const s_atab = reinterpret_cast<int*>(s_tab[it % NB]);
     int* row = &s_atab[tl.q * kSRow];
-    __syncthreads();  // the previous plane's MFMAs are done with V^T; this buffer is zeroed
+    __syncthreads();  // the previous step's MFMAs are done with V^T; this buffer is zeroed
     store_stage<kThreads, HD>(c, vr, s_vt);
-    if (it + 1 < nit) {
-      const int zn = uniform_div(it + 1, nchunks);
-      load_stage_rows<kThreads, HD>(a, tl, make_chunk(box, it + 1 - zn * nchunks), box.zlo + zn,
-                                    a.v, a.vs, tl.head * HD, vr);
-    }
+    if (it + 1 < nit)
+      load_stage_rows<kThreads, HD>(a, tl, wn.c, wn.z, a.v, a.vs, tl.head * HD, vr);
 #pragma unroll
     for (int i = 0; i < kSlots; ++i) {
       float wz, dwz;
@@ -156,8 +161,11 @@ __global__ __launch_bounds__(kThreads, fwd_min_waves<HD>()) void dsa3d_fwd_tiled
         oacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv, oacc, 0, 0, 0);
       }
     }
-    // the other buffer was last read for the previous plane, before the barrier above
-    if (it + 1 < nit) zero_table(s_tab[(it + 1) & 1], kChunkNV);
+    // the next buffer was last read for step it + 1 - NB, before the barrier
+    // above (with one buffer: this step, so wait for every wave's MFMAs first)
+    if constexpr (NB == 1) __syncthreads();
+    if (it + 1 < nit) zero_table(s_tab[(it + 1) % NB], kChunkNV);
+    w = wn;
   }
   __syncthreads();
   // oacc[r] = partial O[query 4*(lane/16) + r][channel 16*ct + lane%16] in
@@ -243,23 +251,21 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p1_kernel(
     s_[i] = dp_[i] = gxs[i] = gxd[i] = gys[i] = gyd[i] = gzs[i] = gzd[i] = 0.0f;
   // K and V rows of the next (plane, chunk) are loaded while the current one is used
   TableRows<HD> rk, rv;
+  Walk w = walk_begin(box);
   if (nit > 0) {
-    const Chunk c0 = make_chunk(box, 0);
-    load_table_rows<HD>(a, tl, c0, box.zlo, a.k, a.ks, rk);
-    load_table_rows<HD>(a, tl, c0, box.zlo, a.v, a.vs, rv);
+    load_table_rows<HD>(a, tl, w.c, w.z, a.k, a.ks, rk);
+    load_table_rows<HD>(a, tl, w.c, w.z, a.v, a.vs, rv);
   }
   for (int it = 0; it < nit; ++it) {
-    const int zi = uniform_div(it, nchunks);
-    const int z = box.zlo + zi;
-    const Chunk c = make_chunk(box, it - zi * nchunks);
-    // buffer it & 1 was last read for plane it - 2, before the previous barrier
+    const Walk wn = walk_next(box, w);
+    const Chunk& c = w.c;
+    const int z = w.z;
+    // buffer it & 1 was last read for step it - 2, before the previous barrier
     store_table<HD>(tl, c, qx, rk, s_t0[it & 1]);
     store_table<HD>(tl, c, gx, rv, s_t1[it & 1]);
     if (it + 1 < nit) {
-      const int zn = uniform_div(it + 1, nchunks);
-      const Chunk cn = make_chunk(box, it + 1 - zn * nchunks);
-      load_table_rows<HD>(a, tl, cn, box.zlo + zn, a.k, a.ks, rk);
-      load_table_rows<HD>(a, tl, cn, box.zlo + zn, a.v, a.vs, rv);
+      load_table_rows<HD>(a, tl, wn.c, wn.z, a.k, a.ks, rk);
+      load_table_rows<HD>(a, tl, wn.c, wn.z, a.v, a.vs, rv);
     }
     __syncthreads();
     // every slot reads its corners (in-bounds for any slot); misses are discarded
@@ -286,6 +292,7 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p1_kernel(
       gyd[i] = __builtin_fmaf(wz, dy, gyd[i]);
       gzd[i] = __builtin_fmaf(dwz, dv, gzd[i]);
     }
+    w = wn;
   }
 
   // p = exp(scale * s - lse), ds = p (dp - Delta).  The coordinate gradient of
@@ -413,12 +420,12 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
 #pragma unroll
   for (int j = 0; j < NDQ; ++j) dq_acc[j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
   StageRows<kThreads, CW> kr;
-  if (nit > 0)
-    load_stage_rows<kThreads, CW>(a, tl, make_chunk(box, 0), box.zlo, a.k, a.ks, cw0, kr);
+  Walk w = walk_begin(box);
+  if (nit > 0) load_stage_rows<kThreads, CW>(a, tl, w.c, w.z, a.k, a.ks, cw0, kr);
   for (int it = 0; it < nit; ++it) {
-    const int zi = uniform_div(it, nchunks);
-    const int z = box.zlo + zi;
-    const Chunk c = make_chunk(box, it - zi * nchunks);
+    const Walk wn = walk_next(box, w);
+    const Chunk& c = w.c;
+    const int z = w.z;
     // zero the transposed A and B tables; token rows of the chunk's voxels
     for (int e = threadIdx.x; e < c.nvp * kP2Row / 4; e += kThreads) {
       const u32x4_t zz = {0u, 0u, 0u, 0u};
@@ -428,11 +435,7 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
     for (int vi = threadIdx.x; vi < c.nv; vi += kThreads)
       s_rows[vi] = static_cast<int>(chunk_row(a, tl, c, z, vi) - tl.sample0);
     store_stage<kThreads, CW>(c, kr, s_kt);
-    if (it + 1 < nit) {
-      const int zn = uniform_div(it + 1, nchunks);
-      load_stage_rows<kThreads, CW>(a, tl, make_chunk(box, it + 1 - zn * nchunks), box.zlo + zn,
-                                    a.k, a.ks, cw0, kr);
-    }
+    if (it + 1 < nit) load_stage_rows<kThreads, CW>(a, tl, wn.c, wn.z, a.k, a.ks, cw0, kr);
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < kP2Slots; ++i) {
@@ -513,6 +516,7 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
       }
     }
     __syncthreads();
+    w = wn;
   }
   // dq_acc[j][r] = dq[query 16*fq + 4*(lane/16) + r][channel 16*ct + lane%16]
 #pragma unroll

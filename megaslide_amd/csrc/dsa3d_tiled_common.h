@@ -297,6 +297,33 @@ __device__ __forceinline__ Chunk make_chunk(const Box& box, int id) {
   return c;
 }
 
+// Walk over the (plane, chunk) pairs of a box, chunk-major: every plane of
+// chunk 0, then of chunk 1, ...  A tap's corners lie in one chunk and its two
+// planes are consecutive steps, and the chunk geometry is rebuilt only when the
+// walk moves to the next chunk (usually never: most boxes are one chunk).
+struct Walk {
+  Chunk c;
+  int z;
+};
+
+__device__ __forceinline__ Walk walk_begin(const Box& box) {
+  Walk w;
+  w.c = make_chunk(box, 0);
+  w.z = box.zlo;
+  return w;
+}
+
+__device__ __forceinline__ Walk walk_next(const Box& box, const Walk& w) {
+  Walk n = w;
+  if (w.z < box.zhi) {
+    n.z = w.z + 1;
+  } else {
+    n.c = make_chunk(box, w.c.id + 1);
+    n.z = box.zlo;
+  }
+  return n;
+}
+
 // Token row of voxel vi (< nv) of chunk c in plane z.
 __device__ __forceinline__ int64_t chunk_row(const Args& a, const Tile& tl, const Chunk& c, int z,
                                              int vi) {
