@@ -350,7 +350,8 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
   __shared__ __attribute__((aligned(16))) int s_at[kChunkNV * kP2Row];  // A^T = p w (fixed point)
   __shared__ __attribute__((aligned(16))) int s_bt[kChunkNV * kP2Row];  // B^T = ds scale w (fixed point)
   __shared__ __attribute__((aligned(16))) uint16_t s_kt[CW * kVRow];    // K^T chunk
-  __shared__ __attribute__((aligned(16))) int s_rows[kChunkNV];         // token row (within the sample) per voxel
+  // per voxel: element offset (token row within the sample times D) of its accumulator row
+  __shared__ __attribute__((aligned(16))) int s_rows[kChunkNV];
   __shared__ int s_red[kWaves][6];
   __shared__ __attribute__((aligned(16))) float s_binv[kP2Q];  // per query: 1 / fixed-point scale of B
   // the tile's q and dO rows of this window, transposed: [tensor][channel][query]
@@ -433,7 +434,7 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
       __builtin_memcpy(&s_bt[4 * e], &zz, sizeof(zz));
     }
     for (int vi = threadIdx.x; vi < c.nv; vi += kThreads)
-      s_rows[vi] = static_cast<int>(chunk_row(a, tl, c, z, vi) - tl.sample0);
+      s_rows[vi] = static_cast<int>(chunk_row(a, tl, c, z, vi) - tl.sample0) * D;
     store_stage<kThreads, CW>(c, kr, s_kt);
     if (it + 1 < nit) load_stage_rows<kThreads, CW>(a, tl, wn.c, wn.z, a.k, a.ks, cw0, kr);
     __syncthreads();
@@ -500,6 +501,11 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
                                                      gTf, dv, 0, 0, 0);
       }
       const int ch2 = cw0 + och;
+      // accumulator rows of this sample: a wave-uniform base plus a 32-bit lane
+      // byte offset (the host admits N * D < 2^30), so the atomics use scalar-base
+      // addressing; untouched voxels (exact zeros) send nothing
+      char* const dk_s = reinterpret_cast<char*>(dk_acc + tl.sample0 * D);
+      char* const dv_s = reinterpret_cast<char*>(dv_acc + tl.sample0 * D);
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         // registers 4g + i: voxel 32*vb + 8*g + 4*(lane/32) + i
@@ -508,10 +514,11 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
         __builtin_memcpy(rr, &s_rows[v0], sizeof(rr));
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          if (v0 + i >= c.nv) continue;
-          const int64_t off = (tl.sample0 + rr[i]) * D + ch2;
-          if (dk[4 * g + i] != 0.0f) atomicAdd(dk_acc + off, dk[4 * g + i]);
-          if (dv[4 * g + i] != 0.0f) atomicAdd(dv_acc + off, dv[4 * g + i]);
+          const bool in = v0 + i < c.nv;
+          const uint32_t off = static_cast<uint32_t>(rr[i] + ch2) * 4u;
+          const float kv = dk[4 * g + i], vv = dv[4 * g + i];
+          if (in && kv != 0.0f) atomicAdd(reinterpret_cast<float*>(dk_s + off), kv);
+          if (in && vv != 0.0f) atomicAdd(reinterpret_cast<float*>(dv_s + off), vv);
         }
       }
     }
@@ -607,6 +614,9 @@ bool dsa3d_tiled_supported(const msd_dsa3d_desc& d, const void* q, const void* k
   if (tiles > 0x7fffffff || d.num_heads > 65535) return false;
   // 16-byte vector loads of q/k/v rows
   if ((d.q_stride % 8) || (d.k_stride % 8) || (d.v_stride % 8)) return false;
+  // the dK/dV accumulator rows of a sample are addressed with 32-bit byte offsets
+  if (static_cast<int64_t>(d.T) * d.H * d.W * d.num_heads * d.head_dim >= (int64_t{1} << 30))
+    return false;
   // K/V chunk rows are addressed as a 64-bit chunk base plus a 32-bit lane byte
   // offset (24-bit multiplies): kChunk * (W + 1) rows must span < 2^31 bytes
   for (const int64_t st : {d.k_stride, d.v_stride})
