@@ -644,15 +644,27 @@ hipError_t launch_dsa3d_fwd_tiled(const msd_dsa3d_desc& d, const void* q, const 
 }
 
 namespace {
-// fp32 accumulator [rows, D] -> bf16 destination with token stride `stride`.
-__global__ __launch_bounds__(256) void acc_to_bf16_kernel(const float* __restrict__ src,
-                                                          bf16* __restrict__ dst, int64_t rows,
-                                                          int D, int64_t stride) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i >= rows * D) return;
-  const int64_t r = i / D;
-  const int c = static_cast<int>(i - r * D);
-  dst[r * stride + c] = from_f32<bf16>(src[i]);
+// fp32 dK (blockIdx.y 0) or dV (1) accumulator [rows, D] -> bf16 with its token
+// stride, 8 channels per thread (two 16-byte loads, one 16-byte store; D and
+// the strides are multiples of 8, rows * D < 2^30).
+__global__ __launch_bounds__(256) void acc_to_bf16_kernel(const float* __restrict__ dk_acc,
+                                                          const float* __restrict__ dv_acc,
+                                                          bf16* __restrict__ dk,
+                                                          bf16* __restrict__ dv, int rows, int D,
+                                                          int64_t ks, int64_t vs) {
+  const int d8 = D / 8;
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= rows * d8) return;
+  const int r = i / d8, c = 8 * (i - r * d8);
+  const bool is_k = blockIdx.y == 0;
+  const float* src = (is_k ? dk_acc : dv_acc) + static_cast<int64_t>(r) * D + c;
+  bf16* dst = (is_k ? dk : dv) + static_cast<int64_t>(r) * (is_k ? ks : vs) + c;
+  f32x4_t x[2];
+  __builtin_memcpy(x, src, sizeof(x));
+  uint16_t h[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) h[j] = from_f32<bf16>(x[j / 4][j % 4]).bits;
+  __builtin_memcpy(dst, h, sizeof(h));
 }
 }  // namespace
 
@@ -710,11 +722,10 @@ hipError_t launch_dsa3d_bwd_tiled(const msd_dsa3d_desc& d, const void* q, const 
     default:
       return hipErrorInvalidValue;
   }
-  const dim3 cgrid(static_cast<unsigned>((rows * D + 255) / 256));
-  hipLaunchKernelGGL(acc_to_bf16_kernel, cgrid, dim3(256), 0, s, dk_acc, static_cast<bf16*>(dk),
-                     rows, D, d.k_stride);
-  hipLaunchKernelGGL(acc_to_bf16_kernel, cgrid, dim3(256), 0, s, dv_acc, static_cast<bf16*>(dv),
-                     rows, D, d.v_stride);
+  const dim3 cgrid(static_cast<unsigned>((rows * (D / 8) + 255) / 256), 2);
+  hipLaunchKernelGGL(acc_to_bf16_kernel, cgrid, dim3(256), 0, s, dk_acc, dv_acc,
+                     static_cast<bf16*>(dk), static_cast<bf16*>(dv), static_cast<int>(rows), D,
+                     d.k_stride, d.v_stride);
   return hipGetLastError();
 }
 
