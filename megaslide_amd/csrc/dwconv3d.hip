@@ -433,6 +433,106 @@ __global__ __launch_bounds__(64 * kRowWaves) void dwconv_dw_block_kernel(ConvArg
   if (dt == 0 && sb != 0.0f) atomicAdd(acc + static_cast<int64_t>(K) * a.C + c, sb);
 }
 
+// bf16 x and dz: the same walk with the sums over W taken two outputs at a
+// time, sum_j dz[j] x[j+k] as v_dot2 of the packed pairs (dz[j], dz[j+1]) and
+// (x[j+k], x[j+k+1]) (exact bf16 products into fp32); the packed dz block also
+// takes half the registers.
+template <int KH, int KW>
+__global__ __launch_bounds__(64 * kRowWaves) void dwconv_dw_block_dot2_kernel(
+    ConvArgs a, const bf16* __restrict__ x, const bf16* __restrict__ dz, float* __restrict__ acc) {
+  constexpr int R = kDwRows, PH = KH / 2, PW = KW / 2, NX = kRun + KW - 1, JP = kRun / 2;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c = blockIdx.y * 64 + lane;
+  const int dt = blockIdx.z;
+  const int hblocks = (a.H + R - 1) / R;
+  const int strips_per_frame = (hblocks + kDwStripBlocks - 1) / kDwStripBlocks;
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * kRowWaves + wave;  // (b, t, strip)
+  const int64_t items = static_cast<int64_t>(a.B) * a.T * strips_per_frame;
+  if (item >= items) return;
+  const int strip = static_cast<int>(item % strips_per_frame);
+  const int64_t bt = item / strips_per_frame;
+  const int t = static_cast<int>(bt % a.T);
+  const int b = static_cast<int>(bt / a.T);
+  const int tt = t + dt - a.kt / 2;
+  const bool plane_ok = tt >= 0 && tt < a.T;
+  if (!plane_ok && dt != 0) return;  // no taps; the dt == 0 threads still sum dz for the bias
+  const bool c_ok = c < a.C;
+  const uint32_t lc = c_ok ? c : a.C - 1;
+  const int K = a.kt * KH * KW;
+  const int64_t rowstride = static_cast<int64_t>(a.W) * a.C;
+  float s[KH][KW];
+#pragma unroll
+  for (int dh = 0; dh < KH; ++dh)
+#pragma unroll
+    for (int k = 0; k < KW; ++k) s[dh][k] = 0.0f;
+  float sb = 0.0f;
+  const bf16* plane = x + (static_cast<int64_t>(b) * a.T + (plane_ok ? tt : 0)) * a.H * rowstride;
+  const bf16* gplane = dz + (static_cast<int64_t>(b) * a.T + t) * a.H * rowstride;
+  const int hb_end = min(hblocks, (strip + 1) * kDwStripBlocks);
+  for (int hb = strip * kDwStripBlocks; hb < hb_end; ++hb) {
+    const int h0 = hb * R;
+    for (int w0 = 0; w0 < a.W; w0 += kRun) {
+      uint32_t gp[R][JP];  // (dz[2jp], dz[2jp+1]) of row r, packed bf16
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int h = h0 + r;
+#pragma unroll
+        for (int jp = 0; jp < JP; ++jp) {
+          uint32_t lo = 0u, hi = 0u;
+          if (h < a.H) {
+            const bf16* grow = gplane + h * rowstride;
+            const int w = w0 + 2 * jp;
+            const int wl = min(w, a.W - 1), wh = min(w + 1, a.W - 1);
+            lo = w < a.W ? ldu_bits(grow + static_cast<int64_t>(wl) * a.C, lc) : 0u;
+            hi = w + 1 < a.W ? ldu_bits(grow + static_cast<int64_t>(wh) * a.C, lc) : 0u;
+          }
+          gp[r][jp] = lo | (hi << 16);
+          if (dt == 0) sb += __uint_as_float(lo << 16) + __uint_as_float(hi << 16);
+        }
+      }
+      if (!plane_ok) continue;
+#pragma unroll
+      for (int ii = 0; ii < R + KH - 1; ++ii) {
+        const int hh = h0 + ii - PH;
+        if (hh < 0 || hh >= a.H) continue;
+        const bf16* row = plane + hh * rowstride;
+        uint32_t xb[NX];
+#pragma unroll
+        for (int j = 0; j < NX; ++j) {
+          const int ww = w0 + j - PW;
+          const int wc = min(max(ww, 0), a.W - 1);
+          const uint32_t v = ldu_bits(row + static_cast<int64_t>(wc) * a.C, lc);
+          xb[j] = ww == wc ? v : 0u;
+        }
+        uint32_t xp[NX - 1];
+#pragma unroll
+        for (int m = 0; m < NX - 1; ++m) xp[m] = xb[m] | (xb[m + 1] << 16);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const int dh = ii - r;
+          if (dh < 0 || dh >= KH) continue;
+#pragma unroll
+          for (int k = 0; k < KW; ++k) {
+            float part = 0.0f;
+#pragma unroll
+            for (int jp = 0; jp < JP; ++jp) part = dot2_bf16(gp[r][jp], xp[2 * jp + k], part);
+            s[dh][k] += part;
+          }
+        }
+      }
+    }
+  }
+  if (!c_ok) return;
+  float* __restrict__ ac = acc + static_cast<int64_t>(dt * KH * KW) * a.C + c;
+#pragma unroll
+  for (int dh = 0; dh < KH; ++dh)
+#pragma unroll
+    for (int k = 0; k < KW; ++k)
+      if (s[dh][k] != 0.0f) atomicAdd(ac + static_cast<int64_t>(dh * KW + k) * a.C, s[dh][k]);
+  if (dt == 0 && sb != 0.0f) atomicAdd(acc + static_cast<int64_t>(K) * a.C + c, sb);
+}
+
 // ---------------------------------------------------------------------------
 // weight / bias gradient
 // ---------------------------------------------------------------------------
@@ -673,8 +773,12 @@ void launch_dw_block(const ConvArgs& a, const T* x, const G* dz, float* acc, hip
   const int64_t items = static_cast<int64_t>(a.B) * a.T * strips;
   const dim3 grid(static_cast<unsigned>((items + kRowWaves - 1) / kRowWaves),
                   static_cast<unsigned>((a.C + 63) / 64), static_cast<unsigned>(a.kt));
-  hipLaunchKernelGGL((dwconv_dw_block_kernel<T, G, KS, KS>), grid, dim3(64 * kRowWaves), 0, s, a, x,
-                     dz, acc);
+  if constexpr (std::is_same<T, bf16>::value && std::is_same<G, bf16>::value)
+    hipLaunchKernelGGL((dwconv_dw_block_dot2_kernel<KS, KS>), grid, dim3(64 * kRowWaves), 0, s, a,
+                       x, dz, acc);
+  else
+    hipLaunchKernelGGL((dwconv_dw_block_kernel<T, G, KS, KS>), grid, dim3(64 * kRowWaves), 0, s, a,
+                       x, dz, acc);
 }
 
 template <typename T, typename G>
