@@ -33,7 +33,7 @@ constexpr int kRun = 16;        // outputs per thread along W
 constexpr int kRowWaves = 4;    // waves per block in the row kernels
 constexpr int kStripRows = 8;   // (b, t, h) rows per weight-gradient work item
 
-enum Epilogue { kPlain = 0, kGelu = 1, kGeluGrad = 2 };
+enum Epilogue { kPlain = 0, kGelu = 1, kGeluGrad = 2, kGeluGradT = 3 };
 
 // ---------------------------------------------------------------------------
 // row kernels: forward, GELU-gradient recompute, input gradient
@@ -41,7 +41,8 @@ enum Epilogue { kPlain = 0, kGelu = 1, kGeluGrad = 2 };
 
 // out[p] = epilogue(sum_tap w[tap'] in[p + tap - pad]) with tap' = tap, or the
 // mirrored tap K-1-tap when flip (input gradient of the convolution).
-// mode kGeluGrad writes dz = dy * gelu'(z) as fp32 into out_f32.
+// mode kGeluGrad writes dz = dy * gelu'(z) as fp32 into out_f32, kGeluGradT in
+// the element type into out.
 template <typename T, typename G, int KW, int MODE>
 __global__ __launch_bounds__(64 * kRowWaves) void dwconv_rows_kernel(
     ConvArgs a, const G* __restrict__ in, const T* __restrict__ wt, const T* __restrict__ bias,
@@ -104,6 +105,7 @@ __global__ __launch_bounds__(64 * kRowWaves) void dwconv_rows_kernel(
     if (MODE == kPlain) st(out, i, acc[r]);
     if (MODE == kGelu) st(out, i, gelu_erf(acc[r]));
     if (MODE == kGeluGrad) out_f32[i] = ld(dy, i) * gelu_erf_grad(acc[r]);
+    if (MODE == kGeluGradT) st(out, i, ld(dy, i) * gelu_erf_grad(acc[r]));
   }
 }
 
@@ -221,6 +223,7 @@ __global__ __launch_bounds__(64 * kRowWaves) void dwconv_block_kernel(
       if (MODE == kPlain) stu(out + i0, lc, acc[r][j]);
       if (MODE == kGelu) stu(out + i0, lc, gelu_erf(acc[r][j]));
       if (MODE == kGeluGrad) out_f32[i0 + lc] = ldu(dy + i0, lc) * gelu_erf_grad(acc[r][j]);
+      if (MODE == kGeluGradT) stu(out + i0, lc, ldu(dy + i0, lc) * gelu_erf_grad(acc[r][j]));
     }
   }
 }
@@ -336,6 +339,7 @@ __global__ __launch_bounds__(64 * kRowWaves) void dwconv_block_dot2_kernel(
       if (MODE == kPlain) stu(out + i0, lc, acc[r][j]);
       if (MODE == kGelu) stu(out + i0, lc, gelu_erf(acc[r][j]));
       if (MODE == kGeluGrad) out_f32[i0 + lc] = ldu(dy + i0, lc) * gelu_erf_grad(acc[r][j]);
+      if (MODE == kGeluGradT) stu(out + i0, lc, ldu(dy + i0, lc) * gelu_erf_grad(acc[r][j]));
     }
   }
 }
@@ -642,6 +646,7 @@ __global__ __launch_bounds__(256) void dwconv_simple_kernel(ConvArgs a, const G*
   if (MODE == kPlain) st(out, i, acc);
   if (MODE == kGelu) st(out, i, gelu_erf(acc));
   if (MODE == kGeluGrad) out_f32[i] = ld(dy, i) * gelu_erf_grad(acc);
+  if (MODE == kGeluGradT) st(out, i, ld(dy, i) * gelu_erf_grad(acc));
 }
 
 constexpr int kChunk = 512;
@@ -842,11 +847,22 @@ hipError_t bwd_typed(const msd_dwconv3d_desc& d, const void* x, const void* w, c
   const int64_t nacc = static_cast<int64_t>(a.C) * (K + 1);
   if (d.act == 1) {
     float* dz = acc + ((nacc + 63) / 64) * 64;
-    hipError_t e = run_conv<T, T, kGeluGrad>(a, static_cast<const T*>(x), static_cast<const T*>(w),
-                                             static_cast<const T*>(b), static_cast<const T*>(dy),
-                                             nullptr, dz, 0, s);
-    if (e != hipSuccess) return e;
-    return bwd_grads<T, float>(a, x, w, dz, dx, dw, db, acc, s);
+    if constexpr (std::is_same<T, bf16>::value) {
+      // bf16 storage: dz rounded to bf16 as the framework's bf16 GELU backward
+      // leaves it, which lets both gradient convs take the bf16 dot2 kernels
+      bf16* dzb = reinterpret_cast<bf16*>(dz);
+      hipError_t e = run_conv<T, T, kGeluGradT>(a, static_cast<const T*>(x),
+                                                static_cast<const T*>(w), static_cast<const T*>(b),
+                                                static_cast<const T*>(dy), dzb, nullptr, 0, s);
+      if (e != hipSuccess) return e;
+      return bwd_grads<T, T>(a, x, w, dzb, dx, dw, db, acc, s);
+    } else {
+      hipError_t e = run_conv<T, T, kGeluGrad>(a, static_cast<const T*>(x),
+                                               static_cast<const T*>(w), static_cast<const T*>(b),
+                                               static_cast<const T*>(dy), nullptr, dz, 0, s);
+      if (e != hipSuccess) return e;
+      return bwd_grads<T, float>(a, x, w, dz, dx, dw, db, acc, s);
+    }
   }
   return bwd_grads<T, T>(a, x, w, static_cast<const T*>(dy), dx, dw, db, acc, s);
 }
