@@ -17,9 +17,11 @@ tap); k_proj.bias, whose gradient is zero by the softmax's shift invariance, is
 checked against the scale of the k_proj.weight gradient instead.
 """
 
+import math
 import numpy as np
 import pytest
 import torch
+import torch.nn.functional as F
 
 from goldens import C1, CASES, load, regenerate, rel_err
 from oracle.dsa3d_ref import PARAM_NAMES, dsa3d_core_ref, dsa3d_module_ref
@@ -294,3 +296,63 @@ def test_tiled_rejects_ineligible_calls():
     off = torch.zeros(1, 8, 27 * 3, device=DEV, dtype=torch.bfloat16)
     with pytest.raises(RuntimeError, match="tiled"):
         core()(q, q, q, off, (2, 2, 2), 1, (3, 3, 3), algo="tiled")
+
+
+@pytest.mark.parametrize("D,nh", [(256, 4), (192, 2)])
+def test_module_bf16_tiled_matches_oracle(D, nh):
+    """Whole module in bf16 (matrix-core attention kernels, bf16 dwconvs, bf16
+    GEMMs) on a non-tile-aligned grid, with offsets from an offset net whose
+    bias ~ U(-4, 4) voxels as in the DiT-block configuration, against the fp32
+    oracle module on the same bf16-rounded parameters and inputs.
+
+    Sampling is piecewise linear in the offsets, so the oracle must sample at
+    the offsets the bf16 module used: fp32 offsets differ from them by ~0.01
+    voxels, which moves a few percent of the taps across a lattice line or the
+    border clamp and changes their offset gradient by O(1).  The oracle
+    therefore runs the attention with the module's bf16 offsets injected and
+    chains the offset gradient it returns through its own fp32 offset net.
+    """
+    from megaslide_amd import DeformableSlideAttention3D, dwconv3d
+    from oracle.dsa3d_ref import dsa3d_module_ref, predict_offsets_ref
+    T, H, W, B = 5, 9, 14, 1
+    N = T * H * W
+    print(f"[module bf16] D={D} nh={nh}", flush=True)
+    g = torch.Generator().manual_seed(404 + D)
+    m = DeformableSlideAttention3D(D, nh)
+    with torch.no_grad():
+        for name, prm in m.named_parameters():
+            if name == "offset_net.2.bias":
+                prm.copy_(torch.rand(prm.shape, generator=g) * 8 - 4)
+            elif name.endswith("weight") and prm.dim() >= 2 and "offset_net" not in name \
+                    and "dw_conv" not in name:
+                prm.copy_(torch.randn(prm.shape, generator=g) * (1.0 / math.sqrt(D)))
+            else:
+                prm.copy_(torch.randn(prm.shape, generator=g) * 0.05)
+    m = m.to(DEV, torch.bfloat16)
+    x = torch.randn(B, N, D, generator=g).to(torch.bfloat16)
+    gy = torch.randn(B, N, D, generator=g).to(torch.bfloat16)
+    xd = x.to(DEV).requires_grad_(True)
+    y = m(xd, (T, H, W))
+    y.backward(gy.to(DEV))
+    # the offsets the module sampled at (same kernels and inputs: same bits)
+    with torch.no_grad():
+        on2 = m.offset_net[2]
+        feat = dwconv3d(xd.detach(), m.offset_net[0].weight, m.offset_net[0].bias, (T, H, W),
+                        act="gelu")
+        off_mod = F.linear(feat, on2.weight.view(on2.weight.shape[0], -1), on2.bias)
+    torch.cuda.synchronize()
+    params = {n: prm.detach().float().cpu().requires_grad_(True) for n, prm in m.named_parameters()}
+    xr = x.float().requires_grad_(True)
+    offr = off_mod.float().cpu().requires_grad_(True)
+    yr = dsa3d_module_ref(xr, params, (T, H, W), nh, offsets=offr)
+    yr.backward(gy.float())
+    predict_offsets_ref(xr, params, (T, H, W)).backward(offr.grad)
+    errs = {"y": rel_err(y.detach().float().cpu(), yr.detach()),
+            "dx": rel_err(xd.grad.float().cpu(), xr.grad)}
+    for n, prm in m.named_parameters():
+        if n == "k_proj.bias":  # zero by shift invariance of the softmax
+            continue
+        errs[n] = rel_err(prm.grad.float().cpu(), params[n].grad, floor=1e-2)
+    print("  " + "  ".join(f"{k} {v:.1e}" for k, v in errs.items()), flush=True)
+    for k, e in errs.items():
+        assert e < BF16_TOL, k
