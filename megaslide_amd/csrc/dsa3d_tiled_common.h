@@ -565,17 +565,8 @@ __device__ __forceinline__ bf16x8_t fix_to_bf16x8(const int* p) {
   return __builtin_bit_cast(bf16x8_t, r);
 }
 
-__device__ __forceinline__ bf16x8_t to_bf16x8(const float* p) {
-  u32x4_t r;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const f32x2_t f = {p[2 * i], p[2 * i + 1]};
-    r[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_t));
-  }
-  return __builtin_bit_cast(bf16x8_t, r);
-}
-
-// Same, split into hi + lo bf16 parts (value = hi + lo to ~2^-16 relative).
+// 8 floats as bf16x8, split into hi + lo bf16 parts (value = hi + lo to ~2^-16
+// relative).
 __device__ __forceinline__ void to_bf16x8_hilo(const float* p, bf16x8_t& hi, bf16x8_t& lo) {
   u32x4_t h, l;
 #pragma unroll
