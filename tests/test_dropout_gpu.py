@@ -108,3 +108,32 @@ def test_module_dropout_train_and_eval():
     y1.square().mean().backward()
     for name, prm in m.named_parameters():
         assert prm.grad is not None and torch.isfinite(prm.grad).all(), name
+
+
+def test_module_dropout_with_extra_kv():
+    """extra_kv path: local taps dropped in the kernel, extra keys by torch's
+    dropout; p = 0 in training mode equals eval mode, and p > 0 trains."""
+    from megaslide_amd import DeformableSlideAttention3D
+    torch.manual_seed(3)
+    B, T, H, W, D, nh, G = 1, 3, 5, 6, 128, 2, 8
+    m = DeformableSlideAttention3D(D, nh, dropout=0.0).to(DEV)
+    with torch.no_grad():
+        m.offset_net[2].weight.normal_(0, 0.02)
+    x = torch.randn(B, T * H * W, D, device=DEV)
+    ekv = torch.randn(B, G, D, device=DEV)
+    m.eval()
+    with torch.no_grad():
+        y_eval = m(x, (T, H, W), extra_kv=ekv)
+    m.train()
+    with torch.no_grad():
+        y_train0 = m(x, (T, H, W), extra_kv=ekv)
+    assert torch.equal(y_eval, y_train0)
+    m.dropout.p = 0.3
+    xg = x.clone().requires_grad_(True)
+    eg = ekv.clone().requires_grad_(True)
+    y = m(xg, (T, H, W), extra_kv=eg)
+    assert not torch.equal(y.detach(), y_eval)
+    y.square().mean().backward()
+    assert torch.isfinite(xg.grad).all() and torch.isfinite(eg.grad).all()
+    for name, prm in m.named_parameters():
+        assert prm.grad is not None and torch.isfinite(prm.grad).all(), name
