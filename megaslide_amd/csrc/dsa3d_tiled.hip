@@ -115,13 +115,21 @@ __global__ __launch_bounds__(kThreads, fwd_min_waves<HD>()) void dsa3d_fwd_tiled
   if (lse != nullptr && tl.q_ok && tl.sub == 0) lse[tl.qn * a.nh + tl.head] = mx + logf(den);
 
   // ---- pass 2: O = A . V ------------------------------------------------------
-  // wave w: output channels 16*(w % CT) + [0, 16), voxel k-steps of phase
-  // w / CT out of NH (waves with w >= CT * NH have no A . V work)
-  constexpr int CT = HD / 16;
-  constexpr int NH = (kWaves % CT == 0) ? kWaves / CT : 1;
+  // The waves form CG channel groups of KP waves; wave w of group g takes the
+  // voxel k-steps w % KP, + KP, ... of a step for the TPW channel tiles of
+  // group g: one A operand feeds TPW independent MFMAs, and the KP partial O
+  // are summed once at the end.  hd 64 and 128: one group of 8 waves.  hd 96:
+  // six single-tile groups (waves 6, 7 idle), which stays within 128 registers
+  // and measured faster than groups of several tiles.
+  constexpr int CT = HD / 16, CG = HD == 96 ? CT : 1, TPW = CT / CG;
+  constexpr int KP = HD == 96 ? 1 : kWaves;
+  static_assert(TPW * CG == CT && CG * KP <= kWaves, "channel tiles split over the waves");
   const int mq = tl.lane & 15, kq = 8 * (tl.lane >> 4);
-  const int ct = tl.wave % CT, half = tl.wave / CT;
-  f32x4_t oacc = {0.0f, 0.0f, 0.0f, 0.0f};
+  const int cg = tl.wave / KP, kph = tl.wave % KP;
+  const bool av_wave = tl.wave < CG * KP;
+  f32x4_t oacc[TPW];
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) oacc[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
   StageRows<kThreads, HD> vr;
   w = walk_begin(box);
   if (nit > 0) load_stage_rows<kThreads, HD>(a, tl, w.c, w.z, a.v, a.vs, tl.head * HD, vr);
@@ -153,12 +161,13 @@ __global__ __launch_bounds__(kThreads, fwd_min_waves<HD>()) void dsa3d_fwd_tiled
       atomicAdd(&row[base + dy + dx], to_fix(pz * (sl[i].fy * sl[i].fx)));
     }
     __syncthreads();
-    if (half < NH) {
-      for (int kc = 32 * half; kc < c.nvp; kc += 32 * NH) {
-        const bf16x8_t av = fix_to_bf16x8(&s_atab[mq * kSRow + kc + kq]);
+    for (int kc = 32 * kph; av_wave && kc < c.nvp; kc += 32 * KP) {
+      const bf16x8_t av = fix_to_bf16x8(&s_atab[mq * kSRow + kc + kq]);
+#pragma unroll
+      for (int t = 0; t < TPW; ++t) {
         bf16x8_t bv;
-        __builtin_memcpy(&bv, &s_vt[(16 * ct + mq) * kVRow + kc + kq], sizeof(bv));
-        oacc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv, oacc, 0, 0, 0);
+        __builtin_memcpy(&bv, &s_vt[(16 * (cg * TPW + t) + mq) * kVRow + kc + kq], sizeof(bv));
+        oacc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv, oacc[t], 0, 0, 0);
       }
     }
     // the next buffer was last read for step it + 1 - NB, before the barrier
@@ -168,28 +177,28 @@ __global__ __launch_bounds__(kThreads, fwd_min_waves<HD>()) void dsa3d_fwd_tiled
     w = wn;
   }
   __syncthreads();
-  // oacc[r] = partial O[query 4*(lane/16) + r][channel 16*ct + lane%16] in
-  // fixed-point units of A; with two phases the second's partial sums are added
-  // through LDS
-  float* red = s_tab[0];  // 16 x HD
-  if constexpr (NH == 2) {
-    if (half == 1) {
+  // oacc[t][r] = wave partial of O[query 4*(lane/16) + r][channel 16*(cg*TPW +
+  // t) + lane%16] in fixed-point units of A.  The V^T buffer (free after the
+  // barrier above) takes the KP partials of every channel; every thread then
+  // sums KP for its outputs, consecutive threads on consecutive channels.
+  float* red = reinterpret_cast<float*>(s_vt);  // [k phase][16][HD]
+  static_assert(KP * kTQ * HD * 4 <= HD * kVRow * 2, "partials fit the V^T buffer");
+  if (av_wave) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) red[(4 * (tl.lane >> 4) + r) * HD + 16 * ct + mq] = oacc[r];
-    }
-    __syncthreads();
+    for (int t = 0; t < TPW; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        red[(kph * kTQ + 4 * (tl.lane >> 4) + r) * HD + 16 * (cg * TPW + t) + mq] = oacc[t][r];
   }
-  if (half == 0) {
+  __syncthreads();
+  for (int e = threadIdx.x; e < kTQ * HD; e += kThreads) {
+    float o = 0.0f;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int m = 4 * (tl.lane >> 4) + r;
-      const int64_t n = tile_row(a, tl, m);
-      float o = oacc[r];
-      if constexpr (NH == 2) o += red[m * HD + 16 * ct + mq];
-      if (n >= 0)
-        out[n * (static_cast<int64_t>(a.nh) * HD) + tl.head * HD + 16 * ct + mq] =
-            from_f32<bf16>(o * kFixAInv);
-    }
+    for (int kp = 0; kp < KP; ++kp) o += red[kp * kTQ * HD + e];
+    const int m = e / HD, ch = e - m * HD;
+    const int64_t n = tile_row(a, tl, m);
+    if (n >= 0)
+      out[n * (static_cast<int64_t>(a.nh) * HD) + tl.head * HD + ch] = from_f32<bf16>(o * kFixAInv);
   }
 }
 
