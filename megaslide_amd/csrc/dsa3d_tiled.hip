@@ -417,11 +417,17 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
   }
   __syncthreads();
 
-  // dq (16x16x32 MFMA): task t = (frame t / CT, channels 16*(t % CT) + [0, 16))
-  // for t = w + 8 j.  dK/dV (32x32x16 MFMA, one per frame): task t = (channels
-  // 32*(t % NC2) + [0, 32), 32-voxel block t / NC2) for t = w + 8 i.
+  // dq (16x16x32 MFMA).  CW = 64: wave w takes frame w / 4 and the voxel
+  // k-steps w % 4, + 4, ... for all CT channel tiles, so one converted B
+  // operand feeds CT MFMA pairs; the 4 partial dq are summed at the end.
+  // Wider windows (registers): task t = (frame t / CT, channels 16*(t % CT) +
+  // [0, 16)) for t = w + 8 j over all k-steps.  dK/dV (32x32x16 MFMA, one per
+  // frame): task t = (channels 32*(t % NC2) + [0, 32), 32-voxel block t / NC2)
+  // for t = w + 8 i.
   constexpr int CT = CW / 16, NC2 = CW / 32;
-  constexpr int NDQ = (kP2Frames * CT + kWaves - 1) / kWaves;  // dq tasks per wave
+  constexpr bool DQK = CW == 64;  // k-split dq
+  constexpr int KPQ = kWaves / kP2Frames;  // k phases per frame (k-split dq)
+  constexpr int NDQ = DQK ? CT : (kP2Frames * CT + kWaves - 1) / kWaves;  // dq accumulators
   const int mq = tl.lane & 15, kq = 8 * (tl.lane >> 4);
   // operands of the dK/dV MFMAs are re-read from LDS where used (registers are
   // the limit here: a spill reload would wait for every outstanding atomic)
@@ -475,21 +481,40 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
     __syncthreads();
     // dq[q] += sum_v B[q][v] K[v]; B as a bf16 hi/lo pair because
     // sum_v B[q][v] = 0 and K may carry a large common part
-#pragma unroll
-    for (int j = 0; j < NDQ; ++j) {
-      const int t = tl.wave + kWaves * j;
-      if (t >= kP2Frames * CT) continue;
-      const int fq = t / CT, ct = t % CT;
-      for (int kc = 0; kc < c.nvp; kc += 32) {
+    if constexpr (DQK) {
+      const int fq = tl.wave / KPQ;
+      for (int kc = 32 * (tl.wave % KPQ); kc < c.nvp; kc += 32 * KPQ) {
         float bq[8];  // fixed-point units; the query's scale is applied to dq at the end
 #pragma unroll
         for (int jj = 0; jj < 8; ++jj)
           bq[jj] = static_cast<float>(s_bt[(kc + kq + jj) * kP2Row + kTQ * fq + mq]);
-        bf16x8_t bhi, blo, kv;
+        bf16x8_t bhi, blo;
         to_bf16x8_hilo(bq, bhi, blo);
-        __builtin_memcpy(&kv, &s_kt[(16 * ct + mq) * kVRow + kc + kq], sizeof(kv));
-        dq_acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bhi, kv, dq_acc[j], 0, 0, 0);
-        dq_acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(blo, kv, dq_acc[j], 0, 0, 0);
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) {
+          bf16x8_t kv;
+          __builtin_memcpy(&kv, &s_kt[(16 * ct + mq) * kVRow + kc + kq], sizeof(kv));
+          dq_acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bhi, kv, dq_acc[ct], 0, 0, 0);
+          dq_acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(blo, kv, dq_acc[ct], 0, 0, 0);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < NDQ; ++j) {
+        const int t = tl.wave + kWaves * j;
+        if (t >= kP2Frames * CT) continue;
+        const int fq = t / CT, ct = t % CT;
+        for (int kc = 0; kc < c.nvp; kc += 32) {
+          float bq[8];  // fixed-point units; the query's scale is applied to dq at the end
+#pragma unroll
+          for (int jj = 0; jj < 8; ++jj)
+            bq[jj] = static_cast<float>(s_bt[(kc + kq + jj) * kP2Row + kTQ * fq + mq]);
+          bf16x8_t bhi, blo, kv;
+          to_bf16x8_hilo(bq, bhi, blo);
+          __builtin_memcpy(&kv, &s_kt[(16 * ct + mq) * kVRow + kc + kq], sizeof(kv));
+          dq_acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bhi, kv, dq_acc[j], 0, 0, 0);
+          dq_acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(blo, kv, dq_acc[j], 0, 0, 0);
+        }
       }
     }
     // dK[v] += sum_q B[q][v] q[q];  dV[v] += sum_q A[q][v] dO[q]  (fp32 atomics;
@@ -534,17 +559,40 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
     __syncthreads();
     w = wn;
   }
-  // dq_acc[j][r] = dq[query 16*fq + 4*(lane/16) + r][channel 16*ct + lane%16]
+  if constexpr (DQK) {
+    // dq_acc[ct][r] = partial dq[query 16*fq + 4*(lane/16) + r][channel 16*ct +
+    // lane%16] of k phase w % 4; the A^T table (free after the loop's last
+    // barrier) takes the partials, and every thread sums 4 for its outputs
+    float* red = reinterpret_cast<float*>(s_at);  // [frame][k phase][16][CW]
+    static_assert(kWaves * kTQ * CW <= kChunkNV * kP2Row, "partials fit the A^T table");
+    const int fq = tl.wave / KPQ, kph = tl.wave % KPQ;
 #pragma unroll
-  for (int j = 0; j < NDQ; ++j) {
-    const int t = tl.wave + kWaves * j;
-    if (t >= kP2Frames * CT) continue;
-    const int fq = t / CT, ct = t % CT;
+    for (int ct = 0; ct < CT; ++ct)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int m = kTQ * fq + 4 * (tl.lane >> 4) + r;
+      for (int r = 0; r < 4; ++r)
+        red[((fq * KPQ + kph) * kTQ + 4 * (tl.lane >> 4) + r) * CW + 16 * ct + mq] = dq_acc[ct][r];
+    __syncthreads();
+    for (int e = threadIdx.x; e < kP2Q * CW; e += kThreads) {
+      const int m = e / CW, ch = e - m * CW, f = m / kTQ, mm = m % kTQ;
+      float v = 0.0f;
+#pragma unroll
+      for (int kp = 0; kp < KPQ; ++kp) v += red[((f * KPQ + kp) * kTQ + mm) * CW + ch];
       const int64_t n = tile_row(a, tl, m);
-      if (n >= 0) dq[n * a.qs + cw0 + 16 * ct + mq] = from_f32<bf16>(dq_acc[j][r] * s_binv[m]);
+      if (n >= 0) dq[n * a.qs + cw0 + ch] = from_f32<bf16>(v * s_binv[m]);
+    }
+  } else {
+    // dq_acc[j][r] = dq[query 16*fq + 4*(lane/16) + r][channel 16*ct + lane%16]
+#pragma unroll
+    for (int j = 0; j < NDQ; ++j) {
+      const int t = tl.wave + kWaves * j;
+      if (t >= kP2Frames * CT) continue;
+      const int fq = t / CT, ct = t % CT;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = kTQ * fq + 4 * (tl.lane >> 4) + r;
+        const int64_t n = tile_row(a, tl, m);
+        if (n >= 0) dq[n * a.qs + cw0 + 16 * ct + mq] = from_f32<bf16>(dq_acc[j][r] * s_binv[m]);
+      }
     }
   }
 }
