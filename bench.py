@@ -218,7 +218,7 @@ def cpu_baseline(slab_T=2):
 PHASE_KERNELS = {  # bench phase -> the kernels its ABI call launches, in order
     "dsa3d_fwd": ["dsa3d_fwd_tiled_kernel"],
     "dsa3d_bwd": ["fill_zero_f32", "dsa3d_bwd_p1_kernel", "dsa3d_bwd_p2_kernel",
-                  "acc_to_bf16_kernel"],
+                  "acc_to_out_kernel"],
 }
 
 

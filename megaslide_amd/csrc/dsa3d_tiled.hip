@@ -1,5 +1,5 @@
-// Matrix-core (tiled) 3D-DSA forward and backward for gfx950: bf16 storage,
-// fp32 accumulation, head_dim 64, 96 or 128.
+// Matrix-core (tiled) 3D-DSA forward and backward for gfx950: bf16 or fp32
+// storage, fp32 accumulation, head_dim 64, 96 or 128.
 //
 // One workgroup = one (batch, head, tile of 16 queries).  Instead of gathering
 // the 8 corner rows of K and V for each of a query's taps, it builds dense
@@ -21,60 +21,72 @@ namespace {
 
 using namespace tiled;
 
-// Minimum waves per SIMD of the forward kernel: two 512-thread workgroups per
-// CU fit in the LDS up to head_dim 96; head_dim 128 stages 66 KB of V^T, so
-// one workgroup per CU, and the register cap is raised to match.
-//
 // The S (pass 1) and A (pass 2) tables are double-buffered where that keeps
 // the workgroups per CU: a step's table is written while the other buffer may
 // still be read for the previous step, so pass 1 needs one barrier per step and
-// pass 2 two (instead of two and three).  head_dim 96 keeps one buffer: two
-// would drop it to one workgroup per CU (measured 30% slower).
-template <int HD>
-constexpr int fwd_min_waves() {
-  return HD <= 96 ? 4 : 2;
+// pass 2 two (instead of two and three).  bf16 head_dim 96 keeps one buffer:
+// two would drop it to one workgroup per CU (measured 30% slower).  bf16
+// head_dim 128 and every fp32 head stage too much V^T for two workgroups per
+// CU; they run one, with the register cap raised to match.
+constexpr int kLdsBytes = 160 * 1024;
+constexpr int kTabBytes = kTQ * kSRow * 4;
+
+template <int HD, typename E>
+constexpr int fwd_vt_bytes() {
+  return HD * ElemT<E>::kRow * static_cast<int>(sizeof(word_t<E>));
 }
 
-template <int HD>
+template <int HD, typename E>
 constexpr int fwd_table_bufs() {
-  constexpr int kLds = 160 * 1024, kTab = kTQ * kSRow * 4, kVt = HD * kVRow * 2;
-  return 2 * (2 * kTab + kVt) <= kLds ? 2 : (2 * (kTab + kVt) <= kLds ? 1 : 2);
+  constexpr int vt = fwd_vt_bytes<HD, E>();
+  if (2 * (2 * kTabBytes + vt) <= kLdsBytes) return 2;  // two workgroups per CU
+  if (2 * (kTabBytes + vt) <= kLdsBytes) return 1;      // two workgroups per CU
+  return 2 * kTabBytes + vt <= kLdsBytes ? 2 : 1;       // one workgroup per CU
 }
 
-template <int HD>
-__global__ __launch_bounds__(kThreads, fwd_min_waves<HD>()) void dsa3d_fwd_tiled_kernel(
-    Args a, bf16* __restrict__ out, float* __restrict__ lse) {
-  constexpr int NB = fwd_table_bufs<HD>();
+// Minimum waves per SIMD: 4 when two 512-thread workgroups fit in a CU's LDS.
+template <int HD, typename E>
+constexpr int fwd_min_waves() {
+  return 2 * (fwd_table_bufs<HD, E>() * kTabBytes + fwd_vt_bytes<HD, E>()) <= kLdsBytes ? 4 : 2;
+}
+
+template <int HD, typename E>
+__global__ __launch_bounds__(kThreads, (fwd_min_waves<HD, E>())) void dsa3d_fwd_tiled_kernel(
+    Args a, E* __restrict__ out, float* __restrict__ lse) {
+  constexpr int NB = fwd_table_bufs<HD, E>();
+  constexpr int VR = ElemT<E>::kRow;
   __shared__ __attribute__((aligned(16))) float s_tab[NB][kTQ * kSRow];  // S, then A
-  __shared__ __attribute__((aligned(16))) uint16_t s_vt[HD * kVRow];    // V^T chunk
+  __shared__ __attribute__((aligned(16))) word_t<E> s_vt[HD * VR];      // V^T chunk
   __shared__ int s_red[kWaves][6];
 
   const Tile tl = make_tile<1, kSubs>(a);
   Slot sl[kSlots];
   Box box;
-  setup_slots<kSubs, kSlots>(a, tl, sl, box, s_red, true);
+  setup_slots<E, kSubs, kSlots>(a, tl, sl, box, s_red, true);
   const int nchunks = box.ncy * box.ncx;
   const int nit = (box.zhi - box.zlo + 1) * nchunks;
+  const E* const kp = static_cast<const E*>(a.k);
+  const E* const vp = static_cast<const E*>(a.v);
 
-  bf16x8_t qx[HD / 32];
-  load_rows_operand<HD>(a, tl, a.q, a.qs, qx);
+  op_t<E> qx[HD / 32];
+  load_rows_operand<HD, E>(a, tl, static_cast<const E*>(a.q), a.qs, qx);
 
   // ---- pass 1: scores -------------------------------------------------------
   // K rows of the next (plane, chunk) are loaded while the current one is used
   float sc[kSlots];
 #pragma unroll
   for (int i = 0; i < kSlots; ++i) sc[i] = 0.0f;
-  TableRows<HD> rows;
+  TableRows<HD, E> rows;
   Walk w = walk_begin(box);
-  if (nit > 0) load_table_rows<HD>(a, tl, w.c, w.z, a.k, a.ks, rows);
+  if (nit > 0) load_table_rows<HD, E>(a, tl, w.c, w.z, kp, a.ks, rows);
   for (int it = 0; it < nit; ++it) {
     const Walk wn = walk_next(box, w);
     const Chunk& c = w.c;
     const int z = w.z;
     // buffer it % NB was last read for step it - NB, before the previous barrier
     float* tab = s_tab[it % NB];
-    store_table<HD>(tl, c, qx, rows, tab);
-    if (it + 1 < nit) load_table_rows<HD>(a, tl, wn.c, wn.z, a.k, a.ks, rows);
+    store_table<HD, E>(tl, c, qx, rows, tab);
+    if (it + 1 < nit) load_table_rows<HD, E>(a, tl, wn.c, wn.z, kp, a.ks, rows);
     __syncthreads();
     // every slot reads its corners (in-bounds for any slot); misses are discarded
     const float* my_row = &tab[tl.q * kSRow];
@@ -118,11 +130,12 @@ __global__ __launch_bounds__(kThreads, fwd_min_waves<HD>()) void dsa3d_fwd_tiled
   // The waves form CG channel groups of KP waves; wave w of group g takes the
   // voxel k-steps w % KP, + KP, ... of a step for the TPW channel tiles of
   // group g: one A operand feeds TPW independent MFMAs, and the KP partial O
-  // are summed once at the end.  hd 64 and 128: one group of 8 waves.  hd 96:
-  // six single-tile groups (waves 6, 7 idle), which stays within 128 registers
-  // and measured faster than groups of several tiles.
-  constexpr int CT = HD / 16, CG = HD == 96 ? CT : 1, TPW = CT / CG;
-  constexpr int KP = HD == 96 ? 1 : kWaves;
+  // are summed once at the end.  hd 64 and 128: one group of 8 waves (fp32
+  // hd 128: two groups of 4, for registers).  hd 96: six single-tile groups
+  // (waves 6, 7 idle), which stays within 128 registers and measured faster
+  // than groups of several tiles.
+  constexpr int CT = HD / 16, CG = HD == 96 ? CT : (sizeof(E) == 4 && HD == 128 ? 2 : 1);
+  constexpr int TPW = CT / CG, KP = HD == 96 ? 1 : kWaves / CG;
   static_assert(TPW * CG == CT && CG * KP <= kWaves, "channel tiles split over the waves");
   const int mq = tl.lane & 15, kq = 8 * (tl.lane >> 4);
   const int cg = tl.wave / KP, kph = tl.wave % KP;
@@ -130,9 +143,9 @@ __global__ __launch_bounds__(kThreads, fwd_min_waves<HD>()) void dsa3d_fwd_tiled
   f32x4_t oacc[TPW];
 #pragma unroll
   for (int t = 0; t < TPW; ++t) oacc[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-  StageRows<kThreads, HD> vr;
+  StageRows<kThreads, HD, E> vr;
   w = walk_begin(box);
-  if (nit > 0) load_stage_rows<kThreads, HD>(a, tl, w.c, w.z, a.v, a.vs, tl.head * HD, vr);
+  if (nit > 0) load_stage_rows<kThreads, HD, E>(a, tl, w.c, w.z, vp, a.vs, tl.head * HD, vr);
   __syncthreads();  // pass-1 reads of both buffers are done
   zero_table(s_tab[0], kChunkNV);
   for (int it = 0; it < nit; ++it) {
@@ -143,9 +156,9 @@ __global__ __launch_bounds__(kThreads, fwd_min_waves<HD>()) void dsa3d_fwd_tiled
     int* const s_atab = reinterpret_cast<int*>(s_tab[it % NB]);
     int* row = &s_atab[tl.q * kSRow];
     __syncthreads();  // the previous step's MFMAs are done with V^T; this buffer is zeroed
-    store_stage<kThreads, HD>(c, vr, s_vt);
+    store_stage<kThreads, HD, E>(c, vr, s_vt);
     if (it + 1 < nit)
-      load_stage_rows<kThreads, HD>(a, tl, wn.c, wn.z, a.v, a.vs, tl.head * HD, vr);
+      load_stage_rows<kThreads, HD, E>(a, tl, wn.c, wn.z, vp, a.vs, tl.head * HD, vr);
 #pragma unroll
     for (int i = 0; i < kSlots; ++i) {
       float wz, dwz;
@@ -162,13 +175,10 @@ __global__ __launch_bounds__(kThreads, fwd_min_waves<HD>()) void dsa3d_fwd_tiled
     }
     __syncthreads();
     for (int kc = 32 * kph; av_wave && kc < c.nvp; kc += 32 * KP) {
-      const bf16x8_t av = fix_to_bf16x8(&s_atab[mq * kSRow + kc + kq]);
+      const op_t<E> av = fix_to_op<E>(&s_atab[mq * kSRow + kc + kq]);
 #pragma unroll
-      for (int t = 0; t < TPW; ++t) {
-        bf16x8_t bv;
-        __builtin_memcpy(&bv, &s_vt[(16 * (cg * TPW + t) + mq) * kVRow + kc + kq], sizeof(bv));
-        oacc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv, oacc[t], 0, 0, 0);
-      }
+      for (int t = 0; t < TPW; ++t)
+        oacc[t] = mma16(av, load_op<E>(&s_vt[(16 * (cg * TPW + t) + mq) * VR + kc + kq]), oacc[t]);
     }
     // the next buffer was last read for step it + 1 - NB, before the barrier
     // above (with one buffer: this step, so wait for every wave's MFMAs first)
@@ -182,7 +192,7 @@ __global__ __launch_bounds__(kThreads, fwd_min_waves<HD>()) void dsa3d_fwd_tiled
   // barrier above) takes the KP partials of every channel; every thread then
   // sums KP for its outputs, consecutive threads on consecutive channels.
   float* red = reinterpret_cast<float*>(s_vt);  // [k phase][16][HD]
-  static_assert(KP * kTQ * HD * 4 <= HD * kVRow * 2, "partials fit the V^T buffer");
+  static_assert(KP * kTQ * HD * 4 <= fwd_vt_bytes<HD, E>(), "partials fit the V^T buffer");
   if (av_wave) {
 #pragma unroll
     for (int t = 0; t < TPW; ++t)
@@ -198,17 +208,18 @@ __global__ __launch_bounds__(kThreads, fwd_min_waves<HD>()) void dsa3d_fwd_tiled
     const int m = e / HD, ch = e - m * HD;
     const int64_t n = tile_row(a, tl, m);
     if (n >= 0)
-      out[n * (static_cast<int64_t>(a.nh) * HD) + tl.head * HD + ch] = from_f32<bf16>(o * kFixAInv);
+      out[n * (static_cast<int64_t>(a.nh) * HD) + tl.head * HD + ch] = from_f32<E>(o * kFixAInv);
   }
 }
 
 // 32 x 16 block vb of a transposed [voxel][query] fixed-point table (row stride
-// `row`, queries from column col0) as the A operand of the 32x32x16 MFMA: lane l
-// holds voxel 32*vb + l%32, queries col0 + 8*(l/32) + j, rounded to bf16 in
-// fixed-point units (the per-query scales ride on the other operand).
-__device__ __forceinline__ bf16x8_t table_t_rows(const int* table_t, int row, int col0, int vb,
-                                                 int lane) {
-  return fix_to_bf16x8(&table_t[(32 * vb + (lane & 31)) * row + col0 + 8 * (lane >> 5)]);
+// `row`, queries from column col0) as the A operand of the 32x32 MFMA: lane l
+// holds voxel 32*vb + l%32, queries col0 + 8*(l/32) + j, in fixed-point units
+// (the per-query scales ride on the other operand).
+template <typename E>
+__device__ __forceinline__ op_t<E> table_t_rows(const int* table_t, int row, int col0, int vb,
+                                                int lane) {
+  return fix_to_op<E>(&table_t[(32 * vb + (lane & 31)) * row + col0 + 8 * (lane >> 5)]);
 }
 
 // First backward kernel (one frame, 16 queries): pass 1 of the backward.  It
@@ -216,10 +227,10 @@ __device__ __forceinline__ bf16x8_t table_t_rows(const int* table_t, int row, in
 // coordinate derivatives, then writes the offset gradients and, for the second
 // kernel, p times its dropout factor and ds * softmax_scale of every tap (fp32,
 // [token][head][tap]).
-template <int HD>
+template <int HD, typename E>
 __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p1_kernel(
-    Args a, const bf16* __restrict__ out, const bf16* __restrict__ dout,
-    const float* __restrict__ lse, const float* __restrict__ dlse, bf16* __restrict__ doff,
+    Args a, const E* __restrict__ out, const E* __restrict__ dout,
+    const float* __restrict__ lse, const float* __restrict__ dlse, E* __restrict__ doff,
     float* __restrict__ p_ws, float* __restrict__ b_ws) {
   // S and dP tables, double-buffered: one barrier per plane
   __shared__ __attribute__((aligned(16))) float s_t0[2][kTQ * kSRow];  // S
@@ -230,13 +241,15 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p1_kernel(
   const int D = a.nh * HD;
   Slot sl[kSlots];
   Box box;
-  setup_slots<kSubs, kSlots>(a, tl, sl, box, s_red, true);
+  setup_slots<E, kSubs, kSlots>(a, tl, sl, box, s_red, true);
   const int nchunks = box.ncy * box.ncx;
   const int nit = (box.zhi - box.zlo + 1) * nchunks;
+  const E* const kp = static_cast<const E*>(a.k);
+  const E* const vp = static_cast<const E*>(a.v);
 
-  bf16x8_t qx[HD / 32], gx[HD / 32];
-  load_rows_operand<HD>(a, tl, a.q, a.qs, qx);
-  load_rows_operand<HD>(a, tl, dout, D, gx);
+  op_t<E> qx[HD / 32], gx[HD / 32];
+  load_rows_operand<HD, E>(a, tl, static_cast<const E*>(a.q), a.qs, qx);
+  load_rows_operand<HD, E>(a, tl, dout, D, gx);
 
   // Delta = dO . O (- dlse) and lse for this lane's query: 32 lanes x HD/32 channels
   constexpr int CPL = HD / kSubs;
@@ -258,23 +271,36 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p1_kernel(
 #pragma unroll
   for (int i = 0; i < kSlots; ++i)
     s_[i] = dp_[i] = gxs[i] = gxd[i] = gys[i] = gyd[i] = gzs[i] = gzd[i] = 0.0f;
-  // K and V rows of the next (plane, chunk) are loaded while the current one is used
-  TableRows<HD> rk, rv;
+  // K and V rows of the next (plane, chunk) are loaded while the current one is
+  // used.  fp32 rows beyond head_dim 64 would spill that way: they are loaded
+  // at the step, one 16-voxel block at a time.
+  constexpr bool kPrefetch = sizeof(E) == 2 || HD == 64;
+  TableRows<HD, E> rk, rv;
   Walk w = walk_begin(box);
-  if (nit > 0) {
-    load_table_rows<HD>(a, tl, w.c, w.z, a.k, a.ks, rk);
-    load_table_rows<HD>(a, tl, w.c, w.z, a.v, a.vs, rv);
+  if (kPrefetch && nit > 0) {
+    load_table_rows<HD, E>(a, tl, w.c, w.z, kp, a.ks, rk);
+    load_table_rows<HD, E>(a, tl, w.c, w.z, vp, a.vs, rv);
   }
   for (int it = 0; it < nit; ++it) {
     const Walk wn = walk_next(box, w);
     const Chunk& c = w.c;
     const int z = w.z;
     // buffer it & 1 was last read for step it - 2, before the previous barrier
-    store_table<HD>(tl, c, qx, rk, s_t0[it & 1]);
-    store_table<HD>(tl, c, gx, rv, s_t1[it & 1]);
-    if (it + 1 < nit) {
-      load_table_rows<HD>(a, tl, wn.c, wn.z, a.k, a.ks, rk);
-      load_table_rows<HD>(a, tl, wn.c, wn.z, a.v, a.vs, rv);
+    if constexpr (kPrefetch) {
+      store_table<HD, E>(tl, c, qx, rk, s_t0[it & 1]);
+      store_table<HD, E>(tl, c, gx, rv, s_t1[it & 1]);
+      if (it + 1 < nit) {
+        load_table_rows<HD, E>(a, tl, wn.c, wn.z, kp, a.ks, rk);
+        load_table_rows<HD, E>(a, tl, wn.c, wn.z, vp, a.vs, rv);
+      }
+    } else {
+#pragma nounroll
+      for (int j = 0; j < 2; ++j) {
+        load_block_rows<HD, E>(a, tl, c, z, kp, a.ks, j, rk.y[0]);
+        load_block_rows<HD, E>(a, tl, c, z, vp, a.vs, j, rv.y[0]);
+        store_table_block<HD, E>(tl, c, qx, rk.y[0], j, s_t0[it & 1]);
+        store_table_block<HD, E>(tl, c, gx, rv.y[0], j, s_t1[it & 1]);
+      }
     }
     __syncthreads();
     // every slot reads its corners (in-bounds for any slot); misses are discarded
@@ -323,11 +349,11 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p1_kernel(
     const int kap = tl.sub + kSubs * i;
     p_ws[tap0 + kap] = pd;
     b_ws[tap0 + kap] = dss;
-    bf16* dp = doff + tl.qn * a.C + (static_cast<int64_t>(tl.head) * a.K + kap) * 3;
+    E* dp = doff + tl.qn * a.C + (static_cast<int64_t>(tl.head) * a.K + kap) * 3;
     const int m = sl[i].zc >> 17;
-    dp[0] = from_f32<bf16>((m & 1) ? (dss * gxs[i] + pd * gxd[i]) * cxs : 0.0f);
-    dp[1] = from_f32<bf16>((m & 2) ? (dss * gys[i] + pd * gyd[i]) * cys : 0.0f);
-    dp[2] = from_f32<bf16>((m & 4) ? (dss * gzs[i] + pd * gzd[i]) * czs : 0.0f);
+    dp[0] = from_f32<E>((m & 1) ? (dss * gxs[i] + pd * gxd[i]) * cxs : 0.0f);
+    dp[1] = from_f32<E>((m & 2) ? (dss * gys[i] + pd * gyd[i]) * cys : 0.0f);
+    dp[2] = from_f32<E>((m & 4) ? (dss * gzs[i] + pd * gzd[i]) * czs : 0.0f);
   }
 
 }
@@ -347,31 +373,38 @@ constexpr int kP2Q = kTQ * kP2Frames;          // queries per tile
 constexpr int kP2Subs = kThreads / kP2Q;       // lanes per query
 constexpr int kP2Slots = kMaxTaps / kP2Subs;   // taps per lane
 constexpr int kP2Row = kP2Q + 2;               // [voxel][query] table row (ints)
-constexpr int kP2QRow = kP2Q + 8;              // [channel][query] row of staged q / dO (bf16)
 static_assert(kP2Subs * kP2Slots == kMaxTaps, "the tap capacity must match the first kernel");
 
-template <int HD, int CW>
+// [channel][query] row of the staged q / dO (elements): 80 bytes for bf16, 144
+// bytes (= 36 banks: 16 rows of 16-byte reads conflict-free) for fp32.
+template <typename E>
+constexpr int p2_qrow() {
+  return sizeof(E) == 2 ? kP2Q + 8 : kP2Q + 4;
+}
+
+template <int HD, int CW, typename E>
 __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
-    Args a, const bf16* __restrict__ dout, const float* __restrict__ p_ws,
-    const float* __restrict__ b_ws, bf16* __restrict__ dq, float* __restrict__ dk_acc,
+    Args a, const E* __restrict__ dout, const float* __restrict__ p_ws,
+    const float* __restrict__ b_ws, E* __restrict__ dq, float* __restrict__ dk_acc,
     float* __restrict__ dv_acc) {
   static_assert(HD % CW == 0 && CW % 32 == 0, "channel windows are whole 32-channel blocks");
+  constexpr int KR = ElemT<E>::kRow, QR = p2_qrow<E>();
   __shared__ __attribute__((aligned(16))) int s_at[kChunkNV * kP2Row];  // A^T = p w (fixed point)
   __shared__ __attribute__((aligned(16))) int s_bt[kChunkNV * kP2Row];  // B^T = ds scale w (fixed point)
-  __shared__ __attribute__((aligned(16))) uint16_t s_kt[CW * kVRow];    // K^T chunk
+  __shared__ __attribute__((aligned(16))) word_t<E> s_kt[CW * KR];      // K^T chunk
   // per voxel: element offset (token row within the sample times D) of its accumulator row
   __shared__ __attribute__((aligned(16))) int s_rows[kChunkNV];
   __shared__ int s_red[kWaves][6];
   __shared__ __attribute__((aligned(16))) float s_binv[kP2Q];  // per query: 1 / fixed-point scale of B
   // the tile's q and dO rows of this window, transposed: [tensor][channel][query]
-  __shared__ __attribute__((aligned(16))) uint16_t s_qt[2][CW][kP2QRow];
+  __shared__ __attribute__((aligned(16))) word_t<E> s_qt[2][CW][QR];
 
   const Tile tl = make_tile<kP2Frames, kP2Subs>(a);
   const int D = a.nh * HD;
   const int cw0 = tl.head * HD + CW * static_cast<int>(blockIdx.z);  // first channel of the window
   Slot sl[kP2Slots];
   Box box;
-  setup_slots<kP2Subs, kP2Slots>(a, tl, sl, box, s_red);
+  setup_slots<E, kP2Subs, kP2Slots>(a, tl, sl, box, s_red);
   const int nchunks = box.ncy * box.ncx;
   const int nit = (box.zhi - box.zlo + 1) * nchunks;
 
@@ -401,18 +434,25 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
   for (int e = threadIdx.x; e < 2 * kP2Q * (CW / 8); e += kThreads) {
     const int cg = e % (CW / 8), m = (e / (CW / 8)) % kP2Q, tensor = e / (kP2Q * (CW / 8));
     const int64_t n = tile_row(a, tl, m);
-    u32x4_t x = {0u, 0u, 0u, 0u};
+    op_t<E> x = zero_op<E>();
     if (n >= 0) {
-      const bf16* src = tensor == 0 ? a.q + n * a.qs : dout + n * D;
-      x = load16(src + cw0 + 8 * cg);
+      const E* src = tensor == 0 ? static_cast<const E*>(a.q) + n * a.qs : dout + n * D;
+      x = load_op<E>(src + cw0 + 8 * cg);
     }
     const float sc = tensor == 0 ? s_binv[m] : kFixAInv;
+    if constexpr (sizeof(E) == 2) {
+      const u32x4_t xb = __builtin_bit_cast(u32x4_t, x);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const f32x2_t f = {__uint_as_float(x[i] << 16) * sc, __uint_as_float(x[i] & 0xffff0000u) * sc};
-      const uint32_t h = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_t));
-      s_qt[tensor][8 * cg + 2 * i][m] = static_cast<uint16_t>(h & 0xffffu);
-      s_qt[tensor][8 * cg + 2 * i + 1][m] = static_cast<uint16_t>(h >> 16);
+      for (int i = 0; i < 4; ++i) {
+        const f32x2_t f = {__uint_as_float(xb[i] << 16) * sc,
+                           __uint_as_float(xb[i] & 0xffff0000u) * sc};
+        const uint32_t h = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_t));
+        s_qt[tensor][8 * cg + 2 * i][m] = static_cast<uint16_t>(h & 0xffffu);
+        s_qt[tensor][8 * cg + 2 * i + 1][m] = static_cast<uint16_t>(h >> 16);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) s_qt[tensor][8 * cg + i][m] = x[i] * sc;
     }
   }
   __syncthreads();
@@ -435,9 +475,10 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
   f32x4_t dq_acc[NDQ];
 #pragma unroll
   for (int j = 0; j < NDQ; ++j) dq_acc[j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-  StageRows<kThreads, CW> kr;
+  const E* const kp = static_cast<const E*>(a.k);
+  StageRows<kThreads, CW, E> kr;
   Walk w = walk_begin(box);
-  if (nit > 0) load_stage_rows<kThreads, CW>(a, tl, w.c, w.z, a.k, a.ks, cw0, kr);
+  if (nit > 0) load_stage_rows<kThreads, CW, E>(a, tl, w.c, w.z, kp, a.ks, cw0, kr);
   for (int it = 0; it < nit; ++it) {
     const Walk wn = walk_next(box, w);
     const Chunk& c = w.c;
@@ -450,8 +491,8 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
     }
     for (int vi = threadIdx.x; vi < c.nv; vi += kThreads)
       s_rows[vi] = static_cast<int>(chunk_row(a, tl, c, z, vi) - tl.sample0) * D;
-    store_stage<kThreads, CW>(c, kr, s_kt);
-    if (it + 1 < nit) load_stage_rows<kThreads, CW>(a, tl, wn.c, wn.z, a.k, a.ks, cw0, kr);
+    store_stage<kThreads, CW, E>(c, kr, s_kt);
+    if (it + 1 < nit) load_stage_rows<kThreads, CW, E>(a, tl, wn.c, wn.z, kp, a.ks, cw0, kr);
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < kP2Slots; ++i) {
@@ -479,7 +520,7 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
       atomicAdd(rb + (dy + dx) * kP2Row, to_fix(bz * w11));
     }
     __syncthreads();
-    // dq[q] += sum_v B[q][v] K[v]; B as a bf16 hi/lo pair because
+    // dq[q] += sum_v B[q][v] K[v]; in bf16, B as a hi/lo pair because
     // sum_v B[q][v] = 0 and K may carry a large common part
     if constexpr (DQK) {
       const int fq = tl.wave / KPQ;
@@ -488,15 +529,10 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
 #pragma unroll
         for (int jj = 0; jj < 8; ++jj)
           bq[jj] = static_cast<float>(s_bt[(kc + kq + jj) * kP2Row + kTQ * fq + mq]);
-        bf16x8_t bhi, blo;
-        to_bf16x8_hilo(bq, bhi, blo);
+        const PreciseOp<E> bp = precise_op<E>(bq);
 #pragma unroll
-        for (int ct = 0; ct < CT; ++ct) {
-          bf16x8_t kv;
-          __builtin_memcpy(&kv, &s_kt[(16 * ct + mq) * kVRow + kc + kq], sizeof(kv));
-          dq_acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bhi, kv, dq_acc[ct], 0, 0, 0);
-          dq_acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(blo, kv, dq_acc[ct], 0, 0, 0);
-        }
+        for (int ct = 0; ct < CT; ++ct)
+          dq_acc[ct] = mma16(bp, load_op<E>(&s_kt[(16 * ct + mq) * KR + kc + kq]), dq_acc[ct]);
       }
     } else {
 #pragma unroll
@@ -509,16 +545,13 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
 #pragma unroll
           for (int jj = 0; jj < 8; ++jj)
             bq[jj] = static_cast<float>(s_bt[(kc + kq + jj) * kP2Row + kTQ * fq + mq]);
-          bf16x8_t bhi, blo, kv;
-          to_bf16x8_hilo(bq, bhi, blo);
-          __builtin_memcpy(&kv, &s_kt[(16 * ct + mq) * kVRow + kc + kq], sizeof(kv));
-          dq_acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bhi, kv, dq_acc[j], 0, 0, 0);
-          dq_acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(blo, kv, dq_acc[j], 0, 0, 0);
+          dq_acc[j] = mma16(precise_op<E>(bq), load_op<E>(&s_kt[(16 * ct + mq) * KR + kc + kq]),
+                            dq_acc[j]);
         }
       }
     }
-    // dK[v] += sum_q B[q][v] q[q];  dV[v] += sum_q A[q][v] dO[q]  (fp32 atomics;
-    // one register across the wave covers 2 voxels x 32 contiguous channels)
+    // dK[v] += sum_q B[q][v] q[q];  dV[v] += sum_q A[q][v] dO[q]  (32x32 MFMA, fp32
+    // atomics; one register across the wave covers 2 voxels x 32 contiguous channels)
     for (int t = tl.wave;; t += kWaves) {
       const int c2 = t % NC2, vb = t / NC2;
       if (vb * 32 >= c.nv) break;
@@ -526,13 +559,10 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
       f32x16_t dk = {}, dv = {};
 #pragma unroll
       for (int f = 0; f < kP2Frames; ++f) {
-        bf16x8_t qTf, gTf;
-        __builtin_memcpy(&qTf, &s_qt[0][och][kTQ * f + oq], sizeof(qTf));
-        __builtin_memcpy(&gTf, &s_qt[1][och][kTQ * f + oq], sizeof(gTf));
-        dk = __builtin_amdgcn_mfma_f32_32x32x16_bf16(table_t_rows(s_bt, kP2Row, kTQ * f, vb, tl.lane),
-                                                     qTf, dk, 0, 0, 0);
-        dv = __builtin_amdgcn_mfma_f32_32x32x16_bf16(table_t_rows(s_at, kP2Row, kTQ * f, vb, tl.lane),
-                                                     gTf, dv, 0, 0, 0);
+        dk = mma32(table_t_rows<E>(s_bt, kP2Row, kTQ * f, vb, tl.lane),
+                   load_op<E>(&s_qt[0][och][kTQ * f + oq]), dk);
+        dv = mma32(table_t_rows<E>(s_at, kP2Row, kTQ * f, vb, tl.lane),
+                   load_op<E>(&s_qt[1][och][kTQ * f + oq]), dv);
       }
       const int ch2 = cw0 + och;
       // accumulator rows of this sample: a wave-uniform base plus a 32-bit lane
@@ -578,7 +608,7 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
 #pragma unroll
       for (int kp = 0; kp < KPQ; ++kp) v += red[((f * KPQ + kp) * kTQ + mm) * CW + ch];
       const int64_t n = tile_row(a, tl, m);
-      if (n >= 0) dq[n * a.qs + cw0 + ch] = from_f32<bf16>(v * s_binv[m]);
+      if (n >= 0) dq[n * a.qs + cw0 + ch] = from_f32<E>(v * s_binv[m]);
     }
   } else {
     // dq_acc[j][r] = dq[query 16*fq + 4*(lane/16) + r][channel 16*ct + lane%16]
@@ -591,7 +621,7 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
       for (int r = 0; r < 4; ++r) {
         const int m = kTQ * fq + 4 * (tl.lane >> 4) + r;
         const int64_t n = tile_row(a, tl, m);
-        if (n >= 0) dq[n * a.qs + cw0 + 16 * ct + mq] = from_f32<bf16>(dq_acc[j][r] * s_binv[m]);
+        if (n >= 0) dq[n * a.qs + cw0 + 16 * ct + mq] = from_f32<E>(dq_acc[j][r] * s_binv[m]);
       }
     }
   }
@@ -603,10 +633,10 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
 tiled::Args make_tiled_args(const msd_dsa3d_desc& d, const void* q, const void* k, const void* v,
                             const void* off, int64_t tiles) {
   tiled::Args a;
-  a.q = static_cast<const bf16*>(q);
-  a.k = static_cast<const bf16*>(k);
-  a.v = static_cast<const bf16*>(v);
-  a.off = static_cast<const bf16*>(off);
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.off = off;
   a.qs = d.q_stride;
   a.ks = d.k_stride;
   a.vs = d.v_stride;
@@ -660,7 +690,8 @@ bool tiled_head_dim(int hd) { return hd == 64 || hd == 96 || hd == 128; }
 }  // namespace
 
 bool dsa3d_tiled_supported(const msd_dsa3d_desc& d, const void* q, const void* k, const void* v) {
-  if (d.dtype != MSD_BF16 || !tiled_head_dim(d.head_dim)) return false;
+  if ((d.dtype != MSD_BF16 && d.dtype != MSD_F32) || !tiled_head_dim(d.head_dim)) return false;
+  const int64_t eb = d.dtype == MSD_BF16 ? 2 : 4;
   if (d.kt * d.kh * d.kw > tiled::kMaxTaps) return false;
   if (d.T > 32767 || d.H > 32767 || d.W > 32767) return false;
   // the chunk grid of any corner box must number fewer than kMaxChunks
@@ -669,7 +700,7 @@ bool dsa3d_tiled_supported(const msd_dsa3d_desc& d, const void* q, const void* k
   if (cy * cx >= tiled::kMaxChunks) return false;
   const int64_t tiles = static_cast<int64_t>(d.B) * d.T * ((d.H + 3) / 4) * ((d.W + 3) / 4);
   if (tiles > 0x7fffffff || d.num_heads > 65535) return false;
-  // 16-byte vector loads of q/k/v rows
+  // 8-element (16- or 32-byte) vector loads of q/k/v rows
   if ((d.q_stride % 8) || (d.k_stride % 8) || (d.v_stride % 8)) return false;
   // the dK/dV accumulator rows of a sample are addressed with 32-bit byte offsets
   if (static_cast<int64_t>(d.T) * d.H * d.W * d.num_heads * d.head_dim >= (int64_t{1} << 30))
@@ -678,57 +709,125 @@ bool dsa3d_tiled_supported(const msd_dsa3d_desc& d, const void* q, const void* k
   // offset (24-bit multiplies): kChunk * (W + 1) rows must span < 2^31 bytes
   for (const int64_t st : {d.k_stride, d.v_stride})
     if (st >= (int64_t{1} << 23) ||
-        static_cast<int64_t>(tiled::kChunk) * (d.W + 1) * st * 2 >= (int64_t{1} << 31))
+        static_cast<int64_t>(tiled::kChunk) * (d.W + 1) * st * eb >= (int64_t{1} << 31))
       return false;
   for (const void* p : {q, k, v})
     if (reinterpret_cast<uintptr_t>(p) % 16) return false;
   return true;
 }
 
-hipError_t launch_dsa3d_fwd_tiled(const msd_dsa3d_desc& d, const void* q, const void* k,
-                                  const void* v, const void* off, void* out, float* lse,
-                                  hipStream_t s) {
-  const tiled::Args a = make_tiled_args(d, q, k, v, off, tiled_tiles<1>(d));
+namespace {
+template <typename E>
+hipError_t fwd_tiled_typed(const msd_dsa3d_desc& d, const tiled::Args& a, void* out, float* lse,
+                           hipStream_t s) {
   const dim3 grid = tiled_grid<1>(d), block(tiled::kThreads);
-  bf16* o = static_cast<bf16*>(out);
+  E* o = static_cast<E*>(out);
   switch (d.head_dim) {
-    case 64: hipLaunchKernelGGL(dsa3d_fwd_tiled_kernel<64>, grid, block, 0, s, a, o, lse); break;
-    case 96: hipLaunchKernelGGL(dsa3d_fwd_tiled_kernel<96>, grid, block, 0, s, a, o, lse); break;
-    case 128: hipLaunchKernelGGL(dsa3d_fwd_tiled_kernel<128>, grid, block, 0, s, a, o, lse); break;
+    case 64: hipLaunchKernelGGL((dsa3d_fwd_tiled_kernel<64, E>), grid, block, 0, s, a, o, lse); break;
+    case 96: hipLaunchKernelGGL((dsa3d_fwd_tiled_kernel<96, E>), grid, block, 0, s, a, o, lse); break;
+    case 128: hipLaunchKernelGGL((dsa3d_fwd_tiled_kernel<128, E>), grid, block, 0, s, a, o, lse); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }
+}  // namespace
+
+hipError_t launch_dsa3d_fwd_tiled(const msd_dsa3d_desc& d, const void* q, const void* k,
+                                  const void* v, const void* off, void* out, float* lse,
+                                  hipStream_t s) {
+  const tiled::Args a = make_tiled_args(d, q, k, v, off, tiled_tiles<1>(d));
+  if (d.dtype == MSD_BF16) return fwd_tiled_typed<bf16>(d, a, out, lse, s);
+  return fwd_tiled_typed<float>(d, a, out, lse, s);
+}
 
 namespace {
-// fp32 dK (blockIdx.y 0) or dV (1) accumulator [rows, D] -> bf16 with its token
-// stride, 8 channels per thread (two 16-byte loads, one 16-byte store; D and
-// the strides are multiples of 8, rows * D < 2^30).
-__global__ __launch_bounds__(256) void acc_to_bf16_kernel(const float* __restrict__ dk_acc,
-                                                          const float* __restrict__ dv_acc,
-                                                          bf16* __restrict__ dk,
-                                                          bf16* __restrict__ dv, int rows, int D,
-                                                          int64_t ks, int64_t vs) {
+// fp32 dK (blockIdx.y 0) or dV (1) accumulator [rows, D] -> the output type with
+// its token stride, 8 channels per thread (16- or 32-byte loads and stores; D
+// and the strides are multiples of 8, rows * D < 2^30).
+template <typename E>
+__global__ __launch_bounds__(256) void acc_to_out_kernel(const float* __restrict__ dk_acc,
+                                                         const float* __restrict__ dv_acc,
+                                                         E* __restrict__ dk, E* __restrict__ dv,
+                                                         int rows, int D, int64_t ks, int64_t vs) {
   const int d8 = D / 8;
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= rows * d8) return;
   const int r = i / d8, c = 8 * (i - r * d8);
   const bool is_k = blockIdx.y == 0;
   const float* src = (is_k ? dk_acc : dv_acc) + static_cast<int64_t>(r) * D + c;
-  bf16* dst = (is_k ? dk : dv) + static_cast<int64_t>(r) * (is_k ? ks : vs) + c;
+  E* dst = (is_k ? dk : dv) + static_cast<int64_t>(r) * (is_k ? ks : vs) + c;
   f32x4_t x[2];
   __builtin_memcpy(x, src, sizeof(x));
-  uint16_t h[8];
+  if constexpr (sizeof(E) == 2) {
+    uint16_t h[8];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) h[j] = from_f32<bf16>(x[j / 4][j % 4]).bits;
-  __builtin_memcpy(dst, h, sizeof(h));
+    for (int j = 0; j < 8; ++j) h[j] = from_f32<bf16>(x[j / 4][j % 4]).bits;
+    __builtin_memcpy(dst, h, sizeof(h));
+  } else {
+    __builtin_memcpy(dst, x, sizeof(x));
+  }
+}
+
+// Channel window of the second backward kernel.  bf16 takes the whole head
+// (for head_dim 128, two windows of 64 measured 4% slower than one of 128);
+// fp32 K^T and q/dO stages are twice as large, so windows of 64 (32 for
+// head_dim 96) keep them within the LDS.
+template <int HD, typename E>
+constexpr int p2_window() {
+  return sizeof(E) == 2 ? HD : (HD % 64 == 0 ? 64 : 32);
+}
+
+template <int HD, typename E>
+void launch_bwd_pair(const msd_dsa3d_desc& d, const tiled::Args& a1, const tiled::Args& a2,
+                     const E* o, const E* go, const float* lse, const float* dlse, E* gq, E* goff,
+                     float* p_ws, float* b_ws, float* dk_acc, float* dv_acc, hipStream_t s) {
+  constexpr int CW = p2_window<HD, E>();
+  const dim3 block(tiled::kThreads), g1 = tiled_grid<1>(d);
+  dim3 g2 = tiled_grid<kP2Frames>(d);
+  g2.z = HD / CW;
+  hipLaunchKernelGGL((dsa3d_bwd_p1_kernel<HD, E>), g1, block, 0, s, a1, o, go, lse, dlse, goff,
+                     p_ws, b_ws);
+  hipLaunchKernelGGL((dsa3d_bwd_p2_kernel<HD, CW, E>), g2, block, 0, s, a2, go, p_ws, b_ws, gq,
+                     dk_acc, dv_acc);
+}
+
+template <typename E>
+hipError_t bwd_tiled_typed(const msd_dsa3d_desc& d, const tiled::Args& a1, const tiled::Args& a2,
+                           const void* out, const void* dout, const float* lse, const float* dlse,
+                           void* dq, void* dk, void* dv, void* doff, float* dk_acc,
+                           float* dv_acc, float* p_ws, float* b_ws, hipStream_t s) {
+  const int64_t rows = static_cast<int64_t>(d.B) * d.T * d.H * d.W;
+  const int D = d.num_heads * d.head_dim;
+  const auto* o = static_cast<const E*>(out);
+  const auto* go = static_cast<const E*>(dout);
+  auto* gq = static_cast<E*>(dq);
+  auto* goff = static_cast<E*>(doff);
+  switch (d.head_dim) {
+    case 64:
+      launch_bwd_pair<64, E>(d, a1, a2, o, go, lse, dlse, gq, goff, p_ws, b_ws, dk_acc, dv_acc, s);
+      break;
+    case 96:
+      launch_bwd_pair<96, E>(d, a1, a2, o, go, lse, dlse, gq, goff, p_ws, b_ws, dk_acc, dv_acc, s);
+      break;
+    case 128:
+      launch_bwd_pair<128, E>(d, a1, a2, o, go, lse, dlse, gq, goff, p_ws, b_ws, dk_acc, dv_acc, s);
+      break;
+    default:
+      return hipErrorInvalidValue;
+  }
+  const dim3 cgrid(static_cast<unsigned>((rows * (D / 8) + 255) / 256), 2);
+  hipLaunchKernelGGL(acc_to_out_kernel<E>, cgrid, dim3(256), 0, s, dk_acc, dv_acc,
+                     static_cast<E*>(dk), static_cast<E*>(dv), static_cast<int>(rows), D,
+                     d.k_stride, d.v_stride);
+  return hipGetLastError();
 }
 }  // namespace
 
 // Workspace of the tiled backward beyond the dK/dV accumulators: p and
 // ds * softmax_scale of every tap (fp32 [token][head][tap] each).
 size_t dsa3d_tiled_bwd_extra_bytes(const msd_dsa3d_desc& d) {
-  if (d.dtype != MSD_BF16 || !tiled_head_dim(d.head_dim) || d.kt * d.kh * d.kw > tiled::kMaxTaps)
+  if ((d.dtype != MSD_BF16 && d.dtype != MSD_F32) || !tiled_head_dim(d.head_dim) ||
+      d.kt * d.kh * d.kw > tiled::kMaxTaps)
     return 0;
   const int64_t rows = static_cast<int64_t>(d.B) * d.T * d.H * d.W;
   return static_cast<size_t>(2 * rows * d.num_heads * d.kt * d.kh * d.kw) * sizeof(float);
@@ -749,41 +848,11 @@ hipError_t launch_dsa3d_bwd_tiled(const msd_dsa3d_desc& d, const void* q, const 
                      2 * rows * D);
   const tiled::Args a1 = make_tiled_args(d, q, k, v, off, tiled_tiles<1>(d));
   const tiled::Args a2 = make_tiled_args(d, q, k, v, off, tiled_tiles<kP2Frames>(d));
-  const dim3 block(tiled::kThreads), g1 = tiled_grid<1>(d);
-  const auto* o = static_cast<const bf16*>(out);
-  const auto* go = static_cast<const bf16*>(dout);
-  auto* gq = static_cast<bf16*>(dq);
-  auto* goff = static_cast<bf16*>(doff);
-  // the second kernel takes the whole head as its channel window (for
-  // head_dim 128, two windows of 64 measured 4% slower than one of 128)
-  const dim3 g2 = tiled_grid<kP2Frames>(d);
-  switch (d.head_dim) {
-    case 64:
-      hipLaunchKernelGGL(dsa3d_bwd_p1_kernel<64>, g1, block, 0, s, a1, o, go, lse, dlse, goff,
-                         p_ws, b_ws);
-      hipLaunchKernelGGL((dsa3d_bwd_p2_kernel<64, 64>), g2, block, 0, s, a2, go, p_ws, b_ws, gq,
-                         dk_acc, dv_acc);
-      break;
-    case 96:
-      hipLaunchKernelGGL(dsa3d_bwd_p1_kernel<96>, g1, block, 0, s, a1, o, go, lse, dlse, goff,
-                         p_ws, b_ws);
-      hipLaunchKernelGGL((dsa3d_bwd_p2_kernel<96, 96>), g2, block, 0, s, a2, go, p_ws, b_ws, gq,
-                         dk_acc, dv_acc);
-      break;
-    case 128:
-      hipLaunchKernelGGL(dsa3d_bwd_p1_kernel<128>, g1, block, 0, s, a1, o, go, lse, dlse, goff,
-                         p_ws, b_ws);
-      hipLaunchKernelGGL((dsa3d_bwd_p2_kernel<128, 128>), g2, block, 0, s, a2, go, p_ws, b_ws, gq,
-                         dk_acc, dv_acc);
-      break;
-    default:
-      return hipErrorInvalidValue;
-  }
-  const dim3 cgrid(static_cast<unsigned>((rows * (D / 8) + 255) / 256), 2);
-  hipLaunchKernelGGL(acc_to_bf16_kernel, cgrid, dim3(256), 0, s, dk_acc, dv_acc,
-                     static_cast<bf16*>(dk), static_cast<bf16*>(dv), static_cast<int>(rows), D,
-                     d.k_stride, d.v_stride);
-  return hipGetLastError();
+  if (d.dtype == MSD_BF16)
+    return bwd_tiled_typed<bf16>(d, a1, a2, out, dout, lse, dlse, dq, dk, dv, doff, dk_acc, dv_acc,
+                                 p_ws, b_ws, s);
+  return bwd_tiled_typed<float>(d, a1, a2, out, dout, lse, dlse, dq, dk, dv, doff, dk_acc, dv_acc,
+                                p_ws, b_ws, s);
 }
 
 }  // namespace msd

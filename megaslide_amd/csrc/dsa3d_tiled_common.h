@@ -26,6 +26,7 @@ typedef __attribute__((ext_vector_type(4))) float f32x4_t;
 typedef __attribute__((ext_vector_type(16))) float f32x16_t;
 typedef __attribute__((ext_vector_type(2))) float f32x2_t;
 typedef __attribute__((ext_vector_type(4))) unsigned int u32x4_t;
+typedef __attribute__((ext_vector_type(8))) float f32x8_t;
 
 constexpr int kTileH = 4, kTileW = 4;
 constexpr int kTQ = kTileH * kTileW;    // queries per tile
@@ -44,11 +45,74 @@ constexpr int kMaxChunks = 1 << 16;     // chunk ids are kept in 16 bits
 constexpr int kSRow = kChunkNV + 4;
 constexpr int kVRow = kChunkNV + 8;     // bf16 row stride of a transposed K/V chunk
 
+// Matrix-core operands per element type.  A lane's operand of one k block is
+// 8 consecutive k (channels or voxels) of its row or column.  bf16 feeds one
+// 16x16x32 (32x32x16) MFMA with them; fp32 feeds eight 16x16x4 (32x32x2)
+// MFMAs, the j-th taking element j of every lane, so each output sums the same
+// products with fp32 operands and the register layouts stay the same.
+template <typename E>
+struct ElemT;
+template <>
+struct ElemT<bf16> {
+  using op = bf16x8_t;
+  using word = uint16_t;                // LDS element of a transposed chunk
+  static constexpr int kRow = kVRow;    // its row stride (elements)
+};
+template <>
+struct ElemT<float> {
+  using op = f32x8_t;
+  using word = float;
+  static constexpr int kRow = kSRow;    // 260 = 4 (mod 64 banks): 16-byte reads of 16 rows are conflict-free
+};
+template <typename E>
+using op_t = typename ElemT<E>::op;
+template <typename E>
+using word_t = typename ElemT<E>::word;
+
+template <typename E>
+__device__ __forceinline__ op_t<E> zero_op() {
+  if constexpr (sizeof(E) == 2) {
+    const u32x4_t z = {0u, 0u, 0u, 0u};
+    return __builtin_bit_cast(bf16x8_t, z);
+  } else {
+    const f32x8_t z = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    return z;
+  }
+}
+
+// 8 consecutive elements (16 or 32 bytes) from global memory or LDS.
+template <typename E, typename P>
+__device__ __forceinline__ op_t<E> load_op(const P* p) {
+  op_t<E> r;
+  __builtin_memcpy(&r, p, sizeof(r));
+  return r;
+}
+
+__device__ __forceinline__ f32x4_t mma16(const bf16x8_t& a, const bf16x8_t& b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4_t mma16(const f32x8_t& a, const f32x8_t& b, f32x4_t c) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j], b[j], c, 0, 0, 0);
+  return c;
+}
+__device__ __forceinline__ f32x16_t mma32(const bf16x8_t& a, const bf16x8_t& b, f32x16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x16_t mma32(const f32x8_t& a, const f32x8_t& b, f32x16_t c) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) c = __builtin_amdgcn_mfma_f32_32x32x2f32(a[j], b[j], c, 0, 0, 0);
+  return c;
+}
+
+// Element storage of q/k/v/offsets and the outputs: bf16 or fp32 (type E of
+// the kernels; every table, accumulator and reduction is fp32 or fixed point
+// either way).
 struct Args {
-  const bf16* q;
-  const bf16* k;
-  const bf16* v;
-  const bf16* off;
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* off;
   int64_t qs, ks, vs;  // token strides of q, k, v
   int64_t N;
   int B, T, H, W, nh, kt, kh, kw, K, C;
@@ -159,7 +223,7 @@ __device__ __forceinline__ float grid_coord_rn(float base, float o, float div, f
 // Tap geometry for all SLOTS slots of this lane (coordinates exactly as the
 // reference rounds them) and the block-wide bounding box of every corner.
 // With `dropout`, each tap's keep decision is drawn here once (bit 20 of zc).
-template <int SUBS, int SLOTS>
+template <typename E, int SUBS, int SLOTS>
 __device__ __forceinline__ void setup_slots(const Args& a, const Tile& tl, Slot* sl, Box& box,
                                             int (*s_red)[6], bool dropout = false) {
   int zlo = 1 << 30, zhi = -1, ylo = 1 << 30, yhi = -1, xlo = 1 << 30, xhi = -1;
@@ -180,7 +244,8 @@ __device__ __forceinline__ void setup_slots(const Args& a, const Tile& tl, Slot*
     const int cj_ = static_cast<int>((static_cast<float>(rem) + 0.5f) * a.r_kw);
     const int ck_ = rem - cj_ * a.kw;
     const int ci = ci_ - a.kt / 2, cj = cj_ - a.kh / 2, ck = ck_ - a.kw / 2;
-    const bf16* op = a.off + tl.qn * a.C + (static_cast<int64_t>(tl.head) * a.K + kap) * 3;
+    const E* op = static_cast<const E*>(a.off) + tl.qn * a.C +
+                  (static_cast<int64_t>(tl.head) * a.K + kap) * 3;
     const float o0 = to_f32(op[0]) * a.offset_scale;
     const float o1 = to_f32(op[1]) * a.offset_scale;
     const float o2 = to_f32(op[2]) * a.offset_scale;
@@ -337,24 +402,21 @@ __device__ __forceinline__ int64_t chunk_row(const Args& a, const Tile& tl, cons
 // a 32-bit per-lane byte offset, so loads use scalar-base addressing.  The host
 // only admits shapes where (kChunk + 1) * W rows of every operand span less
 // than 2^31 bytes and strides are below 2^23 elements.
-__device__ __forceinline__ const bf16* chunk_voxel_ptr(const Args& a, const Tile& tl,
-                                                       const Chunk& c, int z, const bf16* base,
-                                                       int64_t stride, int col, int vi) {
+template <typename E>
+__device__ __forceinline__ const E* chunk_voxel_ptr(const Args& a, const Tile& tl, const Chunk& c,
+                                                    int z, const E* base, int64_t stride, int col,
+                                                    int vi) {
   const int64_t origin = tl.sample0 + (static_cast<int64_t>(z) * a.H + c.cy0) * a.W + c.cx0;
   const char* rb = reinterpret_cast<const char*>(base + origin * stride + col);
   const int vy = static_cast<int>((static_cast<float>(vi) + 0.5f) * c.rnx);
   const uint32_t vrow = static_cast<uint32_t>(__umul24(vy, a.W)) +
                         static_cast<uint32_t>(vi - vy * c.nx);
-  const uint32_t bytes = static_cast<uint32_t>(__umul24(vrow, static_cast<uint32_t>(stride) * 2u));
-  return reinterpret_cast<const bf16*>(rb + bytes);
+  const uint32_t bytes = static_cast<uint32_t>(
+      __umul24(vrow, static_cast<uint32_t>(stride) * static_cast<uint32_t>(sizeof(E))));
+  return reinterpret_cast<const E*>(rb + bytes);
 }
 
-__device__ __forceinline__ bf16x8_t zero_bf16x8() {
-  const u32x4_t z = {0u, 0u, 0u, 0u};
-  return __builtin_bit_cast(bf16x8_t, z);
-}
-
-__device__ __forceinline__ u32x4_t load16(const bf16* p) {
+__device__ __forceinline__ u32x4_t load16(const void* p) {
   u32x4_t r;
   __builtin_memcpy(&r, p, sizeof(r));
   return r;
@@ -362,111 +424,131 @@ __device__ __forceinline__ u32x4_t load16(const bf16* p) {
 
 // Rows of the tile (queries m = lane % 16) as MFMA A operands: x[c] holds
 // channels 32*c + 8*(lane/16) + [0, 8), c < HD/32.
-template <int HD>
-__device__ __forceinline__ void load_rows_operand(const Args& a, const Tile& tl, const bf16* base,
-                                                  int64_t stride, bf16x8_t (&x)[HD / 32]) {
+template <int HD, typename E>
+__device__ __forceinline__ void load_rows_operand(const Args& a, const Tile& tl, const E* base,
+                                                  int64_t stride, op_t<E> (&x)[HD / 32]) {
 #pragma unroll
-  for (int c = 0; c < HD / 32; ++c) x[c] = zero_bf16x8();
+  for (int c = 0; c < HD / 32; ++c) x[c] = zero_op<E>();
   const int64_t row = tile_row(a, tl, tl.lane & 15);
   if (row < 0) return;
-  const bf16* p = base + row * stride + tl.head * HD + 8 * (tl.lane >> 4);
+  const E* p = base + row * stride + tl.head * HD + 8 * (tl.lane >> 4);
 #pragma unroll
-  for (int c = 0; c < HD / 32; ++c) x[c] = __builtin_bit_cast(bf16x8_t, load16(p + 32 * c));
+  for (int c = 0; c < HD / 32; ++c) x[c] = load_op<E>(p + 32 * c);
 }
 
-// Y rows of a chunk as MFMA B operands, for the two 16-voxel blocks of this
-// wave (blocks w and w + 8; a chunk has at most 16 blocks).  All loads are
-// issued before any is used.
-template <int HD>
+// Y rows of 16-voxel block j (< 2) of this wave (block w + 8 j; a chunk has at
+// most 16 blocks) as MFMA B operands: y[c] holds channels 32*c + 8*(lane/16)
+// + [0, 8) of voxel 16*block + lane % 16.
+template <int HD, typename E>
+__device__ __forceinline__ void load_block_rows(const Args& a, const Tile& tl, const Chunk& c,
+                                                int z, const E* ybase, int64_t ystride, int j,
+                                                op_t<E> (&y)[HD / 32]) {
+  const int kq = 8 * (tl.lane >> 4);
+  const int vi = (tl.wave + kWaves * j) * 16 + (tl.lane & 15);
+#pragma unroll
+  for (int cc = 0; cc < HD / 32; ++cc) y[cc] = zero_op<E>();
+  if (vi < c.nv) {
+    const E* p = chunk_voxel_ptr(a, tl, c, z, ybase, ystride, tl.head * HD + kq, vi);
+#pragma unroll
+    for (int cc = 0; cc < HD / 32; ++cc) y[cc] = load_op<E>(p + 32 * cc);
+  }
+}
+
+// table[m][vi] = X[m] . Y[vi] for the voxels vi of block j of this wave.
+template <int HD, typename E>
+__device__ __forceinline__ void store_table_block(const Tile& tl, const Chunk& c,
+                                                  const op_t<E> (&x)[HD / 32],
+                                                  const op_t<E> (&y)[HD / 32], int j,
+                                                  float* table) {
+  const int blk = tl.wave + kWaves * j;
+  if (blk * 16 >= c.nv) return;
+  f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int cc = 0; cc < HD / 32; ++cc) acc = mma16(x[cc], y[cc], acc);
+  const int vi = blk * 16 + (tl.lane & 15);
+#pragma unroll
+  for (int rr = 0; rr < 4; ++rr) table[(4 * (tl.lane >> 4) + rr) * kSRow + vi] = acc[rr];
+}
+
+// Both blocks of the wave, loaded together: all loads are issued before any
+// is used.
+template <int HD, typename E>
 struct TableRows {
-  u32x4_t y[2][HD / 32];  // [block][channels 32*c + kq]
+  op_t<E> y[2][HD / 32];  // [block][channels 32*c + kq]
 };
 
-template <int HD>
+template <int HD, typename E>
 __device__ __forceinline__ void load_table_rows(const Args& a, const Tile& tl, const Chunk& c,
-                                                int z, const bf16* ybase, int64_t ystride,
-                                                TableRows<HD>& r) {
-  const int kq = 8 * (tl.lane >> 4);
+                                                int z, const E* ybase, int64_t ystride,
+                                                TableRows<HD, E>& r) {
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int vi = (tl.wave + kWaves * j) * 16 + (tl.lane & 15);
-    const u32x4_t z4 = {0u, 0u, 0u, 0u};
-#pragma unroll
-    for (int cc = 0; cc < HD / 32; ++cc) r.y[j][cc] = z4;
-    if (vi < c.nv) {
-      const bf16* p = chunk_voxel_ptr(a, tl, c, z, ybase, ystride, tl.head * HD + kq, vi);
-#pragma unroll
-      for (int cc = 0; cc < HD / 32; ++cc) r.y[j][cc] = load16(p + 32 * cc);
-    }
-  }
+  for (int j = 0; j < 2; ++j) load_block_rows<HD, E>(a, tl, c, z, ybase, ystride, j, r.y[j]);
 }
 
-// table[m][vi] = X[m] . Y[vi] for the wave's blocks of the chunk.
-template <int HD>
+template <int HD, typename E>
 __device__ __forceinline__ void store_table(const Tile& tl, const Chunk& c,
-                                            const bf16x8_t (&x)[HD / 32], const TableRows<HD>& r,
+                                            const op_t<E> (&x)[HD / 32], const TableRows<HD, E>& r,
                                             float* table) {
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int blk = tl.wave + kWaves * j;
-    if (blk * 16 >= c.nv) continue;
-    f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int cc = 0; cc < HD / 32; ++cc)
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x[cc], __builtin_bit_cast(bf16x8_t, r.y[j][cc]),
-                                                    acc, 0, 0, 0);
-    const int vi = blk * 16 + (tl.lane & 15);
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) table[(4 * (tl.lane >> 4) + rr) * kSRow + vi] = acc[rr];
-  }
+  for (int j = 0; j < 2; ++j) store_table_block<HD, E>(tl, c, x, r.y[j], j, table);
 }
 
 // Chunk rows of Y (plane z), channels col0 + [0, CW), transposed into LDS:
-// yt[channel][voxel] (bf16), zero padded up to nvp voxels, by the first NT
-// threads of the workgroup.  Thread t moves voxels 2*(t % 128) + {0, 1},
-// channel groups t / 128 + P*g (P = NT / 128, g < CW / 8 / P; 8 channels
-// each); its loads are issued first.
-template <int NT, int CW>
+// yt[channel][voxel] (row stride ElemT<E>::kRow), zero padded up to nvp
+// voxels, by the first NT threads of the workgroup.  Thread t moves voxels
+// 2*(t % 128) + {0, 1}, channel groups t / 128 + P*g (P = NT / 128,
+// g < CW / 8 / P; 8 channels each); its loads are issued first.
+template <int NT, int CW, typename E>
 struct StageRows {
   static constexpr int P = NT / 128, G = CW / 8 / P;
   static_assert(G * P * 8 == CW, "channel groups must split evenly over the staging threads");
-  u32x4_t x[G][2];  // [channel group][voxel]
+  op_t<E> x[G][2];  // [channel group][voxel]
 };
 
-template <int NT, int CW>
+template <int NT, int CW, typename E>
 __device__ __forceinline__ void load_stage_rows(const Args& a, const Tile& tl, const Chunk& c,
-                                                int z, const bf16* ybase, int64_t ystride,
-                                                int col0, StageRows<NT, CW>& r) {
-  constexpr int P = StageRows<NT, CW>::P, G = StageRows<NT, CW>::G;
+                                                int z, const E* ybase, int64_t ystride,
+                                                int col0, StageRows<NT, CW, E>& r) {
+  constexpr int P = StageRows<NT, CW, E>::P, G = StageRows<NT, CW, E>::G;
   const int cg0 = threadIdx.x >> 7, v0 = 2 * (threadIdx.x & 127);
-  const u32x4_t z4 = {0u, 0u, 0u, 0u};
 #pragma unroll
-  for (int g = 0; g < G; ++g) r.x[g][0] = r.x[g][1] = z4;
+  for (int g = 0; g < G; ++g) r.x[g][0] = r.x[g][1] = zero_op<E>();
 #pragma unroll
   for (int e = 0; e < 2; ++e) {
     if (v0 + e < c.nv) {
-      const bf16* p = chunk_voxel_ptr(a, tl, c, z, ybase, ystride, col0 + 8 * cg0, v0 + e);
+      const E* p = chunk_voxel_ptr(a, tl, c, z, ybase, ystride, col0 + 8 * cg0, v0 + e);
 #pragma unroll
-      for (int g = 0; g < G; ++g) r.x[g][e] = load16(p + 8 * P * g);
+      for (int g = 0; g < G; ++g) r.x[g][e] = load_op<E>(p + 8 * P * g);
     }
   }
 }
 
-template <int NT, int CW>
-__device__ __forceinline__ void store_stage(const Chunk& c, const StageRows<NT, CW>& r,
-                                            uint16_t* yt) {
-  constexpr int P = StageRows<NT, CW>::P, G = StageRows<NT, CW>::G;
+template <int NT, int CW, typename E>
+__device__ __forceinline__ void store_stage(const Chunk& c, const StageRows<NT, CW, E>& r,
+                                            word_t<E>* yt) {
+  constexpr int P = StageRows<NT, CW, E>::P, G = StageRows<NT, CW, E>::G;
+  constexpr int R = ElemT<E>::kRow;
   const int cg0 = threadIdx.x >> 7, v0 = 2 * (threadIdx.x & 127);
   if (v0 >= c.nvp) return;
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     const int ch0 = 8 * (cg0 + P * g);
+    if constexpr (sizeof(E) == 2) {
+      const u32x4_t x0 = __builtin_bit_cast(u32x4_t, r.x[g][0]);
+      const u32x4_t x1 = __builtin_bit_cast(u32x4_t, r.x[g][1]);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t even = (r.x[g][0][i] & 0xffffu) | (r.x[g][1][i] << 16);
-      const uint32_t odd = (r.x[g][0][i] >> 16) | (r.x[g][1][i] & 0xffff0000u);
-      __builtin_memcpy(&yt[(ch0 + 2 * i) * kVRow + v0], &even, sizeof(even));
-      __builtin_memcpy(&yt[(ch0 + 2 * i + 1) * kVRow + v0], &odd, sizeof(odd));
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t even = (x0[i] & 0xffffu) | (x1[i] << 16);
+        const uint32_t odd = (x0[i] >> 16) | (x1[i] & 0xffff0000u);
+        __builtin_memcpy(&yt[(ch0 + 2 * i) * R + v0], &even, sizeof(even));
+        __builtin_memcpy(&yt[(ch0 + 2 * i + 1) * R + v0], &odd, sizeof(odd));
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const f32x2_t pr = {r.x[g][0][i], r.x[g][1][i]};
+        __builtin_memcpy(&yt[(ch0 + i) * R + v0], &pr, sizeof(pr));
+      }
     }
   }
 }
@@ -550,19 +632,28 @@ constexpr float kFixA = 1073741824.0f;          // 2^30
 constexpr float kFixAInv = 1.0f / 1073741824.0f;
 
 // Truncating conversion: one instruction; its error (< 2^-30 of the scale)
-// is far below the bf16 rounding the tables get before the MFMA.
+// is far below the rounding the tables get before the MFMA (bf16: 2^-9; fp32:
+// 2^-24).
 __device__ __forceinline__ int to_fix(float x) { return static_cast<int>(x); }
 
-// 8 fixed-point table entries -> bf16x8 MFMA operand, still in fixed-point
-// units: the power-of-two scale is taken off the MFMA result instead (exact).
-__device__ __forceinline__ bf16x8_t fix_to_bf16x8(const int* p) {
-  u32x4_t r;
+// 8 fixed-point table entries -> MFMA operand, still in fixed-point units: the
+// power-of-two scale is taken off the MFMA result instead (exact).
+template <typename E>
+__device__ __forceinline__ op_t<E> fix_to_op(const int* p) {
+  if constexpr (sizeof(E) == 2) {
+    u32x4_t r;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const f32x2_t f = {static_cast<float>(p[2 * i]), static_cast<float>(p[2 * i + 1])};
-    r[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_t));
+    for (int i = 0; i < 4; ++i) {
+      const f32x2_t f = {static_cast<float>(p[2 * i]), static_cast<float>(p[2 * i + 1])};
+      r[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_t));
+    }
+    return __builtin_bit_cast(bf16x8_t, r);
+  } else {
+    f32x8_t r;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r[i] = static_cast<float>(p[i]);
+    return r;
   }
-  return __builtin_bit_cast(bf16x8_t, r);
 }
 
 // 8 floats as bf16x8, split into hi + lo bf16 parts (value = hi + lo to ~2^-16
@@ -580,6 +671,38 @@ __device__ __forceinline__ void to_bf16x8_hilo(const float* p, bf16x8_t& hi, bf1
   }
   hi = __builtin_bit_cast(bf16x8_t, h);
   lo = __builtin_bit_cast(bf16x8_t, l);
+}
+
+// A operand that must keep ~fp32 precision against a B operand of type E: the
+// values themselves for fp32, a bf16 hi + lo pair (two MFMAs) for bf16.
+template <typename E>
+struct PreciseOp;
+template <>
+struct PreciseOp<bf16> {
+  bf16x8_t hi, lo;
+};
+template <>
+struct PreciseOp<float> {
+  f32x8_t v;
+};
+
+template <typename E>
+__device__ __forceinline__ PreciseOp<E> precise_op(const float (&p)[8]) {
+  PreciseOp<E> r;
+  if constexpr (sizeof(E) == 2) {
+    to_bf16x8_hilo(p, r.hi, r.lo);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r.v[i] = p[i];
+  }
+  return r;
+}
+
+__device__ __forceinline__ f32x4_t mma16(const PreciseOp<bf16>& a, const bf16x8_t& b, f32x4_t c) {
+  return mma16(a.lo, b, mma16(a.hi, b, c));
+}
+__device__ __forceinline__ f32x4_t mma16(const PreciseOp<float>& a, const f32x8_t& b, f32x4_t c) {
+  return mma16(a.v, b, c);
 }
 
 }  // namespace tiled

@@ -85,9 +85,15 @@ def test_empty_batch_is_a_no_op():
 
 def test_workspace_size_and_check():
     lib = _lib.load()
-    d = _desc(B=2)
-    need = lib.msd_dsa3d_bwd_workspace_size(ctypes.byref(d))
-    assert need == 2 * 2 * 4 * 5 * 6 * 128 * 4
+    rows = 2 * 4 * 5 * 6
+    # head_dim 32: direct kernels only, dK/dV fp32 accumulators
+    d32 = _desc(B=2, head_dim=32, q_stride=64, k_stride=64, v_stride=64)
+    assert lib.msd_dsa3d_bwd_workspace_size(ctypes.byref(d32)) == 2 * rows * 64 * 4
+    # head_dim 64, fp32 and bf16: the tiled backward also keeps p and ds of every tap
+    for dtype in (0, 1):
+        d = _desc(B=2, dtype=dtype)
+        need = lib.msd_dsa3d_bwd_workspace_size(ctypes.byref(d))
+        assert need == 2 * rows * 128 * 4 + 2 * rows * 2 * 147 * 4
     rc = lib.msd_dsa3d_bwd(ctypes.byref(d), *([16] * 12), None, need - 1, None)
     assert rc == -4 and b"workspace" in lib.msd_last_error()
     assert lib.msd_dsa3d_bwd_workspace_size(None) == 0

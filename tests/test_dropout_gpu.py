@@ -28,6 +28,8 @@ def core():
     # dtype, algo, B, T, H, W, nh, hd, kernel, off_std, p
     (torch.float32, "direct", 1, 3, 5, 6, 2, 32, (3, 7, 7), 1.0, 0.3),
     (torch.float32, "direct", 2, 2, 4, 4, 1, 64, (3, 3, 3), 0.5, 0.6),
+    (torch.float32, "tiled", 2, 2, 4, 4, 1, 64, (3, 3, 3), 0.5, 0.6),
+    (torch.float32, "tiled", 1, 3, 6, 10, 1, 96, (3, 5, 5), 2.0, 0.3),
     (torch.bfloat16, "tiled", 1, 3, 7, 9, 2, 64, (3, 7, 7), 0.5, 0.2),
     (torch.bfloat16, "tiled", 1, 2, 8, 8, 1, 128, (3, 7, 7), 1.0, 0.5),
     (torch.bfloat16, "tiled", 1, 3, 6, 10, 1, 96, (3, 5, 5), 2.0, 0.1),
@@ -58,7 +60,8 @@ def test_dropout_matches_oracle(case):
         assert e < tol, name
 
 
-@pytest.mark.parametrize("algo,dt", [("direct", torch.float32), ("tiled", torch.bfloat16)])
+@pytest.mark.parametrize("algo,dt", [("direct", torch.float32), ("tiled", torch.float32),
+                                     ("tiled", torch.bfloat16)])
 def test_dropout_zero_and_determinism(algo, dt):
     B, T, H, W, nh, hd, ks = 1, 3, 8, 8, 2, 64, (3, 7, 7)
     N, D, C = T * H * W, nh * hd, nh * 147 * 3

@@ -121,7 +121,9 @@ def _oracle_core(q, k, v, off, vs, nh, ks, scale, dout, query_index=None, head_c
     return out.detach(), _grad_or_zero(qq), _grad_or_zero(kk), _grad_or_zero(vv), _grad_or_zero(oo)
 
 
-@pytest.mark.parametrize("dtype,tol", [(torch.float32, FP32_TOL), (torch.bfloat16, BF16_TOL)])
+@pytest.mark.parametrize("dtype,tol,algo", [(torch.float32, FP32_TOL, "auto"),
+                                             (torch.float32, FP32_TOL, "direct"),
+                                             (torch.bfloat16, BF16_TOL, "auto")])
 @pytest.mark.parametrize("shape", [
     # B, T, H, W, nh, hd, kernel, off_std, scale
     (2, 4, 12, 12, 2, 64, (3, 7, 7), 1.5, 1.0),
@@ -129,9 +131,9 @@ def _oracle_core(q, k, v, off, vs, nh, ks, scale, dout, query_index=None, head_c
     (1, 3, 6, 10, 2, 96, (3, 7, 7), 0.5, 1.0),
     (1, 2, 5, 7, 1, 128, (3, 7, 7), 4.0, 1.0),
 ])
-def test_core_vs_oracle_random(shape, dtype, tol):
+def test_core_vs_oracle_random(shape, dtype, tol, algo):
     B, T, H, W, nh, hd, ks, off_std, scale = shape
-    print(f"[core oracle] {shape} {dtype}", flush=True)
+    print(f"[core oracle] {shape} {dtype} {algo}", flush=True)
     N, D = T * H * W, nh * hd
     C = nh * ks[0] * ks[1] * ks[2] * 3
     g = torch.Generator().manual_seed(1234 + N + hd)
@@ -142,7 +144,7 @@ def test_core_vs_oracle_random(shape, dtype, tol):
     q, k, v, off, dout = (t.to(dtype) for t in (q, k, v, off, dout))
     ref = _oracle_core(q, k, v, off, (T, H, W), nh, ks, scale, dout)
     qd, kd, vd, od = (t.to(DEV).requires_grad_(True) for t in (q, k, v, off))
-    out = core()(qd, kd, vd, od, (T, H, W), nh, ks, scale)
+    out = core()(qd, kd, vd, od, (T, H, W), nh, ks, scale, algo=algo)
     out.backward(dout.to(DEV))
     torch.cuda.synchronize()
     assert out.dtype == dtype
@@ -154,11 +156,12 @@ def test_core_vs_oracle_random(shape, dtype, tol):
 
 
 @pytest.mark.parametrize("cfg", [
-    # name, dtype, B, T, H, W, nh, hd, off_std
-    ("fp32 B2 16x32x32 8x64", torch.float32, 2, 16, 32, 32, 8, 64, 1.5),
-    ("bf16 65536 tokens 16x64", torch.bfloat16, 1, 64, 32, 32, 16, 64, 0.5),
-    ("bf16 131072 tokens 24x128", torch.bfloat16, 1, 32, 64, 64, 24, 128, 0.5),
-    ("bf16 46800 tokens 16x96 (13x45x80)", torch.bfloat16, 1, 13, 45, 80, 16, 96, 2.5),
+    # name, dtype, B, T, H, W, nh, hd, off_std, algo
+    ("fp32 B2 16x32x32 8x64", torch.float32, 2, 16, 32, 32, 8, 64, 1.5, "auto"),
+    ("fp32 B2 16x32x32 8x64 direct", torch.float32, 2, 16, 32, 32, 8, 64, 1.5, "direct"),
+    ("bf16 65536 tokens 16x64", torch.bfloat16, 1, 64, 32, 32, 16, 64, 0.5, "auto"),
+    ("bf16 131072 tokens 24x128", torch.bfloat16, 1, 32, 64, 64, 24, 128, 0.5, "auto"),
+    ("bf16 46800 tokens 16x96 (13x45x80)", torch.bfloat16, 1, 13, 45, 80, 16, 96, 2.5, "auto"),
 ])
 def test_core_full_size_sampled_queries_and_checksums(cfg):
     """Full-size shapes: exact per-query parity on sampled queries (fwd, dq,
@@ -168,7 +171,7 @@ def test_core_full_size_sampled_queries_and_checksums(cfg):
     because every query's tap weights p_k * w_c sum to one; the sum of dK is
     zero because sum_k ds_k = 0.
     """
-    name, dtype, B, T, H, W, nh, hd, off_std = cfg
+    name, dtype, B, T, H, W, nh, hd, off_std, algo = cfg
     print(f"[full size] {name}", flush=True)
     ks = (3, 7, 7)
     N, D = T * H * W, nh * hd
@@ -178,7 +181,7 @@ def test_core_full_size_sampled_queries_and_checksums(cfg):
     off = (torch.randn(B, N, C, generator=g, device=DEV) * off_std).to(dtype)
     dout = torch.randn(B, N, D, generator=g, device=DEV).to(dtype)
     qd, kd, vd, od = (t.clone().requires_grad_(True) for t in (q, k, v, off))
-    out = core()(qd, kd, vd, od, (T, H, W), nh, ks, 1.0)
+    out = core()(qd, kd, vd, od, (T, H, W), nh, ks, 1.0, algo=algo)
     out.backward(dout)
     torch.cuda.synchronize()
     tol = FP32_TOL if dtype == torch.float32 else BF16_TOL

@@ -1,8 +1,8 @@
 """Matrix-core (tiled) attention-core kernels: parity and invariants (GPU).
 
-The tiled kernels serve bf16, head_dim 64, 96 and 128.  They must agree with the fp32
-oracle (tolerance 2e-2, relative to max|ref|) and with the direct kernels; the
-log-sum-exp they return must match the oracle's to 1e-5.
+The tiled kernels serve bf16 and fp32, head_dim 64, 96 and 128.  They must agree
+with the fp32 oracle (relative to max|ref|: bf16 2e-2, fp32 1e-4) and with the
+direct kernels; the log-sum-exp they return must match the oracle's to 1e-5.
 """
 
 import pytest
@@ -15,6 +15,7 @@ pytestmark = pytest.mark.gpu
 
 DEV = "cuda"
 BF16_TOL = 2e-2
+FP32_TOL = 1e-4
 
 
 def core():
@@ -22,12 +23,12 @@ def core():
     return dsa3d_core
 
 
-def _inputs(B, T, H, W, nh, ks, off_std, seed, hd=64):
+def _inputs(B, T, H, W, nh, ks, off_std, seed, hd=64, dtype=torch.bfloat16):
     N, D = T * H * W, nh * hd
     C = nh * ks[0] * ks[1] * ks[2] * 3
     g = torch.Generator().manual_seed(seed)
-    q, k, v = (torch.randn(B, N, D, generator=g).to(torch.bfloat16) for _ in range(3))
-    off = (torch.randn(B, N, C, generator=g) * off_std).to(torch.bfloat16)
+    q, k, v = (torch.randn(B, N, D, generator=g).to(dtype) for _ in range(3))
+    off = (torch.randn(B, N, C, generator=g) * off_std).to(dtype)
     return q, k, v, off
 
 
@@ -117,3 +118,49 @@ def test_tiled_lse_matches_oracle():
     err = rel_err(lse.cpu(), ref_lse.permute(0, 2, 1))
     print("lse err", err, flush=True)
     assert err < 1e-5
+
+
+@pytest.mark.parametrize("shape", [
+    # B, T, H, W, nh, kernel, off_std, scale, head_dim
+    (1, 3, 7, 9, 2, (3, 7, 7), 0.5, 1.0, 64),
+    (2, 4, 8, 8, 1, (3, 5, 5), 1.5, 0.8, 64),
+    (1, 5, 12, 40, 1, (3, 7, 7), 8.0, 1.0, 64),   # corner boxes span several chunks
+    (1, 4, 13, 18, 1, (3, 7, 7), 4.0, 0.9, 96),   # non-tile-aligned grid, large offsets
+    (1, 3, 8, 8, 2, (3, 7, 7), 0.5, 1.0, 128),
+    (1, 4, 1, 9, 2, (3, 7, 7), 1.0, 1.0, 64),     # H = 1
+    (2, 2, 3, 5, 2, (1, 3, 5), 3.0, 1.2, 96),     # B = 2, asymmetric window
+])
+def test_tiled_fp32_vs_oracle_and_direct(shape):
+    """fp32 storage: the tiled kernels run the fp32 matrix-core instructions
+    and must meet the fp32 tolerance against the oracle and the direct kernels."""
+    B, T, H, W, nh, ks, off_std, scale, hd = shape
+    print(f"[tiled fp32] {shape}", flush=True)
+    q, k, v, off = _inputs(B, T, H, W, nh, ks, off_std, 700 + T * H * W + hd, hd=hd,
+                           dtype=torch.float32)
+    g = torch.Generator().manual_seed(23)
+    dout = torch.randn(q.shape, generator=g)
+    qq, kk, vv, oo = (t.clone().requires_grad_(True) for t in (q, k, v, off))
+    ref, ref_lse = dsa3d_core_ref(qq, kk, vv, oo, (T, H, W), nh, ks, scale, return_lse=True)
+    ref.backward(dout)
+    grads, outs, lses = {}, {}, {}
+    for algo in ("tiled", "direct"):
+        ts = [t.to(DEV).requires_grad_(True) for t in (q, k, v, off)]
+        out, lse = core()(*ts, (T, H, W), nh, ks, scale, algo=algo, return_lse=True)
+        out.backward(dout.to(DEV))
+        outs[algo] = out.detach().cpu()
+        lses[algo] = lse.detach().cpu()
+        grads[algo] = [t.grad.cpu() for t in ts]
+    torch.cuda.synchronize()
+    assert outs["tiled"].dtype == torch.float32
+    e_out = rel_err(outs["tiled"], ref.detach())
+    e_lse = rel_err(lses["tiled"], ref_lse.detach().permute(0, 2, 1))
+    print(f"  out: vs oracle {e_out:.2e}  lse {e_lse:.2e}", flush=True)
+    assert e_out < FP32_TOL
+    assert e_lse < 1e-5
+    assert rel_err(outs["tiled"], outs["direct"]) < FP32_TOL
+    for name, r, gt, gd in zip(("dq", "dk", "dv", "doff"), (qq.grad, kk.grad, vv.grad, oo.grad),
+                               grads["tiled"], grads["direct"]):
+        e_ref, e_dir = rel_err(gt, r), rel_err(gt, gd)
+        print(f"  {name}: vs oracle {e_ref:.2e}  vs direct {e_dir:.2e}", flush=True)
+        assert e_ref < FP32_TOL, name
+        assert e_dir < FP32_TOL, name
