@@ -9,7 +9,9 @@ and reference checkpoints load unchanged.
 What runs where:
   * q/k/v/out projections and the 1x1 offset conv (offset_net[2]) are dense
     GEMMs and stay in PyTorch (hipBLASLt); the offset conv runs as a linear
-    layer on channel-last features so offsets come out [B, N, C].
+    layer on channel-last features so offsets come out [B, N, C], and out_proj
+    accumulates onto the dw_conv term in the same GEMM (torch.addmm), its bias
+    folded into the conv's.
   * dw_conv (depthwise kt x kh x kw) and offset_net[0:2] (depthwise 3x3x3 +
     GELU) run as HIP depthwise-conv kernels on channel-last tokens.
   * offset scaling, base grid, trilinear K/V sampling with border clamp,
@@ -95,8 +97,10 @@ class DeformableSlideAttention3D(nn.Module):
         # attention dropout (attention.py:180): in training mode only, as nn.Dropout
         drop_p = self.dropout.p if self.training else 0.0
 
-        # depthwise conv term and offset predictor, channel-last
-        dw = dwconv3d(x, self.dw_conv.weight, self.dw_conv.bias, video_shape)
+        # depthwise conv term and offset predictor, channel-last.  out_proj's bias
+        # rides on the conv's, so the output projection below accumulates onto
+        # the conv term in one GEMM (attention.py:187-192: out_proj(o) + dw_flat)
+        dw = dwconv3d(x, self.dw_conv.weight, self.dw_conv.bias + self.out_proj.bias, video_shape)
         feat = dwconv3d(x, self.offset_net[0].weight, self.offset_net[0].bias, video_shape,
                         act="gelu")
         on2 = self.offset_net[2]
@@ -112,7 +116,8 @@ class DeformableSlideAttention3D(nn.Module):
                               self.kernel_size, self.offset_scale, dropout_p=drop_p)
         else:
             attn = self._with_extra_kv(q, k.to(dt), v.to(dt), off, video_shape, extra_kv, drop_p)
-        return self.out_proj(attn) + dw
+        return torch.addmm(dw.reshape(B * N, D), attn.reshape(B * N, D),
+                           self.out_proj.weight.t()).view(B, N, D)
 
     def _with_extra_kv(self, q, k, v, off, video_shape, extra_kv, drop_p=0.0):
         """Local taps + G shared extra keys, merged through the log-sum-exp.
