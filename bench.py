@@ -1,6 +1,7 @@
 """Benchmark: 3D-DSA forward + backward through the HIP kernel set on one MI355X.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu-baseline] [--copy-calibration]
+                    [--workload long-clip-65k|fp32-32k]
     python bench.py --summarize TRACE_DIR FETCH_DIR WRITE_DIR   (rocprofv3 csv output -> profiles/)
 
 Workload (one step = one pass of the hot path over one batch): the 65,536-token
@@ -11,6 +12,10 @@ upstream grads ~ N(0, 1).  A step runs, on preallocated device buffers:
   attention core bwd, 3x3x3+GELU bwd, 3x7x7 bwd
 i.e. every HIP kernel of the module's forward and backward (the dense GEMMs of
 the projections stay in hipBLASLt and are not part of the step).
+
+--workload fp32-32k runs the same step on the fp32 32,768-token case instead
+(B=2, T=16, H=W=32, dim 512, 8 heads x 64, raw offsets ~ N(0, 1.5)); its line
+names that workload and carries no CPU baseline.
 
 Prints one JSON line.  `value` is tokens/s of the whole step; `roofline` is the
 dominant kernel's algorithmic HBM bytes per launch over its average duration,
@@ -45,7 +50,15 @@ if ROOT not in sys.path:
 METRIC = "3D-DSA fwd+bwd tokens/sec at 65k tokens bf16; achieved HBM GB/s (% of peak)"
 HBM_PEAK_GBPS = 8000.0
 
-CFG = dict(B=1, T=64, H=32, W=32, D=1024, nh=16, hd=64, kernel=(3, 7, 7), off_std=0.5)
+CFG = dict(B=1, T=64, H=32, W=32, D=1024, nh=16, hd=64, kernel=(3, 7, 7), off_std=0.5,
+           dtype="bf16", workload="3D-DSA fwd+bwd HIP kernel set, long-clip 65,536 tokens",
+           metric=METRIC)
+WORKLOADS = {
+    "long-clip-65k": CFG,
+    "fp32-32k": dict(B=2, T=16, H=32, W=32, D=512, nh=8, hd=64, kernel=(3, 7, 7), off_std=1.5,
+                     dtype="fp32", workload="3D-DSA fwd+bwd HIP kernel set, fp32 32,768 tokens",
+                     metric="3D-DSA fwd+bwd tokens/sec at 32k tokens fp32"),
+}
 
 
 def algorithmic_bytes(cfg, e):
@@ -87,7 +100,7 @@ def measured_traffic(kernel):
     return None if rec is None else rec.get("bytes_per_launch")
 
 
-def run_gpu(steps, warmup, calibrate=False):
+def run_gpu(steps, warmup, calibrate=False, cfg=CFG):
     from megaslide_amd import _lib
 
     lib = _lib.load()
@@ -95,12 +108,13 @@ def run_gpu(steps, warmup, calibrate=False):
     torch.cuda.set_device(dev)
     if calibrate:
         copy_calibration(dev)
-    c = CFG
+    c = cfg
     B, T, H, W, D, nh, hd = c["B"], c["T"], c["H"], c["W"], c["D"], c["nh"], c["hd"]
     kt, kh, kw = c["kernel"]
     N = T * H * W
     C = nh * kt * kh * kw * 3
-    dt = torch.bfloat16
+    dt = torch.bfloat16 if c["dtype"] == "bf16" else torch.float32
+    mdt = _lib.MSD_BF16 if c["dtype"] == "bf16" else _lib.MSD_F32
     g = torch.Generator(device=dev).manual_seed(3)
 
     def rnd(*shape, std=1.0):
@@ -120,10 +134,9 @@ def run_gpu(steps, warmup, calibrate=False):
     dx3, dx7 = torch.empty_like(x), torch.empty_like(x)
     dw3, db3, dw7, db7 = (torch.empty_like(t) for t in (w3, b3, w7, b7))
 
-    dsa = _lib.DsaDesc(B, T, H, W, nh, hd, kt, kh, kw, _lib.MSD_BF16, D, D, D, 1.0,
-                       1.0 / math.sqrt(hd))
-    cv7 = _lib.ConvDesc(B, T, H, W, D, kt, kh, kw, _lib.MSD_BF16, 0)
-    cv3 = _lib.ConvDesc(B, T, H, W, D, 3, 3, 3, _lib.MSD_BF16, 1)
+    dsa = _lib.DsaDesc(B, T, H, W, nh, hd, kt, kh, kw, mdt, D, D, D, 1.0, 1.0 / math.sqrt(hd))
+    cv7 = _lib.ConvDesc(B, T, H, W, D, kt, kh, kw, mdt, 0)
+    cv3 = _lib.ConvDesc(B, T, H, W, D, 3, 3, 3, mdt, 1)
     ws_dsa = torch.empty(lib.msd_dsa3d_bwd_workspace_size(ctypes.byref(dsa)), dtype=torch.uint8,
                          device=dev)
     ws7 = torch.empty(lib.msd_dwconv3d_bwd_workspace_size(ctypes.byref(cv7)), dtype=torch.uint8,
@@ -303,6 +316,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run a 512 MiB copy first (scale for the FETCH_SIZE/WRITE_SIZE counters)")
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="long-clip-65k")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: the 3D-DSA kernels run on a single MI355X "
@@ -310,9 +324,10 @@ def main():
               file=sys.stderr)
         sys.exit(2)
 
-    r = run_gpu(args.steps, args.warmup, args.copy_calibration)
-    e = 2
-    ab = algorithmic_bytes(CFG, e)
+    cfg = WORKLOADS[args.workload]
+    r = run_gpu(args.steps, args.warmup, args.copy_calibration, cfg)
+    e = 2 if cfg["dtype"] == "bf16" else 4
+    ab = algorithmic_bytes(cfg, e)
     ms_step = r["total_ms"] / args.steps
     tokens_s = r["tokens"] / (ms_step / 1e3)
     step_bytes = sum(ab.values())
@@ -320,7 +335,7 @@ def main():
     dom_ms = r["per_phase_ms"][dom]
     achieved = ab[dom] / (dom_ms / 1e3) / 1e9
     line = {
-        "metric": METRIC,
+        "metric": cfg["metric"],
         "value": round(tokens_s, 1),
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -330,13 +345,13 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": cfg["dtype"],
         "data": "synthetic",
         "config": {
-            "workload": "3D-DSA fwd+bwd HIP kernel set, long-clip 65,536 tokens",
-            "B": CFG["B"], "T": CFG["T"], "H": CFG["H"], "W": CFG["W"], "dim": CFG["D"],
-            "heads": CFG["nh"], "head_dim": CFG["hd"], "window": list(CFG["kernel"]),
-            "offsets": "raw ~ N(0, 0.5)", "accumulation": "fp32",
+            "workload": cfg["workload"],
+            "B": cfg["B"], "T": cfg["T"], "H": cfg["H"], "W": cfg["W"], "dim": cfg["D"],
+            "heads": cfg["nh"], "head_dim": cfg["hd"], "window": list(cfg["kernel"]),
+            "offsets": f"raw ~ N(0, {cfg['off_std']})", "accumulation": "fp32",
         },
         "hbm_gbps": round(step_bytes / (ms_step / 1e3) / 1e9, 1),
         "hbm_frac_of_peak": round(step_bytes / (ms_step / 1e3) / 1e9 / HBM_PEAK_GBPS, 4),
@@ -347,14 +362,14 @@ def main():
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
-            "traffic": measured_traffic(dom),
+            "traffic": measured_traffic(dom) if cfg is CFG else None,
             "algorithmic_bytes_per_launch": ab[dom],
             "avg_launch_ms": round(dom_ms, 4),
         },
         "per_kernel_ms": {k: round(v, 4) for k, v in r["per_phase_ms"].items()},
         "wall_s_timed_region": round(r["wall_s"], 3),
     }
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and cfg is CFG:
         cb = cpu_baseline()
         line["cpu_baseline"] = {k: (round(v, 2) if isinstance(v, float) else v)
                                 for k, v in cb.items() if k != "seconds"}
