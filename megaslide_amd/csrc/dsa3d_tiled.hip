@@ -96,7 +96,7 @@ __global__ __launch_bounds__(kThreads, (fwd_min_waves<HD, E>())) void dsa3d_fwd_
 #pragma unroll
     for (int i = 0; i < kSlots; ++i) {
       float wz, dwz;
-      const bool hit = slot_weight(sl[i], z, c.id, wz, dwz);
+      const bool hit = slot_weight(sl[i], step_key(c.id, z), wz, dwz);
       const float v = bilerp(sl[i], t[i][0], t[i][1], t[i][2], t[i][3]).val;
       sc[i] = hit ? __builtin_fmaf(wz, v, sc[i]) : sc[i];
     }
@@ -162,7 +162,7 @@ __global__ __launch_bounds__(kThreads, (fwd_min_waves<HD, E>())) void dsa3d_fwd_
 #pragma unroll
     for (int i = 0; i < kSlots; ++i) {
       float wz, dwz;
-      if (!slot_hits(sl[i], z, c.id, wz, dwz)) continue;
+      if (!slot_hits(sl[i], step_key(c.id, z), wz, dwz)) continue;
       const float pz = sc[i] * wz * kFixA;
       const float gx = 1.0f - sl[i].fx, gy = 1.0f - sl[i].fy;
       const int base = sl[i].idx & 0x1ff, dy = (sl[i].idx >> 9) & 0x1f, dx = (sl[i].idx >> 14) & 1;
@@ -294,10 +294,12 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p1_kernel(
         load_table_rows<HD, E>(a, tl, wn.c, wn.z, vp, a.vs, rv);
       }
     } else {
+      const char* ko = head_origin<HD, E>(a, tl, c, z, kp, a.ks);
+      const char* vo = head_origin<HD, E>(a, tl, c, z, vp, a.vs);
 #pragma nounroll
       for (int j = 0; j < 2; ++j) {
-        load_block_rows<HD, E>(a, tl, c, z, kp, a.ks, j, rk.y[0]);
-        load_block_rows<HD, E>(a, tl, c, z, vp, a.vs, j, rv.y[0]);
+        load_block_rows<HD, E>(a, tl, c, ko, a.ks, j, rk.y[0]);
+        load_block_rows<HD, E>(a, tl, c, vo, a.vs, j, rv.y[0]);
         store_table_block<HD, E>(tl, c, qx, rk.y[0], j, s_t0[it & 1]);
         store_table_block<HD, E>(tl, c, gx, rv.y[0], j, s_t1[it & 1]);
       }
@@ -309,7 +311,7 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p1_kernel(
 #pragma unroll
     for (int i = 0; i < kSlots; ++i) {
       float wz, dwz;
-      const bool hit = slot_weight(sl[i], z, c.id, wz, dwz);
+      const bool hit = slot_weight(sl[i], step_key(c.id, z), wz, dwz);
       float t00, t01, t10, t11;
       corners4(sl[i], r0, t00, t01, t10, t11);
       const Bilerp bs = bilerp(sl[i], t00, t01, t10, t11);
@@ -497,7 +499,7 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
 #pragma unroll
     for (int i = 0; i < kP2Slots; ++i) {
       float wz, dwz;
-      if (!slot_hits(sl[i], z, c.id, wz, dwz)) continue;
+      if (!slot_hits(sl[i], step_key(c.id, z), wz, dwz)) continue;
       const float pz = p[i] * wz * kFixA, bz = bsc[i] * wz * bscale;
       const float fx = sl[i].fx, fy = sl[i].fy, gx = 1.0f - fx, gy = 1.0f - fy;
       const float w00 = gy * gx, w01 = gy * fx, w10 = fy * gx, w11 = fy * fx;

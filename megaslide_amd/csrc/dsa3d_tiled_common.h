@@ -397,23 +397,30 @@ __device__ __forceinline__ int64_t chunk_row(const Args& a, const Tile& tl, cons
   return tl.sample0 + (static_cast<int64_t>(z) * a.H + c.cy0 + vy) * a.W + c.cx0 + vx;
 }
 
-// Address of channel `col` of voxel vi of chunk c in plane z, in rows of
-// `stride` elements: a wave-uniform 64-bit base (the chunk's first voxel) plus
-// a 32-bit per-lane byte offset, so loads use scalar-base addressing.  The host
-// only admits shapes where (kChunk + 1) * W rows of every operand span less
-// than 2^31 bytes and strides are below 2^23 elements.
+// Rows of `stride` elements are addressed as a wave-uniform 64-bit base (the
+// chunk's first voxel, channel `col`) plus a 32-bit per-lane byte offset, so
+// loads use scalar-base addressing; the base is computed once per step.  The
+// host only admits shapes where (kChunk + 1) * W rows of every operand span
+// less than 2^31 bytes and strides are below 2^23 elements.
 template <typename E>
-__device__ __forceinline__ const E* chunk_voxel_ptr(const Args& a, const Tile& tl, const Chunk& c,
-                                                    int z, const E* base, int64_t stride, int col,
-                                                    int vi) {
+__device__ __forceinline__ const char* chunk_origin(const Args& a, const Tile& tl, const Chunk& c,
+                                                    int z, const E* base, int64_t stride, int col) {
   const int64_t origin = tl.sample0 + (static_cast<int64_t>(z) * a.H + c.cy0) * a.W + c.cx0;
-  const char* rb = reinterpret_cast<const char*>(base + origin * stride + col);
+  return reinterpret_cast<const char*>(base + origin * stride + col);
+}
+
+// Channel `lane_col` (per lane, relative to the origin's) of voxel vi.
+template <typename E>
+__device__ __forceinline__ const E* chunk_voxel(const char* origin, const Args& a, const Chunk& c,
+                                                int64_t stride, int lane_col, int vi) {
   const int vy = static_cast<int>((static_cast<float>(vi) + 0.5f) * c.rnx);
   const uint32_t vrow = static_cast<uint32_t>(__umul24(vy, a.W)) +
                         static_cast<uint32_t>(vi - vy * c.nx);
-  const uint32_t bytes = static_cast<uint32_t>(
-      __umul24(vrow, static_cast<uint32_t>(stride) * static_cast<uint32_t>(sizeof(E))));
-  return reinterpret_cast<const E*>(rb + bytes);
+  const uint32_t bytes =
+      static_cast<uint32_t>(__umul24(vrow, static_cast<uint32_t>(stride) *
+                                               static_cast<uint32_t>(sizeof(E)))) +
+      static_cast<uint32_t>(lane_col) * static_cast<uint32_t>(sizeof(E));
+  return reinterpret_cast<const E*>(origin + bytes);
 }
 
 __device__ __forceinline__ u32x4_t load16(const void* p) {
@@ -441,17 +448,23 @@ __device__ __forceinline__ void load_rows_operand(const Args& a, const Tile& tl,
 // + [0, 8) of voxel 16*block + lane % 16.
 template <int HD, typename E>
 __device__ __forceinline__ void load_block_rows(const Args& a, const Tile& tl, const Chunk& c,
-                                                int z, const E* ybase, int64_t ystride, int j,
+                                                const char* origin, int64_t ystride, int j,
                                                 op_t<E> (&y)[HD / 32]) {
-  const int kq = 8 * (tl.lane >> 4);
   const int vi = (tl.wave + kWaves * j) * 16 + (tl.lane & 15);
 #pragma unroll
   for (int cc = 0; cc < HD / 32; ++cc) y[cc] = zero_op<E>();
   if (vi < c.nv) {
-    const E* p = chunk_voxel_ptr(a, tl, c, z, ybase, ystride, tl.head * HD + kq, vi);
+    const E* p = chunk_voxel<E>(origin, a, c, ystride, 8 * (tl.lane >> 4), vi);
 #pragma unroll
     for (int cc = 0; cc < HD / 32; ++cc) y[cc] = load_op<E>(p + 32 * cc);
   }
+}
+
+// The chunk's rows of head tl.head in plane z (wave-uniform origin).
+template <int HD, typename E>
+__device__ __forceinline__ const char* head_origin(const Args& a, const Tile& tl, const Chunk& c,
+                                                   int z, const E* ybase, int64_t ystride) {
+  return chunk_origin(a, tl, c, z, ybase, ystride, tl.head * HD);
 }
 
 // table[m][vi] = X[m] . Y[vi] for the voxels vi of block j of this wave.
@@ -481,8 +494,9 @@ template <int HD, typename E>
 __device__ __forceinline__ void load_table_rows(const Args& a, const Tile& tl, const Chunk& c,
                                                 int z, const E* ybase, int64_t ystride,
                                                 TableRows<HD, E>& r) {
+  const char* origin = head_origin<HD, E>(a, tl, c, z, ybase, ystride);
 #pragma unroll
-  for (int j = 0; j < 2; ++j) load_block_rows<HD, E>(a, tl, c, z, ybase, ystride, j, r.y[j]);
+  for (int j = 0; j < 2; ++j) load_block_rows<HD, E>(a, tl, c, origin, ystride, j, r.y[j]);
 }
 
 template <int HD, typename E>
@@ -513,10 +527,11 @@ __device__ __forceinline__ void load_stage_rows(const Args& a, const Tile& tl, c
   const int cg0 = threadIdx.x >> 7, v0 = 2 * (threadIdx.x & 127);
 #pragma unroll
   for (int g = 0; g < G; ++g) r.x[g][0] = r.x[g][1] = zero_op<E>();
+  const char* origin = chunk_origin(a, tl, c, z, ybase, ystride, col0);
 #pragma unroll
   for (int e = 0; e < 2; ++e) {
     if (v0 + e < c.nv) {
-      const E* p = chunk_voxel_ptr(a, tl, c, z, ybase, ystride, col0 + 8 * cg0, v0 + e);
+      const E* p = chunk_voxel<E>(origin, a, c, ystride, 8 * cg0, v0 + e);
 #pragma unroll
       for (int g = 0; g < G; ++g) r.x[g][e] = load_op<E>(p + 8 * P * g);
     }
@@ -564,33 +579,35 @@ __device__ __forceinline__ void zero_table(float* table, int nvp) {
   }
 }
 
-// Does this slot have corners on plane z of chunk c?  Returns the z weight.
-__device__ __forceinline__ bool slot_hits(const Slot& s, int z, int chunk, float& wz, float& dwz) {
-  const int z0 = slot_z0(s);
-  if (slot_chunk(s) != chunk) return false;
-  if (z0 == z) {
-    wz = 1.0f - s.fz;
-    dwz = -1.0f;
-    return true;
-  }
-  if (slot_hz(s) && z0 + 1 == z) {
-    wz = s.fz;
-    dwz = 1.0f;
-    return true;
-  }
-  return false;
+// Step key of (chunk, plane z): chunk << 16 | z.  A slot's key is that of its
+// lower plane z0 (an empty slot's z0 field 0xffff matches no plane), so the
+// distance d = step key - slot key is 0 on the lower plane and 1 on the upper
+// one (a tap's planes are consecutive steps of its chunk); one subtraction
+// replaces the chunk and plane compares.
+__device__ __forceinline__ uint32_t step_key(int chunk, int z) {
+  return (static_cast<uint32_t>(chunk) << 16) | static_cast<uint32_t>(z);
+}
+__device__ __forceinline__ uint32_t slot_key(const Slot& s) {
+  return (static_cast<uint32_t>(s.idx) & 0xffff0000u) | (static_cast<uint32_t>(s.zc) & 0xffffu);
+}
+
+// Does this slot have corners on the step's plane?  Returns the z weight.
+__device__ __forceinline__ bool slot_hits(const Slot& s, uint32_t key, float& wz, float& dwz) {
+  const uint32_t d = key - slot_key(s);
+  if (d > static_cast<uint32_t>(slot_hz(s))) return false;
+  wz = d == 0 ? 1.0f - s.fz : s.fz;
+  dwz = d == 0 ? -1.0f : 1.0f;
+  return true;
 }
 
 // Branch-free form of slot_hits: the z weight (0 when the slot has no corners
-// on plane z of chunk c), its z derivative sign (0 likewise) and the hit flag.
-__device__ __forceinline__ bool slot_weight(const Slot& s, int z, int chunk, float& wz, float& dwz) {
-  const int z0 = slot_z0(s);
-  const bool same = slot_chunk(s) == chunk;
-  const bool h0 = same && z0 == z;
-  const bool h1 = same && slot_hz(s) && z0 + 1 == z;
-  wz = h0 ? 1.0f - s.fz : (h1 ? s.fz : 0.0f);
-  dwz = h0 ? -1.0f : (h1 ? 1.0f : 0.0f);
-  return h0 || h1;
+// on the step's plane), its z derivative sign (0 likewise) and the hit flag.
+__device__ __forceinline__ bool slot_weight(const Slot& s, uint32_t key, float& wz, float& dwz) {
+  const uint32_t d = key - slot_key(s);
+  const bool hit = d <= static_cast<uint32_t>(slot_hz(s));
+  wz = hit ? (d == 0 ? 1.0f - s.fz : s.fz) : 0.0f;
+  dwz = hit ? (d == 0 ? -1.0f : 1.0f) : 0.0f;
+  return hit;
 }
 
 // Table values at the slot's 4 (y, x) corners of the current plane.  A corner
