@@ -123,7 +123,8 @@ __global__ __launch_bounds__(kThreads, (fwd_min_waves<HD, E>())) void dsa3d_fwd_
   for (int m = 1; m < kSubs; m <<= 1) den += __shfl_xor(den, m);
   const float inv_den = 1.0f / den;
 #pragma unroll
-  for (int i = 0; i < kSlots; ++i) sc[i] *= inv_den * slot_dropout(sl[i], a.drop);  // p (dropped)
+  for (int i = 0; i < kSlots; ++i)
+    sc[i] *= inv_den * slot_dropout(sl[i], a.drop) * kFixA;  // p (dropped), fixed-point units
   if (lse != nullptr && tl.q_ok && tl.sub == 0) lse[tl.qn * a.nh + tl.head] = mx + logf(den);
 
   // ---- pass 2: O = A . V ------------------------------------------------------
@@ -163,7 +164,7 @@ __global__ __launch_bounds__(kThreads, (fwd_min_waves<HD, E>())) void dsa3d_fwd_
     for (int i = 0; i < kSlots; ++i) {
       float wz, dwz;
       if (!slot_hits(sl[i], step_key(c.id, z), wz, dwz)) continue;
-      const float pz = sc[i] * wz * kFixA;
+      const float pz = sc[i] * wz;
       const float gx = 1.0f - sl[i].fx, gy = 1.0f - sl[i].fy;
       const int base = sl[i].idx & 0x1ff, dy = (sl[i].idx >> 9) & 0x1f, dx = (sl[i].idx >> 14) & 1;
       // an upper corner outside the volume has offset 0 and weight 0: it adds 0
@@ -391,8 +392,12 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
     float* __restrict__ dv_acc) {
   static_assert(HD % CW == 0 && CW % 32 == 0, "channel windows are whole 32-channel blocks");
   constexpr int KR = ElemT<E>::kRow, QR = p2_qrow<E>();
-  __shared__ __attribute__((aligned(16))) int s_at[kChunkNV * kP2Row];  // A^T = p w (fixed point)
-  __shared__ __attribute__((aligned(16))) int s_bt[kChunkNV * kP2Row];  // B^T = ds scale w (fixed point)
+  // A^T = p w and B^T = ds scale w (fixed point), one array: a B^T entry is its
+  // A^T entry plus a constant, which the LDS instructions take as an offset
+  constexpr int kTab = kChunkNV * kP2Row;
+  __shared__ __attribute__((aligned(16))) int s_ab[2 * kTab];
+  int* const s_at = s_ab;
+  int* const s_bt = s_ab + kTab;
   __shared__ __attribute__((aligned(16))) word_t<E> s_kt[CW * KR];      // K^T chunk
   // per voxel: element offset (token row within the sample times D) of its accumulator row
   __shared__ __attribute__((aligned(16))) int s_rows[kChunkNV];
@@ -429,6 +434,12 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
   const bool l1_ok = l1 > 1e-30f;
   const float bscale = l1_ok ? kFixA / l1 : 0.0f;
   if (tl.sub == 0) s_binv[tl.q] = l1_ok ? l1 * kFixAInv : 0.0f;
+  // p and ds scale in fixed-point units from here on
+#pragma unroll
+  for (int i = 0; i < kP2Slots; ++i) {
+    p[i] *= kFixA;
+    bsc[i] *= bscale;
+  }
   __syncthreads();
   // stage q and dO of the tile transposed, carrying the fixed-point scales of
   // B (per query) and A (2^-30) for the dK/dV products: item e moves 8
@@ -500,7 +511,7 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
     for (int i = 0; i < kP2Slots; ++i) {
       float wz, dwz;
       if (!slot_hits(sl[i], step_key(c.id, z), wz, dwz)) continue;
-      const float pz = p[i] * wz * kFixA, bz = bsc[i] * wz * bscale;
+      const float pz = p[i] * wz, bz = bsc[i] * wz;
       const float fx = sl[i].fx, fy = sl[i].fy, gx = 1.0f - fx, gy = 1.0f - fy;
       const float w00 = gy * gx, w01 = gy * fx, w10 = fy * gx, w11 = fy * fx;
       // decode the corner index here rather than keeping 4 addresses per tap live
@@ -508,18 +519,20 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
       int idx = sl[i].idx;
       asm volatile("" : "+v"(idx));
       const int base = idx & 0x1ff, dy = (idx >> 9) & 0x1f, dx = (idx >> 14) & 1;
-      int* ra = &s_at[base * kP2Row + tl.q];
-      int* rb = &s_bt[base * kP2Row + tl.q];
+      int* const r00 = &s_ab[base * kP2Row + tl.q];
+      int* const r01 = r00 + dx * kP2Row;
+      int* const r10 = r00 + dy * kP2Row;
+      int* const r11 = r10 + dx * kP2Row;
       // an upper corner outside the volume has offset 0 and weight 0: it adds 0
       // to the lower corner, so all eight adds run without branches
-      atomicAdd(ra, to_fix(pz * w00));
-      atomicAdd(rb, to_fix(bz * w00));
-      atomicAdd(ra + dx * kP2Row, to_fix(pz * w01));
-      atomicAdd(rb + dx * kP2Row, to_fix(bz * w01));
-      atomicAdd(ra + dy * kP2Row, to_fix(pz * w10));
-      atomicAdd(rb + dy * kP2Row, to_fix(bz * w10));
-      atomicAdd(ra + (dy + dx) * kP2Row, to_fix(pz * w11));
-      atomicAdd(rb + (dy + dx) * kP2Row, to_fix(bz * w11));
+      atomicAdd(r00, to_fix(pz * w00));
+      atomicAdd(r00 + kTab, to_fix(bz * w00));
+      atomicAdd(r01, to_fix(pz * w01));
+      atomicAdd(r01 + kTab, to_fix(bz * w01));
+      atomicAdd(r10, to_fix(pz * w10));
+      atomicAdd(r10 + kTab, to_fix(bz * w10));
+      atomicAdd(r11, to_fix(pz * w11));
+      atomicAdd(r11 + kTab, to_fix(bz * w11));
     }
     __syncthreads();
     // dq[q] += sum_v B[q][v] K[v]; in bf16, B as a hi/lo pair because
