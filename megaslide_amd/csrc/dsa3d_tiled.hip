@@ -361,8 +361,8 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p1_kernel(
 
 }
 
-// Second backward kernel: dq, dK and dV for tiles of kP2Frames consecutive
-// frames (kP2Q queries) of one 4x4 (h, w) column, over a window of CW of the
+// Second backward kernel: dq, dK and dV for tiles of FR consecutive frames
+// (16 FR queries) of one 4x4 (h, w) column, over a window of CW of the
 // head's HD channels (window blockIdx.z).  Consecutive frames reach nearly the
 // same planes, so one flush of the [voxel][query] tables per plane serves all
 // of them: the fp32 dK/dV atomics (executed past the L2, the backward's
@@ -371,27 +371,35 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p1_kernel(
 // kernel.  The A and B tables do not depend on the channel, so a window
 // narrower than the head rebuilds them per window in exchange for fewer
 // registers and less LDS.
-constexpr int kP2Frames = 2;
-constexpr int kP2Q = kTQ * kP2Frames;          // queries per tile
-constexpr int kP2Subs = kThreads / kP2Q;       // lanes per query
-constexpr int kP2Slots = kMaxTaps / kP2Subs;   // taps per lane
-constexpr int kP2Row = kP2Q + 2;               // [voxel][query] table row (ints)
-static_assert(kP2Subs * kP2Slots == kMaxTaps, "the tap capacity must match the first kernel");
+template <int FR>
+struct P2Tile {
+  static constexpr int Q = kTQ * FR;              // queries per tile
+  static constexpr int Waves = 4 * FR;            // 16 lanes per query
+  static constexpr int Threads = 64 * Waves;
+  static constexpr int Subs = Threads / Q;        // lanes per query
+  static constexpr int Slots = kMaxTaps / Subs;   // taps per lane
+  static constexpr int Row = Q + 2;               // [voxel][query] table row (ints)
+  static_assert(Subs * Slots == kMaxTaps, "the tap capacity must match the first kernel");
+};
+constexpr int kP2Stage = 512;  // threads that stage the K^T chunk
 
-// [channel][query] row of the staged q / dO (elements): 80 bytes for bf16, 144
-// bytes (= 36 banks: 16 rows of 16-byte reads conflict-free) for fp32.
-template <typename E>
+// [channel][query] row of the staged q / dO (elements): 16 FR + 8 bf16 (16 FR + 4
+// fp32, = 36 banks at FR 2: 16 rows of 16-byte reads conflict-free).
+template <typename E, int FR>
 constexpr int p2_qrow() {
-  return sizeof(E) == 2 ? kP2Q + 8 : kP2Q + 4;
+  return sizeof(E) == 2 ? kTQ * FR + 8 : kTQ * FR + 4;
 }
 
-template <int HD, int CW, typename E>
-__global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
+template <int HD, int CW, typename E, int FR>
+__global__ __launch_bounds__(P2Tile<FR>::Threads) void dsa3d_bwd_p2_kernel(
     Args a, const E* __restrict__ dout, const float* __restrict__ p_ws,
     const float* __restrict__ b_ws, E* __restrict__ dq, float* __restrict__ dk_acc,
     float* __restrict__ dv_acc) {
   static_assert(HD % CW == 0 && CW % 32 == 0, "channel windows are whole 32-channel blocks");
-  constexpr int KR = ElemT<E>::kRow, QR = p2_qrow<E>();
+  using G = P2Tile<FR>;
+  constexpr int kP2Frames = FR, kP2Q = G::Q, kP2Subs = G::Subs, kP2Slots = G::Slots;
+  constexpr int kP2Row = G::Row, NW = G::Waves, NT = G::Threads;
+  constexpr int KR = ElemT<E>::kRow, QR = p2_qrow<E, FR>();
   // A^T = p w and B^T = ds scale w (fixed point), one array: a B^T entry is its
   // A^T entry plus a constant, which the LDS instructions take as an offset
   constexpr int kTab = kChunkNV * kP2Row;
@@ -401,7 +409,7 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
   __shared__ __attribute__((aligned(16))) word_t<E> s_kt[CW * KR];      // K^T chunk
   // per voxel: element offset (token row within the sample times D) of its accumulator row
   __shared__ __attribute__((aligned(16))) int s_rows[kChunkNV];
-  __shared__ int s_red[kWaves][6];
+  __shared__ int s_red[NW][6];
   __shared__ __attribute__((aligned(16))) float s_binv[kP2Q];  // per query: 1 / fixed-point scale of B
   // the tile's q and dO rows of this window, transposed: [tensor][channel][query]
   __shared__ __attribute__((aligned(16))) word_t<E> s_qt[2][CW][QR];
@@ -411,7 +419,7 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
   const int cw0 = tl.head * HD + CW * static_cast<int>(blockIdx.z);  // first channel of the window
   Slot sl[kP2Slots];
   Box box;
-  setup_slots<E, kP2Subs, kP2Slots>(a, tl, sl, box, s_red);
+  setup_slots<E, kP2Subs, kP2Slots, NW>(a, tl, sl, box, s_red);
   const int nchunks = box.ncy * box.ncx;
   const int nit = (box.zhi - box.zlo + 1) * nchunks;
 
@@ -444,7 +452,7 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
   // stage q and dO of the tile transposed, carrying the fixed-point scales of
   // B (per query) and A (2^-30) for the dK/dV products: item e moves 8
   // channels of one row
-  for (int e = threadIdx.x; e < 2 * kP2Q * (CW / 8); e += kThreads) {
+  for (int e = threadIdx.x; e < 2 * kP2Q * (CW / 8); e += NT) {
     const int cg = e % (CW / 8), m = (e / (CW / 8)) % kP2Q, tensor = e / (kP2Q * (CW / 8));
     const int64_t n = tile_row(a, tl, m);
     op_t<E> x = zero_op<E>();
@@ -479,8 +487,8 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
   // for t = w + 8 i.
   constexpr int CT = CW / 16, NC2 = CW / 32;
   constexpr bool DQK = CW == 64;  // k-split dq
-  constexpr int KPQ = kWaves / kP2Frames;  // k phases per frame (k-split dq)
-  constexpr int NDQ = DQK ? CT : (kP2Frames * CT + kWaves - 1) / kWaves;  // dq accumulators
+  constexpr int KPQ = NW / kP2Frames;  // k phases per frame (k-split dq)
+  constexpr int NDQ = DQK ? CT : (kP2Frames * CT + NW - 1) / NW;  // dq accumulators
   const int mq = tl.lane & 15, kq = 8 * (tl.lane >> 4);
   // operands of the dK/dV MFMAs are re-read from LDS where used (registers are
   // the limit here: a spill reload would wait for every outstanding atomic)
@@ -489,35 +497,44 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
 #pragma unroll
   for (int j = 0; j < NDQ; ++j) dq_acc[j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
   const E* const kp = static_cast<const E*>(a.k);
-  StageRows<kThreads, CW, E> kr;
+  // K rows of the next (plane, chunk) are loaded while the current one is used,
+  // except with three frames, whose registers are too few to keep them live
+  // across the step (the kernel is atomic-bound there anyway)
+  constexpr bool kPrefetchK = FR == 2;
+  StageRows<kP2Stage, CW, E> kr;
   Walk w = walk_begin(box);
-  if (nit > 0) load_stage_rows<kThreads, CW, E>(a, tl, w.c, w.z, kp, a.ks, cw0, kr);
+  if (kPrefetchK && nit > 0) load_stage_rows<kP2Stage, CW, E>(a, tl, w.c, w.z, kp, a.ks, cw0, kr);
   for (int it = 0; it < nit; ++it) {
     const Walk wn = walk_next(box, w);
     const Chunk& c = w.c;
     const int z = w.z;
+    if (!kPrefetchK) load_stage_rows<kP2Stage, CW, E>(a, tl, c, z, kp, a.ks, cw0, kr);
     // zero the transposed A and B tables; token rows of the chunk's voxels
-    for (int e = threadIdx.x; e < c.nvp * kP2Row / 4; e += kThreads) {
+    for (int e = threadIdx.x; e < c.nvp * kP2Row / 4; e += NT) {
       const u32x4_t zz = {0u, 0u, 0u, 0u};
       __builtin_memcpy(&s_at[4 * e], &zz, sizeof(zz));
       __builtin_memcpy(&s_bt[4 * e], &zz, sizeof(zz));
     }
-    for (int vi = threadIdx.x; vi < c.nv; vi += kThreads)
+    for (int vi = threadIdx.x; vi < c.nv; vi += NT)
       s_rows[vi] = static_cast<int>(chunk_row(a, tl, c, z, vi) - tl.sample0) * D;
-    store_stage<kThreads, CW, E>(c, kr, s_kt);
-    if (it + 1 < nit) load_stage_rows<kThreads, CW, E>(a, tl, wn.c, wn.z, kp, a.ks, cw0, kr);
+    store_stage<kP2Stage, CW, E>(c, kr, s_kt);
+    if (kPrefetchK && it + 1 < nit)
+      load_stage_rows<kP2Stage, CW, E>(a, tl, wn.c, wn.z, kp, a.ks, cw0, kr);
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < kP2Slots; ++i) {
+      // the slot words are re-read opaquely each step, so the corner addresses,
+      // weights and keys derived from them are not hoisted out of the plane
+      // loop (registers are the limit: a spill reload would wait for every
+      // outstanding atomic)
+      Slot si = sl[i];
+      asm volatile("" : "+v"(si.zc), "+v"(si.idx), "+v"(si.fx), "+v"(si.fy));
       float wz, dwz;
-      if (!slot_hits(sl[i], step_key(c.id, z), wz, dwz)) continue;
+      if (!slot_hits(si, step_key(c.id, z), wz, dwz)) continue;
       const float pz = p[i] * wz, bz = bsc[i] * wz;
-      const float fx = sl[i].fx, fy = sl[i].fy, gx = 1.0f - fx, gy = 1.0f - fy;
+      const float fx = si.fx, fy = si.fy, gx = 1.0f - fx, gy = 1.0f - fy;
       const float w00 = gy * gx, w01 = gy * fx, w10 = fy * gx, w11 = fy * fx;
-      // decode the corner index here rather than keeping 4 addresses per tap live
-      // across the plane loop
-      int idx = sl[i].idx;
-      asm volatile("" : "+v"(idx));
+      const int idx = si.idx;
       const int base = idx & 0x1ff, dy = (idx >> 9) & 0x1f, dx = (idx >> 14) & 1;
       int* const r00 = &s_ab[base * kP2Row + tl.q];
       int* const r01 = r00 + dx * kP2Row;
@@ -552,7 +569,7 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
     } else {
 #pragma unroll
       for (int j = 0; j < NDQ; ++j) {
-        const int t = tl.wave + kWaves * j;
+        const int t = tl.wave + NW * j;
         if (t >= kP2Frames * CT) continue;
         const int fq = t / CT, ct = t % CT;
         for (int kc = 0; kc < c.nvp; kc += 32) {
@@ -567,7 +584,7 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
     }
     // dK[v] += sum_q B[q][v] q[q];  dV[v] += sum_q A[q][v] dO[q]  (32x32 MFMA, fp32
     // atomics; one register across the wave covers 2 voxels x 32 contiguous channels)
-    for (int t = tl.wave;; t += kWaves) {
+    for (int t = tl.wave;; t += NW) {
       const int c2 = t % NC2, vb = t / NC2;
       if (vb * 32 >= c.nv) break;
       const int och = 32 * c2 + (tl.lane & 31);
@@ -609,7 +626,7 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
     // lane%16] of k phase w % 4; the A^T table (free after the loop's last
     // barrier) takes the partials, and every thread sums 4 for its outputs
     float* red = reinterpret_cast<float*>(s_at);  // [frame][k phase][16][CW]
-    static_assert(kWaves * kTQ * CW <= kChunkNV * kP2Row, "partials fit the A^T table");
+    static_assert(NW * kTQ * CW <= kChunkNV * kP2Row, "partials fit the A^T table");
     const int fq = tl.wave / KPQ, kph = tl.wave % KPQ;
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct)
@@ -617,7 +634,7 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
       for (int r = 0; r < 4; ++r)
         red[((fq * KPQ + kph) * kTQ + 4 * (tl.lane >> 4) + r) * CW + 16 * ct + mq] = dq_acc[ct][r];
     __syncthreads();
-    for (int e = threadIdx.x; e < kP2Q * CW; e += kThreads) {
+    for (int e = threadIdx.x; e < kP2Q * CW; e += NT) {
       const int m = e / CW, ch = e - m * CW, f = m / kTQ, mm = m % kTQ;
       float v = 0.0f;
 #pragma unroll
@@ -629,7 +646,7 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p2_kernel(
     // dq_acc[j][r] = dq[query 16*fq + 4*(lane/16) + r][channel 16*ct + lane%16]
 #pragma unroll
     for (int j = 0; j < NDQ; ++j) {
-      const int t = tl.wave + kWaves * j;
+      const int t = tl.wave + NW * j;
       if (t >= kP2Frames * CT) continue;
       const int fq = t / CT, ct = t % CT;
 #pragma unroll
@@ -792,25 +809,35 @@ constexpr int p2_window() {
   return sizeof(E) == 2 ? HD : (HD % 64 == 0 ? 64 : 32);
 }
 
+// Frames per tile of the second kernel: 3 where the LDS takes the larger
+// tables (bf16 head_dim 64), else 2.
 template <int HD, typename E>
-void launch_bwd_pair(const msd_dsa3d_desc& d, const tiled::Args& a1, const tiled::Args& a2,
-                     const E* o, const E* go, const float* lse, const float* dlse, E* gq, E* goff,
-                     float* p_ws, float* b_ws, float* dk_acc, float* dv_acc, hipStream_t s) {
-  constexpr int CW = p2_window<HD, E>();
-  const dim3 block(tiled::kThreads), g1 = tiled_grid<1>(d);
-  dim3 g2 = tiled_grid<kP2Frames>(d);
+constexpr int p2_frames() {
+  return sizeof(E) == 2 && HD == 64 ? 3 : 2;
+}
+
+template <int HD, typename E>
+void launch_bwd_pair(const msd_dsa3d_desc& d, const void* q, const void* k, const void* v,
+                     const void* off, const E* o, const E* go, const float* lse,
+                     const float* dlse, E* gq, E* goff, float* p_ws, float* b_ws, float* dk_acc,
+                     float* dv_acc, hipStream_t s) {
+  constexpr int CW = p2_window<HD, E>(), FR = p2_frames<HD, E>();
+  const tiled::Args a1 = make_tiled_args(d, q, k, v, off, tiled_tiles<1>(d));
+  const tiled::Args a2 = make_tiled_args(d, q, k, v, off, tiled_tiles<FR>(d));
+  const dim3 g1 = tiled_grid<1>(d);
+  dim3 g2 = tiled_grid<FR>(d);
   g2.z = HD / CW;
-  hipLaunchKernelGGL((dsa3d_bwd_p1_kernel<HD, E>), g1, block, 0, s, a1, o, go, lse, dlse, goff,
-                     p_ws, b_ws);
-  hipLaunchKernelGGL((dsa3d_bwd_p2_kernel<HD, CW, E>), g2, block, 0, s, a2, go, p_ws, b_ws, gq,
-                     dk_acc, dv_acc);
+  hipLaunchKernelGGL((dsa3d_bwd_p1_kernel<HD, E>), g1, dim3(tiled::kThreads), 0, s, a1, o, go,
+                     lse, dlse, goff, p_ws, b_ws);
+  hipLaunchKernelGGL((dsa3d_bwd_p2_kernel<HD, CW, E, FR>), g2, dim3(P2Tile<FR>::Threads), 0, s,
+                     a2, go, p_ws, b_ws, gq, dk_acc, dv_acc);
 }
 
 template <typename E>
-hipError_t bwd_tiled_typed(const msd_dsa3d_desc& d, const tiled::Args& a1, const tiled::Args& a2,
-                           const void* out, const void* dout, const float* lse, const float* dlse,
-                           void* dq, void* dk, void* dv, void* doff, float* dk_acc,
-                           float* dv_acc, float* p_ws, float* b_ws, hipStream_t s) {
+hipError_t bwd_tiled_typed(const msd_dsa3d_desc& d, const void* q, const void* k, const void* v,
+                           const void* off, const void* out, const void* dout, const float* lse,
+                           const float* dlse, void* dq, void* dk, void* dv, void* doff,
+                           float* dk_acc, float* dv_acc, float* p_ws, float* b_ws, hipStream_t s) {
   const int64_t rows = static_cast<int64_t>(d.B) * d.T * d.H * d.W;
   const int D = d.num_heads * d.head_dim;
   const auto* o = static_cast<const E*>(out);
@@ -819,13 +846,16 @@ hipError_t bwd_tiled_typed(const msd_dsa3d_desc& d, const tiled::Args& a1, const
   auto* goff = static_cast<E*>(doff);
   switch (d.head_dim) {
     case 64:
-      launch_bwd_pair<64, E>(d, a1, a2, o, go, lse, dlse, gq, goff, p_ws, b_ws, dk_acc, dv_acc, s);
+      launch_bwd_pair<64, E>(d, q, k, v, off, o, go, lse, dlse, gq, goff, p_ws, b_ws, dk_acc,
+                               dv_acc, s);
       break;
     case 96:
-      launch_bwd_pair<96, E>(d, a1, a2, o, go, lse, dlse, gq, goff, p_ws, b_ws, dk_acc, dv_acc, s);
+      launch_bwd_pair<96, E>(d, q, k, v, off, o, go, lse, dlse, gq, goff, p_ws, b_ws, dk_acc,
+                               dv_acc, s);
       break;
     case 128:
-      launch_bwd_pair<128, E>(d, a1, a2, o, go, lse, dlse, gq, goff, p_ws, b_ws, dk_acc, dv_acc, s);
+      launch_bwd_pair<128, E>(d, q, k, v, off, o, go, lse, dlse, gq, goff, p_ws, b_ws, dk_acc,
+                               dv_acc, s);
       break;
     default:
       return hipErrorInvalidValue;
@@ -861,13 +891,11 @@ hipError_t launch_dsa3d_bwd_tiled(const msd_dsa3d_desc& d, const void* q, const 
   float* b_ws = p_ws + taps;
   hipLaunchKernelGGL(fill_zero_f32, dim3(fill_blocks(2 * rows * D)), dim3(256), 0, s, dk_acc,
                      2 * rows * D);
-  const tiled::Args a1 = make_tiled_args(d, q, k, v, off, tiled_tiles<1>(d));
-  const tiled::Args a2 = make_tiled_args(d, q, k, v, off, tiled_tiles<kP2Frames>(d));
   if (d.dtype == MSD_BF16)
-    return bwd_tiled_typed<bf16>(d, a1, a2, out, dout, lse, dlse, dq, dk, dv, doff, dk_acc, dv_acc,
-                                 p_ws, b_ws, s);
-  return bwd_tiled_typed<float>(d, a1, a2, out, dout, lse, dlse, dq, dk, dv, doff, dk_acc, dv_acc,
-                                p_ws, b_ws, s);
+    return bwd_tiled_typed<bf16>(d, q, k, v, off, out, dout, lse, dlse, dq, dk, dv, doff, dk_acc,
+                                 dv_acc, p_ws, b_ws, s);
+  return bwd_tiled_typed<float>(d, q, k, v, off, out, dout, lse, dlse, dq, dk, dv, doff, dk_acc,
+                                dv_acc, p_ws, b_ws, s);
 }
 
 }  // namespace msd

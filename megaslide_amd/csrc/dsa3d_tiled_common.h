@@ -223,7 +223,7 @@ __device__ __forceinline__ float grid_coord_rn(float base, float o, float div, f
 // Tap geometry for all SLOTS slots of this lane (coordinates exactly as the
 // reference rounds them) and the block-wide bounding box of every corner.
 // With `dropout`, each tap's keep decision is drawn here once (bit 20 of zc).
-template <typename E, int SUBS, int SLOTS>
+template <typename E, int SUBS, int SLOTS, int NW = kWaves>
 __device__ __forceinline__ void setup_slots(const Args& a, const Tile& tl, Slot* sl, Box& box,
                                             int (*s_red)[6], bool dropout = false) {
   int zlo = 1 << 30, zhi = -1, ylo = 1 << 30, yhi = -1, xlo = 1 << 30, xhi = -1;
@@ -302,7 +302,7 @@ __device__ __forceinline__ void setup_slots(const Args& a, const Tile& tl, Slot*
   box.xlo = s_red[0][4];
   box.xhi = s_red[0][5];
 #pragma unroll
-  for (int w = 1; w < kWaves; ++w) {
+  for (int w = 1; w < NW; ++w) {
     box.zlo = min(box.zlo, s_red[w][0]);
     box.zhi = max(box.zhi, s_red[w][1]);
     box.ylo = min(box.ylo, s_red[w][2]);
@@ -527,6 +527,7 @@ __device__ __forceinline__ void load_stage_rows(const Args& a, const Tile& tl, c
   const int cg0 = threadIdx.x >> 7, v0 = 2 * (threadIdx.x & 127);
 #pragma unroll
   for (int g = 0; g < G; ++g) r.x[g][0] = r.x[g][1] = zero_op<E>();
+  if (threadIdx.x >= NT) return;  // a larger workgroup: the other threads do not stage
   const char* origin = chunk_origin(a, tl, c, z, ybase, ystride, col0);
 #pragma unroll
   for (int e = 0; e < 2; ++e) {
@@ -544,7 +545,7 @@ __device__ __forceinline__ void store_stage(const Chunk& c, const StageRows<NT, 
   constexpr int P = StageRows<NT, CW, E>::P, G = StageRows<NT, CW, E>::G;
   constexpr int R = ElemT<E>::kRow;
   const int cg0 = threadIdx.x >> 7, v0 = 2 * (threadIdx.x & 127);
-  if (v0 >= c.nvp) return;
+  if (threadIdx.x >= NT || v0 >= c.nvp) return;
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     const int ch0 = 8 * (cg0 + P * g);
