@@ -800,20 +800,22 @@ __global__ __launch_bounds__(256) void acc_to_out_kernel(const float* __restrict
   }
 }
 
-// Channel window of the second backward kernel.  bf16 takes the whole head
-// (for head_dim 128, two windows of 64 measured 4% slower than one of 128);
-// fp32 K^T and q/dO stages are twice as large, so windows of 64 (32 for
-// head_dim 96) keep them within the LDS.
-template <int HD, typename E>
-constexpr int p2_window() {
-  return sizeof(E) == 2 ? HD : (HD % 64 == 0 ? 64 : 32);
-}
-
-// Frames per tile of the second kernel: 3 where the LDS takes the larger
-// tables (bf16 head_dim 64), else 2.
+// Frames per tile of the second kernel: 3 for bf16 head_dim 64 and 128 (at
+// the 131,072-token hd-128 shape three frames in two 64-channel windows ran
+// 15% faster than two frames in one window), else 2 (bf16 hd 96 would need
+// three 32-channel windows for three frames: 8% slower).
 template <int HD, typename E>
 constexpr int p2_frames() {
-  return sizeof(E) == 2 && HD == 64 ? 3 : 2;
+  return sizeof(E) == 2 && HD != 96 ? 3 : 2;
+}
+
+// Channel window of the second backward kernel: the whole head where the LDS
+// takes its K^T and q/dO stages beside the tables, else 64 channels (32 for
+// fp32 head_dim 96).
+template <int HD, typename E>
+constexpr int p2_window() {
+  if constexpr (sizeof(E) == 2) return p2_frames<HD, E>() == 3 ? 64 : HD;
+  return HD % 64 == 0 ? 64 : 32;
 }
 
 template <int HD, typename E>
