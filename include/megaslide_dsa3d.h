@@ -75,7 +75,7 @@ typedef struct msd_dsa3d_desc {
 } msd_dsa3d_desc;
 
 /* Kernel family for the attention core.  AUTO picks the matrix-core tiled
- * kernels when the call qualifies (bf16 or fp32, head_dim 64/96/128, <= 160
+ * kernels when the call qualifies (bf16 or fp32, head_dim 32/64/96/128, <= 160
  * taps, token strides multiples of 8 elements, 16-byte aligned rows) and the
  * direct kernels otherwise.  DIRECT and TILED force one family (TILED fails
  * with MSD_ERR_UNSUPPORTED if not eligible). */

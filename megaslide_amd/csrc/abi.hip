@@ -102,7 +102,7 @@ int msd_dsa3d_fwd(const msd_dsa3d_desc* desc, const void* q, const void* k, cons
   const bool tiled_ok = msd::dsa3d_tiled_supported(*desc, q, k, v);
   if (desc->algo == MSD_ALGO_TILED && !tiled_ok)
     return fail(MSD_ERR_UNSUPPORTED,
-                "dsa3d_fwd: tiled kernels need bf16 or fp32, head_dim 64, 96 or 128, <= 160 taps and "
+                "dsa3d_fwd: tiled kernels need bf16 or fp32, head_dim 32, 64, 96 or 128, <= 160 taps and "
                 "16-byte aligned rows");
   if (desc->B == 0) return MSD_OK;
   const hipStream_t s = static_cast<hipStream_t>(stream);
@@ -141,7 +141,7 @@ int msd_dsa3d_bwd(const msd_dsa3d_desc* desc, const void* q, const void* k, cons
                         msd::dsa3d_tiled_supported(*desc, dq, dk, dv);
   if (desc->algo == MSD_ALGO_TILED && !tiled_ok)
     return fail(MSD_ERR_UNSUPPORTED,
-                "dsa3d_bwd: tiled kernels need bf16 or fp32, head_dim 64, 96 or 128, <= 160 taps and "
+                "dsa3d_bwd: tiled kernels need bf16 or fp32, head_dim 32, 64, 96 or 128, <= 160 taps and "
                 "16-byte aligned rows");
   if (tiled_ok && desc->algo != MSD_ALGO_DIRECT)
     return launch_status(msd::launch_dsa3d_bwd_tiled(*desc, q, k, v, offsets, out, dout, lse, dlse,

@@ -1,5 +1,5 @@
 // Matrix-core (tiled) 3D-DSA forward and backward for gfx950: bf16 or fp32
-// storage, fp32 accumulation, head_dim 64, 96 or 128.
+// storage, fp32 accumulation, head_dim 32, 64, 96 or 128.
 //
 // One workgroup = one (batch, head, tile of 16 queries).  Instead of gathering
 // the 8 corner rows of K and V for each of a query's taps, it builds dense
@@ -44,10 +44,21 @@ constexpr int fwd_table_bufs() {
   return 2 * kTabBytes + vt <= kLdsBytes ? 2 : 1;       // one workgroup per CU
 }
 
-// Minimum waves per SIMD: 4 when two 512-thread workgroups fit in a CU's LDS.
+// Minimum waves per SIMD: 4 when two 512-thread workgroups fit in a CU's LDS
+// (bf16; the fp32 operands need more than 128 registers).
 template <int HD, typename E>
 constexpr int fwd_min_waves() {
+  if constexpr (sizeof(E) == 4) return 2;
   return 2 * (fwd_table_bufs<HD, E>() * kTabBytes + fwd_vt_bytes<HD, E>()) <= kLdsBytes ? 4 : 2;
+}
+
+// Slot words as used in the forward's plane loops: at head_dim 96 (128
+// registers at 4 waves/SIMD) opaque, which stops the hoisting that spilled
+// (10% faster); elsewhere the hoisted keys and weights are cheaper (5%).
+template <int HD>
+__device__ __forceinline__ Slot fwd_slot(const Slot& s) {
+  if constexpr (HD == 96) return opaque(s);
+  return s;
 }
 
 template <int HD, typename E>
@@ -92,12 +103,14 @@ __global__ __launch_bounds__(kThreads, (fwd_min_waves<HD, E>())) void dsa3d_fwd_
     const float* my_row = &tab[tl.q * kSRow];
     float t[kSlots][4];
 #pragma unroll
-    for (int i = 0; i < kSlots; ++i) corners4(sl[i], my_row, t[i][0], t[i][1], t[i][2], t[i][3]);
+    for (int i = 0; i < kSlots; ++i)
+      corners4(fwd_slot<HD>(sl[i]), my_row, t[i][0], t[i][1], t[i][2], t[i][3]);
 #pragma unroll
     for (int i = 0; i < kSlots; ++i) {
+      const Slot si = fwd_slot<HD>(sl[i]);
       float wz, dwz;
-      const bool hit = slot_weight(sl[i], step_key(c.id, z), wz, dwz);
-      const float v = bilerp(sl[i], t[i][0], t[i][1], t[i][2], t[i][3]).val;
+      const bool hit = slot_weight(si, step_key(c.id, z), wz, dwz);
+      const float v = bilerp(si, t[i][0], t[i][1], t[i][2], t[i][3]).val;
       sc[i] = hit ? __builtin_fmaf(wz, v, sc[i]) : sc[i];
     }
     if constexpr (NB == 1) __syncthreads();  // the next step overwrites the table
@@ -162,17 +175,18 @@ __global__ __launch_bounds__(kThreads, (fwd_min_waves<HD, E>())) void dsa3d_fwd_
       load_stage_rows<kThreads, HD, E>(a, tl, wn.c, wn.z, vp, a.vs, tl.head * HD, vr);
 #pragma unroll
     for (int i = 0; i < kSlots; ++i) {
+      const Slot si = fwd_slot<HD>(sl[i]);
       float wz, dwz;
-      if (!slot_hits(sl[i], step_key(c.id, z), wz, dwz)) continue;
+      if (!slot_hits(si, step_key(c.id, z), wz, dwz)) continue;
       const float pz = sc[i] * wz;
-      const float gx = 1.0f - sl[i].fx, gy = 1.0f - sl[i].fy;
-      const int base = sl[i].idx & 0x1ff, dy = (sl[i].idx >> 9) & 0x1f, dx = (sl[i].idx >> 14) & 1;
+      const float gx = 1.0f - si.fx, gy = 1.0f - si.fy;
+      const int base = si.idx & 0x1ff, dy = (si.idx >> 9) & 0x1f, dx = (si.idx >> 14) & 1;
       // an upper corner outside the volume has offset 0 and weight 0: it adds 0
       // to the lower corner, so all four adds run without branches
       atomicAdd(&row[base], to_fix(pz * (gy * gx)));
-      atomicAdd(&row[base + dx], to_fix(pz * (gy * sl[i].fx)));
-      atomicAdd(&row[base + dy], to_fix(pz * (sl[i].fy * gx)));
-      atomicAdd(&row[base + dy + dx], to_fix(pz * (sl[i].fy * sl[i].fx)));
+      atomicAdd(&row[base + dx], to_fix(pz * (gy * si.fx)));
+      atomicAdd(&row[base + dy], to_fix(pz * (si.fy * gx)));
+      atomicAdd(&row[base + dy + dx], to_fix(pz * (si.fy * si.fx)));
     }
     __syncthreads();
     for (int kc = 32 * kph; av_wave && kc < c.nvp; kc += 32 * KP) {
@@ -718,7 +732,7 @@ dim3 tiled_grid(const msd_dsa3d_desc& d) {
 
 namespace {
 // head sizes with compiled tiled kernels
-bool tiled_head_dim(int hd) { return hd == 64 || hd == 96 || hd == 128; }
+bool tiled_head_dim(int hd) { return hd == 32 || hd == 64 || hd == 96 || hd == 128; }
 }  // namespace
 
 bool dsa3d_tiled_supported(const msd_dsa3d_desc& d, const void* q, const void* k, const void* v) {
@@ -755,6 +769,7 @@ hipError_t fwd_tiled_typed(const msd_dsa3d_desc& d, const tiled::Args& a, void* 
   const dim3 grid = tiled_grid<1>(d), block(tiled::kThreads);
   E* o = static_cast<E*>(out);
   switch (d.head_dim) {
+    case 32: hipLaunchKernelGGL((dsa3d_fwd_tiled_kernel<32, E>), grid, block, 0, s, a, o, lse); break;
     case 64: hipLaunchKernelGGL((dsa3d_fwd_tiled_kernel<64, E>), grid, block, 0, s, a, o, lse); break;
     case 96: hipLaunchKernelGGL((dsa3d_fwd_tiled_kernel<96, E>), grid, block, 0, s, a, o, lse); break;
     case 128: hipLaunchKernelGGL((dsa3d_fwd_tiled_kernel<128, E>), grid, block, 0, s, a, o, lse); break;
@@ -803,10 +818,10 @@ __global__ __launch_bounds__(256) void acc_to_out_kernel(const float* __restrict
 // Frames per tile of the second kernel: 3 for bf16 head_dim 64 and 128 (at
 // the 131,072-token hd-128 shape three frames in two 64-channel windows ran
 // 15% faster than two frames in one window), else 2 (bf16 hd 96 would need
-// three 32-channel windows for three frames: 8% slower).
+// three 32-channel windows for three frames: 8% slower; hd 32 would spill).
 template <int HD, typename E>
 constexpr int p2_frames() {
-  return sizeof(E) == 2 && HD != 96 ? 3 : 2;
+  return sizeof(E) == 2 && (HD == 64 || HD == 128) ? 3 : 2;
 }
 
 // Channel window of the second backward kernel: the whole head where the LDS
@@ -814,7 +829,7 @@ constexpr int p2_frames() {
 // fp32 head_dim 96).
 template <int HD, typename E>
 constexpr int p2_window() {
-  if constexpr (sizeof(E) == 2) return p2_frames<HD, E>() == 3 ? 64 : HD;
+  if constexpr (sizeof(E) == 2) return p2_frames<HD, E>() == 3 && HD > 64 ? 64 : HD;
   return HD % 64 == 0 ? 64 : 32;
 }
 
@@ -847,6 +862,10 @@ hipError_t bwd_tiled_typed(const msd_dsa3d_desc& d, const void* q, const void* k
   auto* gq = static_cast<E*>(dq);
   auto* goff = static_cast<E*>(doff);
   switch (d.head_dim) {
+    case 32:
+      launch_bwd_pair<32, E>(d, q, k, v, off, o, go, lse, dlse, gq, goff, p_ws, b_ws, dk_acc,
+                               dv_acc, s);
+      break;
     case 64:
       launch_bwd_pair<64, E>(d, q, k, v, off, o, go, lse, dlse, gq, goff, p_ws, b_ws, dk_acc,
                                dv_acc, s);

@@ -136,6 +136,15 @@ struct Slot {
   float fx, fy;  // weights of the upper x / y corners (0 when that corner is outside)
 };
 
+// The slot's words as opaque values at this point: keeps the compiler from
+// hoisting what it derives from them (keys, corner weights and addresses) out
+// of a plane loop, where registers are the limit.  Costs no instruction.
+__device__ __forceinline__ Slot opaque(const Slot& s) {
+  Slot r = s;
+  asm volatile("" : "+v"(r.zc), "+v"(r.idx), "+v"(r.fz), "+v"(r.fx), "+v"(r.fy));
+  return r;
+}
+
 __device__ __forceinline__ int slot_z0(const Slot& s) { return static_cast<int16_t>(s.zc & 0xffff); }
 __device__ __forceinline__ bool slot_hz(const Slot& s) { return (s.zc >> 16) & 1; }
 __device__ __forceinline__ int slot_chunk(const Slot& s) {

@@ -86,9 +86,9 @@ def test_empty_batch_is_a_no_op():
 def test_workspace_size_and_check():
     lib = _lib.load()
     rows = 2 * 4 * 5 * 6
-    # head_dim 32: direct kernels only, dK/dV fp32 accumulators
-    d32 = _desc(B=2, head_dim=32, q_stride=64, k_stride=64, v_stride=64)
-    assert lib.msd_dsa3d_bwd_workspace_size(ctypes.byref(d32)) == 2 * rows * 64 * 4
+    # head_dim 16: direct kernels only, dK/dV fp32 accumulators
+    d16 = _desc(B=2, head_dim=16, q_stride=32, k_stride=32, v_stride=32)
+    assert lib.msd_dsa3d_bwd_workspace_size(ctypes.byref(d16)) == 2 * rows * 32 * 4
     # head_dim 64, fp32 and bf16: the tiled backward also keeps p and ds of every tap
     for dtype in (0, 1):
         d = _desc(B=2, dtype=dtype)

@@ -295,7 +295,7 @@ def test_tiled_forward_vs_oracle_and_direct(shape):
 
 
 def test_tiled_rejects_ineligible_calls():
-    q = torch.zeros(1, 8, 32, device=DEV, dtype=torch.bfloat16)  # head_dim 32
+    q = torch.zeros(1, 8, 16, device=DEV, dtype=torch.bfloat16)  # head_dim 16
     off = torch.zeros(1, 8, 27 * 3, device=DEV, dtype=torch.bfloat16)
     with pytest.raises(RuntimeError, match="tiled"):
         core()(q, q, q, off, (2, 2, 2), 1, (3, 3, 3), algo="tiled")

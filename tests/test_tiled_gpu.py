@@ -1,6 +1,6 @@
 """Matrix-core (tiled) attention-core kernels: parity and invariants (GPU).
 
-The tiled kernels serve bf16 and fp32, head_dim 64, 96 and 128.  They must agree
+The tiled kernels serve bf16 and fp32, head_dim 32, 64, 96 and 128.  They must agree
 with the fp32 oracle (relative to max|ref|: bf16 2e-2, fp32 1e-4) and with the
 direct kernels; the log-sum-exp they return must match the oracle's to 1e-5.
 """
@@ -77,6 +77,8 @@ def test_tiled_constant_values():
     (1, 4, 1, 9, 2, (3, 7, 7), 1.0, 1.0, 64),     # H = 1: y slot dropped, base y divisor 1
     (1, 3, 6, 1, 1, (3, 7, 7), 1.0, 1.0, 64),     # W = 1: z slot dropped (slot/axis quirk)
     (2, 2, 3, 5, 2, (1, 3, 5), 3.0, 1.2, 96),     # B = 2, asymmetric window
+    (1, 4, 9, 10, 3, (3, 7, 7), 1.0, 1.0, 32),
+    (2, 5, 6, 7, 2, (3, 5, 5), 3.0, 0.8, 32),     # B = 2, large offsets
 ])
 def test_tiled_backward_vs_oracle_and_direct(shape):
     B, T, H, W, nh, ks, off_std, scale, hd = shape
@@ -129,6 +131,7 @@ def test_tiled_lse_matches_oracle():
     (1, 3, 8, 8, 2, (3, 7, 7), 0.5, 1.0, 128),
     (1, 4, 1, 9, 2, (3, 7, 7), 1.0, 1.0, 64),     # H = 1
     (2, 2, 3, 5, 2, (1, 3, 5), 3.0, 1.2, 96),     # B = 2, asymmetric window
+    (1, 4, 9, 10, 3, (3, 7, 7), 1.0, 1.0, 32),
 ])
 def test_tiled_fp32_vs_oracle_and_direct(shape):
     """fp32 storage: the tiled kernels run the fp32 matrix-core instructions
