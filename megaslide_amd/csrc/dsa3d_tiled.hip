@@ -237,6 +237,12 @@ __device__ __forceinline__ op_t<E> table_t_rows(const int* table_t, int row, int
   return fix_to_op<E>(&table_t[(32 * vb + (lane & 31)) * row + col0 + 8 * (lane >> 5)]);
 }
 
+// Zero block after each first-backward table: covers a slot's largest corner
+// index dy + dx = 32 (floats; a multiple of 4 keeps the next table 16-byte
+// aligned).
+constexpr int kP1Zero = 36;
+constexpr int kP1Tab = kTQ * kSRow + kP1Zero;
+
 // First backward kernel (one frame, 16 queries): pass 1 of the backward.  It
 // rebuilds S and dP = dO V^T per plane, accumulates per tap s, dp and their
 // coordinate derivatives, then writes the offset gradients and, for the second
@@ -247,9 +253,11 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p1_kernel(
     Args a, const E* __restrict__ out, const E* __restrict__ dout,
     const float* __restrict__ lse, const float* __restrict__ dlse, E* __restrict__ doff,
     float* __restrict__ p_ws, float* __restrict__ b_ws) {
-  // S and dP tables, double-buffered: one barrier per plane
-  __shared__ __attribute__((aligned(16))) float s_t0[2][kTQ * kSRow];  // S
-  __shared__ __attribute__((aligned(16))) float s_t1[2][kTQ * kSRow];  // dP
+  // S and dP tables, double-buffered (one barrier per plane).  A buffer is
+  // [S rows | zeros | dP rows | zeros]: a slot that misses the step reads the
+  // zero block instead of its corners, so its values are 0 with no select, and
+  // dP sits a constant kP1Tab floats past S (immediate offsets on the reads).
+  __shared__ __attribute__((aligned(16))) float s_tb[2][2 * kP1Tab];
   __shared__ int s_red[kWaves][6];
 
   const Tile tl = make_tile<1, kSubs>(a);
@@ -261,6 +269,8 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p1_kernel(
   const int nit = (box.zhi - box.zlo + 1) * nchunks;
   const E* const kp = static_cast<const E*>(a.k);
   const E* const vp = static_cast<const E*>(a.v);
+  for (int e = threadIdx.x; e < 2 * 2 * kP1Zero; e += kThreads)
+    s_tb[e / (2 * kP1Zero)][((e / kP1Zero) & 1) * kP1Tab + kTQ * kSRow + e % kP1Zero] = 0.0f;
 
   op_t<E> qx[HD / 32], gx[HD / 32];
   load_rows_operand<HD, E>(a, tl, static_cast<const E*>(a.q), a.qs, qx);
@@ -301,9 +311,10 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p1_kernel(
     const Chunk& c = w.c;
     const int z = w.z;
     // buffer it & 1 was last read for step it - 2, before the previous barrier
+    float* const tb = s_tb[it & 1];
     if constexpr (kPrefetch) {
-      store_table<HD, E>(tl, c, qx, rk, s_t0[it & 1]);
-      store_table<HD, E>(tl, c, gx, rv, s_t1[it & 1]);
+      store_table<HD, E>(tl, c, qx, rk, tb);
+      store_table<HD, E>(tl, c, gx, rv, tb + kP1Tab);
       if (it + 1 < nit) {
         load_table_rows<HD, E>(a, tl, wn.c, wn.z, kp, a.ks, rk);
         load_table_rows<HD, E>(a, tl, wn.c, wn.z, vp, a.vs, rv);
@@ -315,34 +326,32 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p1_kernel(
       for (int j = 0; j < 2; ++j) {
         load_block_rows<HD, E>(a, tl, c, ko, a.ks, j, rk.y[0]);
         load_block_rows<HD, E>(a, tl, c, vo, a.vs, j, rv.y[0]);
-        store_table_block<HD, E>(tl, c, qx, rk.y[0], j, s_t0[it & 1]);
-        store_table_block<HD, E>(tl, c, gx, rv.y[0], j, s_t1[it & 1]);
+        store_table_block<HD, E>(tl, c, qx, rk.y[0], j, tb);
+        store_table_block<HD, E>(tl, c, gx, rv.y[0], j, tb + kP1Tab);
       }
     }
     __syncthreads();
-    // every slot reads its corners (in-bounds for any slot); misses are discarded
-    const float* r0 = &s_t0[it & 1][tl.q * kSRow];
-    const float* r1 = &s_t1[it & 1][tl.q * kSRow];
+    // a hit reads its 4 corners in both tables; a miss reads the zero block
+    // (never stale entries, which may be non-finite) and has wz = dwz = 0
+    const float* const r0 = &tb[tl.q * kSRow];
+    const float* const zr = &tb[kTQ * kSRow];
 #pragma unroll
     for (int i = 0; i < kSlots; ++i) {
       float wz, dwz;
       const bool hit = slot_weight(sl[i], step_key(c.id, z), wz, dwz);
-      float t00, t01, t10, t11;
-      corners4(sl[i], r0, t00, t01, t10, t11);
-      const Bilerp bs = bilerp(sl[i], t00, t01, t10, t11);
-      corners4(sl[i], r1, t00, t01, t10, t11);
-      const Bilerp bd = bilerp(sl[i], t00, t01, t10, t11);
-      // misses may read stale (even non-finite) entries: select, never scale by 0
-      const float sv = hit ? bs.val : 0.0f, sx = hit ? bs.dx : 0.0f, sy = hit ? bs.dy : 0.0f;
-      const float dv = hit ? bd.val : 0.0f, dx = hit ? bd.dx : 0.0f, dy = hit ? bd.dy : 0.0f;
-      s_[i] = __builtin_fmaf(wz, sv, s_[i]);
-      gxs[i] = __builtin_fmaf(wz, sx, gxs[i]);
-      gys[i] = __builtin_fmaf(wz, sy, gys[i]);
-      gzs[i] = __builtin_fmaf(dwz, sv, gzs[i]);
-      dp_[i] = __builtin_fmaf(wz, dv, dp_[i]);
-      gxd[i] = __builtin_fmaf(wz, dx, gxd[i]);
-      gyd[i] = __builtin_fmaf(wz, dy, gyd[i]);
-      gzd[i] = __builtin_fmaf(dwz, dv, gzd[i]);
+      const int base = sl[i].idx & 0x1ff, dy = (sl[i].idx >> 9) & 0x1f, dx = (sl[i].idx >> 14) & 1;
+      const float* const ps = hit ? r0 + base : zr;
+      const float* const pd = ps + kP1Tab;
+      const Bilerp bs = bilerp(sl[i], ps[0], ps[dx], ps[dy], ps[dy + dx]);
+      const Bilerp bd = bilerp(sl[i], pd[0], pd[dx], pd[dy], pd[dy + dx]);
+      s_[i] = __builtin_fmaf(wz, bs.val, s_[i]);
+      gxs[i] = __builtin_fmaf(wz, bs.dx, gxs[i]);
+      gys[i] = __builtin_fmaf(wz, bs.dy, gys[i]);
+      gzs[i] = __builtin_fmaf(dwz, bs.val, gzs[i]);
+      dp_[i] = __builtin_fmaf(wz, bd.val, dp_[i]);
+      gxd[i] = __builtin_fmaf(wz, bd.dx, gxd[i]);
+      gyd[i] = __builtin_fmaf(wz, bd.dy, gyd[i]);
+      gzd[i] = __builtin_fmaf(dwz, bd.val, gzd[i]);
     }
     w = wn;
   }
