@@ -248,8 +248,18 @@ constexpr int kP1Tab = kTQ * kSRow + kP1Zero;
 // coordinate derivatives, then writes the offset gradients and, for the second
 // kernel, p times its dropout factor and ds * softmax_scale of every tap (fp32,
 // [token][head][tap]).
+// Waves per SIMD of the first backward kernel.  bf16 up to head_dim 64 fits
+// 128 registers, so two workgroups share a CU and each hides the other's
+// latencies (barriers, table loads): q and dO then stay in LDS and K/V rows are
+// loaded at the step.  Larger heads and fp32 keep q/dO in registers and
+// prefetch the next step's rows, at one workgroup per CU.
 template <int HD, typename E>
-__global__ __launch_bounds__(kThreads) void dsa3d_bwd_p1_kernel(
+constexpr int p1_min_waves() {
+  return sizeof(E) == 2 && HD <= 64 ? 4 : 2;
+}
+
+template <int HD, typename E>
+__global__ __launch_bounds__(kThreads, (p1_min_waves<HD, E>())) void dsa3d_bwd_p1_kernel(
     Args a, const E* __restrict__ out, const E* __restrict__ dout,
     const float* __restrict__ lse, const float* __restrict__ dlse, E* __restrict__ doff,
     float* __restrict__ p_ws, float* __restrict__ b_ws) {
@@ -259,6 +269,9 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p1_kernel(
   // dP sits a constant kP1Tab floats past S (immediate offsets on the reads).
   __shared__ __attribute__((aligned(16))) float s_tb[2][2 * kP1Tab];
   __shared__ int s_red[kWaves][6];
+  constexpr bool kTwoWg = p1_min_waves<HD, E>() == 4;
+  constexpr int XR = HD + 8;  // [query][channel] row of the staged q and dO (elements)
+  __shared__ __attribute__((aligned(16))) word_t<E> s_x[kTwoWg ? 2 * kTQ * XR : 1];
 
   const Tile tl = make_tile<1, kSubs>(a);
   const int D = a.nh * HD;
@@ -273,8 +286,31 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p1_kernel(
     s_tb[e / (2 * kP1Zero)][((e / kP1Zero) & 1) * kP1Tab + kTQ * kSRow + e % kP1Zero] = 0.0f;
 
   op_t<E> qx[HD / 32], gx[HD / 32];
-  load_rows_operand<HD, E>(a, tl, static_cast<const E*>(a.q), a.qs, qx);
-  load_rows_operand<HD, E>(a, tl, dout, D, gx);
+  if constexpr (kTwoWg) {
+    // q (t = 0) and dO (t = 1) rows of the tile's queries into LDS, 16 bytes a thread
+    constexpr int CPR = HD * static_cast<int>(sizeof(E)) / 16;
+    for (int e = threadIdx.x; e < 2 * kTQ * CPR; e += kThreads) {
+      const int t = e / (kTQ * CPR), m = (e / CPR) % kTQ, ch = (e % CPR) * (16 / sizeof(E));
+      const int64_t row = tile_row(a, tl, m);
+      uint4 v = {0u, 0u, 0u, 0u};
+      if (row >= 0) {
+        const E* src = t == 0 ? static_cast<const E*>(a.q) + row * a.qs : dout + row * D;
+        v = *reinterpret_cast<const uint4*>(src + tl.head * HD + ch);
+      }
+      *reinterpret_cast<uint4*>(&s_x[(t * kTQ + m) * XR + ch]) = v;
+    }
+    __syncthreads();
+  } else {
+    load_rows_operand<HD, E>(a, tl, static_cast<const E*>(a.q), a.qs, qx);
+    load_rows_operand<HD, E>(a, tl, dout, D, gx);
+  }
+  // MFMA A operand of staged row block t (q or dO): lane l holds channels
+  // 32 c + 8 (l / 16) + [0, 8) of query l % 16
+  auto staged_x = [&](int t, op_t<E> (&x)[HD / 32]) {
+#pragma unroll
+    for (int cc = 0; cc < HD / 32; ++cc)
+      x[cc] = load_op<E>(&s_x[(t * kTQ + (tl.lane & 15)) * XR + 32 * cc + 8 * (tl.lane >> 4)]);
+  };
 
   // Delta = dO . O (- dlse) and lse for this lane's query: 32 lanes x HD/32 channels
   constexpr int CPL = HD / kSubs;
@@ -299,7 +335,7 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p1_kernel(
   // K and V rows of the next (plane, chunk) are loaded while the current one is
   // used.  fp32 rows beyond head_dim 64 would spill that way: they are loaded
   // at the step, one 16-voxel block at a time.
-  constexpr bool kPrefetch = sizeof(E) == 2 || HD == 64;
+  constexpr bool kPrefetch = !kTwoWg && (sizeof(E) == 2 || HD == 64);
   TableRows<HD, E> rk, rv;
   Walk w = walk_begin(box);
   if (kPrefetch && nit > 0) {
@@ -326,8 +362,16 @@ __global__ __launch_bounds__(kThreads) void dsa3d_bwd_p1_kernel(
       for (int j = 0; j < 2; ++j) {
         load_block_rows<HD, E>(a, tl, c, ko, a.ks, j, rk.y[0]);
         load_block_rows<HD, E>(a, tl, c, vo, a.vs, j, rv.y[0]);
-        store_table_block<HD, E>(tl, c, qx, rk.y[0], j, tb);
-        store_table_block<HD, E>(tl, c, gx, rv.y[0], j, tb + kP1Tab);
+        if constexpr (kTwoWg) {
+          op_t<E> x[HD / 32];
+          staged_x(0, x);
+          store_table_block<HD, E>(tl, c, x, rk.y[0], j, tb);
+          staged_x(1, x);
+          store_table_block<HD, E>(tl, c, x, rv.y[0], j, tb + kP1Tab);
+        } else {
+          store_table_block<HD, E>(tl, c, qx, rk.y[0], j, tb);
+          store_table_block<HD, E>(tl, c, gx, rv.y[0], j, tb + kP1Tab);
+        }
       }
     }
     __syncthreads();
