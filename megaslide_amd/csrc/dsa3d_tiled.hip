@@ -99,19 +99,17 @@ __global__ __launch_bounds__(kThreads, (fwd_min_waves<HD, E>())) void dsa3d_fwd_
     store_table<HD, E>(tl, c, qx, rows, tab);
     if (it + 1 < nit) load_table_rows<HD, E>(a, tl, wn.c, wn.z, kp, a.ks, rows);
     __syncthreads();
-    // every slot reads its corners (in-bounds for any slot); misses are discarded
+    // only the lanes whose tap has corners on this step read them; a slot that
+    // no lane of the wave hits (about a third of them) is skipped
     const float* my_row = &tab[tl.q * kSRow];
-    float t[kSlots][4];
-#pragma unroll
-    for (int i = 0; i < kSlots; ++i)
-      corners4(fwd_slot<HD>(sl[i]), my_row, t[i][0], t[i][1], t[i][2], t[i][3]);
 #pragma unroll
     for (int i = 0; i < kSlots; ++i) {
       const Slot si = fwd_slot<HD>(sl[i]);
       float wz, dwz;
-      const bool hit = slot_weight(si, step_key(c.id, z), wz, dwz);
-      const float v = bilerp(si, t[i][0], t[i][1], t[i][2], t[i][3]).val;
-      sc[i] = hit ? __builtin_fmaf(wz, v, sc[i]) : sc[i];
+      if (!slot_hits(si, step_key(c.id, z), wz, dwz)) continue;
+      float t0, t1, t2, t3;
+      corners4(si, my_row, t0, t1, t2, t3);
+      sc[i] = __builtin_fmaf(wz, bilerp(si, t0, t1, t2, t3).val, sc[i]);
     }
     if constexpr (NB == 1) __syncthreads();  // the next step overwrites the table
     w = wn;
@@ -255,7 +253,7 @@ constexpr int kP1Tab = kTQ * kSRow + kP1Zero;
 // prefetch the next step's rows, at one workgroup per CU.
 template <int HD, typename E>
 constexpr int p1_min_waves() {
-  return sizeof(E) == 2 && HD <= 64 ? 4 : 2;
+  return sizeof(E) == 2 && HD <= 96 ? 4 : 2;
 }
 
 template <int HD, typename E>
@@ -376,13 +374,15 @@ __global__ __launch_bounds__(kThreads, (p1_min_waves<HD, E>())) void dsa3d_bwd_p
     }
     __syncthreads();
     // a hit reads its 4 corners in both tables; a miss reads the zero block
-    // (never stale entries, which may be non-finite) and has wz = dwz = 0
+    // (never stale entries, which may be non-finite) and has wz = dwz = 0.  A
+    // slot that no lane of the wave hits (about a third of them) is skipped.
     const float* const r0 = &tb[tl.q * kSRow];
     const float* const zr = &tb[kTQ * kSRow];
 #pragma unroll
     for (int i = 0; i < kSlots; ++i) {
       float wz, dwz;
       const bool hit = slot_weight(sl[i], step_key(c.id, z), wz, dwz);
+      if (__builtin_amdgcn_ballot_w64(hit) == 0) continue;
       const int base = sl[i].idx & 0x1ff, dy = (sl[i].idx >> 9) & 0x1f, dx = (sl[i].idx >> 14) & 1;
       const float* const ps = hit ? r0 + base : zr;
       const float* const pd = ps + kP1Tab;
