@@ -538,6 +538,238 @@ __global__ __launch_bounds__(64 * kRowWaves) void dwconv_dw_block_dot2_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// Weight / bias gradient on the matrix cores (bf16 x and dz, kw <= 16,
+// kt * kh <= 32).  One dz row (b, t, h) of one channel contributes
+//   G[dw][n] = sum_w dz[w] x[t + dt - pt][h + dh - ph][w + dw - pw],  n = dt kh + dh,
+// which is a product over the row's x positions w' = w + dw - pw (k = w' + pw):
+//   G = A B,  A[m][k] = dz[k - m] (0 outside the row: the Toeplitz matrix of
+//   the dz row),  B[k][n] = x_n[k - pw] (x row n of the tap's (dt, dh), zero
+//   padded).
+// The row is taken in segments of 32 dz positions (k < 64: two 16x16x32 MFMAs
+// per tile of 16 n).  A workgroup owns kDwmCh channels, one per wave, and
+// walks bands of R dz rows of consecutive (b, t) items.  Per band it stages
+// into LDS, channel-major, the dz rows (each 32-position segment as [16 zeros
+// | 32 values | 40 zeros], so A's reads outside the segment fall on zeros, in
+// two copies, the second shifted by one element: lane m's 8-element window of
+// A starts 4-byte aligned in copy m & 1) and the kt (R + kh - 1) x rows they
+// reach (x_n[w] at element w + pw of a zero-padded row).  G stays in the MFMA accumulators across the
+// workgroup's bands and is flushed with one fp32 atomic per (channel, tap).
+// ---------------------------------------------------------------------------
+constexpr int kDwmCh = 8;    // channels (one per wave) per workgroup
+typedef __attribute__((ext_vector_type(8))) __bf16 dwm_bf16x8_t;
+typedef __attribute__((ext_vector_type(8))) uint16_t dwm_u16x8_t;
+typedef __attribute__((ext_vector_type(4))) float dwm_f32x4_t;
+constexpr int kDwmSeg = 88;  // LDS elements per staged dz row segment (one copy)
+
+struct DwmGeom {
+  int R;        // dz rows per band
+  int nseg;     // 32-position segments per row
+  int xps;      // LDS stride of a staged x row (elements)
+  int xr;       // staged x rows per plane: R + kh - 1
+  int bands;    // bands per (b, t)
+  int ipw;      // (b, t, band) items per workgroup
+  int x_elems;  // staged x elements per channel: kt * xr * xps
+  int dz_elems; // staged dz elements per channel: 2 copies * R * nseg * kDwmSeg
+  float rW;     // 1 / W and 1 / xr: exact quotients of the small staging
+  float rxr;    // indices (below 2^20) by float multiply and truncation
+};
+
+template <int KH, int KW>
+__global__ __launch_bounds__(64 * kDwmCh) void dwconv_dw_mfma_kernel(ConvArgs a, DwmGeom g,
+                                                                     const bf16* __restrict__ x,
+                                                                     const bf16* __restrict__ dz,
+                                                                     float* __restrict__ acc) {
+  static_assert(KW <= 16, "the 16 MFMA rows hold the kw taps");
+  constexpr int PH = KH / 2, PW = KW / 2;
+  extern __shared__ __attribute__((aligned(16))) uint16_t s_dwm[];
+  uint16_t* const s_x = s_dwm;                       // [ch][dt][xr][xps]
+  uint16_t* const s_dz = s_dwm + kDwmCh * g.x_elems;  // [ch][copy][R][nseg][kDwmSeg]
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int c0 = blockIdx.y * kDwmCh;
+  const int nk = a.kt * KH;  // used MFMA columns
+  const int nnt = (nk + 15) / 16;
+  const int64_t rowstride = static_cast<int64_t>(a.W) * a.C;
+
+  // the pads must read as zeros; value positions are rewritten every band
+  {
+    const int n32 = kDwmCh * (g.x_elems + g.dz_elems) / 2;
+    uint32_t* const z = reinterpret_cast<uint32_t*>(s_dwm);
+    for (int i = threadIdx.x; i < n32; i += blockDim.x) z[i] = 0u;
+  }
+
+  // B operand rows of this lane's column n = 16 nt + lane % 16 (clamped: unused
+  // columns read a valid row and are discarded)
+  const int m = lane & 15, kg = lane >> 4;
+  int brow[2];
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    const int n = min(16 * nt + m, nk - 1);
+    const int dt = n / KH, dh = n - dt * KH;
+    brow[nt] = (dt * g.xr + dh) * g.xps + 8 * kg;
+  }
+  const uint16_t* const xw = s_x + wave * g.x_elems;
+  const uint16_t* const dzw = s_dz + wave * g.dz_elems;
+  dwm_f32x4_t gacc[2] = {{0.0f, 0.0f, 0.0f, 0.0f}, {0.0f, 0.0f, 0.0f, 0.0f}};
+  float sb = 0.0f;
+
+  const int64_t items = static_cast<int64_t>(a.B) * a.T * g.bands;
+  const int64_t it0 = static_cast<int64_t>(blockIdx.x) * g.ipw;
+  const int64_t it1 = min(items, it0 + g.ipw);
+  for (int64_t it = it0; it < it1; ++it) {
+    const int band = static_cast<int>(it % g.bands);
+    const int64_t bt = it / g.bands;
+    const int t = static_cast<int>(bt % a.T);
+    const int b = static_cast<int>(bt / a.T);
+    const int h0 = band * g.R;
+    __syncthreads();  // the previous band's reads are done
+    // Stage the band: voxel e < nx is x voxel (row q = e / W, column e % W) of
+    // the kt x xr halo rows, the rest are the R dz rows; 16 bytes (8
+    // channels) per voxel, four voxels per thread with their loads issued
+    // before any LDS write.  Rows outside the volume stage zeros.
+    const int nx = a.kt * g.xr * a.W, ntot = nx + g.R * a.W;
+    for (int e0 = threadIdx.x; e0 < ntot; e0 += 4 * 64 * kDwmCh) {
+      // LDS destinations as element offsets (-1: none), so the stores stay DS stores
+      uint4 v[4];
+      int dst[4], stride[4];
+      bool dup[4];  // dz voxel: also into the shifted copy
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int e = e0 + u * 64 * kDwmCh;
+        v[u] = uint4{0u, 0u, 0u, 0u};
+        dst[u] = -1;
+        stride[u] = 0;
+        dup[u] = false;
+        if (e >= ntot) continue;
+        const bool is_x = e < nx;
+        const int ee = is_x ? e : e - nx;
+        const int q = static_cast<int>((static_cast<float>(ee) + 0.5f) * g.rW);
+        const int w = ee - q * a.W;
+        const bf16* src = nullptr;
+        if (is_x) {
+          const int dt = static_cast<int>((static_cast<float>(q) + 0.5f) * g.rxr);
+          const int rr = q - dt * g.xr;
+          const int tt = t + dt - a.kt / 2, hh = h0 + rr - PH;
+          if (tt >= 0 && tt < a.T && hh >= 0 && hh < a.H)
+            src = x + ((static_cast<int64_t>(b) * a.T + tt) * a.H + hh) * rowstride;
+          dst[u] = q * g.xps + w + PW;
+          stride[u] = g.x_elems;
+        } else {
+          const int h = h0 + q;
+          if (h < a.H) src = dz + ((static_cast<int64_t>(b) * a.T + t) * a.H + h) * rowstride;
+          dst[u] = kDwmCh * g.x_elems + (q * g.nseg + (w >> 5)) * kDwmSeg + 16 + (w & 31);
+          stride[u] = g.dz_elems;
+          dup[u] = true;
+        }
+        if (src != nullptr)
+          v[u] = *reinterpret_cast<const uint4*>(src + static_cast<int64_t>(w) * a.C + c0);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        if (dst[u] < 0) continue;
+        const uint32_t vv[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+        for (int ch = 0; ch < kDwmCh; ++ch) {
+          const uint16_t h = static_cast<uint16_t>(vv[ch >> 1] >> (16 * (ch & 1)));
+          s_dwm[dst[u] + ch * stride[u]] = h;
+          if (dup[u]) s_dwm[dst[u] + ch * stride[u] + g.dz_elems / 2 + 1] = h;
+        }
+      }
+    }
+    __syncthreads();
+    // this wave's channel: every valid row of the band, every segment
+    const int rows = min(g.R, a.H - h0);
+    for (int r = 0; r < rows; ++r) {
+      for (int s = 0; s < g.nseg; ++s) {
+        // window start 16 + 8 kg + 32 kb - m, made even in copy m & 1
+        const uint16_t* const da =
+            dzw + (m & 1) * (g.dz_elems / 2) + (r * g.nseg + s) * kDwmSeg + 16 + 8 * kg - m + (m & 1);
+        const uint16_t* const xb = xw + r * g.xps + 32 * s;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+          // four aligned dword reads (volatile: not merged into one misaligned
+          // 16-byte read, which stalls)
+          typedef const volatile __attribute__((address_space(3))) uint32_t lds_u32;
+          lds_u32* const pa = (lds_u32*)(da + 32 * kb);
+          uint32_t aw[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) aw[j] = pa[j];
+          const dwm_u16x8_t av = __builtin_bit_cast(dwm_u16x8_t, aw);
+          const dwm_bf16x8_t A = __builtin_bit_cast(dwm_bf16x8_t, av);
+#pragma unroll
+          for (int nt = 0; nt < 2; ++nt) {
+            if (nt >= nnt) break;
+            dwm_u16x8_t bv;
+            __builtin_memcpy(&bv, xb + brow[nt] + 32 * kb, sizeof(bv));
+            gacc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                A, __builtin_bit_cast(dwm_bf16x8_t, bv), gacc[nt], 0, 0, 0);
+          }
+        }
+      }
+      // bias: the row's dz values of this channel
+      for (int w = lane; w < a.W; w += 64)
+        sb += __uint_as_float(static_cast<uint32_t>(dzw[(r * g.nseg + (w >> 5)) * kDwmSeg + 16 +
+                                                        (w & 31)])
+                              << 16);
+    }
+  }
+  // flush: gacc[nt][i] = G[dw = 4 (lane / 16) + i][n = 16 nt + lane % 16]
+  const int c = c0 + wave;
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    const int n = 16 * nt + m;
+    if (n >= nk) continue;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int dw = 4 * kg + i;
+      if (dw < KW && gacc[nt][i] != 0.0f)
+        atomicAdd(acc + static_cast<int64_t>(n * KW + dw) * a.C + c, gacc[nt][i]);
+    }
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) sb += __shfl_xor(sb, o);
+  if (lane == 0 && sb != 0.0f) atomicAdd(acc + static_cast<int64_t>(nk * KW) * a.C + c, sb);
+}
+
+// LDS geometry of the matrix-core weight gradient (at most 64 KB of dynamic
+// LDS: two workgroups per CU), or R = 0 where it does not apply (then the VALU
+// kernels run).
+constexpr int64_t kDwmLdsMax = 64 * 1024;
+
+inline int64_t dwm_lds_bytes(const DwmGeom& g) {
+  return 2LL * kDwmCh * (static_cast<int64_t>(g.x_elems) + g.dz_elems);
+}
+
+inline DwmGeom dwm_geometry(const ConvArgs& a) {
+  DwmGeom g{};
+  if (a.kw > 16 || a.kt * a.kh > 32 || a.C % kDwmCh != 0 || a.W < 1 || a.W > 4096) return g;
+  g.nseg = (a.W + 31) / 32;
+  g.xps = 32 * g.nseg + 40;
+  for (int R = 8; R >= 1; R >>= 1) {
+    const int xr = R + a.kh - 1;
+    const int64_t bytes = 2LL * kDwmCh * (static_cast<int64_t>(a.kt) * xr * g.xps +
+                                          2LL * R * g.nseg * kDwmSeg);
+    if (bytes <= kDwmLdsMax) {
+      g.R = R;
+      g.xr = xr;
+      g.x_elems = a.kt * xr * g.xps;
+      g.dz_elems = 2 * R * g.nseg * kDwmSeg;
+      break;
+    }
+  }
+  if (g.R == 0) return g;
+  g.bands = (a.H + g.R - 1) / g.R;
+  g.rW = 1.0f / static_cast<float>(a.W);
+  g.rxr = 1.0f / static_cast<float>(g.xr);
+  // enough workgroups for two per CU several times over, few atomics each
+  const int64_t items = static_cast<int64_t>(a.B) * a.T * g.bands;
+  const int64_t cblocks = a.C / kDwmCh;
+  const int64_t ipw = (items * cblocks + 2047) / 2048;
+  g.ipw = static_cast<int>(ipw > 0 ? ipw : 1);
+  return g;
+}
+
+// ---------------------------------------------------------------------------
 // weight / bias gradient
 // ---------------------------------------------------------------------------
 
@@ -778,10 +1010,22 @@ void launch_dw_block(const ConvArgs& a, const T* x, const G* dz, float* acc, hip
   const int64_t items = static_cast<int64_t>(a.B) * a.T * strips;
   const dim3 grid(static_cast<unsigned>((items + kRowWaves - 1) / kRowWaves),
                   static_cast<unsigned>((a.C + 63) / 64), static_cast<unsigned>(a.kt));
-  if constexpr (std::is_same<T, bf16>::value && std::is_same<G, bf16>::value)
+  if constexpr (std::is_same<T, bf16>::value && std::is_same<G, bf16>::value) {
+    // the matrix cores pay off from kw = 5 (3x3x3: measured slower than dot2,
+    // whose rows are short)
+    const DwmGeom g = KS >= 5 ? dwm_geometry(a) : DwmGeom{};
+    if (g.R > 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+        reinterpret_cast<uintptr_t>(dz) % 16 == 0) {
+      const int64_t mitems = static_cast<int64_t>(a.B) * a.T * g.bands;
+      const dim3 mgrid(static_cast<unsigned>((mitems + g.ipw - 1) / g.ipw),
+                       static_cast<unsigned>(a.C / kDwmCh));
+      hipLaunchKernelGGL((dwconv_dw_mfma_kernel<KS, KS>), mgrid, dim3(64 * kDwmCh),
+                         static_cast<unsigned>(dwm_lds_bytes(g)), s, a, g, x, dz, acc);
+      return;
+    }
     hipLaunchKernelGGL((dwconv_dw_block_dot2_kernel<KS, KS>), grid, dim3(64 * kRowWaves), 0, s, a,
                        x, dz, acc);
-  else
+  } else
     hipLaunchKernelGGL((dwconv_dw_block_kernel<T, G, KS, KS>), grid, dim3(64 * kRowWaves), 0, s, a,
                        x, dz, acc);
 }
