@@ -518,22 +518,34 @@ __device__ __forceinline__ void store_table(const Tile& tl, const Chunk& c,
 
 // Chunk rows of Y (plane z), channels col0 + [0, CW), transposed into LDS:
 // yt[channel][voxel] (row stride ElemT<E>::kRow), zero padded up to nvp
-// voxels, by the first NT threads of the workgroup.  Thread t moves voxels
-// 2*(t % 128) + {0, 1}, channel groups t / 128 + P*g (P = NT / 128,
-// g < CW / 8 / P; 8 channels each); its loads are issued first.
+// voxels, by the first NT = 512 threads of the workgroup.  Thread t moves
+// voxels 2 p + {0, 1} of channel groups q0 + 4 g (8 channels each, g < CW /
+// 32), p = 32 ((t >> 6) & 3) + (t & 31), q0 = 2 (t >> 8) + ((t >> 5) & 1): a
+// wave's lanes cover 2 adjacent channel groups of 32 voxel pairs, so a load
+// touches 32 rows, 16 channels of each (not 64 rows, 8 channels each), and
+// the LDS writes of a wave fall on 64 distinct banks (odd groups 32 banks
+// from even ones at the row strides used).  Its loads are issued first.
 template <int NT, int CW, typename E>
 struct StageRows {
-  static constexpr int P = NT / 128, G = CW / 8 / P;
-  static_assert(G * P * 8 == CW, "channel groups must split evenly over the staging threads");
+  static_assert(NT == 512, "the staging map covers 128 voxel pairs x 4 groups per pass");
+  static constexpr int G = CW / 32;
+  static_assert(G * 32 == CW, "channel groups must split evenly over the staging threads");
   op_t<E> x[G][2];  // [channel group][voxel]
 };
+
+__device__ __forceinline__ int stage_pair() {
+  return 32 * ((threadIdx.x >> 6) & 3) + (threadIdx.x & 31);
+}
+__device__ __forceinline__ int stage_group0() {
+  return 2 * (threadIdx.x >> 8) + ((threadIdx.x >> 5) & 1);
+}
 
 template <int NT, int CW, typename E>
 __device__ __forceinline__ void load_stage_rows(const Args& a, const Tile& tl, const Chunk& c,
                                                 int z, const E* ybase, int64_t ystride,
                                                 int col0, StageRows<NT, CW, E>& r) {
-  constexpr int P = StageRows<NT, CW, E>::P, G = StageRows<NT, CW, E>::G;
-  const int cg0 = threadIdx.x >> 7, v0 = 2 * (threadIdx.x & 127);
+  constexpr int G = StageRows<NT, CW, E>::G;
+  const int q0 = stage_group0(), v0 = 2 * stage_pair();
 #pragma unroll
   for (int g = 0; g < G; ++g) r.x[g][0] = r.x[g][1] = zero_op<E>();
   if (threadIdx.x >= NT) return;  // a larger workgroup: the other threads do not stage
@@ -541,9 +553,9 @@ __device__ __forceinline__ void load_stage_rows(const Args& a, const Tile& tl, c
 #pragma unroll
   for (int e = 0; e < 2; ++e) {
     if (v0 + e < c.nv) {
-      const E* p = chunk_voxel<E>(origin, a, c, ystride, 8 * cg0, v0 + e);
+      const E* p = chunk_voxel<E>(origin, a, c, ystride, 8 * q0, v0 + e);
 #pragma unroll
-      for (int g = 0; g < G; ++g) r.x[g][e] = load_op<E>(p + 8 * P * g);
+      for (int g = 0; g < G; ++g) r.x[g][e] = load_op<E>(p + 32 * g);
     }
   }
 }
@@ -551,13 +563,13 @@ __device__ __forceinline__ void load_stage_rows(const Args& a, const Tile& tl, c
 template <int NT, int CW, typename E>
 __device__ __forceinline__ void store_stage(const Chunk& c, const StageRows<NT, CW, E>& r,
                                             word_t<E>* yt) {
-  constexpr int P = StageRows<NT, CW, E>::P, G = StageRows<NT, CW, E>::G;
+  constexpr int G = StageRows<NT, CW, E>::G;
   constexpr int R = ElemT<E>::kRow;
-  const int cg0 = threadIdx.x >> 7, v0 = 2 * (threadIdx.x & 127);
+  const int q0 = stage_group0(), v0 = 2 * stage_pair();
   if (threadIdx.x >= NT || v0 >= c.nvp) return;
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    const int ch0 = 8 * (cg0 + P * g);
+    const int ch0 = 8 * (q0 + 4 * g);
     if constexpr (sizeof(E) == 2) {
       const u32x4_t x0 = __builtin_bit_cast(u32x4_t, r.x[g][0]);
       const u32x4_t x1 = __builtin_bit_cast(u32x4_t, r.x[g][1]);
