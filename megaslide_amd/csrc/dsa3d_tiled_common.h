@@ -520,11 +520,12 @@ __device__ __forceinline__ void store_table(const Tile& tl, const Chunk& c,
 // yt[channel][voxel] (row stride ElemT<E>::kRow), zero padded up to nvp
 // voxels, by the first NT = 512 threads of the workgroup.  Thread t moves
 // voxels 2 p + {0, 1} of channel groups q0 + 4 g (8 channels each, g < CW /
-// 32), p = 32 ((t >> 6) & 3) + (t & 31), q0 = 2 (t >> 8) + ((t >> 5) & 1): a
-// wave's lanes cover 2 adjacent channel groups of 32 voxel pairs, so a load
-// touches 32 rows, 16 channels of each (not 64 rows, 8 channels each), and
-// the LDS writes of a wave fall on 64 distinct banks (odd groups 32 banks
-// from even ones at the row strides used).  Its loads are issued first.
+// 32), p = 16 (t >> 6) + (t & 15), q0 = (t >> 4) & 3: a wave's lanes cover 4
+// adjacent channel groups of 16 voxel pairs, so a load touches 16 rows, 32
+// channels of each (64 rows of 8 channels took 4% longer in the forward, 32
+// rows of 16 channels 1.5%).  Its LDS writes fall on 32 banks, two lanes
+// each (groups q and q + 2 share banks at the row strides used).  Its loads
+// are issued first.
 template <int NT, int CW, typename E>
 struct StageRows {
   static_assert(NT == 512, "the staging map covers 128 voxel pairs x 4 groups per pass");
@@ -534,10 +535,10 @@ struct StageRows {
 };
 
 __device__ __forceinline__ int stage_pair() {
-  return 32 * ((threadIdx.x >> 6) & 3) + (threadIdx.x & 31);
+  return 16 * ((threadIdx.x >> 6) & 7) + (threadIdx.x & 15);
 }
 __device__ __forceinline__ int stage_group0() {
-  return 2 * (threadIdx.x >> 8) + ((threadIdx.x >> 5) & 1);
+  return (threadIdx.x >> 4) & 3;
 }
 
 template <int NT, int CW, typename E>
