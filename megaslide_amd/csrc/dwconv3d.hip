@@ -733,7 +733,9 @@ __global__ __launch_bounds__(64 * kDwmCh) void dwconv_dw_mfma_kernel(ConvArgs a,
 
 // LDS geometry of the matrix-core weight gradient (at most 64 KB of dynamic
 // LDS: two workgroups per CU), or R = 0 where it does not apply (then the VALU
-// kernels run).
+// kernels run).  Bands of fewer than 4 rows stage too many halo rows per dz
+// row (kt (R + kh - 1) / R): at W = 80 (1-row bands) it took 2.95 ms against
+// 0.82 for the dot2 kernel.
 constexpr int64_t kDwmLdsMax = 64 * 1024;
 
 inline int64_t dwm_lds_bytes(const DwmGeom& g) {
@@ -745,7 +747,7 @@ inline DwmGeom dwm_geometry(const ConvArgs& a) {
   if (a.kw > 16 || a.kt * a.kh > 32 || a.C % kDwmCh != 0 || a.W < 1 || a.W > 4096) return g;
   g.nseg = (a.W + 31) / 32;
   g.xps = 32 * g.nseg + 40;
-  for (int R = 8; R >= 1; R >>= 1) {
+  for (int R = 8; R >= 4; R >>= 1) {
     const int xr = R + a.kh - 1;
     const int64_t bytes = 2LL * kDwmCh * (static_cast<int64_t>(a.kt) * xr * g.xps +
                                           2LL * R * g.nseg * kDwmSeg);

@@ -3,8 +3,8 @@
 Covers the register-tiled row kernels (kw in {3, 5, 7}), the simple kernels
 (other odd sizes), the GELU epilogue and its backward, W not a multiple of the
 16-output run, channel counts not a multiple of 64, and the bf16 matrix-core
-weight gradient (kw >= 5, channels a multiple of 8; one or several 32-wide row
-segments, ragged row bands).  Tolerances: 1e-4
+weight gradient (kw >= 5, channels a multiple of 8, bands of at least 4 rows;
+one or several 32-wide row segments, ragged row bands).  Tolerances: 1e-4
 (fp32), 2e-2 (bf16, inputs rounded to bf16 before the reference).
 """
 
@@ -38,9 +38,11 @@ def reference(x, w, b, vs, act):
     (1, 2, 9, 16, 64, (1, 5, 5), None),
     (1, 5, 4, 7, 40, (5, 3, 1), "gelu"),    # kw = 1: simple kernels
     (1, 3, 3, 3, 8, (3, 7, 7), None),       # window larger than the grid
-    (1, 3, 9, 80, 64, (3, 7, 7), None),     # 3 row segments, bands of 2 rows (ragged)
+    (1, 3, 9, 80, 64, (3, 7, 7), None),     # W = 80: the dot2 weight gradient
     (2, 4, 7, 45, 48, (3, 3, 3), "gelu"),
-    (1, 2, 6, 70, 16, (3, 5, 5), "gelu"),   # kw = 5 on the matrix cores, 3 segments
+    (1, 2, 6, 70, 16, (3, 5, 5), "gelu"),   # W = 70, kw = 5: dot2 (bands would be 2 rows)
+    (1, 4, 6, 48, 16, (3, 5, 5), "gelu"),   # kw = 5 on the matrix cores: 2 segments, bands 4 + 2
+    (2, 1, 9, 50, 32, (1, 5, 5), None),     # kt = 1 on the matrix cores: 2 segments, bands 8 + 1
 ])
 def test_dwconv_matches_conv3d(cfg, dtype, tol):
     from megaslide_amd import dwconv3d
