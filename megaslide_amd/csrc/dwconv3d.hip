@@ -14,7 +14,9 @@
 // kw taps to all kRun outputs.  A wave covers 64 consecutive channels, so every
 // load is one 128-byte (bf16) or 256-byte (fp32) segment.  The weight-gradient
 // kernel keeps all kt*kh*kw tap sums of its channel in registers over a strip
-// of rows and flushes them with one fp32 atomic per (thread, tap).
+// of rows and flushes them with one fp32 atomic per (thread, tap).  With bf16
+// data, kw in {5, 7} and channels a multiple of 8, the weight gradient runs on
+// the matrix cores instead (dwconv_dw_mfma_kernel).
 // Other odd kernel sizes use the simple one-output-per-thread kernels.
 #include <type_traits>
 
@@ -552,8 +554,9 @@ __global__ __launch_bounds__(64 * kRowWaves) void dwconv_dw_block_dot2_kernel(
 // | 32 values | 40 zeros], so A's reads outside the segment fall on zeros, in
 // two copies, the second shifted by one element: lane m's 8-element window of
 // A starts 4-byte aligned in copy m & 1) and the kt (R + kh - 1) x rows they
-// reach (x_n[w] at element w + pw of a zero-padded row).  G stays in the MFMA accumulators across the
-// workgroup's bands and is flushed with one fp32 atomic per (channel, tap).
+// reach (x_n[w] at element w + pw of a zero-padded row).  G stays in the MFMA
+// accumulators across the workgroup's bands and is flushed with one fp32
+// atomic per (channel, tap).
 // ---------------------------------------------------------------------------
 constexpr int kDwmCh = 8;    // channels (one per wave) per workgroup
 typedef __attribute__((ext_vector_type(8))) __bf16 dwm_bf16x8_t;
