@@ -461,8 +461,8 @@ template <int HD, int CW, typename E, int FR>
 __global__ __launch_bounds__(P2Tile<FR>::Threads) void dsa3d_bwd_p2_kernel(
     Args a, const E* __restrict__ dout, const float* __restrict__ p_ws,
     const float* __restrict__ b_ws, E* __restrict__ dq, float* __restrict__ dk_acc,
-    float* __restrict__ dv_acc) {
-  static_assert(HD % CW == 0 && CW % 32 == 0, "channel windows are whole 32-channel blocks");
+    float* __restrict__ dv_acc, int cw_base) {
+  static_assert(CW <= HD && CW % 32 == 0, "channel windows are whole 32-channel blocks");
   using G = P2Tile<FR>;
   constexpr int kP2Frames = FR, kP2Q = G::Q, kP2Subs = G::Subs, kP2Slots = G::Slots;
   constexpr int kP2Row = G::Row, NW = G::Waves, NT = G::Threads;
@@ -483,7 +483,8 @@ __global__ __launch_bounds__(P2Tile<FR>::Threads) void dsa3d_bwd_p2_kernel(
 
   const Tile tl = make_tile<kP2Frames, kP2Subs>(a);
   const int D = a.nh * HD;
-  const int cw0 = tl.head * HD + CW * static_cast<int>(blockIdx.z);  // first channel of the window
+  // first channel of the window: cw_base + CW blockIdx.z within the head
+  const int cw0 = tl.head * HD + cw_base + CW * static_cast<int>(blockIdx.z);
   Slot sl[kP2Slots];
   Box box;
   setup_slots<E, kP2Subs, kP2Slots, NW>(a, tl, sl, box, s_red);
@@ -545,15 +546,16 @@ __global__ __launch_bounds__(P2Tile<FR>::Threads) void dsa3d_bwd_p2_kernel(
   }
   __syncthreads();
 
-  // dq (16x16x32 MFMA).  CW = 64: wave w takes frame w / 4 and the voxel
-  // k-steps w % 4, + 4, ... for all CT channel tiles, so one converted B
+  // dq (16x16x32 MFMA).  CW = 64 (and 32 at three frames): wave w takes
+  // frame w / 4 and the voxel k-steps w % 4, + 4, ... for all CT channel
+  // tiles, so one converted B
   // operand feeds CT MFMA pairs; the 4 partial dq are summed at the end.
   // Wider windows (registers): task t = (frame t / CT, channels 16*(t % CT) +
   // [0, 16)) for t = w + 8 j over all k-steps.  dK/dV (32x32x16 MFMA, one per
   // frame): task t = (channels 32*(t % NC2) + [0, 32), 32-voxel block t / NC2)
   // for t = w + 8 i.
   constexpr int CT = CW / 16, NC2 = CW / 32;
-  constexpr bool DQK = CW == 64;  // k-split dq
+  constexpr bool DQK = CW == 64 || (CW == 32 && FR == 3);  // k-split dq
   constexpr int KPQ = NW / kP2Frames;  // k phases per frame (k-split dq)
   constexpr int NDQ = DQK ? CT : (kP2Frames * CT + NW - 1) / NW;  // dq accumulators
   const int mq = tl.lane & 15, kq = 8 * (tl.lane >> 4);
@@ -874,12 +876,14 @@ __global__ __launch_bounds__(256) void acc_to_out_kernel(const float* __restrict
 // three 32-channel windows for three frames: 8% slower; hd 32 would spill).
 template <int HD, typename E>
 constexpr int p2_frames() {
-  return sizeof(E) == 2 && (HD == 64 || HD == 128) ? 3 : 2;
+  return sizeof(E) == 2 && (HD == 64 || HD == 96 || HD == 128) ? 3 : 2;
 }
 
 // Channel window of the second backward kernel: the whole head where the LDS
 // takes its K^T and q/dO stages beside the tables, else 64 channels (32 for
-// fp32 head_dim 96).
+// fp32 head_dim 96).  bf16 head_dim 96 at three frames runs a 64- and a
+// 32-channel window (two launches): 8% faster than two frames over the whole
+// head at the 46,800-token DiT-block shape.
 template <int HD, typename E>
 constexpr int p2_window() {
   if constexpr (sizeof(E) == 2) return p2_frames<HD, E>() == 3 && HD > 64 ? 64 : HD;
@@ -900,7 +904,12 @@ void launch_bwd_pair(const msd_dsa3d_desc& d, const void* q, const void* k, cons
   hipLaunchKernelGGL((dsa3d_bwd_p1_kernel<HD, E>), g1, dim3(tiled::kThreads), 0, s, a1, o, go,
                      lse, dlse, goff, p_ws, b_ws);
   hipLaunchKernelGGL((dsa3d_bwd_p2_kernel<HD, CW, E, FR>), g2, dim3(P2Tile<FR>::Threads), 0, s,
-                     a2, go, p_ws, b_ws, gq, dk_acc, dv_acc);
+                     a2, go, p_ws, b_ws, gq, dk_acc, dv_acc, 0);
+  if constexpr (HD % CW != 0) {  // bf16 head_dim 96: a 64- and a 32-channel window
+    g2.z = 1;
+    hipLaunchKernelGGL((dsa3d_bwd_p2_kernel<HD, HD % CW, E, FR>), g2, dim3(P2Tile<FR>::Threads), 0,
+                       s, a2, go, p_ws, b_ws, gq, dk_acc, dv_acc, CW * (HD / CW));
+  }
 }
 
 template <typename E>

@@ -534,11 +534,20 @@ struct StageRows {
   op_t<E> x[G][2];  // [channel group][voxel]
 };
 
+// The thread index is read opaquely, so the map is recomputed where used
+// rather than kept live across a plane loop (where the dq/dK/dV kernel would
+// spill it, and every spill reload waits for the outstanding atomics).
+__device__ __forceinline__ int stage_tid() {
+  int t = static_cast<int>(threadIdx.x);
+  asm volatile("" : "+v"(t));
+  return t;
+}
 __device__ __forceinline__ int stage_pair() {
-  return 16 * ((threadIdx.x >> 6) & 7) + (threadIdx.x & 15);
+  const int t = stage_tid();
+  return 16 * ((t >> 6) & 7) + (t & 15);
 }
 __device__ __forceinline__ int stage_group0() {
-  return (threadIdx.x >> 4) & 3;
+  return (stage_tid() >> 4) & 3;
 }
 
 template <int NT, int CW, typename E>
