@@ -194,8 +194,9 @@ def run_gpu(steps, warmup, calibrate=False, cfg=CFG):
     return dict(total_ms=total_ms, wall_s=wall, per_phase_ms=per_phase, tokens=B * N)
 
 
-def cpu_baseline(slab_T=2):
-    """float32 CPU oracle (reference op sequence) on a T-slab of the workload."""
+def cpu_baseline(slab_T=6):
+    """float32 CPU oracle (reference op sequence) on a T-slab of the workload
+    (T=6: 6,144 tokens, ~10 s on 16 host threads)."""
     from oracle.dsa3d_ref import dsa3d_core_ref, dwconv3d_ref
 
     c = CFG
