@@ -1,6 +1,7 @@
 """Write golden vectors for 3D-DSA from the reference module itself.
 
-Run in the build container only (the GPU box has no reference tree):
+Run where the reference tree is present (the tests read only the committed
+fixtures):
 
     python tests/golden/make_golden.py [--ref /root/reference]
 

@@ -1,6 +1,6 @@
 """Parity of the HIP attention core and module against the reference (GPU).
 
-Tolerances, relative error = max|a-b| / max(max|b|, floor)
+Tolerances (the parity contract), relative error = max|a-b| / max(max|b|, floor)
 (tests/goldens.py:rel_err):
   * fp32 kernels vs the reference: 1e-4;
   * bf16 kernels vs an fp32 evaluation of the reference on the bf16-rounded
