@@ -1,30 +1,47 @@
 """Benchmark: 3D-DSA forward + backward through the HIP kernel set on one MI355X.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 3] [--no-cpu-baseline] [--copy-calibration]
-                    [--workload long-clip-65k|fp32-32k]
-    python bench.py --summarize TRACE_DIR FETCH_DIR WRITE_DIR   (rocprofv3 csv output -> profiles/)
+                    [--workload long-clip-65k|tiny-2k|fp32-32k|large-block-131k|dit-block-46k]
+    python bench.py --summarize WORKLOAD TRACE_DIR FETCH_DIR WRITE_DIR
+                    (rocprofv3 csv output -> markdown tables + profiles/traffic.json)
 
-Workload (one step = one pass of the hot path over one batch): the 65,536-token
-long-clip case -- B=1, T=64, H=W=32, dim 1024, 16 heads x 64, window 3x7x7,
-bf16 storage with fp32 accumulation, raw offsets ~ N(0, 0.5), x ~ N(0, 1),
-upstream grads ~ N(0, 1).  A step runs, on preallocated device buffers:
-  dw_conv 3x7x7 fwd, offset_net depthwise 3x3x3+GELU fwd, attention core fwd,
-  attention core bwd, 3x3x3+GELU bwd, 3x7x7 bwd
-i.e. every HIP kernel of the module's forward and backward (the dense GEMMs of
-the projections stay in hipBLASLt and are not part of the step).
+Workloads (one step = one pass of the hot path over one batch of synthetic
+input, every buffer preallocated and resident in HBM):
 
---workload fp32-32k runs the same step on the fp32 32,768-token case instead
-(B=2, T=16, H=W=32, dim 512, 8 heads x 64, raw offsets ~ N(0, 1.5)); its line
-names that workload and carries no CPU baseline.
+  long-clip-65k    (default) B=1, T=64, H=W=32 (65,536 tokens), dim 1024,
+                   16 heads x 64, bf16 storage with fp32 accumulation, raw
+                   offsets ~ N(0, 0.5)
+  tiny-2k          B=1, T=8, H=W=16 (2,048 tokens), dim 256, 4 x 64, fp32,
+                   forward only, offsets from the offset net (depthwise 3x3x3
+                   conv and 1x1 conv weights ~ N(0, 0.02))
+  fp32-32k         B=2, T=16, H=W=32 (32,768 tokens), dim 512, 8 x 64, fp32,
+                   raw offsets ~ N(0, 1.5)
+  large-block-131k B=1, T=32, H=W=64 (131,072 tokens), dim 3072, 24 x 128,
+                   bf16, offsets from the offset net (conv weights ~ N(0, 0.05))
+  dit-block-46k    B=1, T=13, H=45, W=80 (46,800 tokens), dim 1536, 16 x 96,
+                   bf16, offsets from the offset net with its bias ~ U(-4, 4)
+                   voxels (weights ~ N(0, 0.02))
 
-Prints one JSON line.  `value` is tokens/s of the whole step; `roofline` is the
-dominant kernel's algorithmic HBM bytes per launch over its average duration,
-timed with events on the launch stream; `roofline.traffic` is the measured
-L2<->fabric bytes per launch of that kernel from profiles/traffic.json (two
-rocprofv3 --pmc runs, FETCH_SIZE and WRITE_SIZE, each scaled by the same
+with window 3x7x7, x, q, k, v ~ N(0, 1) and upstream grads ~ N(0, 1).  A step
+runs dw_conv 3x7x7 fwd, offset_net depthwise 3x3x3+GELU fwd, attention core
+fwd, and (except tiny-2k, a forward config) attention core bwd, 3x3x3+GELU
+bwd, 3x7x7 bwd: every HIP kernel of the module's forward and backward.  The
+dense GEMMs (projections, 1x1 offset conv) stay in hipBLASLt and are not part
+of the step; offsets from the offset net are computed once before timing.
+
+Prints one JSON line.  `value` is tokens/s of the whole step.  `hbm_gbps` is the
+step's algorithmic bytes over its time, with the byte model of `byte_model`
+(each interface tensor once at its dtype: core fwd e(4D + C) + 4 nh, core bwd
+e(8D + 2C) + 4 nh, depthwise pair 3eD fwd + 4eD bwd, per token).  `roofline`
+is the dominant kernel's own compulsory bytes per launch over its average
+duration, timed with events on the launch stream; `roofline.traffic` is the
+measured L2<->fabric bytes per launch of that kernel from profiles/traffic.json
+(two rocprofv3 --pmc runs, FETCH_SIZE and WRITE_SIZE, each scaled by the same
 counter on a plain copy of known size -- see --copy-calibration), or null when
-no measurement for that kernel is recorded; `cpu_baseline` is the float32 CPU
-oracle (the reference op sequence) on a bounded T-slab of the same workload.
+none is recorded for the workload; `cpu_baseline` is the float32 CPU oracle
+(the reference op sequence) on a bounded slab of the same workload, median of
+3 timed runs after a warm-up, its tokens/s taken as the workload's
+(slab-extrapolated).
 
 --copy-calibration first runs a plain 512 MiB -> 512 MiB bf16 copy (torch.neg)
 twice, so a counter run of this script also measures the copy the counters
@@ -38,6 +55,8 @@ import ctypes
 import json
 import math
 import os
+import platform
+import statistics
 import sys
 import time
 
@@ -49,24 +68,50 @@ if ROOT not in sys.path:
 
 METRIC = "3D-DSA fwd+bwd tokens/sec at 65k tokens bf16; achieved HBM GB/s (% of peak)"
 HBM_PEAK_GBPS = 8000.0
+DEFAULT = "long-clip-65k"
 
-CFG = dict(B=1, T=64, H=32, W=32, D=1024, nh=16, hd=64, kernel=(3, 7, 7), off_std=0.5,
-           dtype="bf16", workload="3D-DSA fwd+bwd HIP kernel set, long-clip 65,536 tokens",
-           metric=METRIC)
+# offsets: ("normal", std) raw offsets; ("net", conv std, 1x1 weight std, bias) from
+# the offset net, bias ("uniform", a) ~ U(-a, a) or ("normal", std)
 WORKLOADS = {
-    "long-clip-65k": CFG,
-    "fp32-32k": dict(B=2, T=16, H=32, W=32, D=512, nh=8, hd=64, kernel=(3, 7, 7), off_std=1.5,
-                     dtype="fp32", workload="3D-DSA fwd+bwd HIP kernel set, fp32 32,768 tokens",
-                     metric="3D-DSA fwd+bwd tokens/sec at 32k tokens fp32"),
+    "long-clip-65k": dict(
+        B=1, T=64, H=32, W=32, D=1024, nh=16, kernel=(3, 7, 7), dtype="bf16",
+        offsets=("normal", 0.5), backward=True, metric=METRIC,
+        workload="3D-DSA fwd+bwd HIP kernel set, long-clip 65,536 tokens",
+        cpu_slab=dict(T=4)),
+    "tiny-2k": dict(
+        B=1, T=8, H=16, W=16, D=256, nh=4, kernel=(3, 7, 7), dtype="fp32",
+        offsets=("net", 0.02, 0.02, ("normal", 0.02)), backward=False,
+        metric="3D-DSA fwd tokens/sec at 2k tokens fp32",
+        workload="3D-DSA fwd HIP kernel set, tiny 2,048 tokens", cpu_slab=dict()),
+    "fp32-32k": dict(
+        B=2, T=16, H=32, W=32, D=512, nh=8, kernel=(3, 7, 7), dtype="fp32",
+        offsets=("normal", 1.5), backward=True,
+        metric="3D-DSA fwd+bwd tokens/sec at 32k tokens fp32",
+        workload="3D-DSA fwd+bwd HIP kernel set, fp32 32,768 tokens", cpu_slab=dict(B=1, T=4)),
+    "large-block-131k": dict(
+        B=1, T=32, H=64, W=64, D=3072, nh=24, kernel=(3, 7, 7), dtype="bf16",
+        offsets=("net", 0.05, 0.05, ("normal", 0.05)), backward=True,
+        metric="3D-DSA fwd+bwd tokens/sec at 131k tokens bf16",
+        workload="3D-DSA fwd+bwd HIP kernel set, large-block 131,072 tokens, 24 x 128",
+        cpu_slab=dict(T=2, H=24, W=24)),
+    "dit-block-46k": dict(
+        B=1, T=13, H=45, W=80, D=1536, nh=16, kernel=(3, 7, 7), dtype="bf16",
+        offsets=("net", 0.02, 0.02, ("uniform", 4.0)), backward=True,
+        metric="3D-DSA fwd+bwd tokens/sec at 46.8k tokens bf16 (DiT-block shape)",
+        workload="3D-DSA fwd+bwd HIP kernel set, DiT-block 46,800 tokens, 16 x 96",
+        cpu_slab=dict(T=3, H=24, W=40)),
 }
 
 
-def algorithmic_bytes(cfg, e):
-    """Compulsory interface bytes per launch of each kernel (each tensor once)."""
+def _sizes(cfg):
     N = cfg["B"] * cfg["T"] * cfg["H"] * cfg["W"]
-    D, nh = cfg["D"], cfg["nh"]
     kt, kh, kw = cfg["kernel"]
-    C = nh * kt * kh * kw * 3
+    return N, cfg["D"], cfg["nh"], cfg["nh"] * kt * kh * kw * 3
+
+
+def kernel_bytes(cfg, e):
+    """Compulsory bytes per launch of each phase (each tensor once, at its dtype)."""
+    N, D, nh, C = _sizes(cfg)
     return {
         "dwconv7_fwd": N * 2 * e * D,            # read x, write y
         "dwconv3_gelu_fwd": N * 2 * e * D,       # read x, write gelu(z)
@@ -76,6 +121,19 @@ def algorithmic_bytes(cfg, e):
         "dwconv7_bwd": N * 3 * e * D,            # read x, dy; write dx
     }
 
+
+def step_bytes(cfg, e):
+    """Algorithmic bytes of one step with the depthwise pair counted as a unit:
+    x read once for both convs (fwd 3eD: read x, write F and y; bwd 4eD: read
+    x, dF, dy, write one dx)."""
+    N, D, nh, C = _sizes(cfg)
+    fwd = e * (4 * D + C) + 4 * nh + 3 * e * D
+    bwd = e * (8 * D + 2 * C) + 4 * nh + 4 * e * D
+    return N * (fwd + (bwd if cfg["backward"] else 0))
+
+
+BYTE_MODEL = ("per token: core fwd e(4D+C)+4nh, core bwd e(8D+2C)+4nh, depthwise pair "
+              "3eD fwd + 4eD bwd (x read once for both convs); each tensor once at its dtype")
 
 COPY_BYTES = 512 * 2 ** 20  # read and written once each by the calibration copy
 
@@ -89,18 +147,42 @@ def copy_calibration(dev):
     del src, dst
 
 
-def measured_traffic(kernel):
-    """Traffic bytes per launch recorded for `kernel` in profiles/traffic.json, or None."""
+def measured_traffic(workload, kernel):
+    """Traffic bytes per launch recorded for `kernel` of `workload` in
+    profiles/traffic.json, or None."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
     try:
         with open(path) as f:
-            rec = json.load(f).get(kernel)
-    except (OSError, ValueError):
+            rec = json.load(f).get(workload, {}).get(kernel)
+    except (OSError, ValueError, AttributeError):
         return None
     return None if rec is None else rec.get("bytes_per_launch")
 
 
-def run_gpu(steps, warmup, calibrate=False, cfg=CFG):
+def make_offsets(cfg, x, dev, dt, g):
+    """Raw offsets [B, N, C] for the workload (outside the timed region)."""
+    from megaslide_amd import dwconv3d
+
+    B, T, H, W, D = cfg["B"], cfg["T"], cfg["H"], cfg["W"], cfg["D"]
+    _, _, _, C = _sizes(cfg)
+    N = T * H * W
+    spec = cfg["offsets"]
+    if spec[0] == "normal":
+        return (torch.randn(B, N, C, generator=g, device=dev) * spec[1]).to(dt)
+    _, conv_std, w_std, (bias_kind, bias_a) = spec
+    w0 = (torch.randn(D, 1, 3, 3, 3, generator=g, device=dev) * conv_std).to(dt)
+    b0 = (torch.randn(D, generator=g, device=dev) * conv_std).to(dt)
+    w2 = (torch.randn(C, D, generator=g, device=dev) * w_std).to(dt)
+    if bias_kind == "uniform":
+        b2 = (torch.rand(C, generator=g, device=dev) * 2 * bias_a - bias_a).to(dt)
+    else:
+        b2 = (torch.randn(C, generator=g, device=dev) * bias_a).to(dt)
+    with torch.no_grad():
+        feat = dwconv3d(x, w0, b0, (T, H, W), act="gelu")
+        return torch.nn.functional.linear(feat, w2, b2).contiguous()
+
+
+def run_gpu(cfg, steps, warmup, calibrate=False):
     from megaslide_amd import _lib
 
     lib = _lib.load()
@@ -108,13 +190,12 @@ def run_gpu(steps, warmup, calibrate=False, cfg=CFG):
     torch.cuda.set_device(dev)
     if calibrate:
         copy_calibration(dev)
-    c = cfg
-    B, T, H, W, D, nh, hd = c["B"], c["T"], c["H"], c["W"], c["D"], c["nh"], c["hd"]
-    kt, kh, kw = c["kernel"]
+    B, T, H, W, D, nh = cfg["B"], cfg["T"], cfg["H"], cfg["W"], cfg["D"], cfg["nh"]
+    hd = D // nh
+    kt, kh, kw = cfg["kernel"]
     N = T * H * W
-    C = nh * kt * kh * kw * 3
-    dt = torch.bfloat16 if c["dtype"] == "bf16" else torch.float32
-    mdt = _lib.MSD_BF16 if c["dtype"] == "bf16" else _lib.MSD_F32
+    dt = torch.bfloat16 if cfg["dtype"] == "bf16" else torch.float32
+    mdt = _lib.MSD_BF16 if cfg["dtype"] == "bf16" else _lib.MSD_F32
     g = torch.Generator(device=dev).manual_seed(3)
 
     def rnd(*shape, std=1.0):
@@ -122,7 +203,7 @@ def run_gpu(steps, warmup, calibrate=False, cfg=CFG):
 
     x = rnd(B, N, D)
     q, k, v = rnd(B, N, D), rnd(B, N, D), rnd(B, N, D)
-    off = rnd(B, N, C, std=c["off_std"])
+    off = make_offsets(cfg, x, dev, dt, g)
     dout, dF, dY = rnd(B, N, D), rnd(B, N, D), rnd(B, N, D)
     w7, b7 = rnd(D, 1, kt, kh, kw, std=0.05), rnd(D, std=0.02)
     w3, b3 = rnd(D, 1, 3, 3, 3, std=0.1), rnd(D, std=0.02)
@@ -137,12 +218,13 @@ def run_gpu(steps, warmup, calibrate=False, cfg=CFG):
     dsa = _lib.DsaDesc(B, T, H, W, nh, hd, kt, kh, kw, mdt, D, D, D, 1.0, 1.0 / math.sqrt(hd))
     cv7 = _lib.ConvDesc(B, T, H, W, D, kt, kh, kw, mdt, 0)
     cv3 = _lib.ConvDesc(B, T, H, W, D, 3, 3, 3, mdt, 1)
-    ws_dsa = torch.empty(lib.msd_dsa3d_bwd_workspace_size(ctypes.byref(dsa)), dtype=torch.uint8,
-                         device=dev)
-    ws7 = torch.empty(lib.msd_dwconv3d_bwd_workspace_size(ctypes.byref(cv7)), dtype=torch.uint8,
-                      device=dev)
-    ws3 = torch.empty(lib.msd_dwconv3d_bwd_workspace_size(ctypes.byref(cv3)), dtype=torch.uint8,
-                      device=dev)
+
+    def ws(nbytes):
+        return torch.empty(max(int(nbytes), 16), dtype=torch.uint8, device=dev)
+
+    ws_dsa = ws(lib.msd_dsa3d_bwd_workspace_size(ctypes.byref(dsa)))
+    ws7 = ws(lib.msd_dwconv3d_bwd_workspace_size(ctypes.byref(cv7)))
+    ws3 = ws(lib.msd_dwconv3d_bwd_workspace_size(ctypes.byref(cv3)))
     stream = torch.cuda.current_stream(dev)
     sh = stream.cuda_stream
     P = lambda t: t.data_ptr()  # noqa: E731
@@ -152,14 +234,17 @@ def run_gpu(steps, warmup, calibrate=False, cfg=CFG):
         ("dwconv3_gelu_fwd", lambda: lib.msd_dwconv3d_fwd(ctypes.byref(cv3), P(x), P(w3), P(b3), P(F), sh)),
         ("dsa3d_fwd", lambda: lib.msd_dsa3d_fwd(ctypes.byref(dsa), P(q), P(k), P(v), P(off), P(out),
                                                 P(lse), sh)),
-        ("dsa3d_bwd", lambda: lib.msd_dsa3d_bwd(ctypes.byref(dsa), P(q), P(k), P(v), P(off), P(out),
-                                                P(dout), P(lse), None, P(dq), P(dk), P(dv), P(doff),
-                                                P(ws_dsa), ws_dsa.numel(), sh)),
-        ("dwconv3_gelu_bwd", lambda: lib.msd_dwconv3d_bwd(ctypes.byref(cv3), P(x), P(w3), P(b3), P(dF),
-                                                          P(dx3), P(dw3), P(db3), P(ws3), ws3.numel(), sh)),
-        ("dwconv7_bwd", lambda: lib.msd_dwconv3d_bwd(ctypes.byref(cv7), P(x), P(w7), P(b7), P(dY),
-                                                     P(dx7), P(dw7), P(db7), P(ws7), ws7.numel(), sh)),
     ]
+    if cfg["backward"]:
+        phases += [
+            ("dsa3d_bwd", lambda: lib.msd_dsa3d_bwd(ctypes.byref(dsa), P(q), P(k), P(v), P(off), P(out),
+                                                    P(dout), P(lse), None, P(dq), P(dk), P(dv), P(doff),
+                                                    P(ws_dsa), ws_dsa.numel(), sh)),
+            ("dwconv3_gelu_bwd", lambda: lib.msd_dwconv3d_bwd(ctypes.byref(cv3), P(x), P(w3), P(b3), P(dF),
+                                                              P(dx3), P(dw3), P(db3), P(ws3), ws3.numel(), sh)),
+            ("dwconv7_bwd", lambda: lib.msd_dwconv3d_bwd(ctypes.byref(cv7), P(x), P(w7), P(b7), P(dY),
+                                                         P(dx7), P(dw7), P(db7), P(ws7), ws7.numel(), sh)),
+        ]
 
     def step(events=None):
         for i, (name, fn) in enumerate(phases):
@@ -194,55 +279,86 @@ def run_gpu(steps, warmup, calibrate=False, cfg=CFG):
     return dict(total_ms=total_ms, wall_s=wall, per_phase_ms=per_phase, tokens=B * N)
 
 
-def cpu_baseline(slab_T=6):
-    """float32 CPU oracle (reference op sequence) on a T-slab of the workload
-    (T=6: 6,144 tokens, ~10 s on 16 host threads)."""
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline(cfg, runs=3):
+    """float32 CPU oracle (reference op sequence) on a slab of the workload: the
+    same kernel set (both depthwise convs and the attention core, forward and,
+    for a training workload, backward), one warm-up then `runs` timed runs; the
+    median's tokens/s stands for the workload's (slab-extrapolated)."""
     from oracle.dsa3d_ref import dsa3d_core_ref, dwconv3d_ref
 
-    c = CFG
-    B, H, W, D, nh = c["B"], c["H"], c["W"], c["D"], c["nh"]
-    T = slab_T
+    slab = dict(B=cfg["B"], T=cfg["T"], H=cfg["H"], W=cfg["W"])
+    full_cfg = dict(slab)
+    slab.update(cfg["cpu_slab"])
+    B, T, H, W = slab["B"], slab["T"], slab["H"], slab["W"]
+    D, nh = cfg["D"], cfg["nh"]
+    kt, kh, kw = cfg["kernel"]
     N = T * H * W
-    C = nh * 147 * 3
+    C = nh * kt * kh * kw * 3
     torch.manual_seed(0)
-    x = torch.randn(B, N, D, requires_grad=True)
-    q, k, v = (torch.randn(B, N, D, requires_grad=True) for _ in range(3))
-    off = (torch.randn(B, N, C) * c["off_std"]).requires_grad_(True)
-    w7 = (torch.randn(D, 1, 3, 7, 7) * 0.05).requires_grad_(True)
-    w3 = (torch.randn(D, 1, 3, 3, 3) * 0.1).requires_grad_(True)
-    b = torch.zeros(D, requires_grad=True)
-    g = torch.randn(B, N, D)
+    grad = cfg["backward"]
+    x = torch.randn(B, N, D, requires_grad=grad)
+    q, k, v = (torch.randn(B, N, D, requires_grad=grad) for _ in range(3))
+    std = cfg["offsets"][1] if cfg["offsets"][0] == "normal" else 0.5
+    off = (torch.randn(B, N, C) * std).requires_grad_(grad)
+    w7 = (torch.randn(D, 1, kt, kh, kw) * 0.05).requires_grad_(grad)
+    w3 = (torch.randn(D, 1, 3, 3, 3) * 0.1).requires_grad_(grad)
+    b = torch.zeros(D, requires_grad=grad)
+    gy = torch.randn(B, N, D)
 
     def one():
-        y7 = dwconv3d_ref(x, w7, b, (T, H, W))
-        f = dwconv3d_ref(x, w3, b, (T, H, W), act="gelu")
-        o = dsa3d_core_ref(q, k, v, off, (T, H, W), nh, (3, 7, 7), 1.0, head_chunk=4)
-        torch.autograd.backward([y7, f, o], [g, g, g])
+        with torch.set_grad_enabled(grad):
+            y7 = dwconv3d_ref(x, w7, b, (T, H, W))
+            f = dwconv3d_ref(x, w3, b, (T, H, W), act="gelu")
+            o = dsa3d_core_ref(q, k, v, off, (T, H, W), nh, cfg["kernel"], 1.0, head_chunk=4)
+            if grad:
+                torch.autograd.backward([y7, f, o], [gy, gy, gy])
 
-    t0 = time.perf_counter()
-    one()
-    dt = time.perf_counter() - t0
-    return dict(value=N / dt, unit="tokens/s", cores=torch.get_num_threads(), kind="port",
-                sample=f"float32 CPU oracle (grid_sample/matmul/softmax restatement + conv3d), "
-                       f"fwd+bwd of the same kernel set on a T={T} slab "
-                       f"({N} tokens, H=W=32, dim 1024, 16x64, window 3x7x7), one run of {dt:.1f} s",
-                seconds=dt)
+    one()  # warm-up
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        one()
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    what = "fwd+bwd" if grad else "fwd"
+    return dict(
+        value=N * B / med, unit="tokens/s", cores=torch.get_num_threads(), kind="port",
+        sample=(f"{'slab-extrapolated' if full_cfg != slab else 'whole workload'}: float32 CPU "
+                f"oracle (grid_sample/matmul/softmax restatement + conv3d), {what} of the same "
+                f"kernel set on a B={B}, T={T}, H={H}, W={W} slab "
+                f"({B * N} tokens, dim {D}, {nh}x{D // nh}, window {kt}x{kh}x{kw}); median of "
+                f"{runs} runs after a warm-up: " + ", ".join(f"{t:.2f}" for t in times) + " s"),
+        cpu_model=_cpu_model(), torch_version=torch.__version__, seconds=med)
 
 
 PHASE_KERNELS = {  # bench phase -> the kernels its ABI call launches, in order
     "dsa3d_fwd": ["dsa3d_fwd_tiled_kernel"],
-    "dsa3d_bwd": ["fill_zero_f32", "dsa3d_bwd_p1_kernel", "dsa3d_bwd_p2_kernel",
-                  "acc_to_out_kernel"],
+    "dsa3d_bwd": ["dsa3d_bwd_p1_kernel", "dsa3d_bwd_p2_kernel"],
 }
 
 
-def summarize(trace_dir, fetch_dir, write_dir):
+def summarize(workload, trace_dir, fetch_dir, write_dir):
     """Per-kernel averages from a rocprofv3 --kernel-trace --stats run and the
     FETCH_SIZE / WRITE_SIZE runs of this script (--copy-calibration, one step);
-    prints a markdown summary and writes profiles/traffic.json (per bench phase:
-    the summed counters of the kernels of one ABI call, scaled by the copy)."""
+    prints a markdown summary and records in profiles/traffic.json, under the
+    workload, each bench phase's summed counters over the kernels of one ABI
+    call, scaled by the copy."""
     import csv
     import glob
+
+    cfg = WORKLOADS[workload]
+    e = 2 if cfg["dtype"] == "bf16" else 4
 
     def one(pattern):
         hits = glob.glob(os.path.join(pattern))
@@ -270,7 +386,13 @@ def summarize(trace_dir, fetch_dir, write_dir):
         """Counter sum over the first run of consecutive dispatches matching `names`."""
         for i in range(len(seq) - len(names) + 1):
             if all(names[j] in seq[i + j][1] for j in range(len(names))):
-                return sum(seq[i + j][2] for j in range(len(names)))
+                j, total = i, 0.0
+                # a phase may launch a kernel more than once (channel windows)
+                for name in names:
+                    while j < len(seq) and name in seq[j][1]:
+                        total += seq[j][2]
+                        j += 1
+                return total
         return None
 
     fetch = dispatches(one(os.path.join(fetch_dir, "*counter_collection.csv")), "FETCH_SIZE")
@@ -283,7 +405,7 @@ def summarize(trace_dir, fetch_dir, write_dir):
     sf, sw = copy_f[0] / kib, copy_w[0] / kib  # counter KiB per true KiB
     print(f"\ncalibration copy {COPY_BYTES >> 20} MiB -> {COPY_BYTES >> 20} MiB: "
           f"FETCH_SIZE {copy_f[0]:.0f} KiB (x{sf:.3f}), WRITE_SIZE {copy_w[0]:.0f} KiB (x{sw:.3f})\n")
-    ab = algorithmic_bytes(CFG, 2)
+    ab = kernel_bytes(cfg, e)
     rec = {}
     print("| phase (kernels) | FETCH KiB | WRITE KiB | traffic (scaled) | algorithmic | traffic / algorithmic |")
     print("|---|---|---|---|---|---|")
@@ -302,12 +424,19 @@ def summarize(trace_dir, fetch_dir, write_dir):
     for d, n, v in fetch:
         if "msd::" in n:
             print(f"| {d} | `{n[:70]}` | {v:.0f} | {wmap.get((d, n), float('nan')):.0f} |")
-    with open(os.path.join(ROOT, "profiles", "traffic.json"), "w") as f:
-        json.dump(rec, f, indent=1)
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            allrec = json.load(f)
+    except (OSError, ValueError):
+        allrec = {}
+    allrec[workload] = rec
+    with open(path, "w") as f:
+        json.dump(allrec, f, indent=1)
 
 
 def main():
-    if len(sys.argv) == 5 and sys.argv[1] == "--summarize":
+    if len(sys.argv) == 6 and sys.argv[1] == "--summarize":
         summarize(*sys.argv[2:])
         return
     ap = argparse.ArgumentParser()
@@ -317,7 +446,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run a 512 MiB copy first (scale for the FETCH_SIZE/WRITE_SIZE counters)")
-    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="long-clip-65k")
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default=DEFAULT)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: the 3D-DSA kernels run on a single MI355X "
@@ -326,15 +455,16 @@ def main():
         sys.exit(2)
 
     cfg = WORKLOADS[args.workload]
-    r = run_gpu(args.steps, args.warmup, args.copy_calibration, cfg)
+    r = run_gpu(cfg, args.steps, args.warmup, args.copy_calibration)
     e = 2 if cfg["dtype"] == "bf16" else 4
-    ab = algorithmic_bytes(cfg, e)
+    kb = kernel_bytes(cfg, e)
     ms_step = r["total_ms"] / args.steps
     tokens_s = r["tokens"] / (ms_step / 1e3)
-    step_bytes = sum(ab.values())
+    sbytes = step_bytes(cfg, e)
     dom = max(r["per_phase_ms"], key=r["per_phase_ms"].get)
     dom_ms = r["per_phase_ms"][dom]
-    achieved = ab[dom] / (dom_ms / 1e3) / 1e9
+    achieved = kb[dom] / (dom_ms / 1e3) / 1e9
+    N, D, nh, _ = _sizes(cfg)
     line = {
         "metric": cfg["metric"],
         "value": round(tokens_s, 1),
@@ -350,12 +480,17 @@ def main():
         "data": "synthetic",
         "config": {
             "workload": cfg["workload"],
-            "B": cfg["B"], "T": cfg["T"], "H": cfg["H"], "W": cfg["W"], "dim": cfg["D"],
-            "heads": cfg["nh"], "head_dim": cfg["hd"], "window": list(cfg["kernel"]),
-            "offsets": f"raw ~ N(0, {cfg['off_std']})", "accumulation": "fp32",
+            "B": cfg["B"], "T": cfg["T"], "H": cfg["H"], "W": cfg["W"], "dim": D,
+            "heads": nh, "head_dim": D // nh, "window": list(cfg["kernel"]),
+            "offsets": (f"raw ~ N(0, {cfg['offsets'][1]})" if cfg["offsets"][0] == "normal" else
+                        "offset net: depthwise 3x3x3 + GELU + 1x1, weights ~ N(0, {}) / N(0, {}), "
+                        "bias {} {}".format(*cfg["offsets"][1:3], *cfg["offsets"][3])),
+            "accumulation": "fp32", "pass": "fwd+bwd" if cfg["backward"] else "fwd",
         },
-        "hbm_gbps": round(step_bytes / (ms_step / 1e3) / 1e9, 1),
-        "hbm_frac_of_peak": round(step_bytes / (ms_step / 1e3) / 1e9 / HBM_PEAK_GBPS, 4),
+        "hbm_gbps": round(sbytes / (ms_step / 1e3) / 1e9, 1),
+        "hbm_frac_of_peak": round(sbytes / (ms_step / 1e3) / 1e9 / HBM_PEAK_GBPS, 4),
+        "byte_model": BYTE_MODEL,
+        "step_algorithmic_bytes": sbytes,
         "roofline": {
             "bound": "hbm",
             "kernel": dom,
@@ -363,15 +498,15 @@ def main():
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
-            "traffic": measured_traffic(dom) if cfg is CFG else None,
-            "algorithmic_bytes_per_launch": ab[dom],
+            "traffic": measured_traffic(args.workload, dom),
+            "algorithmic_bytes_per_launch": kb[dom],
             "avg_launch_ms": round(dom_ms, 4),
         },
         "per_kernel_ms": {k: round(v, 4) for k, v in r["per_phase_ms"].items()},
         "wall_s_timed_region": round(r["wall_s"], 3),
     }
-    if not args.no_cpu_baseline and cfg is CFG:
-        cb = cpu_baseline()
+    if not args.no_cpu_baseline:
+        cb = cpu_baseline(cfg)
         line["cpu_baseline"] = {k: (round(v, 2) if isinstance(v, float) else v)
                                 for k, v in cb.items() if k != "seconds"}
     print(json.dumps(line), flush=True)

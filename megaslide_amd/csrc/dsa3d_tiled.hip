@@ -135,7 +135,7 @@ __global__ __launch_bounds__(kThreads, (fwd_min_waves<HD, E>())) void dsa3d_fwd_
   const float inv_den = 1.0f / den;
 #pragma unroll
   for (int i = 0; i < kSlots; ++i)
-    sc[i] *= inv_den * slot_dropout(sl[i], a.drop) * kFixA;  // p (dropped), fixed-point units
+    sc[i] *= inv_den * slot_dropout(sl[i], a.drop) * a.fix_a;  // p (dropped), fixed-point units
   if (lse != nullptr && tl.q_ok && tl.sub == 0) lse[tl.qn * a.nh + tl.head] = mx + logf(den);
 
   // ---- pass 2: O = A . V ------------------------------------------------------
@@ -164,7 +164,7 @@ __global__ __launch_bounds__(kThreads, (fwd_min_waves<HD, E>())) void dsa3d_fwd_
     const Walk wn = walk_next(box, w);
     const Chunk& c = w.c;
     const int z = w.z;
-    // A in fixed point (scale 2^30), buffer it % NB: zeroed during the previous step
+    // A in fixed point (scale fix_a), buffer it % NB: zeroed during the previous step
     int* const s_atab = reinterpret_cast<int*>(s_tab[it % NB]);
     int* row = &s_atab[tl.q * kSRow];
     __syncthreads();  // the previous step's MFMAs are done with V^T; this buffer is zeroed
@@ -221,7 +221,7 @@ __global__ __launch_bounds__(kThreads, (fwd_min_waves<HD, E>())) void dsa3d_fwd_
     const int m = e / HD, ch = e - m * HD;
     const int64_t n = tile_row(a, tl, m);
     if (n >= 0)
-      out[n * (static_cast<int64_t>(a.nh) * HD) + tl.head * HD + ch] = from_f32<E>(o * kFixAInv);
+      out[n * (static_cast<int64_t>(a.nh) * HD) + tl.head * HD + ch] = from_f32<E>(o * a.fix_a_inv);
   }
 }
 
@@ -513,12 +513,12 @@ __global__ __launch_bounds__(P2Tile<FR>::Threads) void dsa3d_bwd_p2_kernel(
   // p and ds scale in fixed-point units from here on
 #pragma unroll
   for (int i = 0; i < kP2Slots; ++i) {
-    p[i] *= kFixA;
+    p[i] *= a.fix_a;
     bsc[i] *= bscale;
   }
   __syncthreads();
   // stage q and dO of the tile transposed, carrying the fixed-point scales of
-  // B (per query) and A (2^-30) for the dK/dV products: item e moves 8
+  // B (per query) and A (1 / fix_a) for the dK/dV products: item e moves 8
   // channels of one row
   for (int e = threadIdx.x; e < 2 * kP2Q * (CW / 8); e += NT) {
     const int cg = e % (CW / 8), m = (e / (CW / 8)) % kP2Q, tensor = e / (kP2Q * (CW / 8));
@@ -528,7 +528,7 @@ __global__ __launch_bounds__(P2Tile<FR>::Threads) void dsa3d_bwd_p2_kernel(
       const E* src = tensor == 0 ? static_cast<const E*>(a.q) + n * a.qs : dout + n * D;
       x = load_op<E>(src + cw0 + 8 * cg);
     }
-    const float sc = tensor == 0 ? s_binv[m] : kFixAInv;
+    const float sc = tensor == 0 ? s_binv[m] : a.fix_a_inv;
     if constexpr (sizeof(E) == 2) {
       const u32x4_t xb = __builtin_bit_cast(u32x4_t, x);
 #pragma unroll
@@ -772,6 +772,8 @@ tiled::Args make_tiled_args(const msd_dsa3d_desc& d, const void* q, const void* 
   a.r_kw = 1.0f / static_cast<float>(d.kw);
   a.r_khkw = 1.0f / static_cast<float>(d.kh * d.kw);
   a.drop = dropout_args(d);
+  a.fix_a = tiled::fix_a_scale(a.drop);
+  a.fix_a_inv = 1.0f / a.fix_a;
   return a;
 }
 

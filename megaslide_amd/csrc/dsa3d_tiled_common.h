@@ -125,6 +125,7 @@ struct Args {
   float rbdiv_x, rbdiv_y, rbdiv_z;
   float r_kw, r_khkw;            // 1/kw, 1/(kh*kw): exact small-integer division
   DropoutArgs drop;              // attention dropout on the softmax weights
+  float fix_a, fix_a_inv;        // fixed-point scale of the A (= p w) tables and its inverse
 };
 
 // Geometry of one tap, kept in registers between the passes.
@@ -675,10 +676,23 @@ __device__ __forceinline__ Bilerp bilerp(const Slot& s, float t00, float t01, fl
 // Scatter tables (A = p w, B = ds scale w) accumulate in int32 fixed point:
 // LDS integer atomics run ~30x faster than fp32 ones on gfx950, and integer
 // sums are exact and order-independent.  A query's entries of A sum to at most
-// sum_k p_k = 1, so A uses the fixed scale 2^30; B uses 2^30 / sum_k |ds_k scale|
-// per query, which bounds every entry and every partial sum below 2^30.
+// sum_k p_k f_k, where f_k is the tap's dropout factor (1 without dropout; 0 or
+// 1/(1-p) with it), i.e. to at most F = 1/(1-p).  A therefore uses the scale
+// fix_a = 2^30 / 2^ceil(log2 F) (2^30 without dropout), which bounds every
+// entry and partial sum by 2^30 and keeps the inverse scale a power of two.  B
+// uses 2^30 / sum_k |ds_k scale| per query, which bounds every entry and every
+// partial sum by 2^30.
 constexpr float kFixA = 1073741824.0f;          // 2^30
 constexpr float kFixAInv = 1.0f / 1073741824.0f;
+
+// fix_a of a call with dropout factor `scale` (DropoutArgs::scale) when
+// dropout is on.
+inline float fix_a_scale(const DropoutArgs& d) {
+  if (d.threshold == 0) return kFixA;
+  int e = 0;
+  const float m = std::frexp(d.scale, &e);  // scale = m 2^e, m in [0.5, 1)
+  return std::ldexp(1.0f, 30 - (m == 0.5f ? e - 1 : e));
+}
 
 // Truncating conversion: one instruction; its error (< 2^-30 of the scale)
 // is far below the rounding the tables get before the MFMA (bf16: 2^-9; fp32:

@@ -60,6 +60,61 @@ def test_dropout_matches_oracle(case):
         assert e < tol, name
 
 
+@pytest.mark.parametrize("case", [
+    # dtype, T, H, W, nh, hd, kernel, q scale, offsets, p
+    # one tap per query: a kept tap carries p f = 1/(1-p) = 2.5 on one voxel
+    (torch.float32, 3, 8, 8, 2, 64, (1, 1, 1), 1.0, "zero", 0.6),
+    (torch.bfloat16, 3, 8, 8, 2, 64, (1, 1, 1), 1.0, "zero", 0.6),
+    # peaked softmax (q x 8): most of a query's mass on one tap, factor 4
+    (torch.float32, 3, 7, 9, 2, 64, (3, 7, 7), 8.0, "normal", 0.75),
+    (torch.bfloat16, 3, 7, 9, 2, 64, (3, 7, 7), 8.0, "normal", 0.75),
+    (torch.bfloat16, 2, 6, 8, 1, 128, (3, 7, 7), 8.0, "normal", 0.75),
+    # +-50-voxel offsets: the border clamp piles taps onto the volume's edge voxels
+    (torch.float32, 2, 6, 7, 2, 64, (3, 7, 7), 1.0, "clamp50", 0.6),
+    (torch.bfloat16, 2, 6, 7, 2, 96, (3, 7, 7), 1.0, "clamp50", 0.6),
+])
+def test_dropout_large_kept_weights_match_oracle(case):
+    """Kept weights scaled by 1/(1-p) can put more than a query's whole
+    softmax mass on one voxel; the fixed-point scatter tables must still hold
+    them.  Tiled kernels against the oracle with the same keep mask."""
+    dt, T, H, W, nh, hd, ks, qscale, off_mode, p = case
+    print(f"[dropout large] {case}", flush=True)
+    tol = 1e-4 if dt == torch.float32 else 2e-2
+    B, N, D = 1, T * H * W, nh * hd
+    C = nh * ks[0] * ks[1] * ks[2] * 3
+    g = torch.Generator().manual_seed(71 + N + hd)
+    q = (torch.randn(B, N, D, generator=g) * qscale).to(dt)
+    k, v, dout = (torch.randn(B, N, D, generator=g).to(dt) for _ in range(3))
+    if off_mode == "zero":
+        off = torch.zeros(B, N, C)
+    elif off_mode == "normal":
+        off = torch.randn(B, N, C, generator=g) * 0.5
+    else:
+        off = torch.sign(torch.randn(B, N, C, generator=g)) * 50.0
+    off = off.to(dt)
+    seed, offset = 0x0D1E0000 + N, 5
+    qq, kk, vv, oo = (t.float().clone().requires_grad_(True) for t in (q, k, v, off))
+    ref = dsa3d_core_ref(qq, kk, vv, oo, (T, H, W), nh, ks, 1.0, dropout=(p, seed, offset))
+    ref.backward(dout.float())
+    ts = [t.detach().to(DEV).requires_grad_(True) for t in (q, k, v, off)]
+    out = core()(*ts, (T, H, W), nh, ks, 1.0, algo="tiled", dropout_p=p, dropout_seed=seed,
+                 dropout_offset=offset)
+    out.backward(dout.to(DEV))
+    torch.cuda.synchronize()
+    errs = {"out": rel_err(out.detach().float().cpu(), ref.detach())}
+    # With one tap per query ds = p (f dp - dO.O) is zero up to the rounding of
+    # two products of size |f dp| (~20 here), so dq and dk are fp32 noise: they
+    # are measured against the scale of the gradient that does not vanish (dv).
+    single = ks == (1, 1, 1)
+    dv_scale = float(vv.grad.abs().max())
+    for name, t, r in zip(("dq", "dk", "dv", "doff"), ts, (qq, kk, vv, oo)):
+        floor = dv_scale if single and name in ("dq", "dk") else 1e-2
+        errs[name] = rel_err(t.grad.float().cpu(), r.grad, floor=floor)
+    print("  " + "  ".join(f"{k} {v:.2e}" for k, v in errs.items()), flush=True)
+    for name, e in errs.items():
+        assert e < tol, name
+
+
 @pytest.mark.parametrize("algo,dt", [("direct", torch.float32), ("tiled", torch.float32),
                                      ("tiled", torch.bfloat16)])
 def test_dropout_zero_and_determinism(algo, dt):
