@@ -116,7 +116,7 @@ hipError_t launch_dsa3d_bwd_tiled(const msd_dsa3d_desc& d, const void* q, const 
                                   const void* dout, const float* lse, const float* dlse, void* dq,
                                   void* dk, void* dv, void* doff, void* ws, hipStream_t s);
 size_t dsa3d_bwd_ws_bytes(const msd_dsa3d_desc& d);
-size_t dsa3d_tiled_bwd_extra_bytes(const msd_dsa3d_desc& d);
+size_t dsa3d_tiled_bwd_ws_bytes(const msd_dsa3d_desc& d);
 hipError_t launch_dwconv3d_fwd(const msd_dwconv3d_desc& d, const void* x, const void* w,
                                const void* b, void* y, hipStream_t s);
 hipError_t launch_dwconv3d_bwd(const msd_dwconv3d_desc& d, const void* x, const void* w,

@@ -378,12 +378,16 @@ hipError_t bwd_typed(const msd_dsa3d_desc& d, const CoreArgs& a, const void* out
 
 int dsa3d_max_head_dim() { return kGroup * 16; }
 
-// dK/dV fp32 accumulators, plus what the tiled backward needs when the
-// descriptor can take that path.
+// The larger of the two families' needs, so a descriptor the tiled kernels
+// take still runs if a pointer sends it to the direct ones: the direct
+// backward's dK/dV fp32 accumulators, the tiled backward's per-tap p and ds
+// (the larger whenever kt * kh * kw > head_dim: every tiled head size at the
+// reference 3x7x7 window).
 size_t dsa3d_bwd_ws_bytes(const msd_dsa3d_desc& d) {
   const int64_t rows = static_cast<int64_t>(d.B) * d.T * d.H * d.W;
-  return static_cast<size_t>(2 * rows * d.num_heads * d.head_dim) * sizeof(float) +
-         dsa3d_tiled_bwd_extra_bytes(d);
+  const size_t direct = static_cast<size_t>(2 * rows * d.num_heads * d.head_dim) * sizeof(float);
+  const size_t tiled = dsa3d_tiled_bwd_ws_bytes(d);
+  return direct > tiled ? direct : tiled;
 }
 
 hipError_t launch_dsa3d_fwd_direct(const msd_dsa3d_desc& d, const void* q, const void* k, const void* v,

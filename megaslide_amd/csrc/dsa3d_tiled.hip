@@ -260,7 +260,7 @@ template <int HD, typename E>
 __global__ __launch_bounds__(kThreads, (p1_min_waves<HD, E>())) void dsa3d_bwd_p1_kernel(
     Args a, const E* __restrict__ out, const E* __restrict__ dout,
     const float* __restrict__ lse, const float* __restrict__ dlse, E* __restrict__ doff,
-    float* __restrict__ p_ws, float* __restrict__ b_ws) {
+    float* __restrict__ p_ws, float* __restrict__ b_ws, E* __restrict__ dk, E* __restrict__ dv) {
   // S and dP tables, double-buffered (one barrier per plane).  A buffer is
   // [S rows | zeros | dP rows | zeros]: a slot that misses the step reads the
   // zero block instead of its corners, so its values are 0 with no select, and
@@ -282,6 +282,19 @@ __global__ __launch_bounds__(kThreads, (p1_min_waves<HD, E>())) void dsa3d_bwd_p
   const E* const vp = static_cast<const E*>(a.v);
   for (int e = threadIdx.x; e < 2 * 2 * kP1Zero; e += kThreads)
     s_tb[e / (2 * kP1Zero)][((e / kP1Zero) & 1) * kP1Tab + kTQ * kSRow + e % kP1Zero] = 0.0f;
+  {
+    // The second kernel accumulates dK and dV in place: zero this tile's rows
+    // of the head first (the tiles of a launch partition the (token, head)
+    // pairs, and the second kernel starts after this one ends), 16 bytes a thread.
+    constexpr int CPR = HD * static_cast<int>(sizeof(E)) / 16;
+    for (int e = threadIdx.x; e < 2 * kTQ * CPR; e += kThreads) {
+      const int t = e / (kTQ * CPR), m = (e / CPR) % kTQ, ch = (e % CPR) * (16 / sizeof(E));
+      const int64_t row = tile_row(a, tl, m);
+      if (row < 0) continue;
+      E* dst = (t == 0 ? dk + row * a.ks : dv + row * a.vs) + tl.head * HD + ch;
+      *reinterpret_cast<uint4*>(dst) = uint4{0u, 0u, 0u, 0u};
+    }
+  }
 
   op_t<E> qx[HD / 32], gx[HD / 32];
   if constexpr (kTwoWg) {
@@ -457,11 +470,69 @@ constexpr int p2_qrow() {
   return sizeof(E) == 2 ? kTQ * FR + 8 : kTQ * FR + 4;
 }
 
+// Lanes 2j and 2j + 1 of a 32x32 MFMA result hold channels c and c + 1 (c
+// even) of the same voxels; x0 and x1 are a lane's values at two voxels.  The
+// even lane assembles the (c, c + 1) pair of the first voxel and the odd lane
+// that of the second, swapping one value through DPP (quad_perm 1, 0, 3, 2).
+__device__ __forceinline__ void adjacent_pair(float x0, float x1, bool odd, float& lo, float& hi) {
+  const float keep = odd ? x1 : x0, send = odd ? x0 : x1;
+  const float recv =
+      __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(send), 0xB1, 0xF, 0xF, false));
+  lo = odd ? recv : keep;
+  hi = odd ? keep : recv;
+}
+
+// Adds a 32-voxel x 32-channel block of dK or dV (a 32x32 MFMA result; lane l
+// holds channel `ch` = window channel l % 32 and, in registers 4 g + i, voxel
+// 32 vb + 8 g + 4 (l / 32) + i) into `out` (token stride `stride`): fp32
+// atomic adds for fp32 storage, packed bf16-pair adds (rounded to nearest even)
+// for bf16.  s_rows gives each voxel's token row within the sample; the host
+// admits N * stride < 2^30 elements, so every offset is a 32-bit lane offset
+// from a wave-uniform base.  Untouched voxels (exact zeros) send nothing.
+template <typename E>
+__device__ __forceinline__ void flush_block(const Tile& tl, const f32x16_t& acc, const int* s_rows,
+                                            int vb, int nv, int ch, E* out, int64_t stride) {
+  char* const base = reinterpret_cast<char*>(out + tl.sample0 * stride);
+  const uint32_t st = static_cast<uint32_t>(stride);
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int v0 = 32 * vb + 8 * g + 4 * (tl.lane >> 5);
+    if constexpr (sizeof(E) == 4) {
+      int rr[4];
+      __builtin_memcpy(rr, &s_rows[v0], sizeof(rr));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float x = acc[4 * g + i];
+        if (v0 + i < nv && x != 0.0f)
+          atomicAdd(reinterpret_cast<float*>(base + (static_cast<uint32_t>(rr[i]) * st + ch) * 4u), x);
+      }
+    } else {
+      const bool odd = tl.lane & 1;
+      const uint32_t che = static_cast<uint32_t>(ch & ~1);
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        float lo, hi;
+        adjacent_pair(acc[4 * g + 2 * m], acc[4 * g + 2 * m + 1], odd, lo, hi);
+        // the lane's own voxel: read per lane (a select between two entries of
+        // a register array becomes a scratch-memory index)
+        const int vi = v0 + 2 * m + (odd ? 1 : 0);
+        const uint32_t row = static_cast<uint32_t>(s_rows[vi]);
+        if (vi < nv && (lo != 0.0f || hi != 0.0f)) {
+          const f32x2_t f = {lo, hi};
+          __builtin_amdgcn_global_atomic_fadd_v2bf16(
+              reinterpret_cast<bf16x2_t*>(base + (row * st + che) * 2u),
+              __builtin_convertvector(f, bf16x2_t));
+        }
+      }
+    }
+  }
+}
+
 template <int HD, int CW, typename E, int FR>
 __global__ __launch_bounds__(P2Tile<FR>::Threads) void dsa3d_bwd_p2_kernel(
     Args a, const E* __restrict__ dout, const float* __restrict__ p_ws,
-    const float* __restrict__ b_ws, E* __restrict__ dq, float* __restrict__ dk_acc,
-    float* __restrict__ dv_acc, int cw_base) {
+    const float* __restrict__ b_ws, E* __restrict__ dq, E* __restrict__ dk, E* __restrict__ dv,
+    int cw_base) {
   static_assert(CW <= HD && CW % 32 == 0, "channel windows are whole 32-channel blocks");
   using G = P2Tile<FR>;
   constexpr int kP2Frames = FR, kP2Q = G::Q, kP2Subs = G::Subs, kP2Slots = G::Slots;
@@ -474,7 +545,7 @@ __global__ __launch_bounds__(P2Tile<FR>::Threads) void dsa3d_bwd_p2_kernel(
   int* const s_at = s_ab;
   int* const s_bt = s_ab + kTab;
   __shared__ __attribute__((aligned(16))) word_t<E> s_kt[CW * KR];      // K^T chunk
-  // per voxel: element offset (token row within the sample times D) of its accumulator row
+  // per voxel: its token row within the sample
   __shared__ __attribute__((aligned(16))) int s_rows[kChunkNV];
   __shared__ int s_red[NW][6];
   __shared__ __attribute__((aligned(16))) float s_binv[kP2Q];  // per query: 1 / fixed-point scale of B
@@ -585,7 +656,7 @@ __global__ __launch_bounds__(P2Tile<FR>::Threads) void dsa3d_bwd_p2_kernel(
       __builtin_memcpy(&s_bt[4 * e], &zz, sizeof(zz));
     }
     for (int vi = threadIdx.x; vi < c.nv; vi += NT)
-      s_rows[vi] = static_cast<int>(chunk_row(a, tl, c, z, vi) - tl.sample0) * D;
+      s_rows[vi] = static_cast<int>(chunk_row(a, tl, c, z, vi) - tl.sample0);
     store_stage<kP2Stage, CW, E>(c, kr, s_kt);
     if (kPrefetchK && it + 1 < nit)
       load_stage_rows<kP2Stage, CW, E>(a, tl, wn.c, wn.z, kp, a.ks, cw0, kr);
@@ -651,41 +722,27 @@ __global__ __launch_bounds__(P2Tile<FR>::Threads) void dsa3d_bwd_p2_kernel(
         }
       }
     }
-    // dK[v] += sum_q B[q][v] q[q];  dV[v] += sum_q A[q][v] dO[q]  (32x32 MFMA, fp32
-    // atomics; one register across the wave covers 2 voxels x 32 contiguous channels)
+    // dK[v] += sum_q B[q][v] q[q];  dV[v] += sum_q A[q][v] dO[q]  (32x32 MFMA),
+    // added into the dK and dV outputs with global atomics (executed past the
+    // L2).  One accumulator register across the wave covers 2 voxels x 32
+    // contiguous channels.
     for (int t = tl.wave;; t += NW) {
       const int c2 = t % NC2, vb = t / NC2;
       if (vb * 32 >= c.nv) break;
       const int och = 32 * c2 + (tl.lane & 31);
-      f32x16_t dk = {}, dv = {};
+      // dK, then dV: one accumulator live at a time (registers are the limit)
+      f32x16_t acc = {};
 #pragma unroll
-      for (int f = 0; f < kP2Frames; ++f) {
-        dk = mma32(table_t_rows<E>(s_bt, kP2Row, kTQ * f, vb, tl.lane),
-                   load_op<E>(&s_qt[0][och][kTQ * f + oq]), dk);
-        dv = mma32(table_t_rows<E>(s_at, kP2Row, kTQ * f, vb, tl.lane),
-                   load_op<E>(&s_qt[1][och][kTQ * f + oq]), dv);
-      }
-      const int ch2 = cw0 + och;
-      // accumulator rows of this sample: a wave-uniform base plus a 32-bit lane
-      // byte offset (the host admits N * D < 2^30), so the atomics use scalar-base
-      // addressing; untouched voxels (exact zeros) send nothing
-      char* const dk_s = reinterpret_cast<char*>(dk_acc + tl.sample0 * D);
-      char* const dv_s = reinterpret_cast<char*>(dv_acc + tl.sample0 * D);
+      for (int f = 0; f < kP2Frames; ++f)
+        acc = mma32(table_t_rows<E>(s_bt, kP2Row, kTQ * f, vb, tl.lane),
+                    load_op<E>(&s_qt[0][och][kTQ * f + oq]), acc);
+      flush_block<E>(tl, acc, s_rows, vb, c.nv, cw0 + och, dk, a.ks);
+      acc = f32x16_t{};
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        // registers 4g + i: voxel 32*vb + 8*g + 4*(lane/32) + i
-        const int v0 = 32 * vb + 8 * g + 4 * (tl.lane >> 5);
-        int rr[4];
-        __builtin_memcpy(rr, &s_rows[v0], sizeof(rr));
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const bool in = v0 + i < c.nv;
-          const uint32_t off = static_cast<uint32_t>(rr[i] + ch2) * 4u;
-          const float kv = dk[4 * g + i], vv = dv[4 * g + i];
-          if (in && kv != 0.0f) atomicAdd(reinterpret_cast<float*>(dk_s + off), kv);
-          if (in && vv != 0.0f) atomicAdd(reinterpret_cast<float*>(dv_s + off), vv);
-        }
-      }
+      for (int f = 0; f < kP2Frames; ++f)
+        acc = mma32(table_t_rows<E>(s_at, kP2Row, kTQ * f, vb, tl.lane),
+                    load_op<E>(&s_qt[1][och][kTQ * f + oq]), acc);
+      flush_block<E>(tl, acc, s_rows, vb, c.nv, cw0 + och, dv, a.vs);
     }
     __syncthreads();
     w = wn;
@@ -805,9 +862,10 @@ bool dsa3d_tiled_supported(const msd_dsa3d_desc& d, const void* q, const void* k
   if (tiles > 0x7fffffff || d.num_heads > 65535) return false;
   // 8-element (16- or 32-byte) vector loads of q/k/v rows
   if ((d.q_stride % 8) || (d.k_stride % 8) || (d.v_stride % 8)) return false;
-  // the dK/dV accumulator rows of a sample are addressed with 32-bit byte offsets
-  if (static_cast<int64_t>(d.T) * d.H * d.W * d.num_heads * d.head_dim >= (int64_t{1} << 30))
-    return false;
+  // dK/dV rows of a sample are addressed with 32-bit lane offsets (elements
+  // below 2^30, so bytes below 2^32 even for fp32)
+  const int64_t n = static_cast<int64_t>(d.T) * d.H * d.W;
+  if (n * d.k_stride >= (int64_t{1} << 30) || n * d.v_stride >= (int64_t{1} << 30)) return false;
   // K/V chunk rows are addressed as a 64-bit chunk base plus a 32-bit lane byte
   // offset (24-bit multiplies): kChunk * (W + 1) rows must span < 2^31 bytes
   for (const int64_t st : {d.k_stride, d.v_stride})
@@ -845,33 +903,6 @@ hipError_t launch_dsa3d_fwd_tiled(const msd_dsa3d_desc& d, const void* q, const 
 }
 
 namespace {
-// fp32 dK (blockIdx.y 0) or dV (1) accumulator [rows, D] -> the output type with
-// its token stride, 8 channels per thread (16- or 32-byte loads and stores; D
-// and the strides are multiples of 8, rows * D < 2^30).
-template <typename E>
-__global__ __launch_bounds__(256) void acc_to_out_kernel(const float* __restrict__ dk_acc,
-                                                         const float* __restrict__ dv_acc,
-                                                         E* __restrict__ dk, E* __restrict__ dv,
-                                                         int rows, int D, int64_t ks, int64_t vs) {
-  const int d8 = D / 8;
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= rows * d8) return;
-  const int r = i / d8, c = 8 * (i - r * d8);
-  const bool is_k = blockIdx.y == 0;
-  const float* src = (is_k ? dk_acc : dv_acc) + static_cast<int64_t>(r) * D + c;
-  E* dst = (is_k ? dk : dv) + static_cast<int64_t>(r) * (is_k ? ks : vs) + c;
-  f32x4_t x[2];
-  __builtin_memcpy(x, src, sizeof(x));
-  if constexpr (sizeof(E) == 2) {
-    uint16_t h[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) h[j] = from_f32<bf16>(x[j / 4][j % 4]).bits;
-    __builtin_memcpy(dst, h, sizeof(h));
-  } else {
-    __builtin_memcpy(dst, x, sizeof(x));
-  }
-}
-
 // Frames per tile of the second kernel: 3 for bf16 head_dim 64 and 128 (at
 // the 131,072-token hd-128 shape three frames in two 64-channel windows ran
 // 15% faster than two frames in one window), else 2 (bf16 hd 96 would need
@@ -895,8 +926,8 @@ constexpr int p2_window() {
 template <int HD, typename E>
 void launch_bwd_pair(const msd_dsa3d_desc& d, const void* q, const void* k, const void* v,
                      const void* off, const E* o, const E* go, const float* lse,
-                     const float* dlse, E* gq, E* goff, float* p_ws, float* b_ws, float* dk_acc,
-                     float* dv_acc, hipStream_t s) {
+                     const float* dlse, E* gq, E* gk, E* gv, E* goff, float* p_ws, float* b_ws,
+                     hipStream_t s) {
   constexpr int CW = p2_window<HD, E>(), FR = p2_frames<HD, E>();
   const tiled::Args a1 = make_tiled_args(d, q, k, v, off, tiled_tiles<1>(d));
   const tiled::Args a2 = make_tiled_args(d, q, k, v, off, tiled_tiles<FR>(d));
@@ -904,13 +935,13 @@ void launch_bwd_pair(const msd_dsa3d_desc& d, const void* q, const void* k, cons
   dim3 g2 = tiled_grid<FR>(d);
   g2.z = HD / CW;
   hipLaunchKernelGGL((dsa3d_bwd_p1_kernel<HD, E>), g1, dim3(tiled::kThreads), 0, s, a1, o, go,
-                     lse, dlse, goff, p_ws, b_ws);
+                     lse, dlse, goff, p_ws, b_ws, gk, gv);
   hipLaunchKernelGGL((dsa3d_bwd_p2_kernel<HD, CW, E, FR>), g2, dim3(P2Tile<FR>::Threads), 0, s,
-                     a2, go, p_ws, b_ws, gq, dk_acc, dv_acc, 0);
+                     a2, go, p_ws, b_ws, gq, gk, gv, 0);
   if constexpr (HD % CW != 0) {  // bf16 head_dim 96: a 64- and a 32-channel window
     g2.z = 1;
     hipLaunchKernelGGL((dsa3d_bwd_p2_kernel<HD, HD % CW, E, FR>), g2, dim3(P2Tile<FR>::Threads), 0,
-                       s, a2, go, p_ws, b_ws, gq, dk_acc, dv_acc, CW * (HD / CW));
+                       s, a2, go, p_ws, b_ws, gq, gk, gv, CW * (HD / CW));
   }
 }
 
@@ -918,44 +949,36 @@ template <typename E>
 hipError_t bwd_tiled_typed(const msd_dsa3d_desc& d, const void* q, const void* k, const void* v,
                            const void* off, const void* out, const void* dout, const float* lse,
                            const float* dlse, void* dq, void* dk, void* dv, void* doff,
-                           float* dk_acc, float* dv_acc, float* p_ws, float* b_ws, hipStream_t s) {
-  const int64_t rows = static_cast<int64_t>(d.B) * d.T * d.H * d.W;
-  const int D = d.num_heads * d.head_dim;
+                           float* p_ws, float* b_ws, hipStream_t s) {
   const auto* o = static_cast<const E*>(out);
   const auto* go = static_cast<const E*>(dout);
   auto* gq = static_cast<E*>(dq);
+  auto* gk = static_cast<E*>(dk);
+  auto* gv = static_cast<E*>(dv);
   auto* goff = static_cast<E*>(doff);
   switch (d.head_dim) {
     case 32:
-      launch_bwd_pair<32, E>(d, q, k, v, off, o, go, lse, dlse, gq, goff, p_ws, b_ws, dk_acc,
-                               dv_acc, s);
+      launch_bwd_pair<32, E>(d, q, k, v, off, o, go, lse, dlse, gq, gk, gv, goff, p_ws, b_ws, s);
       break;
     case 64:
-      launch_bwd_pair<64, E>(d, q, k, v, off, o, go, lse, dlse, gq, goff, p_ws, b_ws, dk_acc,
-                               dv_acc, s);
+      launch_bwd_pair<64, E>(d, q, k, v, off, o, go, lse, dlse, gq, gk, gv, goff, p_ws, b_ws, s);
       break;
     case 96:
-      launch_bwd_pair<96, E>(d, q, k, v, off, o, go, lse, dlse, gq, goff, p_ws, b_ws, dk_acc,
-                               dv_acc, s);
+      launch_bwd_pair<96, E>(d, q, k, v, off, o, go, lse, dlse, gq, gk, gv, goff, p_ws, b_ws, s);
       break;
     case 128:
-      launch_bwd_pair<128, E>(d, q, k, v, off, o, go, lse, dlse, gq, goff, p_ws, b_ws, dk_acc,
-                               dv_acc, s);
+      launch_bwd_pair<128, E>(d, q, k, v, off, o, go, lse, dlse, gq, gk, gv, goff, p_ws, b_ws, s);
       break;
     default:
       return hipErrorInvalidValue;
   }
-  const dim3 cgrid(static_cast<unsigned>((rows * (D / 8) + 255) / 256), 2);
-  hipLaunchKernelGGL(acc_to_out_kernel<E>, cgrid, dim3(256), 0, s, dk_acc, dv_acc,
-                     static_cast<E*>(dk), static_cast<E*>(dv), static_cast<int>(rows), D,
-                     d.k_stride, d.v_stride);
   return hipGetLastError();
 }
 }  // namespace
 
-// Workspace of the tiled backward beyond the dK/dV accumulators: p and
-// ds * softmax_scale of every tap (fp32 [token][head][tap] each).
-size_t dsa3d_tiled_bwd_extra_bytes(const msd_dsa3d_desc& d) {
+// Workspace of the tiled backward: p and ds * softmax_scale of every tap
+// (fp32 [token][head][tap] each).  dK and dV accumulate in the outputs.
+size_t dsa3d_tiled_bwd_ws_bytes(const msd_dsa3d_desc& d) {
   if ((d.dtype != MSD_BF16 && d.dtype != MSD_F32) || !tiled_head_dim(d.head_dim) ||
       d.kt * d.kh * d.kw > tiled::kMaxTaps)
     return 0;
@@ -968,19 +991,14 @@ hipError_t launch_dsa3d_bwd_tiled(const msd_dsa3d_desc& d, const void* q, const 
                                   const void* dout, const float* lse, const float* dlse, void* dq,
                                   void* dk, void* dv, void* doff, void* ws, hipStream_t s) {
   const int64_t rows = static_cast<int64_t>(d.B) * d.T * d.H * d.W;
-  const int D = d.num_heads * d.head_dim;
   const int64_t taps = rows * d.num_heads * d.kt * d.kh * d.kw;
-  float* dk_acc = static_cast<float*>(ws);
-  float* dv_acc = dk_acc + rows * D;
-  float* p_ws = dv_acc + rows * D;
+  float* p_ws = static_cast<float*>(ws);
   float* b_ws = p_ws + taps;
-  hipLaunchKernelGGL(fill_zero_f32, dim3(fill_blocks(2 * rows * D)), dim3(256), 0, s, dk_acc,
-                     2 * rows * D);
   if (d.dtype == MSD_BF16)
-    return bwd_tiled_typed<bf16>(d, q, k, v, off, out, dout, lse, dlse, dq, dk, dv, doff, dk_acc,
-                                 dv_acc, p_ws, b_ws, s);
-  return bwd_tiled_typed<float>(d, q, k, v, off, out, dout, lse, dlse, dq, dk, dv, doff, dk_acc,
-                                dv_acc, p_ws, b_ws, s);
+    return bwd_tiled_typed<bf16>(d, q, k, v, off, out, dout, lse, dlse, dq, dk, dv, doff, p_ws,
+                                 b_ws, s);
+  return bwd_tiled_typed<float>(d, q, k, v, off, out, dout, lse, dlse, dq, dk, dv, doff, p_ws,
+                                b_ws, s);
 }
 
 }  // namespace msd

@@ -155,30 +155,62 @@ def test_core_vs_oracle_random(shape, dtype, tol, algo):
     assert rel_err(od.grad.float().cpu(), ref[4]) < tol
 
 
+def _offsets(spec, B, T, H, W, D, C, dtype, g):
+    """Raw offsets [B, N, C] on the device: ("normal", std), or ("net", conv std,
+    1x1 weight std, bias) from an offset net (depthwise 3x3x3 conv + GELU + 1x1
+    conv, as the module predicts them) on x ~ N(0, 1), with the bias ("normal",
+    std) or ("uniform", a) ~ U(-a, a) voxels."""
+    from megaslide_amd import dwconv3d
+    N = T * H * W
+    if spec[0] == "normal":
+        return (torch.randn(B, N, C, generator=g, device=DEV) * spec[1]).to(dtype)
+    _, conv_std, w_std, (kind, a) = spec
+    x = torch.randn(B, N, D, generator=g, device=DEV).to(dtype)
+    w0 = (torch.randn(D, 1, 3, 3, 3, generator=g, device=DEV) * conv_std).to(dtype)
+    b0 = (torch.randn(D, generator=g, device=DEV) * conv_std).to(dtype)
+    w2 = (torch.randn(C, D, generator=g, device=DEV) * w_std).to(dtype)
+    if kind == "uniform":
+        b2 = (torch.rand(C, generator=g, device=DEV) * 2 * a - a).to(dtype)
+    else:
+        b2 = (torch.randn(C, generator=g, device=DEV) * a).to(dtype)
+    with torch.no_grad():
+        return F.linear(dwconv3d(x, w0, b0, (T, H, W), act="gelu"), w2, b2).contiguous()
+
+
 @pytest.mark.parametrize("cfg", [
-    # name, dtype, B, T, H, W, nh, hd, off_std, algo
-    ("fp32 B2 16x32x32 8x64", torch.float32, 2, 16, 32, 32, 8, 64, 1.5, "auto"),
-    ("fp32 B2 16x32x32 8x64 direct", torch.float32, 2, 16, 32, 32, 8, 64, 1.5, "direct"),
-    ("bf16 65536 tokens 16x64", torch.bfloat16, 1, 64, 32, 32, 16, 64, 0.5, "auto"),
-    ("bf16 131072 tokens 24x128", torch.bfloat16, 1, 32, 64, 64, 24, 128, 0.5, "auto"),
-    ("bf16 46800 tokens 16x96 (13x45x80)", torch.bfloat16, 1, 13, 45, 80, 16, 96, 2.5, "auto"),
+    # name, dtype, B, T, H, W, nh, hd, offsets, algo
+    ("fp32 B2 16x32x32 8x64", torch.float32, 2, 16, 32, 32, 8, 64, ("normal", 1.5), "auto"),
+    ("fp32 B2 16x32x32 8x64 direct", torch.float32, 2, 16, 32, 32, 8, 64, ("normal", 1.5),
+     "direct"),
+    ("bf16 65536 tokens 16x64", torch.bfloat16, 1, 64, 32, 32, 16, 64, ("normal", 0.5), "auto"),
+    # offsets from the offset net, conv weights ~ N(0, 0.05)
+    ("bf16 131072 tokens 24x128", torch.bfloat16, 1, 32, 64, 64, 24, 128,
+     ("net", 0.05, 0.05, ("normal", 0.05)), "auto"),
+    # offsets from the offset net with its bias ~ U(-4, 4) voxels
+    ("bf16 46800 tokens 16x96 (13x45x80)", torch.bfloat16, 1, 13, 45, 80, 16, 96,
+     ("net", 0.02, 0.02, ("uniform", 4.0)), "auto"),
 ])
 def test_core_full_size_sampled_queries_and_checksums(cfg):
     """Full-size shapes: exact per-query parity on sampled queries (fwd, dq,
-    d offsets) plus size-independent checksums of dK and dV.
+    d offsets), element-wise dK and dV over the whole volume for those
+    queries, and size-independent checksums of dK and dV.
 
     Sum over voxels of dV equals the sum over queries of dO (per channel),
     because every query's tap weights p_k * w_c sum to one; the sum of dK is
-    zero because sum_k ds_k = 0.
+    zero because sum_k ds_k = 0.  A second backward whose upstream gradient is
+    zero except at the sampled queries gives dK and dV that only those queries
+    feed (a query with dO = 0 has p dO = 0 and ds = p (dp - dO.O) = 0), so the
+    whole tensors are compared with the oracle's autograd over the same queries:
+    a scatter to a wrong voxel or a dropped or doubled flush shows there.
     """
-    name, dtype, B, T, H, W, nh, hd, off_std, algo = cfg
+    name, dtype, B, T, H, W, nh, hd, off_spec, algo = cfg
     print(f"[full size] {name}", flush=True)
     ks = (3, 7, 7)
     N, D = T * H * W, nh * hd
     C = nh * 147 * 3
     g = torch.Generator(device=DEV).manual_seed(7)
     q, k, v = (torch.randn(B, N, D, generator=g, device=DEV).to(dtype) for _ in range(3))
-    off = (torch.randn(B, N, C, generator=g, device=DEV) * off_std).to(dtype)
+    off = _offsets(off_spec, B, T, H, W, D, C, dtype, g)
     dout = torch.randn(B, N, D, generator=g, device=DEV).to(dtype)
     qd, kd, vd, od = (t.clone().requires_grad_(True) for t in (q, k, v, off))
     out = core()(qd, kd, vd, od, (T, H, W), nh, ks, 1.0, algo=algo)
@@ -194,7 +226,7 @@ def test_core_full_size_sampled_queries_and_checksums(cfg):
     assert sum_dk < (1e-5 if dtype == torch.float32 else 1e-2) * scale_dk
     # parity for sampled queries (first, last, random) against the fp32 oracle
     idx = torch.cat([torch.tensor([0, N - 1]), torch.randperm(N, generator=torch.Generator().manual_seed(3))[:30]])
-    ref_out, ref_dq, _, _, ref_doff = _oracle_core(
+    ref_out, ref_dq, ref_dk, ref_dv, ref_doff = _oracle_core(
         q.float(), k.float(), v.float(), off.float(), (T, H, W), nh, ks, 1.0,
         dout.float()[:, idx], query_index=idx, head_chunk=2)
     assert rel_err(out.detach()[:, idx.to(DEV)].float().cpu(), ref_out) < tol
@@ -202,6 +234,19 @@ def test_core_full_size_sampled_queries_and_checksums(cfg):
     ref_dq_rows = ref_dq[:, idx]
     assert rel_err(qgrad, ref_dq_rows) < tol
     assert rel_err(od.grad[:, idx.to(DEV)].float().cpu(), ref_doff[:, idx]) < tol
+    # the whole dK and dV of the sampled queries alone
+    dsparse = torch.zeros_like(dout)
+    dsparse[:, idx.to(DEV)] = dout[:, idx.to(DEV)]
+    for t in (qd, kd, vd, od):
+        t.grad = None
+    out = core()(qd, kd, vd, od, (T, H, W), nh, ks, 1.0, algo=algo)
+    out.backward(dsparse)
+    torch.cuda.synchronize()
+    e_dk = rel_err(kd.grad.float().cpu(), ref_dk)
+    e_dv = rel_err(vd.grad.float().cpu(), ref_dv)
+    print(f"  sampled-query dK {e_dk:.2e}  dV {e_dv:.2e}  (non-zero voxel rows: "
+          f"{int((ref_dv.abs().sum(-1) > 0).sum())})", flush=True)
+    assert e_dk < tol and e_dv < tol
 
 
 def test_nograd_forward_matches_grad_forward_and_streams():
