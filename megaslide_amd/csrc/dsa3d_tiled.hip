@@ -260,7 +260,8 @@ template <int HD, typename E>
 __global__ __launch_bounds__(kThreads, (p1_min_waves<HD, E>())) void dsa3d_bwd_p1_kernel(
     Args a, const E* __restrict__ out, const E* __restrict__ dout,
     const float* __restrict__ lse, const float* __restrict__ dlse, E* __restrict__ doff,
-    float* __restrict__ p_ws, float* __restrict__ b_ws, E* __restrict__ dk, E* __restrict__ dv) {
+    float* __restrict__ p_ws, float* __restrict__ b_ws, float* __restrict__ dk_acc,
+    float* __restrict__ dv_acc, int64_t acc_ks, int64_t acc_vs) {
   // S and dP tables, double-buffered (one barrier per plane).  A buffer is
   // [S rows | zeros | dP rows | zeros]: a slot that misses the step reads the
   // zero block instead of its corners, so its values are 0 with no select, and
@@ -283,15 +284,16 @@ __global__ __launch_bounds__(kThreads, (p1_min_waves<HD, E>())) void dsa3d_bwd_p
   for (int e = threadIdx.x; e < 2 * 2 * kP1Zero; e += kThreads)
     s_tb[e / (2 * kP1Zero)][((e / kP1Zero) & 1) * kP1Tab + kTQ * kSRow + e % kP1Zero] = 0.0f;
   {
-    // The second kernel accumulates dK and dV in place: zero this tile's rows
-    // of the head first (the tiles of a launch partition the (token, head)
-    // pairs, and the second kernel starts after this one ends), 16 bytes a thread.
-    constexpr int CPR = HD * static_cast<int>(sizeof(E)) / 16;
+    // The second kernel adds dK and dV into fp32 rows (the outputs for fp32
+    // storage, an accumulator for bf16): zero this tile's rows of the head first
+    // (the tiles of a launch partition the (token, head) pairs, and the second
+    // kernel starts after this one ends), 16 bytes a thread.
+    constexpr int CPR = HD / 4;
     for (int e = threadIdx.x; e < 2 * kTQ * CPR; e += kThreads) {
-      const int t = e / (kTQ * CPR), m = (e / CPR) % kTQ, ch = (e % CPR) * (16 / sizeof(E));
+      const int t = e / (kTQ * CPR), m = (e / CPR) % kTQ, ch = (e % CPR) * 4;
       const int64_t row = tile_row(a, tl, m);
       if (row < 0) continue;
-      E* dst = (t == 0 ? dk + row * a.ks : dv + row * a.vs) + tl.head * HD + ch;
+      float* dst = (t == 0 ? dk_acc + row * acc_ks : dv_acc + row * acc_vs) + tl.head * HD + ch;
       *reinterpret_cast<uint4*>(dst) = uint4{0u, 0u, 0u, 0u};
     }
   }
@@ -470,60 +472,32 @@ constexpr int p2_qrow() {
   return sizeof(E) == 2 ? kTQ * FR + 8 : kTQ * FR + 4;
 }
 
-// Lanes 2j and 2j + 1 of a 32x32 MFMA result hold channels c and c + 1 (c
-// even) of the same voxels; x0 and x1 are a lane's values at two voxels.  The
-// even lane assembles the (c, c + 1) pair of the first voxel and the odd lane
-// that of the second, swapping one value through DPP (quad_perm 1, 0, 3, 2).
-__device__ __forceinline__ void adjacent_pair(float x0, float x1, bool odd, float& lo, float& hi) {
-  const float keep = odd ? x1 : x0, send = odd ? x0 : x1;
-  const float recv =
-      __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(send), 0xB1, 0xF, 0xF, false));
-  lo = odd ? recv : keep;
-  hi = odd ? keep : recv;
-}
-
 // Adds a 32-voxel x 32-channel block of dK or dV (a 32x32 MFMA result; lane l
 // holds channel `ch` = window channel l % 32 and, in registers 4 g + i, voxel
-// 32 vb + 8 g + 4 (l / 32) + i) into `out` (token stride `stride`): fp32
-// atomic adds for fp32 storage, packed bf16-pair adds (rounded to nearest even)
-// for bf16.  s_rows gives each voxel's token row within the sample; the host
-// admits N * stride < 2^30 elements, so every offset is a 32-bit lane offset
-// from a wave-uniform base.  Untouched voxels (exact zeros) send nothing.
-template <typename E>
-__device__ __forceinline__ void flush_block(const Tile& tl, const f32x16_t& acc, const int* s_rows,
-                                            int vb, int nv, int ch, E* out, int64_t stride) {
-  char* const base = reinterpret_cast<char*>(out + tl.sample0 * stride);
+// 32 vb + 8 g + 4 (l / 32) + i) into fp32 rows of `acc` (token stride
+// `stride`) with global fp32 atomics (executed past the L2), so one register
+// across the wave covers 2 voxels x 32 contiguous channels.  s_rows gives each
+// voxel's token row within the sample; the host admits N * stride < 2^30, so
+// every offset is a 32-bit lane offset from a wave-uniform base.  Untouched
+// voxels (exact zeros) send nothing.  (Packed bf16 atomics into bf16 outputs
+// would halve the bytes, but rounding the running sum to bf16 at every add
+// loses the fp32 accuracy where many tiles add into one voxel, e.g. taps
+// border-clamped onto the volume's edge.)
+__device__ __forceinline__ void flush_block(const Tile& tl, const f32x16_t& x, const int* s_rows,
+                                            int vb, int nv, int ch, float* acc, int64_t stride) {
+  char* const base = reinterpret_cast<char*>(acc + tl.sample0 * stride);
   const uint32_t st = static_cast<uint32_t>(stride);
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
     const int v0 = 32 * vb + 8 * g + 4 * (tl.lane >> 5);
-    if constexpr (sizeof(E) == 4) {
-      int rr[4];
-      __builtin_memcpy(rr, &s_rows[v0], sizeof(rr));
+    int rr[4];
+    __builtin_memcpy(rr, &s_rows[v0], sizeof(rr));
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float x = acc[4 * g + i];
-        if (v0 + i < nv && x != 0.0f)
-          atomicAdd(reinterpret_cast<float*>(base + (static_cast<uint32_t>(rr[i]) * st + ch) * 4u), x);
-      }
-    } else {
-      const bool odd = tl.lane & 1;
-      const uint32_t che = static_cast<uint32_t>(ch & ~1);
-#pragma unroll
-      for (int m = 0; m < 2; ++m) {
-        float lo, hi;
-        adjacent_pair(acc[4 * g + 2 * m], acc[4 * g + 2 * m + 1], odd, lo, hi);
-        // the lane's own voxel: read per lane (a select between two entries of
-        // a register array becomes a scratch-memory index)
-        const int vi = v0 + 2 * m + (odd ? 1 : 0);
-        const uint32_t row = static_cast<uint32_t>(s_rows[vi]);
-        if (vi < nv && (lo != 0.0f || hi != 0.0f)) {
-          const f32x2_t f = {lo, hi};
-          __builtin_amdgcn_global_atomic_fadd_v2bf16(
-              reinterpret_cast<bf16x2_t*>(base + (row * st + che) * 2u),
-              __builtin_convertvector(f, bf16x2_t));
-        }
-      }
+    for (int i = 0; i < 4; ++i) {
+      const float val = x[4 * g + i];
+      if (v0 + i < nv && val != 0.0f)
+        atomicAdd(reinterpret_cast<float*>(base + (static_cast<uint32_t>(rr[i]) * st + ch) * 4u),
+                  val);
     }
   }
 }
@@ -531,8 +505,8 @@ __device__ __forceinline__ void flush_block(const Tile& tl, const f32x16_t& acc,
 template <int HD, int CW, typename E, int FR>
 __global__ __launch_bounds__(P2Tile<FR>::Threads) void dsa3d_bwd_p2_kernel(
     Args a, const E* __restrict__ dout, const float* __restrict__ p_ws,
-    const float* __restrict__ b_ws, E* __restrict__ dq, E* __restrict__ dk, E* __restrict__ dv,
-    int cw_base) {
+    const float* __restrict__ b_ws, E* __restrict__ dq, float* __restrict__ dk_acc,
+    float* __restrict__ dv_acc, int64_t acc_ks, int64_t acc_vs, int cw_base) {
   static_assert(CW <= HD && CW % 32 == 0, "channel windows are whole 32-channel blocks");
   using G = P2Tile<FR>;
   constexpr int kP2Frames = FR, kP2Q = G::Q, kP2Subs = G::Subs, kP2Slots = G::Slots;
@@ -723,9 +697,7 @@ __global__ __launch_bounds__(P2Tile<FR>::Threads) void dsa3d_bwd_p2_kernel(
       }
     }
     // dK[v] += sum_q B[q][v] q[q];  dV[v] += sum_q A[q][v] dO[q]  (32x32 MFMA),
-    // added into the dK and dV outputs with global atomics (executed past the
-    // L2).  One accumulator register across the wave covers 2 voxels x 32
-    // contiguous channels.
+    // added into fp32 rows with global atomics
     for (int t = tl.wave;; t += NW) {
       const int c2 = t % NC2, vb = t / NC2;
       if (vb * 32 >= c.nv) break;
@@ -736,13 +708,13 @@ __global__ __launch_bounds__(P2Tile<FR>::Threads) void dsa3d_bwd_p2_kernel(
       for (int f = 0; f < kP2Frames; ++f)
         acc = mma32(table_t_rows<E>(s_bt, kP2Row, kTQ * f, vb, tl.lane),
                     load_op<E>(&s_qt[0][och][kTQ * f + oq]), acc);
-      flush_block<E>(tl, acc, s_rows, vb, c.nv, cw0 + och, dk, a.ks);
+      flush_block(tl, acc, s_rows, vb, c.nv, cw0 + och, dk_acc, acc_ks);
       acc = f32x16_t{};
 #pragma unroll
       for (int f = 0; f < kP2Frames; ++f)
         acc = mma32(table_t_rows<E>(s_at, kP2Row, kTQ * f, vb, tl.lane),
                     load_op<E>(&s_qt[1][och][kTQ * f + oq]), acc);
-      flush_block<E>(tl, acc, s_rows, vb, c.nv, cw0 + och, dv, a.vs);
+      flush_block(tl, acc, s_rows, vb, c.nv, cw0 + och, dv_acc, acc_vs);
     }
     __syncthreads();
     w = wn;
@@ -926,8 +898,8 @@ constexpr int p2_window() {
 template <int HD, typename E>
 void launch_bwd_pair(const msd_dsa3d_desc& d, const void* q, const void* k, const void* v,
                      const void* off, const E* o, const E* go, const float* lse,
-                     const float* dlse, E* gq, E* gk, E* gv, E* goff, float* p_ws, float* b_ws,
-                     hipStream_t s) {
+                     const float* dlse, E* gq, E* goff, float* p_ws, float* b_ws, float* dk_acc,
+                     float* dv_acc, int64_t acc_ks, int64_t acc_vs, hipStream_t s) {
   constexpr int CW = p2_window<HD, E>(), FR = p2_frames<HD, E>();
   const tiled::Args a1 = make_tiled_args(d, q, k, v, off, tiled_tiles<1>(d));
   const tiled::Args a2 = make_tiled_args(d, q, k, v, off, tiled_tiles<FR>(d));
@@ -935,13 +907,39 @@ void launch_bwd_pair(const msd_dsa3d_desc& d, const void* q, const void* k, cons
   dim3 g2 = tiled_grid<FR>(d);
   g2.z = HD / CW;
   hipLaunchKernelGGL((dsa3d_bwd_p1_kernel<HD, E>), g1, dim3(tiled::kThreads), 0, s, a1, o, go,
-                     lse, dlse, goff, p_ws, b_ws, gk, gv);
+                     lse, dlse, goff, p_ws, b_ws, dk_acc, dv_acc, acc_ks, acc_vs);
   hipLaunchKernelGGL((dsa3d_bwd_p2_kernel<HD, CW, E, FR>), g2, dim3(P2Tile<FR>::Threads), 0, s,
-                     a2, go, p_ws, b_ws, gq, gk, gv, 0);
+                     a2, go, p_ws, b_ws, gq, dk_acc, dv_acc, acc_ks, acc_vs, 0);
   if constexpr (HD % CW != 0) {  // bf16 head_dim 96: a 64- and a 32-channel window
     g2.z = 1;
     hipLaunchKernelGGL((dsa3d_bwd_p2_kernel<HD, HD % CW, E, FR>), g2, dim3(P2Tile<FR>::Threads), 0,
-                       s, a2, go, p_ws, b_ws, gq, gk, gv, CW * (HD / CW));
+                       s, a2, go, p_ws, b_ws, gq, dk_acc, dv_acc, acc_ks, acc_vs,
+                       CW * (HD / CW));
+  }
+}
+
+// fp32 dK (blockIdx.y 0) or dV (1) accumulator [rows, D] -> bf16 with the
+// output's token stride, 8 channels per thread (32-byte loads, 16-byte stores;
+// D and the strides are multiples of 8), grid-stride over 64-bit indices.
+__global__ __launch_bounds__(256) void acc_to_bf16_kernel(const float* __restrict__ dk_acc,
+                                                         const float* __restrict__ dv_acc,
+                                                         bf16* __restrict__ dk,
+                                                         bf16* __restrict__ dv, int64_t rows,
+                                                         int D, int64_t ks, int64_t vs) {
+  const int64_t d8 = D / 8, n = rows * d8;
+  const bool is_k = blockIdx.y == 0;
+  const float* const src0 = is_k ? dk_acc : dv_acc;
+  bf16* const dst0 = is_k ? dk : dv;
+  const int64_t st = is_k ? ks : vs;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t r = i / d8, c = 8 * (i - r * d8);
+    f32x4_t x[2];
+    __builtin_memcpy(x, src0 + r * D + c, sizeof(x));
+    uint16_t h[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) h[j] = from_f32<bf16>(x[j / 4][j % 4]).bits;
+    __builtin_memcpy(dst0 + r * st + c, h, sizeof(h));
   }
 }
 
@@ -949,41 +947,59 @@ template <typename E>
 hipError_t bwd_tiled_typed(const msd_dsa3d_desc& d, const void* q, const void* k, const void* v,
                            const void* off, const void* out, const void* dout, const float* lse,
                            const float* dlse, void* dq, void* dk, void* dv, void* doff,
-                           float* p_ws, float* b_ws, hipStream_t s) {
+                           float* p_ws, float* b_ws, float* acc, hipStream_t s) {
+  const int64_t rows = static_cast<int64_t>(d.B) * d.T * d.H * d.W;
+  const int D = d.num_heads * d.head_dim;
   const auto* o = static_cast<const E*>(out);
   const auto* go = static_cast<const E*>(dout);
   auto* gq = static_cast<E*>(dq);
-  auto* gk = static_cast<E*>(dk);
-  auto* gv = static_cast<E*>(dv);
   auto* goff = static_cast<E*>(doff);
+  // dK and dV add up in fp32: in the outputs themselves for fp32 storage, in
+  // the workspace accumulator (converted once at the end) for bf16
+  constexpr bool kInPlace = sizeof(E) == 4;
+  float* const dk_acc = kInPlace ? static_cast<float*>(dk) : acc;
+  float* const dv_acc = kInPlace ? static_cast<float*>(dv) : acc + rows * D;
+  const int64_t aks = kInPlace ? d.k_stride : D, avs = kInPlace ? d.v_stride : D;
   switch (d.head_dim) {
     case 32:
-      launch_bwd_pair<32, E>(d, q, k, v, off, o, go, lse, dlse, gq, gk, gv, goff, p_ws, b_ws, s);
+      launch_bwd_pair<32, E>(d, q, k, v, off, o, go, lse, dlse, gq, goff, p_ws, b_ws, dk_acc,
+                               dv_acc, aks, avs, s);
       break;
     case 64:
-      launch_bwd_pair<64, E>(d, q, k, v, off, o, go, lse, dlse, gq, gk, gv, goff, p_ws, b_ws, s);
+      launch_bwd_pair<64, E>(d, q, k, v, off, o, go, lse, dlse, gq, goff, p_ws, b_ws, dk_acc,
+                               dv_acc, aks, avs, s);
       break;
     case 96:
-      launch_bwd_pair<96, E>(d, q, k, v, off, o, go, lse, dlse, gq, gk, gv, goff, p_ws, b_ws, s);
+      launch_bwd_pair<96, E>(d, q, k, v, off, o, go, lse, dlse, gq, goff, p_ws, b_ws, dk_acc,
+                               dv_acc, aks, avs, s);
       break;
     case 128:
-      launch_bwd_pair<128, E>(d, q, k, v, off, o, go, lse, dlse, gq, gk, gv, goff, p_ws, b_ws, s);
+      launch_bwd_pair<128, E>(d, q, k, v, off, o, go, lse, dlse, gq, goff, p_ws, b_ws, dk_acc,
+                                dv_acc, aks, avs, s);
       break;
     default:
       return hipErrorInvalidValue;
+  }
+  if constexpr (!kInPlace) {
+    const dim3 cgrid(fill_blocks(rows * (D / 8)), 2);
+    hipLaunchKernelGGL(acc_to_bf16_kernel, cgrid, dim3(256), 0, s, dk_acc, dv_acc,
+                       static_cast<bf16*>(dk), static_cast<bf16*>(dv), rows, D, d.k_stride,
+                       d.v_stride);
   }
   return hipGetLastError();
 }
 }  // namespace
 
-// Workspace of the tiled backward: p and ds * softmax_scale of every tap
-// (fp32 [token][head][tap] each).  dK and dV accumulate in the outputs.
+// Workspace of the tiled backward: for bf16 the dK/dV fp32 accumulators
+// ([token][D] each; fp32 storage accumulates in its outputs), then p and
+// ds * softmax_scale of every tap (fp32 [token][head][tap] each).
 size_t dsa3d_tiled_bwd_ws_bytes(const msd_dsa3d_desc& d) {
   if ((d.dtype != MSD_BF16 && d.dtype != MSD_F32) || !tiled_head_dim(d.head_dim) ||
       d.kt * d.kh * d.kw > tiled::kMaxTaps)
     return 0;
   const int64_t rows = static_cast<int64_t>(d.B) * d.T * d.H * d.W;
-  return static_cast<size_t>(2 * rows * d.num_heads * d.kt * d.kh * d.kw) * sizeof(float);
+  const int64_t acc = d.dtype == MSD_BF16 ? 2 * rows * d.num_heads * d.head_dim : 0;
+  return static_cast<size_t>(acc + 2 * rows * d.num_heads * d.kt * d.kh * d.kw) * sizeof(float);
 }
 
 hipError_t launch_dsa3d_bwd_tiled(const msd_dsa3d_desc& d, const void* q, const void* k,
@@ -992,13 +1008,15 @@ hipError_t launch_dsa3d_bwd_tiled(const msd_dsa3d_desc& d, const void* q, const 
                                   void* dk, void* dv, void* doff, void* ws, hipStream_t s) {
   const int64_t rows = static_cast<int64_t>(d.B) * d.T * d.H * d.W;
   const int64_t taps = rows * d.num_heads * d.kt * d.kh * d.kw;
-  float* p_ws = static_cast<float*>(ws);
+  // accumulators first: rows * D floats keep p and ds 16-byte aligned
+  float* acc = static_cast<float*>(ws);
+  float* p_ws = acc + (d.dtype == MSD_BF16 ? 2 * rows * d.num_heads * d.head_dim : 0);
   float* b_ws = p_ws + taps;
   if (d.dtype == MSD_BF16)
     return bwd_tiled_typed<bf16>(d, q, k, v, off, out, dout, lse, dlse, dq, dk, dv, doff, p_ws,
-                                 b_ws, s);
+                                 b_ws, acc, s);
   return bwd_tiled_typed<float>(d, q, k, v, off, out, dout, lse, dlse, dq, dk, dv, doff, p_ws,
-                                b_ws, s);
+                                b_ws, acc, s);
 }
 
 }  // namespace msd

@@ -89,13 +89,15 @@ def test_workspace_size_and_check():
     # head_dim 16: direct kernels only, dK/dV fp32 accumulators
     d16 = _desc(B=2, head_dim=16, q_stride=32, k_stride=32, v_stride=32)
     assert lib.msd_dsa3d_bwd_workspace_size(ctypes.byref(d16)) == 2 * rows * 32 * 4
-    # head_dim 64, fp32 and bf16: the tiled backward keeps p and ds of every tap
-    # (fp32) and accumulates dK/dV in the outputs; that is more than the direct
-    # kernels' accumulators, so the larger of the two is asked for
-    for dtype in (0, 1):
+    # head_dim 64: the tiled backward keeps p and ds of every tap (fp32); fp32
+    # storage adds dK/dV up in its outputs (the direct kernels' accumulators
+    # are less than p and ds, and the larger of the two is asked for), bf16 in
+    # fp32 accumulators beside p and ds
+    taps = 2 * rows * 2 * 147 * 4
+    for dtype, want in ((0, max(2 * rows * 128 * 4, taps)), (1, 2 * rows * 128 * 4 + taps)):
         d = _desc(B=2, dtype=dtype)
         need = lib.msd_dsa3d_bwd_workspace_size(ctypes.byref(d))
-        assert need == max(2 * rows * 128 * 4, 2 * rows * 2 * 147 * 4)
+        assert need == want
     rc = lib.msd_dsa3d_bwd(ctypes.byref(d), *([16] * 12), None, need - 1, None)
     assert rc == -4 and b"workspace" in lib.msd_last_error()
     assert lib.msd_dsa3d_bwd_workspace_size(None) == 0
@@ -122,3 +124,4 @@ def test_module_rejects_cpu_tensors():
         m(torch.randn(1, 8, 16), (2, 2, 2))
     with pytest.raises(AssertionError):
         m(torch.randn(1, 9, 16), (2, 2, 2))
+
