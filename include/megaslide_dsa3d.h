@@ -22,8 +22,10 @@
  *     ((((head*kt + i)*kh + j)*kw + k)*3 + slot): the reference's
  *     offsets.view(B, nh, kt, kh, kw, 3, T, H, W) order (attention.py:109),
  *     unscaled (the kernels multiply by offset_scale, attention.py:106).
- *   - Every pointer is device memory owned by the caller.  The library never
- *     allocates or frees device memory and keeps no pointer after return.
+ *   - Every pointer is device memory owned by the caller.  No call allocates
+ *     or frees device memory, and none keeps a pointer after return (the one
+ *     static scratch array of msd_dsa3d_bwd_noalloc comes with the library's
+ *     code object).
  *   - `stream` is a hipStream_t (NULL = the null stream).  Work is enqueued;
  *     nothing synchronises the device.
  *   - Return value 0 = success, negative = msd_status; msd_last_error() gives a
@@ -129,6 +131,28 @@ int msd_dsa3d_bwd(const msd_dsa3d_desc* desc, const void* q, const void* k, cons
                   const void* offsets, const void* out, const void* dout, const float* lse,
                   const float* dlse, void* dq, void* dk, void* dv, void* doffsets,
                   void* workspace, size_t workspace_bytes, void* stream);
+
+/* Largest scratch, in bytes, msd_dsa3d_bwd_noalloc can give a call: what
+ * msd_dsa3d_bwd_workspace_size reports for the same descriptor must not exceed
+ * it (128 MiB: e.g. B*T*H*W*num_heads*kt*kh*kw up to 16,777,216 taps). */
+#define MSD_NOALLOC_SCRATCH_BYTES ((size_t)128 << 20)
+
+/*
+ * msd_dsa3d_bwd without a workspace argument, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight training or serving
+ * loops, harnesses that forbid hipMalloc).  It has no counterpart in the
+ * reference.  Same arguments, results and errors as msd_dsa3d_bwd; its
+ * scratch is one static array of MSD_NOALLOC_SCRATCH_BYTES on each GPU that
+ * loads this library, held until the process ends, and no call of it
+ * allocates or frees memory.  A call whose msd_dsa3d_bwd_workspace_size
+ * exceeds MSD_NOALLOC_SCRATCH_BYTES returns MSD_ERR_WORKSPACE.  Every call on
+ * one GPU uses that GPU's array and leaves the last call's contents in it:
+ * calls that overlap on one GPU (other streams, other host threads) race.
+ */
+int msd_dsa3d_bwd_noalloc(const msd_dsa3d_desc* desc, const void* q, const void* k,
+                          const void* v, const void* offsets, const void* out, const void* dout,
+                          const float* lse, const float* dlse, void* dq, void* dk, void* dv,
+                          void* doffsets, void* stream);
 
 /*
  * Depthwise 3-D convolution, channel-last: replaces nn.Conv3d(C, C, k,

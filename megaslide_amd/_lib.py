@@ -21,6 +21,9 @@ ABI_VERSION = 2
 MSD_F32 = 0
 MSD_BF16 = 1
 
+# largest scratch msd_dsa3d_bwd_noalloc gives a call (MSD_NOALLOC_SCRATCH_BYTES)
+NOALLOC_SCRATCH_BYTES = 128 << 20
+
 # Every symbol the header declares (checked by the CPU test suite).
 EXPORTS = (
     "msd_abi_version",
@@ -28,6 +31,7 @@ EXPORTS = (
     "msd_dsa3d_fwd",
     "msd_dsa3d_bwd_workspace_size",
     "msd_dsa3d_bwd",
+    "msd_dsa3d_bwd_noalloc",
     "msd_dwconv3d_fwd",
     "msd_dwconv3d_bwd_workspace_size",
     "msd_dwconv3d_bwd",
@@ -92,6 +96,8 @@ def load() -> ctypes.CDLL:
         lib.msd_dsa3d_bwd_workspace_size.argtypes = [ctypes.POINTER(DsaDesc)]
         lib.msd_dsa3d_bwd.restype = ctypes.c_int
         lib.msd_dsa3d_bwd.argtypes = [ctypes.POINTER(DsaDesc)] + [_vp] * 13 + [ctypes.c_size_t, _vp]
+        lib.msd_dsa3d_bwd_noalloc.restype = ctypes.c_int
+        lib.msd_dsa3d_bwd_noalloc.argtypes = [ctypes.POINTER(DsaDesc)] + [_vp] * 13
         lib.msd_dwconv3d_fwd.restype = ctypes.c_int
         lib.msd_dwconv3d_fwd.argtypes = [ctypes.POINTER(ConvDesc), _vp, _vp, _vp, _vp, _vp]
         lib.msd_dwconv3d_bwd_workspace_size.restype = ctypes.c_size_t

@@ -3,6 +3,8 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <mutex>
+
 #include "common.h"
 
 namespace {
@@ -84,6 +86,84 @@ int check_conv(const msd_dwconv3d_desc* d) {
   return MSD_OK;
 }
 
+// Scratch of msd_dsa3d_bwd_noalloc: one array on every GPU that loads the
+// library, held until the process ends.  Host code never passes the array's
+// name (a host-side stand-in) to a kernel: it uses the per-device address that
+// hipGetSymbolAddress returns.  Calls that overlap on one GPU share it and race.
+constexpr size_t kNoAllocScratchBytes = MSD_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device, looked up once per device
+// with that device current.
+int scratch_address(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess)
+    return fail(MSD_ERR_LAUNCH, "dsa3d_bwd_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(MSD_ERR_UNSUPPORTED, "dsa3d_bwd_noalloc: device %d beyond the %d supported", dev,
+                kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return fail(MSD_ERR_LAUNCH, "dsa3d_bwd_noalloc: hipGetSymbolAddress(scratch): %s",
+                  hipGetErrorString(e));
+    g_scratch[dev] = p;
+  }
+  *out = g_scratch[dev];
+  return MSD_OK;
+}
+
+int dsa3d_bwd_impl(const msd_dsa3d_desc* desc, const void* q, const void* k, const void* v,
+                   const void* offsets, const void* out, const void* dout, const float* lse,
+                   const float* dlse, void* dq, void* dk, void* dv, void* doffsets,
+                   void* workspace, size_t workspace_bytes, void* stream, bool noalloc) {
+  int rc = check_dsa(desc);
+  if (rc != MSD_OK) return rc;
+  rc = check_ptrs("dsa3d_bwd", elem_bytes(desc->dtype),
+                  {q, k, v, offsets, out, dout, dq, dk, dv, doffsets});
+  if (rc != MSD_OK) return rc;
+  rc = check_ptrs("dsa3d_bwd(lse)", 4, {lse});
+  if (rc != MSD_OK) return rc;
+  if (dlse != nullptr && !aligned(dlse, 4)) return fail(MSD_ERR_ALIGN, "dsa3d_bwd: dlse misaligned");
+  if (desc->B == 0) return MSD_OK;
+  const size_t need = msd::dsa3d_bwd_ws_bytes(*desc);
+  if (noalloc) {
+    if (need > kNoAllocScratchBytes)
+      return fail(MSD_ERR_WORKSPACE,
+                  "dsa3d_bwd_noalloc: the call needs %zu bytes of scratch, above the %zu-byte "
+                  "maximum of the no-allocation entry point (use msd_dsa3d_bwd with a workspace)",
+                  need, kNoAllocScratchBytes);
+    rc = scratch_address(&workspace);
+    if (rc != MSD_OK) return rc;
+    workspace_bytes = kNoAllocScratchBytes;
+  }
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need || !aligned(workspace, 16)))
+    return fail(MSD_ERR_WORKSPACE, "dsa3d_bwd: workspace of %zu bytes (16-aligned) needed, got %zu",
+                need, workspace == nullptr ? size_t(0) : workspace_bytes);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  // the tiled backward also writes dq with 16-byte rows and reads out/dout rows of D
+  const bool tiled_ok = msd::dsa3d_tiled_supported(*desc, q, k, v) &&
+                        msd::dsa3d_tiled_supported(*desc, dq, dk, dv);
+  if (desc->algo == MSD_ALGO_TILED && !tiled_ok)
+    return fail(MSD_ERR_UNSUPPORTED,
+                "dsa3d_bwd: tiled kernels need bf16 or fp32, head_dim 32, 64, 96 or 128, <= 160 taps and "
+                "16-byte aligned rows");
+  if (tiled_ok && desc->algo != MSD_ALGO_DIRECT)
+    return launch_status(msd::launch_dsa3d_bwd_tiled(*desc, q, k, v, offsets, out, dout, lse, dlse,
+                                                     dq, dk, dv, doffsets, workspace, s),
+                         "dsa3d_bwd");
+  return launch_status(msd::launch_dsa3d_bwd_direct(*desc, q, k, v, offsets, out, dout, lse, dlse,
+                                                    dq, dk, dv, doffsets, workspace, s),
+                       "dsa3d_bwd");
+}
+
 }  // namespace
 
 extern "C" {
@@ -122,34 +202,16 @@ int msd_dsa3d_bwd(const msd_dsa3d_desc* desc, const void* q, const void* k, cons
                   const void* offsets, const void* out, const void* dout, const float* lse,
                   const float* dlse, void* dq, void* dk, void* dv, void* doffsets,
                   void* workspace, size_t workspace_bytes, void* stream) {
-  int rc = check_dsa(desc);
-  if (rc != MSD_OK) return rc;
-  rc = check_ptrs("dsa3d_bwd", elem_bytes(desc->dtype),
-                  {q, k, v, offsets, out, dout, dq, dk, dv, doffsets});
-  if (rc != MSD_OK) return rc;
-  rc = check_ptrs("dsa3d_bwd(lse)", 4, {lse});
-  if (rc != MSD_OK) return rc;
-  if (dlse != nullptr && !aligned(dlse, 4)) return fail(MSD_ERR_ALIGN, "dsa3d_bwd: dlse misaligned");
-  if (desc->B == 0) return MSD_OK;
-  const size_t need = msd::dsa3d_bwd_ws_bytes(*desc);
-  if (need > 0 && (workspace == nullptr || workspace_bytes < need || !aligned(workspace, 16)))
-    return fail(MSD_ERR_WORKSPACE, "dsa3d_bwd: workspace of %zu bytes (16-aligned) needed, got %zu",
-                need, workspace == nullptr ? size_t(0) : workspace_bytes);
-  const hipStream_t s = static_cast<hipStream_t>(stream);
-  // the tiled backward also writes dq with 16-byte rows and reads out/dout rows of D
-  const bool tiled_ok = msd::dsa3d_tiled_supported(*desc, q, k, v) &&
-                        msd::dsa3d_tiled_supported(*desc, dq, dk, dv);
-  if (desc->algo == MSD_ALGO_TILED && !tiled_ok)
-    return fail(MSD_ERR_UNSUPPORTED,
-                "dsa3d_bwd: tiled kernels need bf16 or fp32, head_dim 32, 64, 96 or 128, <= 160 taps and "
-                "16-byte aligned rows");
-  if (tiled_ok && desc->algo != MSD_ALGO_DIRECT)
-    return launch_status(msd::launch_dsa3d_bwd_tiled(*desc, q, k, v, offsets, out, dout, lse, dlse,
-                                                     dq, dk, dv, doffsets, workspace, s),
-                         "dsa3d_bwd");
-  return launch_status(msd::launch_dsa3d_bwd_direct(*desc, q, k, v, offsets, out, dout, lse, dlse,
-                                                    dq, dk, dv, doffsets, workspace, s),
-                       "dsa3d_bwd");
+  return dsa3d_bwd_impl(desc, q, k, v, offsets, out, dout, lse, dlse, dq, dk, dv, doffsets,
+                        workspace, workspace_bytes, stream, false);
+}
+
+int msd_dsa3d_bwd_noalloc(const msd_dsa3d_desc* desc, const void* q, const void* k,
+                          const void* v, const void* offsets, const void* out, const void* dout,
+                          const float* lse, const float* dlse, void* dq, void* dk, void* dv,
+                          void* doffsets, void* stream) {
+  return dsa3d_bwd_impl(desc, q, k, v, offsets, out, dout, lse, dlse, dq, dk, dv, doffsets,
+                        nullptr, 0, stream, true);
 }
 
 int msd_dwconv3d_fwd(const msd_dwconv3d_desc* desc, const void* x, const void* weight,

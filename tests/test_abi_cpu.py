@@ -125,3 +125,17 @@ def test_module_rejects_cpu_tensors():
     with pytest.raises(AssertionError):
         m(torch.randn(1, 9, 16), (2, 2, 2))
 
+
+def test_noalloc_scratch_limit_and_rejection():
+    """The no-allocation backward's scratch maximum is the header's constant,
+    and a call needing more is rejected by the size check, before any device
+    call (the pointers here are never dereferenced)."""
+    text = open(HEADER).read()
+    m = re.search(r"#define MSD_NOALLOC_SCRATCH_BYTES \(\(size_t\)(\d+) << (\d+)\)", text)
+    assert m and int(m.group(1)) << int(m.group(2)) == _lib.NOALLOC_SCRATCH_BYTES
+    lib = _lib.load()
+    big = _desc(B=1, T=64, H=32, W=32, num_heads=16, dtype=1, q_stride=1024, k_stride=1024,
+                v_stride=1024)
+    assert lib.msd_dsa3d_bwd_workspace_size(ctypes.byref(big)) > _lib.NOALLOC_SCRATCH_BYTES
+    rc = lib.msd_dsa3d_bwd_noalloc(ctypes.byref(big), *([16] * 7), None, *([16] * 4), None)
+    assert rc == -4 and b"maximum" in lib.msd_last_error()
