@@ -4,6 +4,8 @@
                     [--workload long-clip-65k|tiny-2k|fp32-32k|large-block-131k|dit-block-46k]
     python bench.py --summarize WORKLOAD TRACE_DIR FETCH_DIR WRITE_DIR
                     (rocprofv3 csv output -> markdown tables + profiles/traffic.json)
+    python bench.py --counter-table PMC_DIR [PMC_DIR ...]
+                    (rocprofv3 --pmc csv output -> per-kernel instruction/LDS table)
 
 Workloads (one step = one pass of the hot path over one batch of synthetic
 input, every buffer preallocated and resident in HBM):
@@ -342,10 +344,12 @@ def cpu_baseline(cfg, runs=3):
         cpu_model=_cpu_model(), torch_version=torch.__version__, seconds=med)
 
 
-PHASE_KERNELS = {  # bench phase -> the kernels its ABI call launches, in order
-    "dsa3d_fwd": ["dsa3d_fwd_tiled_kernel"],
-    "dsa3d_bwd": ["dsa3d_bwd_p1_kernel", "dsa3d_bwd_p2_kernel"],
-}
+def phase_kernels(dtype):
+    """Bench phase -> the kernels its ABI call launches, in order (bf16 adds the
+    fp32 -> bf16 conversion of the dK/dV accumulators)."""
+    bwd = ["dsa3d_bwd_p1_kernel", "dsa3d_bwd_p2_kernel"]
+    return {"dsa3d_fwd": ["dsa3d_fwd_tiled_kernel"],
+            "dsa3d_bwd": bwd + (["acc_to_bf16_kernel"] if dtype == "bf16" else [])}
 
 
 def summarize(workload, trace_dir, fetch_dir, write_dir):
@@ -409,7 +413,7 @@ def summarize(workload, trace_dir, fetch_dir, write_dir):
     rec = {}
     print("| phase (kernels) | FETCH KiB | WRITE KiB | traffic (scaled) | algorithmic | traffic / algorithmic |")
     print("|---|---|---|---|---|---|")
-    for phase, names in PHASE_KERNELS.items():
+    for phase, names in phase_kernels(cfg["dtype"]).items():
         f_kib, w_kib = phase_sum(fetch, names), phase_sum(write, names)
         if f_kib is None or w_kib is None:
             continue
@@ -435,9 +439,71 @@ def summarize(workload, trace_dir, fetch_dir, write_dir):
         json.dump(allrec, f, indent=1)
 
 
+COUNTER_KERNELS = ("dsa3d_fwd_tiled_kernel", "dsa3d_bwd_p1_kernel", "dsa3d_bwd_p2_kernel",
+                   "dwconv_")
+
+
+def counter_table(*dirs):
+    """Per-kernel table from rocprofv3 --pmc runs of this script (one bench
+    step each, counters split over passes): instructions per wave, LDS
+    bank-conflict cycles per LDS instruction, wave-cycles per busy cycle.
+    Counters are summed over every dispatch of a kernel name in a pass, then
+    divided by the pass's SQ_WAVES for the same kernel name."""
+    import csv
+    import glob
+
+    per = {}  # kernel -> counter -> (value summed over dispatches, dispatches)
+    for d in dirs:
+        for path in glob.glob(os.path.join(d, "*counter_collection.csv")):
+            with open(path) as f:
+                for r in csv.DictReader(f):
+                    name = r["Kernel_Name"]
+                    if "msd::" not in name:
+                        continue
+                    short = name.replace("(anonymous namespace)::", "").replace("msd::", "")
+                    short = short.split("(")[0].replace("void ", "")
+                    c = per.setdefault(short, {}).setdefault(d, {})
+                    key = r["Counter_Name"]
+                    c.setdefault(key, {})
+                    c[key][r["Dispatch_Id"]] = c[key].get(r["Dispatch_Id"], 0.0) + \
+                        float(r["Counter_Value"])
+    cols = ["SQ_INSTS_VALU", "SQ_INSTS_SALU", "SQ_INSTS_LDS", "SQ_INSTS_MFMA",
+            "SQ_INSTS_VMEM_RD", "SQ_INSTS_VMEM_WR"]
+    print("| kernel | waves | VALU/wave | SALU/wave | LDS/wave | MFMA/wave | VMEM rd/wave | "
+          "VMEM wr/wave | LDS bank-conflict cycles / LDS instr | wave-cycles / busy cycle | "
+          "wait-any / wave-cycles |")
+    print("|---|---|---|---|---|---|---|---|---|---|---|")
+    for k in sorted(per):
+        vals, waves = {}, None
+        for d, cs in per[k].items():
+            w = sum(cs.get("SQ_WAVES", {}).values()) or None
+            for name, disp in cs.items():
+                if name == "SQ_WAVES":
+                    waves = w
+                    continue
+                tot = sum(disp.values())
+                vals[name] = tot / w if w and name.startswith("SQ_INSTS") else tot
+        if not waves:
+            continue
+
+        def f(x, p=0):
+            return "—" if x is None else f"{x:.{p}f}"
+        conf = vals.get("SQ_LDS_BANK_CONFLICT")
+        lds = vals.get("SQ_INSTS_LDS")
+        ratio = conf / (lds * waves) if conf is not None and lds else None
+        wc, busy = vals.get("SQ_WAVE_CYCLES"), vals.get("SQ_BUSY_CYCLES")
+        wait = vals.get("SQ_WAIT_ANY")
+        print(f"| `{k[:60]}` | {waves:.0f} | " + " | ".join(f(vals.get(c)) for c in cols) +
+              f" | {f(ratio, 2)} | {f(wc / busy if wc and busy else None, 1)} | "
+              f"{f(wait / wc if wait and wc else None, 2)} |")
+
+
 def main():
     if len(sys.argv) == 6 and sys.argv[1] == "--summarize":
         summarize(*sys.argv[2:])
+        return
+    if len(sys.argv) >= 3 and sys.argv[1] == "--counter-table":
+        counter_table(*sys.argv[2:])
         return
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
