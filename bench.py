@@ -13,6 +13,8 @@ input, every buffer preallocated and resident in HBM):
   long-clip-65k    (default) B=1, T=64, H=W=32 (65,536 tokens), dim 1024,
                    16 heads x 64, bf16 storage with fp32 accumulation, raw
                    offsets ~ N(0, 0.5)
+  long-clip-65k-g128  the same with 128 extra keys shared by every query
+                   (the reference's extra_kv from HybridAttention3D's registers)
   tiny-2k          B=1, T=8, H=W=16 (2,048 tokens), dim 256, 4 x 64, fp32,
                    forward only, offsets from the offset net (depthwise 3x3x3
                    conv and 1x1 conv weights ~ N(0, 0.02))
@@ -79,6 +81,13 @@ WORKLOADS = {
         B=1, T=64, H=32, W=32, D=1024, nh=16, kernel=(3, 7, 7), dtype="bf16",
         offsets=("normal", 0.5), backward=True, metric=METRIC,
         workload="3D-DSA fwd+bwd HIP kernel set, long-clip 65,536 tokens",
+        cpu_slab=dict(T=4)),
+    "long-clip-65k-g128": dict(
+        B=1, T=64, H=32, W=32, D=1024, nh=16, kernel=(3, 7, 7), dtype="bf16",
+        offsets=("normal", 0.5), backward=True, extra_g=128,
+        metric="3D-DSA fwd+bwd tokens/sec at 65k tokens bf16, 128 extra keys",
+        workload="3D-DSA fwd+bwd HIP kernel set, long-clip 65,536 tokens + 128 shared extra keys "
+                 "(hybrid registers)",
         cpu_slab=dict(T=4)),
     "tiny-2k": dict(
         B=1, T=8, H=16, W=16, D=256, nh=4, kernel=(3, 7, 7), dtype="fp32",
@@ -217,7 +226,13 @@ def run_gpu(cfg, steps, warmup, calibrate=False):
     dx3, dx7 = torch.empty_like(x), torch.empty_like(x)
     dw3, db3, dw7, db7 = (torch.empty_like(t) for t in (w3, b3, w7, b7))
 
-    dsa = _lib.DsaDesc(B, T, H, W, nh, hd, kt, kh, kw, mdt, D, D, D, 1.0, 1.0 / math.sqrt(hd))
+    G = cfg.get("extra_g", 0)
+    ek = rnd(B, G, D) if G else None
+    ev = rnd(B, G, D) if G else None
+    dek = torch.empty_like(ek) if G else None
+    dev_ = torch.empty_like(ev) if G else None
+    dsa = _lib.DsaDesc(B, T, H, W, nh, hd, kt, kh, kw, mdt, D, D, D, 1.0, 1.0 / math.sqrt(hd),
+                       0, 0, 0, 0.0, G)
     cv7 = _lib.ConvDesc(B, T, H, W, D, kt, kh, kw, mdt, 0)
     cv3 = _lib.ConvDesc(B, T, H, W, D, 3, 3, 3, mdt, 1)
 
@@ -230,17 +245,19 @@ def run_gpu(cfg, steps, warmup, calibrate=False):
     stream = torch.cuda.current_stream(dev)
     sh = stream.cuda_stream
     P = lambda t: t.data_ptr()  # noqa: E731
+    PX = lambda t: None if t is None else t.data_ptr()  # noqa: E731
 
     phases = [
         ("dwconv7_fwd", lambda: lib.msd_dwconv3d_fwd(ctypes.byref(cv7), P(x), P(w7), P(b7), P(y7), sh)),
         ("dwconv3_gelu_fwd", lambda: lib.msd_dwconv3d_fwd(ctypes.byref(cv3), P(x), P(w3), P(b3), P(F), sh)),
-        ("dsa3d_fwd", lambda: lib.msd_dsa3d_fwd(ctypes.byref(dsa), P(q), P(k), P(v), P(off), P(out),
-                                                P(lse), sh)),
+        ("dsa3d_fwd", lambda: lib.msd_dsa3d_fwd(ctypes.byref(dsa), P(q), P(k), P(v), P(off),
+                                                PX(ek), PX(ev), P(out), P(lse), sh)),
     ]
     if cfg["backward"]:
         phases += [
-            ("dsa3d_bwd", lambda: lib.msd_dsa3d_bwd(ctypes.byref(dsa), P(q), P(k), P(v), P(off), P(out),
-                                                    P(dout), P(lse), None, P(dq), P(dk), P(dv), P(doff),
+            ("dsa3d_bwd", lambda: lib.msd_dsa3d_bwd(ctypes.byref(dsa), P(q), P(k), P(v), P(off),
+                                                    PX(ek), PX(ev), P(out), P(dout), P(lse), None,
+                                                    P(dq), P(dk), P(dv), P(doff), PX(dek), PX(dev_),
                                                     P(ws_dsa), ws_dsa.numel(), sh)),
             ("dwconv3_gelu_bwd", lambda: lib.msd_dwconv3d_bwd(ctypes.byref(cv3), P(x), P(w3), P(b3), P(dF),
                                                               P(dx3), P(dw3), P(db3), P(ws3), ws3.numel(), sh)),
@@ -263,20 +280,20 @@ def run_gpu(cfg, steps, warmup, calibrate=False):
     torch.cuda.synchronize()
 
     # timed region: K steps, bracketed by device synchronisation
-    ev = [[[torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)]
-           for _ in phases] for _ in range(steps)]
+    evs = [[[torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)]
+            for _ in phases] for _ in range(steps)]
     t_start = torch.cuda.Event(enable_timing=True)
     t_end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     wall0 = time.perf_counter()
     t_start.record(stream)
     for s in range(steps):
-        step(ev[s])
+        step(evs[s])
     t_end.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - wall0
     total_ms = t_start.elapsed_time(t_end)
-    per_phase = {name: sum(ev[s][i][0].elapsed_time(ev[s][i][1]) for s in range(steps)) / steps
+    per_phase = {name: sum(evs[s][i][0].elapsed_time(evs[s][i][1]) for s in range(steps)) / steps
                  for i, (name, _) in enumerate(phases)}
     return dict(total_ms=total_ms, wall_s=wall, per_phase_ms=per_phase, tokens=B * N)
 
@@ -317,12 +334,16 @@ def cpu_baseline(cfg, runs=3):
     w3 = (torch.randn(D, 1, 3, 3, 3) * 0.1).requires_grad_(grad)
     b = torch.zeros(D, requires_grad=grad)
     gy = torch.randn(B, N, D)
+    G = cfg.get("extra_g", 0)
+    ek = torch.randn(B, G, D, requires_grad=grad) if G else None
+    ev = torch.randn(B, G, D, requires_grad=grad) if G else None
 
     def one():
         with torch.set_grad_enabled(grad):
             y7 = dwconv3d_ref(x, w7, b, (T, H, W))
             f = dwconv3d_ref(x, w3, b, (T, H, W), act="gelu")
-            o = dsa3d_core_ref(q, k, v, off, (T, H, W), nh, cfg["kernel"], 1.0, head_chunk=4)
+            o = dsa3d_core_ref(q, k, v, off, (T, H, W), nh, cfg["kernel"], 1.0, head_chunk=4,
+                               extra_k=ek, extra_v=ev)
             if grad:
                 torch.autograd.backward([y7, f, o], [gy, gy, gy])
 
@@ -552,6 +573,7 @@ def main():
                         "offset net: depthwise 3x3x3 + GELU + 1x1, weights ~ N(0, {}) / N(0, {}), "
                         "bias {} {}".format(*cfg["offsets"][1:3], *cfg["offsets"][3])),
             "accumulation": "fp32", "pass": "fwd+bwd" if cfg["backward"] else "fwd",
+            "extra_keys": cfg.get("extra_g", 0),
         },
         "hbm_gbps": round(sbytes / (ms_step / 1e3) / 1e9, 1),
         "hbm_frac_of_peak": round(sbytes / (ms_step / 1e3) / 1e9 / HBM_PEAK_GBPS, 4),

@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define MSD_ABI_VERSION 2
+#define MSD_ABI_VERSION 3
 
 typedef enum msd_dtype { MSD_F32 = 0, MSD_BF16 = 1 } msd_dtype;
 
@@ -73,7 +73,11 @@ typedef struct msd_dsa3d_desc {
   uint32_t dropout_offset;     /* counter word: distinct per call for one seed    */
   uint64_t dropout_seed;       /* generator key                                   */
   float dropout_p;             /* drop probability                                */
-  int32_t reserved;            /* must be 0                                       */
+  /* Extra keys shared by every query (the reference's extra_kv, attention.py:
+   * 160-173): G projected keys and values per sample, appended to each query's
+   * kt*kh*kw taps before the softmax.  0 = none; at most 4096 (the tiled
+   * kernels take up to 256).                                                 */
+  int32_t extra_g;
 } msd_dsa3d_desc;
 
 /* Kernel family for the attention core.  AUTO picks the matrix-core tiled
@@ -100,19 +104,23 @@ const char* msd_last_error(void);
 /*
  * Forward of the attention core: replaces attention.py:106-186 (offset scale,
  * base grid + normalised offsets, grid_sample of K and V with border padding
- * and align_corners=False, scores / sqrt(hd), softmax, dropout, weighted sum
- * of V).  With dropout_p > 0, tap k (0 <= k < kt*kh*kw, in the reference's
- * (i*kh + j)*kw + k order) of global token row r = b*N + n and head m is
- * dropped when the first word of Philox4x32-10 (Salmon et al., SC'11) for
- * counter (k, r mod 2^32, (r >> 32) << 16 | m, dropout_offset) and key
- * (dropout_seed mod 2^32, dropout_seed >> 32) is below floor(p * 2^32); kept
- * weights are scaled by 1 / (1 - p) (fp32).
+ * and align_corners=False, the extra keys' concatenation, scores / sqrt(hd),
+ * softmax, dropout, weighted sum of V).  With dropout_p > 0, tap k (0 <= k <
+ * K = kt*kh*kw, in the reference's (i*kh + j)*kw + k order; extra key g is tap
+ * K + g) of global token row r = b*N + n and head m is dropped when the first
+ * word of Philox4x32-10 (Salmon et al., SC'11) for counter (k, r mod 2^32,
+ * (r >> 32) << 16 | m, dropout_offset) and key (dropout_seed mod 2^32,
+ * dropout_seed >> 32) is below floor(p * 2^32); kept weights are scaled by
+ * 1 / (1 - p) (fp32).
+ * extra_k, extra_v: [B, G, D] contiguous, G = desc->extra_g: k_proj and v_proj
+ * of the reference's extra_kv; NULL when G = 0.
  * out [B, N, D] (contiguous, token stride D).  lse [B, N, num_heads] fp32
- * receives the log-sum-exp of each query's scores for the backward; it may be
- * NULL when no backward follows.
+ * receives the log-sum-exp of each query's scores (taps and extra keys) for
+ * the backward; it may be NULL when no backward follows.
  */
 int msd_dsa3d_fwd(const msd_dsa3d_desc* desc, const void* q, const void* k, const void* v,
-                  const void* offsets, void* out, float* lse, void* stream);
+                  const void* offsets, const void* extra_k, const void* extra_v, void* out,
+                  float* lse, void* stream);
 
 /* Bytes of device workspace msd_dsa3d_bwd needs for `desc`. */
 size_t msd_dsa3d_bwd_workspace_size(const msd_dsa3d_desc* desc);
@@ -126,11 +134,14 @@ size_t msd_dsa3d_bwd_workspace_size(const msd_dsa3d_desc* desc);
  *               for callers that merge extra keys through the log-sum-exp.
  *   dq, dk, dv: written (not accumulated) with the strides of q, k, v.
  *   doffsets  : [B, N, C], gradient w.r.t. the unscaled offsets.
+ *   extra_k, extra_v: as for msd_dsa3d_fwd; d_extra_k, d_extra_v: [B, G, D]
+ *               contiguous, written; all four NULL when G = 0.
  */
 int msd_dsa3d_bwd(const msd_dsa3d_desc* desc, const void* q, const void* k, const void* v,
-                  const void* offsets, const void* out, const void* dout, const float* lse,
-                  const float* dlse, void* dq, void* dk, void* dv, void* doffsets,
-                  void* workspace, size_t workspace_bytes, void* stream);
+                  const void* offsets, const void* extra_k, const void* extra_v, const void* out,
+                  const void* dout, const float* lse, const float* dlse, void* dq, void* dk,
+                  void* dv, void* doffsets, void* d_extra_k, void* d_extra_v, void* workspace,
+                  size_t workspace_bytes, void* stream);
 
 /* Largest scratch, in bytes, msd_dsa3d_bwd_noalloc can give a call: what
  * msd_dsa3d_bwd_workspace_size reports for the same descriptor must not exceed
@@ -150,9 +161,10 @@ int msd_dsa3d_bwd(const msd_dsa3d_desc* desc, const void* q, const void* k, cons
  * calls that overlap on one GPU (other streams, other host threads) race.
  */
 int msd_dsa3d_bwd_noalloc(const msd_dsa3d_desc* desc, const void* q, const void* k,
-                          const void* v, const void* offsets, const void* out, const void* dout,
+                          const void* v, const void* offsets, const void* extra_k,
+                          const void* extra_v, const void* out, const void* dout,
                           const float* lse, const float* dlse, void* dq, void* dk, void* dv,
-                          void* doffsets, void* stream);
+                          void* doffsets, void* d_extra_k, void* d_extra_v, void* stream);
 
 /*
  * Depthwise 3-D convolution, channel-last: replaces nn.Conv3d(C, C, k,

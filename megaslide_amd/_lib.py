@@ -16,7 +16,7 @@ import threading
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libmegaslide_dsa3d.so")
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 MSD_F32 = 0
 MSD_BF16 = 1
@@ -50,7 +50,7 @@ class DsaDesc(ctypes.Structure):
         ("offset_scale", ctypes.c_float), ("softmax_scale", ctypes.c_float),
         ("algo", ctypes.c_int32), ("dropout_offset", ctypes.c_uint32),
         ("dropout_seed", ctypes.c_uint64), ("dropout_p", ctypes.c_float),
-        ("reserved", ctypes.c_int32),
+        ("extra_g", ctypes.c_int32),
     ]
 
 
@@ -91,13 +91,13 @@ def load() -> ctypes.CDLL:
         lib.msd_last_error.restype = ctypes.c_char_p
         lib.msd_last_error.argtypes = []
         lib.msd_dsa3d_fwd.restype = ctypes.c_int
-        lib.msd_dsa3d_fwd.argtypes = [ctypes.POINTER(DsaDesc), _vp, _vp, _vp, _vp, _vp, _vp, _vp]
+        lib.msd_dsa3d_fwd.argtypes = [ctypes.POINTER(DsaDesc)] + [_vp] * 9
         lib.msd_dsa3d_bwd_workspace_size.restype = ctypes.c_size_t
         lib.msd_dsa3d_bwd_workspace_size.argtypes = [ctypes.POINTER(DsaDesc)]
         lib.msd_dsa3d_bwd.restype = ctypes.c_int
-        lib.msd_dsa3d_bwd.argtypes = [ctypes.POINTER(DsaDesc)] + [_vp] * 13 + [ctypes.c_size_t, _vp]
+        lib.msd_dsa3d_bwd.argtypes = [ctypes.POINTER(DsaDesc)] + [_vp] * 17 + [ctypes.c_size_t, _vp]
         lib.msd_dsa3d_bwd_noalloc.restype = ctypes.c_int
-        lib.msd_dsa3d_bwd_noalloc.argtypes = [ctypes.POINTER(DsaDesc)] + [_vp] * 13
+        lib.msd_dsa3d_bwd_noalloc.argtypes = [ctypes.POINTER(DsaDesc)] + [_vp] * 17
         lib.msd_dwconv3d_fwd.restype = ctypes.c_int
         lib.msd_dwconv3d_fwd.argtypes = [ctypes.POINTER(ConvDesc), _vp, _vp, _vp, _vp, _vp]
         lib.msd_dwconv3d_bwd_workspace_size.restype = ctypes.c_size_t

@@ -17,17 +17,15 @@ What runs where:
   * offset scaling, base grid, trilinear K/V sampling with border clamp,
     scores, softmax and the weighted sum of V run fused in the HIP attention
     core, forward and backward.
-  * ``extra_kv`` (attention.py:160-173) is merged exactly through the
-    log-sum-exp: the HIP core returns the local output and its lse, the G extra
-    keys shared by every query form a small dense attention in PyTorch, and the
-    two softmax partitions are combined.
+  * ``extra_kv`` (attention.py:160-173): its k_proj / v_proj projections are
+    PyTorch GEMMs; the G extra keys and values join every query's taps in the
+    HIP core's softmax (forward and backward, their gradients included).
 
 There is no CPU path: on CPU tensors ``forward`` raises.
 """
 
 from __future__ import annotations
 
-import math
 from typing import Optional, Tuple
 
 import torch
@@ -111,45 +109,12 @@ class DeformableSlideAttention3D(nn.Module):
         v = self.v_proj(x)
         dt = q.dtype
         off = off.to(dt)
-        if extra_kv is None:
-            attn = dsa3d_core(q, k.to(dt), v.to(dt), off, video_shape, self.num_heads,
-                              self.kernel_size, self.offset_scale, dropout_p=drop_p)
-        else:
-            attn = self._with_extra_kv(q, k.to(dt), v.to(dt), off, video_shape, extra_kv, drop_p)
+        ek = ev = None
+        if extra_kv is not None:  # attention.py:160-173: projected, appended to every query's taps
+            ek = self.k_proj(extra_kv).to(dt)
+            ev = self.v_proj(extra_kv).to(dt)
+        attn = dsa3d_core(q, k.to(dt), v.to(dt), off, video_shape, self.num_heads,
+                          self.kernel_size, self.offset_scale, dropout_p=drop_p, extra_k=ek,
+                          extra_v=ev)
         return torch.addmm(dw.reshape(B * N, D), attn.reshape(B * N, D),
                            self.out_proj.weight.t()).view(B, N, D)
-
-    def _with_extra_kv(self, q, k, v, off, video_shape, extra_kv, drop_p=0.0):
-        """Local taps + G shared extra keys, merged through the log-sum-exp.
-
-        Exactly the reference's concatenation of the extra keys/values to every
-        query's tap list followed by one softmax (attention.py:160-183).  With
-        dropout, the merged weights of the local taps are a_l * p_local and of
-        the extra keys a_e * p_extra; dropping them is dropping p_local (in the
-        kernel) and p_extra (here), since the mask and scale commute with a_l
-        and a_e.
-        """
-        B, N, D = q.shape
-        nh, hd = self.num_heads, self.head_dim
-        G = extra_kv.shape[1]
-        loc, lse_loc = dsa3d_core(q, k, v, off, video_shape, nh, self.kernel_size,
-                                  self.offset_scale, return_lse=True,
-                                  dropout_p=drop_p)  # [B,N,D], [B,N,nh]
-        ek = self.k_proj(extra_kv).float()
-        ev = self.v_proj(extra_kv).float()
-        qh = q.float().view(B, N, nh, hd).permute(0, 2, 1, 3).contiguous()      # [B,nh,N,hd]
-        ekh = ek.view(B, G, nh, hd).permute(0, 2, 3, 1).contiguous()             # [B,nh,hd,G]
-        evh = ev.view(B, G, nh, hd).permute(0, 2, 1, 3).contiguous()             # [B,nh,G,hd]
-        s = torch.matmul(qh, ekh) * (1.0 / math.sqrt(hd))                       # [B,nh,N,G]
-        lse_e = torch.logsumexp(s, dim=-1)                                       # [B,nh,N]
-        pe = torch.softmax(s, dim=-1)
-        if drop_p > 0:
-            pe = F.dropout(pe, drop_p, training=True)
-        o_e = torch.matmul(pe, evh)                                              # [B,nh,N,hd]
-        lse_l = lse_loc.permute(0, 2, 1)                                         # [B,nh,N]
-        lse = torch.logaddexp(lse_l, lse_e)
-        a_l = torch.exp(lse_l - lse).unsqueeze(-1)
-        a_e = torch.exp(lse_e - lse).unsqueeze(-1)
-        loc_h = loc.float().view(B, N, nh, hd).permute(0, 2, 1, 3)
-        out = loc_h * a_l + o_e * a_e
-        return out.permute(0, 2, 1, 3).reshape(B, N, D).to(q.dtype)

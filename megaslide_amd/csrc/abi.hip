@@ -45,8 +45,10 @@ int check_dsa(const msd_dsa3d_desc* d) {
     return fail(MSD_ERR_ARG, "dsa3d: bad window (%d, %d, %d)", d->kt, d->kh, d->kw);
   if (d->dtype != MSD_F32 && d->dtype != MSD_BF16)
     return fail(MSD_ERR_UNSUPPORTED, "dsa3d: dtype %d not supported", d->dtype);
-  if (d->algo < MSD_ALGO_AUTO || d->algo > MSD_ALGO_TILED || d->reserved != 0)
-    return fail(MSD_ERR_ARG, "dsa3d: bad algo %d / reserved %d", d->algo, d->reserved);
+  if (d->algo < MSD_ALGO_AUTO || d->algo > MSD_ALGO_TILED)
+    return fail(MSD_ERR_ARG, "dsa3d: bad algo %d", d->algo);
+  if (d->extra_g < 0 || d->extra_g > 4096)
+    return fail(MSD_ERR_ARG, "dsa3d: extra_g %d outside [0, 4096]", d->extra_g);
   if (!(d->dropout_p >= 0.0f && d->dropout_p < 1.0f))
     return fail(MSD_ERR_ARG, "dsa3d: dropout_p %g outside [0, 1)", static_cast<double>(d->dropout_p));
   const int64_t D = static_cast<int64_t>(d->num_heads) * d->head_dim;
@@ -121,14 +123,19 @@ int scratch_address(void** out) {
 }
 
 int dsa3d_bwd_impl(const msd_dsa3d_desc* desc, const void* q, const void* k, const void* v,
-                   const void* offsets, const void* out, const void* dout, const float* lse,
-                   const float* dlse, void* dq, void* dk, void* dv, void* doffsets,
-                   void* workspace, size_t workspace_bytes, void* stream, bool noalloc) {
+                   const void* offsets, const void* ek, const void* ev, const void* out,
+                   const void* dout, const float* lse, const float* dlse, void* dq, void* dk,
+                   void* dv, void* doffsets, void* dek, void* dev, void* workspace,
+                   size_t workspace_bytes, void* stream, bool noalloc) {
   int rc = check_dsa(desc);
   if (rc != MSD_OK) return rc;
   rc = check_ptrs("dsa3d_bwd", elem_bytes(desc->dtype),
                   {q, k, v, offsets, out, dout, dq, dk, dv, doffsets});
   if (rc != MSD_OK) return rc;
+  if (desc->extra_g > 0) {
+    rc = check_ptrs("dsa3d_bwd(extra_k, extra_v, d_extra_k, d_extra_v)", 16, {ek, ev, dek, dev});
+    if (rc != MSD_OK) return rc;
+  }
   rc = check_ptrs("dsa3d_bwd(lse)", 4, {lse});
   if (rc != MSD_OK) return rc;
   if (dlse != nullptr && !aligned(dlse, 4)) return fail(MSD_ERR_ALIGN, "dsa3d_bwd: dlse misaligned");
@@ -153,14 +160,16 @@ int dsa3d_bwd_impl(const msd_dsa3d_desc* desc, const void* q, const void* k, con
                         msd::dsa3d_tiled_supported(*desc, dq, dk, dv);
   if (desc->algo == MSD_ALGO_TILED && !tiled_ok)
     return fail(MSD_ERR_UNSUPPORTED,
-                "dsa3d_bwd: tiled kernels need bf16 or fp32, head_dim 32, 64, 96 or 128, <= 160 taps and "
-                "16-byte aligned rows");
+                "dsa3d_bwd: tiled kernels need bf16 or fp32, head_dim 32, 64, 96 or 128, <= 160 taps, "
+                "<= 256 extra keys and 16-byte aligned rows");
   if (tiled_ok && desc->algo != MSD_ALGO_DIRECT)
-    return launch_status(msd::launch_dsa3d_bwd_tiled(*desc, q, k, v, offsets, out, dout, lse, dlse,
-                                                     dq, dk, dv, doffsets, workspace, s),
+    return launch_status(msd::launch_dsa3d_bwd_tiled(*desc, q, k, v, offsets, ek, ev, out, dout,
+                                                     lse, dlse, dq, dk, dv, doffsets, dek, dev,
+                                                     workspace, s),
                          "dsa3d_bwd");
-  return launch_status(msd::launch_dsa3d_bwd_direct(*desc, q, k, v, offsets, out, dout, lse, dlse,
-                                                    dq, dk, dv, doffsets, workspace, s),
+  return launch_status(msd::launch_dsa3d_bwd_direct(*desc, q, k, v, offsets, ek, ev, out, dout,
+                                                    lse, dlse, dq, dk, dv, doffsets, dek, dev,
+                                                    workspace, s),
                        "dsa3d_bwd");
 }
 
@@ -173,23 +182,30 @@ int msd_abi_version(void) { return MSD_ABI_VERSION; }
 const char* msd_last_error(void) { return g_err; }
 
 int msd_dsa3d_fwd(const msd_dsa3d_desc* desc, const void* q, const void* k, const void* v,
-                  const void* offsets, void* out, float* lse, void* stream) {
+                  const void* offsets, const void* extra_k, const void* extra_v, void* out,
+                  float* lse, void* stream) {
   int rc = check_dsa(desc);
   if (rc != MSD_OK) return rc;
   rc = check_ptrs("dsa3d_fwd", elem_bytes(desc->dtype), {q, k, v, offsets, out});
   if (rc != MSD_OK) return rc;
+  if (desc->extra_g > 0) {
+    rc = check_ptrs("dsa3d_fwd(extra_k, extra_v)", 16, {extra_k, extra_v});
+    if (rc != MSD_OK) return rc;
+  }
   if (lse != nullptr && !aligned(lse, 4)) return fail(MSD_ERR_ALIGN, "dsa3d_fwd: lse misaligned");
   const bool tiled_ok = msd::dsa3d_tiled_supported(*desc, q, k, v);
   if (desc->algo == MSD_ALGO_TILED && !tiled_ok)
     return fail(MSD_ERR_UNSUPPORTED,
-                "dsa3d_fwd: tiled kernels need bf16 or fp32, head_dim 32, 64, 96 or 128, <= 160 taps and "
-                "16-byte aligned rows");
+                "dsa3d_fwd: tiled kernels need bf16 or fp32, head_dim 32, 64, 96 or 128, <= 160 taps, "
+                "<= 256 extra keys and 16-byte aligned rows");
   if (desc->B == 0) return MSD_OK;
   const hipStream_t s = static_cast<hipStream_t>(stream);
   if (tiled_ok && desc->algo != MSD_ALGO_DIRECT)
-    return launch_status(msd::launch_dsa3d_fwd_tiled(*desc, q, k, v, offsets, out, lse, s),
+    return launch_status(msd::launch_dsa3d_fwd_tiled(*desc, q, k, v, offsets, extra_k, extra_v,
+                                                     out, lse, s),
                          "dsa3d_fwd");
-  return launch_status(msd::launch_dsa3d_fwd_direct(*desc, q, k, v, offsets, out, lse, s),
+  return launch_status(msd::launch_dsa3d_fwd_direct(*desc, q, k, v, offsets, extra_k, extra_v, out,
+                                                    lse, s),
                        "dsa3d_fwd");
 }
 
@@ -199,19 +215,21 @@ size_t msd_dsa3d_bwd_workspace_size(const msd_dsa3d_desc* desc) {
 }
 
 int msd_dsa3d_bwd(const msd_dsa3d_desc* desc, const void* q, const void* k, const void* v,
-                  const void* offsets, const void* out, const void* dout, const float* lse,
-                  const float* dlse, void* dq, void* dk, void* dv, void* doffsets,
-                  void* workspace, size_t workspace_bytes, void* stream) {
-  return dsa3d_bwd_impl(desc, q, k, v, offsets, out, dout, lse, dlse, dq, dk, dv, doffsets,
-                        workspace, workspace_bytes, stream, false);
+                  const void* offsets, const void* extra_k, const void* extra_v, const void* out,
+                  const void* dout, const float* lse, const float* dlse, void* dq, void* dk,
+                  void* dv, void* doffsets, void* d_extra_k, void* d_extra_v, void* workspace,
+                  size_t workspace_bytes, void* stream) {
+  return dsa3d_bwd_impl(desc, q, k, v, offsets, extra_k, extra_v, out, dout, lse, dlse, dq, dk, dv,
+                        doffsets, d_extra_k, d_extra_v, workspace, workspace_bytes, stream, false);
 }
 
 int msd_dsa3d_bwd_noalloc(const msd_dsa3d_desc* desc, const void* q, const void* k,
-                          const void* v, const void* offsets, const void* out, const void* dout,
+                          const void* v, const void* offsets, const void* extra_k,
+                          const void* extra_v, const void* out, const void* dout,
                           const float* lse, const float* dlse, void* dq, void* dk, void* dv,
-                          void* doffsets, void* stream) {
-  return dsa3d_bwd_impl(desc, q, k, v, offsets, out, dout, lse, dlse, dq, dk, dv, doffsets,
-                        nullptr, 0, stream, true);
+                          void* doffsets, void* d_extra_k, void* d_extra_v, void* stream) {
+  return dsa3d_bwd_impl(desc, q, k, v, offsets, extra_k, extra_v, out, dout, lse, dlse, dq, dk, dv,
+                        doffsets, d_extra_k, d_extra_v, nullptr, 0, stream, true);
 }
 
 int msd_dwconv3d_fwd(const msd_dwconv3d_desc* desc, const void* x, const void* weight,

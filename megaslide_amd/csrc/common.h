@@ -101,20 +101,22 @@ inline unsigned fill_blocks(int64_t n) {
 // after argument validation.  They return a hipError_t.
 namespace msd {
 hipError_t launch_dsa3d_fwd_direct(const msd_dsa3d_desc& d, const void* q, const void* k,
-                                   const void* v, const void* off, void* out, float* lse,
-                                   hipStream_t s);
+                                   const void* v, const void* off, const void* ek, const void* ev,
+                                   void* out, float* lse, hipStream_t s);
 hipError_t launch_dsa3d_bwd_direct(const msd_dsa3d_desc& d, const void* q, const void* k,
-                                   const void* v, const void* off, const void* out,
-                                   const void* dout, const float* lse, const float* dlse, void* dq,
-                                   void* dk, void* dv, void* doff, void* ws, hipStream_t s);
+                                   const void* v, const void* off, const void* ek, const void* ev,
+                                   const void* out, const void* dout, const float* lse,
+                                   const float* dlse, void* dq, void* dk, void* dv, void* doff,
+                                   void* dek, void* dev, void* ws, hipStream_t s);
 bool dsa3d_tiled_supported(const msd_dsa3d_desc& d, const void* q, const void* k, const void* v);
 hipError_t launch_dsa3d_fwd_tiled(const msd_dsa3d_desc& d, const void* q, const void* k,
-                                  const void* v, const void* off, void* out, float* lse,
-                                  hipStream_t s);
+                                  const void* v, const void* off, const void* ek, const void* ev,
+                                  void* out, float* lse, hipStream_t s);
 hipError_t launch_dsa3d_bwd_tiled(const msd_dsa3d_desc& d, const void* q, const void* k,
-                                  const void* v, const void* off, const void* out,
-                                  const void* dout, const float* lse, const float* dlse, void* dq,
-                                  void* dk, void* dv, void* doff, void* ws, hipStream_t s);
+                                  const void* v, const void* off, const void* ek, const void* ev,
+                                  const void* out, const void* dout, const float* lse,
+                                  const float* dlse, void* dq, void* dk, void* dv, void* doff,
+                                  void* dek, void* dev, void* ws, hipStream_t s);
 size_t dsa3d_bwd_ws_bytes(const msd_dsa3d_desc& d);
 size_t dsa3d_tiled_bwd_ws_bytes(const msd_dsa3d_desc& d);
 hipError_t launch_dwconv3d_fwd(const msd_dwconv3d_desc& d, const void* x, const void* w,

@@ -45,6 +45,9 @@ struct CoreArgs {
   float div_x, div_y, div_z;     // T-1, H-1, W-1: divisors of slots 0, 1, 2 (0 if that dim is 1)
   float rdiv_x, rdiv_y, rdiv_z;  // their reciprocals (0 if the dim is 1), for the gradient
   DropoutArgs drop;              // attention dropout on the softmax weights
+  const void* ek;                // extra keys / values [B, G, D] (attention.py:160-173)
+  const void* ev;
+  int G;                         // extra keys per sample (0 = none)
 };
 
 template <typename T>
@@ -131,6 +134,27 @@ __global__ __launch_bounds__(kBlock) void dsa3d_fwd_direct_kernel(CoreArgs a, T*
       }
     }
   }
+  // extra keys shared by every query: taps K + g of the same softmax
+  const T* __restrict__ ekp = static_cast<const T*>(a.ek);
+  const T* __restrict__ evp = static_cast<const T*>(a.ev);
+  const int D = a.nh * a.hd;
+  for (int g = 0; g < a.G; ++g) {
+    const int64_t erow = (static_cast<int64_t>(b) * a.G + g) * D + cbase;
+    float part = 0.0f;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j)
+      if (lane * CPL + j < a.hd) part += qv[j] * ld(ekp, erow + j);
+    const float s = group_sum<kGroup>(part) * a.softmax_scale;
+    const float mn = fmaxf(m, s);
+    const float corr = __expf(m - mn);
+    const float e = __expf(s - mn);
+    l = l * corr + e;
+    const float ed = e * dropout_factor(a.drop, bn, head, K + g);
+#pragma unroll
+    for (int j = 0; j < CPL; ++j)
+      acc[j] = acc[j] * corr + (lane * CPL + j < a.hd ? ed * ld(evp, erow + j) : 0.0f);
+    m = mn;
+  }
   T* __restrict__ orow = out + bn * (static_cast<int64_t>(a.nh) * a.hd);
   const float inv = 1.0f / l;
 #pragma unroll
@@ -143,7 +167,8 @@ template <typename T, int CPL>
 __global__ __launch_bounds__(kBlock) void dsa3d_bwd_direct_kernel(
     CoreArgs a, const T* __restrict__ out, const T* __restrict__ dout, const float* __restrict__ lse,
     const float* __restrict__ dlse, T* __restrict__ dq, float* __restrict__ dk_acc,
-    float* __restrict__ dv_acc, T* __restrict__ doff) {
+    float* __restrict__ dv_acc, T* __restrict__ doff, float* __restrict__ dek_acc,
+    float* __restrict__ dev_acc) {
   const int lane = threadIdx.x % kGroup;
   const int64_t gid = static_cast<int64_t>(blockIdx.x) * kGroupsPerBlock + threadIdx.x / kGroup;
   const int64_t total = static_cast<int64_t>(a.B) * a.N * a.nh;
@@ -270,6 +295,34 @@ __global__ __launch_bounds__(kBlock) void dsa3d_bwd_direct_kernel(
       }
     }
   }
+  // extra keys: dq += ds scale ek_g; dEK_g += ds scale q, dEV_g += p f dO (fp32 atomics)
+  const T* __restrict__ ekp = static_cast<const T*>(a.ek);
+  const T* __restrict__ evp = static_cast<const T*>(a.ev);
+  for (int g = 0; g < a.G; ++g) {
+    const int64_t erow = (static_cast<int64_t>(b) * a.G + g) * D + cbase;
+    float ekv[CPL], s_part = 0.0f, dp_part = 0.0f;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      const bool on = lane * CPL + j < a.hd;
+      ekv[j] = on ? ld(ekp, erow + j) : 0.0f;
+      s_part += qv[j] * ekv[j];
+      dp_part += on ? gov[j] * ld(evp, erow + j) : 0.0f;
+    }
+    const float s = group_sum<kGroup>(s_part) * sc;
+    const float dp = group_sum<kGroup>(dp_part);
+    const float p = __expf(s - lse_q);
+    const float dfac = dropout_factor(a.drop, bn, head, K + g);
+    const float pd = p * dfac;
+    const float dss = p * (dfac * dp - delta) * sc;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      if (lane * CPL + j < a.hd) {
+        dqv[j] += dss * ekv[j];
+        atomicAdd(dek_acc + erow + j, dss * qv[j]);
+        atomicAdd(dev_acc + erow + j, pd * gov[j]);
+      }
+    }
+  }
 #pragma unroll
   for (int j = 0; j < CPL; ++j)
     if (lane * CPL + j < a.hd) st(dq, bn * a.qs + cbase + j, dqv[j]);
@@ -288,8 +341,11 @@ __global__ __launch_bounds__(256) void strided_convert_kernel(const float* __res
 }
 
 CoreArgs make_args(const msd_dsa3d_desc& d, const void* q, const void* k, const void* v,
-                   const void* off) {
+                   const void* off, const void* ek, const void* ev) {
   CoreArgs a;
+  a.ek = ek;
+  a.ev = ev;
+  a.G = d.extra_g;
   a.q = q;
   a.k = k;
   a.v = v;
@@ -348,12 +404,15 @@ hipError_t fwd_typed(const msd_dsa3d_desc& d, const CoreArgs& a, void* out, floa
 template <typename T>
 hipError_t bwd_typed(const msd_dsa3d_desc& d, const CoreArgs& a, const void* out, const void* dout,
                      const float* lse, const float* dlse, void* dq, void* dk, void* dv, void* doff,
-                     void* ws, hipStream_t s) {
+                     void* dek, void* dev, void* ws, hipStream_t s) {
   const int64_t rows = static_cast<int64_t>(a.B) * a.N;
   const int D = a.nh * a.hd;
+  const int64_t erows = static_cast<int64_t>(a.B) * a.G;
   float* dk_acc = static_cast<float*>(ws);
   float* dv_acc = dk_acc + rows * D;
-  const int64_t nacc = 2 * rows * D;
+  float* dek_acc = dv_acc + rows * D;
+  float* dev_acc = dek_acc + erows * D;
+  const int64_t nacc = 2 * (rows + erows) * D;
   hipLaunchKernelGGL(fill_zero_f32, dim3(fill_blocks(nacc)), dim3(256), 0, s, dk_acc, nacc);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
@@ -362,7 +421,8 @@ hipError_t bwd_typed(const msd_dsa3d_desc& d, const CoreArgs& a, const void* out
   e = dispatch_cpl(d.head_dim, [&]<int CPL>() {
     hipLaunchKernelGGL((dsa3d_bwd_direct_kernel<T, CPL>), grid, dim3(kBlock), 0, s, a,
                        static_cast<const T*>(out), static_cast<const T*>(dout), lse, dlse,
-                       static_cast<T*>(dq), dk_acc, dv_acc, static_cast<T*>(doff));
+                       static_cast<T*>(dq), dk_acc, dv_acc, static_cast<T*>(doff), dek_acc,
+                       dev_acc);
     return hipGetLastError();
   });
   if (e != hipSuccess) return e;
@@ -371,6 +431,13 @@ hipError_t bwd_typed(const msd_dsa3d_desc& d, const CoreArgs& a, const void* out
                      static_cast<T*>(dk), rows, D, a.ks);
   hipLaunchKernelGGL((strided_convert_kernel<T>), cgrid, dim3(256), 0, s, dv_acc,
                      static_cast<T*>(dv), rows, D, a.vs);
+  if (erows > 0) {
+    const dim3 egrid(static_cast<unsigned>((erows * D + 255) / 256));
+    hipLaunchKernelGGL((strided_convert_kernel<T>), egrid, dim3(256), 0, s, dek_acc,
+                       static_cast<T*>(dek), erows, D, static_cast<int64_t>(D));
+    hipLaunchKernelGGL((strided_convert_kernel<T>), egrid, dim3(256), 0, s, dev_acc,
+                       static_cast<T*>(dev), erows, D, static_cast<int64_t>(D));
+  }
   return hipGetLastError();
 }
 
@@ -380,31 +447,33 @@ int dsa3d_max_head_dim() { return kGroup * 16; }
 
 // The larger of the two families' needs, so a descriptor the tiled kernels
 // take still runs if a pointer sends it to the direct ones: the direct
-// backward's dK/dV fp32 accumulators, the tiled backward's per-tap p and ds
+// backward's dK/dV (and extra-key) fp32 accumulators, the tiled backward's per-tap p and ds
 // (the larger whenever kt * kh * kw > head_dim: every tiled head size at the
 // reference 3x7x7 window).
 size_t dsa3d_bwd_ws_bytes(const msd_dsa3d_desc& d) {
-  const int64_t rows = static_cast<int64_t>(d.B) * d.T * d.H * d.W;
+  const int64_t rows = static_cast<int64_t>(d.B) * d.T * d.H * d.W + int64_t{d.B} * d.extra_g;
   const size_t direct = static_cast<size_t>(2 * rows * d.num_heads * d.head_dim) * sizeof(float);
   const size_t tiled = dsa3d_tiled_bwd_ws_bytes(d);
   return direct > tiled ? direct : tiled;
 }
 
-hipError_t launch_dsa3d_fwd_direct(const msd_dsa3d_desc& d, const void* q, const void* k, const void* v,
-                            const void* off, void* out, float* lse, hipStream_t s) {
-  const CoreArgs a = make_args(d, q, k, v, off);
+hipError_t launch_dsa3d_fwd_direct(const msd_dsa3d_desc& d, const void* q, const void* k,
+                                   const void* v, const void* off, const void* ek, const void* ev,
+                                   void* out, float* lse, hipStream_t s) {
+  const CoreArgs a = make_args(d, q, k, v, off, ek, ev);
   if (d.dtype == MSD_BF16) return fwd_typed<bf16>(d, a, out, lse, s);
   return fwd_typed<float>(d, a, out, lse, s);
 }
 
-hipError_t launch_dsa3d_bwd_direct(const msd_dsa3d_desc& d, const void* q, const void* k, const void* v,
-                            const void* off, const void* out, const void* dout, const float* lse,
-                            const float* dlse, void* dq, void* dk, void* dv, void* doff,
-                            void* ws, hipStream_t s) {
-  const CoreArgs a = make_args(d, q, k, v, off);
+hipError_t launch_dsa3d_bwd_direct(const msd_dsa3d_desc& d, const void* q, const void* k,
+                                   const void* v, const void* off, const void* ek, const void* ev,
+                                   const void* out, const void* dout, const float* lse,
+                                   const float* dlse, void* dq, void* dk, void* dv, void* doff,
+                                   void* dek, void* dev, void* ws, hipStream_t s) {
+  const CoreArgs a = make_args(d, q, k, v, off, ek, ev);
   if (d.dtype == MSD_BF16)
-    return bwd_typed<bf16>(d, a, out, dout, lse, dlse, dq, dk, dv, doff, ws, s);
-  return bwd_typed<float>(d, a, out, dout, lse, dlse, dq, dk, dv, doff, ws, s);
+    return bwd_typed<bf16>(d, a, out, dout, lse, dlse, dq, dk, dv, doff, dek, dev, ws, s);
+  return bwd_typed<float>(d, a, out, dout, lse, dlse, dq, dk, dv, doff, dek, dev, ws, s);
 }
 
 }  // namespace msd

@@ -13,6 +13,8 @@
 // (infinity/video/attention.py:106-186) because trilinear sampling is linear in
 // the sampled rows.  Coordinates and corner choice round exactly as the fp32
 // reference does (div_rn, dsa3d_coords.h).
+#include <algorithm>
+
 #include "dsa3d_tiled_common.h"
 
 namespace msd {
@@ -61,7 +63,9 @@ __device__ __forceinline__ Slot fwd_slot(const Slot& s) {
   return s;
 }
 
-template <int HD, typename E>
+// XK: the call has extra keys (a.G > 0); without them the kernel compiles to
+// the plain tap path.
+template <int HD, typename E, bool XK>
 __global__ __launch_bounds__(kThreads, (fwd_min_waves<HD, E>())) void dsa3d_fwd_tiled_kernel(
     Args a, E* __restrict__ out, float* __restrict__ lse) {
   constexpr int NB = fwd_table_bufs<HD, E>();
@@ -115,12 +119,42 @@ __global__ __launch_bounds__(kThreads, (fwd_min_waves<HD, E>())) void dsa3d_fwd_
     w = wn;
   }
 
-  // ---- softmax over each query's taps (32 lanes x kSlots) -------------------
+  // ---- extra keys (attention.py:160-173): S_e[q][g] = q . ek_g (MFMA) into the
+  // first table, read back by the lanes of each query: lane `sub` takes keys
+  // sub + 32 j ------------------------------------------------------------------
+  constexpr int EPL = XK ? kMaxExtra / kSubs : 1;
+  const int G = XK ? a.G : 0, Gp = (G + 31) & ~31;
+  float se[EPL];
+  if constexpr (XK) {
+    __syncthreads();  // every pass-1 read of the tables is done
+    for (int eb = tl.wave; eb < Gp / 16; eb += kWaves) {
+      op_t<E> y[HD / 32];
+      load_extra_rows<HD, E>(a, tl, a.ek, eb, y);
+      f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int cc = 0; cc < HD / 32; ++cc) acc = mma16(qx[cc], y[cc], acc);
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr)
+        s_tab[0][(4 * (tl.lane >> 4) + rr) * kSRow + 16 * eb + (tl.lane & 15)] = acc[rr];
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) {
+    const int g = tl.sub + kSubs * j;
+    se[j] = XK && g < G ? s_tab[0][tl.q * kSRow + g] * a.softmax_scale : -INFINITY;
+  }
+
+  // ---- softmax over each query's taps (32 lanes x kSlots) and extra keys ----
   float mx = -INFINITY;
 #pragma unroll
   for (int i = 0; i < kSlots; ++i) {
     sc[i] = slot_z0(sl[i]) >= 0 ? sc[i] * a.softmax_scale : -INFINITY;
     mx = fmaxf(mx, sc[i]);
+  }
+  if constexpr (XK) {
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) mx = fmaxf(mx, se[j]);
   }
 #pragma unroll
   for (int m = 1; m < kSubs; m <<= 1) mx = fmaxf(mx, __shfl_xor(mx, m));
@@ -130,6 +164,13 @@ __global__ __launch_bounds__(kThreads, (fwd_min_waves<HD, E>())) void dsa3d_fwd_
     sc[i] = slot_z0(sl[i]) >= 0 ? __expf(sc[i] - mx) : 0.0f;
     den += sc[i];
   }
+  if constexpr (XK) {
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+      se[j] = tl.sub + kSubs * j < G ? __expf(se[j] - mx) : 0.0f;
+      den += se[j];
+    }
+  }
 #pragma unroll
   for (int m = 1; m < kSubs; m <<= 1) den += __shfl_xor(den, m);
   const float inv_den = 1.0f / den;
@@ -138,9 +179,8 @@ __global__ __launch_bounds__(kThreads, (fwd_min_waves<HD, E>())) void dsa3d_fwd_
     sc[i] *= inv_den * slot_dropout(sl[i], a.drop) * a.fix_a;  // p (dropped), fixed-point units
   if (lse != nullptr && tl.q_ok && tl.sub == 0) lse[tl.qn * a.nh + tl.head] = mx + logf(den);
 
-  // ---- pass 2: O = A . V ------------------------------------------------------
-  // The waves form CG channel groups of KP waves; wave w of group g takes the
-  // voxel k-steps w % KP, + KP, ... of a step for the TPW channel tiles of
+  // ---- output.  The waves form CG channel groups of KP waves; wave w of group
+  // g takes the k-steps w % KP, + KP, ... of a table for the TPW channel tiles of
   // group g: one A operand feeds TPW independent MFMAs, and the KP partial O
   // are summed once at the end.  hd 64 and 128: one group of 8 waves (fp32
   // hd 128: two groups of 4, for registers).  hd 96: six single-tile groups
@@ -155,6 +195,32 @@ __global__ __launch_bounds__(kThreads, (fwd_min_waves<HD, E>())) void dsa3d_fwd_
   f32x4_t oacc[TPW];
 #pragma unroll
   for (int t = 0; t < TPW; ++t) oacc[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  if constexpr (XK) {
+    // extra keys: O += P_e . EV with P_e = p f (fixed-point units, as floats)
+    // in place of S_e (each entry is read and written by its own lane) and EV
+    // staged transposed in the V^T buffer
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+      const int g = tl.sub + kSubs * j;
+      if (g < Gp)
+        s_tab[0][tl.q * kSRow + g] =
+            g < G ? se[j] * inv_den * a.fix_a *
+                        (a.drop.threshold == 0
+                             ? 1.0f
+                             : dropout_factor(a.drop, tl.qn, tl.head, a.K + g))
+                  : 0.0f;
+    }
+    stage_extra_t<HD, E>(a, tl, a.ev, 0, Gp, VR, s_vt, kThreads);
+    __syncthreads();
+    for (int kc = 32 * kph; av_wave && kc < Gp; kc += 32 * KP) {
+      const op_t<E> av = f32_to_op<E>(&s_tab[0][mq * kSRow + kc + kq]);
+#pragma unroll
+      for (int t = 0; t < TPW; ++t)
+        oacc[t] = mma16(av, load_op<E>(&s_vt[(16 * (cg * TPW + t) + mq) * VR + kc + kq]), oacc[t]);
+    }
+  }
+
+  // ---- pass 2: O += A . V over the taps --------------------------------------
   StageRows<kThreads, HD, E> vr;
   w = walk_begin(box);
   if (nit > 0) load_stage_rows<kThreads, HD, E>(a, tl, w.c, w.z, vp, a.vs, tl.head * HD, vr);
@@ -738,7 +804,11 @@ __global__ __launch_bounds__(P2Tile<FR>::Threads) void dsa3d_bwd_p2_kernel(
 #pragma unroll
       for (int kp = 0; kp < KPQ; ++kp) v += red[((f * KPQ + kp) * kTQ + mm) * CW + ch];
       const int64_t n = tile_row(a, tl, m);
-      if (n >= 0) dq[n * a.qs + cw0 + ch] = from_f32<E>(v * s_binv[m]);
+      if (n >= 0) {
+        E* const o = &dq[n * a.qs + cw0 + ch];
+        // the first kernel wrote the extra keys' part of dq
+        *o = from_f32<E>(v * s_binv[m] + (a.G > 0 ? to_f32(*o) : 0.0f));
+      }
     }
   } else {
     // dq_acc[j][r] = dq[query 16*fq + 4*(lane/16) + r][channel 16*ct + lane%16]
@@ -751,8 +821,249 @@ __global__ __launch_bounds__(P2Tile<FR>::Threads) void dsa3d_bwd_p2_kernel(
       for (int r = 0; r < 4; ++r) {
         const int m = kTQ * fq + 4 * (tl.lane >> 4) + r;
         const int64_t n = tile_row(a, tl, m);
-        if (n >= 0) dq[n * a.qs + cw0 + 16 * ct + mq] = from_f32<E>(dq_acc[j][r] * s_binv[m]);
+        if (n >= 0) {
+          E* const o = &dq[n * a.qs + cw0 + 16 * ct + mq];
+          *o = from_f32<E>(dq_acc[j][r] * s_binv[m] + (a.G > 0 ? to_f32(*o) : 0.0f));
+        }
       }
+    }
+  }
+}
+
+// Backward of the extra keys (attention.py:160-173) for 16 consecutive tokens
+// of one sample and head (4 waves, 16 lanes per query): S_e = q . ek_g and
+// dP_e = dO . ev_g on the matrix cores, then per (query, key) p = exp(scale
+// S_e - lse), the dropout factor f of tap K + g, ds * scale = p (f dP_e -
+// Delta) scale (Delta = dO . O - dlse).  It writes ds * scale and p f
+// ([B, nh, N, G], for the dEK / dEV reduction) and dq's extra part sum_g
+// ds_g scale ek_g (MFMA, to dq, which the second backward kernel adds to).
+constexpr int kXQ = 16;
+template <int HD, typename E>
+__global__ __launch_bounds__(256) void dsa3d_bwd_extra_kernel(
+    Args a, const E* __restrict__ out, const E* __restrict__ dout, const float* __restrict__ lse,
+    const float* __restrict__ dlse, E* __restrict__ dq, E* __restrict__ ds_e,
+    E* __restrict__ pf_e) {
+  constexpr int EKR = sizeof(E) == 2 ? 40 : 36;  // 16-byte aligned transposed rows
+  __shared__ __attribute__((aligned(16))) float s_s[kXQ * kSRow];   // S_e, then ds * scale
+  __shared__ __attribute__((aligned(16))) float s_dp[kXQ * kSRow];  // dP_e
+  __shared__ __attribute__((aligned(16))) word_t<E> s_ekt[HD * EKR];  // 32 keys of EK^T
+  __shared__ float s_delta[kXQ], s_lse[kXQ];
+  const int G = a.G, Gp = (G + 31) & ~31;
+  const int D = a.nh * HD;
+  const int b = blockIdx.x / ((a.N + kXQ - 1) / kXQ);
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x % ((a.N + kXQ - 1) / kXQ)) * kXQ;
+  const int head = blockIdx.y;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int mq = lane & 15, kq = 8 * (lane >> 4);
+  const int64_t sample0 = static_cast<int64_t>(b) * a.N;
+  // Delta and lse of each query: 16 lanes per query
+  {
+    const int qi = threadIdx.x / 16, sub = threadIdx.x % 16;
+    const int64_t n = n0 + qi;
+    float part = 0.0f;
+    if (n < a.N) {
+      const int64_t base = (sample0 + n) * D + head * HD;
+      for (int c = sub; c < HD; c += 16) part += to_f32(dout[base + c]) * to_f32(out[base + c]);
+    }
+    part = group_sum<16>(part);
+    if (sub == 0) {
+      const int64_t r = (sample0 + (n < a.N ? n : 0)) * a.nh + head;
+      s_delta[qi] = n < a.N ? part - (dlse != nullptr ? dlse[r] : 0.0f) : 0.0f;
+      s_lse[qi] = n < a.N ? lse[r] : 0.0f;
+    }
+  }
+  // q and dO rows of the 16 queries as MFMA A operands (zero past N)
+  op_t<E> xq[HD / 32], xo[HD / 32];
+  {
+    const int64_t n = n0 + mq;
+#pragma unroll
+    for (int c = 0; c < HD / 32; ++c) xq[c] = xo[c] = zero_op<E>();
+    if (n < a.N) {
+      const E* qr = static_cast<const E*>(a.q) + (sample0 + n) * a.qs + head * HD + kq;
+      const E* orow = dout + (sample0 + n) * D + head * HD + kq;
+#pragma unroll
+      for (int c = 0; c < HD / 32; ++c) {
+        xq[c] = load_op<E>(qr + 32 * c);
+        xo[c] = load_op<E>(orow + 32 * c);
+      }
+    }
+  }
+  const E* const ek = static_cast<const E*>(a.ek) + static_cast<int64_t>(b) * a.G * D + head * HD;
+  const E* const ev = static_cast<const E*>(a.ev) + static_cast<int64_t>(b) * a.G * D + head * HD;
+  for (int eb = wave; eb < Gp / 16; eb += 4) {
+    const int g = 16 * eb + mq;
+    f32x4_t sacc = {0.0f, 0.0f, 0.0f, 0.0f}, dacc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int c = 0; c < HD / 32; ++c) {
+      const op_t<E> yk = g < G ? load_op<E>(ek + static_cast<int64_t>(g) * D + 32 * c + kq) : zero_op<E>();
+      const op_t<E> yv = g < G ? load_op<E>(ev + static_cast<int64_t>(g) * D + 32 * c + kq) : zero_op<E>();
+      sacc = mma16(xq[c], yk, sacc);
+      dacc = mma16(xo[c], yv, dacc);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      s_s[(4 * (lane >> 4) + r) * kSRow + g] = sacc[r];
+      s_dp[(4 * (lane >> 4) + r) * kSRow + g] = dacc[r];
+    }
+  }
+  __syncthreads();
+  // p, ds * scale per (query, key): thread t takes query t / 16, keys t % 16 + 16 j
+  {
+    const int qi = threadIdx.x / 16, sub = threadIdx.x % 16;
+    const int64_t n = n0 + qi;
+    const int64_t row = sample0 + n;
+    const int64_t erow = ((static_cast<int64_t>(b) * a.nh + head) * a.N + n) * G;
+    for (int g = sub; g < Gp; g += 16) {
+      float dss = 0.0f;
+      if (g < G && n < a.N) {
+        const float pe = __expf(s_s[qi * kSRow + g] * a.softmax_scale - s_lse[qi]);
+        const float f = a.drop.threshold == 0 ? 1.0f : dropout_factor(a.drop, row, head, a.K + g);
+        dss = pe * (f * s_dp[qi * kSRow + g] - s_delta[qi]) * a.softmax_scale;
+        ds_e[erow + g] = from_f32<E>(dss);
+        pf_e[erow + g] = from_f32<E>(pe * f);
+      }
+      s_s[qi * kSRow + g] = dss;  // read by this thread only above
+    }
+  }
+  // dq_e = DS_e . EK: k-steps of 32 keys, EK^T staged per step; wave w takes
+  // the channel tiles w, w + 4, ...
+  constexpr int CT = HD / 16, TW = (CT + 3) / 4;
+  f32x4_t dqa[TW];
+#pragma unroll
+  for (int t = 0; t < TW; ++t) dqa[t] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int kc = 0; kc < Gp; kc += 32) {
+    __syncthreads();  // the ds table is complete (first step) / the previous step's MFMAs are done
+    for (int e = threadIdx.x; e < 32 * (HD / 8); e += 256) {
+      const int gi = e / (HD / 8), cg = e % (HD / 8), g = kc + gi;
+      op_t<E> x = zero_op<E>();
+      if (g < G) x = load_op<E>(ek + static_cast<int64_t>(g) * D + 8 * cg);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        if constexpr (sizeof(E) == 2) {
+          const u32x4_t xb = __builtin_bit_cast(u32x4_t, x);
+          s_ekt[(8 * cg + i) * EKR + gi] =
+              static_cast<uint16_t>((i & 1) ? (xb[i / 2] >> 16) : (xb[i / 2] & 0xffffu));
+        } else {
+          s_ekt[(8 * cg + i) * EKR + gi] = x[i];
+        }
+      }
+    }
+    __syncthreads();
+    float bq[8];
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) bq[jj] = s_s[mq * kSRow + kc + kq + jj];
+    const PreciseOp<E> bp = precise_op<E>(bq);
+#pragma unroll
+    for (int t = 0; t < TW; ++t) {
+      const int ct = wave + 4 * t;
+      if (ct < CT) dqa[t] = mma16(bp, load_op<E>(&s_ekt[(16 * ct + mq) * EKR + kq]), dqa[t]);
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < TW; ++t) {
+    const int ct = wave + 4 * t;
+    if (ct >= CT) continue;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t n = n0 + 4 * (lane >> 4) + r;
+      if (n < a.N) dq[(sample0 + n) * a.qs + head * HD + 16 * ct + mq] = from_f32<E>(dqa[t][r]);
+    }
+  }
+}
+
+// dEK and dEV of the extra keys (attention.py:160-173): for one (sample,
+// head), dEK[g][c] = sum_n DS_e[n][g] q[n][c] and dEV[g][c] = sum_n PF_e[n][g]
+// dO[n][c] (blockIdx.z 0 / 1), DS_e = ds * scale and PF_e = p * dropout factor
+// of every (query, extra key) from the first backward kernel.  A workgroup
+// reduces `range` tokens (blockIdx.x) in chunks of 32 staged transposed in LDS
+// (32x32 MFMAs over 16 tokens at a time, keys x channels) and adds its fp32
+// partial into acc [B, G, D] with one atomic per element: a few tens of
+// partials per element in all.
+constexpr int kXChunk = 32;
+template <int HD, typename E>
+__global__ __launch_bounds__(256) void extra_grad_kernel(const E* __restrict__ ds_e,
+                                                         const E* __restrict__ pf_e,
+                                                         const E* __restrict__ q, int64_t qs,
+                                                         const E* __restrict__ dout, int64_t N,
+                                                         int nh, int G, int64_t range,
+                                                         float* __restrict__ dek_acc,
+                                                         float* __restrict__ dev_acc) {
+  constexpr int TR = kXChunk + (sizeof(E) == 2 ? 8 : 4);  // 16-byte aligned token rows
+  constexpr int MAXT = (kMaxExtra / 32) * (HD / 32) / 4;  // 32x32 tiles per wave at most
+  __shared__ __attribute__((aligned(16))) word_t<E> s_x[kMaxExtra * TR];  // X^T [key][token]
+  __shared__ __attribute__((aligned(16))) word_t<E> s_y[HD * TR];         // Y^T [channel][token]
+  const int bh = blockIdx.y, b = bh / nh, head = bh % nh;
+  const bool isv = blockIdx.z == 1;
+  const int D = nh * HD, Gp = (G + 31) & ~31;
+  const int MT = Gp / 32, NTL = HD / 32;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const E* const X = (isv ? pf_e : ds_e) + static_cast<int64_t>(bh) * N * G;
+  const E* const Y = isv ? dout + static_cast<int64_t>(b) * N * D : q + static_cast<int64_t>(b) * N * qs;
+  const int64_t ys = isv ? D : qs;
+  f32x16_t acc[MAXT];
+#pragma unroll
+  for (int i = 0; i < MAXT; ++i) acc[i] = f32x16_t{};
+  const int64_t n_begin = static_cast<int64_t>(blockIdx.x) * range;
+  const int64_t n_end = n_begin + range < N ? n_begin + range : N;
+  for (int64_t n0 = n_begin; n0 < n_end; n0 += kXChunk) {
+    __syncthreads();  // the previous chunk's MFMAs are done with the stages
+    // X rows of the chunk (keys g, 8 at a time) and Y rows (8 channels at a time),
+    // transposed; tokens past the range and keys past G read zero
+    for (int e = threadIdx.x; e < kXChunk * (Gp / 8); e += 256) {
+      const int tok = e / (Gp / 8), g8 = 8 * (e % (Gp / 8));
+      const int64_t n = n0 + tok;
+      float v[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        v[i] = (n < n_end && g8 + i < G) ? to_f32(X[n * G + g8 + i]) : 0.0f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        if constexpr (sizeof(E) == 2) s_x[(g8 + i) * TR + tok] = from_f32<bf16>(v[i]).bits;
+        else s_x[(g8 + i) * TR + tok] = v[i];
+      }
+    }
+    for (int e = threadIdx.x; e < kXChunk * (HD / 8); e += 256) {
+      const int tok = e / (HD / 8), c8 = 8 * (e % (HD / 8));
+      const int64_t n = n0 + tok;
+      op_t<E> x = zero_op<E>();
+      if (n < n_end) x = load_op<E>(Y + n * ys + head * HD + c8);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        if constexpr (sizeof(E) == 2) {
+          const u32x4_t xb = __builtin_bit_cast(u32x4_t, x);
+          s_y[(c8 + i) * TR + tok] =
+              static_cast<uint16_t>((i & 1) ? (xb[i / 2] >> 16) : (xb[i / 2] & 0xffffu));
+        } else {
+          s_y[(c8 + i) * TR + tok] = x[i];
+        }
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < MAXT; ++i) {
+      const int t = wave + 4 * i;
+      if (t >= MT * NTL) continue;
+      const int gb = t / NTL, cb = t % NTL;
+#pragma unroll
+      for (int ks = 0; ks < kXChunk; ks += 16) {
+        const int k0 = ks + 8 * (lane >> 5);
+        acc[i] = mma32(load_op<E>(&s_x[(32 * gb + (lane & 31)) * TR + k0]),
+                       load_op<E>(&s_y[(32 * cb + (lane & 31)) * TR + k0]), acc[i]);
+      }
+    }
+  }
+  // acc[i] register r: key 32 gb + 8 (r / 4) + 4 (lane / 32) + r % 4, channel 32 cb + lane % 32
+  float* const out = (isv ? dev_acc : dek_acc) + static_cast<int64_t>(b) * G * D + head * HD;
+#pragma unroll
+  for (int i = 0; i < MAXT; ++i) {
+    const int t = wave + 4 * i;
+    if (t >= MT * NTL) continue;
+    const int gb = t / NTL, cb = t % NTL;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int g = 32 * gb + 8 * (r / 4) + 4 * (lane >> 5) + (r % 4);
+      if (g < G && acc[i][r] != 0.0f)
+        atomicAdd(out + static_cast<int64_t>(g) * D + 32 * cb + (lane & 31), acc[i][r]);
     }
   }
 }
@@ -761,8 +1072,12 @@ __global__ __launch_bounds__(P2Tile<FR>::Threads) void dsa3d_bwd_p2_kernel(
 
 // Kernel arguments for a launch over `tiles` workgroups per head.
 tiled::Args make_tiled_args(const msd_dsa3d_desc& d, const void* q, const void* k, const void* v,
-                            const void* off, int64_t tiles) {
+                            const void* off, int64_t tiles, const void* ek = nullptr,
+                            const void* ev = nullptr) {
   tiled::Args a;
+  a.ek = ek;
+  a.ev = ev;
+  a.G = d.extra_g;
   a.q = q;
   a.k = k;
   a.v = v;
@@ -824,7 +1139,7 @@ bool tiled_head_dim(int hd) { return hd == 32 || hd == 64 || hd == 96 || hd == 1
 bool dsa3d_tiled_supported(const msd_dsa3d_desc& d, const void* q, const void* k, const void* v) {
   if ((d.dtype != MSD_BF16 && d.dtype != MSD_F32) || !tiled_head_dim(d.head_dim)) return false;
   const int64_t eb = d.dtype == MSD_BF16 ? 2 : 4;
-  if (d.kt * d.kh * d.kw > tiled::kMaxTaps) return false;
+  if (d.kt * d.kh * d.kw > tiled::kMaxTaps || d.extra_g > tiled::kMaxExtra) return false;
   if (d.T > 32767 || d.H > 32767 || d.W > 32767) return false;
   // the chunk grid of any corner box must number fewer than kMaxChunks
   const int64_t cy = (d.H + tiled::kChunkStep - 1) / tiled::kChunkStep + 1;
@@ -855,11 +1170,17 @@ hipError_t fwd_tiled_typed(const msd_dsa3d_desc& d, const tiled::Args& a, void* 
                            hipStream_t s) {
   const dim3 grid = tiled_grid<1>(d), block(tiled::kThreads);
   E* o = static_cast<E*>(out);
+  auto go = [&]<int HD>() {
+    if (a.G > 0)
+      hipLaunchKernelGGL((dsa3d_fwd_tiled_kernel<HD, E, true>), grid, block, 0, s, a, o, lse);
+    else
+      hipLaunchKernelGGL((dsa3d_fwd_tiled_kernel<HD, E, false>), grid, block, 0, s, a, o, lse);
+  };
   switch (d.head_dim) {
-    case 32: hipLaunchKernelGGL((dsa3d_fwd_tiled_kernel<32, E>), grid, block, 0, s, a, o, lse); break;
-    case 64: hipLaunchKernelGGL((dsa3d_fwd_tiled_kernel<64, E>), grid, block, 0, s, a, o, lse); break;
-    case 96: hipLaunchKernelGGL((dsa3d_fwd_tiled_kernel<96, E>), grid, block, 0, s, a, o, lse); break;
-    case 128: hipLaunchKernelGGL((dsa3d_fwd_tiled_kernel<128, E>), grid, block, 0, s, a, o, lse); break;
+    case 32: go.template operator()<32>(); break;
+    case 64: go.template operator()<64>(); break;
+    case 96: go.template operator()<96>(); break;
+    case 128: go.template operator()<128>(); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -867,9 +1188,9 @@ hipError_t fwd_tiled_typed(const msd_dsa3d_desc& d, const tiled::Args& a, void* 
 }  // namespace
 
 hipError_t launch_dsa3d_fwd_tiled(const msd_dsa3d_desc& d, const void* q, const void* k,
-                                  const void* v, const void* off, void* out, float* lse,
-                                  hipStream_t s) {
-  const tiled::Args a = make_tiled_args(d, q, k, v, off, tiled_tiles<1>(d));
+                                  const void* v, const void* off, const void* ek, const void* ev,
+                                  void* out, float* lse, hipStream_t s) {
+  const tiled::Args a = make_tiled_args(d, q, k, v, off, tiled_tiles<1>(d), ek, ev);
   if (d.dtype == MSD_BF16) return fwd_tiled_typed<bf16>(d, a, out, lse, s);
   return fwd_tiled_typed<float>(d, a, out, lse, s);
 }
@@ -895,19 +1216,43 @@ constexpr int p2_window() {
   return HD % 64 == 0 ? 64 : 32;
 }
 
+// Buffers of one tiled backward call (workspace carved by tiled_ws).
+template <typename E>
+struct BwdBufs {
+  float* p_ws;     // p * dropout factor per tap
+  float* b_ws;     // ds * softmax_scale per tap
+  float* dk_acc;   // dK / dV fp32 rows (the outputs for fp32 storage)
+  float* dv_acc;
+  int64_t acc_ks, acc_vs;
+  E* ds_e;         // extra keys: ds * scale and p * factor, [B, nh, N, G]
+  E* pf_e;
+  float* dek_acc;  // extra keys: dEK / dEV fp32 [B, G, D] (the outputs for fp32 storage)
+  float* dev_acc;
+};
+
 template <int HD, typename E>
 void launch_bwd_pair(const msd_dsa3d_desc& d, const void* q, const void* k, const void* v,
-                     const void* off, const E* o, const E* go, const float* lse,
-                     const float* dlse, E* gq, E* goff, float* p_ws, float* b_ws, float* dk_acc,
-                     float* dv_acc, int64_t acc_ks, int64_t acc_vs, hipStream_t s) {
+                     const void* off, const void* ek, const void* ev, const E* o, const E* go,
+                     const float* lse, const float* dlse, E* gq, E* goff, const BwdBufs<E>& w,
+                     hipStream_t s) {
   constexpr int CW = p2_window<HD, E>(), FR = p2_frames<HD, E>();
-  const tiled::Args a1 = make_tiled_args(d, q, k, v, off, tiled_tiles<1>(d));
-  const tiled::Args a2 = make_tiled_args(d, q, k, v, off, tiled_tiles<FR>(d));
+  const tiled::Args a1 = make_tiled_args(d, q, k, v, off, tiled_tiles<1>(d), ek, ev);
+  const tiled::Args a2 = make_tiled_args(d, q, k, v, off, tiled_tiles<FR>(d), ek, ev);
   const dim3 g1 = tiled_grid<1>(d);
   dim3 g2 = tiled_grid<FR>(d);
   g2.z = HD / CW;
+  float* const p_ws = w.p_ws;
+  float* const b_ws = w.b_ws;
+  float* const dk_acc = w.dk_acc;
+  float* const dv_acc = w.dv_acc;
+  const int64_t acc_ks = w.acc_ks, acc_vs = w.acc_vs;
   hipLaunchKernelGGL((dsa3d_bwd_p1_kernel<HD, E>), g1, dim3(tiled::kThreads), 0, s, a1, o, go,
                      lse, dlse, goff, p_ws, b_ws, dk_acc, dv_acc, acc_ks, acc_vs);
+  if (d.extra_g > 0) {
+    const dim3 gx(static_cast<unsigned>(d.B * ((a1.N + kXQ - 1) / kXQ)), d.num_heads);
+    hipLaunchKernelGGL((dsa3d_bwd_extra_kernel<HD, E>), gx, dim3(256), 0, s, a1, o, go, lse, dlse,
+                       gq, w.ds_e, w.pf_e);
+  }
   hipLaunchKernelGGL((dsa3d_bwd_p2_kernel<HD, CW, E, FR>), g2, dim3(P2Tile<FR>::Threads), 0, s,
                      a2, go, p_ws, b_ws, gq, dk_acc, dv_acc, acc_ks, acc_vs, 0);
   if constexpr (HD % CW != 0) {  // bf16 head_dim 96: a 64- and a 32-channel window
@@ -915,6 +1260,16 @@ void launch_bwd_pair(const msd_dsa3d_desc& d, const void* q, const void* k, cons
     hipLaunchKernelGGL((dsa3d_bwd_p2_kernel<HD, HD % CW, E, FR>), g2, dim3(P2Tile<FR>::Threads), 0,
                        s, a2, go, p_ws, b_ws, gq, dk_acc, dv_acc, acc_ks, acc_vs,
                        CW * (HD / CW));
+  }
+  if (d.extra_g > 0) {
+    // dEK, dEV: about 1,024 workgroups of token ranges that are multiples of 32
+    const int64_t N = static_cast<int64_t>(d.T) * d.H * d.W;
+    const int64_t parts = std::max<int64_t>(1, 1024 / (2 * int64_t{d.B} * d.num_heads));
+    const int64_t range = ((N + parts - 1) / parts + kXChunk - 1) / kXChunk * kXChunk;
+    const dim3 grid(static_cast<unsigned>((N + range - 1) / range), d.B * d.num_heads, 2);
+    hipLaunchKernelGGL((extra_grad_kernel<HD, E>), grid, dim3(256), 0, s, w.ds_e, w.pf_e,
+                       static_cast<const E*>(q), d.q_stride, go, N, d.num_heads, d.extra_g, range,
+                       w.dek_acc, w.dev_acc);
   }
 }
 
@@ -943,80 +1298,109 @@ __global__ __launch_bounds__(256) void acc_to_bf16_kernel(const float* __restric
   }
 }
 
+// Workspace layout of the tiled backward (byte offsets): the bf16 path's fp32
+// accumulators (dK/dV, then dEK/dEV; fp32 storage accumulates in its outputs),
+// p and ds * scale per tap, and with extra keys their ds * scale and p *
+// factor per (token, head, key) in the element type.
+struct TiledWs {
+  size_t acc, xacc, p, ds, dse, pfe, bytes;
+};
+
+TiledWs tiled_ws(const msd_dsa3d_desc& d) {
+  const size_t rows = static_cast<size_t>(d.B) * d.T * d.H * d.W;
+  const size_t D = static_cast<size_t>(d.num_heads) * d.head_dim;
+  const size_t taps = rows * d.num_heads * d.kt * d.kh * d.kw;
+  const size_t G = static_cast<size_t>(d.extra_g);
+  const bool bf = d.dtype == MSD_BF16;
+  const size_t e = bf ? 2 : 4;
+  auto up = [](size_t x) { return (x + 255) / 256 * 256; };
+  TiledWs w;
+  w.acc = 0;
+  w.xacc = w.acc + (bf ? 2 * rows * D * 4 : 0);
+  w.p = w.xacc + (bf ? 2 * static_cast<size_t>(d.B) * G * D * 4 : 0);
+  w.ds = w.p + taps * 4;
+  w.dse = up(w.ds + taps * 4);
+  w.pfe = up(w.dse + rows * d.num_heads * G * e);
+  w.bytes = w.pfe + rows * d.num_heads * G * e;
+  return w;
+}
+
 template <typename E>
 hipError_t bwd_tiled_typed(const msd_dsa3d_desc& d, const void* q, const void* k, const void* v,
-                           const void* off, const void* out, const void* dout, const float* lse,
-                           const float* dlse, void* dq, void* dk, void* dv, void* doff,
-                           float* p_ws, float* b_ws, float* acc, hipStream_t s) {
+                           const void* off, const void* ek, const void* ev, const void* out,
+                           const void* dout, const float* lse, const float* dlse, void* dq,
+                           void* dk, void* dv, void* doff, void* dek, void* dev, void* ws,
+                           hipStream_t s) {
   const int64_t rows = static_cast<int64_t>(d.B) * d.T * d.H * d.W;
   const int D = d.num_heads * d.head_dim;
+  const int64_t erows = static_cast<int64_t>(d.B) * d.extra_g;
   const auto* o = static_cast<const E*>(out);
   const auto* go = static_cast<const E*>(dout);
   auto* gq = static_cast<E*>(dq);
   auto* goff = static_cast<E*>(doff);
-  // dK and dV add up in fp32: in the outputs themselves for fp32 storage, in
-  // the workspace accumulator (converted once at the end) for bf16
+  char* const base = static_cast<char*>(ws);
+  const TiledWs L = tiled_ws(d);
+  // dK and dV (and dEK, dEV) add up in fp32: in the outputs themselves for
+  // fp32 storage, in workspace accumulators (converted once at the end) for bf16
   constexpr bool kInPlace = sizeof(E) == 4;
-  float* const dk_acc = kInPlace ? static_cast<float*>(dk) : acc;
-  float* const dv_acc = kInPlace ? static_cast<float*>(dv) : acc + rows * D;
-  const int64_t aks = kInPlace ? d.k_stride : D, avs = kInPlace ? d.v_stride : D;
+  BwdBufs<E> w;
+  w.p_ws = reinterpret_cast<float*>(base + L.p);
+  w.b_ws = reinterpret_cast<float*>(base + L.ds);
+  w.dk_acc = kInPlace ? static_cast<float*>(dk) : reinterpret_cast<float*>(base + L.acc);
+  w.dv_acc = kInPlace ? static_cast<float*>(dv) : w.dk_acc + rows * D;
+  w.acc_ks = kInPlace ? d.k_stride : D;
+  w.acc_vs = kInPlace ? d.v_stride : D;
+  w.ds_e = reinterpret_cast<E*>(base + L.dse);
+  w.pf_e = reinterpret_cast<E*>(base + L.pfe);
+  w.dek_acc = kInPlace ? static_cast<float*>(dek) : reinterpret_cast<float*>(base + L.xacc);
+  w.dev_acc = kInPlace ? static_cast<float*>(dev) : w.dek_acc + erows * D;
+  if (erows > 0) {
+    hipLaunchKernelGGL(fill_zero_f32, dim3(fill_blocks(erows * D)), dim3(256), 0, s, w.dek_acc,
+                       erows * D);
+    hipLaunchKernelGGL(fill_zero_f32, dim3(fill_blocks(erows * D)), dim3(256), 0, s, w.dev_acc,
+                       erows * D);
+  }
   switch (d.head_dim) {
-    case 32:
-      launch_bwd_pair<32, E>(d, q, k, v, off, o, go, lse, dlse, gq, goff, p_ws, b_ws, dk_acc,
-                               dv_acc, aks, avs, s);
-      break;
-    case 64:
-      launch_bwd_pair<64, E>(d, q, k, v, off, o, go, lse, dlse, gq, goff, p_ws, b_ws, dk_acc,
-                               dv_acc, aks, avs, s);
-      break;
-    case 96:
-      launch_bwd_pair<96, E>(d, q, k, v, off, o, go, lse, dlse, gq, goff, p_ws, b_ws, dk_acc,
-                               dv_acc, aks, avs, s);
-      break;
-    case 128:
-      launch_bwd_pair<128, E>(d, q, k, v, off, o, go, lse, dlse, gq, goff, p_ws, b_ws, dk_acc,
-                                dv_acc, aks, avs, s);
-      break;
-    default:
-      return hipErrorInvalidValue;
+    case 32: launch_bwd_pair<32, E>(d, q, k, v, off, ek, ev, o, go, lse, dlse, gq, goff, w, s); break;
+    case 64: launch_bwd_pair<64, E>(d, q, k, v, off, ek, ev, o, go, lse, dlse, gq, goff, w, s); break;
+    case 96: launch_bwd_pair<96, E>(d, q, k, v, off, ek, ev, o, go, lse, dlse, gq, goff, w, s); break;
+    case 128: launch_bwd_pair<128, E>(d, q, k, v, off, ek, ev, o, go, lse, dlse, gq, goff, w, s); break;
+    default: return hipErrorInvalidValue;
   }
   if constexpr (!kInPlace) {
     const dim3 cgrid(fill_blocks(rows * (D / 8)), 2);
-    hipLaunchKernelGGL(acc_to_bf16_kernel, cgrid, dim3(256), 0, s, dk_acc, dv_acc,
+    hipLaunchKernelGGL(acc_to_bf16_kernel, cgrid, dim3(256), 0, s, w.dk_acc, w.dv_acc,
                        static_cast<bf16*>(dk), static_cast<bf16*>(dv), rows, D, d.k_stride,
                        d.v_stride);
+    if (erows > 0) {
+      const dim3 egrid(fill_blocks(erows * (D / 8)), 2);
+      hipLaunchKernelGGL(acc_to_bf16_kernel, egrid, dim3(256), 0, s, w.dek_acc, w.dev_acc,
+                         static_cast<bf16*>(dek), static_cast<bf16*>(dev), erows, D,
+                         static_cast<int64_t>(D), static_cast<int64_t>(D));
+    }
   }
   return hipGetLastError();
 }
 }  // namespace
 
-// Workspace of the tiled backward: for bf16 the dK/dV fp32 accumulators
-// ([token][D] each; fp32 storage accumulates in its outputs), then p and
-// ds * softmax_scale of every tap (fp32 [token][head][tap] each).
+// Workspace of the tiled backward (the layout of tiled_ws).
 size_t dsa3d_tiled_bwd_ws_bytes(const msd_dsa3d_desc& d) {
   if ((d.dtype != MSD_BF16 && d.dtype != MSD_F32) || !tiled_head_dim(d.head_dim) ||
-      d.kt * d.kh * d.kw > tiled::kMaxTaps)
+      d.kt * d.kh * d.kw > tiled::kMaxTaps || d.extra_g > tiled::kMaxExtra)
     return 0;
-  const int64_t rows = static_cast<int64_t>(d.B) * d.T * d.H * d.W;
-  const int64_t acc = d.dtype == MSD_BF16 ? 2 * rows * d.num_heads * d.head_dim : 0;
-  return static_cast<size_t>(acc + 2 * rows * d.num_heads * d.kt * d.kh * d.kw) * sizeof(float);
+  return tiled_ws(d).bytes;
 }
 
 hipError_t launch_dsa3d_bwd_tiled(const msd_dsa3d_desc& d, const void* q, const void* k,
-                                  const void* v, const void* off, const void* out,
-                                  const void* dout, const float* lse, const float* dlse, void* dq,
-                                  void* dk, void* dv, void* doff, void* ws, hipStream_t s) {
-  const int64_t rows = static_cast<int64_t>(d.B) * d.T * d.H * d.W;
-  const int64_t taps = rows * d.num_heads * d.kt * d.kh * d.kw;
-  // accumulators first: rows * D floats keep p and ds 16-byte aligned
-  float* acc = static_cast<float*>(ws);
-  float* p_ws = acc + (d.dtype == MSD_BF16 ? 2 * rows * d.num_heads * d.head_dim : 0);
-  float* b_ws = p_ws + taps;
+                                  const void* v, const void* off, const void* ek, const void* ev,
+                                  const void* out, const void* dout, const float* lse,
+                                  const float* dlse, void* dq, void* dk, void* dv, void* doff,
+                                  void* dek, void* dev, void* ws, hipStream_t s) {
   if (d.dtype == MSD_BF16)
-    return bwd_tiled_typed<bf16>(d, q, k, v, off, out, dout, lse, dlse, dq, dk, dv, doff, p_ws,
-                                 b_ws, acc, s);
-  return bwd_tiled_typed<float>(d, q, k, v, off, out, dout, lse, dlse, dq, dk, dv, doff, p_ws,
-                                b_ws, acc, s);
+    return bwd_tiled_typed<bf16>(d, q, k, v, off, ek, ev, out, dout, lse, dlse, dq, dk, dv, doff,
+                                 dek, dev, ws, s);
+  return bwd_tiled_typed<float>(d, q, k, v, off, ek, ev, out, dout, lse, dlse, dq, dk, dv, doff,
+                                dek, dev, ws, s);
 }
 
 }  // namespace msd

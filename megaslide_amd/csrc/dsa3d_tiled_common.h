@@ -126,7 +126,12 @@ struct Args {
   float r_kw, r_khkw;            // 1/kw, 1/(kh*kw): exact small-integer division
   DropoutArgs drop;              // attention dropout on the softmax weights
   float fix_a, fix_a_inv;        // fixed-point scale of the A (= p w) tables and its inverse
+  const void* ek;                // extra keys / values [B, G, D] shared by every query
+  const void* ev;                //   (attention.py:160-173), tap K + g of each query
+  int G;                         // extra keys per sample (0 = none, at most kMaxExtra)
 };
+
+constexpr int kMaxExtra = 256;   // extra keys the tiled kernels take (a table row)
 
 // Geometry of one tap, kept in registers between the passes.
 struct Slot {
@@ -716,6 +721,67 @@ __device__ __forceinline__ op_t<E> fix_to_op(const int* p) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) r[i] = static_cast<float>(p[i]);
     return r;
+  }
+}
+
+// 8 floats -> MFMA operand (rounded to bf16 for bf16 storage).
+template <typename E>
+__device__ __forceinline__ op_t<E> f32_to_op(const float* p) {
+  if constexpr (sizeof(E) == 2) {
+    u32x4_t r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const f32x2_t f = {p[2 * i], p[2 * i + 1]};
+      r[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_t));
+    }
+    return __builtin_bit_cast(bf16x8_t, r);
+  } else {
+    f32x8_t r;
+    __builtin_memcpy(&r, p, sizeof(r));
+    return r;
+  }
+}
+
+// MFMA B operands of 16 extra-key rows (block eb of 16): y[c] holds channels
+// 32 c + 8 (lane / 16) + [0, 8) of extra key 16 eb + lane % 16 of the tile's
+// sample and head; rows past G are zero.
+template <int HD, typename E>
+__device__ __forceinline__ void load_extra_rows(const Args& a, const Tile& tl, const void* base,
+                                                int eb, op_t<E> (&y)[HD / 32]) {
+#pragma unroll
+  for (int c = 0; c < HD / 32; ++c) y[c] = zero_op<E>();
+  const int g = 16 * eb + (tl.lane & 15);
+  if (g >= a.G) return;
+  const int D = a.nh * HD;
+  const E* p = static_cast<const E*>(base) + (static_cast<int64_t>(tl.b) * a.G + g) * D +
+               tl.head * HD + 8 * (tl.lane >> 4);
+#pragma unroll
+  for (int c = 0; c < HD / 32; ++c) y[c] = load_op<E>(p + 32 * c);
+}
+
+// Extra-key rows (key or value) of the tile's head, channels [0, HD), keys
+// g0 + [0, ng) transposed into yt[channel][g - g0] (row stride `row`
+// elements), zero for keys past G: thread item e moves 8 channels of one key.
+template <int HD, typename E>
+__device__ __forceinline__ void stage_extra_t(const Args& a, const Tile& tl, const void* base,
+                                              int g0, int ng, int row, word_t<E>* yt, int nthreads) {
+  const int D = a.nh * HD;
+  for (int e = threadIdx.x; e < ng * (HD / 8); e += nthreads) {
+    const int gi = e / (HD / 8), cg = e % (HD / 8), g = g0 + gi;
+    op_t<E> x = zero_op<E>();
+    if (g < a.G)
+      x = load_op<E>(static_cast<const E*>(base) + (static_cast<int64_t>(tl.b) * a.G + g) * D +
+                     tl.head * HD + 8 * cg);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if constexpr (sizeof(E) == 2) {
+        const u32x4_t xb = __builtin_bit_cast(u32x4_t, x);
+        yt[(8 * cg + i) * row + gi] =
+            static_cast<uint16_t>((i & 1) ? (xb[i / 2] >> 16) : (xb[i / 2] & 0xffffu));
+      } else {
+        yt[(8 * cg + i) * row + gi] = x[i];
+      }
+    }
   }
 }
 

@@ -52,8 +52,8 @@ class _CoreCall:
     """Validated shapes of one attention-core call and its C descriptor."""
 
     def __init__(self, q, k, v, offsets, video_shape, num_heads, kernel_size, offset_scale, algo,
-                 dropout=(0.0, 0, 0)):
-        self.dev = _require_device(q, k, v, offsets)
+                 dropout=(0.0, 0, 0), extra_k=None, extra_v=None):
+        self.dev = _require_device(q, k, v, offsets, extra_k, extra_v)
         B, N, D = q.shape
         T, H, W = (int(s) for s in video_shape)
         if N != T * H * W:
@@ -84,6 +84,20 @@ class _CoreCall:
         if not 0.0 <= float(p) < 1.0:
             raise ValueError(f"dropout probability must be in [0, 1), got {p}")
         self.dropout = (float(p), int(seed) & 0xFFFFFFFFFFFFFFFF, int(offset) & 0xFFFFFFFF)
+        # extra keys / values shared by every query (attention.py:160-173)
+        if (extra_k is None) != (extra_v is None):
+            raise ValueError("extra_k and extra_v go together")
+        self.G = 0
+        self.ek = self.ev = None
+        if extra_k is not None:
+            G = extra_k.shape[1]
+            for name, t in (("extra_k", extra_k), ("extra_v", extra_v)):
+                if t.shape != (B, G, D):
+                    raise ValueError(f"{name} must be {(B, G, D)}, got {tuple(t.shape)}")
+                if t.dtype != dt:
+                    raise TypeError(f"dsa3d_core: {name} is {t.dtype}, q is {dt}")
+            self.G = G
+            self.ek, self.ev = extra_k.contiguous(), extra_v.contiguous()
 
     def desc(self, qs=None, ks=None, vs=None) -> _lib.DsaDesc:
         kt, kh, kw = self.ksz
@@ -94,7 +108,7 @@ class _CoreCall:
             self.k.stride(1) if ks is None else ks,
             self.v.stride(1) if vs is None else vs,
             self.offset_scale, 1.0 / math.sqrt(self.hd), _lib.ALGOS[self.algo],
-            self.dropout[2], self.dropout[1], self.dropout[0], 0)
+            self.dropout[2], self.dropout[1], self.dropout[0], self.G)
 
     def forward(self, want_lse: bool):
         out = torch.empty((self.B, self.N, self.D), dtype=self.dtype, device=self.dev)
@@ -104,28 +118,30 @@ class _CoreCall:
         lib = _lib.load()
         with torch.cuda.device(self.dev):
             _lib.check(lib.msd_dsa3d_fwd(ctypes.byref(desc), self.q.data_ptr(), self.k.data_ptr(),
-                                         self.v.data_ptr(), self.off.data_ptr(), out.data_ptr(),
-                                         _lib.ptr(lse), _lib.stream_handle(self.dev)), "dsa3d_fwd")
+                                         self.v.data_ptr(), self.off.data_ptr(), _lib.ptr(self.ek),
+                                         _lib.ptr(self.ev), out.data_ptr(), _lib.ptr(lse),
+                                         _lib.stream_handle(self.dev)), "dsa3d_fwd")
         return out, lse
 
 
 class DSA3DCoreFunction(torch.autograd.Function):
-    """out, lse = core(q, k, v, offsets); both outputs differentiable."""
+    """out, lse = core(q, k, v, offsets[, extra_k, extra_v]); both outputs differentiable."""
 
     @staticmethod
-    def forward(ctx, q, k, v, offsets, video_shape, num_heads, kernel_size, offset_scale, algo,
-                dropout):
+    def forward(ctx, q, k, v, offsets, extra_k, extra_v, video_shape, num_heads, kernel_size,
+                offset_scale, algo, dropout):
         call = _CoreCall(q, k, v, offsets, video_shape, num_heads, kernel_size, offset_scale, algo,
-                         dropout)
+                         dropout, extra_k, extra_v)
         out, lse = call.forward(want_lse=True)
         ctx.call = (call.B, call.T, call.H, call.W, call.nh, call.hd, call.ksz, call.dtype,
                     call.offset_scale, algo, call.dropout)
-        ctx.save_for_backward(call.q, call.k, call.v, call.off, out, lse)
+        ctx.has_extra = call.G > 0
+        ctx.save_for_backward(call.q, call.k, call.v, call.off, out, lse, call.ek, call.ev)
         return out, lse
 
     @staticmethod
     def backward(ctx, dout, dlse):
-        q, k, v, offsets, out, lse = ctx.saved_tensors
+        q, k, v, offsets, out, lse, ek, ev = ctx.saved_tensors
         B, T, H, W, nh, hd, ksz, dt, offset_scale, algo, dropout = ctx.call
         dev = q.device
         N, D = T * H * W, nh * hd
@@ -136,28 +152,33 @@ class DSA3DCoreFunction(torch.autograd.Function):
             dlse = dlse.to(torch.float32).contiguous()
         # gradients are written with the token strides of the desc: contiguous here
         qc, kc, vc = (t if t.stride(1) == D else t.contiguous() for t in (q, k, v))
-        call = _CoreCall(qc, kc, vc, offsets, (T, H, W), nh, ksz, offset_scale, algo, dropout)
+        call = _CoreCall(qc, kc, vc, offsets, (T, H, W), nh, ksz, offset_scale, algo, dropout,
+                         ek if ctx.has_extra else None, ev if ctx.has_extra else None)
         desc = call.desc(D, D, D)
         dq = torch.empty((B, N, D), dtype=dt, device=dev)
         dk = torch.empty((B, N, D), dtype=dt, device=dev)
         dv = torch.empty((B, N, D), dtype=dt, device=dev)
         doff = torch.empty_like(offsets)
+        dek = torch.empty_like(call.ek) if ctx.has_extra else None
+        dev_ = torch.empty_like(call.ev) if ctx.has_extra else None
         lib = _lib.load()
         ws_bytes = lib.msd_dsa3d_bwd_workspace_size(ctypes.byref(desc))
         ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
         with torch.cuda.device(dev):
             _lib.check(lib.msd_dsa3d_bwd(
                 ctypes.byref(desc), qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), offsets.data_ptr(),
-                out.data_ptr(), dout.data_ptr(), lse.data_ptr(), _lib.ptr(dlse),
-                dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), doff.data_ptr(),
-                ws.data_ptr(), ws_bytes, _lib.stream_handle(dev)), "dsa3d_bwd")
-        return dq, dk, dv, doff, None, None, None, None, None, None
+                _lib.ptr(call.ek), _lib.ptr(call.ev), out.data_ptr(), dout.data_ptr(),
+                lse.data_ptr(), _lib.ptr(dlse), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                doff.data_ptr(), _lib.ptr(dek), _lib.ptr(dev_), ws.data_ptr(), ws_bytes,
+                _lib.stream_handle(dev)), "dsa3d_bwd")
+        return dq, dk, dv, doff, dek, dev_, None, None, None, None, None, None
 
 
 def dsa3d_core(q: Tensor, k: Tensor, v: Tensor, offsets: Tensor, video_shape: Sequence[int],
                num_heads: int, kernel_size: Sequence[int] = (3, 7, 7), offset_scale: float = 1.0,
                return_lse: bool = False, algo: str = "auto", dropout_p: float = 0.0,
-               dropout_seed: Optional[int] = None, dropout_offset: int = 0):
+               dropout_seed: Optional[int] = None, dropout_offset: int = 0,
+               extra_k: Optional[Tensor] = None, extra_v: Optional[Tensor] = None):
     """Attention core on device tensors.
 
     q, k, v: [B, N, D]; offsets: [B, N, num_heads*kt*kh*kw*3] unscaled, channel
@@ -170,18 +191,25 @@ def dsa3d_core(q: Tensor, k: Tensor, v: Tensor, offsets: Tensor, video_shape: Se
     comes from Philox4x32-10 keyed by ``dropout_seed`` (drawn from torch's
     default CPU generator when None, so torch.manual_seed makes it repeatable);
     the backward reuses the forward's mask.
+
+    ``extra_k`` / ``extra_v`` ([B, G, D], already projected) are G keys and
+    values shared by every query, appended to its taps before the softmax
+    (the reference's ``extra_kv``, attention.py:160-173); extra key g is tap
+    K + g for dropout.
     """
     p = float(dropout_p)
     if p > 0.0 and dropout_seed is None:
         dropout_seed = int(torch.randint(0, 2**63 - 1, (1,), dtype=torch.int64).item())
     dropout = (p, 0 if dropout_seed is None else int(dropout_seed), int(dropout_offset))
-    if torch.is_grad_enabled() and any(t.requires_grad for t in (q, k, v, offsets)):
-        out, lse = DSA3DCoreFunction.apply(q, k, v, offsets, tuple(video_shape), int(num_heads),
-                                           tuple(kernel_size), float(offset_scale), algo, dropout)
+    grads = [t for t in (q, k, v, offsets, extra_k, extra_v) if t is not None]
+    if torch.is_grad_enabled() and any(t.requires_grad for t in grads):
+        out, lse = DSA3DCoreFunction.apply(q, k, v, offsets, extra_k, extra_v, tuple(video_shape),
+                                           int(num_heads), tuple(kernel_size), float(offset_scale),
+                                           algo, dropout)
         return (out, lse) if return_lse else out
     # forward only: nothing saved, no lse unless asked for
     call = _CoreCall(q, k, v, offsets, video_shape, num_heads, kernel_size, offset_scale, algo,
-                     dropout)
+                     dropout, extra_k, extra_v)
     out, lse = call.forward(want_lse=return_lse)
     return (out, lse) if return_lse else out
 

@@ -87,7 +87,8 @@ def _heads_volume(t: Tensor, B: int, T: int, H: int, W: int, nh: int, hd: int) -
 
 
 def _dropout_factors(dropout, B, N, Nq, nh, h0, h1, K, query_index, p) -> Tensor:
-    """[B, h1-h0, Nq, K(+G)] factors 0 or 1/(1-p) for the local taps (1 for extra keys)."""
+    """[B, h1-h0, Nq, K(+G)] factors 0 or 1/(1-p): tap k < K of the window, then
+    extra key g as tap K + g (the counter the kernels draw for it)."""
     import numpy as np
 
     from .philox import dropout_scale, keep_mask
@@ -96,12 +97,10 @@ def _dropout_factors(dropout, B, N, Nq, nh, h0, h1, K, query_index, p) -> Tensor
     n = (np.arange(Nq) if query_index is None
          else np.asarray(torch.as_tensor(query_index).cpu(), dtype=np.int64))
     rows = (np.arange(B, dtype=np.int64).reshape(B, 1) * N + n.reshape(1, -1)).reshape(-1)
-    keep = keep_mask(prob, seed, offset, rows, nh, K).reshape(B, Nq, nh, K)[:, :, h0:h1]
+    taps = p.shape[-1]
+    keep = keep_mask(prob, seed, offset, rows, nh, taps).reshape(B, Nq, nh, taps)[:, :, h0:h1]
     f = torch.from_numpy(np.where(keep, dropout_scale(prob), np.float32(0.0)).astype(np.float32))
-    f = f.permute(0, 2, 1, 3).to(p.dtype)
-    if p.shape[-1] > K:  # extra keys appended after the taps are not dropped here
-        f = torch.cat([f, torch.ones(*f.shape[:-1], p.shape[-1] - K, dtype=p.dtype)], dim=-1)
-    return f
+    return f.permute(0, 2, 1, 3).to(p.dtype)
 
 
 def dsa3d_core_ref(q: Tensor, k: Tensor, v: Tensor, off: Tensor,
@@ -133,7 +132,7 @@ def dsa3d_core_ref(q: Tensor, k: Tensor, v: Tensor, off: Tensor,
     ``dropout = (p, seed, offset)`` applies the reference's attention dropout
     (attention.py:180) to the local taps' softmax weights with the keep mask of
     ``oracle.philox.keep_mask`` (the generator the HIP kernels use) and the
-    fp32 scale 1 / (1 - p).  Extra keys are not dropped here.
+    fp32 scale 1 / (1 - p); extra key g is dropped as tap K + g.
     """
     B, N, D = q.shape
     T, H, W = video_shape

@@ -33,7 +33,7 @@ def test_exports_match_header():
 
 
 def test_abi_version():
-    assert _lib.load().msd_abi_version() == _lib.ABI_VERSION == 2
+    assert _lib.load().msd_abi_version() == _lib.ABI_VERSION == 3
 
 
 def _desc(**kw):
@@ -43,14 +43,15 @@ def _desc(**kw):
     return _lib.DsaDesc(**d)
 
 
-def _fwd(desc, ptrs=(16, 16, 16, 16, 16), lse=None):
+def _fwd(desc, ptrs=(16, 16, 16, 16, 16), lse=None, extra=(None, None)):
     lib = _lib.load()
-    return lib.msd_dsa3d_fwd(ctypes.byref(desc) if desc is not None else None, *ptrs, lse, None)
+    return lib.msd_dsa3d_fwd(ctypes.byref(desc) if desc is not None else None, *ptrs[:4], *extra,
+                             ptrs[4], lse, None)
 
 
 def test_null_desc_rejected():
     lib = _lib.load()
-    assert lib.msd_dsa3d_fwd(None, 16, 16, 16, 16, 16, None, None) == -1
+    assert lib.msd_dsa3d_fwd(None, 16, 16, 16, 16, None, None, 16, None, None) == -1
     assert b"desc is NULL" in lib.msd_last_error()
 
 
@@ -64,6 +65,8 @@ def test_null_desc_rejected():
     ("dropout_p", 1.0, -1, b"dropout_p"),
     ("dropout_p", -0.1, -1, b"dropout_p"),
     ("dropout_p", float("nan"), -1, b"dropout_p"),
+    ("extra_g", -1, -1, b"extra_g"),
+    ("extra_g", 5000, -1, b"extra_g"),
 ])
 def test_bad_desc_fields(field, value, code, needle):
     rc = _fwd(_desc(**{field: value}))
@@ -77,6 +80,12 @@ def test_null_and_misaligned_pointers():
     assert b"NULL" in lib.msd_last_error()
     assert _fwd(_desc(), ptrs=(16, 18, 16, 16, 16)) == -3  # fp32 needs 4-byte alignment
     assert _fwd(_desc(dtype=1), ptrs=(16, 17, 16, 16, 16)) == -3
+
+
+def test_extra_keys_need_their_pointers():
+    lib = _lib.load()
+    assert _fwd(_desc(extra_g=4)) == -1 and b"extra_k" in lib.msd_last_error()
+    assert _fwd(_desc(extra_g=4), extra=(16, 24)) == -3  # 16-byte aligned rows
 
 
 def test_empty_batch_is_a_no_op():
@@ -98,7 +107,8 @@ def test_workspace_size_and_check():
         d = _desc(B=2, dtype=dtype)
         need = lib.msd_dsa3d_bwd_workspace_size(ctypes.byref(d))
         assert need == want
-    rc = lib.msd_dsa3d_bwd(ctypes.byref(d), *([16] * 12), None, need - 1, None)
+    rc = lib.msd_dsa3d_bwd(ctypes.byref(d), *([16] * 4), None, None, *([16] * 3), None,
+                           *([16] * 4), None, None, 16, need - 1, None)
     assert rc == -4 and b"workspace" in lib.msd_last_error()
     assert lib.msd_dsa3d_bwd_workspace_size(None) == 0
 
@@ -137,5 +147,6 @@ def test_noalloc_scratch_limit_and_rejection():
     big = _desc(B=1, T=64, H=32, W=32, num_heads=16, dtype=1, q_stride=1024, k_stride=1024,
                 v_stride=1024)
     assert lib.msd_dsa3d_bwd_workspace_size(ctypes.byref(big)) > _lib.NOALLOC_SCRATCH_BYTES
-    rc = lib.msd_dsa3d_bwd_noalloc(ctypes.byref(big), *([16] * 7), None, *([16] * 4), None)
+    rc = lib.msd_dsa3d_bwd_noalloc(ctypes.byref(big), *([16] * 4), None, None, *([16] * 3), None,
+                                   *([16] * 4), None, None, None)
     assert rc == -4 and b"maximum" in lib.msd_last_error()

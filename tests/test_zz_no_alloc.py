@@ -45,14 +45,14 @@ def _both(shape, dtype, algo, seed):
     lse = torch.empty(B, N, nh, device=DEV, dtype=torch.float32)
     sh = torch.cuda.current_stream().cuda_stream
     P = lambda t: t.data_ptr()  # noqa: E731
-    _lib.check(lib.msd_dsa3d_fwd(ctypes.byref(desc), P(q), P(k), P(v), P(off), P(out), P(lse), sh),
-               "fwd")
+    _lib.check(lib.msd_dsa3d_fwd(ctypes.byref(desc), P(q), P(k), P(v), P(off), None, None, P(out),
+                                 P(lse), sh), "fwd")
     res = []
     ws = torch.empty(need, dtype=torch.uint8, device=DEV)
     for noalloc in (False, True):
         grads = [torch.full_like(t, float("nan")) for t in (q, k, v, off)]
-        args = [ctypes.byref(desc), P(q), P(k), P(v), P(off), P(out), P(dout), P(lse), None,
-                *(P(t) for t in grads)]
+        args = [ctypes.byref(desc), P(q), P(k), P(v), P(off), None, None, P(out), P(dout), P(lse),
+                None, *(P(t) for t in grads), None, None]
         if noalloc:
             rc = lib.msd_dsa3d_bwd_noalloc(*args, sh)
         else:
@@ -90,7 +90,7 @@ def test_noalloc_rejects_calls_beyond_its_scratch():
     desc = _lib.DsaDesc(1, 64, 32, 32, 16, 64, 3, 7, 7, _lib.MSD_BF16, 1024, 1024, 1024, 1.0, 0.125)
     x = torch.empty(16, dtype=torch.bfloat16, device=DEV)
     p = x.data_ptr()
-    rc = lib.msd_dsa3d_bwd_noalloc(ctypes.byref(desc), *([p] * 7), None, *([p] * 4),
-                                   torch.cuda.current_stream().cuda_stream)
+    rc = lib.msd_dsa3d_bwd_noalloc(ctypes.byref(desc), *([p] * 4), None, None, *([p] * 3), None,
+                                   *([p] * 4), None, None, torch.cuda.current_stream().cuda_stream)
     assert rc == -4
     assert b"maximum" in lib.msd_last_error()
