@@ -11,6 +11,16 @@ if GOLDEN not in sys.path:
     sys.path.insert(0, GOLDEN)
 
 
+@pytest.fixture(autouse=True)
+def _seed_global_generator():
+    """Every test starts from the same state of torch's global CPU generator
+    (otherwise seeded per process): default parameter initialisation and
+    unseeded draws repeat from run to run."""
+    import torch
+    torch.manual_seed(0)
+    yield
+
+
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs a ROCm GPU (MI355X) and the built HIP library")
 
