@@ -326,8 +326,8 @@ template <int HD, typename E>
 __global__ __launch_bounds__(kThreads, (p1_min_waves<HD, E>())) void dsa3d_bwd_p1_kernel(
     Args a, const E* __restrict__ out, const E* __restrict__ dout,
     const float* __restrict__ lse, const float* __restrict__ dlse, E* __restrict__ doff,
-    float* __restrict__ p_ws, float* __restrict__ b_ws, float* __restrict__ dk_acc,
-    float* __restrict__ dv_acc, int64_t acc_ks, int64_t acc_vs) {
+    float* __restrict__ p_ws, float* __restrict__ b_ws, void* __restrict__ dk_acc,
+    void* __restrict__ dv_acc, int64_t acc_ks, int64_t acc_vs) {
   // S and dP tables, double-buffered (one barrier per plane).  A buffer is
   // [S rows | zeros | dP rows | zeros]: a slot that misses the step reads the
   // zero block instead of its corners, so its values are 0 with no select, and
@@ -350,16 +350,18 @@ __global__ __launch_bounds__(kThreads, (p1_min_waves<HD, E>())) void dsa3d_bwd_p
   for (int e = threadIdx.x; e < 2 * 2 * kP1Zero; e += kThreads)
     s_tb[e / (2 * kP1Zero)][((e / kP1Zero) & 1) * kP1Tab + kTQ * kSRow + e % kP1Zero] = 0.0f;
   {
-    // The second kernel adds dK and dV into fp32 rows (the outputs for fp32
-    // storage, an accumulator for bf16): zero this tile's rows of the head first
-    // (the tiles of a launch partition the (token, head) pairs, and the second
-    // kernel starts after this one ends), 16 bytes a thread.
-    constexpr int CPR = HD / 4;
+    // The second kernel adds dK and dV into accumulator rows (the fp32 outputs
+    // for fp32 storage, fp16 rows for bf16): zero this tile's rows of the head
+    // first (the tiles of a launch partition the (token, head) pairs, and the
+    // second kernel starts after this one ends), 16 bytes a thread.
+    constexpr int AE = acc_bytes<E>();
+    constexpr int CPR = HD * AE / 16;
     for (int e = threadIdx.x; e < 2 * kTQ * CPR; e += kThreads) {
-      const int t = e / (kTQ * CPR), m = (e / CPR) % kTQ, ch = (e % CPR) * 4;
+      const int t = e / (kTQ * CPR), m = (e / CPR) % kTQ, ch = (e % CPR) * (16 / AE);
       const int64_t row = tile_row(a, tl, m);
       if (row < 0) continue;
-      float* dst = (t == 0 ? dk_acc + row * acc_ks : dv_acc + row * acc_vs) + tl.head * HD + ch;
+      const int64_t el = row * (t == 0 ? acc_ks : acc_vs) + tl.head * HD + ch;
+      char* dst = static_cast<char*>(t == 0 ? dk_acc : dv_acc) + el * AE;
       *reinterpret_cast<uint4*>(dst) = uint4{0u, 0u, 0u, 0u};
     }
   }
@@ -506,7 +508,6 @@ __global__ __launch_bounds__(kThreads, (p1_min_waves<HD, E>())) void dsa3d_bwd_p
     dp[1] = from_f32<E>((m & 2) ? (dss * gys[i] + pd * gyd[i]) * cys : 0.0f);
     dp[2] = from_f32<E>((m & 4) ? (dss * gzs[i] + pd * gzd[i]) * czs : 0.0f);
   }
-
 }
 
 // Second backward kernel: dq, dK and dV for tiles of FR consecutive frames
@@ -568,11 +569,51 @@ __device__ __forceinline__ void flush_block(const Tile& tl, const f32x16_t& x, c
   }
 }
 
-template <int HD, int CW, typename E, int FR>
-__global__ __launch_bounds__(P2Tile<FR>::Threads) void dsa3d_bwd_p2_kernel(
-    Args a, const E* __restrict__ dout, const float* __restrict__ p_ws,
-    const float* __restrict__ b_ws, E* __restrict__ dq, float* __restrict__ dk_acc,
-    float* __restrict__ dv_acc, int64_t acc_ks, int64_t acc_vs, int cw_base) {
+// The same block into fp16 rows, times `scale` (a power of two), with packed
+// two-channel atomics: lanes l and l ^ 1 hold adjacent channels of the same
+// voxels, and one swap gives the even lane both channels of voxel i and the
+// odd lane both of voxel i + 1, so one atomic carries two values (they run at
+// the rate of one fp32 atomic; 16 lanes cover 64 contiguous bytes of a row).
+// A sum beyond the fp16 range becomes infinite, which the conversion detects.
+__device__ __forceinline__ void flush_block_h16(const Tile& tl, const f32x16_t& x,
+                                                const int* s_rows, int vb, int nv, int ch,
+                                                void* acc, int64_t stride, float scale) {
+  typedef __attribute__((ext_vector_type(2))) _Float16 h2_t;
+  char* const base = static_cast<char*>(acc) + tl.sample0 * stride * 2;
+  const uint32_t st = static_cast<uint32_t>(stride);
+  const uint32_t che = static_cast<uint32_t>(ch & ~1);
+  const bool odd = tl.lane & 1;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int v0 = 32 * vb + 8 * g + 4 * (tl.lane >> 5);
+#pragma unroll
+    for (int i = 0; i < 4; i += 2) {
+      const float a0 = x[4 * g + i] * scale, a1 = x[4 * g + i + 1] * scale;
+      const float recv = __shfl_xor(odd ? a0 : a1, 1);
+      const float lo = odd ? recv : a0, hi = odd ? a1 : recv;
+      const int vi = v0 + i + (odd ? 1 : 0);
+      if (vi < nv && (lo != 0.0f || hi != 0.0f)) {
+        const h2_t pk = {static_cast<_Float16>(lo), static_cast<_Float16>(hi)};
+        __builtin_amdgcn_global_atomic_fadd_v2f16(
+            reinterpret_cast<h2_t*>(base + (static_cast<uint32_t>(s_rows[vi]) * st + che) * 2u),
+            pk);
+      }
+    }
+  }
+}
+
+// Accumulation modes of the second backward kernel: fp32 atomics (fp32
+// storage), scaled fp16 atomics (bf16 storage), and the fp32 redo of dK / dV
+// alone after an fp16 overflow (dq is already final then).
+enum P2Mode { kP2F32 = 0, kP2F16 = 1, kP2Redo = 2 };
+
+template <int HD, int CW, typename E, int FR, int MODE>
+__device__ __forceinline__ void p2_tile(const Args& a, int tile, const E* __restrict__ dout,
+                                        const float* __restrict__ p_ws,
+                                        const float* __restrict__ b_ws, E* __restrict__ dq,
+                                        void* __restrict__ dk_acc, void* __restrict__ dv_acc,
+                                        int64_t acc_ks, int64_t acc_vs, int cw_base,
+                                        const float* __restrict__ scales) {
   static_assert(CW <= HD && CW % 32 == 0, "channel windows are whole 32-channel blocks");
   using G = P2Tile<FR>;
   constexpr int kP2Frames = FR, kP2Q = G::Q, kP2Subs = G::Subs, kP2Slots = G::Slots;
@@ -592,7 +633,7 @@ __global__ __launch_bounds__(P2Tile<FR>::Threads) void dsa3d_bwd_p2_kernel(
   // the tile's q and dO rows of this window, transposed: [tensor][channel][query]
   __shared__ __attribute__((aligned(16))) word_t<E> s_qt[2][CW][QR];
 
-  const Tile tl = make_tile<kP2Frames, kP2Subs>(a);
+  const Tile tl = make_tile_at<kP2Frames, kP2Subs>(a, tile);
   const int D = a.nh * HD;
   // first channel of the window: cw_base + CW blockIdx.z within the head
   const int cw0 = tl.head * HD + cw_base + CW * static_cast<int>(blockIdx.z);
@@ -677,6 +718,9 @@ __global__ __launch_bounds__(P2Tile<FR>::Threads) void dsa3d_bwd_p2_kernel(
 #pragma unroll
   for (int j = 0; j < NDQ; ++j) dq_acc[j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
   const E* const kp = static_cast<const E*>(a.k);
+  // fp16 accumulation: the powers of two that scale the dK and dV partials
+  const float sc_k = MODE == kP2F16 ? scales[0] : 1.0f;
+  const float sc_v = MODE == kP2F16 ? scales[2] : 1.0f;
   // K rows of the next (plane, chunk) are loaded while the current one is used,
   // except with three frames, whose registers are too few to keep them live
   // across the step (the kernel is atomic-bound there anyway)
@@ -734,7 +778,8 @@ __global__ __launch_bounds__(P2Tile<FR>::Threads) void dsa3d_bwd_p2_kernel(
     __syncthreads();
     // dq[q] += sum_v B[q][v] K[v]; in bf16, B as a hi/lo pair because
     // sum_v B[q][v] = 0 and K may carry a large common part
-    if constexpr (DQK) {
+    if constexpr (MODE == kP2Redo) {
+    } else if constexpr (DQK) {
       const int fq = tl.wave / KPQ;
       for (int kc = 32 * (tl.wave % KPQ); kc < c.nvp; kc += 32 * KPQ) {
         float bq[8];  // fixed-point units; the query's scale is applied to dq at the end
@@ -774,18 +819,25 @@ __global__ __launch_bounds__(P2Tile<FR>::Threads) void dsa3d_bwd_p2_kernel(
       for (int f = 0; f < kP2Frames; ++f)
         acc = mma32(table_t_rows<E>(s_bt, kP2Row, kTQ * f, vb, tl.lane),
                     load_op<E>(&s_qt[0][och][kTQ * f + oq]), acc);
-      flush_block(tl, acc, s_rows, vb, c.nv, cw0 + och, dk_acc, acc_ks);
+      if constexpr (MODE == kP2F16)
+        flush_block_h16(tl, acc, s_rows, vb, c.nv, cw0 + och, dk_acc, acc_ks, sc_k);
+      else
+        flush_block(tl, acc, s_rows, vb, c.nv, cw0 + och, static_cast<float*>(dk_acc), acc_ks);
       acc = f32x16_t{};
 #pragma unroll
       for (int f = 0; f < kP2Frames; ++f)
         acc = mma32(table_t_rows<E>(s_at, kP2Row, kTQ * f, vb, tl.lane),
                     load_op<E>(&s_qt[1][och][kTQ * f + oq]), acc);
-      flush_block(tl, acc, s_rows, vb, c.nv, cw0 + och, dv_acc, acc_vs);
+      if constexpr (MODE == kP2F16)
+        flush_block_h16(tl, acc, s_rows, vb, c.nv, cw0 + och, dv_acc, acc_vs, sc_v);
+      else
+        flush_block(tl, acc, s_rows, vb, c.nv, cw0 + och, static_cast<float*>(dv_acc), acc_vs);
     }
     __syncthreads();
     w = wn;
   }
-  if constexpr (DQK) {
+  if constexpr (MODE == kP2Redo) {
+  } else if constexpr (DQK) {
     // dq_acc[ct][r] = partial dq[query 16*fq + 4*(lane/16) + r][channel 16*ct +
     // lane%16] of k phase w % 4; the A^T table (free after the loop's last
     // barrier) takes the partials, and every thread sums 4 for its outputs
@@ -827,6 +879,35 @@ __global__ __launch_bounds__(P2Tile<FR>::Threads) void dsa3d_bwd_p2_kernel(
         }
       }
     }
+  }
+}
+
+template <int HD, int CW, typename E, int FR, int MODE>
+__global__ __launch_bounds__(P2Tile<FR>::Threads) void dsa3d_bwd_p2_kernel(
+    Args a, const E* __restrict__ dout, const float* __restrict__ p_ws,
+    const float* __restrict__ b_ws, E* __restrict__ dq, void* __restrict__ dk_acc,
+    void* __restrict__ dv_acc, int64_t acc_ks, int64_t acc_vs, int cw_base,
+    const float* __restrict__ scales) {
+  p2_tile<HD, CW, E, FR, MODE>(a, blockIdx.x, dout, p_ws, b_ws, dq, dk_acc, dv_acc, acc_ks, acc_vs,
+                               cw_base, scales);
+}
+
+// dK / dV again with fp32 atomics, only when the fp16 accumulation overflowed
+// (*flag != 0; otherwise every workgroup returns at once): a small grid strides
+// over the tiles.
+template <int HD, int CW, typename E, int FR>
+__global__ __launch_bounds__(P2Tile<FR>::Threads) void dsa3d_bwd_p2_redo_kernel(
+    Args a, const E* __restrict__ dout, const float* __restrict__ p_ws,
+    const float* __restrict__ b_ws, float* __restrict__ dk_acc, float* __restrict__ dv_acc,
+    int64_t acc_ks, int64_t acc_vs, int cw_base, const int* __restrict__ flag, int tiles) {
+  if (*flag == 0) return;
+#pragma nounroll
+  for (int tile = blockIdx.x; tile < tiles; tile += gridDim.x) {
+    int t = tile;
+    asm volatile("" : "+s"(t));  // nothing of one tile is computed ahead for the next
+    p2_tile<HD, CW, E, FR, kP2Redo>(a, t, dout, p_ws, b_ws, nullptr, dk_acc, dv_acc, acc_ks,
+                                    acc_vs, cw_base, nullptr);
+    __syncthreads();  // the next tile rewrites the LDS tables
   }
 }
 
@@ -1195,6 +1276,151 @@ hipError_t launch_dsa3d_fwd_tiled(const msd_dsa3d_desc& d, const void* q, const 
   return fwd_tiled_typed<float>(d, a, out, lse, s);
 }
 
+// Largest power of two s with s * bound <= 2^14 (1 for a zero or non-finite
+// bound; at most 2^100).
+__device__ __forceinline__ float h16_pow2_scale(float bound) {
+  if (!(bound > 0.0f) || !__builtin_isfinite(bound)) return 1.0f;
+  int e;
+  frexpf(16384.0f / bound, &e);  // 16384 / bound = f 2^e, f in [0.5, 1)
+  return ldexpf(1.0f, min(e - 1, 100));
+}
+
+// Magnitudes behind the fp16 dK / dV accumulators' scales (bf16 storage): the
+// largest |q|, |dO|, |v| (extra values included) and |dlse| over an evenly
+// spread sample of at most about kBoundRows token rows (every row of a smaller
+// input), 16 bytes a thread.  Each block writes its maxima to part[blockIdx.x][4].
+constexpr int kBoundsBlocks = 256;
+constexpr int64_t kBoundRows = 4096;
+__global__ __launch_bounds__(256) void h16_bounds_kernel(
+    const bf16* __restrict__ q, int64_t qs, const bf16* __restrict__ dout,
+    const bf16* __restrict__ v, int64_t vs, const bf16* __restrict__ ev, int64_t erows,
+    const float* __restrict__ dlse, int64_t rows, int nh, int D, float* __restrict__ part) {
+  float m[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  const int64_t step = rows > kBoundRows ? rows / kBoundRows : 1;
+  const int64_t nsamp = (rows + step - 1) / step, d8 = D / 8;
+  auto maxabs8 = [](const void* p) {
+    const u32x4_t x = load16(p);
+    float r = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      r = fmaxf(r, fmaxf(fabsf(__uint_as_float(x[k] << 16)),
+                         fabsf(__uint_as_float(x[k] & 0xffff0000u))));
+    return r;
+  };
+  const int64_t n = nsamp * d8, stride = static_cast<int64_t>(gridDim.x) * 256;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n; i += stride) {
+    const int64_t j = i / d8, k = i - j * d8, c = 8 * k, r = j * step;
+    m[0] = fmaxf(m[0], maxabs8(q + r * qs + c));
+    m[1] = fmaxf(m[1], maxabs8(dout + r * D + c));
+    m[2] = fmaxf(m[2], maxabs8(v + r * vs + c));
+    // item k < nh of the row also reads head k's dlse (D / 8 >= nh)
+    if (dlse != nullptr && k < nh) m[3] = fmaxf(m[3], fabsf(dlse[r * nh + k]));
+  }
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < erows * d8; i += stride)
+    m[2] = fmaxf(m[2], maxabs8(ev + i * 8));
+  __shared__ float red[4][4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+#pragma unroll
+    for (int sh = 1; sh < 64; sh <<= 1) m[k] = fmaxf(m[k], __shfl_xor(m[k], sh));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6][k] = m[k];
+  }
+  __syncthreads();
+  if (threadIdx.x < 4)
+    part[blockIdx.x * 4 + threadIdx.x] =
+        fmaxf(fmaxf(red[0][threadIdx.x], red[1][threadIdx.x]),
+              fmaxf(red[2][threadIdx.x], red[3][threadIdx.x]));
+}
+
+// Scales of the fp16 dK / dV accumulators.  A voxel's dV sums p w dO over the
+// queries whose taps reach it, and each query's p w sum to at most the dropout
+// factor F: |dV| <= n F max|dO| for n such queries.  Its dK sums B q with
+// sum_v |B[q][v]| <= sum_k |ds_k scale| <= scale (2 F hd max|dO| max|v| +
+// |dlse_q|) (ds_k = p_k (f_k dO.v_k - Delta), v_k a convex combination of V
+// rows, |O| <= F max|v|, Cauchy-Schwarz over the head's hd channels), so |dK|
+// <= n max|q| times that.  Scaling by 2^14 / (kH16Reach bound) keeps every
+// partial sum below the fp16 limit (65504) for up to 4 kH16Reach queries' full
+// weight on one voxel.  A sum beyond it (more such queries, or maxima above
+// the sampled ones) overflows to infinity: the conversion flags it and dK /
+// dV are redone in fp32, so the scales only trade redo probability against
+// the values left below fp16's normal range.  They are powers of two
+// (unscaling is exact).  Also clears the flag.
+constexpr float kH16Reach = 1024.0f;
+__global__ __launch_bounds__(256) void h16_scales_kernel(const float* __restrict__ part, int nblk,
+                                                         float factor, float softmax_scale, int hd,
+                                                         float* __restrict__ scales,
+                                                         int* __restrict__ flag) {
+  float m[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int i = threadIdx.x; i < nblk; i += 256)
+#pragma unroll
+    for (int k = 0; k < 4; ++k) m[k] = fmaxf(m[k], part[4 * i + k]);
+  __shared__ float red[4][4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+#pragma unroll
+    for (int sh = 1; sh < 64; sh <<= 1) m[k] = fmaxf(m[k], __shfl_xor(m[k], sh));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6][k] = m[k];
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float r[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) r[k] = fmaxf(fmaxf(red[0][k], red[1][k]), fmaxf(red[2][k], red[3][k]));
+    const float l1 = softmax_scale * (2.0f * factor * static_cast<float>(hd) * r[1] * r[2] + r[3]);
+    const float sk = h16_pow2_scale(kH16Reach * l1 * r[0]);
+    const float sv = h16_pow2_scale(kH16Reach * factor * r[1]);
+    scales[0] = sk;
+    scales[1] = 1.0f / sk;
+    scales[2] = sv;
+    scales[3] = 1.0f / sv;
+    *flag = 0;
+  }
+}
+
+// fp16 dK (blockIdx.y 0) or dV (1) rows [rows, D] -> bf16 outputs with their
+// token strides, unscaled; a non-finite value (an fp16 overflow, or a
+// non-finite input) sets *flag.  8 channels per thread, grid-stride.
+__global__ __launch_bounds__(256) void h16_to_bf16_kernel(const _Float16* __restrict__ hk,
+                                                         const _Float16* __restrict__ hv,
+                                                         bf16* __restrict__ dk,
+                                                         bf16* __restrict__ dv, int64_t rows,
+                                                         int D, int64_t ks, int64_t vs,
+                                                         const float* __restrict__ scales,
+                                                         int* __restrict__ flag) {
+  typedef __attribute__((ext_vector_type(8))) _Float16 h8_t;
+  const int64_t d8 = D / 8, n = rows * d8;
+  const bool is_k = blockIdx.y == 0;
+  const _Float16* const src0 = is_k ? hk : hv;
+  bf16* const dst0 = is_k ? dk : dv;
+  const int64_t st = is_k ? ks : vs;
+  const float inv = scales[is_k ? 1 : 3];
+  bool bad = false;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t r = i / d8, c = 8 * (i - r * d8);
+    h8_t x;
+    __builtin_memcpy(&x, src0 + r * D + c, sizeof(x));
+    uint16_t h[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float f = static_cast<float>(x[j]);
+      bad |= !__builtin_isfinite(f);
+      h[j] = from_f32<bf16>(f * inv).bits;
+    }
+    __builtin_memcpy(dst0 + r * st + c, h, sizeof(h));
+  }
+  if (__builtin_amdgcn_ballot_w64(bad) != 0 && (threadIdx.x & 63) == 0) atomicOr(flag, 1);
+}
+
+// Zero n floats, only when *flag != 0.  Grid-stride.
+__global__ __launch_bounds__(256) void fill_zero_if_flag(float* __restrict__ p, int64_t n,
+                                                        const int* __restrict__ flag) {
+  if (*flag == 0) return;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x)
+    p[i] = 0.0f;
+}
+
 namespace {
 // Frames per tile of the second kernel: 3 for bf16 head_dim 64 and 128 (at
 // the 131,072-token hd-128 shape three frames in two 64-channel windows ran
@@ -1221,9 +1447,14 @@ template <typename E>
 struct BwdBufs {
   float* p_ws;     // p * dropout factor per tap
   float* b_ws;     // ds * softmax_scale per tap
-  float* dk_acc;   // dK / dV fp32 rows (the outputs for fp32 storage)
-  float* dv_acc;
+  void* dk_acc;    // dK / dV accumulator rows: the fp32 outputs (fp32 storage) or
+  void* dv_acc;    // scaled fp16 [rows, D] (bf16 storage)
   int64_t acc_ks, acc_vs;
+  float* dk32;     // bf16 storage: fp32 [rows, D] rows for the redo after an fp16
+  float* dv32;     // overflow (the same memory as the fp16 rows)
+  float* bounds;   // bf16 storage: per-block maxima behind the fp16 scales
+  float* scales;   // bf16 storage: sK, 1/sK, sV, 1/sV
+  int* flag;       // bf16 storage: fp16 overflow seen
   E* ds_e;         // extra keys: ds * scale and p * factor, [B, nh, N, G]
   E* pf_e;
   float* dek_acc;  // extra keys: dEK / dEV fp32 [B, G, D] (the outputs for fp32 storage)
@@ -1243,9 +1474,10 @@ void launch_bwd_pair(const msd_dsa3d_desc& d, const void* q, const void* k, cons
   g2.z = HD / CW;
   float* const p_ws = w.p_ws;
   float* const b_ws = w.b_ws;
-  float* const dk_acc = w.dk_acc;
-  float* const dv_acc = w.dv_acc;
+  void* const dk_acc = w.dk_acc;
+  void* const dv_acc = w.dv_acc;
   const int64_t acc_ks = w.acc_ks, acc_vs = w.acc_vs;
+  constexpr bool kH16 = acc_bytes<E>() == 2;
   hipLaunchKernelGGL((dsa3d_bwd_p1_kernel<HD, E>), g1, dim3(tiled::kThreads), 0, s, a1, o, go,
                      lse, dlse, goff, p_ws, b_ws, dk_acc, dv_acc, acc_ks, acc_vs);
   if (d.extra_g > 0) {
@@ -1253,13 +1485,23 @@ void launch_bwd_pair(const msd_dsa3d_desc& d, const void* q, const void* k, cons
     hipLaunchKernelGGL((dsa3d_bwd_extra_kernel<HD, E>), gx, dim3(256), 0, s, a1, o, go, lse, dlse,
                        gq, w.ds_e, w.pf_e);
   }
-  hipLaunchKernelGGL((dsa3d_bwd_p2_kernel<HD, CW, E, FR>), g2, dim3(P2Tile<FR>::Threads), 0, s,
-                     a2, go, p_ws, b_ws, gq, dk_acc, dv_acc, acc_ks, acc_vs, 0);
+  if constexpr (kH16) {
+    const float factor = a1.drop.threshold == 0 ? 1.0f : a1.drop.scale;
+    hipLaunchKernelGGL(h16_bounds_kernel, dim3(kBoundsBlocks), dim3(256), 0, s,
+                       static_cast<const bf16*>(q), d.q_stride, go, static_cast<const bf16*>(v),
+                       d.v_stride, static_cast<const bf16*>(ev), int64_t{d.B} * d.extra_g, dlse,
+                       static_cast<int64_t>(a1.N) * d.B, d.num_heads, d.num_heads * HD, w.bounds);
+    hipLaunchKernelGGL(h16_scales_kernel, dim3(1), dim3(256), 0, s, w.bounds, kBoundsBlocks,
+                       factor, d.softmax_scale, HD, w.scales, w.flag);
+  }
+  constexpr int MODE = kH16 ? kP2F16 : kP2F32;
+  hipLaunchKernelGGL((dsa3d_bwd_p2_kernel<HD, CW, E, FR, MODE>), g2, dim3(P2Tile<FR>::Threads), 0,
+                     s, a2, go, p_ws, b_ws, gq, dk_acc, dv_acc, acc_ks, acc_vs, 0, w.scales);
   if constexpr (HD % CW != 0) {  // bf16 head_dim 96: a 64- and a 32-channel window
     g2.z = 1;
-    hipLaunchKernelGGL((dsa3d_bwd_p2_kernel<HD, HD % CW, E, FR>), g2, dim3(P2Tile<FR>::Threads), 0,
-                       s, a2, go, p_ws, b_ws, gq, dk_acc, dv_acc, acc_ks, acc_vs,
-                       CW * (HD / CW));
+    hipLaunchKernelGGL((dsa3d_bwd_p2_kernel<HD, HD % CW, E, FR, MODE>), g2,
+                       dim3(P2Tile<FR>::Threads), 0, s, a2, go, p_ws, b_ws, gq, dk_acc, dv_acc,
+                       acc_ks, acc_vs, CW * (HD / CW), w.scales);
   }
   if (d.extra_g > 0) {
     // dEK, dEV: about 1,024 workgroups of token ranges that are multiples of 32
@@ -1273,14 +1515,44 @@ void launch_bwd_pair(const msd_dsa3d_desc& d, const void* q, const void* k, cons
   }
 }
 
+// bf16 storage, after an fp16 overflow: dK and dV again into zeroed fp32 rows
+// (every kernel returns at once without the flag).
+template <int HD, typename E>
+void launch_bwd_redo(const msd_dsa3d_desc& d, const void* q, const void* k, const void* v,
+                     const void* off, const void* ek, const void* ev, const E* go,
+                     const BwdBufs<E>& w, hipStream_t s) {
+  constexpr int CW = p2_window<HD, E>(), FR = p2_frames<HD, E>();
+  const int64_t tiles = tiled_tiles<FR>(d);
+  const tiled::Args a2 = make_tiled_args(d, q, k, v, off, tiles, ek, ev);
+  const int64_t rows = static_cast<int64_t>(d.B) * d.T * d.H * d.W;
+  const int64_t n = 2 * rows * d.num_heads * HD;  // dK then dV rows, contiguous
+  hipLaunchKernelGGL(fill_zero_if_flag, dim3(512), dim3(256), 0, s, w.dk32, n, w.flag);
+  // one workgroup per CU over all heads and windows; each strides over the tiles
+  const int per = std::max(1, 256 / (d.num_heads * (HD / CW + (HD % CW != 0 ? 1 : 0))));
+  dim3 g(static_cast<unsigned>(std::min<int64_t>(per, tiles)), d.num_heads, HD / CW);
+  hipLaunchKernelGGL((dsa3d_bwd_p2_redo_kernel<HD, CW, E, FR>), g, dim3(P2Tile<FR>::Threads), 0,
+                     s, a2, go, w.p_ws, w.b_ws, w.dk32, w.dv32, int64_t{d.num_heads} * HD,
+                     int64_t{d.num_heads} * HD, 0, w.flag, static_cast<int>(tiles));
+  if constexpr (HD % CW != 0) {
+    g.z = 1;
+    hipLaunchKernelGGL((dsa3d_bwd_p2_redo_kernel<HD, HD % CW, E, FR>), g,
+                       dim3(P2Tile<FR>::Threads), 0, s, a2, go, w.p_ws, w.b_ws, w.dk32, w.dv32,
+                       int64_t{d.num_heads} * HD, int64_t{d.num_heads} * HD, CW * (HD / CW), w.flag,
+                       static_cast<int>(tiles));
+  }
+}
+
 // fp32 dK (blockIdx.y 0) or dV (1) accumulator [rows, D] -> bf16 with the
 // output's token stride, 8 channels per thread (32-byte loads, 16-byte stores;
 // D and the strides are multiples of 8), grid-stride over 64-bit indices.
+// With `flag`, only when *flag != 0.
 __global__ __launch_bounds__(256) void acc_to_bf16_kernel(const float* __restrict__ dk_acc,
                                                          const float* __restrict__ dv_acc,
                                                          bf16* __restrict__ dk,
                                                          bf16* __restrict__ dv, int64_t rows,
-                                                         int D, int64_t ks, int64_t vs) {
+                                                         int D, int64_t ks, int64_t vs,
+                                                         const int* __restrict__ flag) {
+  if (flag != nullptr && *flag == 0) return;
   const int64_t d8 = D / 8, n = rows * d8;
   const bool is_k = blockIdx.y == 0;
   const float* const src0 = is_k ? dk_acc : dv_acc;
@@ -1302,8 +1574,13 @@ __global__ __launch_bounds__(256) void acc_to_bf16_kernel(const float* __restric
 // accumulators (dK/dV, then dEK/dEV; fp32 storage accumulates in its outputs),
 // p and ds * scale per tap, and with extra keys their ds * scale and p *
 // factor per (token, head, key) in the element type.
+// For bf16 storage the dK / dV region holds fp32 [2, rows, D] rows, whose first
+// half also serves as the fp16 [2, rows, D] accumulator (the fp32 rows are only
+// used, zeroed first, after that has been converted), and the bounds kernel's
+// per-block maxima, the two scales and their inverses and the overflow flag
+// follow the extra keys' buffers.
 struct TiledWs {
-  size_t acc, xacc, p, ds, dse, pfe, bytes;
+  size_t acc, xacc, p, ds, dse, pfe, stats, scales, bytes;
 };
 
 TiledWs tiled_ws(const msd_dsa3d_desc& d) {
@@ -1321,7 +1598,9 @@ TiledWs tiled_ws(const msd_dsa3d_desc& d) {
   w.ds = w.p + taps * 4;
   w.dse = up(w.ds + taps * 4);
   w.pfe = up(w.dse + rows * d.num_heads * G * e);
-  w.bytes = w.pfe + rows * d.num_heads * G * e;
+  w.stats = up(w.pfe + rows * d.num_heads * G * e);
+  w.scales = up(w.stats + (bf ? kBoundsBlocks * 4 * 4 : 0));
+  w.bytes = w.scales + (bf ? 32 : 0);
   return w;
 }
 
@@ -1340,16 +1619,22 @@ hipError_t bwd_tiled_typed(const msd_dsa3d_desc& d, const void* q, const void* k
   auto* goff = static_cast<E*>(doff);
   char* const base = static_cast<char*>(ws);
   const TiledWs L = tiled_ws(d);
-  // dK and dV (and dEK, dEV) add up in fp32: in the outputs themselves for
-  // fp32 storage, in workspace accumulators (converted once at the end) for bf16
+  // fp32 storage: dK and dV (and dEK, dEV) add up in the outputs themselves.
+  // bf16 storage: dK and dV in scaled fp16 rows (fp32 again if that
+  // overflows), dEK and dEV in fp32 accumulators, converted at the end.
   constexpr bool kInPlace = sizeof(E) == 4;
   BwdBufs<E> w;
   w.p_ws = reinterpret_cast<float*>(base + L.p);
   w.b_ws = reinterpret_cast<float*>(base + L.ds);
-  w.dk_acc = kInPlace ? static_cast<float*>(dk) : reinterpret_cast<float*>(base + L.acc);
-  w.dv_acc = kInPlace ? static_cast<float*>(dv) : w.dk_acc + rows * D;
+  w.dk32 = kInPlace ? nullptr : reinterpret_cast<float*>(base + L.acc);
+  w.dv32 = kInPlace ? nullptr : w.dk32 + rows * D;
+  w.dk_acc = kInPlace ? dk : static_cast<void*>(base + L.acc);
+  w.dv_acc = kInPlace ? dv : static_cast<void*>(base + L.acc + rows * D * 2);
   w.acc_ks = kInPlace ? d.k_stride : D;
   w.acc_vs = kInPlace ? d.v_stride : D;
+  w.bounds = kInPlace ? nullptr : reinterpret_cast<float*>(base + L.stats);
+  w.scales = kInPlace ? nullptr : reinterpret_cast<float*>(base + L.scales);
+  w.flag = kInPlace ? nullptr : reinterpret_cast<int*>(base + L.scales + 16);
   w.ds_e = reinterpret_cast<E*>(base + L.dse);
   w.pf_e = reinterpret_cast<E*>(base + L.pfe);
   w.dek_acc = kInPlace ? static_cast<float*>(dek) : reinterpret_cast<float*>(base + L.xacc);
@@ -1369,14 +1654,27 @@ hipError_t bwd_tiled_typed(const msd_dsa3d_desc& d, const void* q, const void* k
   }
   if constexpr (!kInPlace) {
     const dim3 cgrid(fill_blocks(rows * (D / 8)), 2);
-    hipLaunchKernelGGL(acc_to_bf16_kernel, cgrid, dim3(256), 0, s, w.dk_acc, w.dv_acc,
+    hipLaunchKernelGGL(h16_to_bf16_kernel, cgrid, dim3(256), 0, s,
+                       static_cast<const _Float16*>(w.dk_acc), static_cast<const _Float16*>(w.dv_acc),
                        static_cast<bf16*>(dk), static_cast<bf16*>(dv), rows, D, d.k_stride,
-                       d.v_stride);
+                       d.v_stride, w.scales, w.flag);
+    // after an fp16 overflow (flag set): dK and dV again in fp32
+    switch (d.head_dim) {
+      case 32: launch_bwd_redo<32, E>(d, q, k, v, off, ek, ev, go, w, s); break;
+      case 64: launch_bwd_redo<64, E>(d, q, k, v, off, ek, ev, go, w, s); break;
+      case 96: launch_bwd_redo<96, E>(d, q, k, v, off, ek, ev, go, w, s); break;
+      default: launch_bwd_redo<128, E>(d, q, k, v, off, ek, ev, go, w, s); break;
+    }
+    // grid-stride: a small grid keeps the launch cheap when there is nothing to do
+    hipLaunchKernelGGL(acc_to_bf16_kernel, dim3(std::min(cgrid.x, 1024u), 2), dim3(256), 0, s,
+                       w.dk32, w.dv32, static_cast<bf16*>(dk), static_cast<bf16*>(dv), rows, D,
+                       d.k_stride, d.v_stride, static_cast<const int*>(w.flag));
     if (erows > 0) {
       const dim3 egrid(fill_blocks(erows * (D / 8)), 2);
       hipLaunchKernelGGL(acc_to_bf16_kernel, egrid, dim3(256), 0, s, w.dek_acc, w.dev_acc,
                          static_cast<bf16*>(dek), static_cast<bf16*>(dev), erows, D,
-                         static_cast<int64_t>(D), static_cast<int64_t>(D));
+                         static_cast<int64_t>(D), static_cast<int64_t>(D),
+                         static_cast<const int*>(nullptr));
     }
   }
   return hipGetLastError();

@@ -80,6 +80,30 @@ __device__ __forceinline__ op_t<E> zero_op() {
   }
 }
 
+// Bytes of one dK / dV accumulator element of the tiled backward: fp16 for
+// bf16 storage (scaled per call, packed-pair atomics), fp32 otherwise.
+template <typename E>
+constexpr int acc_bytes() {
+  return sizeof(E) == 2 ? 2 : 4;
+}
+
+// Largest |x| of an 8-element operand (a NaN element is passed over).
+template <typename E>
+__device__ __forceinline__ float max_abs_op(const op_t<E>& x) {
+  float m = 0.0f;
+  if constexpr (sizeof(E) == 2) {
+    const u32x4_t b = __builtin_bit_cast(u32x4_t, x);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      m = fmaxf(m, fmaxf(fabsf(__uint_as_float(b[i] << 16)),
+                         fabsf(__uint_as_float(b[i] & 0xffff0000u))));
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(x[j]));
+  }
+  return m;
+}
+
 // 8 consecutive elements (16 or 32 bytes) from global memory or LDS.
 template <typename E, typename P>
 __device__ __forceinline__ op_t<E> load_op(const P* p) {
@@ -177,15 +201,15 @@ inline int64_t tile_count(int B, int T, int H, int W) {
          ((W + kTileW - 1) / kTileW);
 }
 
+// Tile `tile` of head blockIdx.y.
 template <int FRAMES, int SUBS>
-__device__ __forceinline__ Tile make_tile(const Args& a) {
+__device__ __forceinline__ Tile make_tile_at(const Args& a, int tile) {
   Tile t;
   t.head = blockIdx.y;
   // Workgroups are dispatched round-robin over the 8 XCDs; give each XCD a
   // contiguous run of tiles so neighbouring tiles share its L2.  Frames vary
   // fastest: consecutive tiles of one (h, w) column read and accumulate into
   // nearly the same K/V planes.
-  int tile = blockIdx.x;
   if (a.xcd_remap > 0) tile = (tile & 7) * a.xcd_remap + (tile >> 3);
   const int groups = (a.T + FRAMES - 1) / FRAMES;
   t.t0 = (tile % groups) * FRAMES;
@@ -208,6 +232,11 @@ __device__ __forceinline__ Tile make_tile(const Args& a) {
   t.q_ok = t.t < a.T && t.qh < a.H && t.qw < a.W;
   t.qn = t.sample0 + (static_cast<int64_t>(t.t) * a.H + t.qh) * a.W + t.qw;
   return t;
+}
+
+template <int FRAMES, int SUBS>
+__device__ __forceinline__ Tile make_tile(const Args& a) {
+  return make_tile_at<FRAMES, SUBS>(a, blockIdx.x);
 }
 
 // Token row of group query m (frame m / 16, position m % 16), or -1 outside the grid.

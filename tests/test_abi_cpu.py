@@ -101,9 +101,13 @@ def test_workspace_size_and_check():
     # head_dim 64: the tiled backward keeps p and ds of every tap (fp32); fp32
     # storage adds dK/dV up in its outputs (the direct kernels' accumulators
     # are less than p and ds, and the larger of the two is asked for), bf16 in
-    # fp32 accumulators beside p and ds
+    # fp32 rows (which also hold the fp16 accumulators) beside p and ds, then
+    # the scale bounds (4 floats from each of 256 blocks) and 32 bytes of
+    # scales and overflow flag
     taps = 2 * rows * 2 * 147 * 4
-    for dtype, want in ((0, max(2 * rows * 128 * 4, taps)), (1, 2 * rows * 128 * 4 + taps)):
+    records = 256 * 4 * 4
+    for dtype, want in ((0, max(2 * rows * 128 * 4, taps)),
+                        (1, 2 * rows * 128 * 4 + taps + records + 32)):
         d = _desc(B=2, dtype=dtype)
         need = lib.msd_dsa3d_bwd_workspace_size(ctypes.byref(d))
         assert need == want
