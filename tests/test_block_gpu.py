@@ -233,3 +233,94 @@ def test_block_bf16_dit_shape_checkpointed():
             assert (b.float() - a.float()).abs().max().item() < 1e-2 * kw, n
         else:
             assert rel_err(b.float().cpu(), a.float().cpu(), floor=1e-3) < 1e-2, n
+
+
+def test_block_bf16_dit_shape_sampled_rows_match_oracle():
+    """The 46,800-token bf16 block (16 heads x 96, offset biases ~ U(-4, 4)
+    voxels) against a float32 reference on 32 sampled tokens: y there, and for
+    an upstream gradient that is zero except at those tokens, dx and every
+    parameter gradient (the sampled tokens alone feed them).
+
+    The reference is the same block in fp32 PyTorch (LayerNorms, GEMMs,
+    depthwise conv3d, GELU) on the bf16-rounded parameters and input, with the
+    attention core from the oracle restricted to the sampled queries
+    (query_index: exact for them, K and V over the whole volume).  Sampling is
+    piecewise linear in the offsets, so the core samples at the offsets the
+    bf16 module used, and the offset gradient it returns is chained through
+    the reference's own fp32 offset net.
+    """
+    from megaslide_amd import dwconv3d
+    from oracle.dsa3d_ref import dsa3d_core_ref
+    B, T, H, W, D, nh, ks = 1, 13, 45, 80, 1536, 16, (3, 7, 7)
+    N = T * H * W
+    print("[block bf16 46800 tokens 16x96] sampled rows vs oracle", flush=True)
+    g = torch.Generator().manual_seed(5)
+    blk = _make_block(5, D, nh, ks)
+    _randomise(blk, g, off_bias=4.0)
+    blk = blk.to(DEV, torch.bfloat16)
+    x = torch.randn(B, N, D, generator=g).to(DEV, torch.bfloat16)
+    gy = torch.randn(B, N, D, generator=g).to(DEV, torch.bfloat16)
+    idx = torch.cat([torch.tensor([0, N - 1]),
+                     torch.randperm(N - 2, generator=torch.Generator().manual_seed(9))[:30] + 1])
+    idx_d = idx.to(DEV)
+    gs = torch.zeros_like(gy)
+    gs[:, idx_d] = gy[:, idx_d]
+
+    # the module
+    xi = x.clone().requires_grad_(True)
+    y = blk(xi, (T, H, W))
+    names = [n for n, _ in blk.named_parameters()]
+    grads = torch.autograd.grad(y, (xi, *blk.parameters()), grad_outputs=gs)
+    with torch.no_grad():  # the offsets it sampled at (same kernels, same bits)
+        a = blk.norm1(x)
+        on0, on2 = blk.attn.offset_net[0], blk.attn.offset_net[2]
+        feat = dwconv3d(a, on0.weight, on0.bias, (T, H, W), act="gelu")
+        off_mod = F.linear(feat, on2.weight.view(on2.weight.shape[0], -1), on2.bias)
+    torch.cuda.synchronize()
+
+    # the reference, fp32
+    P = {n: prm.detach().float().clone().requires_grad_(True) for n, prm in blk.named_parameters()}
+    xr = x.float().clone().requires_grad_(True)
+
+    def vol(t):  # [B, N, D] -> [B, D, T, H, W]
+        return t.transpose(1, 2).reshape(B, D, T, H, W)
+
+    def tok(t):  # back
+        return t.reshape(B, D, N).transpose(1, 2)
+
+    ar = F.layer_norm(xr, (D,), P["norm1.weight"], P["norm1.bias"], eps=1e-6)
+    dw = tok(F.conv3d(vol(ar), P["attn.dw_conv.weight"], P["attn.dw_conv.bias"],
+                      padding=(ks[0] // 2, ks[1] // 2, ks[2] // 2), groups=D))
+    feat_r = F.gelu(tok(F.conv3d(vol(ar), P["attn.offset_net.0.weight"],
+                                 P["attn.offset_net.0.bias"], padding=1, groups=D)))
+    w2 = P["attn.offset_net.2.weight"]
+    off_r = F.linear(feat_r, w2.view(w2.shape[0], -1), P["attn.offset_net.2.bias"])
+    q_r = F.linear(ar, P["attn.q_proj.weight"], P["attn.q_proj.bias"])
+    k_r = F.linear(ar, P["attn.k_proj.weight"], P["attn.k_proj.bias"])
+    v_r = F.linear(ar, P["attn.v_proj.weight"], P["attn.v_proj.bias"])
+    qc, kc, vc = (t.detach().cpu().requires_grad_(True) for t in (q_r, k_r, v_r))
+    offc = off_mod.detach().float().cpu().requires_grad_(True)
+    attn = dsa3d_core_ref(qc, kc, vc, offc, (T, H, W), nh, ks, 1.0, head_chunk=4,
+                          query_index=idx).to(DEV)
+    o = F.linear(attn, P["attn.out_proj.weight"], P["attn.out_proj.bias"]) + dw[:, idx_d]
+    x1 = xr[:, idx_d] + o
+    h = F.gelu(F.linear(F.layer_norm(x1, (D,), P["norm2.weight"], P["norm2.bias"], eps=1e-6),
+                        P["fc1.weight"], P["fc1.bias"]))
+    y_r = x1 + F.linear(h, P["fc2.weight"], P["fc2.bias"])
+    y_r.backward(gy[:, idx_d].float(), retain_graph=True)
+    torch.autograd.backward([q_r, k_r, v_r, off_r],
+                            [t.grad.to(DEV) for t in (qc, kc, vc, offc)])
+    torch.cuda.synchronize()
+
+    errs = {"y": rel_err(y.detach()[:, idx_d].float().cpu(), y_r.detach().cpu()),
+            "dx": rel_err(grads[0].float().cpu(), xr.grad.cpu())}
+    for n, gr in zip(names, grads[1:]):
+        if n == "attn.k_proj.bias":  # zero by the softmax's shift invariance
+            continue
+        errs[n] = rel_err(gr.float().cpu(), P[n].grad.cpu(), floor=1e-2)
+    worst = max(errs, key=errs.get)
+    print(f"  max rel err {errs[worst]:.2e} ({worst}); y {errs['y']:.1e} dx {errs['dx']:.1e}",
+          flush=True)
+    bad = {k: v for k, v in errs.items() if not v < 2e-2}
+    assert not bad, bad
+
