@@ -224,6 +224,7 @@ def run_gpu(cfg, steps, warmup, calibrate=False):
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     doff = torch.empty_like(off)
     dx3, dx7 = torch.empty_like(x), torch.empty_like(x)
+    Z = torch.empty_like(x)  # the GELU conv's pre-activation, kept for its backward
     dw3, db3, dw7, db7 = (torch.empty_like(t) for t in (w3, b3, w7, b7))
 
     G = cfg.get("extra_g", 0)
@@ -248,8 +249,10 @@ def run_gpu(cfg, steps, warmup, calibrate=False):
     PX = lambda t: None if t is None else t.data_ptr()  # noqa: E731
 
     phases = [
-        ("dwconv7_fwd", lambda: lib.msd_dwconv3d_fwd(ctypes.byref(cv7), P(x), P(w7), P(b7), P(y7), sh)),
-        ("dwconv3_gelu_fwd", lambda: lib.msd_dwconv3d_fwd(ctypes.byref(cv3), P(x), P(w3), P(b3), P(F), sh)),
+        ("dwconv7_fwd", lambda: lib.msd_dwconv3d_fwd(ctypes.byref(cv7), P(x), P(w7), P(b7), P(y7), None,
+                                                     sh)),
+        ("dwconv3_gelu_fwd", lambda: lib.msd_dwconv3d_fwd(ctypes.byref(cv3), P(x), P(w3), P(b3), P(F),
+                                                          P(Z) if cfg["backward"] else None, sh)),
         ("dsa3d_fwd", lambda: lib.msd_dsa3d_fwd(ctypes.byref(dsa), P(q), P(k), P(v), P(off),
                                                 PX(ek), PX(ev), P(out), P(lse), sh)),
     ]
@@ -259,10 +262,12 @@ def run_gpu(cfg, steps, warmup, calibrate=False):
                                                     PX(ek), PX(ev), P(out), P(dout), P(lse), None,
                                                     P(dq), P(dk), P(dv), P(doff), PX(dek), PX(dev_),
                                                     P(ws_dsa), ws_dsa.numel(), sh)),
-            ("dwconv3_gelu_bwd", lambda: lib.msd_dwconv3d_bwd(ctypes.byref(cv3), P(x), P(w3), P(b3), P(dF),
-                                                              P(dx3), P(dw3), P(db3), P(ws3), ws3.numel(), sh)),
-            ("dwconv7_bwd", lambda: lib.msd_dwconv3d_bwd(ctypes.byref(cv7), P(x), P(w7), P(b7), P(dY),
-                                                         P(dx7), P(dw7), P(db7), P(ws7), ws7.numel(), sh)),
+            ("dwconv3_gelu_bwd", lambda: lib.msd_dwconv3d_bwd(ctypes.byref(cv3), P(x), P(w3), P(b3), P(Z),
+                                                              P(dF), P(dx3), P(dw3), P(db3), P(ws3),
+                                                              ws3.numel(), sh)),
+            ("dwconv7_bwd", lambda: lib.msd_dwconv3d_bwd(ctypes.byref(cv7), P(x), P(w7), P(b7), None,
+                                                         P(dY), P(dx7), P(dw7), P(db7), P(ws7),
+                                                         ws7.numel(), sh)),
         ]
 
     def step(events=None):

@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define MSD_ABI_VERSION 3
+#define MSD_ABI_VERSION 4
 
 typedef enum msd_dtype { MSD_F32 = 0, MSD_BF16 = 1 } msd_dtype;
 
@@ -171,21 +171,26 @@ int msd_dsa3d_bwd_noalloc(const msd_dsa3d_desc* desc, const void* q, const void*
  * padding=k//2, groups=C) (attention.py:58-65) and, with act = 1, the
  * offset_net[0:2] pair Conv3d(3, groups=C) + GELU (attention.py:71-72).
  * weight [C, kt*kh*kw] (nn.Conv3d's [C, 1, kt, kh, kw]); bias [C] or NULL.
+ * preact (act = 1 only, may be NULL): also receives the GELU input, the
+ * tensor nn.GELU's autograd keeps, for msd_dwconv3d_bwd.
  */
 int msd_dwconv3d_fwd(const msd_dwconv3d_desc* desc, const void* x, const void* weight,
-                     const void* bias, void* y, void* stream);
+                     const void* bias, void* y, void* preact, void* stream);
 
 /* Bytes of device workspace msd_dwconv3d_bwd needs for `desc`. */
 size_t msd_dwconv3d_bwd_workspace_size(const msd_dwconv3d_desc* desc);
 
 /*
- * Backward of msd_dwconv3d_fwd (conv3d input/weight backward, GELU backward
- * from the recomputed pre-activation).  dx, dweight, dbias may each be NULL
- * when not wanted; dx is written, not accumulated.
+ * Backward of msd_dwconv3d_fwd (conv3d input/weight backward, GELU backward).
+ * With act = 1 the GELU gradient uses preact, the forward's saved GELU input,
+ * or, when preact is NULL, recomputes it (one more convolution).  dx,
+ * dweight, dbias may each be NULL when not wanted; dx is written, not
+ * accumulated.
  */
 int msd_dwconv3d_bwd(const msd_dwconv3d_desc* desc, const void* x, const void* weight,
-                     const void* bias, const void* dy, void* dx, void* dweight, void* dbias,
-                     void* workspace, size_t workspace_bytes, void* stream);
+                     const void* bias, const void* preact, const void* dy, void* dx,
+                     void* dweight, void* dbias, void* workspace, size_t workspace_bytes,
+                     void* stream);
 
 #ifdef __cplusplus
 }

@@ -16,7 +16,7 @@ import threading
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libmegaslide_dsa3d.so")
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 MSD_F32 = 0
 MSD_BF16 = 1
@@ -99,11 +99,11 @@ def load() -> ctypes.CDLL:
         lib.msd_dsa3d_bwd_noalloc.restype = ctypes.c_int
         lib.msd_dsa3d_bwd_noalloc.argtypes = [ctypes.POINTER(DsaDesc)] + [_vp] * 17
         lib.msd_dwconv3d_fwd.restype = ctypes.c_int
-        lib.msd_dwconv3d_fwd.argtypes = [ctypes.POINTER(ConvDesc), _vp, _vp, _vp, _vp, _vp]
+        lib.msd_dwconv3d_fwd.argtypes = [ctypes.POINTER(ConvDesc)] + [_vp] * 6
         lib.msd_dwconv3d_bwd_workspace_size.restype = ctypes.c_size_t
         lib.msd_dwconv3d_bwd_workspace_size.argtypes = [ctypes.POINTER(ConvDesc)]
         lib.msd_dwconv3d_bwd.restype = ctypes.c_int
-        lib.msd_dwconv3d_bwd.argtypes = [ctypes.POINTER(ConvDesc)] + [_vp] * 8 + [ctypes.c_size_t, _vp]
+        lib.msd_dwconv3d_bwd.argtypes = [ctypes.POINTER(ConvDesc)] + [_vp] * 9 + [ctypes.c_size_t, _vp]
         v = lib.msd_abi_version()
         if v != ABI_VERSION:
             raise RuntimeError(f"megaslide_amd: library ABI {v}, bindings expect {ABI_VERSION}")

@@ -233,15 +233,18 @@ int msd_dsa3d_bwd_noalloc(const msd_dsa3d_desc* desc, const void* q, const void*
 }
 
 int msd_dwconv3d_fwd(const msd_dwconv3d_desc* desc, const void* x, const void* weight,
-                     const void* bias, void* y, void* stream) {
+                     const void* bias, void* y, void* preact, void* stream) {
   int rc = check_conv(desc);
   if (rc != MSD_OK) return rc;
   const size_t a = elem_bytes(desc->dtype);
   rc = check_ptrs("dwconv3d_fwd", a, {x, weight, y});
   if (rc != MSD_OK) return rc;
-  if (bias != nullptr && !aligned(bias, a)) return fail(MSD_ERR_ALIGN, "dwconv3d_fwd: bias misaligned");
+  for (const void* p : {static_cast<const void*>(bias), static_cast<const void*>(preact)})
+    if (p != nullptr && !aligned(p, a)) return fail(MSD_ERR_ALIGN, "dwconv3d_fwd: misaligned");
+  if (preact != nullptr && desc->act != 1)
+    return fail(MSD_ERR_ARG, "dwconv3d_fwd: preact is the GELU input (act = 1 only)");
   if (desc->B == 0) return MSD_OK;
-  return launch_status(msd::launch_dwconv3d_fwd(*desc, x, weight, bias, y,
+  return launch_status(msd::launch_dwconv3d_fwd(*desc, x, weight, bias, y, preact,
                                                 static_cast<hipStream_t>(stream)),
                        "dwconv3d_fwd");
 }
@@ -252,24 +255,28 @@ size_t msd_dwconv3d_bwd_workspace_size(const msd_dwconv3d_desc* desc) {
 }
 
 int msd_dwconv3d_bwd(const msd_dwconv3d_desc* desc, const void* x, const void* weight,
-                     const void* bias, const void* dy, void* dx, void* dweight, void* dbias,
-                     void* workspace, size_t workspace_bytes, void* stream) {
+                     const void* bias, const void* preact, const void* dy, void* dx,
+                     void* dweight, void* dbias, void* workspace, size_t workspace_bytes,
+                     void* stream) {
   int rc = check_conv(desc);
   if (rc != MSD_OK) return rc;
   const size_t a = elem_bytes(desc->dtype);
   rc = check_ptrs("dwconv3d_bwd", a, {x, weight, dy});
   if (rc != MSD_OK) return rc;
   for (const void* p : {static_cast<const void*>(bias), static_cast<const void*>(dx),
-                        static_cast<const void*>(dweight), static_cast<const void*>(dbias)})
+                        static_cast<const void*>(dweight), static_cast<const void*>(dbias),
+                        preact})
     if (p != nullptr && !aligned(p, a)) return fail(MSD_ERR_ALIGN, "dwconv3d_bwd: misaligned");
+  if (preact != nullptr && desc->act != 1)
+    return fail(MSD_ERR_ARG, "dwconv3d_bwd: preact is the GELU input (act = 1 only)");
   if (desc->B == 0) return MSD_OK;
   const size_t need = msd::dwconv3d_bwd_ws_bytes(*desc);
   if (workspace == nullptr || workspace_bytes < need || !aligned(workspace, 16))
     return fail(MSD_ERR_WORKSPACE,
                 "dwconv3d_bwd: workspace of %zu bytes (16-aligned) needed, got %zu", need,
                 workspace == nullptr ? size_t(0) : workspace_bytes);
-  return launch_status(msd::launch_dwconv3d_bwd(*desc, x, weight, bias, dy, dx, dweight, dbias,
-                                                workspace, static_cast<hipStream_t>(stream)),
+  return launch_status(msd::launch_dwconv3d_bwd(*desc, x, weight, bias, preact, dy, dx, dweight,
+                                                dbias, workspace, static_cast<hipStream_t>(stream)),
                        "dwconv3d_bwd");
 }
 

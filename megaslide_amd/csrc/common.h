@@ -120,10 +120,10 @@ hipError_t launch_dsa3d_bwd_tiled(const msd_dsa3d_desc& d, const void* q, const 
 size_t dsa3d_bwd_ws_bytes(const msd_dsa3d_desc& d);
 size_t dsa3d_tiled_bwd_ws_bytes(const msd_dsa3d_desc& d);
 hipError_t launch_dwconv3d_fwd(const msd_dwconv3d_desc& d, const void* x, const void* w,
-                               const void* b, void* y, hipStream_t s);
+                               const void* b, void* y, void* z, hipStream_t s);
 hipError_t launch_dwconv3d_bwd(const msd_dwconv3d_desc& d, const void* x, const void* w,
-                               const void* b, const void* dy, void* dx, void* dw, void* db,
-                               void* ws, hipStream_t s);
+                               const void* b, const void* z, const void* dy, void* dx, void* dw,
+                               void* db, void* ws, hipStream_t s);
 size_t dwconv3d_bwd_ws_bytes(const msd_dwconv3d_desc& d);
 int dsa3d_max_head_dim();
 }  // namespace msd

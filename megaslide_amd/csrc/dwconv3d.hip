@@ -35,7 +35,7 @@ constexpr int kRun = 16;        // outputs per thread along W
 constexpr int kRowWaves = 4;    // waves per block in the row kernels
 constexpr int kStripRows = 8;   // (b, t, h) rows per weight-gradient work item
 
-enum Epilogue { kPlain = 0, kGelu = 1, kGeluGrad = 2, kGeluGradT = 3 };
+enum Epilogue { kPlain = 0, kGelu = 1, kGeluGrad = 2, kGeluGradT = 3, kGeluSave = 4 };
 
 // ---------------------------------------------------------------------------
 // row kernels: forward, GELU-gradient recompute, input gradient
@@ -43,12 +43,13 @@ enum Epilogue { kPlain = 0, kGelu = 1, kGeluGrad = 2, kGeluGradT = 3 };
 
 // out[p] = epilogue(sum_tap w[tap'] in[p + tap - pad]) with tap' = tap, or the
 // mirrored tap K-1-tap when flip (input gradient of the convolution).
-// mode kGeluGrad writes dz = dy * gelu'(z) as fp32 into out_f32, kGeluGradT in
-// the element type into out.
+// mode kGeluGrad writes dz = dy * gelu'(z) as fp32 into out2, kGeluGradT in
+// the element type into out; kGeluSave writes gelu(z) into out and the
+// pre-activation z (element type) into out2.
 template <typename T, typename G, int KW, int MODE>
 __global__ __launch_bounds__(64 * kRowWaves) void dwconv_rows_kernel(
     ConvArgs a, const G* __restrict__ in, const T* __restrict__ wt, const T* __restrict__ bias,
-    const T* __restrict__ dy, T* __restrict__ out, float* __restrict__ out_f32, int flip) {
+    const T* __restrict__ dy, T* __restrict__ out, void* __restrict__ out2, int flip) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int c = blockIdx.y * 64 + lane;
@@ -106,7 +107,11 @@ __global__ __launch_bounds__(64 * kRowWaves) void dwconv_rows_kernel(
     const int64_t i = (orow + w) * a.C + c;
     if (MODE == kPlain) st(out, i, acc[r]);
     if (MODE == kGelu) st(out, i, gelu_erf(acc[r]));
-    if (MODE == kGeluGrad) out_f32[i] = ld(dy, i) * gelu_erf_grad(acc[r]);
+    if (MODE == kGeluSave) {
+      st(out, i, gelu_erf(acc[r]));
+      st(static_cast<T*>(out2), i, acc[r]);
+    }
+    if (MODE == kGeluGrad) static_cast<float*>(out2)[i] = ld(dy, i) * gelu_erf_grad(acc[r]);
     if (MODE == kGeluGradT) st(out, i, ld(dy, i) * gelu_erf_grad(acc[r]));
   }
 }
@@ -148,7 +153,7 @@ __device__ __forceinline__ float ld_col(const G* row, int ww, int W, int C, uint
 template <typename T, typename G, int KH, int KW, int MODE>
 __global__ __launch_bounds__(64 * kRowWaves) void dwconv_block_kernel(
     ConvArgs a, const G* __restrict__ in, const T* __restrict__ wt, const T* __restrict__ bias,
-    const T* __restrict__ dy, T* __restrict__ out, float* __restrict__ out_f32, int flip) {
+    const T* __restrict__ dy, T* __restrict__ out, void* __restrict__ out2, int flip) {
   constexpr int R = kBlockRows, PH = KH / 2, PW = KW / 2, NX = kRun + KW - 1;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -224,7 +229,11 @@ __global__ __launch_bounds__(64 * kRowWaves) void dwconv_block_kernel(
       const int64_t i0 = (orow + w) * a.C;  // uniform; + lc per lane
       if (MODE == kPlain) stu(out + i0, lc, acc[r][j]);
       if (MODE == kGelu) stu(out + i0, lc, gelu_erf(acc[r][j]));
-      if (MODE == kGeluGrad) out_f32[i0 + lc] = ldu(dy + i0, lc) * gelu_erf_grad(acc[r][j]);
+      if (MODE == kGeluSave) {
+        stu(out + i0, lc, gelu_erf(acc[r][j]));
+        stu(static_cast<decltype(out)>(out2) + i0, lc, acc[r][j]);
+      }
+      if (MODE == kGeluGrad) static_cast<float*>(out2)[i0 + lc] = ldu(dy + i0, lc) * gelu_erf_grad(acc[r][j]);
       if (MODE == kGeluGradT) stu(out + i0, lc, ldu(dy + i0, lc) * gelu_erf_grad(acc[r][j]));
     }
   }
@@ -249,7 +258,7 @@ template <int KH, int KW, int MODE>
 __global__ __launch_bounds__(64 * kRowWaves) void dwconv_block_dot2_kernel(
     ConvArgs a, const bf16* __restrict__ in, const bf16* __restrict__ wt,
     const bf16* __restrict__ bias, const bf16* __restrict__ dy, bf16* __restrict__ out,
-    float* __restrict__ out_f32, int flip) {
+    void* __restrict__ out2, int flip) {
   constexpr int R = kBlockRows, PH = KH / 2, PW = KW / 2, NX = kRun + KW - 1, KP = KW / 2;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -340,7 +349,11 @@ __global__ __launch_bounds__(64 * kRowWaves) void dwconv_block_dot2_kernel(
       const int64_t i0 = (orow + w) * a.C;  // uniform; + lc per lane
       if (MODE == kPlain) stu(out + i0, lc, acc[r][j]);
       if (MODE == kGelu) stu(out + i0, lc, gelu_erf(acc[r][j]));
-      if (MODE == kGeluGrad) out_f32[i0 + lc] = ldu(dy + i0, lc) * gelu_erf_grad(acc[r][j]);
+      if (MODE == kGeluSave) {
+        stu(out + i0, lc, gelu_erf(acc[r][j]));
+        stu(static_cast<decltype(out)>(out2) + i0, lc, acc[r][j]);
+      }
+      if (MODE == kGeluGrad) static_cast<float*>(out2)[i0 + lc] = ldu(dy + i0, lc) * gelu_erf_grad(acc[r][j]);
       if (MODE == kGeluGradT) stu(out + i0, lc, ldu(dy + i0, lc) * gelu_erf_grad(acc[r][j]));
     }
   }
@@ -853,7 +866,7 @@ __global__ __launch_bounds__(256) void dwconv_simple_kernel(ConvArgs a, const G*
                                                             const T* __restrict__ bias,
                                                             const T* __restrict__ dy,
                                                             T* __restrict__ out,
-                                                            float* __restrict__ out_f32, int flip) {
+                                                            void* __restrict__ out2, int flip) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   const int64_t total = static_cast<int64_t>(a.B) * a.N * a.C;
   if (i >= total) return;
@@ -882,7 +895,11 @@ __global__ __launch_bounds__(256) void dwconv_simple_kernel(ConvArgs a, const G*
   }
   if (MODE == kPlain) st(out, i, acc);
   if (MODE == kGelu) st(out, i, gelu_erf(acc));
-  if (MODE == kGeluGrad) out_f32[i] = ld(dy, i) * gelu_erf_grad(acc);
+  if (MODE == kGeluSave) {
+    st(out, i, gelu_erf(acc));
+    st(static_cast<T*>(out2), i, acc);
+  }
+  if (MODE == kGeluGrad) static_cast<float*>(out2)[i] = ld(dy, i) * gelu_erf_grad(acc);
   if (MODE == kGeluGradT) st(out, i, ld(dy, i) * gelu_erf_grad(acc));
 }
 
@@ -958,7 +975,7 @@ bool block_ok(const ConvArgs& a) { return a.kh == a.kw && (a.kw == 3 || a.kw == 
 
 template <typename T, typename G, int KS, int MODE>
 void launch_block(const ConvArgs& a, const G* in, const T* w, const T* b, const T* dy, T* out,
-                  float* out_f32, int flip, hipStream_t s) {
+                  void* out2, int flip, hipStream_t s) {
   const int runs = (a.W + kRun - 1) / kRun;
   const int hblocks = (a.H + kBlockRows - 1) / kBlockRows;
   const int64_t items = static_cast<int64_t>(a.B) * a.T * hblocks * runs;
@@ -966,20 +983,20 @@ void launch_block(const ConvArgs& a, const G* in, const T* w, const T* b, const 
                   static_cast<unsigned>((a.C + 63) / 64));
   if constexpr (std::is_same<T, bf16>::value && std::is_same<G, bf16>::value)
     hipLaunchKernelGGL((dwconv_block_dot2_kernel<KS, KS, MODE>), grid, dim3(64 * kRowWaves), 0, s,
-                       a, in, w, b, dy, out, out_f32, flip);
+                       a, in, w, b, dy, out, out2, flip);
   else
     hipLaunchKernelGGL((dwconv_block_kernel<T, G, KS, KS, MODE>), grid, dim3(64 * kRowWaves), 0, s,
-                       a, in, w, b, dy, out, out_f32, flip);
+                       a, in, w, b, dy, out, out2, flip);
 }
 
 // conv of `in` (type G) with w (flip: mirrored taps), epilogue MODE
 template <typename T, typename G, int MODE>
 hipError_t run_conv(const ConvArgs& a, const G* in, const T* w, const T* b, const T* dy, T* out,
-                    float* out_f32, int flip, hipStream_t s) {
+                    void* out2, int flip, hipStream_t s) {
   if (block_ok(a)) {
-    if (a.kw == 3) launch_block<T, G, 3, MODE>(a, in, w, b, dy, out, out_f32, flip, s);
-    else if (a.kw == 5) launch_block<T, G, 5, MODE>(a, in, w, b, dy, out, out_f32, flip, s);
-    else launch_block<T, G, 7, MODE>(a, in, w, b, dy, out, out_f32, flip, s);
+    if (a.kw == 3) launch_block<T, G, 3, MODE>(a, in, w, b, dy, out, out2, flip, s);
+    else if (a.kw == 5) launch_block<T, G, 5, MODE>(a, in, w, b, dy, out, out2, flip, s);
+    else launch_block<T, G, 7, MODE>(a, in, w, b, dy, out, out2, flip, s);
   } else if (rows_ok(a)) {
     const int runs = (a.W + kRun - 1) / kRun;
     const int64_t items = static_cast<int64_t>(a.B) * a.T * a.H * runs;
@@ -989,21 +1006,21 @@ hipError_t run_conv(const ConvArgs& a, const G* in, const T* w, const T* b, cons
     switch (a.kw) {
       case 3:
         hipLaunchKernelGGL((dwconv_rows_kernel<T, G, 3, MODE>), grid, block, 0, s, a, in, w, b, dy, out,
-                           out_f32, flip);
+                           out2, flip);
         break;
       case 5:
         hipLaunchKernelGGL((dwconv_rows_kernel<T, G, 5, MODE>), grid, block, 0, s, a, in, w, b, dy, out,
-                           out_f32, flip);
+                           out2, flip);
         break;
       default:
         hipLaunchKernelGGL((dwconv_rows_kernel<T, G, 7, MODE>), grid, block, 0, s, a, in, w, b, dy, out,
-                           out_f32, flip);
+                           out2, flip);
         break;
     }
   } else {
     const int64_t total = static_cast<int64_t>(a.B) * a.N * a.C;
     hipLaunchKernelGGL((dwconv_simple_kernel<T, G, MODE>), dim3(static_cast<unsigned>((total + 255) / 256)),
-                       dim3(256), 0, s, a, in, w, b, dy, out, out_f32, flip);
+                       dim3(256), 0, s, a, in, w, b, dy, out, out2, flip);
   }
   return hipGetLastError();
 }
@@ -1059,8 +1076,11 @@ void run_dw(const ConvArgs& a, const T* x, const G* dz, float* acc, hipStream_t 
 
 template <typename T>
 hipError_t fwd_typed(const msd_dwconv3d_desc& d, const void* x, const void* w, const void* b,
-                     void* y, hipStream_t s) {
+                     void* y, void* z, hipStream_t s) {
   const ConvArgs a = make_args(d);
+  if (d.act == 1 && z != nullptr)
+    return run_conv<T, T, kGeluSave>(a, static_cast<const T*>(x), static_cast<const T*>(w),
+                                     static_cast<const T*>(b), nullptr, static_cast<T*>(y), z, 0, s);
   if (d.act == 1)
     return run_conv<T, T, kGelu>(a, static_cast<const T*>(x), static_cast<const T*>(w),
                                  static_cast<const T*>(b), nullptr, static_cast<T*>(y), nullptr, 0, s);
@@ -1087,13 +1107,54 @@ hipError_t bwd_grads(const ConvArgs& a, const void* x, const void* w, const G* d
   return hipGetLastError();
 }
 
+// dz = dy * gelu'(z) from the saved pre-activation z, 8 elements a thread
+// where n allows (16-byte bf16 / 32-byte fp32 rows), grid-stride.
+template <typename T, typename O>
+__global__ __launch_bounds__(256) void gelu_grad_kernel(const T* __restrict__ dy,
+                                                        const T* __restrict__ z,
+                                                        O* __restrict__ dz, int64_t n) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  const int64_t n8 = n / 8;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n8; i += stride) {
+    T g[8], p[8];
+    O r[8];
+    __builtin_memcpy(g, dy + 8 * i, sizeof(g));
+    __builtin_memcpy(p, z + 8 * i, sizeof(p));
+#pragma unroll
+    for (int j = 0; j < 8; ++j) r[j] = from_f32<O>(to_f32(g[j]) * gelu_erf_grad(to_f32(p[j])));
+    __builtin_memcpy(dz + 8 * i, r, sizeof(r));
+  }
+  for (int64_t i = 8 * n8 + static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += stride)
+    dz[i] = from_f32<O>(to_f32(dy[i]) * gelu_erf_grad(to_f32(z[i])));
+}
+
 template <typename T>
 hipError_t bwd_typed(const msd_dwconv3d_desc& d, const void* x, const void* w, const void* b,
-                     const void* dy, void* dx, void* dw, void* db, void* ws, hipStream_t s) {
+                     const void* z, const void* dy, void* dx, void* dw, void* db, void* ws,
+                     hipStream_t s) {
   const ConvArgs a = make_args(d);
   const int K = a.kt * a.kh * a.kw;
   float* acc = static_cast<float*>(ws);
   const int64_t nacc = static_cast<int64_t>(a.C) * (K + 1);
+  if (d.act == 1 && z != nullptr) {
+    // the forward's pre-activation: dz elementwise, no recomputed convolution
+    // (bf16 storage: dz rounded to bf16, as the framework's bf16 GELU backward
+    // leaves it, so both gradient convs take the bf16 dot2 kernels)
+    float* dz = acc + ((nacc + 63) / 64) * 64;
+    const int64_t n = static_cast<int64_t>(a.B) * a.N * a.C;
+    const dim3 grid(fill_blocks(n / 8 > 0 ? n / 8 : 1));
+    if constexpr (std::is_same<T, bf16>::value) {
+      bf16* dzb = reinterpret_cast<bf16*>(dz);
+      hipLaunchKernelGGL((gelu_grad_kernel<T, bf16>), grid, dim3(256), 0, s,
+                         static_cast<const T*>(dy), static_cast<const T*>(z), dzb, n);
+      return bwd_grads<T, T>(a, x, w, dzb, dx, dw, db, acc, s);
+    } else {
+      hipLaunchKernelGGL((gelu_grad_kernel<T, float>), grid, dim3(256), 0, s,
+                         static_cast<const T*>(dy), static_cast<const T*>(z), dz, n);
+      return bwd_grads<T, float>(a, x, w, dz, dx, dw, db, acc, s);
+    }
+  }
   if (d.act == 1) {
     float* dz = acc + ((nacc + 63) / 64) * 64;
     if constexpr (std::is_same<T, bf16>::value) {
@@ -1127,16 +1188,16 @@ size_t dwconv3d_bwd_ws_bytes(const msd_dwconv3d_desc& d) {
 }
 
 hipError_t launch_dwconv3d_fwd(const msd_dwconv3d_desc& d, const void* x, const void* w,
-                               const void* b, void* y, hipStream_t s) {
-  if (d.dtype == MSD_BF16) return fwd_typed<bf16>(d, x, w, b, y, s);
-  return fwd_typed<float>(d, x, w, b, y, s);
+                               const void* b, void* y, void* z, hipStream_t s) {
+  if (d.dtype == MSD_BF16) return fwd_typed<bf16>(d, x, w, b, y, z, s);
+  return fwd_typed<float>(d, x, w, b, y, z, s);
 }
 
 hipError_t launch_dwconv3d_bwd(const msd_dwconv3d_desc& d, const void* x, const void* w,
-                               const void* b, const void* dy, void* dx, void* dw, void* db,
-                               void* ws, hipStream_t s) {
-  if (d.dtype == MSD_BF16) return bwd_typed<bf16>(d, x, w, b, dy, dx, dw, db, ws, s);
-  return bwd_typed<float>(d, x, w, b, dy, dx, dw, db, ws, s);
+                               const void* b, const void* z, const void* dy, void* dx, void* dw,
+                               void* db, void* ws, hipStream_t s) {
+  if (d.dtype == MSD_BF16) return bwd_typed<bf16>(d, x, w, b, z, dy, dx, dw, db, ws, s);
+  return bwd_typed<float>(d, x, w, b, z, dy, dx, dw, db, ws, s);
 }
 
 }  // namespace msd

@@ -243,22 +243,26 @@ class DwConv3dFunction(torch.autograd.Function):
         b = None if bias is None else bias.to(x.dtype).contiguous()
         desc = _conv_desc(x, video_shape, kernel, _ACT[act])
         y = torch.empty_like(x)
+        # GELU: keep its input for the backward (what nn.GELU's autograd keeps),
+        # when a gradient will be asked for
+        z = torch.empty_like(x) if (act == "gelu" and torch.is_grad_enabled()) else None
         lib = _lib.load()
         with torch.cuda.device(dev):
             _lib.check(lib.msd_dwconv3d_fwd(ctypes.byref(desc), x.data_ptr(), w.data_ptr(),
-                                            _lib.ptr(b), y.data_ptr(), _lib.stream_handle(dev)),
+                                            _lib.ptr(b), y.data_ptr(), _lib.ptr(z),
+                                            _lib.stream_handle(dev)),
                        "dwconv3d_fwd")
         ctx.video_shape = tuple(video_shape)
         ctx.act = act
         ctx.kernel = kernel
         ctx.wdtype = weight.dtype
         ctx.bdtype = None if bias is None else bias.dtype
-        ctx.save_for_backward(x, w, b)
+        ctx.save_for_backward(x, w, b, z)
         return y
 
     @staticmethod
     def backward(ctx, dy):
-        x, w, b = ctx.saved_tensors
+        x, w, b, z = ctx.saved_tensors
         dev = x.device
         dy = dy.to(x.dtype).contiguous()
         need_x, need_w, need_b = ctx.needs_input_grad[:3]
@@ -271,8 +275,8 @@ class DwConv3dFunction(torch.autograd.Function):
         ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
         with torch.cuda.device(dev):
             _lib.check(lib.msd_dwconv3d_bwd(
-                ctypes.byref(desc), x.data_ptr(), w.data_ptr(), _lib.ptr(b), dy.data_ptr(),
-                _lib.ptr(dx), _lib.ptr(dw), _lib.ptr(db), ws.data_ptr(), ws_bytes,
+                ctypes.byref(desc), x.data_ptr(), w.data_ptr(), _lib.ptr(b), _lib.ptr(z),
+                dy.data_ptr(), _lib.ptr(dx), _lib.ptr(dw), _lib.ptr(db), ws.data_ptr(), ws_bytes,
                 _lib.stream_handle(dev)), "dwconv3d_bwd")
         if dw is not None:
             dw = dw.to(ctx.wdtype)

@@ -33,7 +33,7 @@ def test_exports_match_header():
 
 
 def test_abi_version():
-    assert _lib.load().msd_abi_version() == _lib.ABI_VERSION == 3
+    assert _lib.load().msd_abi_version() == _lib.ABI_VERSION == 4
 
 
 def _desc(**kw):
@@ -121,13 +121,17 @@ def test_dwconv_validation():
     lib = _lib.load()
     d = _lib.ConvDesc(1, 4, 5, 6, 32, 3, 7, 7, 0, 0)
     bad = _lib.ConvDesc(1, 4, 5, 6, 32, 3, 6, 7, 0, 0)  # even kernel
-    assert lib.msd_dwconv3d_fwd(ctypes.byref(bad), 16, 16, None, 16, None) == -2
+    assert lib.msd_dwconv3d_fwd(ctypes.byref(bad), 16, 16, None, 16, None, None) == -2
     assert b"odd" in lib.msd_last_error()
-    assert lib.msd_dwconv3d_fwd(ctypes.byref(d), 16, None, None, 16, None) == -1
+    assert lib.msd_dwconv3d_fwd(ctypes.byref(d), 16, None, None, 16, None, None) == -1
+    # the saved pre-activation belongs to the GELU form only
+    assert lib.msd_dwconv3d_fwd(ctypes.byref(d), 16, 16, None, 16, 16, None) == -1
+    assert b"act = 1" in lib.msd_last_error()
     gelu = _lib.ConvDesc(2, 4, 5, 6, 32, 3, 3, 3, 1, 1)
+    assert lib.msd_dwconv3d_fwd(ctypes.byref(gelu), 16, 16, None, 16, 17, None) == -3
     ws = lib.msd_dwconv3d_bwd_workspace_size(ctypes.byref(gelu))
     assert ws >= 4 * (2 * 4 * 5 * 6 * 32 + 32 * 28)
-    assert lib.msd_dwconv3d_bwd(ctypes.byref(gelu), 16, 16, 16, 16, 16, 16, 16, None, ws,
+    assert lib.msd_dwconv3d_bwd(ctypes.byref(gelu), 16, 16, 16, None, 16, 16, 16, 16, None, ws,
                                 None) == -4
 
 

@@ -65,3 +65,47 @@ def test_dwconv_matches_conv3d(cfg, dtype, tol):
     assert rel_err(xd.grad.double().cpu(), xr.grad) < tol
     assert rel_err(wd.grad.double().cpu(), wr.grad) < tol
     assert rel_err(bd.grad.double().cpu(), br.grad) < tol
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-4), (torch.bfloat16, 2e-2)])
+@pytest.mark.parametrize("cfg", [(2, 3, 5, 20, 130, (3, 3, 3)), (1, 4, 9, 32, 64, (3, 3, 3)),
+                                 (1, 5, 4, 7, 40, (5, 3, 1))])
+def test_gelu_preact_kept_or_recomputed(cfg, dtype, tol):
+    """The GELU form through the C ABI: the forward's optional pre-activation
+    output equals the convolution before GELU, and the backward gives the same
+    gradients from it as from recomputing it (preact NULL)."""
+    import ctypes
+    from megaslide_amd import _lib
+    B, T, H, W, C, ks = cfg
+    N = T * H * W
+    print(f"[dwconv gelu preact] {cfg} {dtype}", flush=True)
+    g = torch.Generator().manual_seed(3 * C + W)
+    x = torch.randn(B, N, C, generator=g).to(dtype)
+    w = (torch.randn(C, 1, *ks, generator=g) * 0.2).to(dtype)
+    b = (torch.randn(C, generator=g) * 0.1).to(dtype)
+    dy = torch.randn(B, N, C, generator=g).to(dtype)
+    xr, wr, br = (t.double().requires_grad_(True) for t in (x, w, b))
+    zr = reference(xr, wr, br, (T, H, W), None)
+    F.gelu(zr).backward(dy.double())
+    lib = _lib.load()
+    desc = _lib.ConvDesc(B, T, H, W, C, *ks, _lib.dtype_code(dtype), 1)
+    xd, wd, bd, dyd = (t.to(DEV).contiguous() for t in (x, w.reshape(C, -1), b, dy))
+    y, z = torch.empty_like(xd), torch.empty_like(xd)
+    sh = torch.cuda.current_stream().cuda_stream
+    P = lambda t: t.data_ptr()  # noqa: E731
+    assert lib.msd_dwconv3d_fwd(ctypes.byref(desc), P(xd), P(wd), P(bd), P(y), P(z), sh) == 0
+    nbytes = lib.msd_dwconv3d_bwd_workspace_size(ctypes.byref(desc))
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=DEV)
+    grads = {}
+    for name, pre in (("kept", P(z)), ("recomputed", None)):
+        dx, dw, db = torch.empty_like(xd), torch.empty_like(wd), torch.empty_like(bd)
+        assert lib.msd_dwconv3d_bwd(ctypes.byref(desc), P(xd), P(wd), P(bd), pre, P(dyd), P(dx),
+                                    P(dw), P(db), P(ws), nbytes, sh) == 0
+        grads[name] = (dx, dw, db)
+    torch.cuda.synchronize()
+    assert rel_err(z.double().cpu(), zr.detach()) < tol
+    assert rel_err(y.double().cpu(), F.gelu(zr).detach()) < tol
+    for name, (dx, dw, db) in grads.items():
+        assert rel_err(dx.double().cpu(), xr.grad) < tol, name
+        assert rel_err(dw.double().cpu().reshape(wr.shape), wr.grad) < tol, name
+        assert rel_err(db.double().cpu(), br.grad) < tol, name
