@@ -372,10 +372,16 @@ def cpu_baseline(cfg, runs=3):
 
 def phase_kernels(dtype):
     """Bench phase -> the kernels its ABI call launches, in order (bf16 adds the
-    fp32 -> bf16 conversion of the dK/dV accumulators)."""
-    bwd = ["dsa3d_bwd_p1_kernel", "dsa3d_bwd_p2_kernel"]
+    fp16 accumulators' scale kernels before the dq/dK/dV kernel, their
+    conversion to bf16, and the fp32 redo after an overflow, whose kernels
+    return at once without one)."""
+    if dtype != "bf16":
+        return {"dsa3d_fwd": ["dsa3d_fwd_tiled_kernel"],
+                "dsa3d_bwd": ["dsa3d_bwd_p1_kernel", "dsa3d_bwd_p2_kernel"]}
     return {"dsa3d_fwd": ["dsa3d_fwd_tiled_kernel"],
-            "dsa3d_bwd": bwd + (["acc_to_bf16_kernel"] if dtype == "bf16" else [])}
+            "dsa3d_bwd": ["dsa3d_bwd_p1_kernel", "h16_bounds_kernel", "h16_scales_kernel",
+                          "dsa3d_bwd_p2_kernel", "h16_to_bf16_kernel", "fill_zero_if_flag",
+                          "dsa3d_bwd_p2_redo_kernel", "acc_to_bf16_kernel"]}
 
 
 def summarize(workload, trace_dir, fetch_dir, write_dir):
@@ -452,7 +458,7 @@ def summarize(workload, trace_dir, fetch_dir, write_dir):
     print("\nPer kernel (counter KiB, unscaled):\n\n| dispatch | kernel | FETCH | WRITE |\n|---|---|---|---|")
     wmap = {(d, n): v for d, n, v in write}
     for d, n, v in fetch:
-        if "msd::" in n:
+        if "msd" in n:
             print(f"| {d} | `{n[:70]}` | {v:.0f} | {wmap.get((d, n), float('nan')):.0f} |")
     path = os.path.join(ROOT, "profiles", "traffic.json")
     try:
