@@ -75,6 +75,9 @@ __global__ __launch_bounds__(kThreads, (fwd_min_waves<HD, E>())) void dsa3d_fwd_
   __shared__ int s_red[kWaves][6];
 
   const Tile tl = make_tile<1, kSubs>(a);
+  // the tile's q rows load while the slots are set up
+  op_t<E> qx[HD / 32];
+  load_rows_operand<HD, E>(a, tl, static_cast<const E*>(a.q), a.qs, qx);
   Slot sl[kSlots];
   Box box;
   setup_slots<E, kSubs, kSlots>(a, tl, sl, box, s_red, true);
@@ -82,9 +85,6 @@ __global__ __launch_bounds__(kThreads, (fwd_min_waves<HD, E>())) void dsa3d_fwd_
   const int nit = (box.zhi - box.zlo + 1) * nchunks;
   const E* const kp = static_cast<const E*>(a.k);
   const E* const vp = static_cast<const E*>(a.v);
-
-  op_t<E> qx[HD / 32];
-  load_rows_operand<HD, E>(a, tl, static_cast<const E*>(a.q), a.qs, qx);
 
   // ---- pass 1: scores -------------------------------------------------------
   // K rows of the next (plane, chunk) are loaded while the current one is used
@@ -340,6 +340,29 @@ __global__ __launch_bounds__(kThreads, (p1_min_waves<HD, E>())) void dsa3d_bwd_p
 
   const Tile tl = make_tile<1, kSubs>(a);
   const int D = a.nh * HD;
+  // The tile's q and dO rows (staged in LDS, or held as MFMA operands) are
+  // loaded first, so that the slot setup's arithmetic covers their latency.
+  constexpr int XCPR = HD * static_cast<int>(sizeof(E)) / 16;  // 16-byte pieces of a row
+  constexpr int kXItems = 2 * kTQ * XCPR, kXIPT = kTwoWg ? (kXItems + kThreads - 1) / kThreads : 1;
+  uint4 xst[kXIPT];
+  op_t<E> qx[HD / 32], gx[HD / 32];
+  if constexpr (kTwoWg) {
+    // item e: q (t = 0) or dO (t = 1) row m, 16 bytes from channel ch
+#pragma unroll
+    for (int j = 0; j < kXIPT; ++j) {
+      const int e = threadIdx.x + kThreads * j;
+      const int t = e / (kTQ * XCPR), m = (e / XCPR) % kTQ, ch = (e % XCPR) * (16 / sizeof(E));
+      const int64_t row = e < kXItems ? tile_row(a, tl, m) : -1;
+      xst[j] = uint4{0u, 0u, 0u, 0u};
+      if (row >= 0) {
+        const E* src = t == 0 ? static_cast<const E*>(a.q) + row * a.qs : dout + row * D;
+        xst[j] = *reinterpret_cast<const uint4*>(src + tl.head * HD + ch);
+      }
+    }
+  } else {
+    load_rows_operand<HD, E>(a, tl, static_cast<const E*>(a.q), a.qs, qx);
+    load_rows_operand<HD, E>(a, tl, dout, D, gx);
+  }
   Slot sl[kSlots];
   Box box;
   setup_slots<E, kSubs, kSlots>(a, tl, sl, box, s_red, true);
@@ -366,24 +389,15 @@ __global__ __launch_bounds__(kThreads, (p1_min_waves<HD, E>())) void dsa3d_bwd_p
     }
   }
 
-  op_t<E> qx[HD / 32], gx[HD / 32];
   if constexpr (kTwoWg) {
-    // q (t = 0) and dO (t = 1) rows of the tile's queries into LDS, 16 bytes a thread
-    constexpr int CPR = HD * static_cast<int>(sizeof(E)) / 16;
-    for (int e = threadIdx.x; e < 2 * kTQ * CPR; e += kThreads) {
-      const int t = e / (kTQ * CPR), m = (e / CPR) % kTQ, ch = (e % CPR) * (16 / sizeof(E));
-      const int64_t row = tile_row(a, tl, m);
-      uint4 v = {0u, 0u, 0u, 0u};
-      if (row >= 0) {
-        const E* src = t == 0 ? static_cast<const E*>(a.q) + row * a.qs : dout + row * D;
-        v = *reinterpret_cast<const uint4*>(src + tl.head * HD + ch);
-      }
-      *reinterpret_cast<uint4*>(&s_x[(t * kTQ + m) * XR + ch]) = v;
+#pragma unroll
+    for (int j = 0; j < kXIPT; ++j) {
+      const int e = threadIdx.x + kThreads * j;
+      if (e >= kXItems) continue;
+      const int t = e / (kTQ * XCPR), m = (e / XCPR) % kTQ, ch = (e % XCPR) * (16 / sizeof(E));
+      *reinterpret_cast<uint4*>(&s_x[(t * kTQ + m) * XR + ch]) = xst[j];
     }
     __syncthreads();
-  } else {
-    load_rows_operand<HD, E>(a, tl, static_cast<const E*>(a.q), a.qs, qx);
-    load_rows_operand<HD, E>(a, tl, dout, D, gx);
   }
   // MFMA A operand of staged row block t (q or dO): lane l holds channels
   // 32 c + 8 (l / 16) + [0, 8) of query l % 16
@@ -637,22 +651,38 @@ __device__ __forceinline__ void p2_tile(const Args& a, int tile, const E* __rest
   const int D = a.nh * HD;
   // first channel of the window: cw_base + CW blockIdx.z within the head
   const int cw0 = tl.head * HD + cw_base + CW * static_cast<int>(blockIdx.z);
+  // p and ds * scale of this lane's taps (from the first kernel) and the q / dO
+  // items it stages are loaded before the slot setup, whose arithmetic then
+  // covers their latency (one workgroup per CU: nothing else would)
+  float p[kP2Slots], bsc[kP2Slots];
+  const int64_t tap0 = (tl.qn * a.nh + tl.head) * a.K;
+#pragma unroll
+  for (int i = 0; i < kP2Slots; ++i) {
+    const int kap = tl.sub + kP2Subs * i;
+    const bool ok = tl.q_ok && kap < a.K;  // the slots setup_slots leaves empty
+    p[i] = ok ? p_ws[tap0 + kap] : 0.0f;
+    bsc[i] = ok ? b_ws[tap0 + kap] : 0.0f;
+  }
+  // item e = threadIdx.x + NT j moves 8 channels of one q (tensor 0) or dO row
+  constexpr int kItems = 2 * kP2Q * (CW / 8), kIPT = (kItems + NT - 1) / NT;
+  op_t<E> xs[kIPT];
+#pragma unroll
+  for (int j = 0; j < kIPT; ++j) {
+    const int e = threadIdx.x + NT * j;
+    const int cg = e % (CW / 8), m = (e / (CW / 8)) % kP2Q, tensor = e / (kP2Q * (CW / 8));
+    const int64_t n = e < kItems ? tile_row(a, tl, m) : -1;
+    xs[j] = zero_op<E>();
+    if (n >= 0) {
+      const E* src = tensor == 0 ? static_cast<const E*>(a.q) + n * a.qs : dout + n * D;
+      xs[j] = load_op<E>(src + cw0 + 8 * cg);
+    }
+  }
   Slot sl[kP2Slots];
   Box box;
   setup_slots<E, kP2Subs, kP2Slots, NW>(a, tl, sl, box, s_red);
   const int nchunks = box.ncy * box.ncx;
   const int nit = (box.zhi - box.zlo + 1) * nchunks;
 
-  float p[kP2Slots], bsc[kP2Slots];
-  const int64_t tap0 = (tl.qn * a.nh + tl.head) * a.K;
-#pragma unroll
-  for (int i = 0; i < kP2Slots; ++i) {
-    p[i] = bsc[i] = 0.0f;
-    if (slot_z0(sl[i]) < 0) continue;
-    const int kap = tl.sub + kP2Subs * i;
-    p[i] = p_ws[tap0 + kap];
-    bsc[i] = b_ws[tap0 + kap];
-  }
   // fixed-point scale of this query's B entries: 2^30 / sum_k |ds_k scale|
   float l1 = 0.0f;
 #pragma unroll
@@ -670,16 +700,13 @@ __device__ __forceinline__ void p2_tile(const Args& a, int tile, const E* __rest
   }
   __syncthreads();
   // stage q and dO of the tile transposed, carrying the fixed-point scales of
-  // B (per query) and A (1 / fix_a) for the dK/dV products: item e moves 8
-  // channels of one row
-  for (int e = threadIdx.x; e < 2 * kP2Q * (CW / 8); e += NT) {
+  // B (per query) and A (1 / fix_a) for the dK/dV products
+#pragma unroll
+  for (int j = 0; j < kIPT; ++j) {
+    const int e = threadIdx.x + NT * j;
+    if (e >= kItems) continue;
     const int cg = e % (CW / 8), m = (e / (CW / 8)) % kP2Q, tensor = e / (kP2Q * (CW / 8));
-    const int64_t n = tile_row(a, tl, m);
-    op_t<E> x = zero_op<E>();
-    if (n >= 0) {
-      const E* src = tensor == 0 ? static_cast<const E*>(a.q) + n * a.qs : dout + n * D;
-      x = load_op<E>(src + cw0 + 8 * cg);
-    }
+    const op_t<E> x = xs[j];
     const float sc = tensor == 0 ? s_binv[m] : a.fix_a_inv;
     if constexpr (sizeof(E) == 2) {
       const u32x4_t xb = __builtin_bit_cast(u32x4_t, x);
@@ -721,18 +748,15 @@ __device__ __forceinline__ void p2_tile(const Args& a, int tile, const E* __rest
   // fp16 accumulation: the powers of two that scale the dK and dV partials
   const float sc_k = MODE == kP2F16 ? scales[0] : 1.0f;
   const float sc_v = MODE == kP2F16 ? scales[2] : 1.0f;
-  // K rows of the next (plane, chunk) are loaded while the current one is used,
-  // except with three frames, whose registers are too few to keep them live
-  // across the step (the kernel is atomic-bound there anyway)
-  constexpr bool kPrefetchK = FR == 2;
+  // The step's K rows are loaded first and stored to LDS after the table
+  // scatter (below)
   StageRows<kP2Stage, CW, E> kr;
   Walk w = walk_begin(box);
-  if (kPrefetchK && nit > 0) load_stage_rows<kP2Stage, CW, E>(a, tl, w.c, w.z, kp, a.ks, cw0, kr);
   for (int it = 0; it < nit; ++it) {
     const Walk wn = walk_next(box, w);
     const Chunk& c = w.c;
     const int z = w.z;
-    if (!kPrefetchK) load_stage_rows<kP2Stage, CW, E>(a, tl, c, z, kp, a.ks, cw0, kr);
+    load_stage_rows<kP2Stage, CW, E>(a, tl, c, z, kp, a.ks, cw0, kr);
     // zero the transposed A and B tables; token rows of the chunk's voxels
     for (int e = threadIdx.x; e < c.nvp * kP2Row / 4; e += NT) {
       const u32x4_t zz = {0u, 0u, 0u, 0u};
@@ -741,9 +765,6 @@ __device__ __forceinline__ void p2_tile(const Args& a, int tile, const E* __rest
     }
     for (int vi = threadIdx.x; vi < c.nv; vi += NT)
       s_rows[vi] = static_cast<int>(chunk_row(a, tl, c, z, vi) - tl.sample0);
-    store_stage<kP2Stage, CW, E>(c, kr, s_kt);
-    if (kPrefetchK && it + 1 < nit)
-      load_stage_rows<kP2Stage, CW, E>(a, tl, wn.c, wn.z, kp, a.ks, cw0, kr);
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < kP2Slots; ++i) {
@@ -775,6 +796,9 @@ __device__ __forceinline__ void p2_tile(const Args& a, int tile, const E* __rest
       atomicAdd(r11, to_fix(pz * w11));
       atomicAdd(r11 + kTab, to_fix(bz * w11));
     }
+    // the K rows are stored only now: their load waits for every atomic this
+    // wave issued before it (one in-order counter), which the scatter overlaps
+    store_stage<kP2Stage, CW, E>(c, kr, s_kt);
     __syncthreads();
     // dq[q] += sum_v B[q][v] K[v]; in bf16, B as a hi/lo pair because
     // sum_v B[q][v] = 0 and K may carry a large common part
