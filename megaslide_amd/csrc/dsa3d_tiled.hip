@@ -419,6 +419,12 @@ __global__ __launch_bounds__(kThreads, (p1_min_waves<HD, E>())) void dsa3d_bwd_p
 #pragma unroll
   for (int m = 1; m < kSubs; m <<= 1) delta += __shfl_xor(delta, m);
   if (dlse != nullptr && tl.q_ok) delta -= dlse[tl.qn * a.nh + tl.head];
+  // kept in LDS across the plane loop (registers are the limit there)
+  __shared__ float s_dl[kTQ][2];
+  if (tl.sub == 0) {
+    s_dl[tl.q][0] = delta;
+    s_dl[tl.q][1] = lse_q;
+  }
 
   // ---- pass 1: per tap, the interpolated S and dP and their coordinate
   // derivatives (x, y within a plane; z across planes) -------------------------
@@ -503,20 +509,50 @@ __global__ __launch_bounds__(kThreads, (p1_min_waves<HD, E>())) void dsa3d_bwd_p
   const float cxs = 0.5f * a.W * a.rdiv_x * a.offset_scale;
   const float cys = 0.5f * a.H * a.rdiv_y * a.offset_scale;
   const float czs = 0.5f * a.T * a.rdiv_z * a.offset_scale;
-  const int64_t tap0 = (tl.qn * a.nh + tl.head) * a.K;
+  // the output addresses are formed here, from an opaque copy of the query's
+  // token row, rather than hoisted before the plane loop (where they spill)
+  uint32_t qlo = static_cast<uint32_t>(tl.qn), qhi = static_cast<uint32_t>(tl.qn >> 32);
+  asm volatile("" : "+v"(qlo), "+v"(qhi));
+  const int64_t qn = static_cast<int64_t>((static_cast<uint64_t>(qhi) << 32) | qlo);
+  const int64_t tap0 = (qn * a.nh + tl.head) * a.K;
+  delta = s_dl[tl.q][0];  // written before the loop's first barrier
+  lse_q = s_dl[tl.q][1];
+  // p * factor and ds * scale of every tap (0 for empty slots), in place of s and dp
 #pragma unroll
   for (int i = 0; i < kSlots; ++i) {
-    if (slot_z0(sl[i]) < 0) continue;
     const float pi = __expf(s_[i] * a.softmax_scale - lse_q);
     // dropout: o sums pd * v_s with pd = p * factor, so dp and the V-side
     // coordinate gradient see the factor
     const float dfac = slot_dropout(sl[i], a.drop);
-    const float pd = pi * dfac;
-    const float dss = pi * (dfac * dp_[i] - delta) * a.softmax_scale;
+    const bool ok = slot_z0(sl[i]) >= 0;
+    s_[i] = ok ? pi * dfac : 0.0f;
+    dp_[i] = ok ? pi * (dfac * dp_[i] - delta) * a.softmax_scale : 0.0f;
+  }
+  // bf16 storage keeps one word per tap: fp16 p * factor and ds * scale / l1,
+  // with l1 = sum over the query's taps of |ds * scale| kept per token and head
+  // (the normalised values lie in [-1, 1], where fp16 keeps 11 bits)
+  float rl1 = 1.0f;
+  if constexpr (sizeof(E) == 2) {
+    float l1 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kSlots; ++i) l1 += fabsf(dp_[i]);
+#pragma unroll
+    for (int m = 1; m < kSubs; m <<= 1) l1 += __shfl_xor(l1, m);
+    rl1 = l1 > 1e-30f ? 1.0f / l1 : 0.0f;
+    if (tl.sub == 0 && tl.q_ok) b_ws[qn * a.nh + tl.head] = l1;
+  }
+#pragma unroll
+  for (int i = 0; i < kSlots; ++i) {
+    if (slot_z0(sl[i]) < 0) continue;
+    const float pd = s_[i], dss = dp_[i];
     const int kap = tl.sub + kSubs * i;
-    p_ws[tap0 + kap] = pd;
-    b_ws[tap0 + kap] = dss;
-    E* dp = doff + tl.qn * a.C + (static_cast<int64_t>(tl.head) * a.K + kap) * 3;
+    if constexpr (sizeof(E) == 4) {
+      p_ws[tap0 + kap] = pd;
+      b_ws[tap0 + kap] = dss;
+    } else {
+      reinterpret_cast<uint32_t*>(p_ws)[tap0 + kap] = pack_h2(pd, dss * rl1);
+    }
+    E* dp = doff + qn * a.C + (static_cast<int64_t>(tl.head) * a.K + kap) * 3;
     const int m = sl[i].zc >> 17;
     dp[0] = from_f32<E>((m & 1) ? (dss * gxs[i] + pd * gxd[i]) * cxs : 0.0f);
     dp[1] = from_f32<E>((m & 2) ? (dss * gys[i] + pd * gyd[i]) * cys : 0.0f);
@@ -654,15 +690,23 @@ __device__ __forceinline__ void p2_tile(const Args& a, int tile, const E* __rest
   // p and ds * scale of this lane's taps (from the first kernel) and the q / dO
   // items it stages are loaded before the slot setup, whose arithmetic then
   // covers their latency (one workgroup per CU: nothing else would)
+  // (bf16 storage: fp16 pairs of p and ds * scale / l1, and l1 per query)
   float p[kP2Slots], bsc[kP2Slots];
   const int64_t tap0 = (tl.qn * a.nh + tl.head) * a.K;
 #pragma unroll
   for (int i = 0; i < kP2Slots; ++i) {
     const int kap = tl.sub + kP2Subs * i;
     const bool ok = tl.q_ok && kap < a.K;  // the slots setup_slots leaves empty
-    p[i] = ok ? p_ws[tap0 + kap] : 0.0f;
-    bsc[i] = ok ? b_ws[tap0 + kap] : 0.0f;
+    if constexpr (sizeof(E) == 4) {
+      p[i] = ok ? p_ws[tap0 + kap] : 0.0f;
+      bsc[i] = ok ? b_ws[tap0 + kap] : 0.0f;
+    } else {
+      const uint32_t w = ok ? reinterpret_cast<const uint32_t*>(p_ws)[tap0 + kap] : 0u;
+      p[i] = h2_lo(w);
+      bsc[i] = h2_hi(w);
+    }
   }
+  const float l1_q = sizeof(E) == 2 && tl.q_ok ? b_ws[tl.qn * a.nh + tl.head] : 1.0f;
   // item e = threadIdx.x + NT j moves 8 channels of one q (tensor 0) or dO row
   constexpr int kItems = 2 * kP2Q * (CW / 8), kIPT = (kItems + NT - 1) / NT;
   op_t<E> xs[kIPT];
@@ -683,7 +727,9 @@ __device__ __forceinline__ void p2_tile(const Args& a, int tile, const E* __rest
   const int nchunks = box.ncy * box.ncx;
   const int nit = (box.zhi - box.zlo + 1) * nchunks;
 
-  // fixed-point scale of this query's B entries: 2^30 / sum_k |ds_k scale|
+  // fixed-point scale of this query's B entries: 2^30 / sum_k |ds_k scale| (of
+  // the values as stored: normalised ones for bf16 storage, whose l1 then
+  // joins the query's dq scale)
   float l1 = 0.0f;
 #pragma unroll
   for (int i = 0; i < kP2Slots; ++i) l1 += fabsf(bsc[i]);
@@ -691,7 +737,7 @@ __device__ __forceinline__ void p2_tile(const Args& a, int tile, const E* __rest
   for (int m = 1; m < kP2Subs; m <<= 1) l1 += __shfl_xor(l1, m);
   const bool l1_ok = l1 > 1e-30f;
   const float bscale = l1_ok ? kFixA / l1 : 0.0f;
-  if (tl.sub == 0) s_binv[tl.q] = l1_ok ? l1 * kFixAInv : 0.0f;
+  if (tl.sub == 0) s_binv[tl.q] = l1_ok ? l1 * kFixAInv * l1_q : 0.0f;
   // p and ds scale in fixed-point units from here on
 #pragma unroll
   for (int i = 0; i < kP2Slots; ++i) {
@@ -1469,8 +1515,10 @@ constexpr int p2_window() {
 // Buffers of one tiled backward call (workspace carved by tiled_ws).
 template <typename E>
 struct BwdBufs {
-  float* p_ws;     // p * dropout factor per tap
-  float* b_ws;     // ds * softmax_scale per tap
+  float* p_ws;     // per tap: p * dropout factor (fp32 storage), or the fp16 pair
+                   // (p * factor, ds * softmax_scale / l1) in one word (bf16)
+  float* b_ws;     // per tap: ds * softmax_scale (fp32), or per (token, head):
+                   // l1 = sum over its taps of |ds * softmax_scale| (bf16)
   void* dk_acc;    // dK / dV accumulator rows: the fp32 outputs (fp32 storage) or
   void* dv_acc;    // scaled fp16 [rows, D] (bf16 storage)
   int64_t acc_ks, acc_vs;
@@ -1620,7 +1668,7 @@ TiledWs tiled_ws(const msd_dsa3d_desc& d) {
   w.xacc = w.acc + (bf ? 2 * rows * D * 4 : 0);
   w.p = w.xacc + (bf ? 2 * static_cast<size_t>(d.B) * G * D * 4 : 0);
   w.ds = w.p + taps * 4;
-  w.dse = up(w.ds + taps * 4);
+  w.dse = up(w.ds + (bf ? rows * d.num_heads * 4 : taps * 4));
   w.pfe = up(w.dse + rows * d.num_heads * G * e);
   w.stats = up(w.pfe + rows * d.num_heads * G * e);
   w.scales = up(w.stats + (bf ? kBoundsBlocks * 4 * 4 : 0));

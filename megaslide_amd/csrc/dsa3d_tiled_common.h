@@ -247,6 +247,18 @@ __device__ __forceinline__ int64_t tile_row(const Args& a, const Tile& t, int m)
   return t.sample0 + (static_cast<int64_t>(tt) * a.H + h) * a.W + w;
 }
 
+// Two floats as an fp16 pair in one word (round to nearest), and back.
+__device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {
+  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(lo))) |
+         (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(hi))) << 16);
+}
+__device__ __forceinline__ float h2_lo(uint32_t w) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w & 0xffffu)));
+}
+__device__ __forceinline__ float h2_hi(uint32_t w) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w >> 16)));
+}
+
 struct Box {
   int zlo, zhi, ylo, yhi, xlo, xhi;
   int ncy, ncx;  // chunk grid

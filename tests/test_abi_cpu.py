@@ -98,16 +98,17 @@ def test_workspace_size_and_check():
     # head_dim 16: direct kernels only, dK/dV fp32 accumulators
     d16 = _desc(B=2, head_dim=16, q_stride=32, k_stride=32, v_stride=32)
     assert lib.msd_dsa3d_bwd_workspace_size(ctypes.byref(d16)) == 2 * rows * 32 * 4
-    # head_dim 64: the tiled backward keeps p and ds of every tap (fp32); fp32
-    # storage adds dK/dV up in its outputs (the direct kernels' accumulators
-    # are less than p and ds, and the larger of the two is asked for), bf16 in
-    # fp32 rows (which also hold the fp16 accumulators) beside p and ds, then
-    # the scale bounds (4 floats from each of 256 blocks) and 32 bytes of
+    # head_dim 64: the tiled backward keeps p and ds of every tap: two fp32
+    # arrays for fp32 storage, which adds dK/dV up in its outputs (the direct
+    # kernels' accumulators are less than p and ds, and the larger of the two
+    # is asked for); for bf16 one word of two fp16 per tap plus one fp32 per
+    # (token, head), beside fp32 rows (which also hold the fp16 accumulators),
+    # then the scale bounds (4 floats from each of 256 blocks) and 32 bytes of
     # scales and overflow flag
-    taps = 2 * rows * 2 * 147 * 4
+    taps = rows * 2 * 147 * 4
     records = 256 * 4 * 4
-    for dtype, want in ((0, max(2 * rows * 128 * 4, taps)),
-                        (1, 2 * rows * 128 * 4 + taps + records + 32)):
+    for dtype, want in ((0, max(2 * rows * 128 * 4, 2 * taps)),
+                        (1, 2 * rows * 128 * 4 + taps + rows * 2 * 4 + records + 32)):
         d = _desc(B=2, dtype=dtype)
         need = lib.msd_dsa3d_bwd_workspace_size(ctypes.byref(d))
         assert need == want
