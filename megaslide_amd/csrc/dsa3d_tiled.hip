@@ -506,9 +506,7 @@ __global__ __launch_bounds__(kThreads, (p1_min_waves<HD, E>())) void dsa3d_bwd_p
   // p = exp(scale * s - lse), ds = p (dp - Delta).  The coordinate gradient of
   // a tap is ds*scale*dS/du + p*dP/du; chain it through the clamp mask, the
   // unnormalisation (S/2), the slot divisor and offset_scale into d offsets.
-  const float cxs = 0.5f * a.W * a.rdiv_x * a.offset_scale;
-  const float cys = 0.5f * a.H * a.rdiv_y * a.offset_scale;
-  const float czs = 0.5f * a.T * a.rdiv_z * a.offset_scale;
+  const float cxs = a.gsx, cys = a.gsy, czs = a.gsz;
   // the output addresses are formed here, from an opaque copy of the query's
   // token row, rather than hoisted before the plane loop (where they spill)
   uint32_t qlo = static_cast<uint32_t>(tl.qn), qhi = static_cast<uint32_t>(tl.qn >> 32);
@@ -1266,6 +1264,11 @@ tiled::Args make_tiled_args(const msd_dsa3d_desc& d, const void* q, const void* 
   a.rbdiv_z = 1.0f / a.bdiv_z;
   a.r_kw = 1.0f / static_cast<float>(d.kw);
   a.r_khkw = 1.0f / static_cast<float>(d.kh * d.kw);
+  // the unnormalisation (S/2), the slot divisor and offset_scale, multiplied
+  // left to right in fp32
+  a.gsx = 0.5f * static_cast<float>(d.W) * a.rdiv_x * a.offset_scale;
+  a.gsy = 0.5f * static_cast<float>(d.H) * a.rdiv_y * a.offset_scale;
+  a.gsz = 0.5f * static_cast<float>(d.T) * a.rdiv_z * a.offset_scale;
   a.drop = dropout_args(d);
   a.fix_a = tiled::fix_a_scale(a.drop);
   a.fix_a_inv = 1.0f / a.fix_a;

@@ -148,6 +148,7 @@ struct Args {
   float bdiv_x, bdiv_y, bdiv_z;  // base-grid divisors max(S-1, 1) of x (W), y (H), z (T)
   float rbdiv_x, rbdiv_y, rbdiv_z;
   float r_kw, r_khkw;            // 1/kw, 1/(kh*kw): exact small-integer division
+  float gsx, gsy, gsz;           // d offset per d sampling coordinate: 0.5 S rdiv offset_scale
   DropoutArgs drop;              // attention dropout on the softmax weights
   float fix_a, fix_a_inv;        // fixed-point scale of the A (= p w) tables and its inverse
   const void* ek;                // extra keys / values [B, G, D] shared by every query
