@@ -254,6 +254,23 @@ __device__ __forceinline__ float dot2_bf16(uint32_t w, uint32_t x, float acc) {
                                          __builtin_bit_cast(bf16x2_dot_t, x), acc, false);
 }
 
+// bf16 rows read through a buffer resource: the lane's channel is the vector
+// offset (the same for every load of a thread) and the voxel a scalar byte
+// offset, so a load costs no vector instruction (64-bit per-load vector
+// addresses, and the scalar registers they were built from, had made a third
+// of these kernels' instructions).  The host admits tensors below 2^31 bytes.
+constexpr int64_t kBufMaxBytes = int64_t{1} << 31;
+constexpr int kBufWord3 = 0x00020000;  // raw 32-bit dwords, no swizzle (gfx9)
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t bf16_rows(const bf16* p, int64_t elems) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16*>(p), 0, static_cast<int>(elems * 2),
+                                           kBufWord3);
+}
+__device__ __forceinline__ uint32_t buf_bits(__amdgpu_buffer_rsrc_t r, uint32_t lane_bytes,
+                                             uint32_t voxel_bytes) {
+  return __builtin_amdgcn_raw_buffer_load_b16(r, lane_bytes, voxel_bytes, 0);
+}
+
 template <int KH, int KW, int MODE>
 __global__ __launch_bounds__(64 * kRowWaves) void dwconv_block_dot2_kernel(
     ConvArgs a, const bf16* __restrict__ in, const bf16* __restrict__ wt,
@@ -278,6 +295,11 @@ __global__ __launch_bounds__(64 * kRowWaves) void dwconv_block_dot2_kernel(
   const int b = static_cast<int>(bt / a.T);
   const int h0 = hb * R, w0 = run * kRun;
   const int K = a.kt * KH * KW;
+  // wide rows (kw >= 5) through a buffer resource; three-tap rows, whose
+  // loads outnumber their products, measured faster with plain loads
+  constexpr bool kBuf = KW >= 5;
+  const __amdgpu_buffer_rsrc_t xr = bf16_rows(in, kBuf ? a.B * a.N * a.C : 0);
+  const uint32_t lb = lc * 2u, cb = static_cast<uint32_t>(a.C) * 2u;  // lane, voxel bytes
   const int64_t rowstride = static_cast<int64_t>(a.W) * a.C;
 
   float acc[R][kRun];
@@ -306,17 +328,20 @@ __global__ __launch_bounds__(64 * kRowWaves) void dwconv_block_dot2_kernel(
       wl[dh] = ldu(wt + (flip ? K - 1 - tl : tl), lc * K);
     }
     const bf16* plane = in + (static_cast<int64_t>(b) * a.T + tt) * a.H * rowstride;
+    const uint32_t plane_v = static_cast<uint32_t>((b * a.T + tt) * a.H);  // row index of hh = 0
 #pragma unroll
     for (int ii = 0; ii < R + KH - 1; ++ii) {
       const int hh = h0 + ii - PH;
       if (hh < 0 || hh >= a.H) continue;
       const bf16* row = plane + hh * rowstride;
+      const uint32_t row_v = (plane_v + hh) * static_cast<uint32_t>(a.W);  // voxel of ww = 0
       uint32_t xb[NX];
 #pragma unroll
       for (int j = 0; j < NX; ++j) {
         const int ww = w0 + j - PW;
         const int wc = min(max(ww, 0), a.W - 1);
-        const uint32_t v = ldu_bits(row + static_cast<int64_t>(wc) * a.C, lc);
+        const uint32_t v = kBuf ? buf_bits(xr, lb, (row_v + wc) * cb)
+                                : ldu_bits(row + static_cast<int64_t>(wc) * a.C, lc);
         xb[j] = ww == wc ? v : 0u;
       }
       uint32_t xp[NX - 1];
@@ -981,12 +1006,16 @@ void launch_block(const ConvArgs& a, const G* in, const T* w, const T* b, const 
   const int64_t items = static_cast<int64_t>(a.B) * a.T * hblocks * runs;
   const dim3 grid(static_cast<unsigned>((items + kRowWaves - 1) / kRowWaves),
                   static_cast<unsigned>((a.C + 63) / 64));
-  if constexpr (std::is_same<T, bf16>::value && std::is_same<G, bf16>::value)
-    hipLaunchKernelGGL((dwconv_block_dot2_kernel<KS, KS, MODE>), grid, dim3(64 * kRowWaves), 0, s,
-                       a, in, w, b, dy, out, out2, flip);
-  else
-    hipLaunchKernelGGL((dwconv_block_kernel<T, G, KS, KS, MODE>), grid, dim3(64 * kRowWaves), 0, s,
-                       a, in, w, b, dy, out, out2, flip);
+  if constexpr (std::is_same<T, bf16>::value && std::is_same<G, bf16>::value) {
+    // the dot2 kernel's wide rows are addressed with 32-bit buffer offsets
+    if (KS < 5 || static_cast<int64_t>(a.B) * a.N * a.C * 2 < kBufMaxBytes) {
+      hipLaunchKernelGGL((dwconv_block_dot2_kernel<KS, KS, MODE>), grid, dim3(64 * kRowWaves), 0,
+                         s, a, in, w, b, dy, out, out2, flip);
+      return;
+    }
+  }
+  hipLaunchKernelGGL((dwconv_block_kernel<T, G, KS, KS, MODE>), grid, dim3(64 * kRowWaves), 0, s,
+                     a, in, w, b, dy, out, out2, flip);
 }
 
 // conv of `in` (type G) with w (flip: mirrored taps), epilogue MODE
