@@ -64,7 +64,9 @@ def build(verbose: bool = False) -> str:
         objs = list(ex.map(_compile, SOURCES))
     out = os.path.join(LIB_DIR, LIB_NAME)
     tmp = out + ".tmp"
-    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
+    # -z defs: every symbol resolved at link time (a kernel whose host-side
+    # launch stub was not emitted would otherwise only fail when loaded)
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,-z,defs", *objs, "-o", tmp]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")

@@ -510,7 +510,8 @@ __global__ __launch_bounds__(kThreads, (p1_min_waves<HD, E>())) void dsa3d_bwd_p
   // the output addresses are formed here, from an opaque copy of the query's
   // token row, rather than hoisted before the plane loop (where they spill)
   uint32_t qlo = static_cast<uint32_t>(tl.qn), qhi = static_cast<uint32_t>(tl.qn >> 32);
-  asm volatile("" : "+v"(qlo), "+v"(qhi));
+  int sub = tl.sub;  // (and the taps' offsets within the row)
+  asm volatile("" : "+v"(qlo), "+v"(qhi), "+v"(sub));
   const int64_t qn = static_cast<int64_t>((static_cast<uint64_t>(qhi) << 32) | qlo);
   const int64_t tap0 = (qn * a.nh + tl.head) * a.K;
   delta = s_dl[tl.q][0];  // written before the loop's first barrier
@@ -543,7 +544,7 @@ __global__ __launch_bounds__(kThreads, (p1_min_waves<HD, E>())) void dsa3d_bwd_p
   for (int i = 0; i < kSlots; ++i) {
     if (slot_z0(sl[i]) < 0) continue;
     const float pd = s_[i], dss = dp_[i];
-    const int kap = tl.sub + kSubs * i;
+    const int kap = sub + kSubs * i;
     if constexpr (sizeof(E) == 4) {
       p_ws[tap0 + kap] = pd;
       b_ws[tap0 + kap] = dss;
