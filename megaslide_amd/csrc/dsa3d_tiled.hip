@@ -507,15 +507,16 @@ __global__ __launch_bounds__(kThreads, (p1_min_waves<HD, E>())) void dsa3d_bwd_p
   // a tap is ds*scale*dS/du + p*dP/du; chain it through the clamp mask, the
   // unnormalisation (S/2), the slot divisor and offset_scale into d offsets.
   const float cxs = a.gsx, cys = a.gsy, czs = a.gsz;
-  // the output addresses are formed here, from an opaque copy of the query's
-  // token row, rather than hoisted before the plane loop (where they spill)
-  uint32_t qlo = static_cast<uint32_t>(tl.qn), qhi = static_cast<uint32_t>(tl.qn >> 32);
-  int sub = tl.sub;  // (and the taps' offsets within the row)
-  asm volatile("" : "+v"(qlo), "+v"(qhi), "+v"(sub));
-  const int64_t qn = static_cast<int64_t>((static_cast<uint64_t>(qhi) << 32) | qlo);
+  // the query's token row and the taps' offsets are recomputed here from the
+  // wave (a scalar) and the lane id: kept from before the plane loop, they
+  // spill (as does the thread index register)
+  const int tid = 64 * __builtin_amdgcn_readfirstlane(tl.wave) +
+                  static_cast<int>(__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)));
+  const int sub = tid % kSubs;
+  const int64_t qn = tile_row(a, tl, tid / kSubs);
   const int64_t tap0 = (qn * a.nh + tl.head) * a.K;
-  delta = s_dl[tl.q][0];  // written before the loop's first barrier
-  lse_q = s_dl[tl.q][1];
+  delta = s_dl[tid / kSubs][0];  // written before the loop's first barrier
+  lse_q = s_dl[tid / kSubs][1];
   // p * factor and ds * scale of every tap (0 for empty slots), in place of s and dp
 #pragma unroll
   for (int i = 0; i < kSlots; ++i) {
@@ -538,7 +539,7 @@ __global__ __launch_bounds__(kThreads, (p1_min_waves<HD, E>())) void dsa3d_bwd_p
 #pragma unroll
     for (int m = 1; m < kSubs; m <<= 1) l1 += __shfl_xor(l1, m);
     rl1 = l1 > 1e-30f ? 1.0f / l1 : 0.0f;
-    if (tl.sub == 0 && tl.q_ok) b_ws[qn * a.nh + tl.head] = l1;
+    if (sub == 0 && qn >= 0) b_ws[qn * a.nh + tl.head] = l1;
   }
 #pragma unroll
   for (int i = 0; i < kSlots; ++i) {
