@@ -43,6 +43,7 @@ def reference(x, w, b, vs, act):
     (1, 2, 6, 70, 16, (3, 5, 5), "gelu"),   # W = 70, kw = 5: dot2 (bands would be 2 rows)
     (1, 4, 6, 48, 16, (3, 5, 5), "gelu"),   # kw = 5 on the matrix cores: 2 segments, bands 4 + 2
     (1, 4, 9, 32, 64, (3, 7, 7), None),     # the long-clip row width on the matrix cores: bands 4+4+1
+    (1, 2, 8, 64, 64, (3, 7, 7), None),     # the large-block row width: the dot2 weight gradient
     (2, 1, 9, 50, 32, (1, 5, 5), None),     # kt = 1 on the matrix cores: 2 segments, bands 8 + 1
 ])
 def test_dwconv_matches_conv3d(cfg, dtype, tol):
