@@ -504,15 +504,20 @@ __global__ __launch_bounds__(64 * kRowWaves) void dwconv_dw_block_dot2_kernel(
   const bool c_ok = c < a.C;
   const uint32_t lc = c_ok ? c : a.C - 1;
   const int K = a.kt * KH * KW;
-  const int64_t rowstride = static_cast<int64_t>(a.W) * a.C;
+  // x and dz rows through buffer resources (lane channel as vector offset,
+  // voxel as scalar offset); the host admits tensors below 2^31 bytes
+  const __amdgpu_buffer_rsrc_t xr = bf16_rows(x, a.B * a.N * a.C);
+  const __amdgpu_buffer_rsrc_t gr = bf16_rows(dz, a.B * a.N * a.C);
+  const uint32_t lb = lc * 2u, cb = static_cast<uint32_t>(a.C) * 2u;
   float s[KH][KW];
 #pragma unroll
   for (int dh = 0; dh < KH; ++dh)
 #pragma unroll
     for (int k = 0; k < KW; ++k) s[dh][k] = 0.0f;
   float sb = 0.0f;
-  const bf16* plane = x + (static_cast<int64_t>(b) * a.T + (plane_ok ? tt : 0)) * a.H * rowstride;
-  const bf16* gplane = dz + (static_cast<int64_t>(b) * a.T + t) * a.H * rowstride;
+  // row indices of h = 0 in the x plane tt and the dz plane t
+  const uint32_t plane = static_cast<uint32_t>((b * a.T + (plane_ok ? tt : 0)) * a.H);
+  const uint32_t gplane = static_cast<uint32_t>((b * a.T + t) * a.H);
   const int hb_end = min(hblocks, (strip + 1) * kDwStripBlocks);
   for (int hb = strip * kDwStripBlocks; hb < hb_end; ++hb) {
     const int h0 = hb * R;
@@ -525,11 +530,11 @@ __global__ __launch_bounds__(64 * kRowWaves) void dwconv_dw_block_dot2_kernel(
         for (int jp = 0; jp < JP; ++jp) {
           uint32_t lo = 0u, hi = 0u;
           if (h < a.H) {
-            const bf16* grow = gplane + h * rowstride;
+            const uint32_t grow = (gplane + h) * static_cast<uint32_t>(a.W);
             const int w = w0 + 2 * jp;
             const int wl = min(w, a.W - 1), wh = min(w + 1, a.W - 1);
-            lo = w < a.W ? ldu_bits(grow + static_cast<int64_t>(wl) * a.C, lc) : 0u;
-            hi = w + 1 < a.W ? ldu_bits(grow + static_cast<int64_t>(wh) * a.C, lc) : 0u;
+            lo = w < a.W ? buf_bits(gr, lb, (grow + wl) * cb) : 0u;
+            hi = w + 1 < a.W ? buf_bits(gr, lb, (grow + wh) * cb) : 0u;
           }
           gp[r][jp] = lo | (hi << 16);
           if (dt == 0) sb += __uint_as_float(lo << 16) + __uint_as_float(hi << 16);
@@ -540,13 +545,13 @@ __global__ __launch_bounds__(64 * kRowWaves) void dwconv_dw_block_dot2_kernel(
       for (int ii = 0; ii < R + KH - 1; ++ii) {
         const int hh = h0 + ii - PH;
         if (hh < 0 || hh >= a.H) continue;
-        const bf16* row = plane + hh * rowstride;
+        const uint32_t row = (plane + hh) * static_cast<uint32_t>(a.W);
         uint32_t xb[NX];
 #pragma unroll
         for (int j = 0; j < NX; ++j) {
           const int ww = w0 + j - PW;
           const int wc = min(max(ww, 0), a.W - 1);
-          const uint32_t v = ldu_bits(row + static_cast<int64_t>(wc) * a.C, lc);
+          const uint32_t v = buf_bits(xr, lb, (row + wc) * cb);
           xb[j] = ww == wc ? v : 0u;
         }
         uint32_t xp[NX - 1];
@@ -1074,11 +1079,15 @@ void launch_dw_block(const ConvArgs& a, const T* x, const G* dz, float* acc, hip
                          static_cast<unsigned>(dwm_lds_bytes(g)), s, a, g, x, dz, acc);
       return;
     }
-    hipLaunchKernelGGL((dwconv_dw_block_dot2_kernel<KS, KS>), grid, dim3(64 * kRowWaves), 0, s, a,
-                       x, dz, acc);
-  } else
-    hipLaunchKernelGGL((dwconv_dw_block_kernel<T, G, KS, KS>), grid, dim3(64 * kRowWaves), 0, s, a,
-                       x, dz, acc);
+    // the dot2 kernel addresses its rows with 32-bit buffer offsets
+    if (static_cast<int64_t>(a.B) * a.N * a.C * 2 < kBufMaxBytes) {
+      hipLaunchKernelGGL((dwconv_dw_block_dot2_kernel<KS, KS>), grid, dim3(64 * kRowWaves), 0, s,
+                         a, x, dz, acc);
+      return;
+    }
+  }
+  hipLaunchKernelGGL((dwconv_dw_block_kernel<T, G, KS, KS>), grid, dim3(64 * kRowWaves), 0, s, a,
+                     x, dz, acc);
 }
 
 template <typename T, typename G>
