@@ -223,7 +223,7 @@ __global__ __launch_bounds__(kThreads, (fwd_min_waves<HD, E>())) void dsa3d_fwd_
   // ---- pass 2: O += A . V over the taps --------------------------------------
   StageRows<kThreads, HD, E> vr;
   w = walk_begin(box);
-  if (nit > 0) load_stage_rows<kThreads, HD, E>(a, tl, w.c, w.z, vp, a.vs, tl.head * HD, vr);
+  if (nit > 0) load_stage_rows<kThreads, HD, E, true>(a, tl, w.c, w.z, vp, a.vs, tl.head * HD, vr);
   __syncthreads();  // pass-1 reads of both buffers are done
   zero_table(s_tab[0], kChunkNV);
   for (int it = 0; it < nit; ++it) {
@@ -236,7 +236,7 @@ __global__ __launch_bounds__(kThreads, (fwd_min_waves<HD, E>())) void dsa3d_fwd_
     __syncthreads();  // the previous step's MFMAs are done with V^T; this buffer is zeroed
     store_stage<kThreads, HD, E>(c, vr, s_vt);
     if (it + 1 < nit)
-      load_stage_rows<kThreads, HD, E>(a, tl, wn.c, wn.z, vp, a.vs, tl.head * HD, vr);
+      load_stage_rows<kThreads, HD, E, true>(a, tl, wn.c, wn.z, vp, a.vs, tl.head * HD, vr);
 #pragma unroll
     for (int i = 0; i < kSlots; ++i) {
       const Slot si = fwd_slot<HD>(sl[i]);
