@@ -14,6 +14,7 @@
 // the sampled rows.  Coordinates and corner choice round exactly as the fp32
 // reference does (div_rn, dsa3d_coords.h).
 #include <algorithm>
+#include <type_traits>
 
 #include "dsa3d_tiled_common.h"
 
@@ -675,7 +676,10 @@ __device__ __forceinline__ void p2_tile(const Args& a, int tile, const E* __rest
   __shared__ __attribute__((aligned(16))) int s_ab[2 * kTab];
   int* const s_at = s_ab;
   int* const s_bt = s_ab + kTab;
-  __shared__ __attribute__((aligned(16))) word_t<E> s_kt[CW * KR];      // K^T chunk
+  // K^T chunk: a 96-channel window stages it in two rounds (64 + 32 channels)
+  // through one 64-channel buffer, so the whole hd-96 head fits one window
+  constexpr int KW = CW == 96 ? 64 : CW;  // channels of the first round
+  __shared__ __attribute__((aligned(16))) word_t<E> s_kt[KW * KR];
   // per voxel: its token row within the sample
   __shared__ __attribute__((aligned(16))) int s_rows[kChunkNV];
   __shared__ int s_red[NW][6];
@@ -771,16 +775,16 @@ __device__ __forceinline__ void p2_tile(const Args& a, int tile, const E* __rest
   }
   __syncthreads();
 
-  // dq (16x16x32 MFMA).  CW = 64 (and 32 at three frames): wave w takes
+  // dq (16x16x32 MFMA).  CW = 64 or 96 (and 32 at three frames): wave w takes
   // frame w / 4 and the voxel k-steps w % 4, + 4, ... for all CT channel
-  // tiles, so one converted B
-  // operand feeds CT MFMA pairs; the 4 partial dq are summed at the end.
+  // tiles (at 96 in two rounds, one per staged K^T part), so one converted B
+  // operand feeds several MFMA pairs; the 4 partial dq are summed at the end.
   // Wider windows (registers): task t = (frame t / CT, channels 16*(t % CT) +
   // [0, 16)) for t = w + 8 j over all k-steps.  dK/dV (32x32x16 MFMA, one per
   // frame): task t = (channels 32*(t % NC2) + [0, 32), 32-voxel block t / NC2)
   // for t = w + 8 i.
   constexpr int CT = CW / 16, NC2 = CW / 32;
-  constexpr bool DQK = CW == 64 || (CW == 32 && FR == 3);  // k-split dq
+  constexpr bool DQK = CW == 64 || CW == 96 || (CW == 32 && FR == 3);  // k-split dq
   constexpr int KPQ = NW / kP2Frames;  // k phases per frame (k-split dq)
   constexpr int NDQ = DQK ? CT : (kP2Frames * CT + NW - 1) / NW;  // dq accumulators
   const int mq = tl.lane & 15, kq = 8 * (tl.lane >> 4);
@@ -796,13 +800,19 @@ __device__ __forceinline__ void p2_tile(const Args& a, int tile, const E* __rest
   const float sc_v = MODE == kP2F16 ? scales[2] : 1.0f;
   // The step's K rows are loaded first and stored to LDS after the table
   // scatter (below)
-  StageRows<kP2Stage, CW, E> kr;
+  StageRows<kP2Stage, KW, E> kr;
+  StageRows<kP2Stage, CW - KW == 0 ? 32 : CW - KW, E> kr2;  // second round (CW = 96)
   Walk w = walk_begin(box);
   for (int it = 0; it < nit; ++it) {
     const Walk wn = walk_next(box, w);
     const Chunk& c = w.c;
     const int z = w.z;
-    load_stage_rows<kP2Stage, CW, E>(a, tl, c, z, kp, a.ks, cw0, kr);
+    // (the redo of dK / dV alone needs no K)
+    if constexpr (MODE != kP2Redo) {
+      load_stage_rows<kP2Stage, KW, E>(a, tl, c, z, kp, a.ks, cw0, kr);
+      if constexpr (KW < CW)
+        load_stage_rows<kP2Stage, CW - KW, E>(a, tl, c, z, kp, a.ks, cw0 + KW, kr2);
+    }
     // zero the transposed A and B tables; token rows of the chunk's voxels
     for (int e = threadIdx.x; e < c.nvp * kP2Row / 4; e += NT) {
       const u32x4_t zz = {0u, 0u, 0u, 0u};
@@ -844,22 +854,34 @@ __device__ __forceinline__ void p2_tile(const Args& a, int tile, const E* __rest
     }
     // the K rows are stored only now: their load waits for every atomic this
     // wave issued before it (one in-order counter), which the scatter overlaps
-    store_stage<kP2Stage, CW, E>(c, kr, s_kt);
+    if constexpr (MODE != kP2Redo) store_stage<kP2Stage, KW, E>(c, kr, s_kt);
     __syncthreads();
     // dq[q] += sum_v B[q][v] K[v]; in bf16, B as a hi/lo pair because
     // sum_v B[q][v] = 0 and K may carry a large common part
     if constexpr (MODE == kP2Redo) {
     } else if constexpr (DQK) {
       const int fq = tl.wave / KPQ;
-      for (int kc = 32 * (tl.wave % KPQ); kc < c.nvp; kc += 32 * KPQ) {
-        float bq[8];  // fixed-point units; the query's scale is applied to dq at the end
+      // the channel tiles of the staged K^T rounds: [0, KW / 16), then [KW / 16, CT)
+      auto dq_round = [&](auto ct0_c, auto ct1_c) {
+        constexpr int ct0 = decltype(ct0_c)::value, ct1 = decltype(ct1_c)::value;
+        for (int kc = 32 * (tl.wave % KPQ); kc < c.nvp; kc += 32 * KPQ) {
+          float bq[8];  // fixed-point units; the query's scale is applied to dq at the end
 #pragma unroll
-        for (int jj = 0; jj < 8; ++jj)
-          bq[jj] = static_cast<float>(s_bt[(kc + kq + jj) * kP2Row + kTQ * fq + mq]);
-        const PreciseOp<E> bp = precise_op<E>(bq);
+          for (int jj = 0; jj < 8; ++jj)
+            bq[jj] = static_cast<float>(s_bt[(kc + kq + jj) * kP2Row + kTQ * fq + mq]);
+          const PreciseOp<E> bp = precise_op<E>(bq);
 #pragma unroll
-        for (int ct = 0; ct < CT; ++ct)
-          dq_acc[ct] = mma16(bp, load_op<E>(&s_kt[(16 * ct + mq) * KR + kc + kq]), dq_acc[ct]);
+          for (int ct = ct0; ct < ct1; ++ct)
+            dq_acc[ct] = mma16(bp, load_op<E>(&s_kt[(16 * (ct - ct0) + mq) * KR + kc + kq]),
+                               dq_acc[ct]);
+        }
+      };
+      dq_round(std::integral_constant<int, 0>{}, std::integral_constant<int, KW / 16>{});
+      if constexpr (KW < CW) {
+        __syncthreads();  // every wave is done with the first round's K^T
+        store_stage<kP2Stage, CW - KW, E>(c, kr2, s_kt);
+        __syncthreads();
+        dq_round(std::integral_constant<int, KW / 16>{}, std::integral_constant<int, CT>{});
       }
     } else {
 #pragma unroll
@@ -911,8 +933,8 @@ __device__ __forceinline__ void p2_tile(const Args& a, int tile, const E* __rest
     // dq_acc[ct][r] = partial dq[query 16*fq + 4*(lane/16) + r][channel 16*ct +
     // lane%16] of k phase w % 4; the A^T table (free after the loop's last
     // barrier) takes the partials, and every thread sums 4 for its outputs
-    float* red = reinterpret_cast<float*>(s_at);  // [frame][k phase][16][CW]
-    static_assert(NW * kTQ * CW <= kChunkNV * kP2Row, "partials fit the A^T table");
+    float* red = reinterpret_cast<float*>(s_ab);  // [frame][k phase][16][CW]
+    static_assert(NW * kTQ * CW <= 2 * kTab, "partials fit the tables");
     const int fq = tl.wave / KPQ, kph = tl.wave % KPQ;
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct)
@@ -1497,10 +1519,9 @@ __global__ __launch_bounds__(256) void fill_zero_if_flag(float* __restrict__ p, 
 }
 
 namespace {
-// Frames per tile of the second kernel: 3 for bf16 head_dim 64 and 128 (at
-// the 131,072-token hd-128 shape three frames in two 64-channel windows ran
-// 15% faster than two frames in one window), else 2 (bf16 hd 96 would need
-// three 32-channel windows for three frames: 8% slower; hd 32 would spill).
+// Frames per tile of the second kernel: 3 for bf16 head_dim 64, 96 and 128
+// (at the 131,072-token hd-128 shape three frames in two 64-channel windows
+// ran 15% faster than two frames in one window), else 2 (hd 32 would spill).
 template <int HD, typename E>
 constexpr int p2_frames() {
   return sizeof(E) == 2 && (HD == 64 || HD == 96 || HD == 128) ? 3 : 2;
@@ -1508,12 +1529,14 @@ constexpr int p2_frames() {
 
 // Channel window of the second backward kernel: the whole head where the LDS
 // takes its K^T and q/dO stages beside the tables, else 64 channels (32 for
-// fp32 head_dim 96).  bf16 head_dim 96 at three frames runs a 64- and a
-// 32-channel window (two launches): 8% faster than two frames over the whole
-// head at the 46,800-token DiT-block shape.
+// fp32 head_dim 96).  bf16 head_dim 96 at three frames stages its K^T in two
+// rounds (64 + 32 channels) through one buffer: one window instead of a 64-
+// and a 32-channel launch, which repeated the setup, scatter and table work
+// (9.8 -> 7.0 ms at the 46,800-token hd-96 shape, 15.8 -> 12.6 ms with
+// offsets biased by up to 4 voxels).
 template <int HD, typename E>
 constexpr int p2_window() {
-  if constexpr (sizeof(E) == 2) return p2_frames<HD, E>() == 3 && HD > 64 ? 64 : HD;
+  if constexpr (sizeof(E) == 2) return HD == 128 ? 64 : HD;
   return HD % 64 == 0 ? 64 : 32;
 }
 
@@ -1574,12 +1597,7 @@ void launch_bwd_pair(const msd_dsa3d_desc& d, const void* q, const void* k, cons
   constexpr int MODE = kH16 ? kP2F16 : kP2F32;
   hipLaunchKernelGGL((dsa3d_bwd_p2_kernel<HD, CW, E, FR, MODE>), g2, dim3(P2Tile<FR>::Threads), 0,
                      s, a2, go, p_ws, b_ws, gq, dk_acc, dv_acc, acc_ks, acc_vs, 0, w.scales);
-  if constexpr (HD % CW != 0) {  // bf16 head_dim 96: a 64- and a 32-channel window
-    g2.z = 1;
-    hipLaunchKernelGGL((dsa3d_bwd_p2_kernel<HD, HD % CW, E, FR, MODE>), g2,
-                       dim3(P2Tile<FR>::Threads), 0, s, a2, go, p_ws, b_ws, gq, dk_acc, dv_acc,
-                       acc_ks, acc_vs, CW * (HD / CW), w.scales);
-  }
+  static_assert(HD % CW == 0, "channel windows tile the head");
   if (d.extra_g > 0) {
     // dEK, dEV: about 1,024 workgroups of token ranges that are multiples of 32
     const int64_t N = static_cast<int64_t>(d.T) * d.H * d.W;
@@ -1605,18 +1623,11 @@ void launch_bwd_redo(const msd_dsa3d_desc& d, const void* q, const void* k, cons
   const int64_t n = 2 * rows * d.num_heads * HD;  // dK then dV rows, contiguous
   hipLaunchKernelGGL(fill_zero_if_flag, dim3(512), dim3(256), 0, s, w.dk32, n, w.flag);
   // one workgroup per CU over all heads and windows; each strides over the tiles
-  const int per = std::max(1, 256 / (d.num_heads * (HD / CW + (HD % CW != 0 ? 1 : 0))));
+  const int per = std::max(1, 256 / (d.num_heads * (HD / CW)));
   dim3 g(static_cast<unsigned>(std::min<int64_t>(per, tiles)), d.num_heads, HD / CW);
   hipLaunchKernelGGL((dsa3d_bwd_p2_redo_kernel<HD, CW, E, FR>), g, dim3(P2Tile<FR>::Threads), 0,
                      s, a2, go, w.p_ws, w.b_ws, w.dk32, w.dv32, int64_t{d.num_heads} * HD,
                      int64_t{d.num_heads} * HD, 0, w.flag, static_cast<int>(tiles));
-  if constexpr (HD % CW != 0) {
-    g.z = 1;
-    hipLaunchKernelGGL((dsa3d_bwd_p2_redo_kernel<HD, HD % CW, E, FR>), g,
-                       dim3(P2Tile<FR>::Threads), 0, s, a2, go, w.p_ws, w.b_ws, w.dk32, w.dv32,
-                       int64_t{d.num_heads} * HD, int64_t{d.num_heads} * HD, CW * (HD / CW), w.flag,
-                       static_cast<int>(tiles));
-  }
 }
 
 // fp32 dK (blockIdx.y 0) or dV (1) accumulator [rows, D] -> bf16 with the
