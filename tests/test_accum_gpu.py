@@ -52,15 +52,17 @@ def test_gradient_magnitudes_match_oracle(dout_scale):
         assert e < BF16_TOL, name
 
 
-def test_overflowing_pile_up_is_redone_in_fp32():
+@pytest.mark.parametrize("hd", [64, 96, 128])
+def test_overflowing_pile_up_is_redone_in_fp32(hd):
     """Every tap of 8,192 queries clamps onto the volume's far corner (offsets
     +1000 voxels on every axis): each query's softmax weights sum to 1 on that
     one voxel, so dV[corner] = sum_q dO_q = 8,192 with dO = 1, and dV is zero
     elsewhere.  At the accumulator's scale that sum is far beyond the fp16
-    range: the result must come from the fp32 redo, exact and finite."""
-    B, T, H, W, nh, hd = 1, 8, 32, 32, 2, 64
+    range: the result must come from the fp32 redo, exact and finite (head_dim
+    96: one 96-channel window; 128: two 64-channel windows)."""
+    B, T, H, W, nh = 1, 8, 32, 32, 2
     N, D, C = T * H * W, nh * hd, nh * 147 * 3
-    print("[fp16 overflow -> fp32 redo] 8192 queries on one voxel", flush=True)
+    print(f"[fp16 overflow -> fp32 redo] 8192 queries on one voxel, head_dim {hd}", flush=True)
     g = torch.Generator(device=DEV).manual_seed(3)
     q, k, v = (torch.randn(B, N, D, generator=g, device=DEV).to(torch.bfloat16).requires_grad_(True)
                for _ in range(3))
