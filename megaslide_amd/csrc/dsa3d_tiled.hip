@@ -29,19 +29,27 @@ using namespace tiled;
 // still be read for the previous step, so pass 1 needs one barrier per step and
 // pass 2 two (instead of two and three).  bf16 head_dim 96 keeps one buffer:
 // two would drop it to one workgroup per CU (measured 30% slower).  bf16
-// head_dim 128 and every fp32 head stage too much V^T for two workgroups per
-// CU; they run one, with the register cap raised to match.
+// head_dim 128 without extra keys stages V^T in two 64-channel rounds per
+// step, which leaves room for two workgroups per CU; with extra keys it, and
+// every fp32 head, stages too much V^T for two and runs one, with the
+// register cap raised to match.
 constexpr int kLdsBytes = 160 * 1024;
 constexpr int kTabBytes = kTQ * kSRow * 4;
 
-template <int HD, typename E>
-constexpr int fwd_vt_bytes() {
-  return HD * ElemT<E>::kRow * static_cast<int>(sizeof(word_t<E>));
+template <int HD, typename E, bool XK>
+constexpr bool fwd_half_v() {
+  return sizeof(E) == 2 && HD == 128 && !XK;
 }
 
-template <int HD, typename E>
+template <int HD, typename E, bool XK = false>
+constexpr int fwd_vt_bytes() {
+  return (fwd_half_v<HD, E, XK>() ? HD / 2 : HD) * ElemT<E>::kRow *
+         static_cast<int>(sizeof(word_t<E>));
+}
+
+template <int HD, typename E, bool XK = false>
 constexpr int fwd_table_bufs() {
-  constexpr int vt = fwd_vt_bytes<HD, E>();
+  constexpr int vt = fwd_vt_bytes<HD, E, XK>();
   if (2 * (2 * kTabBytes + vt) <= kLdsBytes) return 2;  // two workgroups per CU
   if (2 * (kTabBytes + vt) <= kLdsBytes) return 1;      // two workgroups per CU
   return 2 * kTabBytes + vt <= kLdsBytes ? 2 : 1;       // one workgroup per CU
@@ -49,10 +57,12 @@ constexpr int fwd_table_bufs() {
 
 // Minimum waves per SIMD: 4 when two 512-thread workgroups fit in a CU's LDS
 // (bf16; the fp32 operands need more than 128 registers).
-template <int HD, typename E>
+template <int HD, typename E, bool XK = false>
 constexpr int fwd_min_waves() {
   if constexpr (sizeof(E) == 4) return 2;
-  return 2 * (fwd_table_bufs<HD, E>() * kTabBytes + fwd_vt_bytes<HD, E>()) <= kLdsBytes ? 4 : 2;
+  return 2 * (fwd_table_bufs<HD, E, XK>() * kTabBytes + fwd_vt_bytes<HD, E, XK>()) <= kLdsBytes
+             ? 4
+             : 2;
 }
 
 // Slot words as used in the forward's plane loops: at head_dim 96 (128
@@ -67,12 +77,14 @@ __device__ __forceinline__ Slot fwd_slot(const Slot& s) {
 // XK: the call has extra keys (a.G > 0); without them the kernel compiles to
 // the plain tap path.
 template <int HD, typename E, bool XK>
-__global__ __launch_bounds__(kThreads, (fwd_min_waves<HD, E>())) void dsa3d_fwd_tiled_kernel(
+__global__ __launch_bounds__(kThreads, (fwd_min_waves<HD, E, XK>())) void dsa3d_fwd_tiled_kernel(
     Args a, E* __restrict__ out, float* __restrict__ lse) {
-  constexpr int NB = fwd_table_bufs<HD, E>();
+  constexpr int NB = fwd_table_bufs<HD, E, XK>();
   constexpr int VR = ElemT<E>::kRow;
+  constexpr bool kHV = fwd_half_v<HD, E, XK>();  // V^T in two 64-channel rounds
+  constexpr int VC = kHV ? HD / 2 : HD;           // V^T channels staged at once
   __shared__ __attribute__((aligned(16))) float s_tab[NB][kTQ * kSRow];  // S, then A
-  __shared__ __attribute__((aligned(16))) word_t<E> s_vt[HD * VR];      // V^T chunk
+  __shared__ __attribute__((aligned(16))) word_t<E> s_vt[VC * VR];      // V^T chunk
   __shared__ int s_red[kWaves][6];
 
   const Tile tl = make_tile<1, kSubs>(a);
@@ -222,6 +234,83 @@ __global__ __launch_bounds__(kThreads, (fwd_min_waves<HD, E>())) void dsa3d_fwd_
   }
 
   // ---- pass 2: O += A . V over the taps --------------------------------------
+  if constexpr (kHV) {
+    // channels [0, 64) then [64, 128) of each step's V^T through one buffer;
+    // wave w takes channel tile w % 4 of each round and the k-steps w / 4,
+    // + 2, ...; the two partial O are summed at the end
+    constexpr int RT = VC / 16, KPH = kWaves / RT;
+    const int tt = tl.wave % RT, kh2 = tl.wave / RT;
+    f32x4_t oh[2] = {f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}, f32x4_t{0.0f, 0.0f, 0.0f, 0.0f}};
+    StageRows<kThreads, VC, E> vh;
+    w = walk_begin(box);
+    if (nit > 0)
+      load_stage_rows<kThreads, VC, E, true>(a, tl, w.c, w.z, vp, a.vs, tl.head * HD, vh);
+    __syncthreads();  // pass-1 reads of both buffers are done
+    zero_table(s_tab[0], kChunkNV);
+    for (int it = 0; it < nit; ++it) {
+      const Walk wn = walk_next(box, w);
+      const Chunk& c = w.c;
+      const int z = w.z;
+      int* const s_atab = reinterpret_cast<int*>(s_tab[it % NB]);
+      int* row = &s_atab[tl.q * kSRow];
+      __syncthreads();  // the previous step's MFMAs are done with V^T; this buffer is zeroed
+      store_stage<kThreads, VC, E>(c, vh, s_vt);
+      load_stage_rows<kThreads, VC, E, true>(a, tl, c, z, vp, a.vs, tl.head * HD + VC, vh);
+#pragma unroll
+      for (int i = 0; i < kSlots; ++i) {
+        const Slot si = fwd_slot<HD>(sl[i]);
+        float wz, dwz;
+        if (!slot_hits(si, step_key(c.id, z), wz, dwz)) continue;
+        const float pz = sc[i] * wz;
+        const float gx = 1.0f - si.fx, gy = 1.0f - si.fy;
+        const int base = si.idx & 0x1ff, dy = (si.idx >> 9) & 0x1f, dx = (si.idx >> 14) & 1;
+        atomicAdd(&row[base], to_fix(pz * (gy * gx)));
+        atomicAdd(&row[base + dx], to_fix(pz * (gy * si.fx)));
+        atomicAdd(&row[base + dy], to_fix(pz * (si.fy * gx)));
+        atomicAdd(&row[base + dy + dx], to_fix(pz * (si.fy * si.fx)));
+      }
+      __syncthreads();
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        if (r == 1) {
+          __syncthreads();  // every wave is done with the first round's V^T
+          store_stage<kThreads, VC, E>(c, vh, s_vt);
+          if (it + 1 < nit)
+            load_stage_rows<kThreads, VC, E, true>(a, tl, wn.c, wn.z, vp, a.vs, tl.head * HD, vh);
+          __syncthreads();
+        }
+        for (int kc = 32 * kh2; kc < c.nvp; kc += 32 * KPH) {
+          const op_t<E> av = fix_to_op<E>(&s_atab[mq * kSRow + kc + kq]);
+          oh[r] = mma16(av, load_op<E>(&s_vt[(16 * tt + mq) * VR + kc + kq]), oh[r]);
+        }
+      }
+      if constexpr (NB == 1) __syncthreads();
+      if (it + 1 < nit) zero_table(s_tab[(it + 1) % NB], kChunkNV);
+      w = wn;
+    }
+    __syncthreads();
+    // oh[r][i] = partial O[query 4 (lane / 16) + i][channel 16 (4 r + tt) + lane % 16]
+    // of k phase kh2, through the (free) V^T buffer: red[k phase][16][HD]
+    float* red = reinterpret_cast<float*>(s_vt);
+    static_assert(KPH * kTQ * HD * 4 <= fwd_vt_bytes<HD, E, XK>(), "partials fit the V^T buffer");
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        red[(kh2 * kTQ + 4 * (tl.lane >> 4) + i) * HD + 16 * (RT * r + tt) + mq] = oh[r][i];
+    __syncthreads();
+    for (int e = threadIdx.x; e < kTQ * HD; e += kThreads) {
+      float o = 0.0f;
+#pragma unroll
+      for (int kp = 0; kp < KPH; ++kp) o += red[kp * kTQ * HD + e];
+      const int m = e / HD, ch = e - m * HD;
+      const int64_t n = tile_row(a, tl, m);
+      if (n >= 0)
+        out[n * (static_cast<int64_t>(a.nh) * HD) + tl.head * HD + ch] =
+            from_f32<E>(o * a.fix_a_inv);
+    }
+    return;
+  }
   StageRows<kThreads, HD, E> vr;
   w = walk_begin(box);
   if (nit > 0) load_stage_rows<kThreads, HD, E, true>(a, tl, w.c, w.z, vp, a.vs, tl.head * HD, vr);
@@ -272,7 +361,8 @@ __global__ __launch_bounds__(kThreads, (fwd_min_waves<HD, E>())) void dsa3d_fwd_
   // barrier above) takes the KP partials of every channel; every thread then
   // sums KP for its outputs, consecutive threads on consecutive channels.
   float* red = reinterpret_cast<float*>(s_vt);  // [k phase][16][HD]
-  static_assert(KP * kTQ * HD * 4 <= fwd_vt_bytes<HD, E>(), "partials fit the V^T buffer");
+  static_assert(kHV || KP * kTQ * HD * 4 <= fwd_vt_bytes<HD, E, XK>(),
+                "partials fit the V^T buffer");
   if (av_wave) {
 #pragma unroll
     for (int t = 0; t < TPW; ++t)
