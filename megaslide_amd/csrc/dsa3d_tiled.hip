@@ -403,14 +403,14 @@ constexpr int kP1Tab = kTQ * kSRow + kP1Zero;
 // coordinate derivatives, then writes the offset gradients and, for the second
 // kernel, p times its dropout factor and ds * softmax_scale of every tap (fp32,
 // [token][head][tap]).
-// Waves per SIMD of the first backward kernel.  bf16 up to head_dim 64 fits
-// 128 registers, so two workgroups share a CU and each hides the other's
-// latencies (barriers, table loads): q and dO then stay in LDS and K/V rows are
-// loaded at the step.  Larger heads and fp32 keep q/dO in registers and
-// prefetch the next step's rows, at one workgroup per CU.
+// Waves per SIMD of the first backward kernel.  bf16 fits 128 registers, so
+// two workgroups share a CU and each hides the other's latencies (barriers,
+// table loads): q and dO then stay in LDS and K/V rows are loaded at the step
+// (at head_dim 128 in two 64-channel halves per table block).  fp32 keeps q/dO
+// in registers and prefetches the next step's rows, at one workgroup per CU.
 template <int HD, typename E>
 constexpr int p1_min_waves() {
-  return sizeof(E) == 2 && HD <= 96 ? 4 : 2;
+  return sizeof(E) == 2 ? 4 : 2;
 }
 
 template <int HD, typename E>
@@ -552,6 +552,43 @@ __global__ __launch_bounds__(kThreads, (p1_min_waves<HD, E>())) void dsa3d_bwd_p
       const char* vo = head_origin<HD, E>(a, tl, c, z, vp, a.vs);
 #pragma nounroll
       for (int j = 0; j < 2; ++j) {
+        if constexpr (kTwoWg && HD == 128) {
+          // S and dP of block j over two 64-channel halves: a half's K/V rows
+          // and q/dO operands are 2 operands each (registers are the limit)
+          const int blk = tl.wave + kWaves * j;
+          if (blk * 16 >= c.nv) continue;  // wave-uniform: no voxel of the block
+          const int vi = blk * 16 + (tl.lane & 15);
+          const bool v_ok = vi < c.nv;
+          const int lc = 8 * (tl.lane >> 4);
+          const E* const pk = chunk_voxel<E>(ko, a, c, a.ks, lc, v_ok ? vi : 0);
+          const E* const pv = chunk_voxel<E>(vo, a, c, a.vs, lc, v_ok ? vi : 0);
+          f32x4_t as = {0.0f, 0.0f, 0.0f, 0.0f}, ad = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            op_t<E> yk[2], yv[2];
+#pragma unroll
+            for (int cc = 0; cc < 2; ++cc) {
+              yk[cc] = yv[cc] = zero_op<E>();
+              if (v_ok) {
+                yk[cc] = load_op<E>(pk + 64 * h + 32 * cc);
+                yv[cc] = load_op<E>(pv + 64 * h + 32 * cc);
+              }
+            }
+            const word_t<E>* const xq = &s_x[(tl.lane & 15) * XR + 64 * h + lc];
+            const word_t<E>* const xo = xq + kTQ * XR;
+#pragma unroll
+            for (int cc = 0; cc < 2; ++cc) {
+              as = mma16(load_op<E>(xq + 32 * cc), yk[cc], as);
+              ad = mma16(load_op<E>(xo + 32 * cc), yv[cc], ad);
+            }
+          }
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) {
+            tb[(4 * (tl.lane >> 4) + rr) * kSRow + vi] = as[rr];
+            tb[kP1Tab + (4 * (tl.lane >> 4) + rr) * kSRow + vi] = ad[rr];
+          }
+          continue;
+        }
         load_block_rows<HD, E>(a, tl, c, ko, a.ks, j, rk.y[0]);
         load_block_rows<HD, E>(a, tl, c, vo, a.vs, j, rv.y[0]);
         if constexpr (kTwoWg) {
