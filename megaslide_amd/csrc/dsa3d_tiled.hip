@@ -38,7 +38,7 @@ constexpr int kTabBytes = kTQ * kSRow * 4;
 
 template <int HD, typename E, bool XK>
 constexpr bool fwd_half_v() {
-  return sizeof(E) == 2 && HD == 128 && !XK;
+  return !XK && ((sizeof(E) == 2 && HD == 128) || (sizeof(E) == 4 && HD == 64));
 }
 
 template <int HD, typename E, bool XK = false>
@@ -59,7 +59,7 @@ constexpr int fwd_table_bufs() {
 // (bf16; the fp32 operands need more than 128 registers).
 template <int HD, typename E, bool XK = false>
 constexpr int fwd_min_waves() {
-  if constexpr (sizeof(E) == 4) return 2;
+  if constexpr (sizeof(E) == 4 && !fwd_half_v<HD, E, XK>()) return 2;
   return 2 * (fwd_table_bufs<HD, E, XK>() * kTabBytes + fwd_vt_bytes<HD, E, XK>()) <= kLdsBytes
              ? 4
              : 2;
@@ -419,7 +419,7 @@ constexpr int kP1Tab = kTQ * kSRow + kP1Zero;
 // in registers and prefetches the next step's rows, at one workgroup per CU.
 template <int HD, typename E>
 constexpr int p1_min_waves() {
-  return sizeof(E) == 2 ? 4 : 2;
+  return sizeof(E) == 2 || HD == 64 ? 4 : 2;
 }
 
 template <int HD, typename E>
@@ -561,9 +561,11 @@ __global__ __launch_bounds__(kThreads, (p1_min_waves<HD, E>())) void dsa3d_bwd_p
       const char* vo = head_origin<HD, E>(a, tl, c, z, vp, a.vs);
 #pragma nounroll
       for (int j = 0; j < 2; ++j) {
-        if constexpr (kTwoWg && HD == 128) {
-          // S and dP of block j over two 64-channel halves: a half's K/V rows
-          // and q/dO operands are 2 operands each (registers are the limit)
+        if constexpr (kTwoWg && HD * sizeof(E) == 256) {
+          // S and dP of block j over two channel halves (bf16 head_dim 128,
+          // fp32 64): a half's K/V rows and q/dO operands are HD / 64
+          // operands each (registers are the limit)
+          constexpr int OPH = HD / 64, CH = HD / 2;
           const int blk = tl.wave + kWaves * j;
           if (blk * 16 >= c.nv) continue;  // wave-uniform: no voxel of the block
           const int vi = blk * 16 + (tl.lane & 15);
@@ -574,19 +576,19 @@ __global__ __launch_bounds__(kThreads, (p1_min_waves<HD, E>())) void dsa3d_bwd_p
           f32x4_t as = {0.0f, 0.0f, 0.0f, 0.0f}, ad = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
           for (int h = 0; h < 2; ++h) {
-            op_t<E> yk[2], yv[2];
+            op_t<E> yk[OPH], yv[OPH];
 #pragma unroll
-            for (int cc = 0; cc < 2; ++cc) {
+            for (int cc = 0; cc < OPH; ++cc) {
               yk[cc] = yv[cc] = zero_op<E>();
               if (v_ok) {
-                yk[cc] = load_op<E>(pk + 64 * h + 32 * cc);
-                yv[cc] = load_op<E>(pv + 64 * h + 32 * cc);
+                yk[cc] = load_op<E>(pk + CH * h + 32 * cc);
+                yv[cc] = load_op<E>(pv + CH * h + 32 * cc);
               }
             }
-            const word_t<E>* const xq = &s_x[(tl.lane & 15) * XR + 64 * h + lc];
+            const word_t<E>* const xq = &s_x[(tl.lane & 15) * XR + CH * h + lc];
             const word_t<E>* const xo = xq + kTQ * XR;
 #pragma unroll
-            for (int cc = 0; cc < 2; ++cc) {
+            for (int cc = 0; cc < OPH; ++cc) {
               as = mma16(load_op<E>(xq + 32 * cc), yk[cc], as);
               ad = mma16(load_op<E>(xo + 32 * cc), yv[cc], ad);
             }
