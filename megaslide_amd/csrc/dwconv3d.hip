@@ -481,10 +481,20 @@ __global__ __launch_bounds__(64 * kRowWaves) void dwconv_dw_block_kernel(ConvArg
 // time, sum_j dz[j] x[j+k] as v_dot2 of the packed pairs (dz[j], dz[j+1]) and
 // (x[j+k], x[j+k+1]) (exact bf16 products into fp32); the packed dz block also
 // takes half the registers.
-template <int KH, int KW>
+// dz rows and columns per block of the dot2 weight gradient, per kernel size:
+// 2-row blocks for kw >= 5, where 4 rows of dz pairs beside the kh x kw sums
+// took 172 registers at 7x7 (2 waves per SIMD); at 124 (4 waves) the 3x7x7
+// backward went 6.13 -> 4.85 ms at 131,072 tokens for 60% more x-row loads
+// (8-column runs instead: 4.89 ms)
+template <int KS>
+constexpr int kDw2Rows = KS >= 5 ? 2 : kDwRows;
+template <int KS>
+constexpr int kDw2Run = kRun;
+
+template <int KH, int KW, int R = kDwRows, int RUN = kRun>
 __global__ __launch_bounds__(64 * kRowWaves) void dwconv_dw_block_dot2_kernel(
     ConvArgs a, const bf16* __restrict__ x, const bf16* __restrict__ dz, float* __restrict__ acc) {
-  constexpr int R = kDwRows, PH = KH / 2, PW = KW / 2, NX = kRun + KW - 1, JP = kRun / 2;
+  constexpr int PH = KH / 2, PW = KW / 2, NX = RUN + KW - 1, JP = RUN / 2;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int c = blockIdx.y * 64 + lane;
@@ -521,7 +531,7 @@ __global__ __launch_bounds__(64 * kRowWaves) void dwconv_dw_block_dot2_kernel(
   const int hb_end = min(hblocks, (strip + 1) * kDwStripBlocks);
   for (int hb = strip * kDwStripBlocks; hb < hb_end; ++hb) {
     const int h0 = hb * R;
-    for (int w0 = 0; w0 < a.W; w0 += kRun) {
+    for (int w0 = 0; w0 < a.W; w0 += RUN) {
       uint32_t gp[R][JP];  // (dz[2jp], dz[2jp+1]) of row r, packed bf16
 #pragma unroll
       for (int r = 0; r < R; ++r) {
@@ -1081,8 +1091,22 @@ void launch_dw_block(const ConvArgs& a, const T* x, const G* dz, float* acc, hip
     }
     // the dot2 kernel addresses its rows with 32-bit buffer offsets
     if (static_cast<int64_t>(a.B) * a.N * a.C * 2 < kBufMaxBytes) {
-      hipLaunchKernelGGL((dwconv_dw_block_dot2_kernel<KS, KS>), grid, dim3(64 * kRowWaves), 0, s,
-                         a, x, dz, acc);
+      auto go = [&]<int R2>() {
+        const int hb2 = (a.H + R2 - 1) / R2;
+        const int64_t items2 =
+            static_cast<int64_t>(a.B) * a.T * ((hb2 + kDwStripBlocks - 1) / kDwStripBlocks);
+        const dim3 grid2(static_cast<unsigned>((items2 + kRowWaves - 1) / kRowWaves),
+                         static_cast<unsigned>((a.C + 63) / 64), static_cast<unsigned>(a.kt));
+        hipLaunchKernelGGL((dwconv_dw_block_dot2_kernel<KS, KS, R2, kDw2Run<KS>>), grid2,
+                           dim3(64 * kRowWaves), 0, s, a, x, dz, acc);
+      };
+      // 3x3x3 rows wider than 32 voxels: 2-row blocks as well (0.61 -> 0.48 ms at
+      // the 46,800-token W = 80 shape, 2.97 -> 2.72 ms at 131,072 tokens; at
+      // W = 32, 4-row blocks stay 3% faster)
+      if (KS == 3 && a.W > 32)
+        go.template operator()<2>();
+      else
+        go.template operator()<kDw2Rows<KS>>();
       return;
     }
   }
