@@ -313,7 +313,7 @@ __global__ __launch_bounds__(64 * kRowWaves) void dwconv_block_dot2_kernel(
     const int tt = t + dt - a.kt / 2;
     if (tt < 0 || tt >= a.T) continue;
     uint32_t wp[KH][KP];  // taps (2kp, 2kp+1) of row dh, packed bf16
-    float wl[KH];         // tap KW-1
+    uint32_t wl[KH];      // tap KW-1 as the pair (w, 0): one dot2 with (x, 0)
 #pragma unroll
     for (int dh = 0; dh < KH; ++dh) {
       const int tap0 = (dt * KH + dh) * KW;
@@ -325,7 +325,7 @@ __global__ __launch_bounds__(64 * kRowWaves) void dwconv_block_dot2_kernel(
         wp[dh][kp] = lo | (hi << 16);
       }
       const int tl = tap0 + KW - 1;
-      wl[dh] = ldu(wt + (flip ? K - 1 - tl : tl), lc * K);
+      wl[dh] = ldu_bits(wt + (flip ? K - 1 - tl : tl), lc * K);
     }
     const bf16* plane = in + (static_cast<int64_t>(b) * a.T + tt) * a.H * rowstride;
     const uint32_t plane_v = static_cast<uint32_t>((b * a.T + tt) * a.H);  // row index of hh = 0
@@ -356,7 +356,8 @@ __global__ __launch_bounds__(64 * kRowWaves) void dwconv_block_dot2_kernel(
           float v = acc[r][j];
 #pragma unroll
           for (int kp = 0; kp < KP; ++kp) v = dot2_bf16(wp[dh][kp], xp[j + 2 * kp], v);
-          acc[r][j] = __builtin_fmaf(wl[dh], __uint_as_float(xb[j + KW - 1] << 16), v);
+          // xb holds the bf16 bits zero-extended: the pair (x, 0)
+          acc[r][j] = dot2_bf16(wl[dh], xb[j + KW - 1], v);
         }
       }
     }
