@@ -190,11 +190,12 @@ __global__ __launch_bounds__(kThreads, (fwd_min_waves<HD, E, XK>())) void dsa3d_
 #pragma unroll
   for (int i = 0; i < kSlots; ++i)
     sc[i] *= inv_den * slot_dropout(sl[i], a.drop) * a.fix_a;  // p (dropped), fixed-point units
-  if (lse != nullptr && tl.sub == 0 && HD != 128) {
+  if (lse != nullptr && tl.sub == 0 && !kHV) {
     if (tl.q_ok) lse[tl.qn * a.nh + tl.head] = mx + logf(den);
   } else if (lse != nullptr && tl.sub == 0) {
-    // head_dim 128: the query's token row rebuilt from the wave (a scalar) and
-    // the lane id (kept across the plane loop, it spilled)
+    // V^T in rounds (bf16 head_dim 128, fp32 64): the query's token row rebuilt
+    // from the wave (a scalar) and the lane id (kept across the plane loop, it
+    // spilled)
     const unsigned tid = 64u * static_cast<unsigned>(__builtin_amdgcn_readfirstlane(tl.wave)) +
                          __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
     const int64_t qn = tile_row(a, tl, static_cast<int>(tid / kSubs));
