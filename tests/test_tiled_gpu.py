@@ -167,3 +167,44 @@ def test_tiled_fp32_vs_oracle_and_direct(shape):
         print(f"  {name}: vs oracle {e_ref:.2e}  vs direct {e_dir:.2e}", flush=True)
         assert e_ref < FP32_TOL, name
         assert e_dir < FP32_TOL, name
+
+
+@pytest.mark.parametrize("hd,dtype", [(64, torch.bfloat16), (96, torch.bfloat16),
+                                      (128, torch.bfloat16), (64, torch.float32)])
+def test_tiled_tap_shifted_offsets(hd, dtype):
+    """Offsets that move whole taps apart, as an offset net's per-tap bias does
+    (each (head, tap) shifted by U(-4, 4) voxels per axis, plus N(0, 0.1) per
+    query): a tile's corners spread over a box of several chunks, part of whose
+    (chunk, plane) steps no corner reaches.  Every output and gradient must
+    match the oracle and the direct kernels."""
+    B, T, H, W, nh, ks, scale = 1, 6, 24, 24, 2, (3, 7, 7), 1.0
+    K = ks[0] * ks[1] * ks[2]
+    print(f"[tiled tap-shifted] hd {hd} {dtype}", flush=True)
+    q, k, v, _ = _inputs(B, T, H, W, nh, ks, 0.0, 900 + hd, hd=hd, dtype=dtype)
+    g = torch.Generator().manual_seed(31 + hd)
+    shift = torch.rand(nh, K, 3, generator=g) * 8.0 - 4.0
+    off = (shift.reshape(1, 1, -1) + 0.1 * torch.randn(B, T * H * W, nh * K * 3, generator=g))
+    off = off.to(dtype)
+    dout = torch.randn(q.shape, generator=g).to(dtype)
+    qq, kk, vv, oo = (t.float().clone().requires_grad_(True) for t in (q, k, v, off))
+    ref = dsa3d_core_ref(qq, kk, vv, oo, (T, H, W), nh, ks, scale)
+    ref.backward(dout.float())
+    grads, outs = {}, {}
+    for algo in ("tiled", "direct"):
+        ts = [t.to(DEV).requires_grad_(True) for t in (q, k, v, off)]
+        out = core()(*ts, (T, H, W), nh, ks, scale, algo=algo)
+        out.backward(dout.to(DEV))
+        outs[algo] = out.detach().float().cpu()
+        grads[algo] = [t.grad.float().cpu() for t in ts]
+    torch.cuda.synchronize()
+    tol = FP32_TOL if dtype == torch.float32 else BF16_TOL
+    e_out = rel_err(outs["tiled"], ref.detach())
+    print(f"  out: vs oracle {e_out:.2e}", flush=True)
+    assert e_out < tol
+    assert rel_err(outs["tiled"], outs["direct"]) < tol
+    for name, r, gt, gd in zip(("dq", "dk", "dv", "doff"), (qq.grad, kk.grad, vv.grad, oo.grad),
+                               grads["tiled"], grads["direct"]):
+        e_ref, e_dir = rel_err(gt, r), rel_err(gt, gd)
+        print(f"  {name}: vs oracle {e_ref:.2e}  vs direct {e_dir:.2e}", flush=True)
+        assert e_ref < tol, name
+        assert e_dir < tol, name
