@@ -91,6 +91,10 @@ __global__ __launch_bounds__(kThreads, (fwd_min_waves<HD, E, XK>())) void dsa3d_
   // the tile's q rows load while the slots are set up
   op_t<E> qx[HD / 32];
   load_rows_operand<HD, E>(a, tl, static_cast<const E*>(a.q), a.qs, qx);
+  // finite tables before the first step (the paired corner reads may read an
+  // entry no step has written yet); the setup's barrier orders this before
+  // the first table store
+  zero_tables_all<NB>(&s_tab[0][0]);
   Slot sl[kSlots];
   Box box;
   setup_slots<E, kSubs, kSlots>(a, tl, sl, box, s_red, true);

@@ -707,17 +707,30 @@ __device__ __forceinline__ bool slot_weight(const Slot& s, uint32_t key, float& 
   return hit;
 }
 
-// Table values at the slot's 4 (y, x) corners of the current plane.  A corner
-// outside the volume reads its in-volume neighbour (it has weight 0).  Every
-// index is below kChunkNV, so the reads stay inside a table row even for a slot
-// of another chunk (whose values are then discarded).
+// Table values at the slot's 4 (y, x) corners of the current plane.  A lower
+// corner row outside the volume reads its in-volume neighbour row (it has
+// weight 0).  Each row's two x corners are one paired read of entries base and
+// base + 1: an upper x corner outside the volume (weight fx = 0) reads the
+// next entry, which the table's zeroed start or an earlier step left finite.
+// Every index is at most kChunkNV, inside a table row even for a slot of
+// another chunk (whose values are then discarded).
 __device__ __forceinline__ void corners4(const Slot& s, const float* row, float& t00, float& t01,
                                          float& t10, float& t11) {
-  const int base = s.idx & 0x1ff, dy = (s.idx >> 9) & 0x1f, dx = (s.idx >> 14) & 1;
+  const int base = s.idx & 0x1ff, dy = (s.idx >> 9) & 0x1f;
   t00 = row[base];
-  t01 = row[base + dx];
+  t01 = row[base + 1];
   t10 = row[base + dy];
-  t11 = row[base + dy + dx];
+  t11 = row[base + dy + 1];
+}
+
+// Zeroes NB whole tables (pad columns included).
+template <int NB>
+__device__ __forceinline__ void zero_tables_all(float* tables) {
+  constexpr int n4 = NB * kTQ * kSRow / 4;
+  for (int e = threadIdx.x; e < n4; e += blockDim.x) {
+    const f32x4_t z = {0.0f, 0.0f, 0.0f, 0.0f};
+    __builtin_memcpy(&tables[4 * e], &z, sizeof(z));
+  }
 }
 
 // Bilinear (y, x) interpolation of 4 corner values and its two partial
