@@ -277,11 +277,11 @@ __global__ __launch_bounds__(kThreads, (fwd_min_waves<HD, E, XK>())) void dsa3d_
         if (!slot_hits(si, step_key(c.id, z), wz, dwz)) continue;
         const float pz = sc[i] * wz;
         const float gx = 1.0f - si.fx, gy = 1.0f - si.fy;
-        const int base = si.idx & 0x1ff, dy = (si.idx >> 9) & 0x1f, dx = (si.idx >> 14) & 1;
+        const int base = si.idx & 0x1ff, dy = (si.idx >> 9) & 0x1f;
         atomicAdd(&row[base], to_fix(pz * (gy * gx)));
-        atomicAdd(&row[base + dx], to_fix(pz * (gy * si.fx)));
+        atomicAdd(&row[base + 1], to_fix(pz * (gy * si.fx)));
         atomicAdd(&row[base + dy], to_fix(pz * (si.fy * gx)));
-        atomicAdd(&row[base + dy + dx], to_fix(pz * (si.fy * si.fx)));
+        atomicAdd(&row[base + dy + 1], to_fix(pz * (si.fy * si.fx)));
       }
       __syncthreads();
 #pragma unroll
@@ -348,13 +348,15 @@ __global__ __launch_bounds__(kThreads, (fwd_min_waves<HD, E, XK>())) void dsa3d_
       if (!slot_hits(si, step_key(c.id, z), wz, dwz)) continue;
       const float pz = sc[i] * wz;
       const float gx = 1.0f - si.fx, gy = 1.0f - si.fy;
-      const int base = si.idx & 0x1ff, dy = (si.idx >> 9) & 0x1f, dx = (si.idx >> 14) & 1;
-      // an upper corner outside the volume has offset 0 and weight 0: it adds 0
-      // to the lower corner, so all four adds run without branches
+      const int base = si.idx & 0x1ff, dy = (si.idx >> 9) & 0x1f;
+      // an upper corner outside the volume has weight 0, so all four adds run
+      // without branches: a y corner (offset 0) adds 0 to the lower one, an x
+      // corner adds 0 to the next entry (at most column kChunkNV, inside the
+      // row), and the x pair keeps one address with immediate offsets
       atomicAdd(&row[base], to_fix(pz * (gy * gx)));
-      atomicAdd(&row[base + dx], to_fix(pz * (gy * si.fx)));
+      atomicAdd(&row[base + 1], to_fix(pz * (gy * si.fx)));
       atomicAdd(&row[base + dy], to_fix(pz * (si.fy * gx)));
-      atomicAdd(&row[base + dy + dx], to_fix(pz * (si.fy * si.fx)));
+      atomicAdd(&row[base + dy + 1], to_fix(pz * (si.fy * si.fx)));
     }
     __syncthreads();
     for (int kc = 32 * kph; av_wave && kc < c.nvp; kc += 32 * KP) {
