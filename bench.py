@@ -11,8 +11,11 @@ Workloads (one step = one pass of the hot path over one batch of synthetic
 input, every buffer preallocated and resident in HBM):
 
   long-clip-65k    (default) B=1, T=64, H=W=32 (65,536 tokens), dim 1024,
-                   16 heads x 64, bf16 storage with fp32 accumulation, raw
-                   offsets ~ N(0, 0.5)
+                   16 heads x 64, bf16 storage with fp32 accumulation (dK / dV
+                   summed over query tiles with fp32 atomics), raw offsets
+                   ~ N(0, 0.5)
+  long-clip-65k-f16acc  the same with dK / dV summed in power-of-two-scaled
+                   fp16 pairs (MSD_ACCUM_F16; fp32 redo on overflow)
   long-clip-65k-g128  the same with 128 extra keys shared by every query
                    (the reference's extra_kv from HybridAttention3D's registers)
   tiny-2k          B=1, T=8, H=W=16 (2,048 tokens), dim 256, 4 x 64, fp32,
@@ -81,6 +84,13 @@ WORKLOADS = {
         B=1, T=64, H=32, W=32, D=1024, nh=16, kernel=(3, 7, 7), dtype="bf16",
         offsets=("normal", 0.5), backward=True, metric=METRIC,
         workload="3D-DSA fwd+bwd HIP kernel set, long-clip 65,536 tokens",
+        cpu_slab=dict(T=4)),
+    "long-clip-65k-f16acc": dict(
+        B=1, T=64, H=32, W=32, D=1024, nh=16, kernel=(3, 7, 7), dtype="bf16",
+        offsets=("normal", 0.5), backward=True, dkv_accum="fp16",
+        metric="3D-DSA fwd+bwd tokens/sec at 65k tokens bf16, dK/dV summed in scaled fp16",
+        workload="3D-DSA fwd+bwd HIP kernel set, long-clip 65,536 tokens, dK/dV accumulated in "
+                 "scaled fp16 pairs",
         cpu_slab=dict(T=4)),
     "long-clip-65k-g128": dict(
         B=1, T=64, H=32, W=32, D=1024, nh=16, kernel=(3, 7, 7), dtype="bf16",
@@ -233,7 +243,7 @@ def run_gpu(cfg, steps, warmup, calibrate=False):
     dek = torch.empty_like(ek) if G else None
     dev_ = torch.empty_like(ev) if G else None
     dsa = _lib.DsaDesc(B, T, H, W, nh, hd, kt, kh, kw, mdt, D, D, D, 1.0, 1.0 / math.sqrt(hd),
-                       0, 0, 0, 0.0, G)
+                       0, 0, 0, 0.0, G, _lib.ACCUMS[accumulation(cfg)])
     cv7 = _lib.ConvDesc(B, T, H, W, D, kt, kh, kw, mdt, 0)
     cv3 = _lib.ConvDesc(B, T, H, W, D, 3, 3, 3, mdt, 1)
 
@@ -370,14 +380,23 @@ def cpu_baseline(cfg, runs=3):
         cpu_model=_cpu_model(), torch_version=torch.__version__, seconds=med)
 
 
-def phase_kernels(dtype):
+def accumulation(cfg):
+    """How the workload's backward sums dK / dV over query tiles (msd_accum)."""
+    return cfg.get("dkv_accum", "fp32")
+
+
+def phase_kernels(dtype, accum="fp32"):
     """Bench phase -> the kernels its ABI call launches, in order (bf16 adds the
-    fp16 accumulators' scale kernels before the dq/dK/dV kernel, their
-    conversion to bf16, and the fp32 redo after an overflow, whose kernels
-    return at once without one)."""
+    conversion of the fp32 dK / dV rows to bf16; with fp16 accumulation the
+    scale kernels before the dq/dK/dV kernel, the conversion, and the fp32 redo
+    after an overflow, whose kernels return at once without one)."""
     if dtype != "bf16":
         return {"dsa3d_fwd": ["dsa3d_fwd_tiled_kernel"],
                 "dsa3d_bwd": ["dsa3d_bwd_p1_kernel", "dsa3d_bwd_p2_kernel"]}
+    if accum == "fp32":
+        return {"dsa3d_fwd": ["dsa3d_fwd_tiled_kernel"],
+                "dsa3d_bwd": ["dsa3d_bwd_p1_kernel", "dsa3d_bwd_p2_kernel",
+                              "acc_to_bf16_kernel"]}
     return {"dsa3d_fwd": ["dsa3d_fwd_tiled_kernel"],
             "dsa3d_bwd": ["dsa3d_bwd_p1_kernel", "h16_bounds_kernel", "h16_scales_kernel",
                           "dsa3d_bwd_p2_kernel", "h16_to_bf16_kernel", "fill_zero_if_flag",
@@ -445,7 +464,7 @@ def summarize(workload, trace_dir, fetch_dir, write_dir):
     rec = {}
     print("| phase (kernels) | FETCH KiB | WRITE KiB | traffic (scaled) | algorithmic | traffic / algorithmic |")
     print("|---|---|---|---|---|---|")
-    for phase, names in phase_kernels(cfg["dtype"]).items():
+    for phase, names in phase_kernels(cfg["dtype"], accumulation(cfg)).items():
         f_kib, w_kib = phase_sum(fetch, names), phase_sum(write, names)
         if f_kib is None or w_kib is None:
             continue
@@ -583,7 +602,11 @@ def main():
             "offsets": (f"raw ~ N(0, {cfg['offsets'][1]})" if cfg["offsets"][0] == "normal" else
                         "offset net: depthwise 3x3x3 + GELU + 1x1, weights ~ N(0, {}) / N(0, {}), "
                         "bias {} {}".format(*cfg["offsets"][1:3], *cfg["offsets"][3])),
-            "accumulation": "fp32", "pass": "fwd+bwd" if cfg["backward"] else "fwd",
+            "accumulation": ("fp32" if cfg["dtype"] == "fp32" or not cfg["backward"] else
+                             {"fp32": "fp32 (dK/dV: fp32 atomics)",
+                              "fp16": "fp32 except dK/dV: summed across query tiles in "
+                                      "power-of-two-scaled fp16 atomics"}[accumulation(cfg)]),
+            "pass": "fwd+bwd" if cfg["backward"] else "fwd",
             "extra_keys": cfg.get("extra_g", 0),
         },
         "hbm_gbps": round(sbytes / (ms_step / 1e3) / 1e9, 1),

@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define MSD_ABI_VERSION 4
+#define MSD_ABI_VERSION 5
 
 typedef enum msd_dtype { MSD_F32 = 0, MSD_BF16 = 1 } msd_dtype;
 
@@ -78,7 +78,19 @@ typedef struct msd_dsa3d_desc {
    * kt*kh*kw taps before the softmax.  0 = none; at most 4096 (the tiled
    * kernels take up to 256).                                                 */
   int32_t extra_g;
+  /* How msd_dsa3d_bwd sums the dK / dV contributions of different query tiles
+   * (msd_accum).  MSD_ACCUM_F32 (0, the default) adds them in fp32, as the
+   * reference's grid_sampler_3d_backward does at fp32 grid precision
+   * (attention.py:240-273); bf16 dK / dV are rounded once at the end.
+   * MSD_ACCUM_F16 (bf16 storage and the tiled kernels only; an error for
+   * fp32 storage) adds power-of-two-scaled fp16 pairs instead: about half the
+   * atomic traffic, 11 significant bits per running sum, and an fp32 redo of
+   * dK / dV when a sum leaves the fp16 range.  The direct kernels always add
+   * in fp32.                                                                  */
+  int32_t dkv_accum;
 } msd_dsa3d_desc;
+
+typedef enum msd_accum { MSD_ACCUM_F32 = 0, MSD_ACCUM_F16 = 1 } msd_accum;
 
 /* Kernel family for the attention core.  AUTO picks the matrix-core tiled
  * kernels when the call qualifies (bf16 or fp32, head_dim 32/64/96/128, <= 160

@@ -16,7 +16,7 @@ import threading
 import torch
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libmegaslide_dsa3d.so")
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 MSD_F32 = 0
 MSD_BF16 = 1
@@ -50,11 +50,14 @@ class DsaDesc(ctypes.Structure):
         ("offset_scale", ctypes.c_float), ("softmax_scale", ctypes.c_float),
         ("algo", ctypes.c_int32), ("dropout_offset", ctypes.c_uint32),
         ("dropout_seed", ctypes.c_uint64), ("dropout_p", ctypes.c_float),
-        ("extra_g", ctypes.c_int32),
+        ("extra_g", ctypes.c_int32), ("dkv_accum", ctypes.c_int32),
     ]
 
 
 ALGOS = {"auto": 0, "direct": 1, "tiled": 2}
+
+# msd_accum: how the backward sums dK / dV across query tiles
+ACCUMS = {"fp32": 0, "fp16": 1}
 
 
 class ConvDesc(ctypes.Structure):

@@ -78,6 +78,11 @@ class DeformableSlideAttention3D(nn.Module):
         nn.init.zeros_(self.offset_net[-1].weight)
         nn.init.zeros_(self.offset_net[-1].bias)
         self.dropout = nn.Dropout(dropout)
+        # How the backward sums dK / dV over query tiles (not a constructor
+        # argument, so the reference's signature stays as it is): "fp32", the
+        # reference's precision, or for bfloat16 weights "fp16" (scaled fp16
+        # pairs, about half the atomic traffic).
+        self.dkv_accum = "fp32"
 
     @property
     def kernel_size(self) -> Tuple[int, int, int]:
@@ -115,6 +120,6 @@ class DeformableSlideAttention3D(nn.Module):
             ev = self.v_proj(extra_kv).to(dt)
         attn = dsa3d_core(q, k.to(dt), v.to(dt), off, video_shape, self.num_heads,
                           self.kernel_size, self.offset_scale, dropout_p=drop_p, extra_k=ek,
-                          extra_v=ev)
+                          extra_v=ev, dkv_accum=self.dkv_accum)
         return torch.addmm(dw.reshape(B * N, D), attn.reshape(B * N, D),
                            self.out_proj.weight.t()).view(B, N, D)

@@ -49,6 +49,10 @@ int check_dsa(const msd_dsa3d_desc* d) {
     return fail(MSD_ERR_ARG, "dsa3d: bad algo %d", d->algo);
   if (d->extra_g < 0 || d->extra_g > 4096)
     return fail(MSD_ERR_ARG, "dsa3d: extra_g %d outside [0, 4096]", d->extra_g);
+  if (d->dkv_accum != MSD_ACCUM_F32 && d->dkv_accum != MSD_ACCUM_F16)
+    return fail(MSD_ERR_ARG, "dsa3d: bad dkv_accum %d", d->dkv_accum);
+  if (d->dkv_accum == MSD_ACCUM_F16 && d->dtype != MSD_BF16)
+    return fail(MSD_ERR_ARG, "dsa3d: dkv_accum MSD_ACCUM_F16 needs bf16 storage");
   if (!(d->dropout_p >= 0.0f && d->dropout_p < 1.0f))
     return fail(MSD_ERR_ARG, "dsa3d: dropout_p %g outside [0, 1)", static_cast<double>(d->dropout_p));
   const int64_t D = static_cast<int64_t>(d->num_heads) * d->head_dim;

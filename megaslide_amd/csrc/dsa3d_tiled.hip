@@ -86,6 +86,9 @@ __global__ __launch_bounds__(kThreads, (fwd_min_waves<HD, E, XK>())) void dsa3d_
   __shared__ __attribute__((aligned(16))) float s_tab[NB][kTQ * kSRow];  // S, then A
   __shared__ __attribute__((aligned(16))) word_t<E> s_vt[VC * VR];      // V^T chunk
   __shared__ int s_red[kWaves][6];
+  // per query: 1, or NaN when a score is not finite (its output is NaN then, as
+  // softmax makes it in the reference; the fixed-point weights alone would drop it)
+  __shared__ float s_qnan[kTQ];
 
   const Tile tl = make_tile<1, kSubs>(a);
   // the tile's q rows load while the slots are set up
@@ -194,6 +197,13 @@ __global__ __launch_bounds__(kThreads, (fwd_min_waves<HD, E, XK>())) void dsa3d_
 #pragma unroll
   for (int i = 0; i < kSlots; ++i)
     sc[i] *= inv_den * slot_dropout(sl[i], a.drop) * a.fix_a;  // p (dropped), fixed-point units
+  {
+    // the query index from the wave (a scalar) and the lane id: a per-lane
+    // index kept across the plane loops spilled
+    const unsigned tid = 64u * static_cast<unsigned>(__builtin_amdgcn_readfirstlane(tl.wave)) +
+                         __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+    if (tid % kSubs == 0) s_qnan[tid / kSubs] = den == den ? 1.0f : __builtin_nanf("");
+  }
   if (lse != nullptr && tl.sub == 0 && !kHV) {
     if (tl.q_ok) lse[tl.qn * a.nh + tl.head] = mx + logf(den);
   } else if (lse != nullptr && tl.sub == 0) {
@@ -321,7 +331,7 @@ __global__ __launch_bounds__(kThreads, (fwd_min_waves<HD, E, XK>())) void dsa3d_
       const int64_t n = tile_row(a, tl, m);
       if (n >= 0)
         out[n * (static_cast<int64_t>(a.nh) * HD) + tl.head * HD + ch] =
-            from_f32<E>(o * a.fix_a_inv);
+            from_f32<E>(o * a.fix_a_inv * s_qnan[m]);
     }
     return;
   }
@@ -394,7 +404,8 @@ __global__ __launch_bounds__(kThreads, (fwd_min_waves<HD, E, XK>())) void dsa3d_
     const int m = e / HD, ch = e - m * HD;
     const int64_t n = tile_row(a, tl, m);
     if (n >= 0)
-      out[n * (static_cast<int64_t>(a.nh) * HD) + tl.head * HD + ch] = from_f32<E>(o * a.fix_a_inv);
+      out[n * (static_cast<int64_t>(a.nh) * HD) + tl.head * HD + ch] =
+          from_f32<E>(o * a.fix_a_inv * s_qnan[m]);
   }
 }
 
@@ -429,7 +440,8 @@ constexpr int p1_min_waves() {
   return sizeof(E) == 2 || HD == 64 ? 4 : 2;
 }
 
-template <int HD, typename E>
+// AE: bytes of one dK / dV accumulator element (4 = fp32 rows, 2 = scaled fp16).
+template <int HD, typename E, int AE>
 __global__ __launch_bounds__(kThreads, (p1_min_waves<HD, E>())) void dsa3d_bwd_p1_kernel(
     Args a, const E* __restrict__ out, const E* __restrict__ dout,
     const float* __restrict__ lse, const float* __restrict__ dlse, E* __restrict__ doff,
@@ -481,10 +493,9 @@ __global__ __launch_bounds__(kThreads, (p1_min_waves<HD, E>())) void dsa3d_bwd_p
     s_tb[e / (2 * kP1Zero)][((e / kP1Zero) & 1) * kP1Tab + kTQ * kSRow + e % kP1Zero] = 0.0f;
   {
     // The second kernel adds dK and dV into accumulator rows (the fp32 outputs
-    // for fp32 storage, fp16 rows for bf16): zero this tile's rows of the head
-    // first (the tiles of a launch partition the (token, head) pairs, and the
-    // second kernel starts after this one ends), 16 bytes a thread.
-    constexpr int AE = acc_bytes<E>();
+    // for fp32 storage, fp32 or scaled fp16 rows for bf16): zero this tile's
+    // rows of the head first (the tiles of a launch partition the (token, head)
+    // pairs, and the second kernel starts after this one ends), 16 bytes a thread.
     constexpr int CPR = HD * AE / 16;
     for (int e = threadIdx.x; e < 2 * kTQ * CPR; e += kThreads) {
       const int t = e / (kTQ * CPR), m = (e / CPR) % kTQ, ch = (e % CPR) * (16 / AE);
@@ -514,17 +525,26 @@ __global__ __launch_bounds__(kThreads, (p1_min_waves<HD, E>())) void dsa3d_bwd_p
       x[cc] = load_op<E>(&s_x[(t * kTQ + (tl.lane & 15)) * XR + 32 * cc + 8 * (tl.lane >> 4)]);
   };
 
-  // Delta = dO . O (- dlse) and lse for this lane's query: 32 lanes x HD/32 channels
+  // Delta = dO . O - dlse and lse for this lane's query.  Without extra keys,
+  // dO . O = sum_k p_k f_k dP_k over the query's taps, formed in fp32 after the
+  // plane walk: that sum does not see the rounding of the stored output (bf16
+  // storage), which a peaked softmax would otherwise turn into ds errors as
+  // large as ds itself.  With extra keys (their dP is not formed here) it is
+  // dO . O from the output rows, 32 lanes x HD/32 channels.
   constexpr int CPL = HD / kSubs;
   float delta = 0.0f, lse_q = 0.0f;
   if (tl.q_ok) {
-    const int64_t base = tl.qn * D + tl.head * HD + CPL * tl.sub;
+    if (a.G > 0) {
+      const int64_t base = tl.qn * D + tl.head * HD + CPL * tl.sub;
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) delta += to_f32(dout[base + j]) * to_f32(out[base + j]);
+      for (int j = 0; j < CPL; ++j) delta += to_f32(dout[base + j]) * to_f32(out[base + j]);
+    }
     lse_q = lse[tl.qn * a.nh + tl.head];
   }
+  if (a.G > 0) {
 #pragma unroll
-  for (int m = 1; m < kSubs; m <<= 1) delta += __shfl_xor(delta, m);
+    for (int m = 1; m < kSubs; m <<= 1) delta += __shfl_xor(delta, m);
+  }
   if (dlse != nullptr && tl.q_ok) delta -= dlse[tl.qn * a.nh + tl.head];
   // kept in LDS across the plane loop (registers are the limit there)
   __shared__ float s_dl[kTQ][2];
@@ -663,16 +683,27 @@ __global__ __launch_bounds__(kThreads, (p1_min_waves<HD, E>())) void dsa3d_bwd_p
   const int64_t tap0 = (qn * a.nh + tl.head) * a.K;
   delta = s_dl[tid / kSubs][0];  // written before the loop's first barrier
   lse_q = s_dl[tid / kSubs][1];
-  // p * factor and ds * scale of every tap (0 for empty slots), in place of s and dp
+  // p of every tap (0 for empty slots) in place of s.  Dropout: o sums
+  // pd * v_s with pd = p * factor, so dp and the V-side coordinate gradient
+  // see the factor.
+  float pdp = 0.0f;  // sum_k p_k f_k dP_k over this lane's taps
 #pragma unroll
   for (int i = 0; i < kSlots; ++i) {
-    const float pi = __expf(s_[i] * a.softmax_scale - lse_q);
-    // dropout: o sums pd * v_s with pd = p * factor, so dp and the V-side
-    // coordinate gradient see the factor
-    const float dfac = slot_dropout(sl[i], a.drop);
     const bool ok = slot_z0(sl[i]) >= 0;
-    s_[i] = ok ? pi * dfac : 0.0f;
-    dp_[i] = ok ? pi * (dfac * dp_[i] - delta) * a.softmax_scale : 0.0f;
+    s_[i] = ok ? __expf(s_[i] * a.softmax_scale - lse_q) : 0.0f;
+    pdp = __builtin_fmaf(s_[i] * slot_dropout(sl[i], a.drop), dp_[i], pdp);
+  }
+  if (a.G == 0) {
+#pragma unroll
+    for (int m = 1; m < kSubs; m <<= 1) pdp += __shfl_xor(pdp, m);
+    delta += pdp;
+  }
+  // p * factor in place of p, ds * scale = p (f dP - Delta) scale in place of dp
+#pragma unroll
+  for (int i = 0; i < kSlots; ++i) {
+    const float dfac = slot_dropout(sl[i], a.drop);
+    dp_[i] = s_[i] * (dfac * dp_[i] - delta) * a.softmax_scale;
+    s_[i] *= dfac;
   }
   // bf16 storage keeps one word per tap: fp16 p * factor and ds * scale / l1,
   // with l1 = sum over the query's taps of |ds * scale| kept per token and head
@@ -809,7 +840,8 @@ __device__ __forceinline__ void p2_tile(const Args& a, int tile, const E* __rest
                                         const float* __restrict__ b_ws, E* __restrict__ dq,
                                         void* __restrict__ dk_acc, void* __restrict__ dv_acc,
                                         int64_t acc_ks, int64_t acc_vs, int cw_base,
-                                        const float* __restrict__ scales) {
+                                        const float* __restrict__ scales,
+                                        const float* __restrict__ dqx) {
   static_assert(CW <= HD && CW % 32 == 0, "channel windows are whole 32-channel blocks");
   using G = P2Tile<FR>;
   constexpr int kP2Frames = FR, kP2Q = G::Q, kP2Subs = G::Subs, kP2Slots = G::Slots;
@@ -1094,9 +1126,10 @@ __device__ __forceinline__ void p2_tile(const Args& a, int tile, const E* __rest
       for (int kp = 0; kp < KPQ; ++kp) v += red[((f * KPQ + kp) * kTQ + mm) * CW + ch];
       const int64_t n = tile_row(a, tl, m);
       if (n >= 0) {
-        E* const o = &dq[n * a.qs + cw0 + ch];
-        // the first kernel wrote the extra keys' part of dq
-        *o = from_f32<E>(v * s_binv[m] + (a.G > 0 ? to_f32(*o) : 0.0f));
+        // the extra keys' part of dq (fp32, from their backward kernel) joins
+        // before the one rounding to the element type
+        dq[n * a.qs + cw0 + ch] =
+            from_f32<E>(v * s_binv[m] + (a.G > 0 ? dqx[n * D + cw0 + ch] : 0.0f));
       }
     }
   } else {
@@ -1111,8 +1144,9 @@ __device__ __forceinline__ void p2_tile(const Args& a, int tile, const E* __rest
         const int m = kTQ * fq + 4 * (tl.lane >> 4) + r;
         const int64_t n = tile_row(a, tl, m);
         if (n >= 0) {
-          E* const o = &dq[n * a.qs + cw0 + 16 * ct + mq];
-          *o = from_f32<E>(dq_acc[j][r] * s_binv[m] + (a.G > 0 ? to_f32(*o) : 0.0f));
+          const int c = cw0 + 16 * ct + mq;
+          dq[n * a.qs + c] =
+              from_f32<E>(dq_acc[j][r] * s_binv[m] + (a.G > 0 ? dqx[n * D + c] : 0.0f));
         }
       }
     }
@@ -1124,9 +1158,9 @@ __global__ __launch_bounds__(P2Tile<FR>::Threads) void dsa3d_bwd_p2_kernel(
     Args a, const E* __restrict__ dout, const float* __restrict__ p_ws,
     const float* __restrict__ b_ws, E* __restrict__ dq, void* __restrict__ dk_acc,
     void* __restrict__ dv_acc, int64_t acc_ks, int64_t acc_vs, int cw_base,
-    const float* __restrict__ scales) {
+    const float* __restrict__ scales, const float* __restrict__ dqx) {
   p2_tile<HD, CW, E, FR, MODE>(a, blockIdx.x, dout, p_ws, b_ws, dq, dk_acc, dv_acc, acc_ks, acc_vs,
-                               cw_base, scales);
+                               cw_base, scales, dqx);
 }
 
 // dK / dV again with fp32 atomics, only when the fp16 accumulation overflowed
@@ -1143,7 +1177,7 @@ __global__ __launch_bounds__(P2Tile<FR>::Threads) void dsa3d_bwd_p2_redo_kernel(
     int t = tile;
     asm volatile("" : "+s"(t));  // nothing of one tile is computed ahead for the next
     p2_tile<HD, CW, E, FR, kP2Redo>(a, t, dout, p_ws, b_ws, nullptr, dk_acc, dv_acc, acc_ks,
-                                    acc_vs, cw_base, nullptr);
+                                    acc_vs, cw_base, nullptr, nullptr);
     __syncthreads();  // the next tile rewrites the LDS tables
   }
 }
@@ -1154,12 +1188,13 @@ __global__ __launch_bounds__(P2Tile<FR>::Threads) void dsa3d_bwd_p2_redo_kernel(
 // S_e - lse), the dropout factor f of tap K + g, ds * scale = p (f dP_e -
 // Delta) scale (Delta = dO . O - dlse).  It writes ds * scale and p f
 // ([B, nh, N, G], for the dEK / dEV reduction) and dq's extra part sum_g
-// ds_g scale ek_g (MFMA, to dq, which the second backward kernel adds to).
+// ds_g scale ek_g (MFMA, fp32 [rows, D] dqx, which the second backward kernel
+// adds to its tap part before dq's one rounding).
 constexpr int kXQ = 16;
 template <int HD, typename E>
 __global__ __launch_bounds__(256) void dsa3d_bwd_extra_kernel(
     Args a, const E* __restrict__ out, const E* __restrict__ dout, const float* __restrict__ lse,
-    const float* __restrict__ dlse, E* __restrict__ dq, E* __restrict__ ds_e,
+    const float* __restrict__ dlse, float* __restrict__ dqx, E* __restrict__ ds_e,
     E* __restrict__ pf_e) {
   constexpr int EKR = sizeof(E) == 2 ? 40 : 36;  // 16-byte aligned transposed rows
   __shared__ __attribute__((aligned(16))) float s_s[kXQ * kSRow];   // S_e, then ds * scale
@@ -1284,7 +1319,7 @@ __global__ __launch_bounds__(256) void dsa3d_bwd_extra_kernel(
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int64_t n = n0 + 4 * (lane >> 4) + r;
-      if (n < a.N) dq[(sample0 + n) * a.qs + head * HD + 16 * ct + mq] = from_f32<E>(dqa[t][r]);
+      if (n < a.N) dqx[(sample0 + n) * D + head * HD + 16 * ct + mq] = dqa[t][r];
     }
   }
 }
@@ -1527,49 +1562,68 @@ __device__ __forceinline__ float h16_pow2_scale(float bound) {
   return ldexpf(1.0f, min(e - 1, 100));
 }
 
-// Magnitudes behind the fp16 dK / dV accumulators' scales (bf16 storage): the
-// largest |q|, |dO|, |v| (extra values included) and |dlse| over an evenly
-// spread sample of at most about kBoundRows token rows (every row of a smaller
-// input), 16 bytes a thread.  Each block writes its maxima to part[blockIdx.x][4].
+// Magnitudes behind the fp16 dK / dV accumulators' scales (bf16 storage), over
+// an evenly spread sample of at most about kBoundRows token rows (every row of
+// a smaller input): the largest |q| and |dO| element, the largest L2 norm of a
+// head's slice of a dO row and of a V row (extra values included), and the
+// largest |dlse|.  One thread per (sampled row, head), 16-byte loads; each
+// block writes its maxima to part[blockIdx.x][kBoundsWords].
 constexpr int kBoundsBlocks = 256;
+constexpr int kBoundsWords = 8;
 constexpr int64_t kBoundRows = 4096;
 __global__ __launch_bounds__(256) void h16_bounds_kernel(
     const bf16* __restrict__ q, int64_t qs, const bf16* __restrict__ dout,
     const bf16* __restrict__ v, int64_t vs, const bf16* __restrict__ ev, int64_t erows,
-    const float* __restrict__ dlse, int64_t rows, int nh, int D, float* __restrict__ part) {
-  float m[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    const float* __restrict__ dlse, int64_t rows, int nh, int hd, float* __restrict__ part) {
+  float m[5] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
   const int64_t step = rows > kBoundRows ? rows / kBoundRows : 1;
-  const int64_t nsamp = (rows + step - 1) / step, d8 = D / 8;
-  auto maxabs8 = [](const void* p) {
-    const u32x4_t x = load16(p);
-    float r = 0.0f;
+  const int64_t nsamp = (rows + step - 1) / step;
+  const int D = nh * hd;
+  // (largest |x|, sum of x^2) over hd elements from p
+  auto scan = [hd](const bf16* p, float& mx, float& ss) {
+    for (int c = 0; c < hd; c += 8) {
+      const u32x4_t x = load16(p + c);
 #pragma unroll
-    for (int k = 0; k < 4; ++k)
-      r = fmaxf(r, fmaxf(fabsf(__uint_as_float(x[k] << 16)),
-                         fabsf(__uint_as_float(x[k] & 0xffff0000u))));
-    return r;
+      for (int k = 0; k < 4; ++k) {
+        const float lo = __uint_as_float(x[k] << 16), hi = __uint_as_float(x[k] & 0xffff0000u);
+        mx = fmaxf(mx, fmaxf(fabsf(lo), fabsf(hi)));
+        ss += lo * lo + hi * hi;
+      }
+    }
   };
-  const int64_t n = nsamp * d8, stride = static_cast<int64_t>(gridDim.x) * 256;
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n; i += stride) {
-    const int64_t j = i / d8, k = i - j * d8, c = 8 * k, r = j * step;
-    m[0] = fmaxf(m[0], maxabs8(q + r * qs + c));
-    m[1] = fmaxf(m[1], maxabs8(dout + r * D + c));
-    m[2] = fmaxf(m[2], maxabs8(v + r * vs + c));
-    // item k < nh of the row also reads head k's dlse (D / 8 >= nh)
-    if (dlse != nullptr && k < nh) m[3] = fmaxf(m[3], fabsf(dlse[r * nh + k]));
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < nsamp * nh;
+       i += stride) {
+    const int64_t j = i / nh, r = j * step;
+    const int h = static_cast<int>(i - j * nh);
+    float mx = 0.0f, ss = 0.0f;
+    scan(q + r * qs + h * hd, mx, ss);
+    m[0] = fmaxf(m[0], mx);
+    mx = ss = 0.0f;
+    scan(dout + r * D + h * hd, mx, ss);
+    m[1] = fmaxf(m[1], mx);
+    m[2] = fmaxf(m[2], sqrtf(ss));
+    mx = ss = 0.0f;
+    scan(v + r * vs + h * hd, mx, ss);
+    m[3] = fmaxf(m[3], sqrtf(ss));
+    if (dlse != nullptr) m[4] = fmaxf(m[4], fabsf(dlse[r * nh + h]));
   }
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < erows * d8; i += stride)
-    m[2] = fmaxf(m[2], maxabs8(ev + i * 8));
-  __shared__ float red[4][4];
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < erows * nh;
+       i += stride) {
+    float mx = 0.0f, ss = 0.0f;
+    scan(ev + (i / nh) * D + (i % nh) * hd, mx, ss);
+    m[3] = fmaxf(m[3], sqrtf(ss));
+  }
+  __shared__ float red[4][5];
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
+  for (int k = 0; k < 5; ++k) {
 #pragma unroll
     for (int sh = 1; sh < 64; sh <<= 1) m[k] = fmaxf(m[k], __shfl_xor(m[k], sh));
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6][k] = m[k];
   }
   __syncthreads();
-  if (threadIdx.x < 4)
-    part[blockIdx.x * 4 + threadIdx.x] =
+  if (threadIdx.x < 5)
+    part[blockIdx.x * kBoundsWords + threadIdx.x] =
         fmaxf(fmaxf(red[0][threadIdx.x], red[1][threadIdx.x]),
               fmaxf(red[2][threadIdx.x], red[3][threadIdx.x]));
 }
@@ -1577,38 +1631,38 @@ __global__ __launch_bounds__(256) void h16_bounds_kernel(
 // Scales of the fp16 dK / dV accumulators.  A voxel's dV sums p w dO over the
 // queries whose taps reach it, and each query's p w sum to at most the dropout
 // factor F: |dV| <= n F max|dO| for n such queries.  Its dK sums B q with
-// sum_v |B[q][v]| <= sum_k |ds_k scale| <= scale (2 F hd max|dO| max|v| +
-// |dlse_q|) (ds_k = p_k (f_k dO.v_k - Delta), v_k a convex combination of V
-// rows, |O| <= F max|v|, Cauchy-Schwarz over the head's hd channels), so |dK|
-// <= n max|q| times that.  Scaling by 2^14 / (kH16Reach bound) keeps every
-// partial sum below the fp16 limit (65504) for up to 4 kH16Reach queries' full
-// weight on one voxel.  A sum beyond it (more such queries, or maxima above
-// the sampled ones) overflows to infinity: the conversion flags it and dK /
-// dV are redone in fp32, so the scales only trade redo probability against
-// the values left below fp16's normal range.  They are powers of two
-// (unscaling is exact).  Also clears the flag.
+// sum_v |B[q][v]| <= sum_k |ds_k scale| <= scale (2 F |dO| max|v| + |dlse_q|)
+// (ds_k = p_k (f_k dO.v_k - Delta), v_k a convex combination of V rows,
+// |O| <= F max|v|; |.| of dO and v is the L2 norm of the head's slice, by
+// Cauchy-Schwarz), so |dK| <= n max|q| times that.  Scaling by 2^14 /
+// (kH16Reach bound) keeps every partial sum below the fp16 limit (65504) for up
+// to 4 kH16Reach queries' full weight on one voxel.  A sum beyond it (more such
+// queries, or maxima above the sampled ones) overflows to infinity: the
+// conversion flags it and dK / dV are redone in fp32, so the scales only trade
+// redo probability against the values left below fp16's normal range.  They
+// are powers of two (unscaling is exact).  Also clears the flag.
 constexpr float kH16Reach = 1024.0f;
 __global__ __launch_bounds__(256) void h16_scales_kernel(const float* __restrict__ part, int nblk,
-                                                         float factor, float softmax_scale, int hd,
+                                                         float factor, float softmax_scale,
                                                          float* __restrict__ scales,
                                                          int* __restrict__ flag) {
-  float m[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  float m[5] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
   for (int i = threadIdx.x; i < nblk; i += 256)
 #pragma unroll
-    for (int k = 0; k < 4; ++k) m[k] = fmaxf(m[k], part[4 * i + k]);
-  __shared__ float red[4][4];
+    for (int k = 0; k < 5; ++k) m[k] = fmaxf(m[k], part[kBoundsWords * i + k]);
+  __shared__ float red[4][5];
 #pragma unroll
-  for (int k = 0; k < 4; ++k) {
+  for (int k = 0; k < 5; ++k) {
 #pragma unroll
     for (int sh = 1; sh < 64; sh <<= 1) m[k] = fmaxf(m[k], __shfl_xor(m[k], sh));
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6][k] = m[k];
   }
   __syncthreads();
   if (threadIdx.x == 0) {
-    float r[4];
+    float r[5];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) r[k] = fmaxf(fmaxf(red[0][k], red[1][k]), fmaxf(red[2][k], red[3][k]));
-    const float l1 = softmax_scale * (2.0f * factor * static_cast<float>(hd) * r[1] * r[2] + r[3]);
+    for (int k = 0; k < 5; ++k) r[k] = fmaxf(fmaxf(red[0][k], red[1][k]), fmaxf(red[2][k], red[3][k]));
+    const float l1 = softmax_scale * (2.0f * factor * r[2] * r[3] + r[4]);
     const float sk = h16_pow2_scale(kH16Reach * l1 * r[0]);
     const float sv = h16_pow2_scale(kH16Reach * factor * r[1]);
     scales[0] = sk;
@@ -1692,11 +1746,13 @@ struct BwdBufs {
                    // (p * factor, ds * softmax_scale / l1) in one word (bf16)
   float* b_ws;     // per tap: ds * softmax_scale (fp32), or per (token, head):
                    // l1 = sum over its taps of |ds * softmax_scale| (bf16)
-  void* dk_acc;    // dK / dV accumulator rows: the fp32 outputs (fp32 storage) or
-  void* dv_acc;    // scaled fp16 [rows, D] (bf16 storage)
+  void* dk_acc;    // dK / dV accumulator rows: the fp32 outputs (fp32 storage),
+  void* dv_acc;    // dk32 / dv32, or scaled fp16 [rows, D] (bf16, MSD_ACCUM_F16)
   int64_t acc_ks, acc_vs;
-  float* dk32;     // bf16 storage: fp32 [rows, D] rows for the redo after an fp16
-  float* dv32;     // overflow (the same memory as the fp16 rows)
+  bool h16;       // bf16 storage with MSD_ACCUM_F16: scaled fp16 accumulator rows
+  float* dk32;     // bf16 storage: fp32 [rows, D] accumulator rows (MSD_ACCUM_F32),
+  float* dv32;     // or the redo's rows after an fp16 overflow (the same memory as
+                   // the fp16 rows)
   float* bounds;   // bf16 storage: per-block maxima behind the fp16 scales
   float* scales;   // bf16 storage: sK, 1/sK, sV, 1/sV
   int* flag;       // bf16 storage: fp16 overflow seen
@@ -1704,6 +1760,7 @@ struct BwdBufs {
   E* pf_e;
   float* dek_acc;  // extra keys: dEK / dEV fp32 [B, G, D] (the outputs for fp32 storage)
   float* dev_acc;
+  float* dqx;      // extra keys: their part of dq, fp32 [rows, D] (null without them)
 };
 
 template <int HD, typename E>
@@ -1722,26 +1779,39 @@ void launch_bwd_pair(const msd_dsa3d_desc& d, const void* q, const void* k, cons
   void* const dk_acc = w.dk_acc;
   void* const dv_acc = w.dv_acc;
   const int64_t acc_ks = w.acc_ks, acc_vs = w.acc_vs;
-  constexpr bool kH16 = acc_bytes<E>() == 2;
-  hipLaunchKernelGGL((dsa3d_bwd_p1_kernel<HD, E>), g1, dim3(tiled::kThreads), 0, s, a1, o, go,
-                     lse, dlse, goff, p_ws, b_ws, dk_acc, dv_acc, acc_ks, acc_vs);
+  // scaled fp16 accumulation: bf16 storage with MSD_ACCUM_F16 only
+  const bool h16 = sizeof(E) == 2 && w.h16;
+  if constexpr (sizeof(E) == 2) {
+    if (h16)
+      hipLaunchKernelGGL((dsa3d_bwd_p1_kernel<HD, E, 2>), g1, dim3(tiled::kThreads), 0, s, a1, o,
+                         go, lse, dlse, goff, p_ws, b_ws, dk_acc, dv_acc, acc_ks, acc_vs);
+  }
+  if (!h16)
+    hipLaunchKernelGGL((dsa3d_bwd_p1_kernel<HD, E, 4>), g1, dim3(tiled::kThreads), 0, s, a1, o,
+                       go, lse, dlse, goff, p_ws, b_ws, dk_acc, dv_acc, acc_ks, acc_vs);
   if (d.extra_g > 0) {
     const dim3 gx(static_cast<unsigned>(d.B * ((a1.N + kXQ - 1) / kXQ)), d.num_heads);
     hipLaunchKernelGGL((dsa3d_bwd_extra_kernel<HD, E>), gx, dim3(256), 0, s, a1, o, go, lse, dlse,
-                       gq, w.ds_e, w.pf_e);
+                       w.dqx, w.ds_e, w.pf_e);
   }
-  if constexpr (kH16) {
-    const float factor = a1.drop.threshold == 0 ? 1.0f : a1.drop.scale;
-    hipLaunchKernelGGL(h16_bounds_kernel, dim3(kBoundsBlocks), dim3(256), 0, s,
-                       static_cast<const bf16*>(q), d.q_stride, go, static_cast<const bf16*>(v),
-                       d.v_stride, static_cast<const bf16*>(ev), int64_t{d.B} * d.extra_g, dlse,
-                       static_cast<int64_t>(a1.N) * d.B, d.num_heads, d.num_heads * HD, w.bounds);
-    hipLaunchKernelGGL(h16_scales_kernel, dim3(1), dim3(256), 0, s, w.bounds, kBoundsBlocks,
-                       factor, d.softmax_scale, HD, w.scales, w.flag);
+  if constexpr (sizeof(E) == 2) {
+    if (h16) {
+      const float factor = a1.drop.threshold == 0 ? 1.0f : a1.drop.scale;
+      hipLaunchKernelGGL(h16_bounds_kernel, dim3(kBoundsBlocks), dim3(256), 0, s,
+                         static_cast<const bf16*>(q), d.q_stride, go, static_cast<const bf16*>(v),
+                         d.v_stride, static_cast<const bf16*>(ev), int64_t{d.B} * d.extra_g, dlse,
+                         static_cast<int64_t>(a1.N) * d.B, d.num_heads, HD, w.bounds);
+      hipLaunchKernelGGL(h16_scales_kernel, dim3(1), dim3(256), 0, s, w.bounds, kBoundsBlocks,
+                         factor, d.softmax_scale, w.scales, w.flag);
+      hipLaunchKernelGGL((dsa3d_bwd_p2_kernel<HD, CW, E, FR, kP2F16>), g2,
+                         dim3(P2Tile<FR>::Threads), 0, s, a2, go, p_ws, b_ws, gq, dk_acc, dv_acc,
+                         acc_ks, acc_vs, 0, w.scales, w.dqx);
+    }
   }
-  constexpr int MODE = kH16 ? kP2F16 : kP2F32;
-  hipLaunchKernelGGL((dsa3d_bwd_p2_kernel<HD, CW, E, FR, MODE>), g2, dim3(P2Tile<FR>::Threads), 0,
-                     s, a2, go, p_ws, b_ws, gq, dk_acc, dv_acc, acc_ks, acc_vs, 0, w.scales);
+  if (!h16)
+    hipLaunchKernelGGL((dsa3d_bwd_p2_kernel<HD, CW, E, FR, kP2F32>), g2,
+                       dim3(P2Tile<FR>::Threads), 0, s, a2, go, p_ws, b_ws, gq, dk_acc, dv_acc,
+                       acc_ks, acc_vs, 0, w.scales, w.dqx);
   static_assert(HD % CW == 0, "channel windows tile the head");
   if (d.extra_g > 0) {
     // dEK, dEV: about 1,024 workgroups of token ranges that are multiples of 32
@@ -1806,14 +1876,15 @@ __global__ __launch_bounds__(256) void acc_to_bf16_kernel(const float* __restric
 // Workspace layout of the tiled backward (byte offsets): the bf16 path's fp32
 // accumulators (dK/dV, then dEK/dEV; fp32 storage accumulates in its outputs),
 // p and ds * scale per tap, and with extra keys their ds * scale and p *
-// factor per (token, head, key) in the element type.
-// For bf16 storage the dK / dV region holds fp32 [2, rows, D] rows, whose first
-// half also serves as the fp16 [2, rows, D] accumulator (the fp32 rows are only
-// used, zeroed first, after that has been converted), and the bounds kernel's
+// factor per (token, head, key) in the element type and their fp32 part of dq.
+// For bf16 storage the dK / dV region holds the fp32 [2, rows, D] accumulator
+// rows; with MSD_ACCUM_F16 its first half serves as the fp16 [2, rows, D]
+// accumulator (the fp32 rows are then only used, zeroed first, after that has
+// been converted, for the redo after an overflow), and the bounds kernel's
 // per-block maxima, the two scales and their inverses and the overflow flag
 // follow the extra keys' buffers.
 struct TiledWs {
-  size_t acc, xacc, p, ds, dse, pfe, stats, scales, bytes;
+  size_t acc, xacc, p, ds, dse, pfe, dqx, stats, scales, bytes;
 };
 
 TiledWs tiled_ws(const msd_dsa3d_desc& d) {
@@ -1831,8 +1902,9 @@ TiledWs tiled_ws(const msd_dsa3d_desc& d) {
   w.ds = w.p + taps * 4;
   w.dse = up(w.ds + (bf ? rows * d.num_heads * 4 : taps * 4));
   w.pfe = up(w.dse + rows * d.num_heads * G * e);
-  w.stats = up(w.pfe + rows * d.num_heads * G * e);
-  w.scales = up(w.stats + (bf ? kBoundsBlocks * 4 * 4 : 0));
+  w.dqx = up(w.pfe + rows * d.num_heads * G * e);
+  w.stats = up(w.dqx + (G > 0 ? rows * D * 4 : 0));
+  w.scales = up(w.stats + (bf ? kBoundsBlocks * kBoundsWords * 4 : 0));
   w.bytes = w.scales + (bf ? 32 : 0);
   return w;
 }
@@ -1853,16 +1925,18 @@ hipError_t bwd_tiled_typed(const msd_dsa3d_desc& d, const void* q, const void* k
   char* const base = static_cast<char*>(ws);
   const TiledWs L = tiled_ws(d);
   // fp32 storage: dK and dV (and dEK, dEV) add up in the outputs themselves.
-  // bf16 storage: dK and dV in scaled fp16 rows (fp32 again if that
-  // overflows), dEK and dEV in fp32 accumulators, converted at the end.
+  // bf16 storage: dK and dV in fp32 rows, or with MSD_ACCUM_F16 in scaled fp16
+  // rows (fp32 again if that overflows); dEK and dEV in fp32 accumulators;
+  // converted at the end.
   constexpr bool kInPlace = sizeof(E) == 4;
   BwdBufs<E> w;
+  w.h16 = !kInPlace && d.dkv_accum == MSD_ACCUM_F16;
   w.p_ws = reinterpret_cast<float*>(base + L.p);
   w.b_ws = reinterpret_cast<float*>(base + L.ds);
   w.dk32 = kInPlace ? nullptr : reinterpret_cast<float*>(base + L.acc);
   w.dv32 = kInPlace ? nullptr : w.dk32 + rows * D;
-  w.dk_acc = kInPlace ? dk : static_cast<void*>(base + L.acc);
-  w.dv_acc = kInPlace ? dv : static_cast<void*>(base + L.acc + rows * D * 2);
+  w.dk_acc = kInPlace ? dk : w.h16 ? static_cast<void*>(base + L.acc) : w.dk32;
+  w.dv_acc = kInPlace ? dv : w.h16 ? static_cast<void*>(base + L.acc + rows * D * 2) : w.dv32;
   w.acc_ks = kInPlace ? d.k_stride : D;
   w.acc_vs = kInPlace ? d.v_stride : D;
   w.bounds = kInPlace ? nullptr : reinterpret_cast<float*>(base + L.stats);
@@ -1872,6 +1946,7 @@ hipError_t bwd_tiled_typed(const msd_dsa3d_desc& d, const void* q, const void* k
   w.pf_e = reinterpret_cast<E*>(base + L.pfe);
   w.dek_acc = kInPlace ? static_cast<float*>(dek) : reinterpret_cast<float*>(base + L.xacc);
   w.dev_acc = kInPlace ? static_cast<float*>(dev) : w.dek_acc + erows * D;
+  w.dqx = erows > 0 ? reinterpret_cast<float*>(base + L.dqx) : nullptr;
   if (erows > 0) {
     hipLaunchKernelGGL(fill_zero_f32, dim3(fill_blocks(erows * D)), dim3(256), 0, s, w.dek_acc,
                        erows * D);
@@ -1887,21 +1962,27 @@ hipError_t bwd_tiled_typed(const msd_dsa3d_desc& d, const void* q, const void* k
   }
   if constexpr (!kInPlace) {
     const dim3 cgrid(fill_blocks(rows * (D / 8)), 2);
-    hipLaunchKernelGGL(h16_to_bf16_kernel, cgrid, dim3(256), 0, s,
-                       static_cast<const _Float16*>(w.dk_acc), static_cast<const _Float16*>(w.dv_acc),
-                       static_cast<bf16*>(dk), static_cast<bf16*>(dv), rows, D, d.k_stride,
-                       d.v_stride, w.scales, w.flag);
-    // after an fp16 overflow (flag set): dK and dV again in fp32
-    switch (d.head_dim) {
-      case 32: launch_bwd_redo<32, E>(d, q, k, v, off, ek, ev, go, w, s); break;
-      case 64: launch_bwd_redo<64, E>(d, q, k, v, off, ek, ev, go, w, s); break;
-      case 96: launch_bwd_redo<96, E>(d, q, k, v, off, ek, ev, go, w, s); break;
-      default: launch_bwd_redo<128, E>(d, q, k, v, off, ek, ev, go, w, s); break;
+    if (!w.h16) {
+      hipLaunchKernelGGL(acc_to_bf16_kernel, cgrid, dim3(256), 0, s, w.dk32, w.dv32,
+                         static_cast<bf16*>(dk), static_cast<bf16*>(dv), rows, D, d.k_stride,
+                         d.v_stride, static_cast<const int*>(nullptr));
+    } else {
+      hipLaunchKernelGGL(h16_to_bf16_kernel, cgrid, dim3(256), 0, s,
+                         static_cast<const _Float16*>(w.dk_acc), static_cast<const _Float16*>(w.dv_acc),
+                         static_cast<bf16*>(dk), static_cast<bf16*>(dv), rows, D, d.k_stride,
+                         d.v_stride, w.scales, w.flag);
+      // after an fp16 overflow (flag set): dK and dV again in fp32
+      switch (d.head_dim) {
+        case 32: launch_bwd_redo<32, E>(d, q, k, v, off, ek, ev, go, w, s); break;
+        case 64: launch_bwd_redo<64, E>(d, q, k, v, off, ek, ev, go, w, s); break;
+        case 96: launch_bwd_redo<96, E>(d, q, k, v, off, ek, ev, go, w, s); break;
+        default: launch_bwd_redo<128, E>(d, q, k, v, off, ek, ev, go, w, s); break;
+      }
+      // grid-stride: a small grid keeps the launch cheap when there is nothing to do
+      hipLaunchKernelGGL(acc_to_bf16_kernel, dim3(std::min(cgrid.x, 1024u), 2), dim3(256), 0, s,
+                         w.dk32, w.dv32, static_cast<bf16*>(dk), static_cast<bf16*>(dv), rows, D,
+                         d.k_stride, d.v_stride, static_cast<const int*>(w.flag));
     }
-    // grid-stride: a small grid keeps the launch cheap when there is nothing to do
-    hipLaunchKernelGGL(acc_to_bf16_kernel, dim3(std::min(cgrid.x, 1024u), 2), dim3(256), 0, s,
-                       w.dk32, w.dv32, static_cast<bf16*>(dk), static_cast<bf16*>(dv), rows, D,
-                       d.k_stride, d.v_stride, static_cast<const int*>(w.flag));
     if (erows > 0) {
       const dim3 egrid(fill_blocks(erows * (D / 8)), 2);
       hipLaunchKernelGGL(acc_to_bf16_kernel, egrid, dim3(256), 0, s, w.dek_acc, w.dev_acc,

@@ -707,20 +707,25 @@ __device__ __forceinline__ bool slot_weight(const Slot& s, uint32_t key, float& 
   return hit;
 }
 
-// Table values at the slot's 4 (y, x) corners of the current plane.  A lower
-// corner row outside the volume reads its in-volume neighbour row (it has
-// weight 0).  Each row's two x corners are one paired read of entries base and
-// base + 1: an upper x corner outside the volume (weight fx = 0) reads the
-// next entry, which the table's zeroed start or an earlier step left finite.
-// Every index is at most kChunkNV, inside a table row even for a slot of
-// another chunk (whose values are then discarded).
+// Table values at the slot's 4 (y, x) corners of the current plane.  An upper
+// corner row outside the volume (dy = 0, weight fy = 0) reads the lower row
+// again.  Each row's two x corners are one paired read of entries base and
+// base + 1; for an upper x corner outside the volume (weight fx = 0) entry
+// base + 1 belongs to another voxel, so its value is replaced by 0 (one
+// select): grid_sample skips out-of-volume corners, and a non-finite score of
+// that other voxel must not reach this tap as 0 * inf.  Every index is at most
+// kChunkNV, inside a table row even for a slot of another chunk (whose values
+// are then discarded).
 __device__ __forceinline__ void corners4(const Slot& s, const float* row, float& t00, float& t01,
                                          float& t10, float& t11) {
   const int base = s.idx & 0x1ff, dy = (s.idx >> 9) & 0x1f;
+  const bool hx = (s.idx >> 14) & 1;
   t00 = row[base];
-  t01 = row[base + 1];
+  const float r01 = row[base + 1];
   t10 = row[base + dy];
-  t11 = row[base + dy + 1];
+  const float r11 = row[base + dy + 1];
+  t01 = hx ? r01 : 0.0f;
+  t11 = hx ? r11 : 0.0f;
 }
 
 // Zeroes NB whole tables (pad columns included).

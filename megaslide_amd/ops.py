@@ -52,7 +52,7 @@ class _CoreCall:
     """Validated shapes of one attention-core call and its C descriptor."""
 
     def __init__(self, q, k, v, offsets, video_shape, num_heads, kernel_size, offset_scale, algo,
-                 dropout=(0.0, 0, 0), extra_k=None, extra_v=None):
+                 dropout=(0.0, 0, 0), extra_k=None, extra_v=None, dkv_accum="fp32"):
         self.dev = _require_device(q, k, v, offsets, extra_k, extra_v)
         B, N, D = q.shape
         T, H, W = (int(s) for s in video_shape)
@@ -70,6 +70,10 @@ class _CoreCall:
             raise ValueError(f"offsets must be {(B, N, C)}, got {tuple(offsets.shape)}")
         if algo not in _lib.ALGOS:
             raise ValueError(f"algo must be one of {sorted(_lib.ALGOS)}")
+        if dkv_accum not in _lib.ACCUMS:
+            raise ValueError(f"dkv_accum must be one of {sorted(_lib.ACCUMS)}")
+        if dkv_accum == "fp16" and dt != torch.bfloat16:
+            raise ValueError("dkv_accum='fp16' needs bfloat16 tensors")
         self.q = _tokens_major(q, B, N, D)
         self.k = _tokens_major(k, B, N, D)
         self.v = _tokens_major(v, B, N, D)
@@ -80,6 +84,7 @@ class _CoreCall:
         self.dtype = dt
         self.offset_scale = float(offset_scale)
         self.algo = algo
+        self.dkv_accum = dkv_accum
         p, seed, offset = dropout
         if not 0.0 <= float(p) < 1.0:
             raise ValueError(f"dropout probability must be in [0, 1), got {p}")
@@ -108,7 +113,8 @@ class _CoreCall:
             self.k.stride(1) if ks is None else ks,
             self.v.stride(1) if vs is None else vs,
             self.offset_scale, 1.0 / math.sqrt(self.hd), _lib.ALGOS[self.algo],
-            self.dropout[2], self.dropout[1], self.dropout[0], self.G)
+            self.dropout[2], self.dropout[1], self.dropout[0], self.G,
+            _lib.ACCUMS[self.dkv_accum])
 
     def forward(self, want_lse: bool):
         out = torch.empty((self.B, self.N, self.D), dtype=self.dtype, device=self.dev)
@@ -129,12 +135,12 @@ class DSA3DCoreFunction(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, v, offsets, extra_k, extra_v, video_shape, num_heads, kernel_size,
-                offset_scale, algo, dropout):
+                offset_scale, algo, dropout, dkv_accum):
         call = _CoreCall(q, k, v, offsets, video_shape, num_heads, kernel_size, offset_scale, algo,
-                         dropout, extra_k, extra_v)
+                         dropout, extra_k, extra_v, dkv_accum)
         out, lse = call.forward(want_lse=True)
         ctx.call = (call.B, call.T, call.H, call.W, call.nh, call.hd, call.ksz, call.dtype,
-                    call.offset_scale, algo, call.dropout)
+                    call.offset_scale, algo, call.dropout, dkv_accum)
         ctx.has_extra = call.G > 0
         ctx.save_for_backward(call.q, call.k, call.v, call.off, out, lse, call.ek, call.ev)
         return out, lse
@@ -142,7 +148,7 @@ class DSA3DCoreFunction(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dout, dlse):
         q, k, v, offsets, out, lse, ek, ev = ctx.saved_tensors
-        B, T, H, W, nh, hd, ksz, dt, offset_scale, algo, dropout = ctx.call
+        B, T, H, W, nh, hd, ksz, dt, offset_scale, algo, dropout, dkv_accum = ctx.call
         dev = q.device
         N, D = T * H * W, nh * hd
         if dout is None:
@@ -153,7 +159,7 @@ class DSA3DCoreFunction(torch.autograd.Function):
         # gradients are written with the token strides of the desc: contiguous here
         qc, kc, vc = (t if t.stride(1) == D else t.contiguous() for t in (q, k, v))
         call = _CoreCall(qc, kc, vc, offsets, (T, H, W), nh, ksz, offset_scale, algo, dropout,
-                         ek if ctx.has_extra else None, ev if ctx.has_extra else None)
+                         ek if ctx.has_extra else None, ev if ctx.has_extra else None, dkv_accum)
         desc = call.desc(D, D, D)
         dq = torch.empty((B, N, D), dtype=dt, device=dev)
         dk = torch.empty((B, N, D), dtype=dt, device=dev)
@@ -171,14 +177,15 @@ class DSA3DCoreFunction(torch.autograd.Function):
                 lse.data_ptr(), _lib.ptr(dlse), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
                 doff.data_ptr(), _lib.ptr(dek), _lib.ptr(dev_), ws.data_ptr(), ws_bytes,
                 _lib.stream_handle(dev)), "dsa3d_bwd")
-        return dq, dk, dv, doff, dek, dev_, None, None, None, None, None, None
+        return dq, dk, dv, doff, dek, dev_, None, None, None, None, None, None, None
 
 
 def dsa3d_core(q: Tensor, k: Tensor, v: Tensor, offsets: Tensor, video_shape: Sequence[int],
                num_heads: int, kernel_size: Sequence[int] = (3, 7, 7), offset_scale: float = 1.0,
                return_lse: bool = False, algo: str = "auto", dropout_p: float = 0.0,
                dropout_seed: Optional[int] = None, dropout_offset: int = 0,
-               extra_k: Optional[Tensor] = None, extra_v: Optional[Tensor] = None):
+               extra_k: Optional[Tensor] = None, extra_v: Optional[Tensor] = None,
+               dkv_accum: str = "fp32"):
     """Attention core on device tensors.
 
     q, k, v: [B, N, D]; offsets: [B, N, num_heads*kt*kh*kw*3] unscaled, channel
@@ -196,6 +203,11 @@ def dsa3d_core(q: Tensor, k: Tensor, v: Tensor, offsets: Tensor, video_shape: Se
     values shared by every query, appended to its taps before the softmax
     (the reference's ``extra_kv``, attention.py:160-173); extra key g is tap
     K + g for dropout.
+
+    ``dkv_accum`` chooses how the backward sums dK / dV over query tiles:
+    "fp32" (default, the reference's fp32 grid_sample backward precision) or,
+    for bfloat16 tensors, "fp16" (power-of-two-scaled fp16 pairs: fewer atomic
+    bytes, 11 significant bits per running sum, an fp32 redo on overflow).
     """
     p = float(dropout_p)
     if p > 0.0 and dropout_seed is None:
@@ -205,11 +217,11 @@ def dsa3d_core(q: Tensor, k: Tensor, v: Tensor, offsets: Tensor, video_shape: Se
     if torch.is_grad_enabled() and any(t.requires_grad for t in grads):
         out, lse = DSA3DCoreFunction.apply(q, k, v, offsets, extra_k, extra_v, tuple(video_shape),
                                            int(num_heads), tuple(kernel_size), float(offset_scale),
-                                           algo, dropout)
+                                           algo, dropout, dkv_accum)
         return (out, lse) if return_lse else out
     # forward only: nothing saved, no lse unless asked for
     call = _CoreCall(q, k, v, offsets, video_shape, num_heads, kernel_size, offset_scale, algo,
-                     dropout, extra_k, extra_v)
+                     dropout, extra_k, extra_v, dkv_accum)
     out, lse = call.forward(want_lse=return_lse)
     return (out, lse) if return_lse else out
 
@@ -232,7 +244,7 @@ def _conv_desc(x: Tensor, video_shape, kernel: Tuple[int, int, int], act: int) -
 
 class DwConv3dFunction(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, x, weight, bias, video_shape, act):
+    def forward(ctx, x, weight, bias, video_shape, act, keep_preact):
         dev = _require_device(x, weight, bias)
         x = x.contiguous()
         C = x.shape[2]
@@ -243,9 +255,10 @@ class DwConv3dFunction(torch.autograd.Function):
         b = None if bias is None else bias.to(x.dtype).contiguous()
         desc = _conv_desc(x, video_shape, kernel, _ACT[act])
         y = torch.empty_like(x)
-        # GELU: keep its input for the backward (what nn.GELU's autograd keeps),
-        # when a gradient will be asked for
-        z = torch.empty_like(x) if (act == "gelu" and torch.is_grad_enabled()) else None
+        # GELU: keep its input for the backward (what nn.GELU's autograd keeps)
+        # when the caller will ask for a gradient (decided outside: autograd runs
+        # this forward with gradients disabled)
+        z = torch.empty_like(x) if (act == "gelu" and keep_preact) else None
         lib = _lib.load()
         with torch.cuda.device(dev):
             _lib.check(lib.msd_dwconv3d_fwd(ctypes.byref(desc), x.data_ptr(), w.data_ptr(),
@@ -282,10 +295,12 @@ class DwConv3dFunction(torch.autograd.Function):
             dw = dw.to(ctx.wdtype)
         if db is not None:
             db = db.to(ctx.bdtype)
-        return dx, dw, db, None, None
+        return dx, dw, db, None, None, None
 
 
 def dwconv3d(x: Tensor, weight: Tensor, bias: Optional[Tensor], video_shape: Sequence[int],
              act: Optional[str] = None) -> Tensor:
     """Depthwise conv on channel-last tokens x [B, N, C]; weight [C, 1, kt, kh, kw]."""
-    return DwConv3dFunction.apply(x, weight, bias, tuple(video_shape), act)
+    keep = torch.is_grad_enabled() and any(
+        t is not None and t.requires_grad for t in (x, weight, bias))
+    return DwConv3dFunction.apply(x, weight, bias, tuple(video_shape), act, keep)

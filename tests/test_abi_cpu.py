@@ -33,7 +33,7 @@ def test_exports_match_header():
 
 
 def test_abi_version():
-    assert _lib.load().msd_abi_version() == _lib.ABI_VERSION == 4
+    assert _lib.load().msd_abi_version() == _lib.ABI_VERSION == 5
 
 
 def _desc(**kw):
@@ -67,6 +67,8 @@ def test_null_desc_rejected():
     ("dropout_p", float("nan"), -1, b"dropout_p"),
     ("extra_g", -1, -1, b"extra_g"),
     ("extra_g", 5000, -1, b"extra_g"),
+    ("dkv_accum", 2, -1, b"dkv_accum"),
+    ("dkv_accum", 1, -1, b"bf16 storage"),   # scaled fp16 sums: bf16 only (dtype 0 here)
 ])
 def test_bad_desc_fields(field, value, code, needle):
     rc = _fwd(_desc(**{field: value}))
@@ -103,15 +105,23 @@ def test_workspace_size_and_check():
     # kernels' accumulators are less than p and ds, and the larger of the two
     # is asked for); for bf16 one word of two fp16 per tap plus one fp32 per
     # (token, head), beside fp32 rows (which also hold the fp16 accumulators),
-    # then the scale bounds (4 floats from each of 256 blocks) and 32 bytes of
+    # then the scale bounds (8 floats from each of 256 blocks) and 32 bytes of
     # scales and overflow flag
     taps = rows * 2 * 147 * 4
-    records = 256 * 4 * 4
+    records = 256 * 8 * 4
     for dtype, want in ((0, max(2 * rows * 128 * 4, 2 * taps)),
                         (1, 2 * rows * 128 * 4 + taps + rows * 2 * 4 + records + 32)):
         d = _desc(B=2, dtype=dtype)
         need = lib.msd_dsa3d_bwd_workspace_size(ctypes.byref(d))
         assert need == want
+    # with extra keys the tiled backward also keeps their fp32 part of dq
+    dx = _desc(B=2, dtype=1, extra_g=8)
+    G, D = 8, 128
+    want = (2 * rows * D * 4 + 2 * 2 * G * D * 4 + taps + rows * 2 * 4)
+    want = (want + 255) // 256 * 256 + 2 * rows * 2 * G * 2
+    want = (want + 255) // 256 * 256 + rows * D * 4
+    want = (want + 255) // 256 * 256 + records + 32
+    assert lib.msd_dsa3d_bwd_workspace_size(ctypes.byref(dx)) == want
     rc = lib.msd_dsa3d_bwd(ctypes.byref(d), *([16] * 4), None, None, *([16] * 3), None,
                            *([16] * 4), None, None, 16, need - 1, None)
     assert rc == -4 and b"workspace" in lib.msd_last_error()

@@ -110,3 +110,40 @@ def test_gelu_preact_kept_or_recomputed(cfg, dtype, tol):
         assert rel_err(dx.double().cpu(), xr.grad) < tol, name
         assert rel_err(dw.double().cpu().reshape(wr.shape), wr.grad) < tol, name
         assert rel_err(db.double().cpu(), br.grad) < tol, name
+
+
+def _saved_preacts(t):
+    """The GELU input each depthwise-conv node of t's graph saved (None where
+    it saved none), for the nodes with act = "gelu"."""
+    seen, stack, found = set(), [t.grad_fn], []
+    while stack:
+        fn = stack.pop()
+        if fn is None or fn in seen:
+            continue
+        seen.add(fn)
+        if type(fn).__name__ == "DwConv3dFunctionBackward" and getattr(fn, "act", None) == "gelu":
+            found.append(fn.saved_tensors[3])
+        stack.extend(f for f, _ in fn.next_functions)
+    return found
+
+
+def test_module_keeps_gelu_input_for_backward():
+    """Inside the module (autograd runs a Function's forward with gradients
+    disabled) the offset predictor's conv still keeps the GELU input when a
+    gradient will be taken, and keeps nothing under no_grad."""
+    from megaslide_amd import DeformableSlideAttention3D
+
+    print("[module GELU input kept]", flush=True)
+    m = DeformableSlideAttention3D(128, 2).to(DEV)
+    x = torch.randn(1, 2 * 4 * 5, 128, device=DEV, requires_grad=True)
+    y = m(x, (2, 4, 5))
+    z = _saved_preacts(y)
+    assert len(z) == 1 and z[0] is not None and z[0].shape == x.shape
+    y.sum().backward()
+    assert x.grad is not None and torch.isfinite(x.grad).all()
+    with torch.no_grad():
+        assert m(x, (2, 4, 5)).grad_fn is None
+    # parameters needing a gradient suffice (input without one)
+    x2 = torch.randn(1, 2 * 4 * 5, 128, device=DEV)
+    z2 = _saved_preacts(m(x2, (2, 4, 5)))
+    assert len(z2) == 1 and z2[0] is not None
