@@ -115,6 +115,28 @@ WORKLOADS = {
         metric="3D-DSA fwd+bwd tokens/sec at 131k tokens bf16",
         workload="3D-DSA fwd+bwd HIP kernel set, large-block 131,072 tokens, 24 x 128",
         cpu_slab=dict(T=2, H=24, W=24)),
+    "long-clip-65k-module": dict(
+        B=1, T=64, H=32, W=32, D=1024, nh=16, kernel=(3, 7, 7), dtype="bf16",
+        offsets=("module", 0.5), backward=True, module="attention",
+        metric="3D-DSA module fwd+bwd tokens/sec at 65k tokens bf16, projections and offset "
+               "GEMM included",
+        workload="DeformableSlideAttention3D fwd+bwd (HIP kernels + PyTorch GEMMs), long-clip "
+                 "65,536 tokens",
+        cpu_slab=dict(T=4)),
+    "dit-block-46k-ckpt": dict(
+        B=1, T=13, H=45, W=80, D=1536, nh=16, kernel=(3, 7, 7), dtype="bf16",
+        offsets=("block", 4.0), backward=True, module="block", checkpoint="keep-core",
+        metric="DiT block fwd+bwd tokens/sec at 46.8k tokens bf16, gradient checkpointing",
+        workload="MegaSlideDiT block (pre-LN 3D-DSA + MLP x4) fwd+bwd under gradient "
+                 "checkpointing that keeps the attention core's outputs, 46,800 tokens, 16 x 96",
+        cpu_slab=dict(T=3, H=24, W=40)),
+    "dit-block-46k-ckpt-plain": dict(
+        B=1, T=13, H=45, W=80, D=1536, nh=16, kernel=(3, 7, 7), dtype="bf16",
+        offsets=("block", 4.0), backward=True, module="block", checkpoint="plain",
+        metric="DiT block fwd+bwd tokens/sec at 46.8k tokens bf16, gradient checkpointing",
+        workload="MegaSlideDiT block (pre-LN 3D-DSA + MLP x4) fwd+bwd under plain gradient "
+                 "checkpointing (whole forward recomputed), 46,800 tokens, 16 x 96",
+        cpu_slab=dict(T=3, H=24, W=40)),
     "dit-block-46k": dict(
         B=1, T=13, H=45, W=80, D=1536, nh=16, kernel=(3, 7, 7), dtype="bf16",
         offsets=("net", 0.02, 0.02, ("uniform", 4.0)), backward=True,
@@ -311,6 +333,217 @@ def run_gpu(cfg, steps, warmup, calibrate=False):
     per_phase = {name: sum(evs[s][i][0].elapsed_time(evs[s][i][1]) for s in range(steps)) / steps
                  for i, (name, _) in enumerate(phases)}
     return dict(total_ms=total_ms, wall_s=wall, per_phase_ms=per_phase, tokens=B * N)
+
+
+class _BlockConfig:
+    """The MegaSlideConfig fields a DiT block reads (MLP ratio 4, no dropout)."""
+
+    def __init__(self, D, nh, kernel):
+        self.hidden_size, self.num_heads, self.dsa_kernel_size = D, nh, kernel
+        self.offset_scale, self.dropout, self.mlp_hidden_size = 1.0, 0.0, 4 * D
+
+
+def _init_like_model(mod, g):
+    """MegaSlideDiT._init_weights (model.py:164-178): Xavier-uniform weights and
+    zero biases for every Linear and Conv3d (the offset net's last conv
+    included), LayerNorms at their defaults."""
+    for m in mod.modules():
+        if isinstance(m, (torch.nn.Linear, torch.nn.Conv3d)):
+            w = m.weight
+            fan_out = w.shape[0] * (w[0][0].numel() if w.dim() > 2 else 1)
+            fan_in = w[0].numel()
+            a = math.sqrt(6.0 / (fan_in + fan_out))
+            with torch.no_grad():
+                w.copy_((torch.rand(w.shape, generator=g) * 2 - 1) * a)
+                if m.bias is not None:
+                    m.bias.zero_()
+
+
+def build_module(cfg, dev):
+    """The module of a module workload, in its dtype on `dev`, and its inputs:
+    x (for the block: tokens plus a timestep embedding ~ N(0, 1), added at the
+    model input as model.py:212-214 does) and an upstream gradient ~ N(0, 1)."""
+    from megaslide_amd import DeformableSlideAttention3D, DiTBlock, dwconv3d
+
+    B, T, H, W, D, nh = cfg["B"], cfg["T"], cfg["H"], cfg["W"], cfg["D"], cfg["nh"]
+    N = T * H * W
+    dt = torch.bfloat16 if cfg["dtype"] == "bf16" else torch.float32
+    g = torch.Generator().manual_seed(11)
+    if cfg["module"] == "attention":
+        mod = DeformableSlideAttention3D(D, nh, kernel_size=cfg["kernel"])
+    else:
+        mod = DiTBlock(_BlockConfig(D, nh, cfg["kernel"]))
+    _init_like_model(mod, g)
+    attn = mod if cfg["module"] == "attention" else mod.attn
+    gd = torch.Generator(device=dev).manual_seed(12)
+    x = torch.randn(B, N, D, generator=gd, device=dev)
+    if cfg["module"] == "block":
+        x = x + torch.randn(B, 1, D, generator=gd, device=dev)
+        # offsets with a uniform per-tap voxel bias (config's U(-a, a))
+        with torch.no_grad():
+            on2 = attn.offset_net[2]
+            a = cfg["offsets"][1]
+            on2.bias.copy_(torch.rand(on2.bias.shape, generator=g) * 2 * a - a)
+    mod = mod.to(dev, dt)
+    x = x.to(dt)
+    if cfg["module"] == "attention":
+        # predicted offsets of the configured spread: the last conv's weights
+        # scaled from the features they see
+        with torch.no_grad():
+            on0, on2 = attn.offset_net[0], attn.offset_net[2]
+            feat = dwconv3d(x, on0.weight, on0.bias, (T, H, W), act="gelu").float()
+            sd = cfg["offsets"][1] / (feat.std().item() * math.sqrt(D))
+            on2.weight.copy_((torch.randn(on2.weight.shape, generator=g) * sd).to(dt))
+    gy = torch.randn(B, N, D, generator=gd, device=dev).to(dt)
+    return mod, attn, x, gy
+
+
+def run_module(cfg, steps, warmup):
+    """Module workloads: forward + backward of the whole module (the attention
+    module with its PyTorch GEMMs, or the DiT block, optionally checkpointed),
+    torch.autograd.grad over the input and every parameter, as the trainer
+    takes them (infinity/video/trainer.py:431-438).  One more, untimed step
+    brackets every call of the HIP library with events on the current stream
+    (per-kernel-set times; the rest is PyTorch: GEMMs, norms, elementwise)."""
+    from torch.utils.checkpoint import checkpoint
+
+    from megaslide_amd import _lib, checkpoint_keep_core
+
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    B, T, H, W = cfg["B"], cfg["T"], cfg["H"], cfg["W"]
+    mod, attn, x, gy = build_module(cfg, dev)
+    params = list(mod.parameters())
+    ckpt = cfg.get("checkpoint")
+    stream = torch.cuda.current_stream(dev)
+
+    def step(ev=None):
+        xi = x.detach().requires_grad_(True)
+        if ckpt == "keep-core":
+            y = checkpoint_keep_core(mod, xi, (T, H, W))
+        elif ckpt == "plain":
+            y = checkpoint(mod, xi, (T, H, W), use_reentrant=False)
+        else:
+            y = mod(xi, (T, H, W))
+        if ev is not None:
+            ev.record(stream)
+        return torch.autograd.grad(y, [xi] + params, grad_outputs=gy, allow_unused=True)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    marks = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+    t_start = torch.cuda.Event(enable_timing=True)
+    t_end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    wall0 = time.perf_counter()
+    t_start.record(stream)
+    for sidx in range(steps):
+        marks[sidx][0].record(stream)
+        step(marks[sidx][1])
+        marks[sidx][2].record(stream)
+    t_end.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    total_ms = t_start.elapsed_time(t_end)
+    fwd = sum(m[0].elapsed_time(m[1]) for m in marks) / steps
+    bwd = sum(m[1].elapsed_time(m[2]) for m in marks) / steps
+
+    # instrumented step: events around each library call
+    lib = _lib.load()
+    names = ("msd_dsa3d_fwd", "msd_dsa3d_bwd", "msd_dwconv3d_fwd", "msd_dwconv3d_bwd")
+    orig = {n: getattr(lib, n) for n in names}
+    rec = {n: [] for n in names}
+
+    def wrap(n):
+        f = orig[n]
+
+        def w(*a):
+            s = torch.cuda.current_stream()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(s)
+            rc = f(*a)
+            e1.record(s)
+            rec[n].append((e0, e1))
+            return rc
+        return w
+
+    for n in names:
+        setattr(lib, n, wrap(n))
+    try:
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        step()
+        e1.record(stream)
+        torch.cuda.synchronize()
+    finally:
+        for n in names:
+            setattr(lib, n, orig[n])
+    inst_ms = e0.elapsed_time(e1)
+    hip = {n[4:]: dict(calls=len(v), ms=round(sum(a.elapsed_time(b) for a, b in v), 4))
+           for n, v in rec.items()}
+    hip_total = sum(v["ms"] for v in hip.values())
+    return dict(total_ms=total_ms, wall_s=wall, tokens=B * T * H * W, fwd_ms=fwd, bwd_ms=bwd,
+                hip=hip, other_ms=inst_ms - hip_total, inst_ms=inst_ms,
+                bwd_call_ms=hip["dsa3d_bwd"]["ms"] / max(1, hip["dsa3d_bwd"]["calls"]))
+
+
+def module_flops(cfg):
+    """Dense GEMM flops of one step (forward, backward's two products per GEMM,
+    and the checkpoint's recomputed forward)."""
+    N, D, nh, C = _sizes(cfg)
+    per = 2 * N * (4 * D * D + D * C)          # q, k, v, out projections and the offset 1x1 conv
+    if cfg["module"] == "block":
+        per += 2 * N * 2 * D * 4 * D           # MLP fc1, fc2
+    return per * (3 + (1 if cfg.get("checkpoint") else 0))
+
+
+def cpu_baseline_module(cfg, runs=3):
+    """float32 CPU oracle of the same module (the reference op sequence: the
+    attention module restatement, or the DiT block around it) on a slab of the
+    workload, forward + backward over the input and every parameter, one
+    warm-up then the median of `runs`; its tokens/s stands for the workload's."""
+    from oracle.dsa3d_ref import dit_block_ref, dsa3d_module_ref
+
+    slab = dict(B=cfg["B"], T=cfg["T"], H=cfg["H"], W=cfg["W"])
+    slab.update(cfg["cpu_slab"])
+    B, T, H, W = slab["B"], slab["T"], slab["H"], slab["W"]
+    from megaslide_amd import DeformableSlideAttention3D, DiTBlock
+    D, nh = cfg["D"], cfg["nh"]
+    g = torch.Generator().manual_seed(11)
+    m = (DeformableSlideAttention3D(D, nh, kernel_size=cfg["kernel"]) if cfg["module"] == "attention"
+         else DiTBlock(_BlockConfig(D, nh, cfg["kernel"])))
+    _init_like_model(m, g)
+    params = {n: p.detach().float().clone().requires_grad_(True) for n, p in m.named_parameters()}
+    N = T * H * W
+    x = torch.randn(B, N, D, requires_grad=True)
+    gy = torch.randn(B, N, D)
+
+    def one():
+        if cfg["module"] == "attention":
+            y = dsa3d_module_ref(x, params, (T, H, W), nh, cfg["kernel"], 1.0, head_chunk=4)
+        else:
+            y = dit_block_ref(x, params, (T, H, W), nh, cfg["kernel"], 1.0, head_chunk=4)
+        torch.autograd.grad(y, [x] + list(params.values()), grad_outputs=gy, allow_unused=True)
+
+    one()
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        one()
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    return dict(
+        value=B * N / med, unit="tokens/s", cores=torch.get_num_threads(), kind="port",
+        sample=(f"slab-extrapolated: float32 CPU oracle of the whole "
+                f"{'attention module' if cfg['module'] == 'attention' else 'DiT block'} "
+                f"(GEMMs, depthwise convs, grid_sample/matmul/softmax core"
+                f"{', LayerNorms, MLP' if cfg['module'] == 'block' else ''}), fwd+bwd on a "
+                f"B={B}, T={T}, H={H}, W={W} slab ({B * N} tokens, dim {D}, {nh}x{D // nh}); "
+                f"median of {runs} runs after a warm-up: " + ", ".join(f"{t:.2f}" for t in times)
+                + " s"),
+        cpu_model=_cpu_model(), torch_version=torch.__version__, seconds=med)
 
 
 def _cpu_model():
@@ -549,6 +782,68 @@ def counter_table(*dirs):
               f"{f(wait / wc if wait and wc else None, 2)} |")
 
 
+def module_line(args, cfg):
+    """The JSON line of a module workload (the attention module with its GEMMs,
+    or the DiT block)."""
+    r = run_module(cfg, args.steps, args.warmup)
+    e = 2 if cfg["dtype"] == "bf16" else 4
+    kb = kernel_bytes(cfg, e)
+    ms_step = r["total_ms"] / args.steps
+    N, D, nh, C = _sizes(cfg)
+    bwd_ms = r["bwd_call_ms"]
+    achieved = kb["dsa3d_bwd"] / (bwd_ms / 1e3) / 1e9
+    flops = module_flops(cfg)
+    line = {
+        "metric": cfg["metric"],
+        "value": round(r["tokens"] / (ms_step / 1e3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": cfg["dtype"],
+        "data": "synthetic",
+        "config": {
+            "workload": cfg["workload"],
+            "B": cfg["B"], "T": cfg["T"], "H": cfg["H"], "W": cfg["W"], "dim": D,
+            "heads": nh, "head_dim": D // nh, "window": list(cfg["kernel"]),
+            "offsets": (f"offset net's predictions, spread ~ N(0, {cfg['offsets'][1]})"
+                        if cfg["module"] == "attention" else
+                        f"offset net with its bias ~ U(-{cfg['offsets'][1]}, "
+                        f"{cfg['offsets'][1]}) voxels, Xavier weights (model.py:164-178)"),
+            "accumulation": "fp32 (dK/dV: fp32 atomics)",
+            "pass": "fwd+bwd", "checkpoint": cfg.get("checkpoint", "none"),
+            "init": "Xavier-uniform weights, zero biases (MegaSlideDiT._init_weights)",
+        },
+        "per_phase_ms": {"forward": round(r["fwd_ms"], 4), "backward": round(r["bwd_ms"], 4)},
+        "hip_calls_one_step": r["hip"],
+        "pytorch_ops_ms_one_step": round(r["other_ms"], 4),
+        "gemm_tflops": round(flops / (ms_step / 1e3) / 1e12, 1),
+        "gemm_flops_per_step": flops,
+        "hbm_gbps_hip_set": round(step_bytes(cfg, e) / (ms_step / 1e3) / 1e9, 1),
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "dsa3d_bwd",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBPS, 4),
+            "traffic": measured_traffic(args.workload, "dsa3d_bwd"),
+            "algorithmic_bytes_per_launch": kb["dsa3d_bwd"],
+            "avg_launch_ms": round(bwd_ms, 4),
+        },
+        "wall_s_timed_region": round(r["wall_s"], 3),
+    }
+    if not args.no_cpu_baseline:
+        cb = cpu_baseline_module(cfg)
+        line["cpu_baseline"] = {k: (round(v, 2) if isinstance(v, float) else v)
+                                for k, v in cb.items() if k != "seconds"}
+    return line
+
+
 def main():
     if len(sys.argv) == 6 and sys.argv[1] == "--summarize":
         summarize(*sys.argv[2:])
@@ -567,11 +862,13 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: the 3D-DSA kernels run on a single MI355X "
-              "and no multi-GPU path is built (see DESIGN.md for how it would shard).",
-              file=sys.stderr)
+              "and no multi-GPU path is built.", file=sys.stderr)
         sys.exit(2)
 
     cfg = WORKLOADS[args.workload]
+    if "module" in cfg:
+        print(json.dumps(module_line(args, cfg)), flush=True)
+        return
     r = run_gpu(cfg, args.steps, args.warmup, args.copy_calibration)
     e = 2 if cfg["dtype"] == "bf16" else 4
     kb = kernel_bytes(cfg, e)

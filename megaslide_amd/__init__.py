@@ -2,12 +2,17 @@
 
 Public surface:
   DeformableSlideAttention3D   drop-in for infinity/video/attention.py:19-273
-  dsa3d_core                   fused attention core (autograd)
+  DiTBlock, MLP                drop-ins for infinity/video/model.py:21-117 around it
+  dsa3d_core                   fused attention core (autograd; the custom
+                               operator torch.ops.megaslide.dsa3d_core)
   dwconv3d                     depthwise 3-D conv (+GELU) on channel-last tokens (autograd)
+  keep_core_policy, keep_core_context, checkpoint_keep_core
+                               selective checkpointing that keeps the core's outputs
 """
 
 from .attention import DeformableSlideAttention3D
-from .ops import DSA3DCoreFunction, DwConv3dFunction, dsa3d_core, dwconv3d
+from .block import MLP, DiTBlock, checkpoint_keep_core
+from .ops import DwConv3dFunction, dsa3d_core, dwconv3d, keep_core_context, keep_core_policy
 
-__all__ = ["DeformableSlideAttention3D", "DSA3DCoreFunction", "DwConv3dFunction", "dsa3d_core",
-           "dwconv3d"]
+__all__ = ["DeformableSlideAttention3D", "DiTBlock", "MLP", "DwConv3dFunction", "dsa3d_core",
+           "dwconv3d", "keep_core_policy", "keep_core_context", "checkpoint_keep_core"]

@@ -1,20 +1,21 @@
 """Autograd functions over the HIP kernels.
 
 ``dsa3d_core``   attention core (trilinear K/V sampling + local softmax attention)
-                 replacing infinity/video/attention.py:106-186 of the reference.
+                 replacing infinity/video/attention.py:106-186 of the reference,
+                 as the custom operators megaslide::dsa3d_core (+ _bwd).
 ``dwconv3d``     depthwise 3-D conv (+ optional exact-erf GELU) replacing the
                  reference's nn.Conv3d(groups=D) terms (attention.py:58-74).
 
-Both follow the reference's own idiom for custom autograd
-(infinity/ops/layers.py:16-62: save_for_backward + explicit backward).  They
-run only on ROCm device tensors; there is no CPU path.
+Both save their inputs and outputs for an explicit backward, the reference's
+own idiom for custom autograd (infinity/ops/layers.py:16-62).  They run only on
+ROCm device tensors; there is no CPU path.
 """
 
 from __future__ import annotations
 
 import ctypes
 import math
-from typing import Optional, Sequence, Tuple
+from typing import List, Optional, Sequence, Tuple
 
 import torch
 
@@ -130,54 +131,135 @@ class _CoreCall:
         return out, lse
 
 
-class DSA3DCoreFunction(torch.autograd.Function):
-    """out, lse = core(q, k, v, offsets[, extra_k, extra_v]); both outputs differentiable."""
+# The attention core is a torch.library custom operator (forward and
+# backward), so the dispatcher sees it: torch.utils.checkpoint's selective
+# policies can keep its outputs instead of recomputing it (keep_core_policy
+# below), and torch.compile treats it as one opaque op.  The seed travels as a
+# signed 64-bit int (the schema's int), the bits unchanged.
 
-    @staticmethod
-    def forward(ctx, q, k, v, offsets, extra_k, extra_v, video_shape, num_heads, kernel_size,
-                offset_scale, algo, dropout, dkv_accum):
-        call = _CoreCall(q, k, v, offsets, video_shape, num_heads, kernel_size, offset_scale, algo,
-                         dropout, extra_k, extra_v, dkv_accum)
-        out, lse = call.forward(want_lse=True)
-        ctx.call = (call.B, call.T, call.H, call.W, call.nh, call.hd, call.ksz, call.dtype,
-                    call.offset_scale, algo, call.dropout, dkv_accum)
-        ctx.has_extra = call.G > 0
-        ctx.save_for_backward(call.q, call.k, call.v, call.off, out, lse, call.ek, call.ev)
-        return out, lse
+def _seed_in(seed: int) -> int:
+    seed &= 0xFFFFFFFFFFFFFFFF
+    return seed - (1 << 64) if seed >= (1 << 63) else seed
 
-    @staticmethod
-    def backward(ctx, dout, dlse):
-        q, k, v, offsets, out, lse, ek, ev = ctx.saved_tensors
-        B, T, H, W, nh, hd, ksz, dt, offset_scale, algo, dropout, dkv_accum = ctx.call
-        dev = q.device
-        N, D = T * H * W, nh * hd
-        if dout is None:
-            dout = torch.zeros_like(out)
-        dout = dout.to(dt).contiguous()
-        if dlse is not None:
-            dlse = dlse.to(torch.float32).contiguous()
-        # gradients are written with the token strides of the desc: contiguous here
-        qc, kc, vc = (t if t.stride(1) == D else t.contiguous() for t in (q, k, v))
-        call = _CoreCall(qc, kc, vc, offsets, (T, H, W), nh, ksz, offset_scale, algo, dropout,
-                         ek if ctx.has_extra else None, ev if ctx.has_extra else None, dkv_accum)
-        desc = call.desc(D, D, D)
-        dq = torch.empty((B, N, D), dtype=dt, device=dev)
-        dk = torch.empty((B, N, D), dtype=dt, device=dev)
-        dv = torch.empty((B, N, D), dtype=dt, device=dev)
-        doff = torch.empty_like(offsets)
-        dek = torch.empty_like(call.ek) if ctx.has_extra else None
-        dev_ = torch.empty_like(call.ev) if ctx.has_extra else None
-        lib = _lib.load()
-        ws_bytes = lib.msd_dsa3d_bwd_workspace_size(ctypes.byref(desc))
-        ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
-        with torch.cuda.device(dev):
-            _lib.check(lib.msd_dsa3d_bwd(
-                ctypes.byref(desc), qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), offsets.data_ptr(),
-                _lib.ptr(call.ek), _lib.ptr(call.ev), out.data_ptr(), dout.data_ptr(),
-                lse.data_ptr(), _lib.ptr(dlse), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
-                doff.data_ptr(), _lib.ptr(dek), _lib.ptr(dev_), ws.data_ptr(), ws_bytes,
-                _lib.stream_handle(dev)), "dsa3d_bwd")
-        return dq, dk, dv, doff, dek, dev_, None, None, None, None, None, None, None
+
+def _call(q, k, v, offsets, extra_k, extra_v, video_shape, num_heads, kernel_size,
+          offset_scale, algo, dropout_p, dropout_seed, dropout_offset, dkv_accum) -> _CoreCall:
+    return _CoreCall(q, k, v, offsets, video_shape, num_heads, kernel_size, offset_scale, algo,
+                     (dropout_p, dropout_seed & 0xFFFFFFFFFFFFFFFF, dropout_offset), extra_k,
+                     extra_v, dkv_accum)
+
+
+@torch.library.custom_op("megaslide::dsa3d_core", mutates_args=(), device_types="cuda")
+def _core_fwd_op(q: Tensor, k: Tensor, v: Tensor, offsets: Tensor, extra_k: Optional[Tensor],
+                 extra_v: Optional[Tensor], video_shape: List[int], num_heads: int,
+                 kernel_size: List[int], offset_scale: float, algo: str, dropout_p: float,
+                 dropout_seed: int, dropout_offset: int,
+                 dkv_accum: str) -> Tuple[Tensor, Tensor]:
+    """out [B, N, D] and lse [B, N, num_heads] (fp32) of the attention core."""
+    call = _call(q, k, v, offsets, extra_k, extra_v, video_shape, num_heads, kernel_size,
+                 offset_scale, algo, dropout_p, dropout_seed, dropout_offset, dkv_accum)
+    return call.forward(want_lse=True)
+
+
+@_core_fwd_op.register_fake
+def _(q, k, v, offsets, extra_k, extra_v, video_shape, num_heads, kernel_size, offset_scale, algo,
+      dropout_p, dropout_seed, dropout_offset, dkv_accum):
+    B, N, D = q.shape
+    return q.new_empty((B, N, D)), q.new_empty((B, N, num_heads), dtype=torch.float32)
+
+
+@torch.library.custom_op("megaslide::dsa3d_core_bwd", mutates_args=(), device_types="cuda")
+def _core_bwd_op(q: Tensor, k: Tensor, v: Tensor, offsets: Tensor, extra_k: Optional[Tensor],
+                 extra_v: Optional[Tensor], out: Tensor, lse: Tensor, dout: Tensor,
+                 dlse: Optional[Tensor], video_shape: List[int], num_heads: int,
+                 kernel_size: List[int], offset_scale: float, algo: str, dropout_p: float,
+                 dropout_seed: int, dropout_offset: int,
+                 dkv_accum: str) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """dq, dk, dv, d offsets and (empty without extra keys) d extra_k, d extra_v."""
+    B, N, D = q.shape
+    dt, dev = q.dtype, q.device
+    dout = dout.to(dt).contiguous()
+    if dlse is not None:
+        dlse = dlse.to(torch.float32).contiguous()
+    # gradients are written with the token strides of the desc: contiguous here
+    qc, kc, vc = (t if t.stride(1) == D else t.contiguous() for t in (q, k, v))
+    call = _call(qc, kc, vc, offsets, extra_k, extra_v, video_shape, num_heads, kernel_size,
+                 offset_scale, algo, dropout_p, dropout_seed, dropout_offset, dkv_accum)
+    desc = call.desc(D, D, D)
+    dq = torch.empty((B, N, D), dtype=dt, device=dev)
+    dk = torch.empty((B, N, D), dtype=dt, device=dev)
+    dv = torch.empty((B, N, D), dtype=dt, device=dev)
+    doff = torch.empty_like(call.off)
+    has_extra = call.G > 0
+    dek = torch.empty_like(call.ek) if has_extra else q.new_empty((0,))
+    dev_ = torch.empty_like(call.ev) if has_extra else q.new_empty((0,))
+    lib = _lib.load()
+    ws_bytes = lib.msd_dsa3d_bwd_workspace_size(ctypes.byref(desc))
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        _lib.check(lib.msd_dsa3d_bwd(
+            ctypes.byref(desc), qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), call.off.data_ptr(),
+            _lib.ptr(call.ek), _lib.ptr(call.ev), out.contiguous().data_ptr(), dout.data_ptr(),
+            lse.contiguous().data_ptr(), _lib.ptr(dlse), dq.data_ptr(), dk.data_ptr(),
+            dv.data_ptr(), doff.data_ptr(), _lib.ptr(dek if has_extra else None),
+            _lib.ptr(dev_ if has_extra else None), ws.data_ptr(), ws_bytes,
+            _lib.stream_handle(dev)), "dsa3d_bwd")
+    return dq, dk, dv, doff, dek, dev_
+
+
+@_core_bwd_op.register_fake
+def _(q, k, v, offsets, extra_k, extra_v, out, lse, dout, dlse, video_shape, num_heads,
+      kernel_size, offset_scale, algo, dropout_p, dropout_seed, dropout_offset, dkv_accum):
+    e = q.new_empty((0,))
+    return (torch.empty_like(q), torch.empty_like(k), torch.empty_like(v),
+            torch.empty_like(offsets), torch.empty_like(extra_k) if extra_k is not None else e,
+            torch.empty_like(extra_v) if extra_v is not None else e)
+
+
+_NON_TENSOR = ("video_shape", "num_heads", "kernel_size", "offset_scale", "algo", "dropout_p",
+               "dropout_seed", "dropout_offset", "dkv_accum")
+
+
+def _core_setup(ctx, inputs, output):
+    q, k, v, offsets, extra_k, extra_v = inputs[:6]
+    ctx.args = inputs[6:]
+    ctx.has_extra = extra_k is not None
+    out, lse = output
+    ctx.save_for_backward(q, k, v, offsets, extra_k, extra_v, out, lse)
+
+
+def _core_backward(ctx, dout, dlse):
+    q, k, v, offsets, extra_k, extra_v, out, lse = ctx.saved_tensors
+    if dout is None:
+        dout = torch.zeros_like(out)
+    dq, dk, dv, doff, dek, dev_ = _core_bwd_op(q, k, v, offsets, extra_k, extra_v, out, lse, dout,
+                                               dlse, *ctx.args)
+    if not ctx.has_extra:
+        dek = dev_ = None
+    return (dq, dk, dv, doff, dek, dev_) + (None,) * len(_NON_TENSOR)
+
+
+_core_fwd_op.register_autograd(_core_backward, setup_context=_core_setup)
+
+
+def keep_core_policy(ctx, op, *args, **kwargs):
+    """Selective-checkpoint policy (torch.utils.checkpoint with
+    create_selective_checkpoint_contexts): keep the attention core's outputs
+    (out, lse: D + 4 nh / e bytes a token) from the forward, recompute the
+    rest.  The backward's recomputed forward then skips the core, the costliest
+    kernel of the recompute, while the projections, convolutions and norms are
+    rerun as usual."""
+    from torch.utils.checkpoint import CheckpointPolicy
+    if op is torch.ops.megaslide.dsa3d_core.default:
+        return CheckpointPolicy.MUST_SAVE
+    return CheckpointPolicy.PREFER_RECOMPUTE
+
+
+def keep_core_context():
+    """context_fn for torch.utils.checkpoint.checkpoint(..., use_reentrant=False)
+    that applies keep_core_policy."""
+    from torch.utils.checkpoint import create_selective_checkpoint_contexts
+    return create_selective_checkpoint_contexts(keep_core_policy)
 
 
 def dsa3d_core(q: Tensor, k: Tensor, v: Tensor, offsets: Tensor, video_shape: Sequence[int],
@@ -215,9 +297,10 @@ def dsa3d_core(q: Tensor, k: Tensor, v: Tensor, offsets: Tensor, video_shape: Se
     dropout = (p, 0 if dropout_seed is None else int(dropout_seed), int(dropout_offset))
     grads = [t for t in (q, k, v, offsets, extra_k, extra_v) if t is not None]
     if torch.is_grad_enabled() and any(t.requires_grad for t in grads):
-        out, lse = DSA3DCoreFunction.apply(q, k, v, offsets, extra_k, extra_v, tuple(video_shape),
-                                           int(num_heads), tuple(kernel_size), float(offset_scale),
-                                           algo, dropout, dkv_accum)
+        out, lse = torch.ops.megaslide.dsa3d_core(
+            q, k, v, offsets, extra_k, extra_v, [int(s) for s in video_shape], int(num_heads),
+            [int(s) for s in kernel_size], float(offset_scale), algo, dropout[0],
+            _seed_in(dropout[1]), dropout[2], dkv_accum)
         return (out, lse) if return_lse else out
     # forward only: nothing saved, no lse unless asked for
     call = _CoreCall(q, k, v, offsets, video_shape, num_heads, kernel_size, offset_scale, algo,

@@ -265,3 +265,26 @@ def dsa3d_module_ref(x: Tensor, params: Dict[str, Tensor], video_shape: Sequence
     a = dsa3d_core_ref(q, k, v, off, video_shape, num_heads, kernel_size, offset_scale,
                        head_chunk=head_chunk, extra_k=ek, extra_v=ev)
     return F.linear(a, params["out_proj.weight"], params["out_proj.bias"]) + dw
+
+
+# ---------------------------------------------------------------------------
+# DiT block around the module (the path's caller)
+# ---------------------------------------------------------------------------
+
+def dit_block_ref(x: Tensor, params: Dict[str, Tensor], video_shape: Sequence[int],
+                  num_heads: int, kernel_size: Sequence[int] = (3, 7, 7),
+                  offset_scale: float = 1.0, head_chunk: Optional[int] = None) -> Tensor:
+    """DiTBlock.forward without text conditioning (infinity/video/model.py:83-117,
+    dropout p = 0): ``x + attn(norm1(x))`` (:102), then ``x + mlp(norm2(x))``
+    (:115) with the MLP fc1 -> exact-erf GELU -> fc2 (model.py:21-35) and both
+    LayerNorms at eps 1e-6 (:51, :63).  ``params`` uses the block's own
+    parameter names (``norm1.*``, ``attn.*``, ``norm2.*``, ``mlp.fc1.*``,
+    ``mlp.fc2.*``)."""
+    D = x.shape[-1]
+    attn_p = {n[len("attn."):]: t for n, t in params.items() if n.startswith("attn.")}
+    a = F.layer_norm(x, (D,), params["norm1.weight"], params["norm1.bias"], eps=1e-6)
+    x = x + dsa3d_module_ref(a, attn_p, video_shape, num_heads, kernel_size, offset_scale,
+                             head_chunk=head_chunk)
+    h = F.layer_norm(x, (D,), params["norm2.weight"], params["norm2.bias"], eps=1e-6)
+    h = F.gelu(F.linear(h, params["mlp.fc1.weight"], params["mlp.fc1.bias"]))
+    return x + F.linear(h, params["mlp.fc2.weight"], params["mlp.fc2.bias"])

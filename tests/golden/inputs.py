@@ -136,3 +136,40 @@ def case_params(case):
     return p, x, gy, off, extra
 
 
+
+
+# A tiny DiT block (infinity/video/model.py:40-117 with MegaSlideConfig): D=32,
+# 2 heads, window 3x5x5, MLP ratio 4, on a 3x4x5 grid, B=2.  Parameters in the
+# block's named_parameters() order; the offset net's last conv is non-zero
+# (inside MegaSlideDiT every Conv3d is re-initialised, model.py:164-178).  The
+# seed keeps every sampling coordinate at least 1.7e-5 voxel from a lattice line
+# (where the trilinear gradient jumps), so an fp32 evaluation takes the same
+# corners as the reference's float64 one.
+BLOCK = dict(name="dit_block", B=2, T=3, H=4, W=5, D=32, nh=2, kernel=(3, 5, 5), scale=1.0,
+             mlp_ratio=4.0, seed=40, on_std=0.3)
+
+
+def block_params(case) -> Dict[str, np.ndarray]:
+    g = rng(case["seed"])
+    D = case["D"]
+    M = int(D * case["mlp_ratio"])
+    p = {"norm1.weight": 1.0 + g.normal(0.0, 0.1, size=(D,)),
+         "norm1.bias": g.normal(0.0, 0.1, size=(D,))}
+    for n, v in module_params(g, D, case["nh"], case["kernel"], on_std=case["on_std"]).items():
+        p["attn." + n] = v
+    p["norm2.weight"] = 1.0 + g.normal(0.0, 0.1, size=(D,))
+    p["norm2.bias"] = g.normal(0.0, 0.1, size=(D,))
+    p["mlp.fc1.weight"] = xavier(g, (M, D), D, M)
+    p["mlp.fc1.bias"] = g.normal(0.0, 0.1, size=(M,))
+    p["mlp.fc2.weight"] = xavier(g, (D, M), M, D)
+    p["mlp.fc2.bias"] = g.normal(0.0, 0.1, size=(D,))
+    return p
+
+
+def block_inputs(case):
+    """Parameters, x and upstream grad of the block case."""
+    p = block_params(case)
+    g = rng(case["seed"] + 1000)
+    x = g.normal(0.0, 1.0, size=(case["B"], case["T"] * case["H"] * case["W"], case["D"]))
+    gy = g.normal(0.0, 1.0, size=x.shape)
+    return p, x, gy

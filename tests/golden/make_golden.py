@@ -26,6 +26,11 @@ the border clamp.
 
 Inputs are regenerated from their seeds by the tests; the fixture stores their
 sums as a check that regeneration matches.
+
+The ``dit_block`` case runs the reference DiT block around the operator
+(infinity/video/model.py:40-117, built from a MegaSlideConfig): model.py,
+attention.py and config.py are loaded by path as submodules of a stand-in
+package, and y, dx and every parameter gradient are recorded in float64.
 """
 
 from __future__ import annotations
@@ -53,6 +58,60 @@ def load_reference(ref_root: str):
     with open(path, "rb") as f:
         digest = hashlib.sha256(f.read()).hexdigest()
     return mod.DeformableSlideAttention3D, digest
+
+
+def load_reference_block(ref_root: str):
+    """DiTBlock and MegaSlideConfig from infinity/video/model.py and config.py.
+
+    model.py imports its siblings relatively (``from .attention import``,
+    ``from .config import``), so the three files are loaded as submodules of a
+    stand-in package whose search path is the infinity/video directory: the
+    real package ``__init__`` files (and their LLM and data imports) never run.
+    """
+    import types
+    vdir = os.path.join(ref_root, "infinity", "video")
+    pkg = types.ModuleType("_ref_video")
+    pkg.__path__ = [vdir]
+    sys.modules["_ref_video"] = pkg
+    mods = {}
+    for name in ("config", "attention", "model"):
+        path = os.path.join(vdir, name + ".py")
+        spec = importlib.util.spec_from_file_location(f"_ref_video.{name}", path)
+        mod = importlib.util.module_from_spec(spec)
+        sys.modules[spec.name] = mod
+        spec.loader.exec_module(mod)
+        mods[name] = mod
+    h = hashlib.sha256()
+    for name in ("config", "attention", "model"):
+        with open(os.path.join(vdir, name + ".py"), "rb") as f:
+            h.update(f.read())
+    return mods["model"].DiTBlock, mods["config"].MegaSlideConfig, h.hexdigest()
+
+
+def run_block(Block, Config, case, dtype):
+    """The reference DiTBlock on the seeded block case: y, dx and every
+    parameter gradient for an upstream grad g."""
+    p, x_np, gy_np = gin.block_inputs(case)
+    B, T, H, W, D, nh = (case[k] for k in ("B", "T", "H", "W", "D", "nh"))
+    cfg = Config(frames=T, height=16 * H, width=16 * W, patch_size=16, hidden_size=D,
+                 num_layers=1, num_heads=nh, mlp_ratio=case["mlp_ratio"],
+                 dsa_kernel_size=tuple(case["kernel"]), offset_scale=case["scale"], dropout=0.0)
+    blk = Block(cfg).to(dtype)
+    names = [n for n, _ in blk.named_parameters()]
+    assert names == list(p), (names, list(p))
+    with torch.no_grad():
+        for n, prm in blk.named_parameters():
+            prm.copy_(torch.from_numpy(p[n]).to(dtype))
+    x = torch.from_numpy(x_np).to(dtype).requires_grad_(True)
+    y = blk(x, (T, H, W))
+    (y * torch.from_numpy(gy_np).to(dtype)).sum().backward()
+    out = {"y": y.detach(), "dx": x.grad}
+    for n, prm in blk.named_parameters():
+        out["grad." + n] = prm.grad if prm.grad is not None else torch.zeros_like(prm)
+    meta = dict(case, dtype=str(dtype).replace("torch.", ""), param_names=names,
+                x_sum=float(x_np.sum()), gy_sum=float(gy_np.sum()),
+                param_sums={k: float(v.sum()) for k, v in p.items()})
+    return meta, {k: v.detach().contiguous().numpy() for k, v in out.items()}
 
 
 class _Inject(torch.nn.Module):
@@ -144,15 +203,23 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--ref", default="/root/reference")
     ap.add_argument("--out", default=HERE)
+    ap.add_argument("--only", default=None, help="write just this case (e.g. dit_block)")
     args = ap.parse_args()
     torch.set_num_threads(min(8, os.cpu_count() or 1))
+    if args.only == gin.BLOCK["name"]:
+        write_block(args)
+        return
     Ref, digest = load_reference(args.ref)
     for case in CASES:
+        if args.only is not None and case["name"] != args.only:
+            continue
         meta, arrs = run_case(Ref, case, torch.float64)
         meta["reference_sha256"] = digest
         np.savez_compressed(os.path.join(args.out, f"{case['name']}.npz"),
                             meta=np.array(json.dumps(meta)), **arrs)
         print("wrote", case["name"], {k: v.shape for k, v in arrs.items() if k in ("y", "offsets")})
+    if args.only is not None and args.only != C1["name"]:
+        return
     meta, arrs = run_case(Ref, C1, torch.float32)
     g = gin.rng(1000)
     rows = np.sort(g.choice(arrs["y"].shape[1], size=C1["rows"], replace=False))
@@ -164,6 +231,16 @@ def main():
     np.savez_compressed(os.path.join(args.out, "c1_fwd_fp32.npz"), meta=np.array(json.dumps(meta)),
                         **keep)
     print("wrote c1_fwd_fp32")
+    write_block(args)
+
+
+def write_block(args):
+    Block, Config, bdigest = load_reference_block(args.ref)
+    meta, arrs = run_block(Block, Config, gin.BLOCK, torch.float64)
+    meta["reference_sha256"] = bdigest
+    np.savez_compressed(os.path.join(args.out, f"{gin.BLOCK['name']}.npz"),
+                        meta=np.array(json.dumps(meta)), **arrs)
+    print("wrote", gin.BLOCK["name"], arrs["y"].shape)
 
 
 if __name__ == "__main__":

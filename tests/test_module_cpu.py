@@ -48,3 +48,41 @@ def test_reference_state_dict_loads(name):
     missing, unexpected = m.load_state_dict(sd, strict=True)
     assert not missing and not unexpected
     assert list(m.state_dict().keys()) == meta["param_names"]
+
+
+class _Config:
+    """The MegaSlideConfig fields a DiTBlock reads (infinity/video/config.py)."""
+
+    def __init__(self, hidden_size, num_heads, dsa_kernel_size=(3, 7, 7), offset_scale=1.0,
+                 dropout=0.0, mlp_ratio=4.0, use_text_conditioning=False):
+        self.hidden_size, self.num_heads = hidden_size, num_heads
+        self.dsa_kernel_size, self.offset_scale, self.dropout = dsa_kernel_size, offset_scale, dropout
+        self.mlp_ratio, self.use_text_conditioning = mlp_ratio, use_text_conditioning
+
+    @property
+    def mlp_hidden_size(self):
+        return int(self.hidden_size * self.mlp_ratio)
+
+
+def test_dit_block_parameters_match_reference_block():
+    """The drop-in DiTBlock registers the reference block's parameters in its
+    order (the golden fixture records the reference's named_parameters()), with
+    the same shapes, and loads the reference's values strictly."""
+    from inputs import BLOCK, block_params
+    from megaslide_amd import DiTBlock
+
+    meta, arrs = load(BLOCK["name"])
+    cfg = _Config(BLOCK["D"], BLOCK["nh"], BLOCK["kernel"], BLOCK["scale"],
+                  mlp_ratio=BLOCK["mlp_ratio"])
+    blk = DiTBlock(cfg)
+    assert [n for n, _ in blk.named_parameters()] == meta["param_names"]
+    p = block_params(BLOCK)
+    sd = {n: torch.from_numpy(v).float() for n, v in p.items()}
+    blk.load_state_dict(sd, strict=True)
+    for n, prm in blk.named_parameters():
+        assert prm.shape == tuple(arrs["grad." + n].shape), n
+    # text conditioning adds the reference's norm_cross and cross_attn, in order
+    names = [n for n, _ in DiTBlock(_Config(32, 2, use_text_conditioning=True)).named_parameters()]
+    assert names[-6:] == ["norm_cross.weight", "norm_cross.bias", "cross_attn.in_proj_weight",
+                          "cross_attn.in_proj_bias", "cross_attn.out_proj.weight",
+                          "cross_attn.out_proj.bias"]

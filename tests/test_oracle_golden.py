@@ -104,3 +104,28 @@ def test_c1_forward_fp32_matches_reference():
     rows = arrs["rows"]
     assert rel_err(y[:, rows], arrs["y_rows"]) < 1e-5
     assert abs(float(y.double().norm()) / float(arrs["y_norm"]) - 1.0) < 1e-5
+
+
+def test_block_restatement_matches_reference_dit_block():
+    """oracle.dit_block_ref (model.py:83-117 around the module restatement)
+    against the reference DiTBlock's own y, dx and parameter gradients."""
+    from inputs import BLOCK, block_inputs
+    from oracle.dsa3d_ref import dit_block_ref
+
+    meta, arrs = load(BLOCK["name"])
+    p, x_np, gy_np = block_inputs(BLOCK)
+    assert abs(float(x_np.sum()) - meta["x_sum"]) < 1e-9
+    assert list(p) == meta["param_names"]
+    for k, v in p.items():
+        assert abs(float(v.sum()) - meta["param_sums"][k]) < 1e-9, k
+    params = {n: torch.from_numpy(v).requires_grad_(True) for n, v in p.items()}
+    x = torch.from_numpy(x_np).requires_grad_(True)
+    T, H, W = BLOCK["T"], BLOCK["H"], BLOCK["W"]
+    y = dit_block_ref(x, params, (T, H, W), BLOCK["nh"], BLOCK["kernel"], BLOCK["scale"])
+    (y * torch.from_numpy(gy_np)).sum().backward()
+    assert rel_err(y.detach(), arrs["y"]) < 1e-10
+    assert rel_err(x.grad, arrs["dx"]) < 1e-10
+    for n, prm in params.items():
+        assert rel_err(prm.grad, arrs["grad." + n], floor=1e-12) < 1e-10, n
+    # the block is not the bare module: the residuals and the MLP carry weight
+    assert rel_err(arrs["y"], x_np) > 0.1
