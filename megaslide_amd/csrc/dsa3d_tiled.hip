@@ -441,12 +441,16 @@ constexpr int p1_min_waves() {
 }
 
 // AE: bytes of one dK / dV accumulator element (4 = fp32 rows, 2 = scaled fp16).
-template <int HD, typename E, int AE>
+// REC: also write the tap records, tile header and transposed q / dO of the
+// column-streaming kernel (bf16 storage).
+template <int HD, typename E, int AE, bool REC = false>
 __global__ __launch_bounds__(kThreads, (p1_min_waves<HD, E>())) void dsa3d_bwd_p1_kernel(
     Args a, const E* __restrict__ out, const E* __restrict__ dout,
     const float* __restrict__ lse, const float* __restrict__ dlse, E* __restrict__ doff,
     float* __restrict__ p_ws, float* __restrict__ b_ws, void* __restrict__ dk_acc,
-    void* __restrict__ dv_acc, int64_t acc_ks, int64_t acc_vs) {
+    void* __restrict__ dv_acc, int64_t acc_ks, int64_t acc_vs, RecArgs rc) {
+  static_assert(!REC || (sizeof(E) == 2 && p1_min_waves<HD, E>() == 4),
+                "records come from the bf16 kernel that stages q and dO in LDS");
   // S and dP tables, double-buffered (one barrier per plane).  A buffer is
   // [S rows | zeros | dP rows | zeros]: a slot that misses the step reads the
   // zero block instead of its corners, so its values are 0 with no select, and
@@ -708,7 +712,7 @@ __global__ __launch_bounds__(kThreads, (p1_min_waves<HD, E>())) void dsa3d_bwd_p
   // bf16 storage keeps one word per tap: fp16 p * factor and ds * scale / l1,
   // with l1 = sum over the query's taps of |ds * scale| kept per token and head
   // (the normalised values lie in [-1, 1], where fp16 keeps 11 bits)
-  float rl1 = 1.0f;
+  float rl1 = 1.0f, l1q = 0.0f;
   if constexpr (sizeof(E) == 2) {
     float l1 = 0.0f;
 #pragma unroll
@@ -716,24 +720,123 @@ __global__ __launch_bounds__(kThreads, (p1_min_waves<HD, E>())) void dsa3d_bwd_p
 #pragma unroll
     for (int m = 1; m < kSubs; m <<= 1) l1 += __shfl_xor(l1, m);
     rl1 = l1 > 1e-30f ? 1.0f / l1 : 0.0f;
+    l1q = l1;
     if (sub == 0 && qn >= 0) b_ws[qn * a.nh + tl.head] = l1;
   }
+  // Records for the column-streaming kernel (REC), counting-sorted by z0: the
+  // bins' counts by LDS atomics (their return values place each record in its
+  // bin), then one thread's prefix sum.  Within a bin the order is the
+  // atomics' order, which no result depends on (the consumer sums integers).
+  int pos[kSlots];
+  int* const s_bin = reinterpret_cast<int*>(&s_tb[0][0]);  // [counts | starts], tables are free
+  const bool rec_wide = REC && !(box.zhi < box.zlo) && box.zhi - box.zlo + 1 > kRecBins;
+  if constexpr (REC) {
+    const int64_t trec = static_cast<int64_t>(tl.head) * rc.tiles +
+                         rec_tile(a, tl.b, tl.t0, tl.h0 / kTileH, tl.w0 / kTileW);
+    if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) rc.collist[0] = 0;
+    const int nb = box.zhi < box.zlo ? 0 : box.zhi - box.zlo + 1;
+    __syncthreads();  // every table read of the plane loop and s_dl read above is done
+    if (threadIdx.x < kRecBins) s_bin[threadIdx.x] = 0;
+    if (sub == 0) s_dl[tid / kSubs][0] = l1q;  // this query's l1
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kSlots; ++i) {
+      pos[i] = 0;
+      if (!rec_wide && slot_z0(sl[i]) >= 0)
+        pos[i] = atomicAdd(&s_bin[slot_z0(sl[i]) - box.zlo], 1);
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      int* const hdr = rc.hdr + trec * kRecHdr;
+      int acc = 0;
+      for (int bb = 0; bb < kRecBins; ++bb) {
+        const int cnt = s_bin[bb];
+        s_bin[kRecBins + bb] = acc;
+        hdr[8 + bb] = acc;
+        acc += cnt;
+      }
+      hdr[8 + kRecBins] = acc;
+      hdr[0] = box.zlo;
+      hdr[1] = box.zhi;
+      hdr[2] = box.ylo;
+      hdr[3] = box.yhi;
+      hdr[4] = box.xlo;
+      hdr[5] = box.xhi;
+      hdr[6] = rec_wide ? -1 : nb;
+    }
+    __syncthreads();
+  }
+  // a record's corner (y0, x0) from the tap's table index in its chunk of
+  // the box; one chunk column (the usual case): the box's x origin and width
+  const bool one_cx = box.ncx == 1;
+  const int nx1 = min(kChunk, box.xhi - box.xlo + 1);
+  const float rnx1 = __builtin_amdgcn_rcpf(static_cast<float>(nx1));
+  u32x4_t* const rec = REC ? rc.rec + (static_cast<int64_t>(tl.head) * rc.tiles +
+                                       rec_tile(a, tl.b, tl.t0, tl.h0 / kTileH, tl.w0 / kTileW)) *
+                                          (static_cast<int64_t>(a.K) * kTQ)
+                           : nullptr;
 #pragma unroll
   for (int i = 0; i < kSlots; ++i) {
     if (slot_z0(sl[i]) < 0) continue;
     const float pd = s_[i], dss = dp_[i];
     const int kap = sub + kSubs * i;
+    uint32_t pair = 0;
     if constexpr (sizeof(E) == 4) {
       p_ws[tap0 + kap] = pd;
       b_ws[tap0 + kap] = dss;
     } else {
-      reinterpret_cast<uint32_t*>(p_ws)[tap0 + kap] = pack_h2(pd, dss * rl1);
+      pair = pack_h2(pd, dss * rl1);
+      reinterpret_cast<uint32_t*>(p_ws)[tap0 + kap] = pair;
     }
     E* dp = doff + qn * a.C + (static_cast<int64_t>(tl.head) * a.K + kap) * 3;
     const int m = sl[i].zc >> 17;
     dp[0] = from_f32<E>((m & 1) ? (dss * gxs[i] + pd * gxd[i]) * cxs : 0.0f);
     dp[1] = from_f32<E>((m & 2) ? (dss * gys[i] + pd * gyd[i]) * cys : 0.0f);
     dp[2] = from_f32<E>((m & 4) ? (dss * gzs[i] + pd * gzd[i]) * czs : 0.0f);
+    if constexpr (REC) {
+      if (rec_wide) continue;
+      const int idx = sl[i].idx;
+      const int base = idx & 0x1ff, ch = static_cast<int>(static_cast<uint32_t>(idx) >> 16);
+      int cy = ch, cx0 = box.xlo, nx = nx1;
+      float rnx = rnx1;
+      if (!one_cx) {
+        cy = ch / box.ncx;
+        cx0 = box.xlo + kChunkStep * (ch - cy * box.ncx);
+        nx = min(kChunk, box.xhi - cx0 + 1);
+        rnx = __builtin_amdgcn_rcpf(static_cast<float>(nx));
+      }
+      const int vy = static_cast<int>((static_cast<float>(base) + 0.5f) * rnx);
+      const int y0 = box.ylo + kChunkStep * cy + vy, x0 = cx0 + base - vy * nx;
+      const uint32_t ux = min(65535u, static_cast<uint32_t>(sl[i].fx * 65536.0f + 0.5f));
+      const uint32_t uy = min(65535u, static_cast<uint32_t>(sl[i].fy * 65536.0f + 0.5f));
+      u32x4_t r;
+      r[0] = static_cast<uint32_t>(y0) | (static_cast<uint32_t>(x0) << 14) |
+             (static_cast<uint32_t>(tid / kSubs) << 28);
+      r[1] = ux | (uy << 16);
+      r[2] = __float_as_uint(sl[i].fz);
+      r[3] = pair;
+      rec[s_bin[kRecBins + slot_z0(sl[i]) - box.zlo] + pos[i]] = r;
+    }
+  }
+  if constexpr (REC) {
+    const int64_t trec = static_cast<int64_t>(tl.head) * rc.tiles +
+                         rec_tile(a, tl.b, tl.t0, tl.h0 / kTileH, tl.w0 / kTileW);
+    // q and dO of the tile transposed, with the fixed-point scales of the B
+    // (l1 / 2^30, per query) and A (1 / fix_a) tables: item e = (tensor,
+    // channel, query half) writes 8 queries (16 bytes)
+    E* const qt = static_cast<E*>(rc.qt) + trec * (2 * HD * kTQ);
+    for (int e = threadIdx.x; e < 2 * HD * 2; e += kThreads) {
+      const int t = e / (2 * HD), chn = (e / 2) % HD, h8 = 8 * (e & 1);
+      uint16_t v8[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int m = h8 + j;
+        const float sc = t == 0 ? s_dl[m][0] * kFixAInv : a.fix_a_inv;
+        const uint16_t raw = s_x[(t * kTQ + m) * XR + chn];
+        v8[j] = from_f32<E>(__uint_as_float(static_cast<uint32_t>(raw) << 16) * sc).bits;
+      }
+      __builtin_memcpy(&qt[(t * HD + chn) * kTQ + h8], v8, sizeof(v8));
+    }
   }
 }
 
@@ -1163,6 +1266,31 @@ __global__ __launch_bounds__(P2Tile<FR>::Threads) void dsa3d_bwd_p2_kernel(
                                cw_base, scales, dqx);
 }
 
+// The tiles of the columns the column-streaming kernel left (its list: count,
+// then head * columns + column), fp32 accumulation: a small grid strides over
+// them (most calls have none).
+template <int HD, int CW, typename E, int FR>
+__global__ __launch_bounds__(P2Tile<FR>::Threads) void dsa3d_bwd_p2_list_kernel(
+    Args a, const E* __restrict__ dout, const float* __restrict__ p_ws,
+    const float* __restrict__ b_ws, E* __restrict__ dq, void* __restrict__ dk_acc,
+    void* __restrict__ dv_acc, int64_t acc_ks, int64_t acc_vs, const int* __restrict__ list) {
+  const int n = list[0];
+  const int groups = (a.T + FR - 1) / FR;
+  const int ncol = a.B * a.tiles_h * a.tiles_w;
+#pragma nounroll
+  for (int item = blockIdx.x; item < n * groups; item += gridDim.x) {
+    int it = item;
+    asm volatile("" : "+s"(it));  // nothing of one tile is computed ahead for the next
+    const int e = list[1 + it / groups], g = it % groups;
+    Args b = a;
+    b.head0 = e / ncol;  // blockIdx.y is 0
+    b.xcd_remap = 0;
+    p2_tile<HD, CW, E, FR, kP2F32>(b, (e % ncol) * groups + g, dout, p_ws, b_ws, dq, dk_acc,
+                                   dv_acc, acc_ks, acc_vs, 0, nullptr, nullptr);
+    __syncthreads();  // the next tile rewrites the LDS tables
+  }
+}
+
 // dK / dV again with fp32 atomics, only when the fp16 accumulation overflowed
 // (*flag != 0; otherwise every workgroup returns at once): a small grid strides
 // over the tiles.
@@ -1179,6 +1307,334 @@ __global__ __launch_bounds__(P2Tile<FR>::Threads) void dsa3d_bwd_p2_redo_kernel(
     p2_tile<HD, CW, E, FR, kP2Redo>(a, t, dout, p_ws, b_ws, nullptr, dk_acc, dv_acc, acc_ks,
                                     acc_vs, cw_base, nullptr, nullptr);
     __syncthreads();  // the next tile rewrites the LDS tables
+  }
+}
+
+// Column-streaming dq/dK/dV kernel (bf16 storage, fp32 dK/dV accumulation).
+// One workgroup walks one 4x4 (h, w) column of one head through every plane
+// of the column's corner box.  At plane z, the frames whose tiles have
+// corners on z are live; each holds the 16 table columns of a ring slot
+// (frame t in slot t % SR), and its taps with a corner on z come from the
+// first kernel's records (bins z0 = z: lower corners, z0 = z - 1: upper).  Per
+// plane and 16x16 chunk of the column's box, the [voxel][ring query] table of
+// B = ds * scale * w gives dq += B K (K^T staged in 32-channel rounds) and
+// dK = B^T q; the table of A = p * w then gives dV = A^T dO.  dK and dV are
+// added with fp32 atomics once per plane and column: tiles of FR frames flush
+// each plane of their box once per tile, and a voxel lies in the boxes of
+// about three consecutive tiles of its column (the window spans ~7 planes),
+// so the atomics, executed past the L2 and the bound of that kernel, drop to
+// about 40% (the frames of a column share every flush).  Columns whose frames
+// need more than SR slots at once, or whose tile headers carry no records,
+// are flagged and left to the tile kernel.
+// Ring and K^T staging: eight slots and 32-channel K^T rounds.  (Nine slots,
+// which would take every column at the long-clip shape, where a few frames'
+// corner planes span nine planes, leave LDS for 16-channel rounds only: the
+// kernel then took 1.2 ms longer than the ~4% of columns it would keep from
+// the tile kernel.)
+template <int HD>
+struct S2 {
+  static constexpr int SR = 8;                   // ring slots (live frames)
+  static constexpr int KC = 32;                  // K^T channels staged per round
+  static constexpr int NR = HD / KC;             // rounds
+  static constexpr int Row = SR * kTQ + 2;       // [voxel][ring query] table row (ints)
+  static constexpr int Ranges = 2 * SR;          // record ranges per plane: (slot, lower / upper)
+};
+constexpr int kS2Waves = 16;
+constexpr int kS2Threads = 64 * kS2Waves;
+constexpr int kS2MaxT = 256;              // frames per column (LDS frame table)
+
+template <int HD, typename E>
+__global__ __launch_bounds__(kS2Threads) void dsa3d_bwd_p2s_kernel(
+    Args a, RecArgs rc, const float* __restrict__ l1_ws, E* __restrict__ dq,
+    float* __restrict__ dk_acc, float* __restrict__ dv_acc, int64_t acc_ks, int64_t acc_vs) {
+  static_assert(sizeof(E) == 2, "the records carry bf16 storage's fp16 (p, ds) pairs");
+  constexpr int KR = ElemT<E>::kRow;
+  constexpr int SR = S2<HD>::SR, KC = S2<HD>::KC, NR = S2<HD>::NR, kS2Row = S2<HD>::Row;
+  constexpr int kS2Ranges = S2<HD>::Ranges;
+  static_assert(kS2Waves == 2 * SR, "two waves hold the dq tiles of each ring slot");
+  __shared__ __attribute__((aligned(16))) int s_tab[kChunkNV * kS2Row];
+  __shared__ __attribute__((aligned(16))) word_t<E> s_kt[KC * KR];
+  __shared__ __attribute__((aligned(16))) int s_rows[kChunkNV];
+  __shared__ int s_fz[kS2MaxT][2];         // per frame: zlo, zhi (zlo > zhi: never live)
+  __shared__ int s_live[SR];               // frame in each slot at this plane, or -1
+  __shared__ int s_rg[kS2Ranges][3];       // record range: first record, count, upper
+  __shared__ int s_pre[kS2Ranges + 1];     // range prefix sums
+  __shared__ int s_red[kS2Waves][8];
+
+  const int ncpb = a.tiles_h * a.tiles_w;  // columns per sample
+  const int ncol = a.B * ncpb;
+  int col = static_cast<int>(blockIdx.x);
+  // columns of one XCD are contiguous (they share K rows in its L2)
+  if (ncol % 8 == 0) col = (col & 7) * (ncol / 8) + (col >> 3);
+  const int b = col / ncpb, th = (col % ncpb) / a.tiles_w, tw = col % a.tiles_w;
+  Tile tl;
+  tl.head = a.head0 + static_cast<int>(blockIdx.y);
+  tl.b = b;
+  tl.sample0 = static_cast<int64_t>(b) * a.N;
+  tl.wave = threadIdx.x >> 6;
+  tl.lane = threadIdx.x & 63;
+  tl.t0 = tl.t = 0;
+  tl.h0 = th * kTileH;
+  tl.w0 = tw * kTileW;
+  const int64_t trec0 = static_cast<int64_t>(tl.head) * rc.tiles + rec_tile(a, b, 0, th, tw);
+  const int64_t tstep = ncpb;  // tiles between consecutive frames of the column
+  const int K16 = a.K * kTQ;
+
+  // ---- the column's frames: plane ranges, corner box, ring check -----------
+  int zlo = 1 << 30, zhi = -1, ylo = 1 << 30, yhi = -1, xlo = 1 << 30, xhi = -1, bad = 0;
+  if (a.T > kS2MaxT) bad = 1;
+  for (int t = threadIdx.x; t < a.T && t < kS2MaxT; t += kS2Threads) {
+    const int* h = rc.hdr + (trec0 + t * tstep) * kRecHdr;
+    const int nb = h[6];
+    if (nb < 0) bad = 1;
+    if (nb > 0) {
+      s_fz[t][0] = h[0];
+      s_fz[t][1] = h[1];
+      zlo = min(zlo, h[0]);
+      zhi = max(zhi, h[1]);
+      ylo = min(ylo, h[2]);
+      yhi = max(yhi, h[3]);
+      xlo = min(xlo, h[4]);
+      xhi = max(xhi, h[5]);
+    } else {
+      s_fz[t][0] = 1;
+      s_fz[t][1] = 0;
+    }
+  }
+  __syncthreads();
+  // the next frame of a slot starts after the previous one ends
+  for (int t = threadIdx.x; t < a.T && t < kS2MaxT; t += kS2Threads) {
+    if (s_fz[t][0] > s_fz[t][1]) continue;
+    for (int u = t + SR; u < a.T && u < kS2MaxT; u += SR) {
+      if (s_fz[u][0] > s_fz[u][1]) continue;
+      if (s_fz[u][0] <= s_fz[t][1]) bad = 1;
+      break;
+    }
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    zlo = min(zlo, __shfl_xor(zlo, m));
+    zhi = max(zhi, __shfl_xor(zhi, m));
+    ylo = min(ylo, __shfl_xor(ylo, m));
+    yhi = max(yhi, __shfl_xor(yhi, m));
+    xlo = min(xlo, __shfl_xor(xlo, m));
+    xhi = max(xhi, __shfl_xor(xhi, m));
+    bad = max(bad, __shfl_xor(bad, m));
+  }
+  if (tl.lane == 0) {
+    s_red[tl.wave][0] = zlo;
+    s_red[tl.wave][1] = zhi;
+    s_red[tl.wave][2] = ylo;
+    s_red[tl.wave][3] = yhi;
+    s_red[tl.wave][4] = xlo;
+    s_red[tl.wave][5] = xhi;
+    s_red[tl.wave][6] = bad;
+  }
+  __syncthreads();
+  Box box;
+  box.zlo = s_red[0][0];
+  box.zhi = s_red[0][1];
+  box.ylo = s_red[0][2];
+  box.yhi = s_red[0][3];
+  box.xlo = s_red[0][4];
+  box.xhi = s_red[0][5];
+  bad = s_red[0][6];
+#pragma unroll
+  for (int w = 1; w < kS2Waves; ++w) {
+    box.zlo = min(box.zlo, s_red[w][0]);
+    box.zhi = max(box.zhi, s_red[w][1]);
+    box.ylo = min(box.ylo, s_red[w][2]);
+    box.yhi = max(box.yhi, s_red[w][3]);
+    box.xlo = min(box.xlo, s_red[w][4]);
+    box.xhi = max(box.xhi, s_red[w][5]);
+    bad = max(bad, s_red[w][6]);
+  }
+  box.zlo = __builtin_amdgcn_readfirstlane(box.zlo);
+  box.zhi = __builtin_amdgcn_readfirstlane(box.zhi);
+  box.ylo = __builtin_amdgcn_readfirstlane(box.ylo);
+  box.yhi = __builtin_amdgcn_readfirstlane(box.yhi);
+  box.xlo = __builtin_amdgcn_readfirstlane(box.xlo);
+  box.xhi = __builtin_amdgcn_readfirstlane(box.xhi);
+  bad = __builtin_amdgcn_readfirstlane(bad);
+  if (bad) {
+    if (threadIdx.x == 0) rc.collist[1 + atomicAdd(&rc.collist[0], 1)] = tl.head * ncol + col;
+    return;
+  }
+  if (box.zhi < box.zlo) return;  // no tap at all
+  box.ncy = max(1, (box.yhi - box.ylo + kChunkStep - 1) / kChunkStep);
+  box.ncx = max(1, (box.xhi - box.xlo + kChunkStep - 1) / kChunkStep);
+  const int nchunks = box.ncy * box.ncx;
+
+  const int D = a.nh * HD;
+  const int hc0 = tl.head * HD;
+  const E* const kp = static_cast<const E*>(a.k);
+  const E* const qtb = static_cast<const E*>(rc.qt);
+  const int mq = tl.lane & 15, kq = 8 * (tl.lane >> 4), oq = 8 * (tl.lane >> 5);
+  // dq tiles of this wave: slot wave / 2, channels 32 rd + 16 (wave % 2) + [0, 16)
+  const int my_slot = tl.wave >> 1, my_ct = tl.wave & 1;
+  f32x4_t dq_acc[NR];
+#pragma unroll
+  for (int rd = 0; rd < NR; ++rd) dq_acc[rd] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  StageRows<kP2Stage, KC, E> kr;
+
+  for (int z = box.zlo; z <= box.zhi; ++z) {
+    // ---- live frames of this plane and their record ranges ----------------
+    __syncthreads();  // the previous plane's dq write-out has read s_live
+    if (threadIdx.x < SR) s_live[threadIdx.x] = -1;
+    __syncthreads();
+    for (int t = threadIdx.x; t < a.T; t += kS2Threads)
+      if (s_fz[t][0] <= z && z <= s_fz[t][1]) s_live[t % SR] = t;
+    __syncthreads();
+    if (threadIdx.x < kS2Ranges) {
+      const int r = threadIdx.x >> 1, up = threadIdx.x & 1;
+      const int t = s_live[r];
+      int first = 0, cnt = 0;
+      if (t >= 0) {
+        const int bin = z - up - s_fz[t][0];
+        const int* h = rc.hdr + (trec0 + t * tstep) * kRecHdr;
+        if (bin >= 0 && bin < h[6]) {
+          first = h[8 + bin];
+          cnt = h[9 + bin] - first;
+        }
+      }
+      s_rg[threadIdx.x][0] = first;
+      s_rg[threadIdx.x][1] = cnt;
+      s_rg[threadIdx.x][2] = up;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      int acc = 0;
+      for (int j = 0; j < kS2Ranges; ++j) {
+        s_pre[j] = acc;
+        acc += s_rg[j][1];
+      }
+      s_pre[kS2Ranges] = acc;
+    }
+    __syncthreads();
+    const int nrec = s_pre[kS2Ranges];
+
+    for (int ci = 0; ci < nchunks; ++ci) {
+      const Chunk c = make_chunk(box, ci);
+      const int cyi = box.ncx == 1 ? 0 : ci / box.ncx, cxi = ci - cyi * box.ncx;
+      for (int vi = threadIdx.x; vi < c.nv; vi += kS2Threads)
+        s_rows[vi] = static_cast<int>(chunk_row(a, tl, c, z, vi) - tl.sample0);
+
+      // one pass of the table: B (ds * scale * w, phase 0) or A (p * w, phase 1)
+      auto scatter = [&](int phase) {
+        for (int e = threadIdx.x; e < c.nvp * kS2Row / 4; e += kS2Threads) {
+          const u32x4_t zz = {0u, 0u, 0u, 0u};
+          __builtin_memcpy(&s_tab[4 * e], &zz, sizeof(zz));
+        }
+        __syncthreads();
+        for (int i = threadIdx.x; i < nrec; i += kS2Threads) {
+          int j = 0;
+#pragma unroll
+          for (int k = 1; k < kS2Ranges; ++k) j += i >= s_pre[k] ? 1 : 0;
+          const int slot = j >> 1, t = s_live[slot];
+          const int64_t ridx = (trec0 + t * tstep) * K16 + s_rg[j][0] + (i - s_pre[j]);
+          const u32x4_t r = rc.rec[ridx];
+          const int y0 = static_cast<int>(r[0] & 0x3fffu);
+          const int x0 = static_cast<int>((r[0] >> 14) & 0x3fffu);
+          const int qq = static_cast<int>(r[0] >> 28);
+          const float fz = __uint_as_float(r[2]);
+          const float wz = s_rg[j][2] ? fz : 1.0f - fz;
+          if (nchunks > 1) {
+            const int ky = min((y0 - box.ylo) / kChunkStep, box.ncy - 1);
+            const int kx = min((x0 - box.xlo) / kChunkStep, box.ncx - 1);
+            if (ky != cyi || kx != cxi) continue;
+          }
+          const float fx = static_cast<float>(r[1] & 0xffffu) * (1.0f / 65536.0f);
+          const float fy = static_cast<float>(r[1] >> 16) * (1.0f / 65536.0f);
+          const float v = (phase == 0 ? h2_hi(r[3]) * kFixA : h2_lo(r[3]) * a.fix_a) * wz;
+          const float gx = 1.0f - fx, gy = 1.0f - fy;
+          const int base = (y0 - c.cy0) * c.nx + (x0 - c.cx0);
+          const int dy = fy != 0.0f ? c.nx : 0, dx = fx != 0.0f ? 1 : 0;
+          int* const r00 = &s_tab[base * kS2Row + kTQ * slot + qq];
+          int* const r10 = r00 + dy * kS2Row;
+          atomicAdd(r00, to_fix(v * (gy * gx)));
+          atomicAdd(r00 + dx * kS2Row, to_fix(v * (gy * fx)));
+          atomicAdd(r10, to_fix(v * (fy * gx)));
+          atomicAdd(r10 + dx * kS2Row, to_fix(v * (fy * fx)));
+        }
+      };
+
+      // ---- B: dq and dK -----------------------------------------------------
+      load_stage_rows<kP2Stage, KC, E>(a, tl, c, z, kp, a.ks, hc0, kr);
+      scatter(0);
+      __syncthreads();
+#pragma unroll
+      for (int rd = 0; rd < NR; ++rd) {
+        store_stage<kP2Stage, KC, E>(c, kr, s_kt);
+        __syncthreads();
+        if (rd + 1 < NR)
+          load_stage_rows<kP2Stage, KC, E>(a, tl, c, z, kp, a.ks, hc0 + KC * (rd + 1), kr);
+        if (s_live[my_slot] >= 0) {
+          for (int kc = 0; kc < c.nvp; kc += 32) {
+            float bq[8];  // fixed-point units; the query's l1 / 2^30 is applied to dq at the end
+#pragma unroll
+            for (int jj = 0; jj < 8; ++jj)
+              bq[jj] = static_cast<float>(s_tab[(kc + kq + jj) * kS2Row + kTQ * my_slot + mq]);
+            dq_acc[rd] = mma16(precise_op<E>(bq),
+                               load_op<E>(&s_kt[(16 * my_ct + mq) * KR + kc + kq]), dq_acc[rd]);
+          }
+        }
+        __syncthreads();  // every wave is done with this round's K^T
+      }
+      // dK[v] += sum over ring queries of B[q][v] q[q] (32x32 MFMA per live slot)
+      for (int task = tl.wave;; task += kS2Waves) {
+        const int c2 = task % (HD / 32), vb = task / (HD / 32);
+        if (vb * 32 >= c.nv) break;
+        const int och = 32 * c2 + (tl.lane & 31);
+        f32x16_t acc = {};
+#pragma unroll
+        for (int r = 0; r < SR; ++r) {
+          const int t = s_live[r];
+          if (t < 0) continue;
+          const E* qp = qtb + (trec0 + t * tstep) * (2 * HD * kTQ) + och * kTQ + oq;
+          acc = mma32(table_t_rows<E>(s_tab, kS2Row, kTQ * r, vb, tl.lane), load_op<E>(qp), acc);
+        }
+        flush_block(tl, acc, s_rows, vb, c.nv, hc0 + och, dk_acc, acc_ks);
+      }
+      __syncthreads();  // every wave is done with the B table
+
+      // ---- A: dV --------------------------------------------------------------
+      scatter(1);
+      __syncthreads();
+      for (int task = tl.wave;; task += kS2Waves) {
+        const int c2 = task % (HD / 32), vb = task / (HD / 32);
+        if (vb * 32 >= c.nv) break;
+        const int och = 32 * c2 + (tl.lane & 31);
+        f32x16_t acc = {};
+#pragma unroll
+        for (int r = 0; r < SR; ++r) {
+          const int t = s_live[r];
+          if (t < 0) continue;
+          const E* gp = qtb + (trec0 + t * tstep) * (2 * HD * kTQ) + (HD + och) * kTQ + oq;
+          acc = mma32(table_t_rows<E>(s_tab, kS2Row, kTQ * r, vb, tl.lane), load_op<E>(gp), acc);
+        }
+        flush_block(tl, acc, s_rows, vb, c.nv, hc0 + och, dv_acc, acc_vs);
+      }
+      __syncthreads();  // the table and s_rows are rewritten by the next step
+    }
+
+    // ---- frames that end at this plane: their dq ---------------------------
+    const int tr = s_live[my_slot];
+    if (tr >= 0 && s_fz[tr][1] == z) {
+#pragma unroll
+      for (int rd = 0; rd < NR; ++rd) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int m = 4 * (tl.lane >> 4) + i;
+          const int h = tl.h0 + m / kTileW, w = tl.w0 + m % kTileW;
+          if (h < a.H && w < a.W) {
+            const int64_t n = tl.sample0 + (static_cast<int64_t>(tr) * a.H + h) * a.W + w;
+            const int ch = hc0 + KC * rd + 16 * my_ct + mq;
+            dq[n * a.qs + ch] = from_f32<E>(dq_acc[rd][i] * l1_ws[n * a.nh + tl.head] * kFixAInv);
+          }
+        }
+        dq_acc[rd] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+      }
+    }
   }
 }
 
@@ -1452,6 +1908,7 @@ tiled::Args make_tiled_args(const msd_dsa3d_desc& d, const void* q, const void* 
   a.tiles_h = (d.H + tiled::kTileH - 1) / tiled::kTileH;
   a.tiles_w = (d.W + tiled::kTileW - 1) / tiled::kTileW;
   a.xcd_remap = (tiles % 8 == 0) ? static_cast<int>(tiles / 8) : 0;
+  a.head0 = 0;
   a.offset_scale = d.offset_scale;
   a.softmax_scale = d.softmax_scale;
   a.div_x = d.T > 1 ? static_cast<float>(d.T - 1) : 0.0f;
@@ -1761,6 +2218,7 @@ struct BwdBufs {
   float* dek_acc;  // extra keys: dEK / dEV fp32 [B, G, D] (the outputs for fp32 storage)
   float* dev_acc;
   float* dqx;      // extra keys: their part of dq, fp32 [rows, D] (null without them)
+  RecArgs rec;     // column-streaming kernel's records (rec.rec null: not used)
 };
 
 template <int HD, typename E>
@@ -1781,14 +2239,32 @@ void launch_bwd_pair(const msd_dsa3d_desc& d, const void* q, const void* k, cons
   const int64_t acc_ks = w.acc_ks, acc_vs = w.acc_vs;
   // scaled fp16 accumulation: bf16 storage with MSD_ACCUM_F16 only
   const bool h16 = sizeof(E) == 2 && w.h16;
+  // bf16 with fp32 accumulation and no extra keys: the first kernel also
+  // writes tap records, the column-streaming kernel takes every column it can
+  // and the tile kernel the columns it flags
+  if constexpr (sizeof(E) == 2) {
+    if (!h16 && w.rec.rec != nullptr) {
+      hipLaunchKernelGGL((dsa3d_bwd_p1_kernel<HD, E, 4, true>), g1, dim3(tiled::kThreads), 0, s,
+                         a1, o, go, lse, dlse, goff, p_ws, b_ws, dk_acc, dv_acc, acc_ks, acc_vs,
+                         w.rec);
+      const dim3 gs(static_cast<unsigned>(d.B * a1.tiles_h * a1.tiles_w), d.num_heads);
+      hipLaunchKernelGGL((dsa3d_bwd_p2s_kernel<HD, E>), gs, dim3(kS2Threads), 0, s, a1, w.rec,
+                         b_ws, gq, static_cast<float*>(dk_acc), static_cast<float*>(dv_acc),
+                         acc_ks, acc_vs);
+      hipLaunchKernelGGL((dsa3d_bwd_p2_list_kernel<HD, CW, E, FR>), dim3(256, 1, HD / CW),
+                         dim3(P2Tile<FR>::Threads), 0, s, a2, go, p_ws, b_ws, gq, dk_acc, dv_acc,
+                         acc_ks, acc_vs, w.rec.collist);
+      return;
+    }
+  }
   if constexpr (sizeof(E) == 2) {
     if (h16)
       hipLaunchKernelGGL((dsa3d_bwd_p1_kernel<HD, E, 2>), g1, dim3(tiled::kThreads), 0, s, a1, o,
-                         go, lse, dlse, goff, p_ws, b_ws, dk_acc, dv_acc, acc_ks, acc_vs);
+                         go, lse, dlse, goff, p_ws, b_ws, dk_acc, dv_acc, acc_ks, acc_vs, RecArgs{});
   }
   if (!h16)
     hipLaunchKernelGGL((dsa3d_bwd_p1_kernel<HD, E, 4>), g1, dim3(tiled::kThreads), 0, s, a1, o,
-                       go, lse, dlse, goff, p_ws, b_ws, dk_acc, dv_acc, acc_ks, acc_vs);
+                       go, lse, dlse, goff, p_ws, b_ws, dk_acc, dv_acc, acc_ks, acc_vs, RecArgs{});
   if (d.extra_g > 0) {
     const dim3 gx(static_cast<unsigned>(d.B * ((a1.N + kXQ - 1) / kXQ)), d.num_heads);
     hipLaunchKernelGGL((dsa3d_bwd_extra_kernel<HD, E>), gx, dim3(256), 0, s, a1, o, go, lse, dlse,
@@ -1884,8 +2360,14 @@ __global__ __launch_bounds__(256) void acc_to_bf16_kernel(const float* __restric
 // per-block maxima, the two scales and their inverses and the overflow flag
 // follow the extra keys' buffers.
 struct TiledWs {
-  size_t acc, xacc, p, ds, dse, pfe, dqx, stats, scales, bytes;
+  size_t acc, xacc, p, ds, dse, pfe, dqx, stats, scales, rec, hdr, qt, collist, bytes;
 };
+
+// Calls that take the column-streaming dq/dK/dV kernel: bf16 storage with fp32
+// dK/dV accumulation and no extra keys.
+bool tiled_streams(const msd_dsa3d_desc& d) {
+  return d.dtype == MSD_BF16 && d.dkv_accum == MSD_ACCUM_F32 && d.extra_g == 0;
+}
 
 TiledWs tiled_ws(const msd_dsa3d_desc& d) {
   const size_t rows = static_cast<size_t>(d.B) * d.T * d.H * d.W;
@@ -1905,7 +2387,18 @@ TiledWs tiled_ws(const msd_dsa3d_desc& d) {
   w.dqx = up(w.pfe + rows * d.num_heads * G * e);
   w.stats = up(w.dqx + (G > 0 ? rows * D * 4 : 0));
   w.scales = up(w.stats + (bf ? kBoundsBlocks * kBoundsWords * 4 : 0));
-  w.bytes = w.scales + (bf ? 32 : 0);
+  // column-streaming kernel: records, tile headers, transposed q / dO, flags
+  const bool st = tiled_streams(d);
+  const size_t tiles = static_cast<size_t>(d.B) * d.T * ((d.H + tiled::kTileH - 1) / tiled::kTileH) *
+                       ((d.W + tiled::kTileW - 1) / tiled::kTileW) * d.num_heads;
+  const size_t cols = static_cast<size_t>(d.B) * ((d.H + tiled::kTileH - 1) / tiled::kTileH) *
+                      ((d.W + tiled::kTileW - 1) / tiled::kTileW) * d.num_heads;
+  const size_t K = static_cast<size_t>(d.kt) * d.kh * d.kw;
+  w.rec = up(w.scales + (bf ? 32 : 0));
+  w.hdr = up(w.rec + (st ? tiles * K * tiled::kTQ * 16 : 0));
+  w.qt = up(w.hdr + (st ? tiles * tiled::kRecHdr * 4 : 0));
+  w.collist = up(w.qt + (st ? tiles * 2 * d.head_dim * tiled::kTQ * e : 0));
+  w.bytes = w.collist + (st ? (cols + 1) * 4 : 0);
   return w;
 }
 
@@ -1947,6 +2440,14 @@ hipError_t bwd_tiled_typed(const msd_dsa3d_desc& d, const void* q, const void* k
   w.dek_acc = kInPlace ? static_cast<float*>(dek) : reinterpret_cast<float*>(base + L.xacc);
   w.dev_acc = kInPlace ? static_cast<float*>(dev) : w.dek_acc + erows * D;
   w.dqx = erows > 0 ? reinterpret_cast<float*>(base + L.dqx) : nullptr;
+  w.rec = RecArgs{};
+  if (tiled_streams(d)) {
+    w.rec.rec = reinterpret_cast<tiled::u32x4_t*>(base + L.rec);
+    w.rec.hdr = reinterpret_cast<int*>(base + L.hdr);
+    w.rec.qt = base + L.qt;
+    w.rec.collist = reinterpret_cast<int*>(base + L.collist);
+    w.rec.tiles = tiled_tiles<1>(d);
+  }
   if (erows > 0) {
     hipLaunchKernelGGL(fill_zero_f32, dim3(fill_blocks(erows * D)), dim3(256), 0, s, w.dek_acc,
                        erows * D);

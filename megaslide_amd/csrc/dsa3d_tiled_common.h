@@ -142,6 +142,7 @@ struct Args {
   int B, T, H, W, nh, kt, kh, kw, K, C;
   int tiles_h, tiles_w;
   int xcd_remap;       // tiles per XCD when tiles are spread XCD-contiguously, else 0
+  int head0;           // head of blockIdx.y 0 (a launch over a group of heads)
   float offset_scale, softmax_scale;
   float div_x, div_y, div_z;     // divisors of offset slots 0, 1, 2 (0 = slot dropped)
   float rdiv_x, rdiv_y, rdiv_z;  // their reciprocals, rounded to nearest (0 = slot dropped)
@@ -157,6 +158,35 @@ struct Args {
 };
 
 constexpr int kMaxExtra = 256;   // extra keys the tiled kernels take (a table row)
+
+// Tap records of the first backward kernel for the column-streaming dq/dK/dV
+// kernel (bf16 storage).  Per (head, one-frame tile): up to K * 16 records of
+// 16 bytes, counting-sorted by the tap's lower corner plane z0 into kRecBins
+// bins from the tile's lowest plane, and a header of kRecHdr ints:
+//   [0..5] the tile's corner box zlo, zhi, ylo, yhi, xlo, xhi; [6] bins used
+//   (0: no tap; -1: the planes span more than kRecBins bins, no records);
+//   [8 + b] first record of bin b (b <= bins used: [8 + bins] = count).
+// Record words: y0 | x0 << 14 | query << 28 (the tile's query 0..15); fx and
+// fy as 16-bit fractions (lo, hi); fz (fp32 bits); the fp16 pair (p * dropout
+// factor, ds * scale / l1) of the tap, l1 = sum over the query's taps of
+// |ds * scale|.  Per (head, tile) too: q and dO of the tile's 16 queries,
+// transposed ([tensor][channel][query], bf16), q times l1 / 2^30 and dO times
+// 1 / fix_a: the scales of the B and A tables' fixed point.
+constexpr int kRecBins = 16;
+constexpr int kRecHdr = 32;
+struct RecArgs {
+  u32x4_t* rec;    // [nh][tiles][K * 16] records
+  int* hdr;        // [nh][tiles][kRecHdr]
+  void* qt;        // [nh][tiles][2][HD][16] element type
+  int* collist;    // [0]: count, then head * columns + column of each column
+                   // left to the tile kernel
+  int64_t tiles;   // one-frame tiles per head
+};
+
+// Index of the one-frame tile (b, t, th, tw) among a head's tiles.
+__device__ __forceinline__ int64_t rec_tile(const Args& a, int b, int t, int th, int tw) {
+  return ((static_cast<int64_t>(b) * a.T + t) * a.tiles_h + th) * a.tiles_w + tw;
+}
 
 // Geometry of one tap, kept in registers between the passes.
 struct Slot {
@@ -202,11 +232,11 @@ inline int64_t tile_count(int B, int T, int H, int W) {
          ((W + kTileW - 1) / kTileW);
 }
 
-// Tile `tile` of head blockIdx.y.
+// Tile `tile` of head head0 + blockIdx.y.
 template <int FRAMES, int SUBS>
 __device__ __forceinline__ Tile make_tile_at(const Args& a, int tile) {
   Tile t;
-  t.head = blockIdx.y;
+  t.head = a.head0 + static_cast<int>(blockIdx.y);
   // Workgroups are dispatched round-robin over the 8 XCDs; give each XCD a
   // contiguous run of tiles so neighbouring tiles share its L2.  Frames vary
   // fastest: consecutive tiles of one (h, w) column read and accumulate into
