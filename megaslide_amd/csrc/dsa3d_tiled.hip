@@ -2394,11 +2394,14 @@ TiledWs tiled_ws(const msd_dsa3d_desc& d) {
   const size_t cols = static_cast<size_t>(d.B) * ((d.H + tiled::kTileH - 1) / tiled::kTileH) *
                       ((d.W + tiled::kTileW - 1) / tiled::kTileW) * d.num_heads;
   const size_t K = static_cast<size_t>(d.kt) * d.kh * d.kw;
-  w.rec = up(w.scales + (bf ? 32 : 0));
-  w.hdr = up(w.rec + (st ? tiles * K * tiled::kTQ * 16 : 0));
-  w.qt = up(w.hdr + (st ? tiles * tiled::kRecHdr * 4 : 0));
-  w.collist = up(w.qt + (st ? tiles * 2 * d.head_dim * tiled::kTQ * e : 0));
-  w.bytes = w.collist + (st ? (cols + 1) * 4 : 0);
+  w.rec = w.hdr = w.qt = w.collist = w.bytes = w.scales + (bf ? 32 : 0);
+  if (st) {
+    w.rec = up(w.bytes);
+    w.hdr = up(w.rec + tiles * K * tiled::kTQ * 16);
+    w.qt = up(w.hdr + tiles * tiled::kRecHdr * 4);
+    w.collist = up(w.qt + tiles * 2 * d.head_dim * tiled::kTQ * e);
+    w.bytes = w.collist + (cols + 1) * 4;
+  }
   return w;
 }
 
