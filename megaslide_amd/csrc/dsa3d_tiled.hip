@@ -457,6 +457,9 @@ __global__ __launch_bounds__(kThreads, (p1_min_waves<HD, E>())) void dsa3d_bwd_p
   // dP sits a constant kP1Tab floats past S (immediate offsets on the reads).
   __shared__ __attribute__((aligned(16))) float s_tb[2][2 * kP1Tab];
   __shared__ int s_red[kWaves][6];
+  // record bins (REC): counts, then starts
+  __shared__ int s_bin[REC ? 2 * kRecBins : 1];
+  if (REC && threadIdx.x < kRecBins) s_bin[threadIdx.x] = 0;  // ordered by the setup's barrier
   constexpr bool kTwoWg = p1_min_waves<HD, E>() == 4;
   constexpr int XR = HD + 8;  // [query][channel] row of the staged q and dO (elements)
   __shared__ __attribute__((aligned(16))) word_t<E> s_x[kTwoWg ? 2 * kTQ * XR : 1];
@@ -728,17 +731,13 @@ __global__ __launch_bounds__(kThreads, (p1_min_waves<HD, E>())) void dsa3d_bwd_p
   // bin), then one thread's prefix sum.  Within a bin the order is the
   // atomics' order, which no result depends on (the consumer sums integers).
   int pos[kSlots];
-  int* const s_bin = reinterpret_cast<int*>(&s_tb[0][0]);  // [counts | starts], tables are free
   const bool rec_wide = REC && !(box.zhi < box.zlo) && box.zhi - box.zlo + 1 > kRecBins;
   if constexpr (REC) {
     const int64_t trec = static_cast<int64_t>(tl.head) * rc.tiles +
                          rec_tile(a, tl.b, tl.t0, tl.h0 / kTileH, tl.w0 / kTileW);
     if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) rc.collist[0] = 0;
     const int nb = box.zhi < box.zlo ? 0 : box.zhi - box.zlo + 1;
-    __syncthreads();  // every table read of the plane loop and s_dl read above is done
-    if (threadIdx.x < kRecBins) s_bin[threadIdx.x] = 0;
-    if (sub == 0) s_dl[tid / kSubs][0] = l1q;  // this query's l1
-    __syncthreads();
+    if (sub == 0) s_dl[tid / kSubs][0] = l1q;  // this query's l1 (delta was read above)
 #pragma unroll
     for (int i = 0; i < kSlots; ++i) {
       pos[i] = 0;
@@ -746,23 +745,31 @@ __global__ __launch_bounds__(kThreads, (p1_min_waves<HD, E>())) void dsa3d_bwd_p
         pos[i] = atomicAdd(&s_bin[slot_z0(sl[i]) - box.zlo], 1);
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-      int* const hdr = rc.hdr + trec * kRecHdr;
-      int acc = 0;
-      for (int bb = 0; bb < kRecBins; ++bb) {
-        const int cnt = s_bin[bb];
-        s_bin[kRecBins + bb] = acc;
-        hdr[8 + bb] = acc;
-        acc += cnt;
+    // exclusive prefix of the 16 counts in wave 0 (lane bb holds bin bb)
+    if (threadIdx.x < 64) {
+      const int bb = threadIdx.x & (kRecBins - 1);
+      const int cnt = threadIdx.x < kRecBins ? s_bin[bb] : 0;
+      int inc = cnt;
+#pragma unroll
+      for (int m = 1; m < kRecBins; m <<= 1) {
+        const int o = __shfl_up(inc, m, kRecBins);
+        if (bb >= m) inc += o;
       }
-      hdr[8 + kRecBins] = acc;
-      hdr[0] = box.zlo;
-      hdr[1] = box.zhi;
-      hdr[2] = box.ylo;
-      hdr[3] = box.yhi;
-      hdr[4] = box.xlo;
-      hdr[5] = box.xhi;
-      hdr[6] = rec_wide ? -1 : nb;
+      int* const hdr = rc.hdr + trec * kRecHdr;
+      if (threadIdx.x < kRecBins) {
+        s_bin[kRecBins + bb] = inc - cnt;
+        hdr[8 + bb] = inc - cnt;
+        if (bb == kRecBins - 1) hdr[8 + kRecBins] = inc;
+      }
+      if (threadIdx.x == 0) {
+        hdr[0] = box.zlo;
+        hdr[1] = box.zhi;
+        hdr[2] = box.ylo;
+        hdr[3] = box.yhi;
+        hdr[4] = box.xlo;
+        hdr[5] = box.xhi;
+        hdr[6] = rec_wide ? -1 : nb;
+      }
     }
     __syncthreads();
   }
