@@ -1363,7 +1363,9 @@ __global__ __launch_bounds__(kS2Threads) void dsa3d_bwd_p2s_kernel(
   __shared__ __attribute__((aligned(16))) word_t<E> s_kt[KC * KR];
   __shared__ __attribute__((aligned(16))) int s_rows[kChunkNV];
   __shared__ int s_fz[kS2MaxT][2];         // per frame: zlo, zhi (zlo > zhi: never live)
-  __shared__ int s_live[SR];               // frame in each slot at this plane, or -1
+  __shared__ int s_live[SR];               // frame in each slot at this plane (pass), or -1
+  __shared__ int s_new[SR];                // a frame that starts on the plane its slot's frame ends
+  __shared__ int s_npass;                  // 2 when some slot has such a frame
   __shared__ int s_rg[kS2Ranges][3];       // record range: first record, count, upper
   __shared__ int s_pre[kS2Ranges + 1];     // range prefix sums
   __shared__ int s_red[kS2Waves][8];
@@ -1409,12 +1411,15 @@ __global__ __launch_bounds__(kS2Threads) void dsa3d_bwd_p2s_kernel(
     }
   }
   __syncthreads();
-  // the next frame of a slot starts after the previous one ends
+  // the next frame of a slot starts after the previous one ends, or on its
+  // last plane (that plane then takes a second pass for the new frames) and
+  // goes on beyond it
   for (int t = threadIdx.x; t < a.T && t < kS2MaxT; t += kS2Threads) {
     if (s_fz[t][0] > s_fz[t][1]) continue;
     for (int u = t + SR; u < a.T && u < kS2MaxT; u += SR) {
       if (s_fz[u][0] > s_fz[u][1]) continue;
-      if (s_fz[u][0] <= s_fz[t][1]) bad = 1;
+      if (s_fz[u][0] < s_fz[t][1] || (s_fz[u][0] == s_fz[t][1] && s_fz[u][1] == s_fz[u][0]))
+        bad = 1;
       break;
     }
   }
@@ -1485,163 +1490,194 @@ __global__ __launch_bounds__(kS2Threads) void dsa3d_bwd_p2s_kernel(
   StageRows<kP2Stage, KC, E> kr;
 
   for (int z = box.zlo; z <= box.zhi; ++z) {
-    // ---- live frames of this plane and their record ranges ----------------
+    // ---- live frames of this plane: per slot the earlier frame, and a later
+    // one that starts here while the earlier one ends here --------------------
     __syncthreads();  // the previous plane's dq write-out has read s_live
-    if (threadIdx.x < SR) s_live[threadIdx.x] = -1;
-    __syncthreads();
-    for (int t = threadIdx.x; t < a.T; t += kS2Threads)
-      if (s_fz[t][0] <= z && z <= s_fz[t][1]) s_live[t % SR] = t;
-    __syncthreads();
-    if (threadIdx.x < kS2Ranges) {
-      const int r = threadIdx.x >> 1, up = threadIdx.x & 1;
-      const int t = s_live[r];
-      int first = 0, cnt = 0;
-      if (t >= 0) {
-        const int bin = z - up - s_fz[t][0];
-        const int* h = rc.hdr + (trec0 + t * tstep) * kRecHdr;
-        if (bin >= 0 && bin < h[6]) {
-          first = h[8 + bin];
-          cnt = h[9 + bin] - first;
-        }
-      }
-      s_rg[threadIdx.x][0] = first;
-      s_rg[threadIdx.x][1] = cnt;
-      s_rg[threadIdx.x][2] = up;
+    if (threadIdx.x < SR) {
+      s_live[threadIdx.x] = 0x7fffffff;
+      s_new[threadIdx.x] = -1;
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-      int acc = 0;
-      for (int j = 0; j < kS2Ranges; ++j) {
-        s_pre[j] = acc;
-        acc += s_rg[j][1];
+    for (int t = threadIdx.x; t < a.T; t += kS2Threads) {
+      if (s_fz[t][0] <= z && z <= s_fz[t][1]) {
+        atomicMin(&s_live[t % SR], t);
+        atomicMax(&s_new[t % SR], t);
       }
-      s_pre[kS2Ranges] = acc;
     }
     __syncthreads();
-    const int nrec = s_pre[kS2Ranges];
-
-    for (int ci = 0; ci < nchunks; ++ci) {
-      const Chunk c = make_chunk(box, ci);
-      const int cyi = box.ncx == 1 ? 0 : ci / box.ncx, cxi = ci - cyi * box.ncx;
-      for (int vi = threadIdx.x; vi < c.nv; vi += kS2Threads)
-        s_rows[vi] = static_cast<int>(chunk_row(a, tl, c, z, vi) - tl.sample0);
-
-      // one pass of the table: B (ds * scale * w, phase 0) or A (p * w, phase 1)
-      auto scatter = [&](int phase) {
-        for (int e = threadIdx.x; e < c.nvp * kS2Row / 4; e += kS2Threads) {
-          const u32x4_t zz = {0u, 0u, 0u, 0u};
-          __builtin_memcpy(&s_tab[4 * e], &zz, sizeof(zz));
-        }
+    if (threadIdx.x < 64) {
+      const int r = threadIdx.x;
+      bool two = false;
+      if (r < SR) {
+        const int lo = s_live[r], hi = s_new[r];
+        two = hi >= 0 && hi != lo;
+        s_live[r] = lo == 0x7fffffff ? -1 : lo;
+        s_new[r] = two ? hi : -1;
+      }
+      const bool any = __builtin_amdgcn_ballot_w64(two) != 0;
+      if (r == 0) s_npass = any ? 2 : 1;
+    }
+    __syncthreads();
+    const int npass = s_npass;
+    for (int pass = 0; pass < npass; ++pass) {
+      if (pass == 1) {
+        // the frames that start on this plane, alone (the others are done)
+        __syncthreads();  // the first pass's dq write-out has read s_live
+        if (threadIdx.x < SR) s_live[threadIdx.x] = s_new[threadIdx.x];
         __syncthreads();
-        for (int i = threadIdx.x; i < nrec; i += kS2Threads) {
-          int j = 0;
-#pragma unroll
-          for (int k = 1; k < kS2Ranges; ++k) j += i >= s_pre[k] ? 1 : 0;
-          const int slot = j >> 1, t = s_live[slot];
-          const int64_t ridx = (trec0 + t * tstep) * K16 + s_rg[j][0] + (i - s_pre[j]);
-          const u32x4_t r = rc.rec[ridx];
-          const int y0 = static_cast<int>(r[0] & 0x3fffu);
-          const int x0 = static_cast<int>((r[0] >> 14) & 0x3fffu);
-          const int qq = static_cast<int>(r[0] >> 28);
-          const float fz = __uint_as_float(r[2]);
-          const float wz = s_rg[j][2] ? fz : 1.0f - fz;
-          if (nchunks > 1) {
-            const int ky = min((y0 - box.ylo) / kChunkStep, box.ncy - 1);
-            const int kx = min((x0 - box.xlo) / kChunkStep, box.ncx - 1);
-            if (ky != cyi || kx != cxi) continue;
+      }
+      // ---- record ranges of the pass's frames ---------------------------------
+      if (threadIdx.x < kS2Ranges) {
+        const int r = threadIdx.x >> 1, up = threadIdx.x & 1;
+        const int t = s_live[r];
+        int first = 0, cnt = 0;
+        if (t >= 0) {
+          const int bin = z - up - s_fz[t][0];
+          const int* h = rc.hdr + (trec0 + t * tstep) * kRecHdr;
+          if (bin >= 0 && bin < h[6]) {
+            first = h[8 + bin];
+            cnt = h[9 + bin] - first;
           }
-          const float fx = static_cast<float>(r[1] & 0xffffu) * (1.0f / 65536.0f);
-          const float fy = static_cast<float>(r[1] >> 16) * (1.0f / 65536.0f);
-          const float v = (phase == 0 ? h2_hi(r[3]) * kFixA : h2_lo(r[3]) * a.fix_a) * wz;
-          const float gx = 1.0f - fx, gy = 1.0f - fy;
-          const int base = (y0 - c.cy0) * c.nx + (x0 - c.cx0);
-          const int dy = fy != 0.0f ? c.nx : 0, dx = fx != 0.0f ? 1 : 0;
-          int* const r00 = &s_tab[base * kS2Row + kTQ * slot + qq];
-          int* const r10 = r00 + dy * kS2Row;
-          atomicAdd(r00, to_fix(v * (gy * gx)));
-          atomicAdd(r00 + dx * kS2Row, to_fix(v * (gy * fx)));
-          atomicAdd(r10, to_fix(v * (fy * gx)));
-          atomicAdd(r10 + dx * kS2Row, to_fix(v * (fy * fx)));
         }
-      };
-
-      // ---- B: dq and dK -----------------------------------------------------
-      load_stage_rows<kP2Stage, KC, E>(a, tl, c, z, kp, a.ks, hc0, kr);
-      scatter(0);
+        s_rg[threadIdx.x][0] = first;
+        s_rg[threadIdx.x][1] = cnt;
+        s_rg[threadIdx.x][2] = up;
+      }
       __syncthreads();
-#pragma unroll
-      for (int rd = 0; rd < NR; ++rd) {
-        store_stage<kP2Stage, KC, E>(c, kr, s_kt);
+      if (threadIdx.x == 0) {
+        int acc = 0;
+        for (int j = 0; j < kS2Ranges; ++j) {
+          s_pre[j] = acc;
+          acc += s_rg[j][1];
+        }
+        s_pre[kS2Ranges] = acc;
+      }
+      __syncthreads();
+      const int nrec = s_pre[kS2Ranges];
+
+      for (int ci = 0; ci < nchunks; ++ci) {
+        const Chunk c = make_chunk(box, ci);
+        const int cyi = box.ncx == 1 ? 0 : ci / box.ncx, cxi = ci - cyi * box.ncx;
+        for (int vi = threadIdx.x; vi < c.nv; vi += kS2Threads)
+          s_rows[vi] = static_cast<int>(chunk_row(a, tl, c, z, vi) - tl.sample0);
+
+        // one pass of the table: B (ds * scale * w, phase 0) or A (p * w, phase 1)
+        auto scatter = [&](int phase) {
+          for (int e = threadIdx.x; e < c.nvp * kS2Row / 4; e += kS2Threads) {
+            const u32x4_t zz = {0u, 0u, 0u, 0u};
+            __builtin_memcpy(&s_tab[4 * e], &zz, sizeof(zz));
+          }
+          __syncthreads();
+          for (int i = threadIdx.x; i < nrec; i += kS2Threads) {
+            int j = 0;
+  #pragma unroll
+            for (int k = 1; k < kS2Ranges; ++k) j += i >= s_pre[k] ? 1 : 0;
+            const int slot = j >> 1, t = s_live[slot];
+            const int64_t ridx = (trec0 + t * tstep) * K16 + s_rg[j][0] + (i - s_pre[j]);
+            const u32x4_t r = rc.rec[ridx];
+            const int y0 = static_cast<int>(r[0] & 0x3fffu);
+            const int x0 = static_cast<int>((r[0] >> 14) & 0x3fffu);
+            const int qq = static_cast<int>(r[0] >> 28);
+            const float fz = __uint_as_float(r[2]);
+            const float wz = s_rg[j][2] ? fz : 1.0f - fz;
+            if (nchunks > 1) {
+              const int ky = min((y0 - box.ylo) / kChunkStep, box.ncy - 1);
+              const int kx = min((x0 - box.xlo) / kChunkStep, box.ncx - 1);
+              if (ky != cyi || kx != cxi) continue;
+            }
+            const float fx = static_cast<float>(r[1] & 0xffffu) * (1.0f / 65536.0f);
+            const float fy = static_cast<float>(r[1] >> 16) * (1.0f / 65536.0f);
+            const float v = (phase == 0 ? h2_hi(r[3]) * kFixA : h2_lo(r[3]) * a.fix_a) * wz;
+            const float gx = 1.0f - fx, gy = 1.0f - fy;
+            const int base = (y0 - c.cy0) * c.nx + (x0 - c.cx0);
+            const int dy = fy != 0.0f ? c.nx : 0, dx = fx != 0.0f ? 1 : 0;
+            int* const r00 = &s_tab[base * kS2Row + kTQ * slot + qq];
+            int* const r10 = r00 + dy * kS2Row;
+            atomicAdd(r00, to_fix(v * (gy * gx)));
+            atomicAdd(r00 + dx * kS2Row, to_fix(v * (gy * fx)));
+            atomicAdd(r10, to_fix(v * (fy * gx)));
+            atomicAdd(r10 + dx * kS2Row, to_fix(v * (fy * fx)));
+          }
+        };
+
+        // ---- B: dq and dK -----------------------------------------------------
+        load_stage_rows<kP2Stage, KC, E>(a, tl, c, z, kp, a.ks, hc0, kr);
+        scatter(0);
         __syncthreads();
-        if (rd + 1 < NR)
-          load_stage_rows<kP2Stage, KC, E>(a, tl, c, z, kp, a.ks, hc0 + KC * (rd + 1), kr);
-        if (s_live[my_slot] >= 0) {
-          for (int kc = 0; kc < c.nvp; kc += 32) {
-            float bq[8];  // fixed-point units; the query's l1 / 2^30 is applied to dq at the end
-#pragma unroll
-            for (int jj = 0; jj < 8; ++jj)
-              bq[jj] = static_cast<float>(s_tab[(kc + kq + jj) * kS2Row + kTQ * my_slot + mq]);
-            dq_acc[rd] = mma16(precise_op<E>(bq),
-                               load_op<E>(&s_kt[(16 * my_ct + mq) * KR + kc + kq]), dq_acc[rd]);
+  #pragma unroll
+        for (int rd = 0; rd < NR; ++rd) {
+          store_stage<kP2Stage, KC, E>(c, kr, s_kt);
+          __syncthreads();
+          if (rd + 1 < NR)
+            load_stage_rows<kP2Stage, KC, E>(a, tl, c, z, kp, a.ks, hc0 + KC * (rd + 1), kr);
+          if (s_live[my_slot] >= 0) {
+            for (int kc = 0; kc < c.nvp; kc += 32) {
+              float bq[8];  // fixed-point units; the query's l1 / 2^30 is applied to dq at the end
+  #pragma unroll
+              for (int jj = 0; jj < 8; ++jj)
+                bq[jj] = static_cast<float>(s_tab[(kc + kq + jj) * kS2Row + kTQ * my_slot + mq]);
+              dq_acc[rd] = mma16(precise_op<E>(bq),
+                                 load_op<E>(&s_kt[(16 * my_ct + mq) * KR + kc + kq]), dq_acc[rd]);
+            }
           }
+          __syncthreads();  // every wave is done with this round's K^T
         }
-        __syncthreads();  // every wave is done with this round's K^T
-      }
-      // dK[v] += sum over ring queries of B[q][v] q[q] (32x32 MFMA per live slot)
-      for (int task = tl.wave;; task += kS2Waves) {
-        const int c2 = task % (HD / 32), vb = task / (HD / 32);
-        if (vb * 32 >= c.nv) break;
-        const int och = 32 * c2 + (tl.lane & 31);
-        f32x16_t acc = {};
-#pragma unroll
-        for (int r = 0; r < SR; ++r) {
-          const int t = s_live[r];
-          if (t < 0) continue;
-          const E* qp = qtb + (trec0 + t * tstep) * (2 * HD * kTQ) + och * kTQ + oq;
-          acc = mma32(table_t_rows<E>(s_tab, kS2Row, kTQ * r, vb, tl.lane), load_op<E>(qp), acc);
-        }
-        flush_block(tl, acc, s_rows, vb, c.nv, hc0 + och, dk_acc, acc_ks);
-      }
-      __syncthreads();  // every wave is done with the B table
-
-      // ---- A: dV --------------------------------------------------------------
-      scatter(1);
-      __syncthreads();
-      for (int task = tl.wave;; task += kS2Waves) {
-        const int c2 = task % (HD / 32), vb = task / (HD / 32);
-        if (vb * 32 >= c.nv) break;
-        const int och = 32 * c2 + (tl.lane & 31);
-        f32x16_t acc = {};
-#pragma unroll
-        for (int r = 0; r < SR; ++r) {
-          const int t = s_live[r];
-          if (t < 0) continue;
-          const E* gp = qtb + (trec0 + t * tstep) * (2 * HD * kTQ) + (HD + och) * kTQ + oq;
-          acc = mma32(table_t_rows<E>(s_tab, kS2Row, kTQ * r, vb, tl.lane), load_op<E>(gp), acc);
-        }
-        flush_block(tl, acc, s_rows, vb, c.nv, hc0 + och, dv_acc, acc_vs);
-      }
-      __syncthreads();  // the table and s_rows are rewritten by the next step
-    }
-
-    // ---- frames that end at this plane: their dq ---------------------------
-    const int tr = s_live[my_slot];
-    if (tr >= 0 && s_fz[tr][1] == z) {
-#pragma unroll
-      for (int rd = 0; rd < NR; ++rd) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int m = 4 * (tl.lane >> 4) + i;
-          const int h = tl.h0 + m / kTileW, w = tl.w0 + m % kTileW;
-          if (h < a.H && w < a.W) {
-            const int64_t n = tl.sample0 + (static_cast<int64_t>(tr) * a.H + h) * a.W + w;
-            const int ch = hc0 + KC * rd + 16 * my_ct + mq;
-            dq[n * a.qs + ch] = from_f32<E>(dq_acc[rd][i] * l1_ws[n * a.nh + tl.head] * kFixAInv);
+        // dK[v] += sum over ring queries of B[q][v] q[q] (32x32 MFMA per live slot)
+        for (int task = tl.wave;; task += kS2Waves) {
+          const int c2 = task % (HD / 32), vb = task / (HD / 32);
+          if (vb * 32 >= c.nv) break;
+          const int och = 32 * c2 + (tl.lane & 31);
+          f32x16_t acc = {};
+  #pragma unroll
+          for (int r = 0; r < SR; ++r) {
+            const int t = s_live[r];
+            if (t < 0) continue;
+            const E* qp = qtb + (trec0 + t * tstep) * (2 * HD * kTQ) + och * kTQ + oq;
+            acc = mma32(table_t_rows<E>(s_tab, kS2Row, kTQ * r, vb, tl.lane), load_op<E>(qp), acc);
           }
+          flush_block(tl, acc, s_rows, vb, c.nv, hc0 + och, dk_acc, acc_ks);
         }
-        dq_acc[rd] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        __syncthreads();  // every wave is done with the B table
+
+        // ---- A: dV --------------------------------------------------------------
+        scatter(1);
+        __syncthreads();
+        for (int task = tl.wave;; task += kS2Waves) {
+          const int c2 = task % (HD / 32), vb = task / (HD / 32);
+          if (vb * 32 >= c.nv) break;
+          const int och = 32 * c2 + (tl.lane & 31);
+          f32x16_t acc = {};
+  #pragma unroll
+          for (int r = 0; r < SR; ++r) {
+            const int t = s_live[r];
+            if (t < 0) continue;
+            const E* gp = qtb + (trec0 + t * tstep) * (2 * HD * kTQ) + (HD + och) * kTQ + oq;
+            acc = mma32(table_t_rows<E>(s_tab, kS2Row, kTQ * r, vb, tl.lane), load_op<E>(gp), acc);
+          }
+          flush_block(tl, acc, s_rows, vb, c.nv, hc0 + och, dv_acc, acc_vs);
+        }
+        __syncthreads();  // the table and s_rows are rewritten by the next step
       }
-    }
+
+      // ---- frames that end at this plane: their dq ---------------------------
+      const int tr = s_live[my_slot];
+      if (tr >= 0 && s_fz[tr][1] == z) {
+  #pragma unroll
+        for (int rd = 0; rd < NR; ++rd) {
+  #pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int m = 4 * (tl.lane >> 4) + i;
+            const int h = tl.h0 + m / kTileW, w = tl.w0 + m % kTileW;
+            if (h < a.H && w < a.W) {
+              const int64_t n = tl.sample0 + (static_cast<int64_t>(tr) * a.H + h) * a.W + w;
+              const int ch = hc0 + KC * rd + 16 * my_ct + mq;
+              dq[n * a.qs + ch] = from_f32<E>(dq_acc[rd][i] * l1_ws[n * a.nh + tl.head] * kFixAInv);
+            }
+          }
+          dq_acc[rd] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+      }
+    }  // passes
   }
 }
 
