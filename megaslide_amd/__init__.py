@@ -8,11 +8,15 @@ Public surface:
   dwconv3d                     depthwise 3-D conv (+GELU) on channel-last tokens (autograd)
   keep_core_policy, keep_core_context, checkpoint_keep_core
                                selective checkpointing that keeps the core's outputs
+  keep_gemms_policy, keep_gemms_context, checkpoint_keep_gemms
+                               ... and every GEMM's outputs
 """
 
 from .attention import DeformableSlideAttention3D
-from .block import MLP, DiTBlock, checkpoint_keep_core
-from .ops import DwConv3dFunction, dsa3d_core, dwconv3d, keep_core_context, keep_core_policy
+from .block import MLP, DiTBlock, checkpoint_keep_core, checkpoint_keep_gemms
+from .ops import (DwConv3dFunction, dsa3d_core, dwconv3d, keep_core_context, keep_core_policy,
+                  keep_gemms_context, keep_gemms_policy)
 
 __all__ = ["DeformableSlideAttention3D", "DiTBlock", "MLP", "DwConv3dFunction", "dsa3d_core",
-           "dwconv3d", "keep_core_policy", "keep_core_context", "checkpoint_keep_core"]
+           "dwconv3d", "keep_core_policy", "keep_core_context", "checkpoint_keep_core",
+           "keep_gemms_policy", "keep_gemms_context", "checkpoint_keep_gemms"]

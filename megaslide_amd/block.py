@@ -15,7 +15,10 @@ trainer.py:377-438's recompute pattern) the backward re-runs the block's
 forward; ``checkpoint_keep_core`` runs it under torch.utils.checkpoint with a
 selective policy that keeps the attention core's outputs (out and lse, about
 D + 2 nh bytes a token in bf16) from the first forward, so the recompute skips
-the core's forward kernel and reruns only the norms, GEMMs and convolutions.
+the core's forward kernel and reruns only the norms, GEMMs and convolutions;
+``checkpoint_keep_gemms`` also keeps every GEMM's output (about 9 D more bytes
+a token in bf16), so the recompute reruns only the norms, the elementwise work
+and the depthwise convolutions.
 """
 
 from __future__ import annotations
@@ -27,7 +30,7 @@ import torch.nn as nn
 from torch import Tensor
 
 from .attention import DeformableSlideAttention3D
-from .ops import keep_core_context
+from .ops import keep_core_context, keep_gemms_context
 
 
 class MLP(nn.Module):
@@ -88,3 +91,14 @@ def checkpoint_keep_core(block: nn.Module, x: Tensor, video_shape: Tuple[int, in
     from torch.utils.checkpoint import checkpoint
     return checkpoint(block, x, video_shape, *args, use_reentrant=False,
                       context_fn=keep_core_context, **kwargs)
+
+
+def checkpoint_keep_gemms(block: nn.Module, x: Tensor, video_shape: Tuple[int, int, int],
+                          *args, **kwargs) -> Tensor:
+    """``block(x, video_shape, ...)`` under torch.utils.checkpoint (non-reentrant)
+    keeping the attention core's and every GEMM's outputs: the backward's
+    recompute reruns the LayerNorms, GELU, residual adds and depthwise
+    convolutions only."""
+    from torch.utils.checkpoint import checkpoint
+    return checkpoint(block, x, video_shape, *args, use_reentrant=False,
+                      context_fn=keep_gemms_context, **kwargs)

@@ -262,6 +262,26 @@ def keep_core_context():
     return create_selective_checkpoint_contexts(keep_core_policy)
 
 
+def keep_gemms_policy(ctx, op, *args, **kwargs):
+    """Selective-checkpoint policy that keeps the attention core's outputs and
+    every GEMM's (the q/k/v, offset, output and MLP projections: aten mm /
+    addmm), so the backward's recomputed forward reruns only elementwise work,
+    the LayerNorms and the depthwise convolutions.  A DiT block at 46,800
+    tokens, dim 1,536, then keeps ~2 GB of activations beyond its input."""
+    from torch.utils.checkpoint import CheckpointPolicy
+    if op in (torch.ops.megaslide.dsa3d_core.default, torch.ops.aten.mm.default,
+              torch.ops.aten.addmm.default):
+        return CheckpointPolicy.MUST_SAVE
+    return CheckpointPolicy.PREFER_RECOMPUTE
+
+
+def keep_gemms_context():
+    """context_fn for torch.utils.checkpoint.checkpoint(..., use_reentrant=False)
+    that applies keep_gemms_policy."""
+    from torch.utils.checkpoint import create_selective_checkpoint_contexts
+    return create_selective_checkpoint_contexts(keep_gemms_policy)
+
+
 def dsa3d_core(q: Tensor, k: Tensor, v: Tensor, offsets: Tensor, video_shape: Sequence[int],
                num_heads: int, kernel_size: Sequence[int] = (3, 7, 7), offset_scale: float = 1.0,
                return_lse: bool = False, algo: str = "auto", dropout_p: float = 0.0,

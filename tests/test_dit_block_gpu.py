@@ -5,9 +5,10 @@
   y, dx and every parameter gradient at the fp32 tolerance 1e-4 relative to
   max|ref| (k_proj.bias, zero by the softmax's shift invariance, against the
   k_proj.weight gradient's scale).
-* Selective checkpointing (checkpoint_keep_core): the backward's recompute
-  skips the attention core's forward kernel, and every gradient equals a plain
-  (not checkpointed) run up to the fp32 atomics' summation order.
+* Selective checkpointing (checkpoint_keep_core, checkpoint_keep_gemms): the
+  backward's recompute skips the attention core's forward kernel (and, keeping
+  the GEMMs, every aten mm / addmm), and every gradient equals a plain (not
+  checkpointed) run up to the fp32 atomics' summation order.
 """
 
 import pytest
@@ -62,9 +63,10 @@ def test_dit_block_matches_reference_golden():
 
 
 @pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
-def test_checkpoint_keep_core_skips_core_recompute(dt):
-    from megaslide_amd import DiTBlock, checkpoint_keep_core
+def test_selective_checkpoint_skips_core_recompute(dt):
+    from megaslide_amd import DiTBlock, checkpoint_keep_core, checkpoint_keep_gemms
     from megaslide_amd import ops
+    from torch.utils._python_dispatch import TorchDispatchMode
     from torch.utils.checkpoint import checkpoint
 
     print(f"[checkpoint keeping the core] {dt}", flush=True)
@@ -88,38 +90,61 @@ def test_checkpoint_keep_core_skips_core_recompute(dt):
         calls.append(want_lse)
         return orig(self, want_lse)
 
+    gemms = (torch.ops.aten.mm.default, torch.ops.aten.addmm.default)
+
+    class CountGemms(TorchDispatchMode):
+        """Counts the GEMMs of the forward, the backward and the backward's
+        recompute (the checkpoint's own mode sits above this one, so a GEMM it
+        answers from its saved outputs is not counted)."""
+        n = 0
+
+        def __torch_dispatch__(self, func, types, args=(), kwargs=None):
+            if func in gemms:
+                CountGemms.n += 1
+            return func(*args, **(kwargs or {}))
+
     def run(mode):
         xi = x.clone().requires_grad_(True)
-        if mode == "plain":
-            y = blk(xi, (T, H, W))
-        elif mode == "checkpoint":
-            y = checkpoint(blk, xi, (T, H, W), use_reentrant=False)
-        else:
-            y = checkpoint_keep_core(blk, xi, (T, H, W))
-        gr = torch.autograd.grad(y, (xi, *blk.parameters()), grad_outputs=gy)
+        with CountGemms():
+            if mode == "plain":
+                y = blk(xi, (T, H, W))
+            elif mode == "checkpoint":
+                y = checkpoint(blk, xi, (T, H, W), use_reentrant=False)
+            elif mode == "keep_core":
+                y = checkpoint_keep_core(blk, xi, (T, H, W))
+            else:
+                y = checkpoint_keep_gemms(blk, xi, (T, H, W))
+            gr = torch.autograd.grad(y, (xi, *blk.parameters()), grad_outputs=gy)
         return y.detach(), gr
 
     ops._CoreCall.forward = counting
     try:
-        counts = {}
-        res = {}
-        for mode in ("plain", "checkpoint", "keep_core"):
+        counts, mms, res = {}, {}, {}
+        for mode in ("plain", "checkpoint", "keep_core", "keep_gemms"):
             calls.clear()
+            CountGemms.n = 0
             res[mode] = run(mode)
             torch.cuda.synchronize()
-            counts[mode] = len(calls)
+            counts[mode], mms[mode] = len(calls), CountGemms.n
     finally:
         ops._CoreCall.forward = orig
-    print(f"  core forward launches: {counts}", flush=True)
-    assert counts == {"plain": 1, "checkpoint": 2, "keep_core": 1}
+    print(f"  core forward launches: {counts}; GEMMs: {mms}", flush=True)
+    assert counts == {"plain": 1, "checkpoint": 2, "keep_core": 1, "keep_gemms": 1}
+    # the plain checkpoint reruns the forward GEMMs up to the last one whose
+    # inputs the backward needs (offset, q, k, v, out, fc1: not fc2), keeping
+    # the GEMMs reruns none
+    assert mms["checkpoint"] - mms["plain"] == 6, mms
+    assert mms["keep_core"] == mms["checkpoint"], mms
+    assert mms["keep_gemms"] == mms["plain"], mms
     y0, g0 = res["plain"]
-    y1, g1 = res["keep_core"]
-    assert torch.equal(y0, y1)
     names = ["x"] + [n for n, _ in blk.named_parameters()]
     kw = g0[names.index("attn.k_proj.weight")].float().abs().max().item()
     tol = 1e-5 if dt == torch.float32 else 1e-2
-    for n, a, b in zip(names, g0, g1):
-        if n == "attn.k_proj.bias":  # rounding noise around zero
-            assert (b.float() - a.float()).abs().max().item() < tol * kw, n
-        else:
-            assert rel_err(b.float().cpu(), a.float().cpu(), floor=1e-6) < tol, n
+    for mode in ("keep_core", "keep_gemms"):
+        y1, g1 = res[mode]
+        assert torch.equal(y0, y1), mode
+        for n, a, b in zip(names, g0, g1):
+            if n == "attn.k_proj.bias":  # rounding noise around zero
+                assert (b.float() - a.float()).abs().max().item() < tol * kw, (mode, n)
+            else:
+                assert rel_err(b.float().cpu(), a.float().cpu(), floor=1e-6) < tol, (mode, n)
