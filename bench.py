@@ -629,18 +629,25 @@ def accumulation(cfg):
     return cfg.get("dkv_accum", "fp32")
 
 
-def phase_kernels(dtype, accum="fp32"):
+def phase_kernels(dtype, accum="fp32", extra=0):
     """Bench phase -> the kernels its ABI call launches, in order (bf16 adds the
-    conversion of the fp32 dK / dV rows to bf16; with fp16 accumulation the
-    scale kernels before the dq/dK/dV kernel, the conversion, and the fp32 redo
-    after an overflow, whose kernels return at once without one)."""
+    conversion of the fp32 dK / dV rows to bf16; bf16 with fp32 accumulation and
+    no extra keys runs the column-streaming dq/dK/dV kernel and the tile kernel
+    over the columns it leaves; with fp16 accumulation the scale kernels before
+    the dq/dK/dV kernel, the conversion, and the fp32 redo after an overflow,
+    whose kernels return at once without one)."""
     if dtype != "bf16":
         return {"dsa3d_fwd": ["dsa3d_fwd_tiled_kernel"],
                 "dsa3d_bwd": ["dsa3d_bwd_p1_kernel", "dsa3d_bwd_p2_kernel"]}
+    if accum == "fp32" and extra:
+        return {"dsa3d_fwd": ["dsa3d_fwd_tiled_kernel"],
+                "dsa3d_bwd": ["dsa3d_bwd_p1_kernel", "dsa3d_bwd_extra_kernel",
+                              "dsa3d_bwd_p2_kernel", "extra_grad_kernel",
+                              "acc_to_bf16_kernel"]}
     if accum == "fp32":
         return {"dsa3d_fwd": ["dsa3d_fwd_tiled_kernel"],
-                "dsa3d_bwd": ["dsa3d_bwd_p1_kernel", "dsa3d_bwd_p2_kernel",
-                              "acc_to_bf16_kernel"]}
+                "dsa3d_bwd": ["dsa3d_bwd_p1_kernel", "dsa3d_bwd_p2s_kernel",
+                              "dsa3d_bwd_p2_list_kernel", "acc_to_bf16_kernel"]}
     return {"dsa3d_fwd": ["dsa3d_fwd_tiled_kernel"],
             "dsa3d_bwd": ["dsa3d_bwd_p1_kernel", "h16_bounds_kernel", "h16_scales_kernel",
                           "dsa3d_bwd_p2_kernel", "h16_to_bf16_kernel", "fill_zero_if_flag",
@@ -708,7 +715,8 @@ def summarize(workload, trace_dir, fetch_dir, write_dir):
     rec = {}
     print("| phase (kernels) | FETCH KiB | WRITE KiB | traffic (scaled) | algorithmic | traffic / algorithmic |")
     print("|---|---|---|---|---|---|")
-    for phase, names in phase_kernels(cfg["dtype"], accumulation(cfg)).items():
+    for phase, names in phase_kernels(cfg["dtype"], accumulation(cfg),
+                                      cfg.get("extra_g", 0)).items():
         f_kib, w_kib = phase_sum(fetch, names), phase_sum(write, names)
         if f_kib is None or w_kib is None:
             continue
@@ -732,10 +740,6 @@ def summarize(workload, trace_dir, fetch_dir, write_dir):
     allrec[workload] = rec
     with open(path, "w") as f:
         json.dump(allrec, f, indent=1)
-
-
-COUNTER_KERNELS = ("dsa3d_fwd_tiled_kernel", "dsa3d_bwd_p1_kernel", "dsa3d_bwd_p2_kernel",
-                   "dwconv_")
 
 
 def counter_table(*dirs):

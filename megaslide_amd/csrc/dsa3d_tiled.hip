@@ -1330,9 +1330,11 @@ __global__ __launch_bounds__(P2Tile<FR>::Threads) void dsa3d_bwd_p2_redo_kernel(
 // each plane of their box once per tile, and a voxel lies in the boxes of
 // about three consecutive tiles of its column (the window spans ~7 planes),
 // so the atomics, executed past the L2 and the bound of that kernel, drop to
-// about 40% (the frames of a column share every flush).  Columns whose frames
-// need more than SR slots at once, or whose tile headers carry no records,
-// are flagged and left to the tile kernel.
+// about 40% (the frames of a column share every flush).  A frame that starts
+// on the last plane of its slot's previous frame takes a second pass over that
+// plane; columns where a frame starts earlier than that (more than SR frames
+// live at once), whose taps span more planes than a tile header has bins, or
+// with more than kS2MaxT frames are listed and left to the tile kernel.
 // Ring and K^T staging: eight slots and 32-channel K^T rounds.  (Nine slots,
 // which would take every column at the long-clip shape, where a few frames'
 // corner planes span nine planes, leave LDS for 16-channel rounds only: the
@@ -1344,7 +1346,6 @@ struct S2 {
   static constexpr int KC = 32;                  // K^T channels staged per round
   static constexpr int NR = HD / KC;             // rounds
   static constexpr int Row = SR * kTQ + 2;       // [voxel][ring query] table row (ints)
-  static constexpr int Ranges = 2 * SR;          // record ranges per plane: (slot, lower / upper)
 };
 constexpr int kS2Waves = 16;
 constexpr int kS2Threads = 64 * kS2Waves;
@@ -1357,7 +1358,6 @@ __global__ __launch_bounds__(kS2Threads) void dsa3d_bwd_p2s_kernel(
   static_assert(sizeof(E) == 2, "the records carry bf16 storage's fp16 (p, ds) pairs");
   constexpr int KR = ElemT<E>::kRow;
   constexpr int SR = S2<HD>::SR, KC = S2<HD>::KC, NR = S2<HD>::NR, kS2Row = S2<HD>::Row;
-  constexpr int kS2Ranges = S2<HD>::Ranges;
   static_assert(kS2Waves == 2 * SR, "two waves hold the dq tiles of each ring slot");
   __shared__ __attribute__((aligned(16))) int s_tab[kChunkNV * kS2Row];
   __shared__ __attribute__((aligned(16))) word_t<E> s_kt[KC * KR];
@@ -1366,8 +1366,9 @@ __global__ __launch_bounds__(kS2Threads) void dsa3d_bwd_p2s_kernel(
   __shared__ int s_live[SR];               // frame in each slot at this plane (pass), or -1
   __shared__ int s_new[SR];                // a frame that starts on the plane its slot's frame ends
   __shared__ int s_npass;                  // 2 when some slot has such a frame
-  __shared__ int s_rg[kS2Ranges][3];       // record range: first record, count, upper
-  __shared__ int s_pre[kS2Ranges + 1];     // range prefix sums
+  __shared__ int64_t s_rbase[SR];          // per slot: record index of the plane's record i, less i
+  __shared__ int s_rsplit[SR];             // per slot: plane records below this are upper corners
+  __shared__ int s_pre[SR + 1];            // per slot: its first plane record
   __shared__ int s_red[kS2Waves][8];
 
   const int ncpb = a.tiles_h * a.tiles_w;  // columns per sample
@@ -1526,34 +1527,36 @@ __global__ __launch_bounds__(kS2Threads) void dsa3d_bwd_p2s_kernel(
         if (threadIdx.x < SR) s_live[threadIdx.x] = s_new[threadIdx.x];
         __syncthreads();
       }
-      // ---- record ranges of the pass's frames ---------------------------------
-      if (threadIdx.x < kS2Ranges) {
-        const int r = threadIdx.x >> 1, up = threadIdx.x & 1;
-        const int t = s_live[r];
-        int first = 0, cnt = 0;
+      // ---- record ranges of the pass's frames: per slot the bins z0 = z - 1
+      // (upper corners on z) and z0 = z (lower), adjacent in the tile's records;
+      // the plane's records are numbered slot after slot
+      if (threadIdx.x < 64) {
+        const int r = threadIdx.x;
+        const int t = r < SR ? s_live[r] : -1;
+        int first = 0, cnt = 0, nup = 0;
         if (t >= 0) {
-          const int bin = z - up - s_fz[t][0];
           const int* h = rc.hdr + (trec0 + t * tstep) * kRecHdr;
-          if (bin >= 0 && bin < h[6]) {
-            first = h[8 + bin];
-            cnt = h[9 + bin] - first;
-          }
+          const int nb = h[6], bl = z - s_fz[t][0];
+          first = h[8 + min(max(bl - 1, 0), nb)];
+          nup = h[8 + min(max(bl, 0), nb)] - first;
+          cnt = h[8 + min(max(bl + 1, 0), nb)] - first;
         }
-        s_rg[threadIdx.x][0] = first;
-        s_rg[threadIdx.x][1] = cnt;
-        s_rg[threadIdx.x][2] = up;
+        int pre = cnt;  // inclusive prefix over the slots (lanes 0..SR-1)
+  #pragma unroll
+        for (int m = 1; m < SR; m <<= 1) {
+          const int o = __shfl_up(pre, m, 64);
+          if (r >= m) pre += o;
+        }
+        pre -= cnt;
+        if (r < SR) {
+          s_pre[r] = pre;
+          s_rsplit[r] = pre + nup;
+          s_rbase[r] = t >= 0 ? (trec0 + t * tstep) * K16 + first - pre : 0;
+        }
+        if (r == SR - 1) s_pre[SR] = pre + cnt;
       }
       __syncthreads();
-      if (threadIdx.x == 0) {
-        int acc = 0;
-        for (int j = 0; j < kS2Ranges; ++j) {
-          s_pre[j] = acc;
-          acc += s_rg[j][1];
-        }
-        s_pre[kS2Ranges] = acc;
-      }
-      __syncthreads();
-      const int nrec = s_pre[kS2Ranges];
+      const int nrec = s_pre[SR];
 
       for (int ci = 0; ci < nchunks; ++ci) {
         const Chunk c = make_chunk(box, ci);
@@ -1561,42 +1564,52 @@ __global__ __launch_bounds__(kS2Threads) void dsa3d_bwd_p2s_kernel(
         for (int vi = threadIdx.x; vi < c.nv; vi += kS2Threads)
           s_rows[vi] = static_cast<int>(chunk_row(a, tl, c, z, vi) - tl.sample0);
 
-        // one pass of the table: B (ds * scale * w, phase 0) or A (p * w, phase 1)
+        // one record into the table: B (ds * scale * w, phase 0) or A (p * w, phase 1)
+        auto scatter_one = [&](const u32x4_t& r, int slot, bool up, int phase) {
+          const int y0 = static_cast<int>(r[0] & 0x3fffu);
+          const int x0 = static_cast<int>((r[0] >> 14) & 0x3fffu);
+          if (nchunks > 1) {
+            const int ky = min((y0 - box.ylo) / kChunkStep, box.ncy - 1);
+            const int kx = min((x0 - box.xlo) / kChunkStep, box.ncx - 1);
+            if (ky != cyi || kx != cxi) return;
+          }
+          const int qq = static_cast<int>(r[0] >> 28);
+          const float fz = __uint_as_float(r[2]);
+          const float wz = up ? fz : 1.0f - fz;
+          const float fx = static_cast<float>(r[1] & 0xffffu) * (1.0f / 65536.0f);
+          const float fy = static_cast<float>(r[1] >> 16) * (1.0f / 65536.0f);
+          const float v = (phase == 0 ? h2_hi(r[3]) * kFixA : h2_lo(r[3]) * a.fix_a) * wz;
+          const float gx = 1.0f - fx, gy = 1.0f - fy;
+          const int base = (y0 - c.cy0) * c.nx + (x0 - c.cx0);
+          const int dy = fy != 0.0f ? c.nx : 0, dx = fx != 0.0f ? 1 : 0;
+          int* const r00 = &s_tab[base * kS2Row + kTQ * slot + qq];
+          int* const r10 = r00 + dy * kS2Row;
+          atomicAdd(r00, to_fix(v * (gy * gx)));
+          atomicAdd(r00 + dx * kS2Row, to_fix(v * (gy * fx)));
+          atomicAdd(r10, to_fix(v * (fy * gx)));
+          atomicAdd(r10 + dx * kS2Row, to_fix(v * (fy * fx)));
+        };
+        auto slot_of = [&](int i) {
+          int j = 0;
+  #pragma unroll
+          for (int k = 1; k < SR; ++k) j += i >= s_pre[k] ? 1 : 0;
+          return j;
+        };
         auto scatter = [&](int phase) {
           for (int e = threadIdx.x; e < c.nvp * kS2Row / 4; e += kS2Threads) {
             const u32x4_t zz = {0u, 0u, 0u, 0u};
             __builtin_memcpy(&s_tab[4 * e], &zz, sizeof(zz));
           }
           __syncthreads();
-          for (int i = threadIdx.x; i < nrec; i += kS2Threads) {
-            int j = 0;
-  #pragma unroll
-            for (int k = 1; k < kS2Ranges; ++k) j += i >= s_pre[k] ? 1 : 0;
-            const int slot = j >> 1, t = s_live[slot];
-            const int64_t ridx = (trec0 + t * tstep) * K16 + s_rg[j][0] + (i - s_pre[j]);
-            const u32x4_t r = rc.rec[ridx];
-            const int y0 = static_cast<int>(r[0] & 0x3fffu);
-            const int x0 = static_cast<int>((r[0] >> 14) & 0x3fffu);
-            const int qq = static_cast<int>(r[0] >> 28);
-            const float fz = __uint_as_float(r[2]);
-            const float wz = s_rg[j][2] ? fz : 1.0f - fz;
-            if (nchunks > 1) {
-              const int ky = min((y0 - box.ylo) / kChunkStep, box.ncy - 1);
-              const int kx = min((x0 - box.xlo) / kChunkStep, box.ncx - 1);
-              if (ky != cyi || kx != cxi) continue;
-            }
-            const float fx = static_cast<float>(r[1] & 0xffffu) * (1.0f / 65536.0f);
-            const float fy = static_cast<float>(r[1] >> 16) * (1.0f / 65536.0f);
-            const float v = (phase == 0 ? h2_hi(r[3]) * kFixA : h2_lo(r[3]) * a.fix_a) * wz;
-            const float gx = 1.0f - fx, gy = 1.0f - fy;
-            const int base = (y0 - c.cy0) * c.nx + (x0 - c.cx0);
-            const int dy = fy != 0.0f ? c.nx : 0, dx = fx != 0.0f ? 1 : 0;
-            int* const r00 = &s_tab[base * kS2Row + kTQ * slot + qq];
-            int* const r10 = r00 + dy * kS2Row;
-            atomicAdd(r00, to_fix(v * (gy * gx)));
-            atomicAdd(r00 + dx * kS2Row, to_fix(v * (gy * fx)));
-            atomicAdd(r10, to_fix(v * (fy * gx)));
-            atomicAdd(r10 + dx * kS2Row, to_fix(v * (fy * fx)));
+          // two records per thread and iteration, both loads issued first
+          for (int i0 = threadIdx.x; i0 < nrec; i0 += 2 * kS2Threads) {
+            const int i1 = i0 + kS2Threads;
+            const bool two = i1 < nrec;
+            const int j0 = slot_of(i0), j1 = slot_of(two ? i1 : i0);
+            const u32x4_t r0 = rc.rec[s_rbase[j0] + i0];
+            const u32x4_t r1 = rc.rec[s_rbase[j1] + (two ? i1 : i0)];
+            scatter_one(r0, j0, i0 < s_rsplit[j0], phase);
+            if (two) scatter_one(r1, j1, i1 < s_rsplit[j1], phase);
           }
         };
 
