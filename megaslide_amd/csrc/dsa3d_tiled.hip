@@ -1340,6 +1340,51 @@ __global__ __launch_bounds__(P2Tile<FR>::Threads) void dsa3d_bwd_p2_redo_kernel(
 // corner planes span nine planes, leave LDS for 16-channel rounds only: the
 // kernel then took 1.2 ms longer than the ~4% of columns it would keep from
 // the tile kernel.)
+// Fixed-point table words -> bf16 (hi, lo) pairs in place, hi = bf16(x) and
+// lo = bf16(x - hi) (the split of precise_op), word = hi | lo << 16.
+__device__ __forceinline__ u32x4_t fix_to_hilo_words(const u32x4_t& w) {
+  u32x4_t r;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const f32x2_t f = {static_cast<float>(static_cast<int>(w[2 * i])),
+                       static_cast<float>(static_cast<int>(w[2 * i + 1]))};
+    const uint32_t hb = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_t));
+    const f32x2_t back = {__uint_as_float(hb << 16), __uint_as_float(hb & 0xffff0000u)};
+    const f32x2_t rem = f - back;
+    const uint32_t lb = __builtin_bit_cast(uint32_t, __builtin_convertvector(rem, bf16x2_t));
+    r[2 * i] = (hb & 0xffffu) | (lb << 16);
+    r[2 * i + 1] = (hb >> 16) | (lb & 0xffff0000u);
+  }
+  return r;
+}
+// The (hi, lo) operands of eight such words.
+__device__ __forceinline__ PreciseOp<bf16> hilo_op(const uint32_t (&w)[8]) {
+  u32x4_t h, l;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    h[i] = (w[2 * i] & 0xffffu) | (w[2 * i + 1] << 16);
+    l[i] = (w[2 * i] >> 16) | (w[2 * i + 1] & 0xffff0000u);
+  }
+  PreciseOp<bf16> r;
+  r.hi = __builtin_bit_cast(bf16x8_t, h);
+  r.lo = __builtin_bit_cast(bf16x8_t, l);
+  return r;
+}
+// table_t_rows of a table of such words: the hi parts (bf16(x), what
+// fix_to_op gives for the fixed-point value).
+__device__ __forceinline__ bf16x8_t table_t_hi(const int* table_t, int row, int col0, int vb,
+                                               int lane) {
+  u32x4_t w0, w1, h;
+  const int* p = &table_t[(32 * vb + (lane & 31)) * row + col0 + 8 * (lane >> 5)];
+  __builtin_memcpy(&w0, p, sizeof(w0));
+  __builtin_memcpy(&w1, p + 4, sizeof(w1));
+  h[0] = (w0[0] & 0xffffu) | (w0[1] << 16);
+  h[1] = (w0[2] & 0xffffu) | (w0[3] << 16);
+  h[2] = (w1[0] & 0xffffu) | (w1[1] << 16);
+  h[3] = (w1[2] & 0xffffu) | (w1[3] << 16);
+  return __builtin_bit_cast(bf16x8_t, h);
+}
+
 template <int HD>
 struct S2 {
   static constexpr int SR = 8;                   // ring slots (live frames)
@@ -1350,6 +1395,7 @@ struct S2 {
 constexpr int kS2Waves = 16;
 constexpr int kS2Threads = 64 * kS2Waves;
 constexpr int kS2MaxT = 256;              // frames per column (LDS frame table)
+constexpr int kS2Batch = 2;               // records a thread loads at once in the table scatter
 
 template <int HD, typename E>
 __global__ __launch_bounds__(kS2Threads) void dsa3d_bwd_p2s_kernel(
@@ -1601,15 +1647,21 @@ __global__ __launch_bounds__(kS2Threads) void dsa3d_bwd_p2s_kernel(
             __builtin_memcpy(&s_tab[4 * e], &zz, sizeof(zz));
           }
           __syncthreads();
-          // two records per thread and iteration, both loads issued first
-          for (int i0 = threadIdx.x; i0 < nrec; i0 += 2 * kS2Threads) {
-            const int i1 = i0 + kS2Threads;
-            const bool two = i1 < nrec;
-            const int j0 = slot_of(i0), j1 = slot_of(two ? i1 : i0);
-            const u32x4_t r0 = rc.rec[s_rbase[j0] + i0];
-            const u32x4_t r1 = rc.rec[s_rbase[j1] + (two ? i1 : i0)];
-            scatter_one(r0, j0, i0 < s_rsplit[j0], phase);
-            if (two) scatter_one(r1, j1, i1 < s_rsplit[j1], phase);
+          // kS2Batch records per thread and iteration, their loads issued first
+          for (int i0 = threadIdx.x; i0 < nrec; i0 += kS2Batch * kS2Threads) {
+            u32x4_t r[kS2Batch];
+            int j[kS2Batch];
+  #pragma unroll
+            for (int u = 0; u < kS2Batch; ++u) {
+              const int i = i0 + u * kS2Threads < nrec ? i0 + u * kS2Threads : i0;
+              j[u] = slot_of(i);
+              r[u] = rc.rec[s_rbase[j[u]] + i];
+            }
+  #pragma unroll
+            for (int u = 0; u < kS2Batch; ++u) {
+              const int i = i0 + u * kS2Threads;
+              if (i < nrec) scatter_one(r[u], j[u], i < s_rsplit[j[u]], phase);
+            }
           }
         };
 
@@ -1617,6 +1669,14 @@ __global__ __launch_bounds__(kS2Threads) void dsa3d_bwd_p2s_kernel(
         load_stage_rows<kP2Stage, KC, E>(a, tl, c, z, kp, a.ks, hc0, kr);
         scatter(0);
         __syncthreads();
+        // B in place as bf16 (hi, lo) pairs, converted once for every dq round
+        // and wave (the round's K^T store below is in the same barrier interval)
+        for (int e = threadIdx.x; e < c.nvp * kS2Row / 4; e += kS2Threads) {
+          u32x4_t w;
+          __builtin_memcpy(&w, &s_tab[4 * e], sizeof(w));
+          w = fix_to_hilo_words(w);
+          __builtin_memcpy(&s_tab[4 * e], &w, sizeof(w));
+        }
   #pragma unroll
         for (int rd = 0; rd < NR; ++rd) {
           store_stage<kP2Stage, KC, E>(c, kr, s_kt);
@@ -1625,11 +1685,13 @@ __global__ __launch_bounds__(kS2Threads) void dsa3d_bwd_p2s_kernel(
             load_stage_rows<kP2Stage, KC, E>(a, tl, c, z, kp, a.ks, hc0 + KC * (rd + 1), kr);
           if (s_live[my_slot] >= 0) {
             for (int kc = 0; kc < c.nvp; kc += 32) {
-              float bq[8];  // fixed-point units; the query's l1 / 2^30 is applied to dq at the end
+              // fixed-point units; the query's l1 / 2^30 is applied to dq at the end
+              uint32_t bw[8];
   #pragma unroll
               for (int jj = 0; jj < 8; ++jj)
-                bq[jj] = static_cast<float>(s_tab[(kc + kq + jj) * kS2Row + kTQ * my_slot + mq]);
-              dq_acc[rd] = mma16(precise_op<E>(bq),
+                bw[jj] = static_cast<uint32_t>(
+                    s_tab[(kc + kq + jj) * kS2Row + kTQ * my_slot + mq]);
+              dq_acc[rd] = mma16(hilo_op(bw),
                                  load_op<E>(&s_kt[(16 * my_ct + mq) * KR + kc + kq]), dq_acc[rd]);
             }
           }
@@ -1646,7 +1708,7 @@ __global__ __launch_bounds__(kS2Threads) void dsa3d_bwd_p2s_kernel(
             const int t = s_live[r];
             if (t < 0) continue;
             const E* qp = qtb + (trec0 + t * tstep) * (2 * HD * kTQ) + och * kTQ + oq;
-            acc = mma32(table_t_rows<E>(s_tab, kS2Row, kTQ * r, vb, tl.lane), load_op<E>(qp), acc);
+            acc = mma32(table_t_hi(s_tab, kS2Row, kTQ * r, vb, tl.lane), load_op<E>(qp), acc);
           }
           flush_block(tl, acc, s_rows, vb, c.nv, hc0 + och, dk_acc, acc_ks);
         }
