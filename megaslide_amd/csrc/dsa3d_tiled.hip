@@ -1404,6 +1404,10 @@ __global__ __launch_bounds__(kS2Threads) void dsa3d_bwd_p2s_kernel(
   static_assert(sizeof(E) == 2, "the records carry bf16 storage's fp16 (p, ds) pairs");
   constexpr int KR = ElemT<E>::kRow;
   constexpr int SR = S2<HD>::SR, KC = S2<HD>::KC, NR = S2<HD>::NR, kS2Row = S2<HD>::Row;
+  // the live slots' transposed q (or dO), [slot][channel][16 queries], fits the K^T buffer
+  constexpr bool kQS = SR * HD * kTQ <= KC * KR;
+  constexpr int kQSThreads = SR * 2 * HD;  // 16 bytes each
+  static_assert(!kQS || kQSThreads <= kS2Threads, "one 16-byte piece per thread");
   static_assert(kS2Waves == 2 * SR, "two waves hold the dq tiles of each ring slot");
   __shared__ __attribute__((aligned(16))) int s_tab[kChunkNV * kS2Row];
   __shared__ __attribute__((aligned(16))) word_t<E> s_kt[KC * KR];
@@ -1666,6 +1670,18 @@ __global__ __launch_bounds__(kS2Threads) void dsa3d_bwd_p2s_kernel(
         };
 
         // ---- B: dq and dK -----------------------------------------------------
+        // With kQS the live slots' transposed q (then dO) wait in the K^T buffer
+        // for the dK (dV) products: each thread loads 16 bytes early and stores
+        // them once that buffer is free, so the products read LDS, not global.
+        u32x4_t qs_reg = {0u, 0u, 0u, 0u};
+        if constexpr (kQS) {
+          if (threadIdx.x < kQSThreads) {
+            const int t = s_live[threadIdx.x / (2 * HD)];
+            if (t >= 0)
+              qs_reg = reinterpret_cast<const u32x4_t*>(
+                  qtb + (trec0 + t * tstep) * (2 * HD * kTQ))[threadIdx.x % (2 * HD)];
+          }
+        }
         load_stage_rows<kP2Stage, KC, E>(a, tl, c, z, kp, a.ks, hc0, kr);
         scatter(0);
         __syncthreads();
@@ -1697,6 +1713,16 @@ __global__ __launch_bounds__(kS2Threads) void dsa3d_bwd_p2s_kernel(
           }
           __syncthreads();  // every wave is done with this round's K^T
         }
+        if constexpr (kQS) {
+          if (threadIdx.x < kQSThreads) {
+            __builtin_memcpy(&s_kt[8 * threadIdx.x], &qs_reg, sizeof(qs_reg));
+            const int t = s_live[threadIdx.x / (2 * HD)];
+            if (t >= 0)
+              qs_reg = reinterpret_cast<const u32x4_t*>(
+                  qtb + (trec0 + t * tstep) * (2 * HD * kTQ) + HD * kTQ)[threadIdx.x % (2 * HD)];
+          }
+          __syncthreads();
+        }
         // dK[v] += sum over ring queries of B[q][v] q[q] (32x32 MFMA per live slot)
         for (int task = tl.wave;; task += kS2Waves) {
           const int c2 = task % (HD / 32), vb = task / (HD / 32);
@@ -1707,15 +1733,23 @@ __global__ __launch_bounds__(kS2Threads) void dsa3d_bwd_p2s_kernel(
           for (int r = 0; r < SR; ++r) {
             const int t = s_live[r];
             if (t < 0) continue;
-            const E* qp = qtb + (trec0 + t * tstep) * (2 * HD * kTQ) + och * kTQ + oq;
-            acc = mma32(table_t_hi(s_tab, kS2Row, kTQ * r, vb, tl.lane), load_op<E>(qp), acc);
+            op_t<E> qo;
+            if constexpr (kQS)
+              qo = load_op<E>(&s_kt[(r * HD + och) * kTQ + oq]);
+            else
+              qo = load_op<E>(qtb + (trec0 + t * tstep) * (2 * HD * kTQ) + och * kTQ + oq);
+            acc = mma32(table_t_hi(s_tab, kS2Row, kTQ * r, vb, tl.lane), qo, acc);
           }
           flush_block(tl, acc, s_rows, vb, c.nv, hc0 + och, dk_acc, acc_ks);
         }
-        __syncthreads();  // every wave is done with the B table
+        __syncthreads();  // every wave is done with the B table (and the staged q)
 
         // ---- A: dV --------------------------------------------------------------
-        scatter(1);
+        if constexpr (kQS) {
+          if (threadIdx.x < kQSThreads)
+            __builtin_memcpy(&s_kt[8 * threadIdx.x], &qs_reg, sizeof(qs_reg));
+        }
+        scatter(1);  // its first barrier orders the staged dO before the products
         __syncthreads();
         for (int task = tl.wave;; task += kS2Waves) {
           const int c2 = task % (HD / 32), vb = task / (HD / 32);
@@ -1726,8 +1760,12 @@ __global__ __launch_bounds__(kS2Threads) void dsa3d_bwd_p2s_kernel(
           for (int r = 0; r < SR; ++r) {
             const int t = s_live[r];
             if (t < 0) continue;
-            const E* gp = qtb + (trec0 + t * tstep) * (2 * HD * kTQ) + (HD + och) * kTQ + oq;
-            acc = mma32(table_t_rows<E>(s_tab, kS2Row, kTQ * r, vb, tl.lane), load_op<E>(gp), acc);
+            op_t<E> go;
+            if constexpr (kQS)
+              go = load_op<E>(&s_kt[(r * HD + och) * kTQ + oq]);
+            else
+              go = load_op<E>(qtb + (trec0 + t * tstep) * (2 * HD * kTQ) + (HD + och) * kTQ + oq);
+            acc = mma32(table_t_rows<E>(s_tab, kS2Row, kTQ * r, vb, tl.lane), go, acc);
           }
           flush_block(tl, acc, s_rows, vb, c.nv, hc0 + och, dv_acc, acc_vs);
         }
