@@ -1404,13 +1404,15 @@ __global__ __launch_bounds__(kS2Threads) void dsa3d_bwd_p2s_kernel(
   static_assert(sizeof(E) == 2, "the records carry bf16 storage's fp16 (p, ds) pairs");
   constexpr int KR = ElemT<E>::kRow;
   constexpr int SR = S2<HD>::SR, KC = S2<HD>::KC, NR = S2<HD>::NR, kS2Row = S2<HD>::Row;
-  // the live slots' transposed q (or dO), [slot][channel][16 queries], fits the K^T buffer
-  constexpr bool kQS = SR * HD * kTQ <= KC * KR;
-  constexpr int kQSThreads = SR * 2 * HD;  // 16 bytes each
-  static_assert(!kQS || kQSThreads <= kS2Threads, "one 16-byte piece per thread");
+  // The live slots' transposed q (or dO), [slot][channel][16 queries], staged in
+  // the K^T buffer, which grows to hold them up to head_dim 96 (LDS 161.5 KB).
+  constexpr bool kQS = HD <= 96;
+  constexpr int kQSPieces = SR * 2 * HD;  // 16 bytes each
+  constexpr int kQSPer = (kQSPieces + kS2Threads - 1) / kS2Threads;  // pieces per thread
+  constexpr int kKtElems = kQS && SR * HD * kTQ > KC * KR ? SR * HD * kTQ : KC * KR;
   static_assert(kS2Waves == 2 * SR, "two waves hold the dq tiles of each ring slot");
   __shared__ __attribute__((aligned(16))) int s_tab[kChunkNV * kS2Row];
-  __shared__ __attribute__((aligned(16))) word_t<E> s_kt[KC * KR];
+  __shared__ __attribute__((aligned(16))) word_t<E> s_kt[kKtElems];
   __shared__ __attribute__((aligned(16))) int s_rows[kChunkNV];
   __shared__ int s_fz[kS2MaxT][2];         // per frame: zlo, zhi (zlo > zhi: never live)
   __shared__ int s_live[SR];               // frame in each slot at this plane (pass), or -1
@@ -1673,15 +1675,28 @@ __global__ __launch_bounds__(kS2Threads) void dsa3d_bwd_p2s_kernel(
         // With kQS the live slots' transposed q (then dO) wait in the K^T buffer
         // for the dK (dV) products: each thread loads 16 bytes early and stores
         // them once that buffer is free, so the products read LDS, not global.
-        u32x4_t qs_reg = {0u, 0u, 0u, 0u};
-        if constexpr (kQS) {
-          if (threadIdx.x < kQSThreads) {
-            const int t = s_live[threadIdx.x / (2 * HD)];
-            if (t >= 0)
-              qs_reg = reinterpret_cast<const u32x4_t*>(
-                  qtb + (trec0 + t * tstep) * (2 * HD * kTQ))[threadIdx.x % (2 * HD)];
+        u32x4_t qs_reg[kQSPer];
+        auto qs_load = [&](int part) {  // part 0: q, 1: dO
+  #pragma unroll
+          for (int k = 0; k < kQSPer; ++k) {
+            const int pc = static_cast<int>(threadIdx.x) + k * kS2Threads;
+            qs_reg[k] = u32x4_t{0u, 0u, 0u, 0u};
+            if (pc < kQSPieces) {
+              const int t = s_live[pc / (2 * HD)];
+              if (t >= 0)
+                qs_reg[k] = reinterpret_cast<const u32x4_t*>(
+                    qtb + (trec0 + t * tstep) * (2 * HD * kTQ) + part * HD * kTQ)[pc % (2 * HD)];
+            }
           }
-        }
+        };
+        auto qs_store = [&]() {
+  #pragma unroll
+          for (int k = 0; k < kQSPer; ++k) {
+            const int pc = static_cast<int>(threadIdx.x) + k * kS2Threads;
+            if (pc < kQSPieces) __builtin_memcpy(&s_kt[8 * pc], &qs_reg[k], sizeof(qs_reg[k]));
+          }
+        };
+        if constexpr (kQS) qs_load(0);
         load_stage_rows<kP2Stage, KC, E>(a, tl, c, z, kp, a.ks, hc0, kr);
         scatter(0);
         __syncthreads();
@@ -1714,13 +1729,8 @@ __global__ __launch_bounds__(kS2Threads) void dsa3d_bwd_p2s_kernel(
           __syncthreads();  // every wave is done with this round's K^T
         }
         if constexpr (kQS) {
-          if (threadIdx.x < kQSThreads) {
-            __builtin_memcpy(&s_kt[8 * threadIdx.x], &qs_reg, sizeof(qs_reg));
-            const int t = s_live[threadIdx.x / (2 * HD)];
-            if (t >= 0)
-              qs_reg = reinterpret_cast<const u32x4_t*>(
-                  qtb + (trec0 + t * tstep) * (2 * HD * kTQ) + HD * kTQ)[threadIdx.x % (2 * HD)];
-          }
+          qs_store();
+          qs_load(1);
           __syncthreads();
         }
         // dK[v] += sum over ring queries of B[q][v] q[q] (32x32 MFMA per live slot)
@@ -1745,10 +1755,7 @@ __global__ __launch_bounds__(kS2Threads) void dsa3d_bwd_p2s_kernel(
         __syncthreads();  // every wave is done with the B table (and the staged q)
 
         // ---- A: dV --------------------------------------------------------------
-        if constexpr (kQS) {
-          if (threadIdx.x < kQSThreads)
-            __builtin_memcpy(&s_kt[8 * threadIdx.x], &qs_reg, sizeof(qs_reg));
-        }
+        if constexpr (kQS) qs_store();
         scatter(1);  // its first barrier orders the staged dO before the products
         __syncthreads();
         for (int task = tl.wave;; task += kS2Waves) {
