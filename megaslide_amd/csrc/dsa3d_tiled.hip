@@ -1405,11 +1405,13 @@ __global__ __launch_bounds__(kS2Threads) void dsa3d_bwd_p2s_kernel(
   constexpr int KR = ElemT<E>::kRow;
   constexpr int SR = S2<HD>::SR, KC = S2<HD>::KC, NR = S2<HD>::NR, kS2Row = S2<HD>::Row;
   // The live slots' transposed q (or dO), [slot][channel][16 queries], staged in
-  // the K^T buffer, which grows to hold them up to head_dim 96 (LDS 161.5 KB).
-  constexpr bool kQS = HD <= 96;
-  constexpr int kQSPieces = SR * 2 * HD;  // 16 bytes each
+  // the K^T buffer in parts of QC channels: the whole head up to head_dim 96
+  // (the buffer grows to 24 KB, LDS 161.5 KB), two 64-channel parts at 128.
+  constexpr int QC = HD <= 96 ? HD : 64, NQ = HD / QC;
+  constexpr int kQSPieces = SR * 2 * QC;  // 16 bytes each
   constexpr int kQSPer = (kQSPieces + kS2Threads - 1) / kS2Threads;  // pieces per thread
-  constexpr int kKtElems = kQS && SR * HD * kTQ > KC * KR ? SR * HD * kTQ : KC * KR;
+  constexpr int kKtElems = SR * QC * kTQ > KC * KR ? SR * QC * kTQ : KC * KR;
+  static_assert(QC * NQ == HD && QC % 32 == 0, "channel parts of whole 32-channel tiles");
   static_assert(kS2Waves == 2 * SR, "two waves hold the dq tiles of each ring slot");
   __shared__ __attribute__((aligned(16))) int s_tab[kChunkNV * kS2Row];
   __shared__ __attribute__((aligned(16))) word_t<E> s_kt[kKtElems];
@@ -1672,20 +1674,22 @@ __global__ __launch_bounds__(kS2Threads) void dsa3d_bwd_p2s_kernel(
         };
 
         // ---- B: dq and dK -----------------------------------------------------
-        // With kQS the live slots' transposed q (then dO) wait in the K^T buffer
-        // for the dK (dV) products: each thread loads 16 bytes early and stores
-        // them once that buffer is free, so the products read LDS, not global.
+        // The live slots' transposed q (then dO) wait in the K^T buffer for the
+        // dK (dV) products, one channel part at a time: each thread loads its
+        // 16-byte pieces a phase early and stores them once that buffer is free,
+        // so the products read LDS instead of waiting on global loads.
         u32x4_t qs_reg[kQSPer];
-        auto qs_load = [&](int part) {  // part 0: q, 1: dO
+        auto qs_load = [&](int part, int qp) {  // part 0: q, 1: dO; channel part qp
   #pragma unroll
           for (int k = 0; k < kQSPer; ++k) {
             const int pc = static_cast<int>(threadIdx.x) + k * kS2Threads;
             qs_reg[k] = u32x4_t{0u, 0u, 0u, 0u};
             if (pc < kQSPieces) {
-              const int t = s_live[pc / (2 * HD)];
+              const int t = s_live[pc / (2 * QC)];
               if (t >= 0)
                 qs_reg[k] = reinterpret_cast<const u32x4_t*>(
-                    qtb + (trec0 + t * tstep) * (2 * HD * kTQ) + part * HD * kTQ)[pc % (2 * HD)];
+                    qtb + (trec0 + t * tstep) * (2 * HD * kTQ) + (part * HD + qp * QC) * kTQ)
+                    [pc % (2 * QC)];
             }
           }
         };
@@ -1696,7 +1700,27 @@ __global__ __launch_bounds__(kS2Threads) void dsa3d_bwd_p2s_kernel(
             if (pc < kQSPieces) __builtin_memcpy(&s_kt[8 * pc], &qs_reg[k], sizeof(qs_reg[k]));
           }
         };
-        if constexpr (kQS) qs_load(0);
+        // products of one channel part over the live slots, flushed per task
+        auto products = [&](int qp, bool dv) {
+          constexpr int C2 = QC / 32;
+          for (int task = tl.wave;; task += kS2Waves) {
+            const int c2 = task % C2, vb = task / C2;
+            if (vb * 32 >= c.nv) break;
+            const int lch = 32 * c2 + (tl.lane & 31), och = qp * QC + lch;
+            f32x16_t acc = {};
+  #pragma unroll
+            for (int r = 0; r < SR; ++r) {
+              if (s_live[r] < 0) continue;
+              const op_t<E> qo = load_op<E>(&s_kt[(r * QC + lch) * kTQ + oq]);
+              acc = mma32(dv ? table_t_rows<E>(s_tab, kS2Row, kTQ * r, vb, tl.lane)
+                             : table_t_hi(s_tab, kS2Row, kTQ * r, vb, tl.lane),
+                          qo, acc);
+            }
+            flush_block(tl, acc, s_rows, vb, c.nv, hc0 + och, dv ? dv_acc : dk_acc,
+                        dv ? acc_vs : acc_ks);
+          }
+        };
+        qs_load(0, 0);
         load_stage_rows<kP2Stage, KC, E>(a, tl, c, z, kp, a.ks, hc0, kr);
         scatter(0);
         __syncthreads();
@@ -1728,53 +1752,33 @@ __global__ __launch_bounds__(kS2Threads) void dsa3d_bwd_p2s_kernel(
           }
           __syncthreads();  // every wave is done with this round's K^T
         }
-        if constexpr (kQS) {
-          qs_store();
-          qs_load(1);
-          __syncthreads();
-        }
         // dK[v] += sum over ring queries of B[q][v] q[q] (32x32 MFMA per live slot)
-        for (int task = tl.wave;; task += kS2Waves) {
-          const int c2 = task % (HD / 32), vb = task / (HD / 32);
-          if (vb * 32 >= c.nv) break;
-          const int och = 32 * c2 + (tl.lane & 31);
-          f32x16_t acc = {};
   #pragma unroll
-          for (int r = 0; r < SR; ++r) {
-            const int t = s_live[r];
-            if (t < 0) continue;
-            op_t<E> qo;
-            if constexpr (kQS)
-              qo = load_op<E>(&s_kt[(r * HD + och) * kTQ + oq]);
-            else
-              qo = load_op<E>(qtb + (trec0 + t * tstep) * (2 * HD * kTQ) + och * kTQ + oq);
-            acc = mma32(table_t_hi(s_tab, kS2Row, kTQ * r, vb, tl.lane), qo, acc);
-          }
-          flush_block(tl, acc, s_rows, vb, c.nv, hc0 + och, dk_acc, acc_ks);
+        for (int qp = 0; qp < NQ; ++qp) {
+          if (qp > 0) __syncthreads();  // every wave is done with the previous part
+          qs_store();
+          if (qp + 1 < NQ)
+            qs_load(0, qp + 1);
+          else
+            qs_load(1, 0);
+          __syncthreads();
+          products(qp, false);
         }
         __syncthreads();  // every wave is done with the B table (and the staged q)
 
         // ---- A: dV --------------------------------------------------------------
-        if constexpr (kQS) qs_store();
+        qs_store();
+        if (NQ > 1) qs_load(1, 1);
         scatter(1);  // its first barrier orders the staged dO before the products
         __syncthreads();
-        for (int task = tl.wave;; task += kS2Waves) {
-          const int c2 = task % (HD / 32), vb = task / (HD / 32);
-          if (vb * 32 >= c.nv) break;
-          const int och = 32 * c2 + (tl.lane & 31);
-          f32x16_t acc = {};
   #pragma unroll
-          for (int r = 0; r < SR; ++r) {
-            const int t = s_live[r];
-            if (t < 0) continue;
-            op_t<E> go;
-            if constexpr (kQS)
-              go = load_op<E>(&s_kt[(r * HD + och) * kTQ + oq]);
-            else
-              go = load_op<E>(qtb + (trec0 + t * tstep) * (2 * HD * kTQ) + (HD + och) * kTQ + oq);
-            acc = mma32(table_t_rows<E>(s_tab, kS2Row, kTQ * r, vb, tl.lane), go, acc);
+        for (int qp = 0; qp < NQ; ++qp) {
+          if (qp > 0) {
+            __syncthreads();  // every wave is done with the previous part
+            qs_store();
+            __syncthreads();
           }
-          flush_block(tl, acc, s_rows, vb, c.nv, hc0 + och, dv_acc, acc_vs);
+          products(qp, true);
         }
         __syncthreads();  // the table and s_rows are rewritten by the next step
       }
