@@ -735,7 +735,10 @@ __global__ __launch_bounds__(kThreads, (p1_min_waves<HD, E>())) void dsa3d_bwd_p
   if constexpr (REC) {
     const int64_t trec = static_cast<int64_t>(tl.head) * rc.tiles +
                          rec_tile(a, tl.b, tl.t0, tl.h0 / kTileH, tl.w0 / kTileW);
-    if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) rc.collist[0] = 0;
+    // the column list's count and, after the list, the 8 work counters of the
+    // column-streaming kernel
+    if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x < 9)
+      rc.collist[threadIdx.x == 0 ? 0 : a.nh * a.B * a.tiles_h * a.tiles_w + threadIdx.x] = 0;
     const int nb = box.zhi < box.zlo ? 0 : box.zhi - box.zlo + 1;
     if (sub == 0) s_dl[tid / kSubs][0] = l1q;  // this query's l1 (delta was read above)
 #pragma unroll
@@ -1417,6 +1420,8 @@ __global__ __launch_bounds__(kS2Threads) void dsa3d_bwd_p2s_kernel(
   __shared__ __attribute__((aligned(16))) word_t<E> s_kt[kKtElems];
   __shared__ __attribute__((aligned(16))) int s_rows[kChunkNV];
   __shared__ int s_fz[kS2MaxT][2];         // per frame: zlo, zhi (zlo > zhi: never live)
+  __shared__ int s_rlo[SR], s_rhi[SR];     // per ring slot: its earliest and latest live frame
+  __shared__ int s_unit;                   // the unit a workgroup takes next
   __shared__ int s_live[SR];               // frame in each slot at this plane (pass), or -1
   __shared__ int s_new[SR];                // a frame that starts on the plane its slot's frame ends
   __shared__ int s_npass;                  // 2 when some slot has such a frame
@@ -1427,115 +1432,26 @@ __global__ __launch_bounds__(kS2Threads) void dsa3d_bwd_p2s_kernel(
 
   const int ncpb = a.tiles_h * a.tiles_w;  // columns per sample
   const int ncol = a.B * ncpb;
-  int col = static_cast<int>(blockIdx.x);
-  // columns of one XCD are contiguous (they share K rows in its L2)
-  if (ncol % 8 == 0) col = (col & 7) * (ncol / 8) + (col >> 3);
-  const int b = col / ncpb, th = (col % ncpb) / a.tiles_w, tw = col % a.tiles_w;
+  // Work units are (head, pair of columns 2j and 2j + 1 of a row), taken by a
+  // persistent grid of one workgroup per CU from 8 counters, one per XCD's
+  // contiguous range of units (neighbouring columns share K rows in its L2);
+  // a workgroup whose range is done helps the next ranges.  (Fixed grids where
+  // some workgroups return at once, e.g. one per column where a pair takes one
+  // walk, left CUs idle.)
+  const int tw2 = (a.tiles_w + 1) / 2;
+  const int npr = a.B * a.tiles_h * tw2;  // pairs per head
+  const int nunits = npr * a.nh;
+  const int per = (nunits + 7) / 8;
+  int* const work = rc.collist + 1 + a.nh * ncol;
+  const int64_t tstep = ncpb;  // tiles between consecutive frames of a column
+  const int K16 = a.K * kTQ;
+  const int D = a.nh * HD;
+  const E* const kp = static_cast<const E*>(a.k);
+  const E* const qtb = static_cast<const E*>(rc.qt);
   Tile tl;
-  tl.head = a.head0 + static_cast<int>(blockIdx.y);
-  tl.b = b;
-  tl.sample0 = static_cast<int64_t>(b) * a.N;
   tl.wave = threadIdx.x >> 6;
   tl.lane = threadIdx.x & 63;
   tl.t0 = tl.t = 0;
-  tl.h0 = th * kTileH;
-  tl.w0 = tw * kTileW;
-  const int64_t trec0 = static_cast<int64_t>(tl.head) * rc.tiles + rec_tile(a, b, 0, th, tw);
-  const int64_t tstep = ncpb;  // tiles between consecutive frames of the column
-  const int K16 = a.K * kTQ;
-
-  // ---- the column's frames: plane ranges, corner box, ring check -----------
-  int zlo = 1 << 30, zhi = -1, ylo = 1 << 30, yhi = -1, xlo = 1 << 30, xhi = -1, bad = 0;
-  if (a.T > kS2MaxT) bad = 1;
-  for (int t = threadIdx.x; t < a.T && t < kS2MaxT; t += kS2Threads) {
-    const int* h = rc.hdr + (trec0 + t * tstep) * kRecHdr;
-    const int nb = h[6];
-    if (nb < 0) bad = 1;
-    if (nb > 0) {
-      s_fz[t][0] = h[0];
-      s_fz[t][1] = h[1];
-      zlo = min(zlo, h[0]);
-      zhi = max(zhi, h[1]);
-      ylo = min(ylo, h[2]);
-      yhi = max(yhi, h[3]);
-      xlo = min(xlo, h[4]);
-      xhi = max(xhi, h[5]);
-    } else {
-      s_fz[t][0] = 1;
-      s_fz[t][1] = 0;
-    }
-  }
-  __syncthreads();
-  // the next frame of a slot starts after the previous one ends, or on its
-  // last plane (that plane then takes a second pass for the new frames) and
-  // goes on beyond it
-  for (int t = threadIdx.x; t < a.T && t < kS2MaxT; t += kS2Threads) {
-    if (s_fz[t][0] > s_fz[t][1]) continue;
-    for (int u = t + SR; u < a.T && u < kS2MaxT; u += SR) {
-      if (s_fz[u][0] > s_fz[u][1]) continue;
-      if (s_fz[u][0] < s_fz[t][1] || (s_fz[u][0] == s_fz[t][1] && s_fz[u][1] == s_fz[u][0]))
-        bad = 1;
-      break;
-    }
-  }
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) {
-    zlo = min(zlo, __shfl_xor(zlo, m));
-    zhi = max(zhi, __shfl_xor(zhi, m));
-    ylo = min(ylo, __shfl_xor(ylo, m));
-    yhi = max(yhi, __shfl_xor(yhi, m));
-    xlo = min(xlo, __shfl_xor(xlo, m));
-    xhi = max(xhi, __shfl_xor(xhi, m));
-    bad = max(bad, __shfl_xor(bad, m));
-  }
-  if (tl.lane == 0) {
-    s_red[tl.wave][0] = zlo;
-    s_red[tl.wave][1] = zhi;
-    s_red[tl.wave][2] = ylo;
-    s_red[tl.wave][3] = yhi;
-    s_red[tl.wave][4] = xlo;
-    s_red[tl.wave][5] = xhi;
-    s_red[tl.wave][6] = bad;
-  }
-  __syncthreads();
-  Box box;
-  box.zlo = s_red[0][0];
-  box.zhi = s_red[0][1];
-  box.ylo = s_red[0][2];
-  box.yhi = s_red[0][3];
-  box.xlo = s_red[0][4];
-  box.xhi = s_red[0][5];
-  bad = s_red[0][6];
-#pragma unroll
-  for (int w = 1; w < kS2Waves; ++w) {
-    box.zlo = min(box.zlo, s_red[w][0]);
-    box.zhi = max(box.zhi, s_red[w][1]);
-    box.ylo = min(box.ylo, s_red[w][2]);
-    box.yhi = max(box.yhi, s_red[w][3]);
-    box.xlo = min(box.xlo, s_red[w][4]);
-    box.xhi = max(box.xhi, s_red[w][5]);
-    bad = max(bad, s_red[w][6]);
-  }
-  box.zlo = __builtin_amdgcn_readfirstlane(box.zlo);
-  box.zhi = __builtin_amdgcn_readfirstlane(box.zhi);
-  box.ylo = __builtin_amdgcn_readfirstlane(box.ylo);
-  box.yhi = __builtin_amdgcn_readfirstlane(box.yhi);
-  box.xlo = __builtin_amdgcn_readfirstlane(box.xlo);
-  box.xhi = __builtin_amdgcn_readfirstlane(box.xhi);
-  bad = __builtin_amdgcn_readfirstlane(bad);
-  if (bad) {
-    if (threadIdx.x == 0) rc.collist[1 + atomicAdd(&rc.collist[0], 1)] = tl.head * ncol + col;
-    return;
-  }
-  if (box.zhi < box.zlo) return;  // no tap at all
-  box.ncy = max(1, (box.yhi - box.ylo + kChunkStep - 1) / kChunkStep);
-  box.ncx = max(1, (box.xhi - box.xlo + kChunkStep - 1) / kChunkStep);
-  const int nchunks = box.ncy * box.ncx;
-
-  const int D = a.nh * HD;
-  const int hc0 = tl.head * HD;
-  const E* const kp = static_cast<const E*>(a.k);
-  const E* const qtb = static_cast<const E*>(rc.qt);
   const int mq = tl.lane & 15, kq = 8 * (tl.lane >> 4), oq = 8 * (tl.lane >> 5);
   // dq tiles of this wave: slot wave / 2, channels 32 rd + 16 (wave % 2) + [0, 16)
   const int my_slot = tl.wave >> 1, my_ct = tl.wave & 1;
@@ -1543,265 +1459,459 @@ __global__ __launch_bounds__(kS2Threads) void dsa3d_bwd_p2s_kernel(
 #pragma unroll
   for (int rd = 0; rd < NR; ++rd) dq_acc[rd] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
   StageRows<kP2Stage, KC, E> kr;
+  // the current unit
+  int b = 0, th = 0, twp = 0, nside = 1, hc0 = 0;
+  int64_t trl = 0;  // record tile of frame 0 of the pair's left column
 
-  for (int z = box.zlo; z <= box.zhi; ++z) {
-    // ---- live frames of this plane: per slot the earlier frame, and a later
-    // one that starts here while the earlier one ends here --------------------
-    __syncthreads();  // the previous plane's dq write-out has read s_live
-    if (threadIdx.x < SR) {
-      s_live[threadIdx.x] = 0x7fffffff;
-      s_new[threadIdx.x] = -1;
-    }
-    __syncthreads();
-    for (int t = threadIdx.x; t < a.T; t += kS2Threads) {
-      if (s_fz[t][0] <= z && z <= s_fz[t][1]) {
-        atomicMin(&s_live[t % SR], t);
-        atomicMax(&s_new[t % SR], t);
+  // A walk takes either both columns together (wide: ring slot t % (SR / 2)
+  // of frame t holds the left tile in table slot 2 (t % (SR / 2)) and the
+  // right one in the next) or one column (ring slot = table slot = t % SR).
+  bool wide = false;
+  int side = 0;  // the column of a one-column walk
+  // column (0 left, 1 right) of table slot v, and the record tile of frame t there
+  auto side_of = [&](int v) { return wide ? (v & 1) : side; };
+  auto tile_of = [&](int v, int t) {
+    return trl + side_of(v) + static_cast<int64_t>(t) * tstep;
+  };
+
+  // ---- a walk's frames: plane ranges (s_fz), corner box, ring check ---------
+  // Returns the box; bad = the walk cannot take these frames; cost = its
+  // chunk steps (chunks x (planes + planes a ring slot shares, which take a
+  // second pass)).
+  auto setup = [&](Box& box, int& bad, int& cost) {
+    const int rs = wide ? SR / 2 : SR;
+    int zlo = 1 << 30, zhi = -1, ylo = 1 << 30, yhi = -1, xlo = 1 << 30, xhi = -1, nsh = 0;
+    bad = a.T > kS2MaxT ? 1 : 0;
+    __syncthreads();  // a previous walk has read s_fz
+    for (int t = threadIdx.x; t < a.T && t < kS2MaxT; t += kS2Threads) {
+      int flo = 1 << 30, fhi = -1;
+      for (int sd = wide ? 0 : side; sd <= (wide ? 1 : side); ++sd) {
+        const int* h = rc.hdr + (trl + sd + static_cast<int64_t>(t) * tstep) * kRecHdr;
+        const int nb = h[6];
+        if (nb < 0) bad = 1;
+        if (nb > 0) {
+          flo = min(flo, h[0]);
+          fhi = max(fhi, h[1]);
+          ylo = min(ylo, h[2]);
+          yhi = max(yhi, h[3]);
+          xlo = min(xlo, h[4]);
+          xhi = max(xhi, h[5]);
+        }
+      }
+      if (fhi >= flo) {
+        s_fz[t][0] = flo;
+        s_fz[t][1] = fhi;
+        zlo = min(zlo, flo);
+        zhi = max(zhi, fhi);
+      } else {
+        s_fz[t][0] = 1;
+        s_fz[t][1] = 0;
       }
     }
     __syncthreads();
-    if (threadIdx.x < 64) {
-      const int r = threadIdx.x;
-      bool two = false;
-      if (r < SR) {
-        const int lo = s_live[r], hi = s_new[r];
-        two = hi >= 0 && hi != lo;
-        s_live[r] = lo == 0x7fffffff ? -1 : lo;
-        s_new[r] = two ? hi : -1;
+    // the next frame of a ring slot starts after the previous one ends, or on
+    // its last plane (that plane then takes a second pass for the new frames)
+    // and goes on beyond it
+    for (int t = threadIdx.x; t < a.T && t < kS2MaxT; t += kS2Threads) {
+      if (s_fz[t][0] > s_fz[t][1]) continue;
+      for (int u = t + rs; u < a.T && u < kS2MaxT; u += rs) {
+        if (s_fz[u][0] > s_fz[u][1]) continue;
+        if (s_fz[u][0] < s_fz[t][1] || (s_fz[u][0] == s_fz[t][1] && s_fz[u][1] == s_fz[u][0]))
+          bad = 1;
+        else if (s_fz[u][0] == s_fz[t][1])
+          ++nsh;
+        break;
       }
-      const bool any = __builtin_amdgcn_ballot_w64(two) != 0;
-      if (r == 0) s_npass = any ? 2 : 1;
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+      zlo = min(zlo, __shfl_xor(zlo, m));
+      zhi = max(zhi, __shfl_xor(zhi, m));
+      ylo = min(ylo, __shfl_xor(ylo, m));
+      yhi = max(yhi, __shfl_xor(yhi, m));
+      xlo = min(xlo, __shfl_xor(xlo, m));
+      xhi = max(xhi, __shfl_xor(xhi, m));
+      bad = max(bad, __shfl_xor(bad, m));
+      nsh += __shfl_xor(nsh, m);
+    }
+    if (tl.lane == 0) {
+      s_red[tl.wave][0] = zlo;
+      s_red[tl.wave][1] = zhi;
+      s_red[tl.wave][2] = ylo;
+      s_red[tl.wave][3] = yhi;
+      s_red[tl.wave][4] = xlo;
+      s_red[tl.wave][5] = xhi;
+      s_red[tl.wave][6] = bad;
+      s_red[tl.wave][7] = nsh;
     }
     __syncthreads();
-    const int npass = s_npass;
-    for (int pass = 0; pass < npass; ++pass) {
-      if (pass == 1) {
-        // the frames that start on this plane, alone (the others are done)
-        __syncthreads();  // the first pass's dq write-out has read s_live
-        if (threadIdx.x < SR) s_live[threadIdx.x] = s_new[threadIdx.x];
-        __syncthreads();
-      }
-      // ---- record ranges of the pass's frames: per slot the bins z0 = z - 1
-      // (upper corners on z) and z0 = z (lower), adjacent in the tile's records;
-      // the plane's records are numbered slot after slot
-      if (threadIdx.x < 64) {
-        const int r = threadIdx.x;
-        const int t = r < SR ? s_live[r] : -1;
-        int first = 0, cnt = 0, nup = 0;
-        if (t >= 0) {
-          const int* h = rc.hdr + (trec0 + t * tstep) * kRecHdr;
-          const int nb = h[6], bl = z - s_fz[t][0];
-          first = h[8 + min(max(bl - 1, 0), nb)];
-          nup = h[8 + min(max(bl, 0), nb)] - first;
-          cnt = h[8 + min(max(bl + 1, 0), nb)] - first;
-        }
-        int pre = cnt;  // inclusive prefix over the slots (lanes 0..SR-1)
-  #pragma unroll
-        for (int m = 1; m < SR; m <<= 1) {
-          const int o = __shfl_up(pre, m, 64);
-          if (r >= m) pre += o;
-        }
-        pre -= cnt;
-        if (r < SR) {
-          s_pre[r] = pre;
-          s_rsplit[r] = pre + nup;
-          s_rbase[r] = t >= 0 ? (trec0 + t * tstep) * K16 + first - pre : 0;
-        }
-        if (r == SR - 1) s_pre[SR] = pre + cnt;
+    nsh = s_red[0][7];
+    box.zlo = s_red[0][0];
+    box.zhi = s_red[0][1];
+    box.ylo = s_red[0][2];
+    box.yhi = s_red[0][3];
+    box.xlo = s_red[0][4];
+    box.xhi = s_red[0][5];
+    bad = s_red[0][6];
+#pragma unroll
+    for (int w = 1; w < kS2Waves; ++w) {
+      box.zlo = min(box.zlo, s_red[w][0]);
+      box.zhi = max(box.zhi, s_red[w][1]);
+      box.ylo = min(box.ylo, s_red[w][2]);
+      box.yhi = max(box.yhi, s_red[w][3]);
+      box.xlo = min(box.xlo, s_red[w][4]);
+      box.xhi = max(box.xhi, s_red[w][5]);
+      bad = max(bad, s_red[w][6]);
+      nsh += s_red[w][7];
+    }
+    box.zlo = __builtin_amdgcn_readfirstlane(box.zlo);
+    box.zhi = __builtin_amdgcn_readfirstlane(box.zhi);
+    box.ylo = __builtin_amdgcn_readfirstlane(box.ylo);
+    box.yhi = __builtin_amdgcn_readfirstlane(box.yhi);
+    box.xlo = __builtin_amdgcn_readfirstlane(box.xlo);
+    box.xhi = __builtin_amdgcn_readfirstlane(box.xhi);
+    bad = __builtin_amdgcn_readfirstlane(bad);
+    box.ncy = max(1, (box.yhi - box.ylo + kChunkStep - 1) / kChunkStep);
+    box.ncx = max(1, (box.xhi - box.xlo + kChunkStep - 1) / kChunkStep);
+    cost = __builtin_amdgcn_readfirstlane(
+        box.zhi < box.zlo ? 0 : box.ncy * box.ncx * (box.zhi - box.zlo + 1 + nsh));
+  };
+
+  // ---- the plane walk ------------------------------------------------------
+  auto walk = [&](const Box& box) {
+    const int rs = wide ? SR / 2 : SR;
+    const int nchunks = box.ncy * box.ncx;
+    for (int z = box.zlo; z <= box.zhi; ++z) {
+      // ---- live frames of this plane: per ring slot the earlier frame, and a
+      // later one that starts here while the earlier one ends here -------------
+      __syncthreads();  // the previous plane's dq write-out has read s_live
+      if (threadIdx.x < SR) {
+        s_rlo[threadIdx.x] = 0x7fffffff;
+        s_rhi[threadIdx.x] = -1;
       }
       __syncthreads();
-      const int nrec = s_pre[SR];
-
-      for (int ci = 0; ci < nchunks; ++ci) {
-        const Chunk c = make_chunk(box, ci);
-        const int cyi = box.ncx == 1 ? 0 : ci / box.ncx, cxi = ci - cyi * box.ncx;
-        for (int vi = threadIdx.x; vi < c.nv; vi += kS2Threads)
-          s_rows[vi] = static_cast<int>(chunk_row(a, tl, c, z, vi) - tl.sample0);
-
-        // one record into the table: B (ds * scale * w, phase 0) or A (p * w, phase 1)
-        auto scatter_one = [&](const u32x4_t& r, int slot, bool up, int phase) {
-          const int y0 = static_cast<int>(r[0] & 0x3fffu);
-          const int x0 = static_cast<int>((r[0] >> 14) & 0x3fffu);
-          if (nchunks > 1) {
-            const int ky = min((y0 - box.ylo) / kChunkStep, box.ncy - 1);
-            const int kx = min((x0 - box.xlo) / kChunkStep, box.ncx - 1);
-            if (ky != cyi || kx != cxi) return;
-          }
-          const int qq = static_cast<int>(r[0] >> 28);
-          const float fz = __uint_as_float(r[2]);
-          const float wz = up ? fz : 1.0f - fz;
-          const float fx = static_cast<float>(r[1] & 0xffffu) * (1.0f / 65536.0f);
-          const float fy = static_cast<float>(r[1] >> 16) * (1.0f / 65536.0f);
-          const float v = (phase == 0 ? h2_hi(r[3]) * kFixA : h2_lo(r[3]) * a.fix_a) * wz;
-          const float gx = 1.0f - fx, gy = 1.0f - fy;
-          const int base = (y0 - c.cy0) * c.nx + (x0 - c.cx0);
-          const int dy = fy != 0.0f ? c.nx : 0, dx = fx != 0.0f ? 1 : 0;
-          int* const r00 = &s_tab[base * kS2Row + kTQ * slot + qq];
-          int* const r10 = r00 + dy * kS2Row;
-          atomicAdd(r00, to_fix(v * (gy * gx)));
-          atomicAdd(r00 + dx * kS2Row, to_fix(v * (gy * fx)));
-          atomicAdd(r10, to_fix(v * (fy * gx)));
-          atomicAdd(r10 + dx * kS2Row, to_fix(v * (fy * fx)));
-        };
-        auto slot_of = [&](int i) {
-          int j = 0;
-  #pragma unroll
-          for (int k = 1; k < SR; ++k) j += i >= s_pre[k] ? 1 : 0;
-          return j;
-        };
-        auto scatter = [&](int phase) {
-          for (int e = threadIdx.x; e < c.nvp * kS2Row / 4; e += kS2Threads) {
-            const u32x4_t zz = {0u, 0u, 0u, 0u};
-            __builtin_memcpy(&s_tab[4 * e], &zz, sizeof(zz));
-          }
+      for (int t = threadIdx.x; t < a.T; t += kS2Threads) {
+        if (s_fz[t][0] <= z && z <= s_fz[t][1]) {
+          atomicMin(&s_rlo[t % rs], t);
+          atomicMax(&s_rhi[t % rs], t);
+        }
+      }
+      __syncthreads();
+      if (threadIdx.x < 64) {
+        const int r = threadIdx.x;
+        bool two = false;
+        if (r < SR) {
+          const int q = wide ? r >> 1 : r;
+          const int lo = s_rlo[q], hi = s_rhi[q];
+          two = hi >= 0 && hi != lo;
+          s_live[r] = lo == 0x7fffffff ? -1 : lo;
+          s_new[r] = two ? hi : -1;
+        }
+        const bool any = __builtin_amdgcn_ballot_w64(two) != 0;
+        if (r == 0) s_npass = any ? 2 : 1;
+      }
+      __syncthreads();
+      const int npass = s_npass;
+      for (int pass = 0; pass < npass; ++pass) {
+        if (pass == 1) {
+          // the frames that start on this plane, alone (the others are done)
+          __syncthreads();  // the first pass's dq write-out has read s_live
+          if (threadIdx.x < SR) s_live[threadIdx.x] = s_new[threadIdx.x];
           __syncthreads();
-          // kS2Batch records per thread and iteration, their loads issued first
-          for (int i0 = threadIdx.x; i0 < nrec; i0 += kS2Batch * kS2Threads) {
-            u32x4_t r[kS2Batch];
-            int j[kS2Batch];
-  #pragma unroll
-            for (int u = 0; u < kS2Batch; ++u) {
-              const int i = i0 + u * kS2Threads < nrec ? i0 + u * kS2Threads : i0;
-              j[u] = slot_of(i);
-              r[u] = rc.rec[s_rbase[j[u]] + i];
-            }
-  #pragma unroll
-            for (int u = 0; u < kS2Batch; ++u) {
-              const int i = i0 + u * kS2Threads;
-              if (i < nrec) scatter_one(r[u], j[u], i < s_rsplit[j[u]], phase);
-            }
+        }
+        // ---- record ranges of the pass's frames: per slot the bins z0 = z - 1
+        // (upper corners on z) and z0 = z (lower), adjacent in the tile's
+        // records; the plane's records are numbered slot after slot
+        if (threadIdx.x < 64) {
+          const int r = threadIdx.x;
+          const int t = r < SR ? s_live[r] : -1;
+          int first = 0, cnt = 0, nup = 0;
+          int64_t tb = 0;
+          if (t >= 0) {
+            tb = tile_of(r, t);
+            const int* h = rc.hdr + tb * kRecHdr;
+            const int nb = max(h[6], 0), bl = z - h[0];
+            first = h[8 + min(max(bl - 1, 0), nb)];
+            nup = h[8 + min(max(bl, 0), nb)] - first;
+            cnt = h[8 + min(max(bl + 1, 0), nb)] - first;
           }
-        };
-
-        // ---- B: dq and dK -----------------------------------------------------
-        // The live slots' transposed q (then dO) wait in the K^T buffer for the
-        // dK (dV) products, one channel part at a time: each thread loads its
-        // 16-byte pieces a phase early and stores them once that buffer is free,
-        // so the products read LDS instead of waiting on global loads.
-        u32x4_t qs_reg[kQSPer];
-        auto qs_load = [&](int part, int qp) {  // part 0: q, 1: dO; channel part qp
+          int pre = cnt;  // inclusive prefix over the slots (lanes 0..SR-1)
   #pragma unroll
-          for (int k = 0; k < kQSPer; ++k) {
-            const int pc = static_cast<int>(threadIdx.x) + k * kS2Threads;
-            qs_reg[k] = u32x4_t{0u, 0u, 0u, 0u};
-            if (pc < kQSPieces) {
-              const int t = s_live[pc / (2 * QC)];
-              if (t >= 0)
-                qs_reg[k] = reinterpret_cast<const u32x4_t*>(
-                    qtb + (trec0 + t * tstep) * (2 * HD * kTQ) + (part * HD + qp * QC) * kTQ)
-                    [pc % (2 * QC)];
-            }
+          for (int m = 1; m < SR; m <<= 1) {
+            const int o = __shfl_up(pre, m, 64);
+            if (r >= m) pre += o;
           }
-        };
-        auto qs_store = [&]() {
-  #pragma unroll
-          for (int k = 0; k < kQSPer; ++k) {
-            const int pc = static_cast<int>(threadIdx.x) + k * kS2Threads;
-            if (pc < kQSPieces) __builtin_memcpy(&s_kt[8 * pc], &qs_reg[k], sizeof(qs_reg[k]));
+          pre -= cnt;
+          if (r < SR) {
+            s_pre[r] = pre;
+            s_rsplit[r] = pre + nup;
+            s_rbase[r] = t >= 0 ? tb * K16 + first - pre : 0;
           }
-        };
-        // products of one channel part over the live slots, flushed per task
-        auto products = [&](int qp, bool dv) {
-          constexpr int C2 = QC / 32;
-          for (int task = tl.wave;; task += kS2Waves) {
-            const int c2 = task % C2, vb = task / C2;
-            if (vb * 32 >= c.nv) break;
-            const int lch = 32 * c2 + (tl.lane & 31), och = qp * QC + lch;
-            f32x16_t acc = {};
-  #pragma unroll
-            for (int r = 0; r < SR; ++r) {
-              if (s_live[r] < 0) continue;
-              const op_t<E> qo = load_op<E>(&s_kt[(r * QC + lch) * kTQ + oq]);
-              acc = mma32(dv ? table_t_rows<E>(s_tab, kS2Row, kTQ * r, vb, tl.lane)
-                             : table_t_hi(s_tab, kS2Row, kTQ * r, vb, tl.lane),
-                          qo, acc);
-            }
-            flush_block(tl, acc, s_rows, vb, c.nv, hc0 + och, dv ? dv_acc : dk_acc,
-                        dv ? acc_vs : acc_ks);
-          }
-        };
-        qs_load(0, 0);
-        load_stage_rows<kP2Stage, KC, E>(a, tl, c, z, kp, a.ks, hc0, kr);
-        scatter(0);
+          if (r == SR - 1) s_pre[SR] = pre + cnt;
+        }
         __syncthreads();
-        // B in place as bf16 (hi, lo) pairs, converted once for every dq round
-        // and wave (the round's K^T store below is in the same barrier interval)
-        for (int e = threadIdx.x; e < c.nvp * kS2Row / 4; e += kS2Threads) {
-          u32x4_t w;
-          __builtin_memcpy(&w, &s_tab[4 * e], sizeof(w));
-          w = fix_to_hilo_words(w);
-          __builtin_memcpy(&s_tab[4 * e], &w, sizeof(w));
-        }
-  #pragma unroll
-        for (int rd = 0; rd < NR; ++rd) {
-          store_stage<kP2Stage, KC, E>(c, kr, s_kt);
-          __syncthreads();
-          if (rd + 1 < NR)
-            load_stage_rows<kP2Stage, KC, E>(a, tl, c, z, kp, a.ks, hc0 + KC * (rd + 1), kr);
-          if (s_live[my_slot] >= 0) {
-            for (int kc = 0; kc < c.nvp; kc += 32) {
-              // fixed-point units; the query's l1 / 2^30 is applied to dq at the end
-              uint32_t bw[8];
-  #pragma unroll
-              for (int jj = 0; jj < 8; ++jj)
-                bw[jj] = static_cast<uint32_t>(
-                    s_tab[(kc + kq + jj) * kS2Row + kTQ * my_slot + mq]);
-              dq_acc[rd] = mma16(hilo_op(bw),
-                                 load_op<E>(&s_kt[(16 * my_ct + mq) * KR + kc + kq]), dq_acc[rd]);
-            }
-          }
-          __syncthreads();  // every wave is done with this round's K^T
-        }
-        // dK[v] += sum over ring queries of B[q][v] q[q] (32x32 MFMA per live slot)
-  #pragma unroll
-        for (int qp = 0; qp < NQ; ++qp) {
-          if (qp > 0) __syncthreads();  // every wave is done with the previous part
-          qs_store();
-          if (qp + 1 < NQ)
-            qs_load(0, qp + 1);
-          else
-            qs_load(1, 0);
-          __syncthreads();
-          products(qp, false);
-        }
-        __syncthreads();  // every wave is done with the B table (and the staged q)
+        const int nrec = s_pre[SR];
 
-        // ---- A: dV --------------------------------------------------------------
-        qs_store();
-        if (NQ > 1) qs_load(1, 1);
-        scatter(1);  // its first barrier orders the staged dO before the products
-        __syncthreads();
-  #pragma unroll
-        for (int qp = 0; qp < NQ; ++qp) {
-          if (qp > 0) {
-            __syncthreads();  // every wave is done with the previous part
-            qs_store();
+        for (int ci = 0; ci < nchunks; ++ci) {
+          const Chunk c = make_chunk(box, ci);
+          const int cyi = box.ncx == 1 ? 0 : ci / box.ncx, cxi = ci - cyi * box.ncx;
+          for (int vi = threadIdx.x; vi < c.nv; vi += kS2Threads)
+            s_rows[vi] = static_cast<int>(chunk_row(a, tl, c, z, vi) - tl.sample0);
+
+          // one record into the table: B (ds * scale * w, phase 0) or A (p * w, phase 1)
+          auto scatter_one = [&](const u32x4_t& r, int slot, bool up, int phase) {
+            const int y0 = static_cast<int>(r[0] & 0x3fffu);
+            const int x0 = static_cast<int>((r[0] >> 14) & 0x3fffu);
+            if (nchunks > 1) {
+              const int ky = min((y0 - box.ylo) / kChunkStep, box.ncy - 1);
+              const int kx = min((x0 - box.xlo) / kChunkStep, box.ncx - 1);
+              if (ky != cyi || kx != cxi) return;
+            }
+            const int qq = static_cast<int>(r[0] >> 28);
+            const float fz = __uint_as_float(r[2]);
+            const float wz = up ? fz : 1.0f - fz;
+            const float fx = static_cast<float>(r[1] & 0xffffu) * (1.0f / 65536.0f);
+            const float fy = static_cast<float>(r[1] >> 16) * (1.0f / 65536.0f);
+            const float v = (phase == 0 ? h2_hi(r[3]) * kFixA : h2_lo(r[3]) * a.fix_a) * wz;
+            const float gx = 1.0f - fx, gy = 1.0f - fy;
+            const int base = (y0 - c.cy0) * c.nx + (x0 - c.cx0);
+            const int dy = fy != 0.0f ? c.nx : 0, dx = fx != 0.0f ? 1 : 0;
+            int* const r00 = &s_tab[base * kS2Row + kTQ * slot + qq];
+            int* const r10 = r00 + dy * kS2Row;
+            atomicAdd(r00, to_fix(v * (gy * gx)));
+            atomicAdd(r00 + dx * kS2Row, to_fix(v * (gy * fx)));
+            atomicAdd(r10, to_fix(v * (fy * gx)));
+            atomicAdd(r10 + dx * kS2Row, to_fix(v * (fy * fx)));
+          };
+          auto slot_of = [&](int i) {
+            int j = 0;
+    #pragma unroll
+            for (int k = 1; k < SR; ++k) j += i >= s_pre[k] ? 1 : 0;
+            return j;
+          };
+          auto scatter = [&](int phase) {
+            for (int e = threadIdx.x; e < c.nvp * kS2Row / 4; e += kS2Threads) {
+              const u32x4_t zz = {0u, 0u, 0u, 0u};
+              __builtin_memcpy(&s_tab[4 * e], &zz, sizeof(zz));
+            }
             __syncthreads();
-          }
-          products(qp, true);
-        }
-        __syncthreads();  // the table and s_rows are rewritten by the next step
-      }
-
-      // ---- frames that end at this plane: their dq ---------------------------
-      const int tr = s_live[my_slot];
-      if (tr >= 0 && s_fz[tr][1] == z) {
-  #pragma unroll
-        for (int rd = 0; rd < NR; ++rd) {
-  #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int m = 4 * (tl.lane >> 4) + i;
-            const int h = tl.h0 + m / kTileW, w = tl.w0 + m % kTileW;
-            if (h < a.H && w < a.W) {
-              const int64_t n = tl.sample0 + (static_cast<int64_t>(tr) * a.H + h) * a.W + w;
-              const int ch = hc0 + KC * rd + 16 * my_ct + mq;
-              dq[n * a.qs + ch] = from_f32<E>(dq_acc[rd][i] * l1_ws[n * a.nh + tl.head] * kFixAInv);
+            // kS2Batch records per thread and iteration, their loads issued first
+            for (int i0 = threadIdx.x; i0 < nrec; i0 += kS2Batch * kS2Threads) {
+              u32x4_t r[kS2Batch];
+              int j[kS2Batch];
+    #pragma unroll
+              for (int u = 0; u < kS2Batch; ++u) {
+                const int i = i0 + u * kS2Threads < nrec ? i0 + u * kS2Threads : i0;
+                j[u] = slot_of(i);
+                r[u] = rc.rec[s_rbase[j[u]] + i];
+              }
+    #pragma unroll
+              for (int u = 0; u < kS2Batch; ++u) {
+                const int i = i0 + u * kS2Threads;
+                if (i < nrec) scatter_one(r[u], j[u], i < s_rsplit[j[u]], phase);
+              }
             }
+          };
+
+          // ---- B: dq and dK -----------------------------------------------------
+          // The live slots' transposed q (then dO) wait in the K^T buffer for the
+          // dK (dV) products, one channel part at a time: each thread loads its
+          // 16-byte pieces a phase early and stores them once that buffer is free,
+          // so the products read LDS instead of waiting on global loads.
+          u32x4_t qs_reg[kQSPer];
+          auto qs_load = [&](int part, int qp) {  // part 0: q, 1: dO; channel part qp
+    #pragma unroll
+            for (int k = 0; k < kQSPer; ++k) {
+              const int pc = static_cast<int>(threadIdx.x) + k * kS2Threads;
+              qs_reg[k] = u32x4_t{0u, 0u, 0u, 0u};
+              if (pc < kQSPieces) {
+                const int v = pc / (2 * QC), t = s_live[v];
+                if (t >= 0)
+                  qs_reg[k] = reinterpret_cast<const u32x4_t*>(
+                      qtb + tile_of(v, t) * (2 * HD * kTQ) + (part * HD + qp * QC) * kTQ)
+                      [pc % (2 * QC)];
+              }
+            }
+          };
+          auto qs_store = [&]() {
+    #pragma unroll
+            for (int k = 0; k < kQSPer; ++k) {
+              const int pc = static_cast<int>(threadIdx.x) + k * kS2Threads;
+              if (pc < kQSPieces) __builtin_memcpy(&s_kt[8 * pc], &qs_reg[k], sizeof(qs_reg[k]));
+            }
+          };
+          // products of one channel part over the live slots, flushed per task
+          auto products = [&](int qp, bool dv) {
+            constexpr int C2 = QC / 32;
+            for (int task = tl.wave;; task += kS2Waves) {
+              const int c2 = task % C2, vb = task / C2;
+              if (vb * 32 >= c.nv) break;
+              const int lch = 32 * c2 + (tl.lane & 31), och = qp * QC + lch;
+              f32x16_t acc = {};
+    #pragma unroll
+              for (int r = 0; r < SR; ++r) {
+                if (s_live[r] < 0) continue;
+                const op_t<E> qo = load_op<E>(&s_kt[(r * QC + lch) * kTQ + oq]);
+                acc = mma32(dv ? table_t_rows<E>(s_tab, kS2Row, kTQ * r, vb, tl.lane)
+                               : table_t_hi(s_tab, kS2Row, kTQ * r, vb, tl.lane),
+                            qo, acc);
+              }
+              flush_block(tl, acc, s_rows, vb, c.nv, hc0 + och, dv ? dv_acc : dk_acc,
+                          dv ? acc_vs : acc_ks);
+            }
+          };
+          qs_load(0, 0);
+          load_stage_rows<kP2Stage, KC, E>(a, tl, c, z, kp, a.ks, hc0, kr);
+          scatter(0);
+          __syncthreads();
+          // B in place as bf16 (hi, lo) pairs, converted once for every dq round
+          // and wave (the round's K^T store below is in the same barrier interval)
+          for (int e = threadIdx.x; e < c.nvp * kS2Row / 4; e += kS2Threads) {
+            u32x4_t w;
+            __builtin_memcpy(&w, &s_tab[4 * e], sizeof(w));
+            w = fix_to_hilo_words(w);
+            __builtin_memcpy(&s_tab[4 * e], &w, sizeof(w));
           }
-          dq_acc[rd] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    #pragma unroll
+          for (int rd = 0; rd < NR; ++rd) {
+            store_stage<kP2Stage, KC, E>(c, kr, s_kt);
+            __syncthreads();
+            if (rd + 1 < NR)
+              load_stage_rows<kP2Stage, KC, E>(a, tl, c, z, kp, a.ks, hc0 + KC * (rd + 1), kr);
+            if (s_live[my_slot] >= 0) {
+              for (int kc = 0; kc < c.nvp; kc += 32) {
+                // fixed-point units; the query's l1 / 2^30 is applied to dq at the end
+                uint32_t bw[8];
+    #pragma unroll
+                for (int jj = 0; jj < 8; ++jj)
+                  bw[jj] = static_cast<uint32_t>(
+                      s_tab[(kc + kq + jj) * kS2Row + kTQ * my_slot + mq]);
+                dq_acc[rd] = mma16(hilo_op(bw),
+                                   load_op<E>(&s_kt[(16 * my_ct + mq) * KR + kc + kq]), dq_acc[rd]);
+              }
+            }
+            __syncthreads();  // every wave is done with this round's K^T
+          }
+          // dK[v] += sum over ring queries of B[q][v] q[q] (32x32 MFMA per live slot)
+    #pragma unroll
+          for (int qp = 0; qp < NQ; ++qp) {
+            if (qp > 0) __syncthreads();  // every wave is done with the previous part
+            qs_store();
+            if (qp + 1 < NQ)
+              qs_load(0, qp + 1);
+            else
+              qs_load(1, 0);
+            __syncthreads();
+            products(qp, false);
+          }
+          __syncthreads();  // every wave is done with the B table (and the staged q)
+
+          // ---- A: dV --------------------------------------------------------------
+          qs_store();
+          if (NQ > 1) qs_load(1, 1);
+          scatter(1);  // its first barrier orders the staged dO before the products
+          __syncthreads();
+    #pragma unroll
+          for (int qp = 0; qp < NQ; ++qp) {
+            if (qp > 0) {
+              __syncthreads();  // every wave is done with the previous part
+              qs_store();
+              __syncthreads();
+            }
+            products(qp, true);
+          }
+          __syncthreads();  // the table and s_rows are rewritten by the next step
+        }
+
+
+        // ---- frames that end at this plane: their dq -------------------------
+        const int tr = s_live[my_slot];
+        if (tr >= 0 && s_fz[tr][1] == z) {
+          const int w0 = tl.w0 + side_of(my_slot) * kTileW;
+  #pragma unroll
+          for (int rd = 0; rd < NR; ++rd) {
+  #pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int m = 4 * (tl.lane >> 4) + i;
+              const int h = tl.h0 + m / kTileW, w = w0 + m % kTileW;
+              if (h < a.H && w < a.W) {
+                const int64_t n = tl.sample0 + (static_cast<int64_t>(tr) * a.H + h) * a.W + w;
+                const int ch = hc0 + KC * rd + 16 * my_ct + mq;
+                dq[n * a.qs + ch] =
+                    from_f32<E>(dq_acc[rd][i] * l1_ws[n * a.nh + tl.head] * kFixAInv);
+              }
+            }
+            dq_acc[rd] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+          }
+        }
+      }  // passes
+    }
+  };
+
+  // Per unit: both columns of the pair in one walk (wide) where the ring takes
+  // their frames and that walk is cheaper than one walk per column (where
+  // frames span more planes than half the ring, the wide walk's shared planes
+  // double its steps, and a wider box can add a chunk), else one walk per
+  // column; a column that its one-column walk cannot take is left to the tile
+  // kernel.
+  constexpr int kNoWalk = 1 << 30;
+#pragma nounroll
+  for (int xq = 0; xq < 8; ++xq) {
+    const int q = (static_cast<int>(blockIdx.x) + xq) & 7;
+    const int ulo = q * per, uhi = min(ulo + per, nunits);
+#pragma nounroll
+    for (;;) {
+      __syncthreads();  // every wave is done with the previous unit and s_unit
+      if (threadIdx.x == 0) s_unit = ulo + atomicAdd(&work[q], 1);
+      __syncthreads();
+      const int u = s_unit;
+      if (u >= uhi) break;
+      const int hl = u / npr, pr = u % npr;
+      b = pr / (a.tiles_h * tw2);
+      th = (pr % (a.tiles_h * tw2)) / tw2;
+      twp = pr % tw2;
+      nside = 2 * twp + 1 < a.tiles_w ? 2 : 1;
+      tl.head = a.head0 + hl;
+      tl.b = b;
+      tl.sample0 = static_cast<int64_t>(b) * a.N;
+      tl.h0 = th * kTileH;
+      tl.w0 = 2 * twp * kTileW;
+      hc0 = tl.head * HD;
+      trl = static_cast<int64_t>(tl.head) * rc.tiles + rec_tile(a, b, 0, th, 2 * twp);
+
+      bool go_wide = false;
+      if (nside == 2) {
+        Box box;
+        int bad, cw, c0 = 0, c1 = 0;
+        wide = true;
+        setup(box, bad, cw);
+        if (!bad) {
+          wide = false;
+#pragma nounroll
+          for (side = 0; side < 2; ++side) {
+            int cs;
+            setup(box, bad, cs);
+            (side == 0 ? c0 : c1) = bad ? kNoWalk : cs;
+          }
+          go_wide = cw < c0 + c1 || c0 == kNoWalk || c1 == kNoWalk;
         }
       }
-    }  // passes
+#pragma nounroll
+      for (int job = go_wide ? 0 : 1; job <= (go_wide ? 0 : nside); ++job) {
+        wide = job == 0;
+        side = job == 2 ? 1 : 0;
+        Box box;
+        int bad, cost;
+        setup(box, bad, cost);
+        if (bad) {
+          if (threadIdx.x == 0)
+            rc.collist[1 + atomicAdd(&rc.collist[0], 1)] =
+                tl.head * ncol + (b * a.tiles_h + th) * a.tiles_w + 2 * twp + side;
+          continue;
+        }
+        if (box.zhi >= box.zlo) walk(box);
+      }
+    }
   }
 }
 
@@ -2388,6 +2498,22 @@ struct BwdBufs {
   RecArgs rec;     // column-streaming kernel's records (rec.rec null: not used)
 };
 
+// CUs of the current device (the column-streaming kernel's persistent grid),
+// cached per device; 256 (MI355X) if the query fails.
+int device_cus() {
+  static int cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    cached[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) ==
+                              hipSuccess && n > 0
+                      ? n
+                      : 256;
+  }
+  return cached[dev];
+}
+
 template <int HD, typename E>
 void launch_bwd_pair(const msd_dsa3d_desc& d, const void* q, const void* k, const void* v,
                      const void* off, const void* ek, const void* ev, const E* o, const E* go,
@@ -2414,10 +2540,10 @@ void launch_bwd_pair(const msd_dsa3d_desc& d, const void* q, const void* k, cons
       hipLaunchKernelGGL((dsa3d_bwd_p1_kernel<HD, E, 4, true>), g1, dim3(tiled::kThreads), 0, s,
                          a1, o, go, lse, dlse, goff, p_ws, b_ws, dk_acc, dv_acc, acc_ks, acc_vs,
                          w.rec);
-      const dim3 gs(static_cast<unsigned>(d.B * a1.tiles_h * a1.tiles_w), d.num_heads);
-      hipLaunchKernelGGL((dsa3d_bwd_p2s_kernel<HD, E>), gs, dim3(kS2Threads), 0, s, a1, w.rec,
-                         b_ws, gq, static_cast<float*>(dk_acc), static_cast<float*>(dv_acc),
-                         acc_ks, acc_vs);
+      // persistent: one workgroup per CU (each takes a CU's LDS)
+      hipLaunchKernelGGL((dsa3d_bwd_p2s_kernel<HD, E>), dim3(device_cus()), dim3(kS2Threads), 0,
+                         s, a1, w.rec, b_ws, gq, static_cast<float*>(dk_acc),
+                         static_cast<float*>(dv_acc), acc_ks, acc_vs);
       hipLaunchKernelGGL((dsa3d_bwd_p2_list_kernel<HD, CW, E, FR>), dim3(256, 1, HD / CW),
                          dim3(P2Tile<FR>::Threads), 0, s, a2, go, p_ws, b_ws, gq, dk_acc, dv_acc,
                          acc_ks, acc_vs, w.rec.collist);
@@ -2567,7 +2693,7 @@ TiledWs tiled_ws(const msd_dsa3d_desc& d) {
     w.hdr = up(w.rec + tiles * K * tiled::kTQ * 16);
     w.qt = up(w.hdr + tiles * tiled::kRecHdr * 4);
     w.collist = up(w.qt + tiles * 2 * d.head_dim * tiled::kTQ * e);
-    w.bytes = w.collist + (cols + 1) * 4;
+    w.bytes = w.collist + (cols + 1 + 8) * 4;  // count, list, 8 work counters
   }
   return w;
 }

@@ -111,14 +111,15 @@ def test_workspace_size_and_check():
     records = 256 * 8 * 4
     # bf16 with fp32 dK/dV accumulation also holds the column-streaming
     # kernel's tap records (16 bytes per tap), 32-int headers and transposed
-    # q/dO (bf16) of every (head, one-frame tile) and a list of one int per
-    # (head, 4x4 column) after its count; T=4, H=5, W=6: 4 frames x 2 x 2 tiles
+    # q/dO (bf16) of every (head, one-frame tile), a list of one int per
+    # (head, 4x4 column) after its count, and 8 work counters; T=4, H=5, W=6:
+    # 4 frames x 2 x 2 tiles
     tiles, cols = 2 * 4 * 2 * 2 * 2, 2 * 2 * 2 * 2
     up = lambda x: (x + 255) // 256 * 256  # noqa: E731
     stream = up(2 * rows * 128 * 4 + taps + rows * 2 * 4 + records + 32)
     stream = up(stream + tiles * 147 * 16 * 16)
     stream = up(stream + tiles * 32 * 4)
-    stream = up(stream + tiles * 2 * 64 * 16 * 2) + (cols + 1) * 4
+    stream = up(stream + tiles * 2 * 64 * 16 * 2) + (cols + 1 + 8) * 4
     for dtype, accum, want in ((0, 0, max(2 * rows * 128 * 4, 2 * taps)),
                                (1, 1, 2 * rows * 128 * 4 + taps + rows * 2 * 4 + records + 32),
                                (1, 0, stream)):

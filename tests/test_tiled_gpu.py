@@ -208,3 +208,52 @@ def test_tiled_tap_shifted_offsets(hd, dtype):
         print(f"  {name}: vs oracle {e_ref:.2e}  vs direct {e_dir:.2e}", flush=True)
         assert e_ref < tol, name
         assert e_dir < tol, name
+
+
+# Shapes where the column-streaming dq/dK/dV kernel (bf16, fp32 dK/dV sums) walks
+# both columns of a pair at once: frames reach few planes (window depth 1, or
+# small offsets) and the pair's box takes no more chunks than one column's, so
+# one walk of four 32-query ring slots costs less than two of eight 16-query
+# slots.  Odd column counts leave a last column to walk alone.
+@pytest.mark.parametrize("shape", [
+    # B, T, H, W, nh, kernel, off_std, scale, head_dim
+    (1, 8, 8, 16, 2, (1, 7, 7), 0.3, 1.0, 64),    # frames reach 2 planes
+    (1, 10, 8, 20, 1, (3, 5, 5), 0.2, 0.9, 96),   # 5 columns; frames share planes
+    (2, 7, 5, 12, 2, (3, 5, 5), 0.4, 1.1, 128),   # 3 columns, B = 2, partial tiles
+    (1, 9, 12, 8, 2, (2, 3, 3), 0.6, 1.0, 32),
+])
+def test_tiled_column_pairs_vs_oracle_and_direct(shape):
+    B, T, H, W, nh, ks, off_std, scale, hd = shape
+    print(f"[tiled column pairs] {shape}", flush=True)
+    q, k, v, off = _inputs(B, T, H, W, nh, ks, off_std, 700 + T * H * W + hd, hd=hd)
+    g = torch.Generator().manual_seed(19)
+    dout = torch.randn(q.shape, generator=g).to(torch.bfloat16)
+    qq, kk, vv, oo = (t.float().requires_grad_(True) for t in (q, k, v, off))
+    ref = dsa3d_core_ref(qq, kk, vv, oo, (T, H, W), nh, ks, scale)
+    ref.backward(dout.float())
+    grads = {}
+    for algo in ("tiled", "direct"):
+        ts = [t.to(DEV).requires_grad_(True) for t in (q, k, v, off)]
+        out = core()(*ts, (T, H, W), nh, ks, scale, algo=algo)
+        out.backward(dout.to(DEV))
+        grads[algo] = [t.grad.float().cpu() for t in ts]
+    torch.cuda.synchronize()
+    for name, r, gt, gd in zip(("dq", "dk", "dv", "doff"), (qq.grad, kk.grad, vv.grad, oo.grad),
+                               grads["tiled"], grads["direct"]):
+        e_ref, e_dir = rel_err(gt, r), rel_err(gt, gd)
+        print(f"  {name}: vs oracle {e_ref:.2e}  vs direct {e_dir:.2e}", flush=True)
+        assert e_ref < BF16_TOL, name
+        assert e_dir < BF16_TOL, name
+
+
+# Shapes where the column-streaming kernel leaves columns to the tile kernel:
+# offsets large enough that a tile's taps span more planes than its record
+# header has bins, or that a frame starts before its ring slot's previous
+# frame ends.
+@pytest.mark.parametrize("shape", [
+    # B, T, H, W, nh, kernel, off_std, scale, head_dim
+    (1, 20, 8, 8, 1, (3, 5, 5), 6.0, 1.0, 64),
+    (1, 14, 8, 12, 2, (3, 7, 7), 2.0, 0.8, 96),
+])
+def test_tiled_listed_columns_vs_oracle_and_direct(shape):
+    test_tiled_column_pairs_vs_oracle_and_direct(shape)
