@@ -1321,23 +1321,26 @@ __global__ __launch_bounds__(P2Tile<FR>::Threads) void dsa3d_bwd_p2_redo_kernel(
 }
 
 // Column-streaming dq/dK/dV kernel (bf16 storage, fp32 dK/dV accumulation).
-// One workgroup walks one 4x4 (h, w) column of one head through every plane
-// of the column's corner box.  At plane z, the frames whose tiles have
-// corners on z are live; each holds the 16 table columns of a ring slot
-// (frame t in slot t % SR), and its taps with a corner on z come from the
-// first kernel's records (bins z0 = z: lower corners, z0 = z - 1: upper).  Per
-// plane and 16x16 chunk of the column's box, the [voxel][ring query] table of
-// B = ds * scale * w gives dq += B K (K^T staged in 32-channel rounds) and
-// dK = B^T q; the table of A = p * w then gives dV = A^T dO.  dK and dV are
-// added with fp32 atomics once per plane and column: tiles of FR frames flush
-// each plane of their box once per tile, and a voxel lies in the boxes of
-// about three consecutive tiles of its column (the window spans ~7 planes),
-// so the atomics, executed past the L2 and the bound of that kernel, drop to
-// about 40% (the frames of a column share every flush).  A frame that starts
-// on the last plane of its slot's previous frame takes a second pass over that
-// plane; columns where a frame starts earlier than that (more than SR frames
-// live at once), whose taps span more planes than a tile header has bins, or
-// with more than kS2MaxT frames are listed and left to the tile kernel.
+// A walk takes a 4x4 (h, w) column of one head (or both columns of a pair of
+// neighbouring columns at once) through every plane of its corner box.  At
+// plane z, the frames whose tiles have corners on z are live; each holds the 16
+// table columns of a table slot (one column: frame t in slot t % SR; a pair:
+// ring slot t % (SR / 2), table slots for the left and the right tile), and its
+// taps with a corner on z come from the first kernel's records (bins z0 = z:
+// lower corners, z0 = z - 1: upper).  Per plane and 16x16 chunk of the box,
+// the [voxel][ring query] table of B = ds * scale * w gives dq += B K (K^T
+// staged in 32-channel rounds) and dK = B^T q; the table of A = p * w then
+// gives dV = A^T dO.  dK and dV are added with fp32 atomics once per plane and
+// walk: tiles of FR frames flush each plane of their box once per tile, and a
+// voxel lies in the boxes of about three consecutive tiles of its column (the
+// window spans ~7 planes), so the atomics, executed past the L2 and the bound
+// of that kernel, drop to about 40% (the frames of a column share every
+// flush); a pair walk halves them again where boxes are much wider than a
+// column.  A frame that starts on the last plane of its ring slot's previous
+// frame takes a second pass over that plane; a column whose frames start
+// earlier than that (more frames live than ring slots), whose taps span more
+// planes than a tile header has bins, or with more than kS2MaxT frames is
+// listed and left to the tile kernel.
 // Ring and K^T staging: eight slots and 32-channel K^T rounds.  (Nine slots,
 // which would take every column at the long-clip shape, where a few frames'
 // corner planes span nine planes, leave LDS for 16-channel rounds only: the
