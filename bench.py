@@ -52,7 +52,8 @@ none is recorded for the workload; `cpu_baseline` is the float32 CPU oracle
 
 --copy-calibration first runs a plain 512 MiB -> 512 MiB bf16 copy (torch.neg)
 twice, so a counter run of this script also measures the copy the counters
-are scaled by.
+are scaled by, then a read-only pass over the same 512 MiB (torch.amax) as a
+second FETCH_SIZE point.
 """
 
 from __future__ import annotations
@@ -191,10 +192,16 @@ COPY_BYTES = 512 * 2 ** 20  # read and written once each by the calibration copy
 
 
 def copy_calibration(dev):
+    """A plain 512 MiB -> 512 MiB copy (torch.neg), twice, which the traffic
+    counters are scaled by, then a read-only pass over the same 512 MiB
+    (torch.amax, a reduction writing one value) as a second FETCH_SIZE point."""
     src = torch.ones(COPY_BYTES // 2, dtype=torch.bfloat16, device=dev)
     dst = torch.empty_like(src)
     for _ in range(2):
         torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    for _ in range(2):
+        torch.amax(src)
     torch.cuda.synchronize()
     del src, dst
 
@@ -710,7 +717,15 @@ def summarize(workload, trace_dir, fetch_dir, write_dir):
     kib = COPY_BYTES / 1024.0
     sf, sw = copy_f[0] / kib, copy_w[0] / kib  # counter KiB per true KiB
     print(f"\ncalibration copy {COPY_BYTES >> 20} MiB -> {COPY_BYTES >> 20} MiB: "
-          f"FETCH_SIZE {copy_f[0]:.0f} KiB (x{sf:.3f}), WRITE_SIZE {copy_w[0]:.0f} KiB (x{sw:.3f})\n")
+          f"FETCH_SIZE {copy_f[0]:.0f} KiB (x{sf:.3f}), WRITE_SIZE {copy_w[0]:.0f} KiB (x{sw:.3f})")
+    # the read-only pass over the same 512 MiB (the largest reduction), a
+    # second point for the FETCH_SIZE scale
+    ro = [v for _, n, v in fetch if "reduce_kernel" in n]
+    sf_ro = max(ro) / kib if ro else None
+    if sf_ro is not None:
+        print(f"read-only pass over {COPY_BYTES >> 20} MiB: FETCH_SIZE {max(ro):.0f} KiB "
+              f"(x{sf_ro:.3f}; the copy's factor over it: {sf / sf_ro:.3f})")
+    print()
     ab = kernel_bytes(cfg, e)
     rec = {}
     print("| phase (kernels) | FETCH KiB | WRITE KiB | traffic (scaled) | algorithmic | traffic / algorithmic |")
@@ -724,6 +739,8 @@ def summarize(workload, trace_dir, fetch_dir, write_dir):
         rec[phase] = {"kernels": names, "bytes_per_launch": int(traffic),
                       "fetch_kib": round(f_kib, 1), "write_kib": round(w_kib, 1),
                       "fetch_scale": round(sf, 4), "write_scale": round(sw, 4)}
+        if sf_ro is not None:
+            rec[phase]["fetch_scale_read_only"] = round(sf_ro, 4)
         print(f"| {phase} ({', '.join(names)}) | {f_kib:.0f} | {w_kib:.0f} | {traffic / 1e9:.3f} GB | "
               f"{ab[phase] / 1e9:.3f} GB | {traffic / ab[phase]:.2f} |")
     print("\nPer kernel (counter KiB, unscaled):\n\n| dispatch | kernel | FETCH | WRITE |\n|---|---|---|---|")
