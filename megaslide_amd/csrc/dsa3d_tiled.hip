@@ -41,9 +41,15 @@ constexpr bool fwd_half_v() {
   return !XK && ((sizeof(E) == 2 && HD == 128) || (sizeof(E) == 4 && HD == 64));
 }
 
+// bf16 V^T chunks take the swizzled (bank-conflict-free) layout.
+template <typename E>
+constexpr int fwd_vt_row() {
+  return sizeof(E) == 2 ? kVRowSwz : ElemT<E>::kRow;
+}
+
 template <int HD, typename E, bool XK = false>
 constexpr int fwd_vt_bytes() {
-  return (fwd_half_v<HD, E, XK>() ? HD / 2 : HD) * ElemT<E>::kRow *
+  return (fwd_half_v<HD, E, XK>() ? HD / 2 : HD) * fwd_vt_row<E>() *
          static_cast<int>(sizeof(word_t<E>));
 }
 
@@ -80,7 +86,7 @@ template <int HD, typename E, bool XK>
 __global__ __launch_bounds__(kThreads, (fwd_min_waves<HD, E, XK>())) void dsa3d_fwd_tiled_kernel(
     Args a, E* __restrict__ out, float* __restrict__ lse) {
   constexpr int NB = fwd_table_bufs<HD, E, XK>();
-  constexpr int VR = ElemT<E>::kRow;
+  constexpr int VR = fwd_vt_row<E>();
   constexpr bool kHV = fwd_half_v<HD, E, XK>();  // V^T in two 64-channel rounds
   constexpr int VC = kHV ? HD / 2 : HD;           // V^T channels staged at once
   __shared__ __attribute__((aligned(16))) float s_tab[NB][kTQ * kSRow];  // S, then A
@@ -227,6 +233,9 @@ __global__ __launch_bounds__(kThreads, (fwd_min_waves<HD, E, XK>())) void dsa3d_
   constexpr int TPW = CT / CG, KP = HD == 96 ? 1 : kWaves / CG;
   static_assert(TPW * CG == CT && CG * KP <= kWaves, "channel tiles split over the waves");
   const int mq = tl.lane & 15, kq = 8 * (tl.lane >> 4);
+  // bf16 V^T chunks are stored swizzled (row 16 t + mq: channel bits 2, 3 = those of mq)
+  constexpr bool kSwz = sizeof(E) == 2;
+  const int sw = kSwz ? vt_swz(mq) : 0;
   const int cg = tl.wave / KP, kph = tl.wave % KP;
   const bool av_wave = tl.wave < CG * KP;
   f32x4_t oacc[TPW];
@@ -278,7 +287,7 @@ __global__ __launch_bounds__(kThreads, (fwd_min_waves<HD, E, XK>())) void dsa3d_
       int* const s_atab = reinterpret_cast<int*>(s_tab[it % NB]);
       int* row = &s_atab[tl.q * kSRow];
       __syncthreads();  // the previous step's MFMAs are done with V^T; this buffer is zeroed
-      store_stage<kThreads, VC, E>(c, vh, s_vt);
+      store_stage<kThreads, VC, E, kSwz>(c, vh, s_vt);
       load_stage_rows<kThreads, VC, E, true>(a, tl, c, z, vp, a.vs, tl.head * HD + VC, vh);
 #pragma unroll
       for (int i = 0; i < kSlots; ++i) {
@@ -298,14 +307,14 @@ __global__ __launch_bounds__(kThreads, (fwd_min_waves<HD, E, XK>())) void dsa3d_
       for (int r = 0; r < 2; ++r) {
         if (r == 1) {
           __syncthreads();  // every wave is done with the first round's V^T
-          store_stage<kThreads, VC, E>(c, vh, s_vt);
+          store_stage<kThreads, VC, E, kSwz>(c, vh, s_vt);
           if (it + 1 < nit)
             load_stage_rows<kThreads, VC, E, true>(a, tl, wn.c, wn.z, vp, a.vs, tl.head * HD, vh);
           __syncthreads();
         }
         for (int kc = 32 * kh2; kc < c.nvp; kc += 32 * KPH) {
           const op_t<E> av = fix_to_op<E>(&s_atab[mq * kSRow + kc + kq]);
-          oh[r] = mma16(av, load_op<E>(&s_vt[(16 * tt + mq) * VR + kc + kq]), oh[r]);
+          oh[r] = mma16(av, load_op<E>(&s_vt[(16 * tt + mq) * VR + ((kc + kq) ^ sw)]), oh[r]);
         }
       }
       if constexpr (NB == 1) __syncthreads();
@@ -348,7 +357,7 @@ __global__ __launch_bounds__(kThreads, (fwd_min_waves<HD, E, XK>())) void dsa3d_
     int* const s_atab = reinterpret_cast<int*>(s_tab[it % NB]);
     int* row = &s_atab[tl.q * kSRow];
     __syncthreads();  // the previous step's MFMAs are done with V^T; this buffer is zeroed
-    store_stage<kThreads, HD, E>(c, vr, s_vt);
+    store_stage<kThreads, HD, E, kSwz>(c, vr, s_vt);
     if (it + 1 < nit)
       load_stage_rows<kThreads, HD, E, true>(a, tl, wn.c, wn.z, vp, a.vs, tl.head * HD, vr);
 #pragma unroll
@@ -373,7 +382,8 @@ __global__ __launch_bounds__(kThreads, (fwd_min_waves<HD, E, XK>())) void dsa3d_
       const op_t<E> av = fix_to_op<E>(&s_atab[mq * kSRow + kc + kq]);
 #pragma unroll
       for (int t = 0; t < TPW; ++t)
-        oacc[t] = mma16(av, load_op<E>(&s_vt[(16 * (cg * TPW + t) + mq) * VR + kc + kq]), oacc[t]);
+        oacc[t] = mma16(av, load_op<E>(&s_vt[(16 * (cg * TPW + t) + mq) * VR + ((kc + kq) ^ sw)]),
+                        oacc[t]);
     }
     // the next buffer was last read for step it + 1 - NB, before the barrier
     // above (with one buffer: this step, so wait for every wave's MFMAs first)
@@ -1408,11 +1418,14 @@ __global__ __launch_bounds__(kS2Threads) void dsa3d_bwd_p2s_kernel(
     Args a, RecArgs rc, const float* __restrict__ l1_ws, E* __restrict__ dq,
     float* __restrict__ dk_acc, float* __restrict__ dv_acc, int64_t acc_ks, int64_t acc_vs) {
   static_assert(sizeof(E) == 2, "the records carry bf16 storage's fp16 (p, ds) pairs");
-  constexpr int KR = ElemT<E>::kRow;
+  constexpr int KR = kVRowSwz;  // K^T chunks in the swizzled (bank-conflict-free) layout
   constexpr int SR = S2<HD>::SR, KC = S2<HD>::KC, NR = S2<HD>::NR, kS2Row = S2<HD>::Row;
   // The live slots' transposed q (or dO), [slot][channel][16 queries], staged in
   // the K^T buffer in parts of QC channels: the whole head up to head_dim 96
   // (the buffer grows to 24 KB, LDS 161.5 KB), two 64-channel parts at 128.
+  // Rows whose channel has bit 3 set hold their two 8-query halves swapped: the
+  // MFMA operand read (lane l: channel l % 32, half l / 32) then meets 16 bank
+  // windows in each 16-lane pass instead of 8.
   constexpr int QC = HD <= 96 ? HD : 64, NQ = HD / QC;
   constexpr int kQSPieces = SR * 2 * QC;  // 16 bytes each
   constexpr int kQSPer = (kQSPieces + kS2Threads - 1) / kS2Threads;  // pieces per thread
@@ -1740,7 +1753,9 @@ __global__ __launch_bounds__(kS2Threads) void dsa3d_bwd_p2s_kernel(
     #pragma unroll
             for (int k = 0; k < kQSPer; ++k) {
               const int pc = static_cast<int>(threadIdx.x) + k * kS2Threads;
-              if (pc < kQSPieces) __builtin_memcpy(&s_kt[8 * pc], &qs_reg[k], sizeof(qs_reg[k]));
+              // piece pc = half pc % 2 of row pc / 2 (bit 3 of the row: bit 4 of pc)
+              if (pc < kQSPieces)
+                __builtin_memcpy(&s_kt[8 * (pc ^ ((pc >> 4) & 1))], &qs_reg[k], sizeof(qs_reg[k]));
             }
           };
           // products of one channel part over the live slots, flushed per task
@@ -1754,7 +1769,8 @@ __global__ __launch_bounds__(kS2Threads) void dsa3d_bwd_p2s_kernel(
     #pragma unroll
               for (int r = 0; r < SR; ++r) {
                 if (s_live[r] < 0) continue;
-                const op_t<E> qo = load_op<E>(&s_kt[(r * QC + lch) * kTQ + oq]);
+                const op_t<E> qo =
+                    load_op<E>(&s_kt[(r * QC + lch) * kTQ + (oq ^ (8 * ((lch >> 3) & 1)))]);
                 acc = mma32(dv ? table_t_rows<E>(s_tab, kS2Row, kTQ * r, vb, tl.lane)
                                : table_t_hi(s_tab, kS2Row, kTQ * r, vb, tl.lane),
                             qo, acc);
@@ -1777,7 +1793,7 @@ __global__ __launch_bounds__(kS2Threads) void dsa3d_bwd_p2s_kernel(
           }
     #pragma unroll
           for (int rd = 0; rd < NR; ++rd) {
-            store_stage<kP2Stage, KC, E>(c, kr, s_kt);
+            store_stage<kP2Stage, KC, E, true>(c, kr, s_kt);
             __syncthreads();
             if (rd + 1 < NR)
               load_stage_rows<kP2Stage, KC, E>(a, tl, c, z, kp, a.ks, hc0 + KC * (rd + 1), kr);
@@ -1790,7 +1806,8 @@ __global__ __launch_bounds__(kS2Threads) void dsa3d_bwd_p2s_kernel(
                   bw[jj] = static_cast<uint32_t>(
                       s_tab[(kc + kq + jj) * kS2Row + kTQ * my_slot + mq]);
                 dq_acc[rd] = mma16(hilo_op(bw),
-                                   load_op<E>(&s_kt[(16 * my_ct + mq) * KR + kc + kq]), dq_acc[rd]);
+                                   load_op<E>(&s_kt[(16 * my_ct + mq) * KR + ((kc + kq) ^ vt_swz(mq))]),
+                                   dq_acc[rd]);
               }
             }
             __syncthreads();  // every wave is done with this round's K^T
