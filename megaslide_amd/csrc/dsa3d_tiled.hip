@@ -471,7 +471,10 @@ __global__ __launch_bounds__(kThreads, (p1_min_waves<HD, E>())) void dsa3d_bwd_p
   __shared__ int s_bin[REC ? 2 * kRecBins : 1];
   if (REC && threadIdx.x < kRecBins) s_bin[threadIdx.x] = 0;  // ordered by the setup's barrier
   constexpr bool kTwoWg = p1_min_waves<HD, E>() == 4;
-  constexpr int XR = HD + 8;  // [query][channel] row of the staged q and dO (elements)
+  // [query][channel] row of the staged q and dO (elements): HD / 2 + 8 words makes
+  // the MFMA operand reads (lane l: query l % 16, 8 channels from 8 (l / 16))
+  // bank-conflict-free on gfx950 (64 banks, 16-lane passes for 16-byte reads)
+  constexpr int XR = HD + 16;
   __shared__ __attribute__((aligned(16))) word_t<E> s_x[kTwoWg ? 2 * kTQ * XR : 1];
 
   const Tile tl = make_tile<1, kSubs>(a);
