@@ -39,9 +39,11 @@ constexpr int kChunk = 16;              // chunk edge in y and x
 constexpr int kChunkStep = 15;          // chunk start spacing (one voxel of overlap)
 constexpr int kChunkNV = kChunk * kChunk;
 constexpr int kMaxChunks = 1 << 16;     // chunk ids are kept in 16 bits
-// fp32 row stride of the tables: 260 = 4 (mod 64 banks), so the four row groups
-// an MFMA result writes (rows r, r+4, r+8, r+12) and the 16 rows an operand
-// read touches fall on distinct banks.
+// fp32 row stride of the tables: 260 words.  The four row groups an MFMA result
+// writes (rows r, r+4, r+8, r+12; 4-byte stores over 32 banks per half-wave)
+// fall on distinct banks.  The operand reads (16 rows, two 16-byte reads per
+// lane; 64 banks in four 16-lane passes) are 2-way conflicted in each pass, and
+// no stride or row order avoids that without conflicting the result writes.
 constexpr int kSRow = kChunkNV + 4;
 constexpr int kVRow = kChunkNV + 8;     // bf16 row stride of a transposed K/V chunk
 
@@ -62,7 +64,7 @@ template <>
 struct ElemT<float> {
   using op = f32x8_t;
   using word = float;
-  static constexpr int kRow = kSRow;    // 260 = 4 (mod 64 banks): 16-byte reads of 16 rows are conflict-free
+  static constexpr int kRow = kSRow;    // 260 words, as the tables
 };
 template <typename E>
 using op_t = typename ElemT<E>::op;
