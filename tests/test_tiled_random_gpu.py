@@ -7,7 +7,9 @@ every gradient (dq, dK, dV, d offsets) against the oracle:
   - bf16, default accumulation (the column-streaming dq/dK/dV kernel, with its
     pair walks and the tile kernel for listed columns), 2e-2 of max|ref|;
   - bf16 with dK/dV summed in scaled fp16 (the tile kernel), 2e-2;
-  - fp32 storage (fp32 matrix-core kernels), 1e-4.
+  - fp32 storage (fp32 matrix-core kernels), 1e-4;
+  - bf16 with G shared extra keys (their gradients checked too), 2e-2;
+  - bf16 with attention dropout (the oracle applies the same Philox keep mask), 2e-2.
 """
 
 import random
@@ -24,7 +26,8 @@ DEV = "cuda"
 BF16_TOL = 2e-2
 FP32_TOL = 1e-4
 MODES = {"bf16": (torch.bfloat16, "fp32", BF16_TOL), "bf16-f16acc": (torch.bfloat16, "fp16", BF16_TOL),
-         "fp32": (torch.float32, "fp32", FP32_TOL)}
+         "fp32": (torch.float32, "fp32", FP32_TOL), "bf16-extra": (torch.bfloat16, "fp32", BF16_TOL),
+         "bf16-dropout": (torch.bfloat16, "fp32", BF16_TOL)}
 WINDOWS = [(1, 1, 1), (1, 3, 3), (3, 3, 3), (3, 5, 5), (3, 7, 7), (1, 7, 7), (3, 1, 3),
            (5, 3, 3), (2, 3, 5), (3, 5, 7)]
 
@@ -52,7 +55,8 @@ def draw(seed):
 
 
 CASES = ([("bf16", s) for s in range(48)] + [("bf16-f16acc", s) for s in range(48, 64)] +
-         [("fp32", s) for s in range(64, 80)])
+         [("fp32", s) for s in range(64, 80)] + [("bf16-extra", s) for s in range(80, 96)] +
+         [("bf16-dropout", s) for s in range(96, 112)])
 
 
 @pytest.mark.parametrize("mode,seed", CASES)
@@ -70,22 +74,38 @@ def test_tiled_random_shape_vs_oracle(mode, seed):
         off = off + (torch.rand(nh * K * 3, generator=g) * 2.0 - 1.0) * shift
     off = off.to(dtype)
     dout = torch.randn(B, N, D, generator=g).to(dtype)
+    G = [1, 7, 32, 128][seed % 4] if mode == "bf16-extra" else 0
+    inputs = [q, k, v, off]
+    if G:
+        inputs += [torch.randn(B, G, D, generator=g).to(dtype) for _ in range(2)]
+    drop = (0.1 if seed % 2 else 0.3, 1000 + seed, seed % 3) if mode == "bf16-dropout" else None
+    if G or drop:
+        print(f"  extra keys G={G} dropout={drop}", flush=True)
 
-    qq, kk, vv, oo = (t.float().clone().requires_grad_(True) for t in (q, k, v, off))
-    ref = dsa3d_core_ref(qq, kk, vv, oo, (T, H, W), nh, ks, scale)
+    ref_in = [t.float().clone().requires_grad_(True) for t in inputs]
+    ref = dsa3d_core_ref(*ref_in[:4], (T, H, W), nh, ks, scale,
+                         extra_k=ref_in[4] if G else None, extra_v=ref_in[5] if G else None,
+                         dropout=drop)
     ref.backward(dout.float())
 
     from megaslide_amd import dsa3d_core
-    ts = [t.detach().to(DEV).requires_grad_(True) for t in (q, k, v, off)]
-    out = dsa3d_core(*ts, (T, H, W), nh, ks, scale, algo="tiled", dkv_accum=accum)
+    ts = [t.detach().to(DEV).requires_grad_(True) for t in inputs]
+    kw = dict(algo="tiled", dkv_accum=accum)
+    if G:
+        kw.update(extra_k=ts[4], extra_v=ts[5])
+    if drop:
+        kw.update(dropout_p=drop[0], dropout_seed=drop[1], dropout_offset=drop[2])
+    out = dsa3d_core(*ts[:4], (T, H, W), nh, ks, scale, **kw)
     out.backward(dout.to(DEV))
     torch.cuda.synchronize()
 
     e_out = rel_err(out.detach().float().cpu(), ref.detach())
     print(f"  out: {e_out:.2e}", flush=True)
     assert e_out < tol
-    for name, r, t in zip(("dq", "dk", "dv", "doff"), (qq.grad, kk.grad, vv.grad, oo.grad), ts):
-        if name in ("dq", "dk") and K == 1:
+    names = ("dq", "dk", "dv", "doff", "dek", "dev")
+    for name, r, t in zip(names, ref_in, ts):
+        r = r.grad
+        if name in ("dq", "dk") and K == 1 and G == 0:
             # one tap: p = 1 and ds = p (dp - p dp) = 0, so dq and dK (both
             # carried by ds) are zero up to the rounding of p (the oracle's are
             # exactly 0); the inputs are O(1)
