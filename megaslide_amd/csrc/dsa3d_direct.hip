@@ -17,7 +17,11 @@
 //     weight 0 and are skipped.
 //   s = q . sum_c w_c K_c / sqrt(hd); p = softmax(s); o = sum p sum_c w_c V_c.
 //
-// Backward per tap: dp = dO . v_s, ds = p (dp - Delta), Delta = dO . o - dlse;
+// Backward per tap: dp = dO . v_s, ds = p (dp - Delta), Delta = sum over taps
+// (and extra keys) of p f dp - dlse, formed in fp32 by a first pass over the
+// taps (dO . o from the stored output would carry its rounding: for bf16
+// storage that is of the size of ds itself where the softmax is peaked, and
+// the reference's softmax backward sums p dp over its taps as well);
 // dq += ds*scale*k_s; dK_c += w_c ds scale q; dV_c += w_c p dO (fp32 atomics
 // into an fp32 accumulator); d u = sum_c dw_c/du (ds scale q.K_c + p dO.V_c),
 // zeroed where u <= 0 or u >= S-1 (border clamp), times S/2 (unnormalise),
@@ -169,6 +173,7 @@ __global__ __launch_bounds__(kBlock) void dsa3d_bwd_direct_kernel(
     const float* __restrict__ dlse, T* __restrict__ dq, float* __restrict__ dk_acc,
     float* __restrict__ dv_acc, T* __restrict__ doff, float* __restrict__ dek_acc,
     float* __restrict__ dev_acc) {
+  (void)out;  // Delta comes from the taps, not from the stored output
   const int lane = threadIdx.x % kGroup;
   const int64_t gid = static_cast<int64_t>(blockIdx.x) * kGroupsPerBlock + threadIdx.x / kGroup;
   const int64_t total = static_cast<int64_t>(a.B) * a.N * a.nh;
@@ -191,20 +196,80 @@ __global__ __launch_bounds__(kBlock) void dsa3d_bwd_direct_kernel(
   const int64_t sample0 = static_cast<int64_t>(b) * a.N;
 
   float qv[CPL], gov[CPL], dqv[CPL];
-  float delta_part = 0.0f;
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
     const bool on = lane * CPL + j < a.hd;
     qv[j] = on ? ld(qp, bn * a.qs + cbase + j) : 0.0f;
     gov[j] = on ? ld(dout, bn * D + cbase + j) : 0.0f;
-    const float ov = on ? ld(out, bn * D + cbase + j) : 0.0f;
-    delta_part += gov[j] * ov;
     dqv[j] = 0.0f;
   }
-  float delta = group_sum<kGroup>(delta_part);
-  if (dlse != nullptr) delta -= dlse[bn * a.nh + head];
   const float lse_q = lse[bn * a.nh + head];
   const float sc = a.softmax_scale;
+  const T* __restrict__ ekp = static_cast<const T*>(a.ek);
+  const T* __restrict__ evp = static_cast<const T*>(a.ev);
+
+  // s and dp of tap kap (the same gathers and rounding as the main pass below)
+  auto tap_s_dp = [&](int kap, float bx, float by, float bz, float& s, float& dp) {
+    float o0, o1, o2;
+    load_offsets(op + kap * 3, a.offset_scale, o0, o1, o2);
+    const Axis ax = axis_sample(grid_coord(bx, o0, a.div_x), a.W);
+    const Axis ay = axis_sample(grid_coord(by, o1, a.div_y), a.H);
+    const Axis az = axis_sample(grid_coord(bz, o2, a.div_z), a.T);
+    float s_part = 0.0f, dp_part = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const int dz = c >> 2, dy = (c >> 1) & 1, dx = c & 1;
+      if ((dz && !az.hi_ok) || (dy && !ay.hi_ok) || (dx && !ax.hi_ok)) continue;
+      const float wgt = (dz ? az.f : 1.0f - az.f) * (dy ? ay.f : 1.0f - ay.f) *
+                        (dx ? ax.f : 1.0f - ax.f);
+      const int64_t row =
+          sample0 + (static_cast<int64_t>(az.i0 + dz) * a.H + (ay.i0 + dy)) * a.W + (ax.i0 + dx);
+      float pkc = 0.0f, pvc = 0.0f;
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+        if (lane * CPL + j < a.hd) {
+          pkc += qv[j] * ld(kp, row * a.ks + cbase + j);
+          pvc += gov[j] * ld(vp, row * a.vs + cbase + j);
+        }
+      }
+      s_part += wgt * pkc;
+      dp_part += wgt * pvc;
+    }
+    s = group_sum<kGroup>(s_part) * sc;
+    dp = group_sum<kGroup>(dp_part);
+  };
+
+  // Delta = dO . o = sum of p f dp over the taps and extra keys, in fp32
+  float delta = 0.0f;
+  {
+    int kap = 0;
+    for (int i = 0; i < a.kt; ++i) {
+      const float bz = base_coord(t, i - a.kt / 2, a.T);
+      for (int jj = 0; jj < a.kh; ++jj) {
+        const float by = base_coord(h, jj - a.kh / 2, a.H);
+        for (int kk = 0; kk < a.kw; ++kk, ++kap) {
+          float s, dp;
+          tap_s_dp(kap, base_coord(w, kk - a.kw / 2, a.W), by, bz, s, dp);
+          delta += __expf(s - lse_q) * dropout_factor(a.drop, bn, head, kap) * dp;
+        }
+      }
+    }
+    for (int g = 0; g < a.G; ++g) {
+      const int64_t erow = (static_cast<int64_t>(b) * a.G + g) * D + cbase;
+      float s_part = 0.0f, dp_part = 0.0f;
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+        if (lane * CPL + j < a.hd) {
+          s_part += qv[j] * ld(ekp, erow + j);
+          dp_part += gov[j] * ld(evp, erow + j);
+        }
+      }
+      const float s = group_sum<kGroup>(s_part) * sc;
+      const float dp = group_sum<kGroup>(dp_part);
+      delta += __expf(s - lse_q) * dropout_factor(a.drop, bn, head, K + g) * dp;
+    }
+  }
+  if (dlse != nullptr) delta -= dlse[bn * a.nh + head];
 
   int kap = 0;
   for (int i = 0; i < a.kt; ++i) {
@@ -296,8 +361,6 @@ __global__ __launch_bounds__(kBlock) void dsa3d_bwd_direct_kernel(
     }
   }
   // extra keys: dq += ds scale ek_g; dEK_g += ds scale q, dEV_g += p f dO (fp32 atomics)
-  const T* __restrict__ ekp = static_cast<const T*>(a.ek);
-  const T* __restrict__ evp = static_cast<const T*>(a.ev);
   for (int g = 0; g < a.G; ++g) {
     const int64_t erow = (static_cast<int64_t>(b) * a.G + g) * D + cbase;
     float ekv[CPL], s_part = 0.0f, dp_part = 0.0f;
