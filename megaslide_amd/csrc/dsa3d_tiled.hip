@@ -545,25 +545,16 @@ __global__ __launch_bounds__(kThreads, (p1_min_waves<HD, E>())) void dsa3d_bwd_p
       x[cc] = load_op<E>(&s_x[(t * kTQ + (tl.lane & 15)) * XR + 32 * cc + 8 * (tl.lane >> 4)]);
   };
 
-  // Delta = dO . O - dlse and lse for this lane's query.  Without extra keys,
-  // dO . O = sum_k p_k f_k dP_k over the query's taps, formed in fp32 after the
-  // plane walk: that sum does not see the rounding of the stored output (bf16
-  // storage), which a peaked softmax would otherwise turn into ds errors as
-  // large as ds itself.  With extra keys (their dP is not formed here) it is
-  // dO . O from the output rows, 32 lanes x HD/32 channels.
-  constexpr int CPL = HD / kSubs;
+  // Delta = dO . O - dlse and lse for this lane's query.  dO . O = sum_k p_k f_k
+  // dP_k over the query's taps (formed in fp32 after the plane walk) plus, with
+  // extra keys, the same sum over the keys (formed by their kernel before this
+  // one): neither sees the rounding of the stored output (bf16 storage), which
+  // a peaked softmax would otherwise turn into ds errors as large as ds itself.
   float delta = 0.0f, lse_q = 0.0f;
   if (tl.q_ok) {
-    if (a.G > 0) {
-      const int64_t base = tl.qn * D + tl.head * HD + CPL * tl.sub;
-#pragma unroll
-      for (int j = 0; j < CPL; ++j) delta += to_f32(dout[base + j]) * to_f32(out[base + j]);
-    }
+    // with extra keys: their sum of p f dP (their kernel ran first)
+    if (a.G > 0) delta = a.dlt[tl.qn * a.nh + tl.head];
     lse_q = lse[tl.qn * a.nh + tl.head];
-  }
-  if (a.G > 0) {
-#pragma unroll
-    for (int m = 1; m < kSubs; m <<= 1) delta += __shfl_xor(delta, m);
   }
   if (dlse != nullptr && tl.q_ok) delta -= dlse[tl.qn * a.nh + tl.head];
   // kept in LDS across the plane loop (registers are the limit there)
@@ -713,11 +704,12 @@ __global__ __launch_bounds__(kThreads, (p1_min_waves<HD, E>())) void dsa3d_bwd_p
     s_[i] = ok ? __expf(s_[i] * a.softmax_scale - lse_q) : 0.0f;
     pdp = __builtin_fmaf(s_[i] * slot_dropout(sl[i], a.drop), dp_[i], pdp);
   }
-  if (a.G == 0) {
 #pragma unroll
-    for (int m = 1; m < kSubs; m <<= 1) pdp += __shfl_xor(pdp, m);
-    delta += pdp;
-  }
+  for (int m = 1; m < kSubs; m <<= 1) pdp += __shfl_xor(pdp, m);
+  delta += pdp;
+  // the whole Delta for the extra keys' kernel that runs next (each query's
+  // entry is read above and written here by this workgroup only)
+  if (a.G > 0 && sub == 0 && qn >= 0) a.dlt[qn * a.nh + tl.head] = delta;
   // p * factor in place of p, ds * scale = p (f dP - Delta) scale in place of dp
 #pragma unroll
   for (int i = 0; i < kSlots; ++i) {
@@ -1941,17 +1933,19 @@ __global__ __launch_bounds__(kS2Threads) void dsa3d_bwd_p2s_kernel(
 // Backward of the extra keys (attention.py:160-173) for 16 consecutive tokens
 // of one sample and head (4 waves, 16 lanes per query): S_e = q . ek_g and
 // dP_e = dO . ev_g on the matrix cores, then per (query, key) p = exp(scale
-// S_e - lse), the dropout factor f of tap K + g, ds * scale = p (f dP_e -
-// Delta) scale (Delta = dO . O - dlse).  It writes ds * scale and p f
-// ([B, nh, N, G], for the dEK / dEV reduction) and dq's extra part sum_g
-// ds_g scale ek_g (MFMA, fp32 [rows, D] dqx, which the second backward kernel
-// adds to its tap part before dq's one rounding).
+// S_e - lse) and the dropout factor f of tap K + g.  Two launches:
+//   DLT: before the first backward kernel, the keys' part of Delta, sum_g p f
+//     dP_e per (token, head) in fp32, into a.dlt (the first backward kernel
+//     adds the taps' part and dlse and writes the whole Delta back);
+//   otherwise: after it, ds * scale = p (f dP_e - Delta) scale with that
+//     Delta, written with p f ([B, nh, N, G], for the dEK / dEV reduction), and
+//     dq's extra part sum_g ds_g scale ek_g (MFMA, fp32 [rows, D] dqx, which
+//     the second backward kernel adds to its tap part before dq's one rounding).
 constexpr int kXQ = 16;
-template <int HD, typename E>
+template <int HD, typename E, bool DLT>
 __global__ __launch_bounds__(256) void dsa3d_bwd_extra_kernel(
-    Args a, const E* __restrict__ out, const E* __restrict__ dout, const float* __restrict__ lse,
-    const float* __restrict__ dlse, float* __restrict__ dqx, E* __restrict__ ds_e,
-    E* __restrict__ pf_e) {
+    Args a, const E* __restrict__ dout, const float* __restrict__ lse, float* __restrict__ dqx,
+    E* __restrict__ ds_e, E* __restrict__ pf_e) {
   constexpr int EKR = sizeof(E) == 2 ? 40 : 36;  // 16-byte aligned transposed rows
   __shared__ __attribute__((aligned(16))) float s_s[kXQ * kSRow];   // S_e, then ds * scale
   __shared__ __attribute__((aligned(16))) float s_dp[kXQ * kSRow];  // dP_e
@@ -1965,21 +1959,12 @@ __global__ __launch_bounds__(256) void dsa3d_bwd_extra_kernel(
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int mq = lane & 15, kq = 8 * (lane >> 4);
   const int64_t sample0 = static_cast<int64_t>(b) * a.N;
-  // Delta and lse of each query: 16 lanes per query
-  {
-    const int qi = threadIdx.x / 16, sub = threadIdx.x % 16;
-    const int64_t n = n0 + qi;
-    float part = 0.0f;
-    if (n < a.N) {
-      const int64_t base = (sample0 + n) * D + head * HD;
-      for (int c = sub; c < HD; c += 16) part += to_f32(dout[base + c]) * to_f32(out[base + c]);
-    }
-    part = group_sum<16>(part);
-    if (sub == 0) {
-      const int64_t r = (sample0 + (n < a.N ? n : 0)) * a.nh + head;
-      s_delta[qi] = n < a.N ? part - (dlse != nullptr ? dlse[r] : 0.0f) : 0.0f;
-      s_lse[qi] = n < a.N ? lse[r] : 0.0f;
-    }
+  // Delta (the whole, from the first backward kernel) and lse of each query
+  if (threadIdx.x < kXQ) {
+    const int64_t n = n0 + threadIdx.x;
+    const int64_t r = (sample0 + (n < a.N ? n : 0)) * a.nh + head;
+    s_delta[threadIdx.x] = !DLT && n < a.N ? a.dlt[r] : 0.0f;
+    s_lse[threadIdx.x] = n < a.N ? lse[r] : 0.0f;
   }
   // q and dO rows of the 16 queries as MFMA A operands (zero past N)
   op_t<E> xq[HD / 32], xo[HD / 32];
@@ -2016,6 +2001,21 @@ __global__ __launch_bounds__(256) void dsa3d_bwd_extra_kernel(
     }
   }
   __syncthreads();
+  if constexpr (DLT) {
+    // the keys' part of Delta: thread t takes query t / 16, keys t % 16 + 16 j
+    const int qi = threadIdx.x / 16, sub = threadIdx.x % 16;
+    const int64_t n = n0 + qi;
+    const int64_t row = sample0 + n;
+    float part = 0.0f;
+    for (int g = sub; g < G; g += 16) {
+      const float pe = __expf(s_s[qi * kSRow + g] * a.softmax_scale - s_lse[qi]);
+      const float f = a.drop.threshold == 0 ? 1.0f : dropout_factor(a.drop, row, head, a.K + g);
+      part = __builtin_fmaf(pe * f, s_dp[qi * kSRow + g], part);
+    }
+    part = group_sum<16>(part);
+    if (sub == 0 && n < a.N) a.dlt[row * a.nh + head] = part;
+    return;
+  }
   // p, ds * scale per (query, key): thread t takes query t / 16, keys t % 16 + 16 j
   {
     const int qi = threadIdx.x / 16, sub = threadIdx.x % 16;
@@ -2187,6 +2187,7 @@ tiled::Args make_tiled_args(const msd_dsa3d_desc& d, const void* q, const void* 
   a.ek = ek;
   a.ev = ev;
   a.G = d.extra_g;
+  a.dlt = nullptr;
   a.q = q;
   a.k = k;
   a.v = v;
@@ -2518,6 +2519,7 @@ struct BwdBufs {
   float* dek_acc;  // extra keys: dEK / dEV fp32 [B, G, D] (the outputs for fp32 storage)
   float* dev_acc;
   float* dqx;      // extra keys: their part of dq, fp32 [rows, D] (null without them)
+  float* dlt;      // extra keys: Delta per (token, head), fp32 [rows, nh] (null without them)
   RecArgs rec;     // column-streaming kernel's records (rec.rec null: not used)
 };
 
@@ -2543,7 +2545,8 @@ void launch_bwd_pair(const msd_dsa3d_desc& d, const void* q, const void* k, cons
                      const float* lse, const float* dlse, E* gq, E* goff, const BwdBufs<E>& w,
                      hipStream_t s) {
   constexpr int CW = p2_window<HD, E>(), FR = p2_frames<HD, E>();
-  const tiled::Args a1 = make_tiled_args(d, q, k, v, off, tiled_tiles<1>(d), ek, ev);
+  tiled::Args a1 = make_tiled_args(d, q, k, v, off, tiled_tiles<1>(d), ek, ev);
+  a1.dlt = w.dlt;
   const tiled::Args a2 = make_tiled_args(d, q, k, v, off, tiled_tiles<FR>(d), ek, ev);
   const dim3 g1 = tiled_grid<1>(d);
   dim3 g2 = tiled_grid<FR>(d);
@@ -2573,6 +2576,10 @@ void launch_bwd_pair(const msd_dsa3d_desc& d, const void* q, const void* k, cons
       return;
     }
   }
+  const dim3 gx(static_cast<unsigned>(d.B * ((a1.N + kXQ - 1) / kXQ)), d.num_heads);
+  if (d.extra_g > 0)  // the keys' part of Delta, for the first backward kernel
+    hipLaunchKernelGGL((dsa3d_bwd_extra_kernel<HD, E, true>), gx, dim3(256), 0, s, a1, go, lse,
+                       w.dqx, w.ds_e, w.pf_e);
   if constexpr (sizeof(E) == 2) {
     if (h16)
       hipLaunchKernelGGL((dsa3d_bwd_p1_kernel<HD, E, 2>), g1, dim3(tiled::kThreads), 0, s, a1, o,
@@ -2581,11 +2588,9 @@ void launch_bwd_pair(const msd_dsa3d_desc& d, const void* q, const void* k, cons
   if (!h16)
     hipLaunchKernelGGL((dsa3d_bwd_p1_kernel<HD, E, 4>), g1, dim3(tiled::kThreads), 0, s, a1, o,
                        go, lse, dlse, goff, p_ws, b_ws, dk_acc, dv_acc, acc_ks, acc_vs, RecArgs{});
-  if (d.extra_g > 0) {
-    const dim3 gx(static_cast<unsigned>(d.B * ((a1.N + kXQ - 1) / kXQ)), d.num_heads);
-    hipLaunchKernelGGL((dsa3d_bwd_extra_kernel<HD, E>), gx, dim3(256), 0, s, a1, o, go, lse, dlse,
+  if (d.extra_g > 0)
+    hipLaunchKernelGGL((dsa3d_bwd_extra_kernel<HD, E, false>), gx, dim3(256), 0, s, a1, go, lse,
                        w.dqx, w.ds_e, w.pf_e);
-  }
   if constexpr (sizeof(E) == 2) {
     if (h16) {
       const float factor = a1.drop.threshold == 0 ? 1.0f : a1.drop.scale;
@@ -2668,7 +2673,8 @@ __global__ __launch_bounds__(256) void acc_to_bf16_kernel(const float* __restric
 // Workspace layout of the tiled backward (byte offsets): the bf16 path's fp32
 // accumulators (dK/dV, then dEK/dEV; fp32 storage accumulates in its outputs),
 // p and ds * scale per tap, and with extra keys their ds * scale and p *
-// factor per (token, head, key) in the element type and their fp32 part of dq.
+// factor per (token, head, key) in the element type, their fp32 part of dq
+// and the fp32 Delta per (token, head).
 // For bf16 storage the dK / dV region holds the fp32 [2, rows, D] accumulator
 // rows; with MSD_ACCUM_F16 its first half serves as the fp16 [2, rows, D]
 // accumulator (the fp32 rows are then only used, zeroed first, after that has
@@ -2676,7 +2682,7 @@ __global__ __launch_bounds__(256) void acc_to_bf16_kernel(const float* __restric
 // per-block maxima, the two scales and their inverses and the overflow flag
 // follow the extra keys' buffers.
 struct TiledWs {
-  size_t acc, xacc, p, ds, dse, pfe, dqx, stats, scales, rec, hdr, qt, collist, bytes;
+  size_t acc, xacc, p, ds, dse, pfe, dqx, dlt, stats, scales, rec, hdr, qt, collist, bytes;
 };
 
 // Calls that take the column-streaming dq/dK/dV kernel: bf16 storage with fp32
@@ -2701,7 +2707,8 @@ TiledWs tiled_ws(const msd_dsa3d_desc& d) {
   w.dse = up(w.ds + (bf ? rows * d.num_heads * 4 : taps * 4));
   w.pfe = up(w.dse + rows * d.num_heads * G * e);
   w.dqx = up(w.pfe + rows * d.num_heads * G * e);
-  w.stats = up(w.dqx + (G > 0 ? rows * D * 4 : 0));
+  w.dlt = up(w.dqx + (G > 0 ? rows * D * 4 : 0));
+  w.stats = up(w.dlt + (G > 0 ? rows * d.num_heads * 4 : 0));
   w.scales = up(w.stats + (bf ? kBoundsBlocks * kBoundsWords * 4 : 0));
   // column-streaming kernel: records, tile headers, transposed q / dO, flags
   const bool st = tiled_streams(d);
@@ -2759,6 +2766,7 @@ hipError_t bwd_tiled_typed(const msd_dsa3d_desc& d, const void* q, const void* k
   w.dek_acc = kInPlace ? static_cast<float*>(dek) : reinterpret_cast<float*>(base + L.xacc);
   w.dev_acc = kInPlace ? static_cast<float*>(dev) : w.dek_acc + erows * D;
   w.dqx = erows > 0 ? reinterpret_cast<float*>(base + L.dqx) : nullptr;
+  w.dlt = erows > 0 ? reinterpret_cast<float*>(base + L.dlt) : nullptr;
   w.rec = RecArgs{};
   if (tiled_streams(d)) {
     w.rec.rec = reinterpret_cast<tiled::u32x4_t*>(base + L.rec);

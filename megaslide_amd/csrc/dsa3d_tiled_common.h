@@ -157,6 +157,8 @@ struct Args {
   const void* ek;                // extra keys / values [B, G, D] shared by every query
   const void* ev;                //   (attention.py:160-173), tap K + g of each query
   int G;                         // extra keys per sample (0 = none, at most kMaxExtra)
+  float* dlt;                    // backward with extra keys: per (token, head) fp32 Delta,
+                                 //   their part, then (first backward kernel) the whole
 };
 
 constexpr int kMaxExtra = 256;   // extra keys the tiled kernels take (a table row)

@@ -126,12 +126,14 @@ def test_workspace_size_and_check():
         d = _desc(B=2, dtype=dtype, dkv_accum=accum)
         need = lib.msd_dsa3d_bwd_workspace_size(ctypes.byref(d))
         assert need == want
-    # with extra keys the tiled backward also keeps their fp32 part of dq
+    # with extra keys the tiled backward also keeps their fp32 part of dq and
+    # the fp32 Delta per (token, head)
     dx = _desc(B=2, dtype=1, extra_g=8)
     G, D = 8, 128
     want = (2 * rows * D * 4 + 2 * 2 * G * D * 4 + taps + rows * 2 * 4)
     want = (want + 255) // 256 * 256 + 2 * rows * 2 * G * 2
     want = (want + 255) // 256 * 256 + rows * D * 4
+    want = (want + 255) // 256 * 256 + rows * 2 * 4
     want = (want + 255) // 256 * 256 + records + 32
     assert lib.msd_dsa3d_bwd_workspace_size(ctypes.byref(dx)) == want
     rc = lib.msd_dsa3d_bwd(ctypes.byref(d), *([16] * 4), None, None, *([16] * 3), None,
