@@ -9,7 +9,10 @@ every gradient (dq, dK, dV, d offsets) against the oracle:
   - bf16 with dK/dV summed in scaled fp16 (the tile kernel), 2e-2;
   - fp32 storage (fp32 matrix-core kernels), 1e-4;
   - bf16 with G shared extra keys (their gradients checked too), 2e-2;
-  - bf16 with attention dropout (the oracle applies the same Philox keep mask), 2e-2.
+  - bf16 with attention dropout (the oracle applies the same Philox keep mask), 2e-2;
+  - head sizes and windows the tiled kernels do not take (head_dim 8 to 112 off the
+    32/64/96/128 set, windows of more than 160 taps), which the default dispatch
+    sends to the general (direct) kernels: bf16 2e-2, fp32 1e-4.
 """
 
 import random
@@ -27,7 +30,8 @@ BF16_TOL = 2e-2
 FP32_TOL = 1e-4
 MODES = {"bf16": (torch.bfloat16, "fp32", BF16_TOL), "bf16-f16acc": (torch.bfloat16, "fp16", BF16_TOL),
          "fp32": (torch.float32, "fp32", FP32_TOL), "bf16-extra": (torch.bfloat16, "fp32", BF16_TOL),
-         "bf16-dropout": (torch.bfloat16, "fp32", BF16_TOL)}
+         "bf16-dropout": (torch.bfloat16, "fp32", BF16_TOL),
+         "general-bf16": (torch.bfloat16, "fp32", BF16_TOL), "general-fp32": (torch.float32, "fp32", FP32_TOL)}
 WINDOWS = [(1, 1, 1), (1, 3, 3), (3, 3, 3), (3, 5, 5), (3, 7, 7), (1, 7, 7), (3, 1, 3),
            (5, 3, 3), (2, 3, 5), (3, 5, 7)]
 
@@ -56,13 +60,20 @@ def draw(seed):
 
 CASES = ([("bf16", s) for s in range(48)] + [("bf16-f16acc", s) for s in range(48, 64)] +
          [("fp32", s) for s in range(64, 80)] + [("bf16-extra", s) for s in range(80, 96)] +
-         [("bf16-dropout", s) for s in range(96, 112)])
+         [("bf16-dropout", s) for s in range(96, 112)] + [("general-bf16", s) for s in range(112, 120)] +
+         [("general-fp32", s) for s in range(120, 128)])
 
 
 @pytest.mark.parametrize("mode,seed", CASES)
 def test_tiled_random_shape_vs_oracle(mode, seed):
     dtype, accum, tol = MODES[mode]
     B, T, H, W, nh, ks, hd, off_std, shift, scale = draw(seed)
+    general = mode.startswith("general")
+    if general:
+        # a head size off the tiled set, or (every third case) a 5x7x7 window of 245 taps
+        hd = [8, 16, 40, 48, 80, 112][seed % 6]
+        if seed % 3 == 0:
+            hd, ks = 64, (5, 7, 7)
     K = ks[0] * ks[1] * ks[2]
     N, D = T * H * W, nh * hd
     print(f"[tiled random {mode} {seed}] B={B} T={T} H={H} W={W} nh={nh} hd={hd} window={ks} "
@@ -90,7 +101,7 @@ def test_tiled_random_shape_vs_oracle(mode, seed):
 
     from megaslide_amd import dsa3d_core
     ts = [t.detach().to(DEV).requires_grad_(True) for t in inputs]
-    kw = dict(algo="tiled", dkv_accum=accum)
+    kw = dict(algo="auto" if general else "tiled", dkv_accum=accum)
     if G:
         kw.update(extra_k=ts[4], extra_v=ts[5])
     if drop:
