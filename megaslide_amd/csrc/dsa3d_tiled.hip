@@ -1665,7 +1665,7 @@ __global__ __launch_bounds__(kS2Threads) void dsa3d_bwd_p2s_kernel(
 
         for (int ci = 0; ci < nchunks; ++ci) {
           const Chunk c = make_chunk(box, ci);
-          const int cyi = box.ncx == 1 ? 0 : ci / box.ncx, cxi = ci - cyi * box.ncx;
+          const int cyi = box.ncx == 1 ? ci : ci / box.ncx, cxi = ci - cyi * box.ncx;
           for (int vi = threadIdx.x; vi < c.nv; vi += kS2Threads)
             s_rows[vi] = static_cast<int>(chunk_row(a, tl, c, z, vi) - tl.sample0);
 

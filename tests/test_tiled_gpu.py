@@ -257,3 +257,16 @@ def test_tiled_column_pairs_vs_oracle_and_direct(shape):
 ])
 def test_tiled_listed_columns_vs_oracle_and_direct(shape):
     test_tiled_column_pairs_vs_oracle_and_direct(shape)
+
+
+# Corner boxes two chunks tall and one chunk wide (W <= 16, tall grids, large
+# offsets): the column-streaming kernel's plane walk visits chunks (1, 0),
+# (2, 0), ... whose records it must match by row chunk as well.
+@pytest.mark.parametrize("shape", [
+    # B, T, H, W, nh, kernel, off_std, scale, head_dim
+    (1, 5, 24, 8, 1, (3, 7, 7), 4.0, 1.0, 64),
+    (1, 7, 17, 6, 2, (3, 3, 3), 6.0, 1.2, 64),
+    (2, 4, 20, 1, 2, (3, 5, 5), 8.0, 1.0, 96),
+])
+def test_tiled_tall_boxes_vs_oracle_and_direct(shape):
+    test_tiled_column_pairs_vs_oracle_and_direct(shape)
