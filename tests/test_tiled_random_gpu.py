@@ -12,7 +12,10 @@ every gradient (dq, dK, dV, d offsets) against the oracle:
   - bf16 with attention dropout (the oracle applies the same Philox keep mask), 2e-2;
   - head sizes and windows the tiled kernels do not take (head_dim 8 to 112 off the
     32/64/96/128 set, windows of more than 160 taps), which the default dispatch
-    sends to the general (direct) kernels: bf16 2e-2, fp32 1e-4.
+    sends to the general (direct) kernels: bf16 2e-2, fp32 1e-4;
+  - the returned log-sum-exp differentiated with the output (loss = sum(out g_out)
+    + sum(lse g_lse), the dlse input of the backward), bf16 and fp32; lse itself
+    within 1e-4 (bf16: 2e-3 of max|lse|).
 """
 
 import random
@@ -31,7 +34,8 @@ FP32_TOL = 1e-4
 MODES = {"bf16": (torch.bfloat16, "fp32", BF16_TOL), "bf16-f16acc": (torch.bfloat16, "fp16", BF16_TOL),
          "fp32": (torch.float32, "fp32", FP32_TOL), "bf16-extra": (torch.bfloat16, "fp32", BF16_TOL),
          "bf16-dropout": (torch.bfloat16, "fp32", BF16_TOL),
-         "general-bf16": (torch.bfloat16, "fp32", BF16_TOL), "general-fp32": (torch.float32, "fp32", FP32_TOL)}
+         "general-bf16": (torch.bfloat16, "fp32", BF16_TOL), "general-fp32": (torch.float32, "fp32", FP32_TOL),
+         "bf16-lse": (torch.bfloat16, "fp32", BF16_TOL), "fp32-lse": (torch.float32, "fp32", FP32_TOL)}
 WINDOWS = [(1, 1, 1), (1, 3, 3), (3, 3, 3), (3, 5, 5), (3, 7, 7), (1, 7, 7), (3, 1, 3),
            (5, 3, 3), (2, 3, 5), (3, 5, 7)]
 
@@ -61,7 +65,8 @@ def draw(seed):
 CASES = ([("bf16", s) for s in range(48)] + [("bf16-f16acc", s) for s in range(48, 64)] +
          [("fp32", s) for s in range(64, 80)] + [("bf16-extra", s) for s in range(80, 96)] +
          [("bf16-dropout", s) for s in range(96, 112)] + [("general-bf16", s) for s in range(112, 120)] +
-         [("general-fp32", s) for s in range(120, 128)])
+         [("general-fp32", s) for s in range(120, 128)] + [("bf16-lse", s) for s in range(128, 144)] +
+         [("fp32-lse", s) for s in range(144, 152)])
 
 
 @pytest.mark.parametrize("mode,seed", CASES)
@@ -93,11 +98,18 @@ def test_tiled_random_shape_vs_oracle(mode, seed):
     if G or drop:
         print(f"  extra keys G={G} dropout={drop}", flush=True)
 
+    with_lse = mode.endswith("-lse")
+    glse = torch.randn(B, N, nh, generator=g) if with_lse else None
+
     ref_in = [t.float().clone().requires_grad_(True) for t in inputs]
     ref = dsa3d_core_ref(*ref_in[:4], (T, H, W), nh, ks, scale,
                          extra_k=ref_in[4] if G else None, extra_v=ref_in[5] if G else None,
-                         dropout=drop)
-    ref.backward(dout.float())
+                         dropout=drop, return_lse=with_lse)
+    if with_lse:
+        ref, ref_lse = ref
+        ((ref * dout.float()).sum() + (ref_lse.transpose(1, 2) * glse).sum()).backward()
+    else:
+        ref.backward(dout.float())
 
     from megaslide_amd import dsa3d_core
     ts = [t.detach().to(DEV).requires_grad_(True) for t in inputs]
@@ -106,9 +118,17 @@ def test_tiled_random_shape_vs_oracle(mode, seed):
         kw.update(extra_k=ts[4], extra_v=ts[5])
     if drop:
         kw.update(dropout_p=drop[0], dropout_seed=drop[1], dropout_offset=drop[2])
-    out = dsa3d_core(*ts[:4], (T, H, W), nh, ks, scale, **kw)
-    out.backward(dout.to(DEV))
+    out = dsa3d_core(*ts[:4], (T, H, W), nh, ks, scale, return_lse=with_lse, **kw)
+    if with_lse:
+        out, lse = out
+        ((out.float() * dout.to(DEV).float()).sum() + (lse * glse.to(DEV)).sum()).backward()
+    else:
+        out.backward(dout.to(DEV))
     torch.cuda.synchronize()
+    if with_lse:
+        e_lse = rel_err(lse.detach().cpu(), ref_lse.detach().transpose(1, 2))
+        print(f"  lse: {e_lse:.2e}", flush=True)
+        assert e_lse < (1e-4 if dtype == torch.float32 else 2e-3)
 
     e_out = rel_err(out.detach().float().cpu(), ref.detach())
     print(f"  out: {e_out:.2e}", flush=True)
@@ -123,7 +143,7 @@ def test_tiled_random_shape_vs_oracle(mode, seed):
         # to 0 against one interpolated key, so dq and dK (both carried by ds)
         # are zero up to rounding (the oracle's are exactly 0); the inputs are O(1)
         one_point = K == 1 or (H == 1 and W == 1 and (ks[0] == 1 or T == 1))
-        if name in ("dq", "dk") and one_point and G == 0:
+        if name in ("dq", "dk") and one_point and G == 0 and not with_lse:
             m = t.grad.float().abs().max().item()
             print(f"  {name} (one point, zero): max |{name}| {m:.2e}", flush=True)
             assert m < 1e-4, name
