@@ -1431,7 +1431,6 @@ __global__ __launch_bounds__(kS2Threads) void dsa3d_bwd_p2s_kernel(
   __shared__ __attribute__((aligned(16))) word_t<E> s_kt[kKtElems];
   __shared__ __attribute__((aligned(16))) int s_rows[kChunkNV];
   __shared__ int s_fz[kS2MaxT][2];         // per frame: zlo, zhi (zlo > zhi: never live)
-  __shared__ int s_rlo[SR], s_rhi[SR];     // per ring slot: its earliest and latest live frame
   __shared__ int s_unit;                   // the unit a workgroup takes next
   __shared__ int s_live[SR];               // frame in each slot at this plane (pass), or -1
   __shared__ int s_new[SR];                // a frame that starts on the plane its slot's frame ends
@@ -1596,24 +1595,28 @@ __global__ __launch_bounds__(kS2Threads) void dsa3d_bwd_p2s_kernel(
       // ---- live frames of this plane: per ring slot the earlier frame, and a
       // later one that starts here while the earlier one ends here -------------
       __syncthreads();  // the previous plane's dq write-out has read s_live
-      if (threadIdx.x < SR) {
-        s_rlo[threadIdx.x] = 0x7fffffff;
-        s_rhi[threadIdx.x] = -1;
-      }
-      __syncthreads();
-      for (int t = threadIdx.x; t < a.T; t += kS2Threads) {
-        if (s_fz[t][0] <= z && z <= s_fz[t][1]) {
-          atomicMin(&s_rlo[t % rs], t);
-          atomicMax(&s_rhi[t % rs], t);
-        }
-      }
-      __syncthreads();
       if (threadIdx.x < 64) {
-        const int r = threadIdx.x;
+        // wave 0: lane l scans the frames t = l, l + 64, ... of ring slot l % rs
+        // (rs divides 64); the lanes of one ring slot then reduce to its
+        // earliest and latest frame live on this plane
+        const int l = threadIdx.x;
+        int lo = 0x7fffffff, hi = -1;
+        for (int t = l; t < a.T; t += 64) {
+          if (s_fz[t][0] <= z && z <= s_fz[t][1]) {
+            lo = min(lo, t);
+            hi = max(hi, t);
+          }
+        }
+        for (int m = rs; m < 64; m <<= 1) {
+          lo = min(lo, __shfl_xor(lo, m));
+          hi = max(hi, __shfl_xor(hi, m));
+        }
+        const int r = l;
+        const int q = wide ? (r >> 1) : r;  // ring slot of table slot r (lane q holds its range)
+        lo = __shfl(lo, q & (rs - 1));
+        hi = __shfl(hi, q & (rs - 1));
         bool two = false;
         if (r < SR) {
-          const int q = wide ? r >> 1 : r;
-          const int lo = s_rlo[q], hi = s_rhi[q];
           two = hi >= 0 && hi != lo;
           s_live[r] = lo == 0x7fffffff ? -1 : lo;
           s_new[r] = two ? hi : -1;
