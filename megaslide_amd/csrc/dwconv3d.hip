@@ -18,6 +18,7 @@
 // data, kw in {5, 7} and channels a multiple of 8, the weight gradient runs on
 // the matrix cores instead (dwconv_dw_mfma_kernel).
 // Other odd kernel sizes use the simple one-output-per-thread kernels.
+#include <algorithm>
 #include <type_traits>
 
 #include "common.h"
@@ -654,6 +655,7 @@ __global__ __launch_bounds__(64 * kDwmCh) void dwconv_dw_mfma_kernel(ConvArgs a,
     uint32_t* const z = reinterpret_cast<uint32_t*>(s_dwm);
     for (int i = threadIdx.x; i < n32; i += blockDim.x) z[i] = 0u;
   }
+  __syncthreads();
 
   // B operand rows of this lane's column n = 16 nt + lane % 16 (clamped: unused
   // columns read a valid row and are discarded)
@@ -825,6 +827,349 @@ inline DwmGeom dwm_geometry(const ConvArgs& a) {
   const int64_t cblocks = a.C / kDwmCh;
   const int64_t ipw = (items * cblocks + 2047) / 2048;
   g.ipw = static_cast<int>(ipw > 0 ? ipw : 1);
+  return g;
+}
+
+// ---------------------------------------------------------------------------
+// Convolution (forward, and the input gradient with mirrored taps) on the
+// matrix cores: bf16, kh = kw in {5, 7}, kt in {1, 3}.  For one channel, one
+// tap row (dt, dh) and one segment of 16 outputs w0..w0+15 of an output row h:
+//   out[w0 + m] += sum_k wt[dt][dh][k - m] x[t + dt - pt][h + dh - ph][w0 - pw + k],
+// k < 32, which is D = A B with A[m][k] = wt[dt][dh][k - m] (0 outside
+// [0, kw): the banded Toeplitz matrix of the tap row) and B[k][n] the 32
+// input values of segment n: one 16x16x32 MFMA takes 16 segments (any rows
+// and x tiles) for one tap row.  A workgroup owns kFwmCh channels, one per
+// wave, and a run of bands of R output rows of one frame (b, t).  Each wave
+// keeps its channel's kt kh A operands in registers for the run.  Per band it
+// stages the kt (R + kh - 1) input rows channel-major into LDS (x[w] at
+// element w + pw of a zero-padded row; 16 bytes = 8 channels per voxel load),
+// runs kt kh MFMAs per 16 segments (segment s = (xt, r) = divmod(s, R), x tile
+// major, with a row stride the host picks so that a wave's 16-byte B reads
+// fall on distinct banks), and writes the band through LDS as 16-byte
+// (8-channel) stores.  Products are exact and summed in fp32, as in the dot2
+// kernels; only the order of the fp32 sums differs.
+// Work order: workgroup L runs on XCD L % 8; within an XCD consecutive
+// workgroups take consecutive channel blocks of the same bands, so the 128-byte
+// lines of a voxel's channels are read and written through one L2.
+// ---------------------------------------------------------------------------
+constexpr int kFwmCh = 8;          // channels (one per wave) per workgroup
+constexpr int kFwmMaxTiles = 4;    // MFMA tiles of 16 segments per band
+constexpr int kFwmGrp = 2;         // staged 4-voxel groups per thread and band (at most)
+constexpr int kFwmPadL = 4;        // staged row: voxel w at element w + kFwmPadL
+typedef __attribute__((ext_vector_type(4))) unsigned int fwm_u32x4_t;
+constexpr int kFwmTopRow = 96;     // Toeplitz row in LDS: two 48-element copies
+constexpr int64_t kFwmLdsMax = 64 * 1024;  // dynamic LDS of a launch
+
+struct FwmGeom {
+  int R;        // output rows per band (0: the kernel does not apply)
+  int nxt;      // 16-position x tiles per row
+  int xps;      // LDS stride of a staged row (elements, a multiple of 8)
+  int xr;       // staged rows per frame: R + kh - 1
+  int tiles;    // ceil(R nxt / 16)
+  int bands;    // bands per frame
+  int tr;       // output frames per work item (a run along T)
+  int nruns;    // runs per (b, band): ceil(T / tr)
+  int nig;      // work items per channel block, rounded up to a multiple of 8
+  int x_elems;  // staged elements per channel: kt xr xps
+  int ng;       // 4-voxel staging groups per staged row: W / 4
+  int lds;      // dynamic LDS bytes
+  float rW;     // 1 / W, 1 / xr and 1 / ng: exact quotients of the staging
+  float rxr;    // indices (below 2^20) by float multiply and truncation
+  float rng;
+};
+
+template <int KT, int KS>
+__global__ __launch_bounds__(64 * kFwmCh) void dwconv_fwd_mfma_kernel(
+    ConvArgs a, FwmGeom g, const bf16* __restrict__ in, const bf16* __restrict__ wt,
+    const bf16* __restrict__ bias, bf16* __restrict__ out, int flip) {
+  constexpr int KH = KS, KW = KS, PT = KT / 2, PH = KH / 2, PW = KW / 2, K = KT * KH * KW;
+  extern __shared__ __attribute__((aligned(16))) uint16_t s_fwm[];
+  uint16_t* const s_x = s_fwm;                       // [ch][dt][xr][xps]
+  uint16_t* const s_o = s_fwm + kFwmCh * g.x_elems;  // [R][W (+1)][ch] band outputs
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int ncb = a.C / kFwmCh;
+  const int j = static_cast<int>(blockIdx.x >> 3);
+  const int cb = j % ncb, ig = (j / ncb) * 8 + static_cast<int>(blockIdx.x & 7);
+  // work item ig: a run of g.tr output frames of band `band` of batch b
+  if (ig >= a.B * g.bands * g.nruns) return;
+  const int run = ig % g.nruns, bb = ig / g.nruns;
+  const int band = bb % g.bands, b = bb / g.bands;
+  const int t0 = run * g.tr, t1 = min(a.T, t0 + g.tr), h0 = band * g.R;
+  const int c0 = cb * kFwmCh, c = c0 + wave;
+  const int m = lane & 15, kg = lane >> 4;
+
+  // A operands.  Row (dt, dh) of this wave's Toeplitz table: elements [0, 48)
+  // hold P[e] = w[e - 16] (0 outside [0, kw)), [48, 96) the copy shifted by
+  // one, P[e + 1].  Lane (m, kg) needs P[s .. s + 7], s = 16 + 8 kg - m in
+  // [1, 40]: from the first copy when s is even, else from the second at s - 1,
+  // so its four dword reads are aligned.
+  {
+    // the channel's K weights (mirrored for the input gradient) into LDS with
+    // independent loads, then the table rows from them
+    constexpr int KP = (K + 7) / 8 * 8;
+    uint16_t* const tw = s_fwm + wave * (KT * KH * kFwmTopRow);
+    uint16_t* const rw = s_fwm + kFwmCh * (KT * KH * kFwmTopRow) + wave * KP;
+    const bf16* const wc = wt + static_cast<int64_t>(c) * K;
+    uint16_t wv[(K + 63) / 64];
+#pragma unroll
+    for (int u = 0; u < (K + 63) / 64; ++u) {
+      const int i = lane + 64 * u;
+      wv[u] = i < K ? wc[flip ? K - 1 - i : i].bits : uint16_t{0};
+    }
+#pragma unroll
+    for (int u = 0; u < (K + 63) / 64; ++u)
+      if (lane + 64 * u < K) rw[lane + 64 * u] = wv[u];
+    __syncthreads();
+    for (int i = lane; i < KT * KH * kFwmTopRow; i += 64) {
+      const int row = i / kFwmTopRow, e = i - row * kFwmTopRow;
+      const int dw = (e < 48 ? e - 16 : e - 63) - (kFwmPadL - PW);
+      tw[i] = (dw >= 0 && dw < KW) ? rw[row * KW + dw] : uint16_t{0};
+    }
+  }
+  __syncthreads();
+  dwm_bf16x8_t A[KT][KH];
+  {
+    const int s = 16 + 8 * kg - m;
+    const int off = (m & 1) ? 48 + s - 1 : s;
+    typedef const volatile __attribute__((address_space(3))) uint32_t lds_u32;
+#pragma unroll
+    for (int dt = 0; dt < KT; ++dt)
+#pragma unroll
+      for (int dh = 0; dh < KH; ++dh) {
+        lds_u32* const p =
+            (lds_u32*)(s_fwm + wave * (KT * KH * kFwmTopRow) + (dt * KH + dh) * kFwmTopRow + off);
+        uint32_t w4[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) w4[q] = p[q];
+        A[dt][dh] = __builtin_bit_cast(dwm_bf16x8_t, w4);
+      }
+  }
+  __syncthreads();  // every wave holds its A operands: the table space is reused
+  {
+    const int n32 = kFwmCh * g.x_elems / 2;  // the row pads must read as zeros
+    uint32_t* const z = reinterpret_cast<uint32_t*>(s_fwm);
+    for (int i = threadIdx.x; i < n32; i += blockDim.x) z[i] = 0u;
+  }
+  __syncthreads();
+
+  const float bc = bias != nullptr ? to_f32(bias[c]) : 0.0f;
+  const int S = g.R * g.nxt;
+  const int orow = a.W * kFwmCh + 8;  // output staging row (elements): 16-byte pad
+  const int64_t rowstride = static_cast<int64_t>(a.W) * a.C;
+  // LDS byte address of this wave's staged rows
+  const uint32_t xw = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(s_x + wave * g.x_elems));
+  typedef const __attribute__((address_space(3))) dwm_u16x8_t lds_u16x8;
+
+  // The staged frames form a ring of kt slots: input frame f sits in slot
+  // (f + kt) mod kt, so output frame t reads frames t - pt .. t + pt and each
+  // input frame of the run is staged once.  Staging in groups of four voxels
+  // along W (W is a multiple of 4): group (q, j) of a frame's staged row q holds
+  // voxels w = 4j .. 4j + 3 at elements 4j + kFwmPadL .. (8-byte aligned),
+  // written per channel as one 8-byte LDS store.  The loads go through a
+  // buffer resource: rows and frames outside the volume get an offset past the
+  // buffer's end and read zeros, and the four voxels of a group differ only in
+  // the scalar offset.  Group gi goes to thread gi mod 512; the next frame's
+  // groups are loaded into registers while the current frame's MFMAs run.
+  const int ng = g.ng, nfg = g.xr * ng;
+  const __amdgpu_buffer_rsrc_t xrs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16*>(in), 0,
+                                        static_cast<int>(static_cast<int64_t>(a.B) * a.N * a.C * 2), kBufWord3);
+  const int vb = a.C * 2;  // bytes per voxel
+  fwm_u32x4_t pv[kFwmGrp][4];
+  auto prefetch = [&](int tt) {
+#pragma unroll
+    for (int u = 0; u < kFwmGrp; ++u) {
+      const int gi = threadIdx.x + u * 64 * kFwmCh;
+      if (u > 0 && gi >= nfg) break;  // no group (u = 0 loads zeros from past the end instead)
+      const int q = static_cast<int>((static_cast<float>(gi) + 0.5f) * g.rng);
+      const int jg = gi - q * ng, hh = h0 + q - PH;
+      const bool ok = gi < nfg && tt >= 0 && tt < a.T && hh >= 0 && hh < a.H;
+      const uint32_t off = ok ? static_cast<uint32_t>((((b * a.T + tt) * a.H + hh) * a.W + 4 * jg) * vb + c0 * 2)
+                              : 0x80000000u;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) pv[u][v] = __builtin_amdgcn_raw_buffer_load_b128(xrs, off, v * vb, 0);
+    }
+  };
+  auto commit = [&](int tt) {
+    const int slot = (tt + KT) % KT;
+#pragma unroll
+    for (int u = 0; u < kFwmGrp; ++u) {
+      const int gi = threadIdx.x + u * 64 * kFwmCh;
+      if (gi >= nfg) continue;
+      const int q = static_cast<int>((static_cast<float>(gi) + 0.5f) * g.rng);
+      uint16_t* const dst = s_x + (slot * g.xr + q) * g.xps + 4 * (gi - q * ng) + kFwmPadL;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        // channels 2k (low halves) and 2k + 1 (high halves) of the four voxels
+        const uint2 lo = {__builtin_amdgcn_perm(pv[u][1][k], pv[u][0][k], 0x05040100u),
+                          __builtin_amdgcn_perm(pv[u][3][k], pv[u][2][k], 0x05040100u)};
+        const uint2 hi = {__builtin_amdgcn_perm(pv[u][1][k], pv[u][0][k], 0x07060302u),
+                          __builtin_amdgcn_perm(pv[u][3][k], pv[u][2][k], 0x07060302u)};
+        *reinterpret_cast<uint2*>(dst + (2 * k) * g.x_elems) = lo;
+        *reinterpret_cast<uint2*>(dst + (2 * k + 1) * g.x_elems) = hi;
+      }
+    }
+  };
+  // the ring's first kt - 1 frames, then the loads of the next one
+  for (int f = t0 - PT; f < t0 + PT; ++f) {
+    prefetch(f);
+    commit(f);
+  }
+  prefetch(t0 + PT);
+
+  for (int t = t0; t < t1; ++t) {
+    __syncthreads();  // the previous frame's B reads (of the slot refilled now) and output reads are done
+    commit(t + PT);
+    __syncthreads();
+    if (t + 1 < t1) prefetch(t + 1 + PT);
+    // tile by tile: lane column n = m is segment s = (xt, r) = divmod(s, R),
+    // clamped to the last segment where the tile is partial (not stored)
+    for (int tile = 0; tile < g.tiles; ++tile) {
+      const int sr = 16 * tile + m;
+      const int sg = min(sr, S - 1);
+      const int xt = sg / g.R, r = sg - xt * g.R;
+      const uint32_t addr = xw + 2u * static_cast<uint32_t>(r * g.xps + 16 * xt + 8 * kg);
+      dwm_f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int dt = 0; dt < KT; ++dt) {
+        // the frame's kh B operands are read together, then consumed in order
+        const int slot = (t + dt - PT + KT) % KT;
+        dwm_u16x8_t bv[KH];
+#pragma unroll
+        for (int dh = 0; dh < KH; ++dh)
+          bv[dh] = *reinterpret_cast<lds_u16x8*>(
+              addr + 2u * static_cast<uint32_t>((slot * g.xr + dh) * g.xps));
+        __builtin_amdgcn_sched_barrier(0);  // keep the reads issued together
+#pragma unroll
+        for (int dh = 0; dh < KH; ++dh)
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              A[dt][dh], __builtin_bit_cast(dwm_bf16x8_t, bv[dh]), acc, 0, 0, 0);
+      }
+      // acc[i] = out[row r][x = 16 xt + 4 kg + i] of this wave's channel
+      if (sr < S) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int x = 16 * xt + 4 * kg + i;
+          if (x < a.W) s_o[r * orow + x * kFwmCh + wave] = from_f32<bf16>(acc[i] + bc).bits;
+        }
+      }
+    }
+    __syncthreads();
+    const int rows = min(g.R, a.H - h0);
+    bf16* const obase = out + ((static_cast<int64_t>(b) * a.T + t) * a.H + h0) * rowstride + c0;
+    for (int e = threadIdx.x; e < rows * a.W; e += 64 * kFwmCh) {
+      const int r = static_cast<int>((static_cast<float>(e) + 0.5f) * g.rW);
+      const int x = e - r * a.W;
+      *reinterpret_cast<uint4*>(obase + r * rowstride + static_cast<int64_t>(x) * a.C) =
+          *reinterpret_cast<const uint4*>(s_o + r * orow + x * kFwmCh);
+    }
+  }
+}
+
+// Cycles of a wave's 16-byte B reads of one tile under the LDS bank model
+// (64 banks of 4 bytes; lanes served in four passes of 16, pass = 2 (l >> 5) +
+// parity of bits 2-4 of l; 4 = conflict-free).
+inline int fwm_read_cycles(int xps, int R, int S, int tile) {
+  int addr[64], pass[64];
+  for (int l = 0; l < 64; ++l) {
+    const int n = l & 15, kg = l >> 4;
+    const int s = std::min(16 * tile + n, S - 1);
+    const int xt = s / R, r = s - xt * R;
+    addr[l] = 2 * (r * xps + 16 * xt + 8 * kg);
+    pass[l] = 2 * (l >> 5) + (__builtin_popcount((l >> 2) & 7) & 1);
+  }
+  int cyc = 0;
+  for (int p = 0; p < 4; ++p) {
+    int cnt[16] = {};
+    for (int l = 0; l < 64; ++l) {
+      if (pass[l] != p) continue;
+      bool dup = false;
+      for (int k = 0; k < l; ++k) dup = dup || (pass[k] == p && addr[k] == addr[l]);
+      if (!dup) ++cnt[(addr[l] / 16) % 16];
+    }
+    cyc += *std::max_element(cnt, cnt + 16);
+  }
+  return cyc;
+}
+
+// Read cycles per band (all tiles) by x tiles (1..16), band rows (16, 8, 4, 2,
+// 1) and row padding (0, 8, ..., 120 elements), computed once.
+struct FwmCycles {
+  int c[16][5][16];
+};
+inline const FwmCycles& fwm_cycles() {
+  static const FwmCycles tab = [] {
+    FwmCycles t{};
+    for (int nxt = 1; nxt <= 16; ++nxt)
+      for (int ri = 0; ri < 5; ++ri)
+        for (int pi = 0; pi < 16; ++pi) {
+          const int R = 16 >> ri, S = R * nxt, xps = 16 * nxt + 16 + 8 * pi;
+          int cyc = 0;
+          if (S <= 16 * kFwmMaxTiles)
+            for (int tile = 0; tile < (S + 15) / 16; ++tile) cyc += fwm_read_cycles(xps, R, S, tile);
+          t.c[nxt - 1][ri][pi] = cyc;
+        }
+    return t;
+  }();
+  return tab;
+}
+
+// Geometry of the matrix-core convolution, or R = 0 where it does not apply.
+inline FwmGeom fwm_geometry(const ConvArgs& a) {
+  FwmGeom g{};
+  if (a.C % kFwmCh != 0 || a.W % 4 != 0 || a.W < 4 || a.W > 256 || a.H < 1) return g;
+  // the input is read through a buffer resource (32-bit byte offsets)
+  if (static_cast<int64_t>(a.B) * a.N * a.C * 2 >= kBufMaxBytes) return g;
+  if (static_cast<int64_t>(a.B) * a.T * a.H >= (int64_t{1} << 30)) return g;  // 32-bit indices
+  g.nxt = (a.W + 15) / 16;
+  for (int R = 16; R >= 1; R >>= 1) {
+    if (R > 1 && R / 2 >= a.H) continue;  // bands no taller than needed
+    const int S = R * g.nxt;
+    if (S > 16 * kFwmMaxTiles) continue;
+    const int xr = R + a.kh - 1;
+    if (xr * (a.W / 4) > kFwmGrp * 64 * kFwmCh) continue;  // staged groups per thread
+    const int tiles = (S + 15) / 16;
+    int best = -1, best_cyc = 1 << 30;
+    const int ri = 31 - __builtin_clz(16 / R);
+    for (int pi = 0; pi < 16; ++pi) {
+      const int xps = 16 * g.nxt + 16 + 8 * pi;
+      const int64_t bytes = 2LL * (kFwmCh * static_cast<int64_t>(a.kt) * xr * xps +
+                                   static_cast<int64_t>(R) * (a.W * kFwmCh + 8));
+      if (bytes > kFwmLdsMax) break;
+      const int cyc = fwm_cycles().c[g.nxt - 1][ri][pi];
+      if (cyc < best_cyc) {
+        best_cyc = cyc;
+        best = xps;
+      }
+    }
+    if (best < 0) continue;
+    g.R = R;
+    g.xr = xr;
+    g.xps = best;
+    g.tiles = tiles;
+    break;
+  }
+  if (g.R == 0) return g;
+  g.x_elems = a.kt * g.xr * g.xps;
+  const int64_t stage = 2LL * (kFwmCh * static_cast<int64_t>(g.x_elems) +
+                               static_cast<int64_t>(g.R) * (a.W * kFwmCh + 8));
+  const int kp = (a.kt * a.kh * a.kw + 7) / 8 * 8;  // raw weight row
+  const int64_t table = 2LL * kFwmCh * (a.kt * a.kh * kFwmTopRow + kp);
+  g.lds = static_cast<int>(std::max(stage, table));
+  g.bands = (a.H + g.R - 1) / g.R;
+  g.rW = 1.0f / static_cast<float>(a.W);
+  g.rxr = 1.0f / static_cast<float>(g.xr);
+  g.ng = a.W / 4;
+  g.rng = 1.0f / static_cast<float>(g.ng);
+  // runs along T: as long as leaves about four rounds of one workgroup per CU
+  // (each run stages kt - 1 frames beyond its own)
+  const int64_t ncb = a.C / kFwmCh;
+  g.tr = a.T;
+  while (g.tr > 8 && static_cast<int64_t>(a.B) * g.bands * ((a.T + g.tr - 1) / g.tr) * ncb < 1024)
+    g.tr = (g.tr + 1) / 2;
+  g.nruns = (a.T + g.tr - 1) / g.tr;
+  g.nig = static_cast<int>((static_cast<int64_t>(a.B) * g.bands * g.nruns + 7) / 8 * 8);
   return g;
 }
 
@@ -1023,6 +1368,20 @@ void launch_block(const ConvArgs& a, const G* in, const T* w, const T* b, const 
   const dim3 grid(static_cast<unsigned>((items + kRowWaves - 1) / kRowWaves),
                   static_cast<unsigned>((a.C + 63) / 64));
   if constexpr (std::is_same<T, bf16>::value && std::is_same<G, bf16>::value) {
+    if constexpr (MODE == kPlain && KS >= 5) {
+      const FwmGeom g = (a.kt == 1 || a.kt == 3) ? fwm_geometry(a) : FwmGeom{};
+      if (g.R > 0 && reinterpret_cast<uintptr_t>(in) % 16 == 0 &&
+          reinterpret_cast<uintptr_t>(out) % 16 == 0) {
+        const dim3 mgrid(static_cast<unsigned>((a.C / kFwmCh) * g.nig));
+        if (a.kt == 3)
+          hipLaunchKernelGGL((dwconv_fwd_mfma_kernel<3, KS>), mgrid, dim3(64 * kFwmCh),
+                             static_cast<unsigned>(g.lds), s, a, g, in, w, b, out, flip);
+        else
+          hipLaunchKernelGGL((dwconv_fwd_mfma_kernel<1, KS>), mgrid, dim3(64 * kFwmCh),
+                             static_cast<unsigned>(g.lds), s, a, g, in, w, b, out, flip);
+        return;
+      }
+    }
     // the dot2 kernel's wide rows are addressed with 32-bit buffer offsets
     if (KS < 5 || static_cast<int64_t>(a.B) * a.N * a.C * 2 < kBufMaxBytes) {
       hipLaunchKernelGGL((dwconv_block_dot2_kernel<KS, KS, MODE>), grid, dim3(64 * kRowWaves), 0,
