@@ -1011,51 +1011,70 @@ __global__ __launch_bounds__(64 * kFwmCh) void dwconv_fwd_mfma_kernel(
       }
     }
   };
+  // Per tile, this lane's B column n = m: segment s = (xt, r) = divmod(s, R),
+  // clamped to the last segment where the tile is partial (its results are
+  // not stored); its LDS address in a frame's rows and its output slot.
+  uint32_t taddr[kFwmMaxTiles];
+  int to[kFwmMaxTiles], tx[kFwmMaxTiles];
+  bool tval[kFwmMaxTiles];
+#pragma unroll
+  for (int tile = 0; tile < kFwmMaxTiles; ++tile) {
+    const int sr = 16 * tile + m;
+    const int sg = min(sr, S - 1);
+    const int xt = sg / g.R, r = sg - xt * g.R;
+    taddr[tile] = xw + 2u * static_cast<uint32_t>(r * g.xps + 16 * xt + 8 * kg);
+    tx[tile] = 16 * xt + 4 * kg;
+    to[tile] = r * orow + tx[tile] * kFwmCh + wave;
+    tval[tile] = sr < S;
+  }
   // the ring's first kt - 1 frames, then the loads of the next one
   for (int f = t0 - PT; f < t0 + PT; ++f) {
     prefetch(f);
     commit(f);
   }
   prefetch(t0 + PT);
+  commit(t0 + PT);
 
   for (int t = t0; t < t1; ++t) {
-    __syncthreads();  // the previous frame's B reads (of the slot refilled now) and output reads are done
-    commit(t + PT);
-    __syncthreads();
+    __syncthreads();  // frame t + pt is staged; the previous frame's output reads are done
     if (t + 1 < t1) prefetch(t + 1 + PT);
-    // tile by tile: lane column n = m is segment s = (xt, r) = divmod(s, R),
-    // clamped to the last segment where the tile is partial (not stored)
     for (int tile = 0; tile < g.tiles; ++tile) {
-      const int sr = 16 * tile + m;
-      const int sg = min(sr, S - 1);
-      const int xt = sg / g.R, r = sg - xt * g.R;
-      const uint32_t addr = xw + 2u * static_cast<uint32_t>(r * g.xps + 16 * xt + 8 * kg);
+      const uint32_t addr = taddr[tile];
       dwm_f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-      for (int dt = 0; dt < KT; ++dt) {
-        // the frame's kh B operands are read together, then consumed in order
+      // a frame's kh B operands are read together; the next frame's reads are
+      // issued before this frame's MFMAs
+      dwm_u16x8_t bv[2][KH];
+      auto read_frame = [&](int dt, dwm_u16x8_t* dst) {
         const int slot = (t + dt - PT + KT) % KT;
-        dwm_u16x8_t bv[KH];
 #pragma unroll
         for (int dh = 0; dh < KH; ++dh)
-          bv[dh] = *reinterpret_cast<lds_u16x8*>(
+          dst[dh] = *reinterpret_cast<lds_u16x8*>(
               addr + 2u * static_cast<uint32_t>((slot * g.xr + dh) * g.xps));
-        __builtin_amdgcn_sched_barrier(0);  // keep the reads issued together
+      };
+      read_frame(0, bv[0]);
+#pragma unroll
+      for (int dt = 0; dt < KT; ++dt) {
+        if (dt + 1 < KT) read_frame(dt + 1, bv[(dt + 1) & 1]);
+        __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the MFMAs
 #pragma unroll
         for (int dh = 0; dh < KH; ++dh)
           acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-              A[dt][dh], __builtin_bit_cast(dwm_bf16x8_t, bv[dh]), acc, 0, 0, 0);
+              A[dt][dh], __builtin_bit_cast(dwm_bf16x8_t, bv[dt & 1][dh]), acc, 0, 0, 0);
       }
       // acc[i] = out[row r][x = 16 xt + 4 kg + i] of this wave's channel
-      if (sr < S) {
+      if (tval[tile]) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int x = 16 * xt + 4 * kg + i;
-          if (x < a.W) s_o[r * orow + x * kFwmCh + wave] = from_f32<bf16>(acc[i] + bc).bits;
+          // the hardware conversion rounds to nearest even, as from_f32 does
+          if (tx[tile] + i < a.W)
+            s_o[to[tile] + i * kFwmCh] = __builtin_bit_cast(uint16_t, static_cast<__bf16>(acc[i] + bc));
         }
       }
     }
-    __syncthreads();
+    __syncthreads();  // every wave's B reads of this frame and output writes are done
+    // the next frame into the ring slot of frame t - pt (no longer read), and
+    // this frame's outputs from LDS to the token rows
+    if (t + 1 < t1) commit(t + 1 + PT);
     const int rows = min(g.R, a.H - h0);
     bf16* const obase = out + ((static_cast<int64_t>(b) * a.T + t) * a.H + h0) * rowstride + c0;
     for (int e = threadIdx.x; e < rows * a.W; e += 64 * kFwmCh) {
