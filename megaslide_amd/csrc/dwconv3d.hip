@@ -858,7 +858,7 @@ constexpr int kFwmGrp = 2;         // staged 4-voxel groups per thread and band 
 constexpr int kFwmPadL = 4;        // staged row: voxel w at element w + kFwmPadL
 typedef __attribute__((ext_vector_type(4))) unsigned int fwm_u32x4_t;
 constexpr int kFwmTopRow = 96;     // Toeplitz row in LDS: two 48-element copies
-constexpr int64_t kFwmLdsMax = 64 * 1024;  // dynamic LDS of a launch
+constexpr int64_t kFwmLdsMax = 80 * 1024;  // two workgroups per CU
 
 struct FwmGeom {
   int R;        // output rows per band (0: the kernel does not apply)
@@ -1112,18 +1112,18 @@ inline int fwm_read_cycles(int xps, int R, int S, int tile) {
   return cyc;
 }
 
-// Read cycles per band (all tiles) by x tiles (1..16), band rows (16, 8, 4, 2,
-// 1) and row padding (0, 8, ..., 120 elements), computed once.
+// Read cycles per band (all tiles) by x tiles (1..16), band rows (32, 16, 8,
+// 4, 2, 1) and row padding (0, 8, ..., 120 elements), computed once.
 struct FwmCycles {
-  int c[16][5][16];
+  int c[16][6][16];
 };
 inline const FwmCycles& fwm_cycles() {
   static const FwmCycles tab = [] {
     FwmCycles t{};
     for (int nxt = 1; nxt <= 16; ++nxt)
-      for (int ri = 0; ri < 5; ++ri)
+      for (int ri = 0; ri < 6; ++ri)
         for (int pi = 0; pi < 16; ++pi) {
-          const int R = 16 >> ri, S = R * nxt, xps = 16 * nxt + 16 + 8 * pi;
+          const int R = 32 >> ri, S = R * nxt, xps = 16 * nxt + 16 + 8 * pi;
           int cyc = 0;
           if (S <= 16 * kFwmMaxTiles)
             for (int tile = 0; tile < (S + 15) / 16; ++tile) cyc += fwm_read_cycles(xps, R, S, tile);
@@ -1142,7 +1142,7 @@ inline FwmGeom fwm_geometry(const ConvArgs& a) {
   if (static_cast<int64_t>(a.B) * a.N * a.C * 2 >= kBufMaxBytes) return g;
   if (static_cast<int64_t>(a.B) * a.T * a.H >= (int64_t{1} << 30)) return g;  // 32-bit indices
   g.nxt = (a.W + 15) / 16;
-  for (int R = 16; R >= 1; R >>= 1) {
+  for (int R = 32; R >= 1; R >>= 1) {
     if (R > 1 && R / 2 >= a.H) continue;  // bands no taller than needed
     const int S = R * g.nxt;
     if (S > 16 * kFwmMaxTiles) continue;
@@ -1150,7 +1150,7 @@ inline FwmGeom fwm_geometry(const ConvArgs& a) {
     if (xr * (a.W / 4) > kFwmGrp * 64 * kFwmCh) continue;  // staged groups per thread
     const int tiles = (S + 15) / 16;
     int best = -1, best_cyc = 1 << 30;
-    const int ri = 31 - __builtin_clz(16 / R);
+    const int ri = 31 - __builtin_clz(32 / R);
     for (int pi = 0; pi < 16; ++pi) {
       const int xps = 16 * g.nxt + 16 + 8 * pi;
       const int64_t bytes = 2LL * (kFwmCh * static_cast<int64_t>(a.kt) * xr * xps +
@@ -1181,7 +1181,7 @@ inline FwmGeom fwm_geometry(const ConvArgs& a) {
   g.rxr = 1.0f / static_cast<float>(g.xr);
   g.ng = a.W / 4;
   g.rng = 1.0f / static_cast<float>(g.ng);
-  // runs along T: as long as leaves about four rounds of one workgroup per CU
+  // runs along T: as long as leaves about two rounds of two workgroups per CU
   // (each run stages kt - 1 frames beyond its own)
   const int64_t ncb = a.C / kFwmCh;
   g.tr = a.T;
