@@ -832,25 +832,30 @@ inline DwmGeom dwm_geometry(const ConvArgs& a) {
 
 // ---------------------------------------------------------------------------
 // Convolution (forward, and the input gradient with mirrored taps) on the
-// matrix cores: bf16, kh = kw in {5, 7}, kt in {1, 3}.  For one channel, one
-// tap row (dt, dh) and one segment of 16 outputs w0..w0+15 of an output row h:
-//   out[w0 + m] += sum_k wt[dt][dh][k - m] x[t + dt - pt][h + dh - ph][w0 - pw + k],
-// k < 32, which is D = A B with A[m][k] = wt[dt][dh][k - m] (0 outside
-// [0, kw): the banded Toeplitz matrix of the tap row) and B[k][n] the 32
-// input values of segment n: one 16x16x32 MFMA takes 16 segments (any rows
+// matrix cores: bf16, kh = kw in {5, 7}, kt in {1, 3}, W a multiple of 4, no
+// activation.  (3x3 rows stay on the dot2 kernels: with 9 tap rows per frame
+// the staging outweighs the products, and the matrix-core version of the
+// offset net's 3x3x3 + GELU measured 0.187 ms against 0.176 at 65,536 tokens.)
+// For one channel, one tap row (dt, dh) and one segment of 16 outputs
+// w0 .. w0 + 15 of an output row h, with the input row staged from w0 - 4:
+//   out[w0 + m] += sum_k A[m][k] x[t + dt - pt][h + dh - ph][w0 - 4 + k],  k < 32,
+//   A[m][k] = wt[dt][dh][k - m - (4 - pw)]  (0 outside [0, kw)),
+// the banded Toeplitz matrix of the tap row: D = A B with B[k][n] the 32
+// input values of segment n, so one 16x16x32 MFMA takes 16 segments (any rows
 // and x tiles) for one tap row.  A workgroup owns kFwmCh channels, one per
-// wave, and a run of bands of R output rows of one frame (b, t).  Each wave
-// keeps its channel's kt kh A operands in registers for the run.  Per band it
-// stages the kt (R + kh - 1) input rows channel-major into LDS (x[w] at
-// element w + pw of a zero-padded row; 16 bytes = 8 channels per voxel load),
-// runs kt kh MFMAs per 16 segments (segment s = (xt, r) = divmod(s, R), x tile
-// major, with a row stride the host picks so that a wave's 16-byte B reads
-// fall on distinct banks), and writes the band through LDS as 16-byte
-// (8-channel) stores.  Products are exact and summed in fp32, as in the dot2
-// kernels; only the order of the fp32 sums differs.
+// wave, a band of R output rows and a run of consecutive frames of one batch
+// entry.  Each wave keeps its channel's kt kh A operands in registers for the
+// run.  The staged input frames form a ring of kt slots in LDS (channel-major,
+// x[w] at element w + kFwmPadL of a zero-padded row), so each input frame of
+// the run is staged once; per output frame the kernel runs kt kh MFMAs per 16
+// segments (segment s = (xt, r) = divmod(s, R), x tile major, with a row
+// stride the host picks so that a wave's 16-byte B reads fall on distinct
+// banks) and writes the band through LDS as 16-byte (8-channel) stores.
+// Products are exact and summed in fp32, as in the dot2 kernels; only the
+// order of the fp32 sums differs.
 // Work order: workgroup L runs on XCD L % 8; within an XCD consecutive
-// workgroups take consecutive channel blocks of the same bands, so the 128-byte
-// lines of a voxel's channels are read and written through one L2.
+// workgroups take consecutive channel blocks of the same work item, so the
+// 128-byte lines of a voxel's channels are read and written through one L2.
 // ---------------------------------------------------------------------------
 constexpr int kFwmCh = 8;          // channels (one per wave) per workgroup
 constexpr int kFwmMaxTiles = 4;    // MFMA tiles of 16 segments per band
