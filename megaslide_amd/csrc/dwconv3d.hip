@@ -859,7 +859,7 @@ inline DwmGeom dwm_geometry(const ConvArgs& a) {
 // ---------------------------------------------------------------------------
 constexpr int kFwmCh = 8;          // channels (one per wave) per workgroup
 constexpr int kFwmMaxTiles = 4;    // MFMA tiles of 16 segments per band
-constexpr int kFwmGrp = 2;         // staged 4-voxel groups per thread and band (at most)
+constexpr int kFwmGrp = 2;         // staged 4-voxel groups per thread and frame (at most)
 constexpr int kFwmPadL = 4;        // staged row: voxel w at element w + kFwmPadL
 typedef __attribute__((ext_vector_type(4))) unsigned int fwm_u32x4_t;
 constexpr int kFwmTopRow = 96;     // Toeplitz row in LDS: two 48-element copies
@@ -878,9 +878,8 @@ struct FwmGeom {
   int x_elems;  // staged elements per channel: kt xr xps
   int ng;       // 4-voxel staging groups per staged row: W / 4
   int lds;      // dynamic LDS bytes
-  float rW;     // 1 / W, 1 / xr and 1 / ng: exact quotients of the staging
-  float rxr;    // indices (below 2^20) by float multiply and truncation
-  float rng;
+  float rW;     // 1 / W and 1 / ng: exact quotients of the staging and output
+  float rng;    // indices (below 2^20) by float multiply and truncation
 };
 
 template <int KT, int KS>
@@ -905,10 +904,11 @@ __global__ __launch_bounds__(64 * kFwmCh) void dwconv_fwd_mfma_kernel(
   const int m = lane & 15, kg = lane >> 4;
 
   // A operands.  Row (dt, dh) of this wave's Toeplitz table: elements [0, 48)
-  // hold P[e] = w[e - 16] (0 outside [0, kw)), [48, 96) the copy shifted by
-  // one, P[e + 1].  Lane (m, kg) needs P[s .. s + 7], s = 16 + 8 kg - m in
-  // [1, 40]: from the first copy when s is even, else from the second at s - 1,
-  // so its four dword reads are aligned.
+  // hold P[e] = w[e - 16 - (kFwmPadL - pw)] (0 outside [0, kw)), [48, 96) the
+  // copy shifted by one, P[e + 1].  Lane (m, kg) needs P[s .. s + 7],
+  // s = 16 + 8 kg - m in [1, 40] (A[m][k] = P[16 + k - m]): from the first copy
+  // when s is even, else from the second at s - 1, so its four dword reads are
+  // aligned.
   {
     // the channel's K weights (mirrored for the input gradient) into LDS with
     // independent loads, then the table rows from them
@@ -1183,7 +1183,6 @@ inline FwmGeom fwm_geometry(const ConvArgs& a) {
   g.lds = static_cast<int>(std::max(stage, table));
   g.bands = (a.H + g.R - 1) / g.R;
   g.rW = 1.0f / static_cast<float>(a.W);
-  g.rxr = 1.0f / static_cast<float>(g.xr);
   g.ng = a.W / 4;
   g.rng = 1.0f / static_cast<float>(g.ng);
   // runs along T: as long as leaves about two rounds of two workgroups per CU
